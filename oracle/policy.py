@@ -1,0 +1,154 @@
+"""MLP actor/critic forward and masked factored sampling (restates
+train/model.py:121-196 and :215-245).
+
+The forward runs in float32 (or float64) torch ops on an `ActorCritic`
+mlp state_dict (keys `shared.0.weight`, ..., `critic.2.bias`).  The sampler is
+the build's injected-uniform rule, written in float32 numpy arithmetic that
+the HIP kernel reproduces operation for operation:
+
+    ml_k = mask_k ? logit_k : -FLT_MAX          (train/model.py:215-220)
+    m = max_k ml_k,  e_k = exp(ml_k - m),  S = sum_k e_k (in k order)
+    a = #{k : e_0 + ... + e_k <= u * S}, clamped to the last k with e_k > 0
+    logp = (ml_a - m) - log(S)
+
+`exp` and `log` are this module's own float32 routines (Cody-Waite range
+reduction with a degree-6 Taylor polynomial; an atanh series for log), so
+host and device agree bit for bit given identical logits and uniforms.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+F32 = np.float32
+NEG_MAX = F32(-3.4028234663852886e38)           # torch.finfo(float32).min
+LOG2E = F32(1.4426950408889634)
+LN2_HI = F32(0.693145751953125)                 # 0x3f317200, exact in 16 bits
+LN2_LO = F32(1.428606765330187e-06)             # ln2 - LN2_HI
+LN2 = F32(0.6931471805599453)
+EXP_CUTOFF = F32(-80.0)
+_EXP_C = [F32(1.0 / 720.0), F32(1.0 / 120.0), F32(1.0 / 24.0), F32(1.0 / 6.0),
+          F32(0.5), F32(1.0), F32(1.0)]
+_LOG_C = [F32(1.0 / 9.0), F32(1.0 / 7.0), F32(1.0 / 5.0), F32(1.0 / 3.0), F32(1.0)]
+SQRT_HALF = F32(0.70710678118654752)
+
+
+def exp_f32(x) -> np.ndarray:
+    """exp for x <= 0 in float32: x = n ln2 + r, |r| <= ln2/2; exp(r) by Horner
+    on the Taylor coefficients; times 2^n; 0 below EXP_CUTOFF."""
+    x = np.asarray(x, dtype=F32)
+    xc = np.maximum(x, EXP_CUTOFF)
+    n = np.rint(xc * LOG2E).astype(F32)
+    r = (xc - n * LN2_HI) - n * LN2_LO
+    p = _EXP_C[0]
+    for c in _EXP_C[1:]:
+        p = p * r + c
+    scale = ((n.astype(np.int32) + 127) << 23).astype(np.uint32).view(F32)
+    out = (p * scale).astype(F32)
+    return np.where(x < EXP_CUTOFF, F32(0.0), out).astype(F32)
+
+
+def log_f32(x) -> np.ndarray:
+    """log for normal x > 0 in float32: x = 2^k m with m in [sqrt(1/2), sqrt(2));
+    log m = 2 atanh(s), s = (m-1)/(m+1), odd series to s^9."""
+    x = np.asarray(x, dtype=F32)
+    bits = x.view(np.uint32).astype(np.int64)
+    k = ((bits >> 23) & 0xFF) - 127
+    m = ((bits & 0x7FFFFF) | (127 << 23)).astype(np.uint32).view(F32)
+    big = m >= F32(1.4142135623730951)
+    m = np.where(big, m * F32(0.5), m).astype(F32)
+    k = np.where(big, k + 1, k)
+    s = ((m - F32(1.0)) / (m + F32(1.0))).astype(F32)
+    s2 = (s * s).astype(F32)
+    q = _LOG_C[0]
+    for c in _LOG_C[1:]:
+        q = q * s2 + c
+    lm = F32(2.0) * (s * q)
+    return (k.astype(F32) * LN2 + lm).astype(F32)
+
+
+def sample_masked(logits, mask, u):
+    """(a int64 (B,), logp float32 (B,)) for (B, K) logits/mask and (B,) u."""
+    logits = np.asarray(logits, dtype=F32)
+    mask = np.asarray(mask, dtype=bool)
+    u = np.asarray(u, dtype=F32)
+    b, k = logits.shape
+    ml = np.where(mask, logits, NEG_MAX).astype(F32)
+    m = ml[:, 0].copy()
+    for j in range(1, k):
+        m = np.maximum(m, ml[:, j])
+    e = np.stack([exp_f32(ml[:, j] - m) for j in range(k)], 1)
+    s = e[:, 0].copy()
+    for j in range(1, k):
+        s = (s + e[:, j]).astype(F32)
+    t = (u * s).astype(F32)
+    run = F32(0.0) * s
+    count = np.zeros(b, dtype=np.int64)
+    last = np.zeros(b, dtype=np.int64)
+    for j in range(k):
+        run = (run + e[:, j]).astype(F32)
+        count += (run <= t)
+        last = np.where(e[:, j] > 0, j, last)
+    a = np.where(count >= k, last, count)
+    picked = ml[np.arange(b), a]
+    logp = ((picked - m).astype(F32) - log_f32(s)).astype(F32)
+    return a.astype(np.int64), logp
+
+
+def view_perm(me: int, p: int, c: int) -> list[int]:
+    opp = [i for i in range(p) if i != me]
+    head = [me, p + me] + opp + [p + o for o in opp] + [2 * p, 2 * p + 1, 2 * p + 2]
+    return head + list(range(2 * p + 3, c))
+
+
+def column_permutation(pid: int, p: int, c: int, hw: int) -> torch.Tensor:
+    """Column index map folding player `pid`'s view permutation into the
+    first layer: block k of the permuted weight is block inv[k] of the
+    original, inv = argsort(view_perm) (train/model.py:121-139)."""
+    perm = torch.tensor(view_perm(pid, p, c))
+    inv = torch.argsort(perm)
+    cols = torch.empty(c * hw, dtype=torch.long)
+    for k in range(c):
+        cols[k * hw:(k + 1) * hw] = torch.arange(hw) + int(inv[k]) * hw
+    return cols
+
+
+def mlp_forward(params: dict, obs: torch.Tensor, pid: int, n_players: int = 2,
+                dtype=torch.float32):
+    """(move_logits, bomb_logits, value) of the mlp ActorCritic for player
+    `pid` (train/model.py:192-196); `params` is its state_dict."""
+    P = {k: v.to(dtype) for k, v in params.items()}
+    b = obs.shape[0]
+    c, h, w = obs.shape[1:]
+    x = obs.to(dtype).reshape(b, -1)
+    cols = column_permutation(pid, n_players, c, h * w)
+    x = F.linear(x, P["shared.0.weight"][:, cols], P["shared.0.bias"])
+    x = F.relu(F.layer_norm(x, (x.shape[-1],), P["shared.1.weight"], P["shared.1.bias"]))
+    x = F.linear(x, P["shared.3.weight"], P["shared.3.bias"])
+    x = F.relu(F.layer_norm(x, (x.shape[-1],), P["shared.4.weight"], P["shared.4.bias"]))
+
+    def head(name):
+        y = F.relu(F.linear(x, P[f"{name}.0.weight"], P[f"{name}.0.bias"]))
+        return F.linear(y, P[f"{name}.2.weight"], P[f"{name}.2.bias"])
+
+    return head("move_head"), head("bomb_head"), head("critic").squeeze(-1)
+
+
+def default_init_params(c: int = 14, hw: int = 169, n_moves: int = 5, n_bomb: int = 2,
+                        seed: int = 0) -> dict:
+    """PyTorch default init (nn.Linear: kaiming-uniform a=sqrt(5) weights,
+    U(+-1/sqrt(fan_in)) bias; LayerNorm gamma=1, beta=0) for the mlp
+    ActorCritic under torch.manual_seed(seed), layers created in module order."""
+    torch.manual_seed(seed)
+    shared = torch.nn.Sequential(torch.nn.Linear(c * hw, 128), torch.nn.LayerNorm(128),
+                                 torch.nn.ReLU(), torch.nn.Linear(128, 128),
+                                 torch.nn.LayerNorm(128), torch.nn.ReLU())
+    heads = {name: torch.nn.Sequential(torch.nn.Linear(128, 64), torch.nn.ReLU(),
+                                       torch.nn.Linear(64, k))
+             for name, k in (("move_head", n_moves), ("bomb_head", n_bomb), ("critic", 1))}
+    out = {f"shared.{k}": v for k, v in shared.state_dict().items()}
+    for name, mod in heads.items():
+        out.update({f"{name}.{k}": v for k, v in mod.state_dict().items()})
+    return {k: v.detach().clone() for k, v in out.items()}

@@ -1,0 +1,273 @@
+#!/usr/bin/env python3
+"""Write golden input/output vectors by running the reference implementation.
+
+Run in the build container, where the reference checkout sits at
+/root/reference:
+
+    python tests/golden/gen_reference_vectors.py
+
+It imports the reference's `sim` and `train.model` packages (their Triton move
+kernel is switched off, so `BatchedSim.step` takes the eager `move_players`,
+which the reference keeps bit-identical to it) and writes `.npz` fixtures next
+to this script.  Only vectors are written; no reference source is copied.
+
+Fixtures (the functions they pin are the ones the JSON fixtures under the
+reference's deploy/ leave open: multi-tick `BatchedSim.step` including
+placement reward, hit-attribute penalty, combo, crate growth, auto-free chain
+truncation at 8 rounds, and the MLP forward with its per-player column
+permutation):
+
+* traj_<name>.npz - a 64-env rollout of T ticks with `auto_reset=False`.
+  The initial state comes from the oracle's template maps; actions and crate
+  uniforms are injected and recorded; after every tick the full state,
+  reward, done, info and the next tick's masks are stored, plus the
+  observation of envs 0..3.
+* deep_chain.npz - single-tick states with chains longer than 8 rounds.
+* mlp.npz - MLP ActorCritic weights, inputs and forward/evaluate outputs.
+"""
+
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(os.path.dirname(HERE))
+REF = "/root/reference"
+sys.path.insert(0, os.path.join(REPO, "qqt-gpu-sim_amd"))
+sys.path.insert(0, REPO)
+sys.path.insert(0, REF)
+
+import sim.torch_sim as ref_torch_sim  # noqa: E402
+from sim.config import SimConfig as RefConfig  # noqa: E402
+from train.model import ActorCritic  # noqa: E402
+
+from oracle import philox  # noqa: E402
+from oracle.policy import sample_masked  # noqa: E402
+from oracle.sim import template_maps  # noqa: E402
+from qqtsim.maps import MapSpec  # noqa: E402
+
+ref_torch_sim._HAS_TRITON = False
+ref_torch_sim._move_triton = None
+
+CFG_KW = dict(map_mode="corridor", speed=3.0, tick_hz=10, max_steps=1800,
+              open_fraction=0.0, n_players=2, obs_fp16=True)
+
+
+def ref_sim(n, spec, seed, cfg_kw=None):
+    cfg = RefConfig(**dict(CFG_KW, **(cfg_kw or {})))
+    s = ref_torch_sim.BatchedSim(cfg, n, device="cpu", seed=seed)
+    wall, brick, pos, bombs, blast, spd = template_maps(cfg, spec, np.arange(n), seed, 0)
+    s.wall.copy_(torch.from_numpy(wall))
+    s.brick.copy_(torch.from_numpy(brick))
+    s.crate.zero_()
+    s._recycle_crate.zero_()
+    s.fuse.zero_()
+    s.owner.fill_(-1)
+    s.bomb_blast.zero_()
+    s.pos.copy_(torch.from_numpy(pos))
+    s.alive.fill_(True)
+    s.hp.fill_(cfg.max_hp)
+    s.since_bomb.fill_(cfg.place_dist_cooldown)
+    s.t.zero_()
+    s.bombs_cap = torch.from_numpy(bombs).clone()
+    s.blast_cap = torch.from_numpy(blast).clone()
+    s.spd_g = torch.from_numpy(spd).clone()
+    s.invuln.zero_()
+    s._combo.zero_()
+    s._last_hit.fill_(-10 ** 9)
+    s._pending_lost.zero_()
+    s.crate_prob.fill_(cfg.growth_crate_prob)
+    s._lo_bombs = torch.from_numpy(bombs).clone()
+    s._lo_blast = torch.from_numpy(blast).clone()
+    s._lo_spd = torch.from_numpy(spd).clone()
+    s._map_kind.zero_()
+    s._is_open.zero_()
+    s._hazard.zero_()
+    return s
+
+
+def snapshot(s):
+    return dict(
+        wall=s.wall.numpy().copy(), brick=s.brick.numpy().copy(),
+        crate=s.crate.numpy().copy(), recycle=s._recycle_crate.numpy().copy(),
+        fuse=s.fuse.numpy().copy(), owner=s.owner.numpy().copy(),
+        bomb_blast=s.bomb_blast.numpy().copy(), pos=s.pos.numpy().copy(),
+        alive=s.alive.numpy().copy(), hp=s.hp.numpy().copy(),
+        since_bomb=s.since_bomb.numpy().copy(), t=s.t.numpy().copy(),
+        bombs_cap=s.bombs_cap.numpy().copy(), blast_cap=s.blast_cap.numpy().copy(),
+        spd_g=s.spd_g.numpy().copy(), invuln=s.invuln.numpy().copy(),
+        combo=s._combo.numpy().copy(), last_hit=s._last_hit.numpy().copy(),
+        pending_lost=s._pending_lost.numpy().copy(),
+    )
+
+
+def actions_for(kind, mm, bm, n, seed, tick):
+    p = mm.shape[1]
+    if kind == "legal":
+        u = philox.uniforms(seed, np.arange(n), tick, philox.STREAM_RANDOM_ACT, 2 * p)
+        out = np.zeros((n, p, 2), dtype=np.int64)
+        for i in range(p):
+            out[:, i, 0] = sample_masked(mm[:, i].astype(np.float32), mm[:, i], u[:, 2 * i])[0]
+            out[:, i, 1] = sample_masked(bm[:, i].astype(np.float32), bm[:, i], u[:, 2 * i + 1])[0]
+        return out
+    u = philox.uniforms(seed, np.arange(n), tick, philox.STREAM_INJECT_ACT, 2 * p)
+    out = np.zeros((n, p, 2), dtype=np.int64)
+    for i in range(p):
+        out[:, i, 0] = np.minimum(np.floor(u[:, 2 * i] * np.float32(5)).astype(np.int64), 4)
+        out[:, i, 1] = (u[:, 2 * i + 1] < np.float32(0.5)).astype(np.int64)
+    return out
+
+
+def rollout(name, spec, kind, n=64, ticks=128, seed=0, obs_envs=4, cfg_kw=None):
+    s = ref_sim(n, spec, seed, cfg_kw)
+    p = s.cfg.n_players
+    rec = {k: [] for k in ("actions", "crate_u", "reward", "done", "n_alive", "covered",
+                           "trig", "died", "winner", "mm", "bm", "obs", "danger")}
+    states = []
+    init = snapshot(s)
+    mm, bm = (m.numpy().copy() for m in s.legal_mask())
+    rec["mm"].append(mm)
+    rec["bm"].append(bm)
+    rec["obs"].append(s.observe()[:obs_envs].numpy().copy())
+    for tick in range(ticks):
+        a = actions_for(kind, mm, bm, n, seed, tick)
+        cu = philox.uniforms(seed, np.arange(n), tick, philox.STREAM_CRATE, 2 * p)
+        cu = cu.reshape(n, p, 2).transpose(1, 2, 0).copy()          # (P, 2, N)
+        s._rand_buf = torch.from_numpy(np.concatenate(
+            [cu[:, 0, :].T.reshape(-1), cu[:, 1, :].T.reshape(-1)]))
+        r, d, info = s.step(torch.from_numpy(a), auto_reset=False)
+        rec["actions"].append(a)
+        rec["crate_u"].append(cu)
+        rec["reward"].append(r.numpy().copy())
+        rec["done"].append(d.numpy().copy())
+        rec["n_alive"].append(info["n_alive"].numpy().copy())
+        rec["covered"].append(info["blast"].numpy().copy())
+        rec["trig"].append(info["trig"].numpy().copy())
+        rec["died"].append(info["died"].numpy().copy())
+        rec["winner"].append(info["winner"].numpy().copy())
+        rec["danger"].append(s._dng_cache.numpy().copy())
+        states.append(snapshot(s))
+        mm, bm = (m.numpy().copy() for m in s.legal_mask())
+        rec["mm"].append(mm)
+        rec["bm"].append(bm)
+        rec["obs"].append(s.observe()[:obs_envs].numpy().copy())
+    out = {f"init_{k}": v for k, v in init.items()}
+    for k in states[0]:
+        out[f"state_{k}"] = np.stack([st[k] for st in states])
+    for k, v in rec.items():
+        out[k] = np.stack(v)
+    out["seed"] = np.int64(seed)
+    out["resolve_hint"] = np.int64(s._res_cached.__defaults__[0])
+    out["map_spec"] = np.array([spec.kind, str(spec.brick_p), str(int(spec.swap_spawns)),
+                                str(spec.bombs_cap[0]), str(spec.bombs_cap[1]),
+                                str(spec.blast_cap[0]), str(spec.blast_cap[1]),
+                                str(spec.speed)])
+    np.savez_compressed(os.path.join(HERE, f"traj_{name}.npz"), **out)
+    placed = int((np.stack([st["fuse"] for st in states]) == 30).sum())
+    print(f"{name}: ticks={ticks} placed~{placed} deaths={int(out['died'].sum())} "
+          f"done_ticks={int(out['done'].sum())} resolve_hint={int(out['resolve_hint'])}")
+
+
+def deep_chain():
+    """States whose chain needs more than 8 relay rounds."""
+    cfg = RefConfig(**CFG_KW)
+    n = 4
+    s = ref_sim(n, MapSpec(kind="open"), 1)
+    s.wall.zero_()
+    s.brick.zero_()
+    # env 0: 13 bombs in row 6, blast 1, leftmost due now
+    for i in range(13):
+        s.fuse[0, 6, i] = 1 if i == 0 else cfg.fuse
+        s.owner[0, 6, i] = 0
+        s.bomb_blast[0, 6, i] = 1
+    # env 1: snake of blast-2 bombs alternating rows, mixed fuses
+    cells = [(2, 1), (2, 3), (4, 3), (4, 5), (6, 5), (6, 7), (8, 7), (8, 9), (10, 9),
+             (10, 11), (12, 11), (12, 9)]
+    for k, (r, c) in enumerate(cells):
+        s.fuse[1, r, c] = 1 if k == 0 else 5 + 2 * k
+        s.owner[1, r, c] = k % 2
+        s.bomb_blast[1, r, c] = 2
+    # env 2: a column chain with a brick gap and a wall stop
+    s.brick[2, 5, 4] = True
+    s.wall[2, 9, 4] = True
+    for r in range(0, 13):
+        if r in (5, 9):
+            continue
+        s.fuse[2, r, 4] = 1 if r == 0 else 3 + r
+        s.owner[2, r, 4] = r % 2
+        s.bomb_blast[2, r, 4] = 3 if r % 3 == 0 else 1
+    # env 3: a cross of bombs, blasts 2..7
+    for k, (r, c) in enumerate([(6, 6), (6, 8), (6, 11), (3, 6), (1, 6), (9, 6), (12, 6),
+                                (6, 3), (6, 1)]):
+        s.fuse[3, r, c] = 1 if k == 0 else 20 - k
+        s.owner[3, r, c] = k % 2
+        s.bomb_blast[3, r, c] = 2 + (k % 6)
+    s.pos[:, 0] = torch.tensor([6.5, 2.5])
+    s.pos[:, 1] = torch.tensor([3.5, 10.5])
+    init = snapshot(s)
+    danger0 = ref_torch_sim.danger_map(
+        s.fuse, s.wall, s._blast_map(), cfg.fuse, s.brick, cfg.max_chain,
+        early_exit=False, blast_max_hint=7, chain_cap=cfg.chain_cap_rounds).numpy().copy()
+    a = np.full((n, 2, 2), 0, dtype=np.int64)
+    a[..., 0] = 4
+    s._rand_buf = torch.zeros(2 * n * 2)
+    r, d, info = s.step(torch.from_numpy(a), auto_reset=False)
+    out = {f"init_{k}": v for k, v in init.items()}
+    out.update({f"state_{k}": v for k, v in snapshot(s).items()})
+    out.update(resolve_hint=np.int64(s._res_cached.__defaults__[0]))
+    out.update(actions=a, reward=r.numpy(), covered=info["blast"].numpy(),
+               trig=info["trig"].numpy(), danger_init=danger0,
+               danger=s._dng_cache.numpy())
+    np.savez_compressed(os.path.join(HERE, "deep_chain.npz"), **out)
+    print("deep_chain: trig per env", info["trig"].flatten(1).sum(1).tolist())
+
+
+def mlp(traj_name="pillars70"):
+    torch.manual_seed(0)
+    net = ActorCritic((14, 13, 13), arch="mlp", n_players=2)
+    # Perturb biases and LayerNorm affine terms so every parameter matters.
+    g = torch.Generator().manual_seed(1)
+    with torch.no_grad():
+        for name, prm in net.named_parameters():
+            if name.endswith("bias") or ".1." in name or ".4." in name:
+                prm.add_(0.1 * torch.randn(prm.shape, generator=g))
+    z = np.load(os.path.join(HERE, f"traj_{traj_name}.npz"))
+    obs = torch.from_numpy(z["obs"][::4].reshape(-1, 14, 13, 13)[:96].copy())
+    b = obs.shape[0]
+    mm = torch.from_numpy(z["mm"][::4, :4].reshape(-1, 2, 5)[:b].copy())
+    bm = torch.from_numpy(z["bm"][::4, :4].reshape(-1, 2, 2)[:b].copy())
+    acts = torch.from_numpy(z["actions"][::4, :4].reshape(-1, 2, 2)[:b].copy())
+    out = {k: v.numpy().copy() for k, v in net.state_dict().items()}
+    out = {"w_" + k.replace(".", "_"): v for k, v in out.items()}
+    out["obs"] = obs.numpy()
+    out["mm"] = mm.numpy()
+    out["bm"] = bm.numpy()
+    out["actions"] = acts.numpy()
+    with torch.no_grad():
+        for pid in range(2):
+            ml, bl, v = net(obs, pid)
+            lp, ent, v2 = net.evaluate(obs, mm[:, pid], bm[:, pid], acts[:, pid], pid)
+            out[f"move_logits_{pid}"] = ml.numpy()
+            out[f"bomb_logits_{pid}"] = bl.numpy()
+            out[f"value_{pid}"] = v.numpy()
+            out[f"logp_{pid}"] = lp.numpy()
+            out[f"entropy_{pid}"] = ent.numpy()
+    out["param_count"] = np.int64(sum(p.numel() for p in net.parameters()))
+    np.savez_compressed(os.path.join(HERE, "mlp.npz"), **out)
+    print("mlp: batch", b, "params", int(out["param_count"]))
+
+
+if __name__ == "__main__":
+    rollout("pillars0", MapSpec(kind="pillars", brick_p=0.0), "legal", ticks=128, seed=0)
+    rollout("pillars70", MapSpec(kind="pillars", brick_p=0.7), "legal", ticks=128, seed=3)
+    rollout("stress40", MapSpec(kind="pillars", brick_p=0.4, bombs_cap=(1, 4),
+                                blast_cap=(2, 5)), "inject", ticks=128, seed=5)
+    rollout("deathmatch", MapSpec(kind="pillars", brick_p=0.3, bombs_cap=(2, 4),
+                                  blast_cap=(2, 3)), "inject", ticks=96, seed=7,
+            cfg_kw=dict(max_hp=2, invuln_ticks=4, max_steps=70))
+    deep_chain()
+    mlp()
