@@ -1,0 +1,121 @@
+/*
+ * qqt_hip.h - C ABI of the MI355X rollout hot path (libqqt_hip.so).
+ *
+ * Every entry point takes plain device pointers and sizes plus a hipStream_t
+ * (passed as void*), launches asynchronously on that stream, never allocates
+ * and never synchronises.  It returns 0 on success or a negative QQT_E* code;
+ * qqt_last_error() then describes the failure (thread-local).
+ *
+ * Device state of one batched sim (N envs, H x W grid, P players), all
+ * env-major:
+ *   cells   int32 [N][H*W]  cell word: bits 0-7 fuse (0..255), 8-15 owner
+ *                           (int8, -1 = none), 16-23 bomb_blast, 24 wall,
+ *                           25 brick, 26 crate, 27 recycle-crate
+ *   players int32 [N][P][16] player record (slots QQT_P_*; float slots hold
+ *                           IEEE-754 bits)
+ *   envs    int32 [N][4]    t, crate_prob (float bits), map_kind, reserved
+ * Reference layout (N,H,W) / (N,P) tensors are converted by the Python host
+ * layer (qqtsim/state.py).
+ */
+#ifndef QQT_HIP_H
+#define QQT_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QQT_ABI_VERSION 1
+
+#define QQT_OK 0
+#define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
+#define QQT_E_LAUNCH (-2)   /* kernel launch failed */
+#define QQT_E_UNSUPPORTED (-3) /* grid/player combination not compiled */
+
+/* player record slots */
+enum {
+  QQT_P_Y = 0, QQT_P_X = 1, QQT_P_ALIVE = 2, QQT_P_HP = 3, QQT_P_SINCE_BOMB = 4,
+  QQT_P_BOMBS_CAP = 5, QQT_P_BLAST_CAP = 6, QQT_P_SPD = 7, QQT_P_INVULN = 8,
+  QQT_P_COMBO = 9, QQT_P_LAST_HIT = 10, QQT_P_PENDING_LOST = 11,
+  QQT_P_LO_BOMBS = 12, QQT_P_LO_BLAST = 13, QQT_P_LO_SPD = 14, QQT_P_SLOTS = 16
+};
+/* env record slots */
+enum { QQT_E_T = 0, QQT_E_CRATE_PROB = 1, QQT_E_MAP_KIND = 2, QQT_E_SLOTS = 4 };
+
+/* Rule constants of one sim; mirrors the SimConfig fields the tick reads
+ * (reference sim/config.py:102-443).  Float fields are the float32 values
+ * the reference's tensor ops use (Python doubles rounded once). */
+typedef struct qqt_sim_config {
+  int32_t height, width, n_players;
+  int32_t fuse, blast, max_steps, max_chain, chain_cap_rounds;
+  int32_t max_hp, invuln_ticks, hit_attr_penalty, place_dist_cooldown;
+  int32_t growth_bombs_max, growth_blast_max, corridor, timeout_draw, win_hp_scaled;
+  float radius, step_len, pos_hi_y, pos_hi_x;
+  float step_penalty, hit_reward, win_bonus, win_per_hp, danger_penalty, brick_reward;
+  float place_cover_reward, place_chain_reward, place_dist_reward, place_dist_radius;
+  float chain_time_factor, chain_time_rest;   /* rest = 1 - chain_time_factor */
+  float combo_reward, combo_gap_factor;
+  float growth_speed_step, growth_speed_max, hit_speed_drop; /* drop = pen*step */
+  float recycle_crate_prob, growth_crate_prob;
+  /* reset template (qqtsim/maps.py MapSpec) */
+  int32_t map_kind, swap_spawns, bombs_lo, bombs_hi, blast_lo, blast_hi, spawn_cooldown;
+  float brick_p, spawn_speed;
+} qqt_sim_config;
+
+/* modes of qqt_tick */
+#define QQT_MODE_STEP 0     /* one tick, then auto-reset, observe and masks */
+#define QQT_MODE_OBSERVE 1  /* observe + masks of the current state only */
+#define QQT_MODE_RESET 2    /* template reset where reset_mask, then observe */
+#define QQT_MODE_PROBE 3    /* largest bomb_blast after this tick's placement */
+
+typedef struct qqt_tick_args {
+  int32_t n_envs;
+  int32_t mode;
+  int32_t auto_reset;         /* STEP: reset envs that finish */
+  int32_t resolve_tiers;      /* blast tiers the explosion resolves (see sim.py) */
+  float explore_coef;         /* annealing alpha of the shaping rewards */
+  float danger_coef;          /* explore_coef * danger_penalty (rounded once) */
+  uint64_t seed;              /* Philox key */
+  uint32_t tick;              /* keys per-tick uniforms (crates) */
+  uint32_t epoch;             /* keys template draws of this call's resets */
+  /* state (in/out) */
+  int32_t* cells;
+  int32_t* players;
+  int32_t* envs;
+  /* inputs */
+  const int64_t* actions;     /* STEP: [N][P][2] move, bomb (int64) */
+  const int8_t* actions_i8;   /* or the same as int8 (one of the two) */
+  const float* crate_u;       /* STEP: [P][2][N] or NULL = Philox stream */
+  const uint8_t* reset_mask;  /* RESET: [N] */
+  /* outputs (NULL = not wanted, except obs/masks in STEP/OBSERVE/RESET) */
+  float* reward;              /* [N][P] */
+  uint8_t* done;              /* [N] */
+  int32_t* n_alive;           /* [N] */
+  uint8_t* died;              /* [N][P] */
+  uint8_t* winner;            /* [N][P] */
+  uint32_t* covered;          /* [N][8] bitset of the tick's flame cover */
+  uint32_t* triggered;        /* [N][8] bitset of the tick's exploded bombs */
+  uint16_t* obs;              /* [N][5P+4][H][W] float16 bits */
+  uint8_t* move_mask;         /* [N][P][5] */
+  uint8_t* bomb_mask;         /* [N][P][2] */
+  int32_t* probe_out;         /* PROBE: [N] largest bomb_blast */
+} qqt_tick_args;
+
+/* ABI version (QQT_ABI_VERSION). */
+int qqt_abi_version(void);
+
+/* Last error message of this thread ("" if none). */
+const char* qqt_last_error(void);
+
+/* One launch of the fused tick kernel.  Replaces, on the device, the
+ * reference's BatchedSim.step (sim/torch_sim.py:895-1261) followed by
+ * BatchedSim.observe (:605-627) and BatchedSim.legal_mask (:636-645), plus
+ * reset_ (:178-420) with template maps, per `mode`. */
+int qqt_tick(const qqt_sim_config* cfg, const qqt_tick_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QQT_HIP_H */

@@ -1,0 +1,88 @@
+// Shared device helpers: Philox4x32-10, unit uniforms, the sampler's exp/log.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qqt {
+
+// Philox stream ids (third counter word); the host oracle uses the same ids.
+enum : uint32_t {
+  STREAM_CRATE = 1, STREAM_RESET_CELL = 2, STREAM_RESET_MISC = 3,
+  STREAM_POLICY = 4, STREAM_RANDOM_ACT = 5, STREAM_INJECT_ACT = 6, STREAM_BOT = 7
+};
+
+// Philox4x32 with 10 rounds (Salmon et al., SC'11).  c holds the counter on
+// entry and the four output words on exit.
+__device__ __forceinline__ void philox10(uint32_t c[4], uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint32_t lo0 = 0xD2511F53u * c[0];
+    const uint32_t hi0 = __umulhi(0xD2511F53u, c[0]);
+    const uint32_t lo1 = 0xCD9E8D57u * c[2];
+    const uint32_t hi1 = __umulhi(0xCD9E8D57u, c[2]);
+    const uint32_t n0 = hi1 ^ c[1] ^ k0;
+    const uint32_t n2 = hi0 ^ c[3] ^ k1;
+    c[0] = n0; c[1] = lo1; c[2] = n2; c[3] = lo0;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+}
+
+// 24 random bits -> float in [0, 1), exact.
+__device__ __forceinline__ float unit24(uint32_t x) {
+  return (float)(x >> 8) * (1.0f / 16777216.0f);
+}
+
+// Uniform j of Philox(key=seed, ctr=(env, epoch, stream, j / 4)), word j % 4.
+__device__ __forceinline__ float philox_uniform(uint64_t seed, uint32_t env, uint32_t epoch,
+                                                uint32_t stream, uint32_t j) {
+  uint32_t c[4] = {env, epoch, stream, j >> 2};
+  philox10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+  const uint32_t w = (j & 3) == 0 ? c[0] : (j & 3) == 1 ? c[1] : (j & 3) == 2 ? c[2] : c[3];
+  return unit24(w);
+}
+
+// Four uniforms of one block.
+__device__ __forceinline__ void philox_block(uint64_t seed, uint32_t env, uint32_t epoch,
+                                             uint32_t stream, uint32_t block, float u[4]) {
+  uint32_t c[4] = {env, epoch, stream, block};
+  philox10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+  u[0] = unit24(c[0]); u[1] = unit24(c[1]); u[2] = unit24(c[2]); u[3] = unit24(c[3]);
+}
+
+// exp(x) for x <= 0 (Cody-Waite reduction, degree-6 Taylor polynomial), 0 below
+// -80.  Same float32 operation sequence as the host sampler (no contraction).
+__device__ __forceinline__ float exp_q(float x) {
+  if (x < -80.0f) return 0.0f;
+  const float n = rintf(x * 1.4426950408889634f);
+  const float r = (x - n * 0.693145751953125f) - n * 1.428606765330187e-06f;
+  float p = 1.0f / 720.0f;
+  p = p * r + 1.0f / 120.0f;
+  p = p * r + 1.0f / 24.0f;
+  p = p * r + 1.0f / 6.0f;
+  p = p * r + 0.5f;
+  p = p * r + 1.0f;
+  p = p * r + 1.0f;
+  const float scale = __int_as_float(((int)n + 127) << 23);
+  return p * scale;
+}
+
+// log(x) for normal x > 0: x = 2^k m, m in [sqrt(1/2), sqrt(2)), 2 atanh series.
+__device__ __forceinline__ float log_q(float x) {
+  const int bits = __float_as_int(x);
+  int k = ((bits >> 23) & 0xFF) - 127;
+  float m = __int_as_float((bits & 0x7FFFFF) | (127 << 23));
+  if (m >= 1.4142135623730951f) { m = m * 0.5f; k += 1; }
+  const float s = __fdiv_rn(m - 1.0f, m + 1.0f);
+  const float s2 = s * s;
+  float q = 1.0f / 9.0f;
+  q = q * s2 + 1.0f / 7.0f;
+  q = q * s2 + 1.0f / 5.0f;
+  q = q * s2 + 1.0f / 3.0f;
+  q = q * s2 + 1.0f;
+  const float lm = 2.0f * (s * q);
+  return (float)k * 0.6931471805599453f + lm;
+}
+
+}  // namespace qqt

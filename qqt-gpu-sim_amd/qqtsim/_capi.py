@@ -1,0 +1,85 @@
+"""ctypes binding of libqqt_hip.so (include/qqt_hip.h).
+
+The library is loaded after `torch` so that it binds to the HIP runtime torch
+already loaded (same SONAME).  Nothing here falls back to a CPU path: a
+missing library or a failed launch raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (load torch's HIP runtime first)
+
+from ._build import LIB
+
+ABI_VERSION = 1
+
+MODE_STEP, MODE_OBSERVE, MODE_RESET, MODE_PROBE = 0, 1, 2, 3
+
+_i32, _f32, _u32, _u64, _vp = (ctypes.c_int32, ctypes.c_float, ctypes.c_uint32,
+                               ctypes.c_uint64, ctypes.c_void_p)
+
+
+class SimConfigC(ctypes.Structure):
+    _fields_ = [(n, _i32) for n in (
+        "height", "width", "n_players", "fuse", "blast", "max_steps", "max_chain",
+        "chain_cap_rounds", "max_hp", "invuln_ticks", "hit_attr_penalty",
+        "place_dist_cooldown", "growth_bombs_max", "growth_blast_max", "corridor",
+        "timeout_draw", "win_hp_scaled")] + [(n, _f32) for n in (
+        "radius", "step_len", "pos_hi_y", "pos_hi_x", "step_penalty", "hit_reward",
+        "win_bonus", "win_per_hp", "danger_penalty", "brick_reward", "place_cover_reward",
+        "place_chain_reward", "place_dist_reward", "place_dist_radius", "chain_time_factor",
+        "chain_time_rest", "combo_reward", "combo_gap_factor", "growth_speed_step",
+        "growth_speed_max", "hit_speed_drop", "recycle_crate_prob", "growth_crate_prob")] + [
+        (n, _i32) for n in ("map_kind", "swap_spawns", "bombs_lo", "bombs_hi", "blast_lo",
+                            "blast_hi", "spawn_cooldown")] + [
+        (n, _f32) for n in ("brick_p", "spawn_speed")]
+
+
+class TickArgsC(ctypes.Structure):
+    _fields_ = [("n_envs", _i32), ("mode", _i32), ("auto_reset", _i32),
+                ("resolve_tiers", _i32), ("explore_coef", _f32), ("danger_coef", _f32),
+                ("seed", _u64), ("tick", _u32), ("epoch", _u32)] + [
+        (n, _vp) for n in ("cells", "players", "envs", "actions", "actions_i8", "crate_u",
+                           "reset_mask", "reward", "done", "n_alive", "died", "winner",
+                           "covered", "triggered", "obs", "move_mask", "bomb_mask",
+                           "probe_out")]
+
+
+_LIB = None
+
+
+def lib():
+    """The loaded library (raises if it is missing or has another ABI)."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB):
+            raise RuntimeError(
+                f"{LIB} is not built; run `python -m qqtsim._build` (HIP path required)")
+        L = ctypes.CDLL(LIB)
+        L.qqt_abi_version.restype = ctypes.c_int
+        L.qqt_last_error.restype = ctypes.c_char_p
+        L.qqt_tick.restype = ctypes.c_int
+        L.qqt_tick.argtypes = [ctypes.POINTER(SimConfigC), ctypes.POINTER(TickArgsC), _vp]
+        if L.qqt_abi_version() != ABI_VERSION:
+            raise RuntimeError("libqqt_hip.so ABI version mismatch; rebuild it")
+        _LIB = L
+    return _LIB
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        msg = lib().qqt_last_error().decode(errors="replace")
+        if rc == -1:
+            raise ValueError(msg)
+        raise RuntimeError(f"qqt_hip error {rc}: {msg}")
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

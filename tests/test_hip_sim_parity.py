@@ -1,0 +1,153 @@
+"""HIP tick kernel vs the oracle / reference vectors (needs an MI355X).
+
+Bar: grid, bomb, hp, done and every other integer state bit-exact; positions
+bit-exact (the kernel follows the reference's float32 operation order);
+observations bit-exact in float16; rewards within 1e-5 absolute (the tolerance
+north of the float32 summation-order differences in the placement reward and
+the device powf of the combo factor; the spec bound is 1e-3).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from golden_io import TRAJ_CFG, json_state_tensors, json_states, state_at, traj
+
+pytestmark = pytest.mark.gpu
+
+REWARD_ATOL = 1e-5
+INT_KEYS = ("wall", "brick", "crate", "recycle", "fuse", "owner", "bomb_blast", "alive",
+            "hp", "since_bomb", "t", "bombs_cap", "blast_cap", "invuln", "combo",
+            "last_hit", "pending_lost")
+FLOAT_KEYS = ("pos", "spd_g")
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+def _compare_state(hip_sd, ref, tick, keys=INT_KEYS + FLOAT_KEYS):
+    for k in keys:
+        a = hip_sd[k].cpu().numpy()
+        b = ref[k].cpu().numpy() if torch.is_tensor(ref[k]) else ref[k]
+        np.testing.assert_array_equal(a, b.astype(a.dtype), err_msg=f"{k} after tick {tick}")
+
+
+@pytest.mark.parametrize("name", list(TRAJ_CFG))
+def test_hip_replays_reference_trajectory(dev, name):
+    from qqtsim.config import corridor_training_config
+    from qqtsim.maps import MapSpec
+    from qqtsim.sim import HipBatchedSim
+
+    z = traj(name)
+    cfg = corridor_training_config(**TRAJ_CFG[name])
+    n = z["init_fuse"].shape[0]
+    sim = HipBatchedSim(cfg, n, device=dev, seed=0, map_spec=MapSpec())
+    init = state_at(z, 0)
+    init.update(lo_bombs=init["bombs_cap"], lo_blast=init["blast_cap"], lo_spd=init["spd_g"],
+                crate_prob=torch.full((n,), cfg.growth_crate_prob), map_kind=torch.zeros(n))
+    sim.load_state_dict(init)
+    sim.resolve_tiers = int(z["resolve_hint"])
+    ticks = z["actions"].shape[0]
+    worst = 0.0
+    for t in range(ticks):
+        mm, bm = sim.legal_mask()
+        np.testing.assert_array_equal(mm.cpu().numpy(), z["mm"][t], err_msg=f"mm tick {t}")
+        np.testing.assert_array_equal(bm.cpu().numpy(), z["bm"][t], err_msg=f"bm tick {t}")
+        obs = sim.observe()[:4].cpu().numpy()
+        np.testing.assert_array_equal(obs.view(np.uint16), z["obs"][t].view(np.uint16),
+                                      err_msg=f"obs tick {t}")
+        r, d, info = sim.step(torch.from_numpy(z["actions"][t]), auto_reset=False,
+                              crate_u=torch.from_numpy(z["crate_u"][t]))
+        sd = sim.state_dict()
+        ref = {k: z["state_" + k][t] for k in INT_KEYS + FLOAT_KEYS}
+        _compare_state(sd, ref, t)
+        worst = max(worst, float(np.abs(r.cpu().numpy() - z["reward"][t]).max()))
+        assert worst <= REWARD_ATOL, f"reward tick {t}: {worst}"
+        np.testing.assert_array_equal(d.cpu().numpy(), z["done"][t])
+        np.testing.assert_array_equal(info["n_alive"].cpu().numpy(), z["n_alive"][t])
+        np.testing.assert_array_equal(info["died"].cpu().numpy(), z["died"][t])
+        np.testing.assert_array_equal(info["winner"].cpu().numpy(), z["winner"][t])
+        np.testing.assert_array_equal(info["blast"].cpu().numpy(), z["covered"][t])
+        np.testing.assert_array_equal(info["trig"].cpu().numpy(), z["trig"][t])
+    mm, bm = sim.legal_mask()
+    np.testing.assert_array_equal(mm.cpu().numpy(), z["mm"][ticks])
+    print(f"{name}: {ticks} ticks bit-exact, worst reward diff {worst:.3g}")
+
+
+@pytest.mark.parametrize("name", ["ref_state.json", "sweep_states.json"])
+def test_hip_observe_matches_reference_json_fixtures(dev, name):
+    """Observation (float16 of the fixtures' float32 values) and masks of the
+    reference's single-state fixtures, all states in one batch."""
+    from qqtsim.config import SimConfig
+    from qqtsim.sim import HipBatchedSim
+
+    states = json_states(name)
+    cfg = SimConfig(height=13, width=13, n_players=2, map_mode="corridor", speed=3.0,
+                    max_steps=1800)
+    n = len(states)
+    sim = HipBatchedSim(cfg, n, device=dev)
+    parts = [json_state_tensors(s) for s in states]
+    snap = {k: torch.cat([p[k] for p in parts]) for k in parts[0]}
+    snap["recycle"] = torch.zeros_like(snap["wall"])
+    sim.load_state_dict(snap)
+    obs = sim.observe().cpu().numpy()
+    mm, bm = sim.legal_mask()
+    for i, s in enumerate(states):
+        want = np.float32(s["obs"]).astype(np.float16).reshape(obs.shape[1:])
+        np.testing.assert_array_equal(obs[i].view(np.uint16), want.view(np.uint16),
+                                      err_msg=f"obs state {i}")
+        np.testing.assert_array_equal(mm[i].int().cpu().numpy(), np.array(s["mm"]))
+        np.testing.assert_array_equal(bm[i].int().cpu().numpy(), np.array(s["bm"]))
+
+
+@pytest.mark.parametrize("spec_name,n,ticks", [("pillars70", 256, 48), ("stress40", 256, 48)])
+def test_hip_matches_oracle_with_auto_reset(dev, spec_name, n, ticks):
+    """Random legal / injected actions with auto-reset and Philox crate
+    uniforms: the HIP sim and the oracle stay bit-exact tick after tick."""
+    from oracle import philox
+    from oracle.policy import sample_masked
+    from oracle.sim import OracleSim
+    from qqtsim.config import corridor_training_config
+    from qqtsim.maps import MapSpec
+    from qqtsim.sim import HipBatchedSim
+
+    spec = {"pillars70": MapSpec(kind="pillars", brick_p=0.7, swap_spawns=True),
+            "stress40": MapSpec(kind="pillars", brick_p=0.4, bombs_cap=(1, 4),
+                                blast_cap=(2, 5))}[spec_name]
+    cfg = corridor_training_config(max_hp=2, invuln_ticks=3, max_steps=40)
+    seed = 11
+    hip = HipBatchedSim(cfg, n, device=dev, seed=seed, map_spec=spec)
+    ora = OracleSim(cfg, n, spec, seed=seed)
+    _compare_state(hip.state_dict(), ora.state_dict(), -1,
+                   INT_KEYS + FLOAT_KEYS + ("lo_bombs", "lo_blast", "lo_spd", "crate_prob"))
+    resets = 0
+    for t in range(ticks):
+        mm, bm = ora.legal_mask()
+        hm, hb = hip.legal_mask()
+        np.testing.assert_array_equal(hm.cpu().numpy(), mm.numpy(), err_msg=f"mm {t}")
+        np.testing.assert_array_equal(hb.cpu().numpy(), bm.numpy(), err_msg=f"bm {t}")
+        np.testing.assert_array_equal(hip.observe().cpu().numpy().view(np.uint16),
+                                      ora.observe().numpy().view(np.uint16), err_msg=f"obs {t}")
+        u = philox.uniforms(seed, np.arange(n), t, philox.STREAM_RANDOM_ACT, 4)
+        a = np.zeros((n, 2, 2), dtype=np.int64)
+        for i in range(2):
+            a[:, i, 0] = sample_masked(mm[:, i].numpy().astype(np.float32), mm[:, i].numpy(),
+                                       u[:, 2 * i])[0]
+            a[:, i, 1] = sample_masked(bm[:, i].numpy().astype(np.float32), bm[:, i].numpy(),
+                                       u[:, 2 * i + 1])[0]
+        act = torch.from_numpy(a)
+        r1, d1, _ = ora.step(act, auto_reset=True)
+        r2, d2, _ = hip.step(act, auto_reset=True)
+        resets += int(d1.sum())
+        np.testing.assert_array_equal(d2.cpu().numpy(), d1.numpy(), err_msg=f"done {t}")
+        assert float((r2.cpu() - r1).abs().max()) <= REWARD_ATOL, f"reward {t}"
+        _compare_state(hip.state_dict(), ora.state_dict(), t,
+                       INT_KEYS + FLOAT_KEYS + ("lo_bombs", "lo_blast", "lo_spd", "crate_prob"))
+    assert resets > 0, "the run must exercise auto-reset"
+    print(f"{spec_name}: {ticks} ticks x {n} envs bit-exact, {resets} resets")
