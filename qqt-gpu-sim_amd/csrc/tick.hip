@@ -1,24 +1,27 @@
 // Fused rollout tick for gfx950: step + auto-reset + danger + observation +
 // legality masks of a batch of envs in one launch.
 //
-// Mapping: one 64-lane wavefront (= one workgroup) owns EPW = 4 consecutive
-// envs; each env gets 16 lanes.  Lane l of an env walks the cells
-// c = l, l+16, l+32, ...  Per-env grids live in LDS for the whole tick; the
-// observation is staged in LDS in its final (N, C, H, W) float16 layout and
-// leaves with 16-byte stores, so the output stream is written once, fully
-// coalesced.  Per-player scalar work (placement, movement, damage, rewards,
-// masks) runs on a few lanes per env while the grid phases use all 16.
+// Mapping: one 64-lane wavefront (= one workgroup) owns EPW = 64 / LPE
+// consecutive envs; each env gets LPE lanes (LPE = 64 on MI355X: a wavefront
+// per env keeps ~5 waves per SIMD in flight at 5632 envs).  Lane l of an env
+// walks the cells c = l, l + LPE, ...  Per-env grids live in LDS for the
+// whole tick; the observation is staged in LDS in its final (N, C, H, W)
+// float16 layout and leaves with wide, fully coalesced stores.
 //
 // Semantics follow the reference tick (sim/torch_sim.py:895-1261) stage by
-// stage in float32 with the reference's operation order; the library is
-// built with -ffp-contract=off so no product is fused into an add.
+// stage in float32 with the reference's operation order; the library is built
+// with -ffp-contract=off so no product is fused into an add.
 //
-// Chain explosion: flame is scattered from each source cell along its four
-// rays (byte stores of 1 into an LDS cover map are idempotent, so lanes that
-// reach the same cell need no atomics), one synchronous round at a time.
-// Danger map: gathered (each cell scans back along the four directions to
-// the first bomb/brick/wall), never scattered, so max-combining needs no
-// atomics either.
+// Explosions and danger work on a per-env list of bomb cells built with a
+// wavefront ballot, not on all H*W cells:
+// * chain explosion: each source scatters its four rays into a byte cover
+//   map; stores of 1 are idempotent, so overlapping rays need no atomics;
+// * danger stage A: each bomb gathers from its (at most four) in-neighbours,
+//   the first solid cell behind it in each direction, for a fixed number of
+//   synchronous rounds;
+// * danger stage B: bombs scatter their corrected weight one direction at a
+//   time.  Within one direction two rays never share a cell (the nearer bomb
+//   stops the farther one's ray), so a plain LDS max-update is race free.
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -31,10 +34,8 @@
 
 namespace qqt {
 
-constexpr int EPW = 4;   // envs per wavefront
-constexpr int LPE = 16;  // lanes per env
-
 constexpr uint32_t F_WALL = 1u << 24, F_BRICK = 1u << 25, F_CRATE = 1u << 26, F_REC = 1u << 27;
+constexpr uint32_t EMPTY_CELL = 0x0000FF00u;  // fuse 0, owner -1, blast 0, no flags
 
 __device__ __forceinline__ int cw_fuse(uint32_t w) { return (int)(w & 0xFFu); }
 __device__ __forceinline__ int cw_owner(uint32_t w) { return (int)(int8_t)((w >> 8) & 0xFFu); }
@@ -43,92 +44,122 @@ __device__ __forceinline__ uint32_t cw_make(uint32_t flags, int fuse, int owner,
   return (flags & 0xFF000000u) | ((uint32_t)fuse & 0xFFu) | (((uint32_t)owner & 0xFFu) << 8) |
          (((uint32_t)bb & 0xFFu) << 16);
 }
-
-// Sum / max over the 16 lanes of one env (all 16 lanes receive the result).
-__device__ __forceinline__ int sum16(int v) {
-  v += __shfl_xor(v, 8, 16);
-  v += __shfl_xor(v, 4, 16);
-  v += __shfl_xor(v, 2, 16);
-  v += __shfl_xor(v, 1, 16);
-  return v;
+__device__ __forceinline__ bool cw_solid(uint32_t w) {  // stops flame and players
+  return (w & F_BRICK) || cw_fuse(w) > 0;
 }
-__device__ __forceinline__ int max16(int v) {
-  v = max(v, __shfl_xor(v, 8, 16));
-  v = max(v, __shfl_xor(v, 4, 16));
-  v = max(v, __shfl_xor(v, 2, 16));
-  v = max(v, __shfl_xor(v, 1, 16));
-  return v;
+__device__ __forceinline__ int blast_of(uint32_t w, int cfg_blast) {
+  const int b = cw_bb(w);
+  return b > 0 ? b : cfg_blast;
 }
 
-template <int H, int W, int P>
+// Danger weight (1 - (f-1)/FUSE)^2 clamped at 0 (sim/blast.py:218-220).
+__device__ __forceinline__ float bomb_weight(int f, float fuse_max) {
+  const float raw = 1.0f - __fdiv_rn((float)f - 1.0f, fuse_max);
+  const float v = raw > 0.0f ? raw : 0.0f;
+  return v * v;
+}
+
+__device__ __forceinline__ int dir_dr(int d) { return d == 0 ? -1 : (d == 1 ? 1 : 0); }
+__device__ __forceinline__ int dir_dc(int d) { return d == 2 ? -1 : (d == 3 ? 1 : 0); }
+
+template <int H, int W, int P, int LPE_>
 struct Geo {
+  static constexpr int LPE = LPE_;
+  static constexpr int EPW = 64 / LPE;
   static constexpr int C = H * W;
+  static constexpr int CW4 = (C + 3) / 4;       // dwords of a byte map
   static constexpr int NCH = 5 * P + 4;
-  static constexpr int OBS = NCH * C;  // float16 values per env
-  static constexpr int MAXR = (H > W ? H : W) - 1;  // longest in-grid ray
+  static constexpr int OBS = NCH * C;          // float16 values per env
+  static constexpr int KMAX = (C + LPE - 1) / LPE;
 };
 
-template <int H, int W, int P>
+template <class G, int P>
 struct __align__(16) Lds {
-  using G = Geo<H, W, P>;
-  uint16_t obs[EPW][G::OBS];
-  uint32_t cw[EPW][G::C];
-  float fw[EPW][G::C];   // danger: stage-A front / stage-B sender weight
-  float dng[EPW][G::C];  // danger output
-  uint8_t cov[EPW][G::C];
-  uint8_t trg[EPW][G::C];
-  int32_t pl[EPW][P][QQT_P_SLOTS];
-  int32_t ev[EPW][QQT_E_SLOTS];
-  int32_t alive0[EPW][P], hp0[EPW][P], placed[EPW][P], live[EPW][P];
-  int32_t fpre[EPW][P], fpost[EPW][P], act_m[EPW][P], act_b[EPW][P];
-  float pbonus[EPW][P];
-  float splat_w[EPW][P][4];
-  int32_t splat_i[EPW][P][4];
-  int32_t done[EPW];
-  int32_t any[EPW];
+  float dd[G::EPW][4][G::C];  // danger stage B: per-direction ray values
+  // observation staging: envs back to back in output layout, placed at byte
+  // offset (output address mod 16) so that copy-out can use 16-byte units
+  uint8_t obs_raw[(G::EPW * G::OBS * 2 + 16 + 15) / 16 * 16];
+  uint32_t cw[G::EPW][G::C];
+  float fw[G::EPW][G::C];    // danger stage-A front (by cell)
+  float dng[G::EPW][G::C];   // danger map
+  float wl[G::EPW][G::C];    // per listed bomb: corrected weight
+  uint32_t cov[G::EPW][G::CW4];  // byte maps viewed as dwords for clearing
+  uint32_t trg[G::EPW][G::CW4];
+  uint16_t edge[G::EPW][G::C][4];  // stage-A in-edge per listed bomb: sender | dist << 8
+  uint8_t list[G::EPW][G::C];
+  int32_t nlist[G::EPW];
+  int32_t pl[G::EPW][P][QQT_P_SLOTS];
+  int32_t ev[G::EPW][QQT_E_SLOTS];
+  int32_t alive0[G::EPW][P], hp0[G::EPW][P], placed[G::EPW][P], live[G::EPW][P];
+  int32_t fpre[G::EPW][P], fpost[G::EPW][P], act_m[G::EPW][P], act_b[G::EPW][P];
+  float pbonus[G::EPW][P];
+  int32_t done[G::EPW];
+  int32_t boom[G::EPW];
 };
 
-struct DevCfg {
-  qqt_sim_config c;
-};
+// ---------------------------------------------------------------- lane helpers
+template <int LPE>
+__device__ __forceinline__ int env_sum(int v) {
+#pragma unroll
+  for (int m = LPE / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, LPE);
+  return v;
+}
+template <int LPE>
+__device__ __forceinline__ int env_max(int v) {
+#pragma unroll
+  for (int m = LPE / 2; m >= 1; m >>= 1) v = max(v, __shfl_xor(v, m, LPE));
+  return v;
+}
+template <int LPE>
+__device__ __forceinline__ uint64_t env_bits(bool pred, int e) {
+  const uint64_t b = __ballot(pred);
+  return LPE == 64 ? b : ((b >> (LPE * e)) & ((1ull << LPE) - 1ull));
+}
+
+// Number of cells c = l + LPE*k (k < KMAX) of this env satisfying pred (same
+// result in every lane of the env; the popcounts run on the scalar unit).
+template <class G, class Pred>
+__device__ __forceinline__ int env_count(int e, int l, Pred pred) {
+  int n = 0;
+#pragma unroll
+  for (int k = 0; k < G::KMAX; ++k) {
+    const int c = l + G::LPE * k;
+    n += __popcll(env_bits<G::LPE>(c < G::C && pred(c), e));
+  }
+  return n;
+}
 
 // ---------------------------------------------------------------- movement
 // One axis of the AABB slide-stop resolution (sim/move.py:154-231).
-template <int H, int W>
-__device__ __forceinline__ bool blocked_pair(const uint32_t* cw, int r0, int c0, int r1, int c1,
-                                             float yb, float xb, float rad) {
-  const bool oob = (r0 < 0) | (r0 >= H) | (c0 < 0) | (c0 >= W) | (r1 < 0) | (r1 >= H) |
-                   (c1 < 0) | (c1 >= W);
-  const int i0 = min(max(r0, 0), H - 1) * W + min(max(c0, 0), W - 1);
-  const int i1 = min(max(r1, 0), H - 1) * W + min(max(c1, 0), W - 1);
-  const uint32_t w0 = cw[i0], w1 = cw[i1];
-  const bool s0 = (w0 & (F_WALL | F_BRICK)) || cw_fuse(w0) > 0;
-  const bool s1 = (w1 & (F_WALL | F_BRICK)) || cw_fuse(w1) > 0;
-  const int top = (int)floorf(yb - rad), bot = (int)floorf(yb + rad);
-  const int lef = (int)floorf(xb - rad), rig = (int)floorf(xb + rad);
-  const bool in0 = (r0 >= top) & (r0 <= bot) & (c0 >= lef) & (c0 <= rig);
-  const bool in1 = (r1 >= top) & (r1 <= bot) & (c1 >= lef) & (c1 <= rig);
-  return oob | (s0 & !in0) | (s1 & !in1);
-}
-
+// `coord`/`delta` are the moved coordinate and displacement on this axis;
+// (y, x) is the pre-move centre.  The two probed cells of a lead line lie at
+// the box's own extent on the other axis (floor(other -+ r) with other the
+// box centre), so the reference's "cell inside the current box" test reduces
+// to the lead coordinate lying inside the box's extent on this axis.
 template <int H, int W>
 __device__ __forceinline__ float resolve_axis(const uint32_t* cw, float coord, float delta,
-                                              float other, float y, float x, float rad,
-                                              bool vertical) {
+                                              float y, float x, float rad, bool vertical) {
   const float eps = 1e-4f;
+  const float own = vertical ? y : x, other = vertical ? x : y;
+  const int lim_own = vertical ? H : W, lim_oth = vertical ? W : H;
   const float sgn = delta > 0.0f ? 1.0f : (delta < 0.0f ? -1.0f : 0.0f);
   const int old_lead = (int)floorf((coord - delta) + sgn * rad);
   const int new_lead = (int)floorf(coord + sgn * rad);
   const int lo = min(old_lead, new_lead), hi = max(old_lead, new_lead);
   const int a0 = (int)floorf(other - rad), a1 = (int)floorf(other + rad);
-  bool hit_lo, hit_hi;
-  if (vertical) {
-    hit_lo = blocked_pair<H, W>(cw, lo, a0, lo, a1, y, x, rad);
-    hit_hi = blocked_pair<H, W>(cw, hi, a0, hi, a1, y, x, rad);
-  } else {
-    hit_lo = blocked_pair<H, W>(cw, a0, lo, a1, lo, y, x, rad);
-    hit_hi = blocked_pair<H, W>(cw, a0, hi, a1, hi, y, x, rad);
-  }
+  const int b0 = (int)floorf(own - rad), b1 = (int)floorf(own + rad);
+  const bool span_oob = (a0 < 0) | (a0 >= lim_oth) | (a1 < 0) | (a1 >= lim_oth);
+  const int a0c = min(max(a0, 0), lim_oth - 1), a1c = min(max(a1, 0), lim_oth - 1);
+  auto hit = [&](int lead) -> bool {
+    const int lc = min(max(lead, 0), lim_own - 1);
+    const uint32_t w0 = vertical ? cw[lc * W + a0c] : cw[a0c * W + lc];
+    const uint32_t w1 = vertical ? cw[lc * W + a1c] : cw[a1c * W + lc];
+    const bool blk = (w0 & F_WALL) || cw_solid(w0) || (w1 & F_WALL) || cw_solid(w1);
+    const bool inside = (lead >= b0) & (lead <= b1);
+    return span_oob | (lead < 0) | (lead >= lim_own) | (blk & !inside);
+  };
+  const bool hit_lo = hit(lo);
+  const bool hit_hi = hi == lo ? hit_lo : hit(hi);
   const bool fwd = sgn > 0.0f;
   const int first_lead = fwd ? hi : lo, second_lead = fwd ? lo : hi;
   const bool fh = fwd ? hit_hi : hit_lo, sh = fwd ? hit_lo : hit_hi;
@@ -138,32 +169,34 @@ __device__ __forceinline__ float resolve_axis(const uint32_t* cw, float coord, f
   return (fh | sh) ? stop : coord;
 }
 
-__device__ __forceinline__ int blast_of(uint32_t w, int cfg_blast) {
-  const int b = cw_bb(w);
-  return b > 0 ? b : cfg_blast;
-}
-
-// Danger weight (1 - (f-1)/FUSE)^2 clamped at 0 (sim/blast.py:218-220).
-__device__ __forceinline__ float bomb_weight(int f, float fuse_max) {
-  if (f <= 0) return 0.0f;
-  const float raw = 1.0f - __fdiv_rn((float)f - 1.0f, fuse_max);
-  const float v = raw > 0.0f ? raw : 0.0f;
-  return v * v;
+// Collect the cells satisfying `pred` into list[] (ascending cell order).
+template <class G, class Pred>
+__device__ __forceinline__ int build_list(uint8_t* list, int e, int l, Pred pred) {
+  int base = 0;
+#pragma unroll
+  for (int k = 0; k < G::KMAX; ++k) {
+    const int c = l + G::LPE * k;
+    const bool p = c < G::C && pred(c);
+    const uint64_t bits = env_bits<G::LPE>(p, e);
+    if (p) list[base + __popcll(bits & ((1ull << l) - 1ull))] = (uint8_t)c;
+    base += __popcll(bits);
+  }
+  return base;
 }
 
 // ---------------------------------------------------------------- kernel
-template <int H, int W, int P>
-__global__ __launch_bounds__(64) void tick_kernel(const DevCfg dc, const qqt_tick_args a) {
-  using G = Geo<H, W, P>;
+template <int H, int W, int P, int LPE>
+__global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const qqt_tick_args a) {
+  using G = Geo<H, W, P, LPE>;
   constexpr int C = G::C;
-  constexpr int NCH = G::NCH;
+  constexpr int EPW = G::EPW;
   constexpr int OBS = G::OBS;
-  __shared__ Lds<H, W, P> s;
-  const qqt_sim_config& cf = dc.c;
+  constexpr int KMAX = G::KMAX;
+  __shared__ Lds<G, P> s;
 
   const int lane = threadIdx.x;
-  const int e = lane >> 4;
-  const int l = lane & 15;
+  const int e = lane / LPE;
+  const int l = lane % LPE;
   const int g = blockIdx.x * EPW + e;
   const bool valid = g < a.n_envs;
   const int mode = a.mode;
@@ -172,55 +205,65 @@ __global__ __launch_bounds__(64) void tick_kernel(const DevCfg dc, const qqt_tic
 
   uint32_t* cw = s.cw[e];
   int32_t(*pl)[QQT_P_SLOTS] = s.pl[e];
+  uint8_t* cov = reinterpret_cast<uint8_t*>(s.cov[e]);
+  uint8_t* trg = reinterpret_cast<uint8_t*>(s.trg[e]);
+  uint8_t* list = s.list[e];
 
   // ---- load
-  for (int c = l; c < C; c += LPE)
-    cw[c] = valid ? (uint32_t)a.cells[(size_t)g * C + c] : (F_WALL | 0x0000FF00u);
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) {
+    const int c = l + LPE * k;
+    if (c < C) cw[c] = valid ? (uint32_t)a.cells[(size_t)g * C + c] : (F_WALL | EMPTY_CELL);
+  }
   for (int i = l; i < P * QQT_P_SLOTS; i += LPE)
     pl[i / QQT_P_SLOTS][i % QQT_P_SLOTS] = valid ? a.players[(size_t)g * P * QQT_P_SLOTS + i] : 0;
   if (l < QQT_E_SLOTS) s.ev[e][l] = valid ? a.envs[(size_t)g * QQT_E_SLOTS + l] : 0;
-  if (l == 0) { s.done[e] = 0; s.any[e] = 0; }
+  if (l == 0) s.done[e] = 0;
+  // per-player inputs, issued together with the state loads
+  int in_mv = 4, in_bb = 0;
+  float in_uh = 0.0f, in_ug = 0.0f;
+  if (mode == QQT_MODE_STEP || mode == QQT_MODE_PROBE) {
+    if (l < P && valid) {
+      if (a.actions) {
+        in_mv = (int)a.actions[((size_t)g * P + l) * 2 + 0];
+        in_bb = (int)a.actions[((size_t)g * P + l) * 2 + 1];
+      } else if (a.actions_i8) {
+        in_mv = a.actions_i8[((size_t)g * P + l) * 2 + 0];
+        in_bb = a.actions_i8[((size_t)g * P + l) * 2 + 1];
+      }
+      if (a.crate_u) {
+        in_uh = a.crate_u[((size_t)l * 2 + 0) * a.n_envs + g];
+        in_ug = a.crate_u[((size_t)l * 2 + 1) * a.n_envs + g];
+      }
+    }
+  }
   __syncthreads();
 
-  bool do_reset = false;
-
   if (mode == QQT_MODE_STEP || mode == QQT_MODE_PROBE) {
-    // ---- 1. snapshots, actions, fuse countdown
+    // ---- 1. snapshots, actions, fuse countdown, live counts
     if (l < P) {
       s.alive0[e][l] = pl[l][QQT_P_ALIVE];
       s.hp0[e][l] = pl[l][QQT_P_HP];
-      int mv = 4, bb = 0;
-      if (valid) {
-        if (a.actions) {
-          mv = (int)a.actions[((size_t)g * P + l) * 2 + 0];
-          bb = (int)a.actions[((size_t)g * P + l) * 2 + 1];
-        } else if (a.actions_i8) {
-          mv = a.actions_i8[((size_t)g * P + l) * 2 + 0];
-          bb = a.actions_i8[((size_t)g * P + l) * 2 + 1];
-        }
-      }
-      s.act_m[e][l] = mv;
-      s.act_b[e][l] = bb;
+      s.act_m[e][l] = in_mv;
+      s.act_b[e][l] = in_bb;
       const float y = __int_as_float(pl[l][QQT_P_Y]), x = __int_as_float(pl[l][QQT_P_X]);
-      const int cy = (int)floorf(y), cx = (int)floorf(x);
-      s.fpre[e][l] = min(max(cy * W + cx, 0), C - 1);
+      s.fpre[e][l] = min(max((int)floorf(y) * W + (int)floorf(x), 0), C - 1);
     }
-    int cnt[P];
 #pragma unroll
-    for (int i = 0; i < P; ++i) cnt[i] = 0;
-    for (int c = l; c < C; c += LPE) {
-      uint32_t w = cw[c];
-      const int f = cw_fuse(w);
-      if (f > 0) { w = (w & ~0xFFu) | (uint32_t)(f - 1); cw[c] = w; }
-      const int o = cw_owner(w);
-      if (cw_fuse(w) > 0) {
-#pragma unroll
-        for (int i = 0; i < P; ++i) cnt[i] += (o == i);
+    for (int k = 0; k < KMAX; ++k) {
+      const int c = l + LPE * k;
+      if (c < C) {
+        const uint32_t w = cw[c];
+        const int f = cw_fuse(w);
+        if (f > 0) cw[c] = (w & ~0xFFu) | (uint32_t)(f - 1);
       }
     }
 #pragma unroll
     for (int i = 0; i < P; ++i) {
-      const int t = sum16(cnt[i]);
+      const int t = env_count<G>(e, l, [&](int c) {
+        const uint32_t w = cw[c];
+        return cw_fuse(w) > 0 && cw_owner(w) == i;
+      });
       if (l == 0) s.live[e][i] = t;
     }
     __syncthreads();
@@ -240,8 +283,12 @@ __global__ __launch_bounds__(64) void tick_kernel(const DevCfg dc, const qqt_tic
 
     if (mode == QQT_MODE_PROBE) {
       int mb = 0;
-      for (int c = l; c < C; c += LPE) mb = max(mb, cw_bb(cw[c]));
-      mb = max16(mb);
+#pragma unroll
+      for (int k = 0; k < KMAX; ++k) {
+        const int c = l + LPE * k;
+        if (c < C) mb = max(mb, cw_bb(cw[c]));
+      }
+      mb = env_max<LPE>(mb);
       if (valid && l == 0) a.probe_out[g] = mb;
       return;
     }
@@ -254,18 +301,18 @@ __global__ __launch_bounds__(64) void tick_kernel(const DevCfg dc, const qqt_tic
       if (me < P && s.placed[e][me]) {
         const int s0 = s.fpre[e][me];
         const uint32_t w0 = cw[s0];
-        const bool seed_ok = !(w0 & (F_WALL | F_BRICK));
-        if (seed_ok) {
+        if (!(w0 & (F_WALL | F_BRICK))) {
           const int r0 = s0 / W, c0 = s0 % W;
-          const int dr = d == 0 ? -1 : (d == 1 ? 1 : 0);
-          const int dcol = d == 2 ? -1 : (d == 3 ? 1 : 0);
+          const int dr = dir_dr(d), dc = dir_dc(d);
           auto visit = [&](int x) {
+#pragma unroll
             for (int o = 0; o < P; ++o)
               if (o != me && s.fpre[e][o] == x && s.alive0[e][o]) cover_bits |= 1 << o;
             const uint32_t wx = cw[x];
             const int fx = cw_fuse(wx);
             if (fx > 0 && cw_owner(wx) >= 0) {
               int pm = 0;
+#pragma unroll
               for (int i = 0; i < P; ++i)
                 if (s.fpre[e][i] == x) pm = s.placed[e][i];
               if (!pm) {
@@ -279,25 +326,25 @@ __global__ __launch_bounds__(64) void tick_kernel(const DevCfg dc, const qqt_tic
           if (d == 0) visit(s0);
           const int b = blast_of(w0, cf.blast);
           for (int k = 1; k <= b; ++k) {
-            const int rr = r0 + k * dr, cc = c0 + k * dcol;
+            const int rr = r0 + k * dr, cc = c0 + k * dc;
             if (rr < 0 || rr >= H || cc < 0 || cc >= W) break;
             const int x = rr * W + cc;
             const uint32_t wx = cw[x];
             if (wx & F_WALL) break;
             visit(x);
-            if ((wx & F_BRICK) || cw_fuse(wx) > 0) break;
+            if (cw_solid(wx)) break;
           }
         }
       }
-      // combine the four direction lanes of each player
-      chain += __shfl_xor(chain, 1, 16);
-      chain += __shfl_xor(chain, 2, 16);
-      cover_bits |= __shfl_xor(cover_bits, 1, 16);
-      cover_bits |= __shfl_xor(cover_bits, 2, 16);
+      chain += __shfl_xor(chain, 1, LPE);
+      chain += __shfl_xor(chain, 2, LPE);
+      cover_bits |= __shfl_xor(cover_bits, 1, LPE);
+      cover_bits |= __shfl_xor(cover_bits, 2, LPE);
       if (me < P && d == 0) {
         float bonus = 0.0f;
         if (s.placed[e][me]) {
           float cover = 0.0f, dist = 0.0f;
+#pragma unroll
           for (int o = 0; o < P; ++o) cover += (float)((cover_bits >> o) & 1);
           if (cf.place_dist_reward > 0.0f) {
             const float ym = floorf(__int_as_float(pl[me][QQT_P_Y]));
@@ -322,41 +369,42 @@ __global__ __launch_bounds__(64) void tick_kernel(const DevCfg dc, const qqt_tic
     }
     __syncthreads();
 
-    // ---- 4. since_bomb; 5. movement (sim/move.py:234-279)
-    if (l < P) {
-      const int me = l;
-      int sb = pl[me][QQT_P_SINCE_BOMB] + 1;
-      if (s.placed[e][me]) sb = 0;
+    // ---- 4. since_bomb; 5. movement (sim/move.py:234-279); explosion list
+    if (l < 2 * P) {  // lane = player * 2 + axis; both axes start from the pre-move box
+      const int me = l >> 1;
+      const bool vert = (l & 1) == 0;
       const float y = __int_as_float(pl[me][QQT_P_Y]), x = __int_as_float(pl[me][QQT_P_X]);
       const int mv = s.act_m[e][me];
       const int mc = min(max(mv, 0), 4);
       const float spd = __int_as_float(pl[me][QQT_P_SPD]);
       const float st = cf.step_len;
-      float ty = 0.0f, tx = 0.0f;
-      if (mc == 0) ty = -st; else if (mc == 1) ty = st; else if (mc == 2) tx = -st; else if (mc == 3) tx = st;
-      float dy = ty * spd, dx = tx * spd;
-      const bool moving = s.alive0[e][me] && mv != 4;
-      if (!moving) { dy = 0.0f; dx = 0.0f; }
-      const float ny = resolve_axis<H, W>(cw, y + dy, dy, x, y, x, rad, true);
-      const float nx = resolve_axis<H, W>(cw, x + dx, dx, y, y, x, rad, false);
-      float oy = dy != 0.0f ? ny : y;
-      float ox = dx != 0.0f ? nx : x;
-      oy = fminf(fmaxf(oy, rad), cf.pos_hi_y);
-      ox = fminf(fmaxf(ox, rad), cf.pos_hi_x);
-      pl[me][QQT_P_SINCE_BOMB] = sb;
-      pl[me][QQT_P_Y] = __float_as_int(oy);
-      pl[me][QQT_P_X] = __float_as_int(ox);
+      float tv = 0.0f;
+      if (vert) { if (mc == 0) tv = -st; else if (mc == 1) tv = st; }
+      else { if (mc == 2) tv = -st; else if (mc == 3) tv = st; }
+      float dv = tv * spd;
+      if (!(s.alive0[e][me] && mv != 4)) dv = 0.0f;
+      const float own = vert ? y : x;
+      const float nv = resolve_axis<H, W>(cw, own + dv, dv, y, x, rad, vert);
+      float ov = dv != 0.0f ? nv : own;
+      ov = fminf(fmaxf(ov, rad), vert ? cf.pos_hi_y : cf.pos_hi_x);
+      if (vert) {
+        int sb = pl[me][QQT_P_SINCE_BOMB] + 1;
+        if (s.placed[e][me]) sb = 0;
+        pl[me][QQT_P_SINCE_BOMB] = sb;
+        pl[me][QQT_P_Y] = __float_as_int(ov);
+      } else {
+        pl[me][QQT_P_X] = __float_as_int(ov);
+      }
     }
+    for (int i = l; i < G::CW4; i += LPE) { s.cov[e][i] = 0u; s.trg[e][i] = 0u; }
+    // bomb cells: live (fuse > 0) or due (fuse == 0 with an owner)
+    const int nl = build_list<G>(list, e, l, [&](int c) {
+      const uint32_t w = cw[c];
+      return cw_fuse(w) > 0 || cw_owner(w) >= 0;
+    });
     __syncthreads();
 
     // ---- 6. explosions (sim/blast.py:101-155), fixed synchronous rounds
-    for (int c = l; c < C; c += LPE) {
-      const uint32_t w = cw[c];
-      const bool t0 = cw_fuse(w) == 0 && cw_owner(w) >= 0;
-      s.trg[e][c] = t0;
-      s.cov[e][c] = t0 && !(w & (F_WALL | F_BRICK));
-    }
-    __syncthreads();
     auto fire = [&](int src) {  // rays of one seed cell into cov
       const uint32_t w = cw[src];
       if (w & (F_WALL | F_BRICK)) return;
@@ -365,59 +413,79 @@ __global__ __launch_bounds__(64) void tick_kernel(const DevCfg dc, const qqt_tic
       const int r0 = src / W, c0 = src % W;
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        const int dr = d == 0 ? -1 : (d == 1 ? 1 : 0);
-        const int dcol = d == 2 ? -1 : (d == 3 ? 1 : 0);
+        const int dr = dir_dr(d), dc = dir_dc(d);
         for (int k = 1; k <= b; ++k) {
-          const int rr = r0 + k * dr, cc = c0 + k * dcol;
+          const int rr = r0 + k * dr, cc = c0 + k * dc;
           if (rr < 0 || rr >= H || cc < 0 || cc >= W) break;
           const int x = rr * W + cc;
           const uint32_t wx = cw[x];
           if (wx & F_WALL) break;
-          s.cov[e][x] = 1;
-          if ((wx & F_BRICK) || cw_fuse(wx) > 0) break;
+          cov[x] = 1;
+          if (cw_solid(wx)) break;
         }
       }
     };
-    for (int c = l; c < C; c += LPE)
-      if (s.trg[e][c]) fire(c);
-    const int rounds = min(cf.max_chain - 1, cf.chain_cap_rounds);
-    for (int r = 0; r < rounds; ++r) {
-      __syncthreads();
-      uint32_t newly_bits = 0;  // bit k: cell l + 16k
-      int kk = 0;
-      for (int c = l; c < C; c += LPE, ++kk) {
-        const bool nw = cw_fuse(cw[c]) > 0 && s.cov[e][c] && !s.trg[e][c];
-        if (nw) newly_bits |= 1u << kk;
-      }
-      if (!__any(newly_bits != 0)) break;
-      __syncthreads();
-      kk = 0;
-      for (int c = l; c < C; c += LPE, ++kk) {
-        if (newly_bits & (1u << kk)) {
-          s.trg[e][c] = 1;
-          fire(c);
-        }
+    bool boom = false;
+    for (int j = l; j < nl; j += LPE) {
+      const int c = list[j];
+      const uint32_t w = cw[c];
+      if (cw_fuse(w) == 0 && cw_owner(w) >= 0) {
+        trg[c] = 1;
+        if (!(w & (F_WALL | F_BRICK))) cov[c] = 1;
+        boom = true;
       }
     }
+    const bool env_boom = env_bits<LPE>(boom, e) != 0;
     __syncthreads();
-
-    // ---- 7. bricks burn (corridor: into crates); 8. damage (sim/torch_sim.py:1004-1040)
-    for (int c = l; c < C; c += LPE) {
-      if (s.cov[e][c]) {
-        uint32_t w = cw[c];
-        if (w & F_BRICK) {
-          if (cf.corridor) w |= F_CRATE;
-          w &= ~F_BRICK;
-          cw[c] = w;
+    if (__any(env_boom)) {
+      for (int j = l; j < nl; j += LPE) {
+        const int c = list[j];
+        if (trg[c]) fire(c);
+      }
+      const int rounds = min(cf.max_chain - 1, cf.chain_cap_rounds);
+      for (int r = 0; r < rounds; ++r) {
+        __syncthreads();
+        uint32_t newly = 0;  // bit i: list entry l + LPE*i
+        int i = 0;
+        for (int j = l; j < nl; j += LPE, ++i) {
+          const int c = list[j];
+          if (cw_fuse(cw[c]) > 0 && cov[c] && !trg[c]) newly |= 1u << (i & 31);
+        }
+        if (!__any(newly != 0)) break;
+        __syncthreads();
+        i = 0;
+        for (int j = l; j < nl; j += LPE, ++i) {
+          if (newly & (1u << (i & 31))) {
+            const int c = list[j];
+            trg[c] = 1;
+            fire(c);
+          }
+        }
+      }
+      __syncthreads();
+      // ---- 7. burnt bricks (corridor: into crates)
+      if (env_boom) {
+#pragma unroll
+        for (int k = 0; k < KMAX; ++k) {
+          const int c = l + LPE * k;
+          if (c < C && cov[c]) {
+            uint32_t w = cw[c];
+            if (w & F_BRICK) {
+              if (cf.corridor) w |= F_CRATE;
+              w &= ~F_BRICK;
+              cw[c] = w;
+            }
+          }
         }
       }
     }
+    // ---- 8. damage at the post-move centre cell (sim/torch_sim.py:1007-1034)
     if (l < P) {
       const int me = l;
       const float y = __int_as_float(pl[me][QQT_P_Y]), x = __int_as_float(pl[me][QQT_P_X]);
       const int flat = min(max((int)floorf(y) * W + (int)floorf(x), 0), C - 1);
       s.fpost[e][me] = flat;
-      const bool hit = s.alive0[e][me] && s.cov[e][flat];
+      const bool hit = s.alive0[e][me] && cov[flat];
       const bool hit_eff = hit && pl[me][QQT_P_INVULN] <= 0;
       const int hp_new = max(pl[me][QQT_P_HP] - (int)hit_eff, 0);
       const bool died = hit_eff && hp_new == 0;
@@ -428,23 +496,23 @@ __global__ __launch_bounds__(64) void tick_kernel(const DevCfg dc, const qqt_tic
       pl[me][QQT_P_INVULN] = inv;
       if (valid && a.died) a.died[(size_t)g * P + me] = died;
     }
-    __syncthreads();
-
-    // ---- 9. clear exploded cells; info bitsets (bit c of the env's words)
-    {
-      constexpr int KMAX = (C + LPE - 1) / LPE;
+    // ---- 9. info bitsets (bit c of 8 words per env), then clear exploded cells
+    if (a.covered || a.triggered) {
       uint32_t myc = 0, myt = 0;
 #pragma unroll
       for (int k = 0; k < KMAX; ++k) {
         const int c = l + LPE * k;
-        const bool tc = c < C && s.cov[e][c];
-        const bool tt = c < C && s.trg[e][c];
-        if (tt) cw[c] = cw_make(cw[c], 0, -1, 0);
-        const uint32_t hc = (uint32_t)(__ballot(tc) >> (16 * e)) & 0xFFFFu;
-        const uint32_t ht = (uint32_t)(__ballot(tt) >> (16 * e)) & 0xFFFFu;
-        if ((k >> 1) == l) {
-          myc |= hc << (16 * (k & 1));
-          myt |= ht << (16 * (k & 1));
+        const uint64_t bc = env_bits<LPE>(c < C && cov[c], e);
+        const uint64_t bt = env_bits<LPE>(c < C && trg[c], e);
+        // chunk k covers cells [LPE*k, LPE*k + LPE): word (LPE*k)/32 + q
+#pragma unroll
+        for (int q = 0; q < (LPE + 31) / 32; ++q) {
+          const int word = (LPE * k) / 32 + q;
+          const int shift = (LPE >= 32) ? 0 : (16 * (k & 1));
+          const uint32_t vc = (uint32_t)(bc >> (32 * q)) << shift;
+          const uint32_t vt = (uint32_t)(bt >> (32 * q)) << shift;
+          myc = (word == l) ? (myc | vc) : myc;
+          myt = (word == l) ? (myt | vt) : myt;
         }
       }
       if (valid && l < 8) {
@@ -452,268 +520,36 @@ __global__ __launch_bounds__(64) void tick_kernel(const DevCfg dc, const qqt_tic
         if (a.triggered) a.triggered[(size_t)g * 8 + l] = myt;
       }
     }
+    for (int j = l; j < nl; j += LPE) {
+      const int c = list[j];
+      if (trg[c]) cw[c] = cw_make(cw[c], 0, -1, 0);
+    }
     __syncthreads();
   }
 
-  // ---- danger map of the current state (sim/blast.py:158-317)
-  {
-    constexpr int KMAX = (C + LPE - 1) / LPE;
-    float wreg[KMAX];
-    bool any_bomb = false;
+  bool do_reset = false;
+  auto template_reset = [&]() {  // qqtsim/maps.py; re-init of sim/torch_sim.py:178-420
+    const uint32_t env_id = (uint32_t)g;
 #pragma unroll
     for (int k = 0; k < KMAX; ++k) {
       const int c = l + LPE * k;
-      wreg[k] = 0.0f;
-      if (c < C) {
-        const int f = cw_fuse(cw[c]);
-        const float w0 = bomb_weight(f, fmax_f);
-        wreg[k] = w0;
-        s.fw[e][c] = w0;
-        any_bomb |= f > 0;
-      }
-    }
-    auto gather = [&](int c, float v) {  // max over senders whose range reaches c
-      const int r0 = c / W, c0 = c % W;
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const int dr = d == 0 ? -1 : (d == 1 ? 1 : 0);
-        const int dcol = d == 2 ? -1 : (d == 3 ? 1 : 0);
-        for (int k = 1; k <= G::MAXR; ++k) {
-          const int rr = r0 - k * dr, cc = c0 - k * dcol;
-          if (rr < 0 || rr >= H || cc < 0 || cc >= W) break;
-          const int u = rr * W + cc;
-          const uint32_t wu = cw[u];
-          if (cw_fuse(wu) > 0) {
-            if (blast_of(wu, cf.blast) >= k) v = fmaxf(v, s.fw[e][u]);
-            break;
-          }
-          if (wu & (F_WALL | F_BRICK)) break;
-        }
-      }
-      return v;
-    };
-    if (__any(any_bomb)) {
-      // stage A: synchronous relay of weights between bombs (front in s.fw)
-      if (cf.max_chain > 1) {
-        const int rounds = min(cf.max_chain, cf.chain_cap_rounds);
-        for (int r = 0; r < rounds; ++r) {
-          __syncthreads();
-          float nfront[KMAX];
-          bool newly_any = false;
-#pragma unroll
-          for (int k = 0; k < KMAX; ++k) {
-            const int c = l + LPE * k;
-            nfront[k] = 0.0f;
-            if (c < C) {
-              const uint32_t wc = cw[c];
-              if (cw_fuse(wc) > 0 && !(wc & F_WALL)) {
-                const float spread = gather(c, 0.0f);
-                if (spread > wreg[k]) {
-                  wreg[k] = spread;
-                  nfront[k] = spread;
-                  newly_any = true;
-                }
-              }
-            }
-          }
-          __syncthreads();
-#pragma unroll
-          for (int k = 0; k < KMAX; ++k) {
-            const int c = l + LPE * k;
-            if (c < C) s.fw[e][c] = nfront[k];
-          }
-          if (!__any(newly_any)) break;
-        }
-        __syncthreads();
-      }
-      // stage B: each bomb's corrected weight spreads along its cross
-#pragma unroll
-      for (int k = 0; k < KMAX; ++k) {
-        const int c = l + LPE * k;
-        if (c < C) {
-          const uint32_t wc = cw[c];
-          s.fw[e][c] = (cw_fuse(wc) > 0 && !(wc & F_WALL)) ? wreg[k] : 0.0f;
-        }
-      }
-      __syncthreads();
-      for (int c = l; c < C; c += LPE) {
-        const uint32_t wc = cw[c];
-        s.dng[e][c] = (wc & F_WALL) ? 0.0f : gather(c, s.fw[e][c]);
-      }
-    } else {
-      for (int c = l; c < C; c += LPE) s.dng[e][c] = 0.0f;
-    }
-    __syncthreads();
-  }
-
-  if (mode == QQT_MODE_STEP) {
-    // ---- 10. time, rewards, growth, combo, terminal terms (lane 0 of each env)
-    if (l == 0) {
-      const float alpha = a.explore_coef;
-      int t = s.ev[e][QQT_E_T] + 1;
-      s.ev[e][QQT_E_T] = t;
-      int n_alive = 0;
-      for (int i = 0; i < P; ++i) n_alive += pl[i][QQT_P_ALIVE] != 0;
-      const bool done = (n_alive <= 1) || (t >= cf.max_steps);
-      float dmg[P], rw[P], a0[P];
-      float dsum = 0.0f;
-      for (int i = 0; i < P; ++i) {
-        dmg[i] = (float)max(s.hp0[e][i] - pl[i][QQT_P_HP], 0);
-        dsum = dsum + dmg[i];
-        a0[i] = (float)(s.alive0[e][i] != 0);
-      }
-      for (int i = 0; i < P; ++i) {
-        const float dealt = dsum - dmg[i];
-        float r = (-cf.step_penalty) * a0[i];
-        r = r + cf.hit_reward * dealt;
-        r = r - cf.hit_reward * dmg[i];
-        r = r + (alpha * s.pbonus[e][i]) * a0[i];
-        rw[i] = r;
-      }
-      if (cf.hit_attr_penalty > 0) {
-        const int pen = cf.hit_attr_penalty;
-        for (int i = 0; i < P; ++i) {
-          if (!(dmg[i] > 0.0f && s.alive0[e][i])) continue;
-          const int bc = pl[i][QQT_P_BOMBS_CAP], zc = pl[i][QQT_P_BLAST_CAP];
-          const float sp = __int_as_float(pl[i][QQT_P_SPD]);
-          const int nb = max(bc - pen, pl[i][QQT_P_LO_BOMBS]);
-          const int nz = max(zc - pen, pl[i][QQT_P_LO_BLAST]);
-          const float ns = fmaxf(sp - cf.hit_speed_drop, __int_as_float(pl[i][QQT_P_LO_SPD]));
-          const float lost_f = (float)((bc - nb) + (zc - nz)) +
-                               rintf(__fdiv_rn(sp - ns, cf.growth_speed_step));
-          pl[i][QQT_P_BOMBS_CAP] = nb;
-          pl[i][QQT_P_BLAST_CAP] = nz;
-          pl[i][QQT_P_SPD] = __float_as_int(ns);
-          pl[i][QQT_P_PENDING_LOST] += (int)lost_f;
-        }
-      }
-      for (int i = 0; i < P; ++i) rw[i] = rw[i] + (alpha * 0.0f) * a0[i];
-      if (cf.corridor) {
-        int hits[P], stood_v[P];
-        float ug[P];
-        for (int i = 0; i < P; ++i) {
-          const uint32_t wc = cw[s.fpost[e][i]];
-          const int stood = (wc & F_CRATE) != 0;
-          stood_v[i] = stood;
-          rw[i] = rw[i] + (cf.brick_reward * (float)stood) * a0[i];
-          float uh, ugr;
-          if (a.crate_u) {
-            uh = a.crate_u[((size_t)i * 2 + 0) * a.n_envs + g];
-            ugr = a.crate_u[((size_t)i * 2 + 1) * a.n_envs + g];
-          } else {
-            uh = philox_uniform(a.seed, (uint32_t)g, a.tick, STREAM_CRATE, 2 * i);
-            ugr = philox_uniform(a.seed, (uint32_t)g, a.tick, STREAM_CRATE, 2 * i + 1);
-          }
-          const float prob = (wc & F_REC) ? cf.recycle_crate_prob
-                                          : __int_as_float(s.ev[e][QQT_E_CRATE_PROB]);
-          hits[i] = stood && (uh < prob) && s.alive0[e][i];
-          ug[i] = ugr;
-        }
-        (void)stood_v;
-        for (int i = 0; i < P; ++i) {
-          const int h = hits[i] * (s.alive0[e][i] != 0);
-          const int attr = (int)floorf(ug[i] * 3.0f);
-          pl[i][QQT_P_BOMBS_CAP] = min(pl[i][QQT_P_BOMBS_CAP] + (attr == 0) * h, cf.growth_bombs_max);
-          pl[i][QQT_P_BLAST_CAP] = min(pl[i][QQT_P_BLAST_CAP] + (attr == 1) * h, cf.growth_blast_max);
-          const float sp = __int_as_float(pl[i][QQT_P_SPD]) + (float)((attr == 2) * h) * cf.growth_speed_step;
-          pl[i][QQT_P_SPD] = __float_as_int(fminf(sp, cf.growth_speed_max));
-        }
-        for (int i = 0; i < P; ++i) {
-          const int f = s.fpost[e][i];
-          cw[f] &= ~(F_CRATE | F_REC);
-        }
-      }
-      for (int i = 0; i < P; ++i) {
-        const float standing = s.dng[e][s.fpost[e][i]];
-        rw[i] = rw[i] - (a.danger_coef * standing) * a0[i];
-      }
-      if (cf.combo_reward > 0.0f) {
-        for (int i = 0; i < P; ++i) {
-          const float dealt = dsum - dmg[i];
-          const int c = pl[i][QQT_P_COMBO];
-          const int gap = t - pl[i][QQT_P_LAST_HIT];
-          const float factor = powf(cf.combo_gap_factor, (float)max(gap, 0));
-          const int inc = dealt > 0.0f;
-          const int combo_now = (c + inc) * inc;
-          const float pts = (((float)combo_now * cf.combo_reward) * factor) * fminf(dealt, 1.0f);
-          rw[i] = rw[i] + pts * a0[i];
-          int cn = inc ? combo_now : c;
-          if (inc) pl[i][QQT_P_LAST_HIT] = t;
-          if (dmg[i] > 0.0f) cn = 0;
-          pl[i][QQT_P_COMBO] = cn;
-        }
-      }
-      const bool death_done = done && n_alive == 1;
-      const bool all_alive = done && n_alive == P;
-      float hpf[P];
-      float hsum = 0.0f;
-      for (int i = 0; i < P; ++i) { hpf[i] = (float)pl[i][QQT_P_HP]; hsum = hsum + hpf[i]; }
-      int win[P], lose[P];
-      for (int i = 0; i < P; ++i) {
-        const bool al = pl[i][QQT_P_ALIVE] != 0;
-        win[i] = death_done && al;
-        lose[i] = death_done && !al;
-      }
-      float tscale = alpha;
-      if (!cf.timeout_draw) {
-        for (int i = 0; i < P; ++i) {
-          bool gt = true, lt = false;
-          for (int o = 0; o < P; ++o) {
-            if (o == i) continue;
-            gt = gt && (hpf[i] > hpf[o]);
-            lt = lt || (hpf[i] < hpf[o]);
-          }
-          win[i] |= all_alive && gt;
-          lose[i] |= all_alive && lt;
-        }
-        tscale = 1.0f;
-      }
-      for (int i = 0; i < P; ++i) {
-        const float diff = hpf[i] - __fdiv_rn(hsum - hpf[i], (float)(P - 1));
-        if (cf.win_hp_scaled) {
-          const float base = cf.win_per_hp * diff;
-          rw[i] = rw[i] + (base * (float)death_done + (base * (float)all_alive) * tscale);
-        } else {
-          rw[i] = rw[i] + cf.win_bonus * ((float)win[i] - (float)lose[i]);
-          if (cf.timeout_draw)
-            rw[i] = rw[i] + ((cf.win_per_hp * diff) * (float)all_alive) * tscale;
-        }
-      }
-      if (valid) {
-        for (int i = 0; i < P; ++i) {
-          if (a.reward) a.reward[(size_t)g * P + i] = rw[i];
-          if (a.winner) a.winner[(size_t)g * P + i] = win[i];
-        }
-        if (a.done) a.done[g] = done;
-        if (a.n_alive) a.n_alive[g] = n_alive;
-      }
-      s.done[e] = done && a.auto_reset;
-    }
-    __syncthreads();
-    do_reset = s.done[e] != 0;
-  } else if (mode == QQT_MODE_RESET) {
-    do_reset = valid && a.reset_mask[g] != 0;
-  }
-
-  // ---- template reset (qqtsim/maps.py; re-init values of sim/torch_sim.py:178-420)
-  if (do_reset) {
-    const uint32_t env_id = (uint32_t)g;
-    for (int c = l; c < C; c += LPE) {
+      if (c >= C) continue;
       const int r = c / W, col = c % W;
       bool wall = false;
       if (cf.map_kind == 0)
         wall = r == 0 || r == H - 1 || col == 0 || col == W - 1 || ((r % 2 == 0) && (col % 2 == 0));
       bool keep = false;
+#pragma unroll
       for (int i = 0; i < P; ++i) {
         const int sr = (i == 0 || i == 2) ? 1 : H - 2;
         const int sc = (i == 0 || i == 3) ? 1 : W - 2;
-        const int dr = sr < H / 2 ? 1 : -1, dcol = sc < W / 2 ? 1 : -1;
-        keep |= (r == sr && col == sc) || (r == sr && col == sc + dcol) || (r == sr + dr && col == sc);
+        const int dr = sr < H / 2 ? 1 : -1, dc = sc < W / 2 ? 1 : -1;
+        keep |= (r == sr && col == sc) || (r == sr && col == sc + dc) || (r == sr + dr && col == sc);
       }
       bool brick = false;
       if (!wall && !keep && cf.brick_p > 0.0f)
         brick = philox_uniform(a.seed, env_id, a.epoch, STREAM_RESET_CELL, (uint32_t)c) < cf.brick_p;
-      cw[c] = (wall ? F_WALL : 0u) | (brick ? F_BRICK : 0u) | 0x0000FF00u;
+      cw[c] = (wall ? F_WALL : 0u) | (brick ? F_BRICK : 0u) | EMPTY_CELL;
       s.dng[e][c] = 0.0f;
     }
     if (l == 0) {
@@ -722,22 +558,20 @@ __global__ __launch_bounds__(64) void tick_kernel(const DevCfg dc, const qqt_tic
       philox_block(a.seed, env_id, a.epoch, STREAM_RESET_MISC, 1, u + 4);
       philox_block(a.seed, env_id, a.epoch, STREAM_RESET_MISC, 2, u + 8);
       float py[P], px[P];
+#pragma unroll
       for (int i = 0; i < P; ++i) {
-        const int sr = (i == 0 || i == 2) ? 1 : H - 2;
-        const int sc = (i == 0 || i == 3) ? 1 : W - 2;
-        py[i] = (float)sr + 0.5f;
-        px[i] = (float)sc + 0.5f;
+        py[i] = (float)((i == 0 || i == 2) ? 1 : H - 2) + 0.5f;
+        px[i] = (float)((i == 0 || i == 3) ? 1 : W - 2) + 0.5f;
       }
       if (cf.swap_spawns && u[0] < 0.5f) {
-        float ty = py[0], tx = px[0];
+        const float ty = py[0], tx = px[0];
         py[0] = py[1]; px[0] = px[1]; py[1] = ty; px[1] = tx;
       }
+      const int bspan = cf.bombs_hi - cf.bombs_lo + 1, zspan = cf.blast_hi - cf.blast_lo + 1;
+#pragma unroll
       for (int i = 0; i < P; ++i) {
-        const int bspan = cf.bombs_hi - cf.bombs_lo + 1, zspan = cf.blast_hi - cf.blast_lo + 1;
-        const float ub = u[1 + 2 * i];
-        const float uz = u[2 + 2 * i];
-        const int bc = cf.bombs_lo + min((int)floorf(ub * (float)bspan), bspan - 1);
-        const int zc = cf.blast_lo + min((int)floorf(uz * (float)zspan), zspan - 1);
+        const int bc = cf.bombs_lo + min((int)floorf(u[1 + 2 * i] * (float)bspan), bspan - 1);
+        const int zc = cf.blast_lo + min((int)floorf(u[2 + 2 * i] * (float)zspan), zspan - 1);
         int32_t* q = pl[i];
         q[QQT_P_Y] = __float_as_int(py[i]);
         q[QQT_P_X] = __float_as_int(px[i]);
@@ -760,31 +594,315 @@ __global__ __launch_bounds__(64) void tick_kernel(const DevCfg dc, const qqt_tic
       s.ev[e][QQT_E_CRATE_PROB] = __float_as_int(cf.growth_crate_prob);
       s.ev[e][QQT_E_MAP_KIND] = 0;
     }
+  };
+
+  if (mode == QQT_MODE_RESET) {
+    do_reset = valid && a.reset_mask[g] != 0;
+    if (do_reset) template_reset();
+    __syncthreads();
   }
-  __syncthreads();
+
+  // ---- danger map of the current state (sim/blast.py:158-317)
+  {
+    float* dng = s.dng[e];
+    float* fw = s.fw[e];
+    float* wl = s.wl[e];
+    float(*dd)[C] = s.dd[e];
+    const int nb = build_list<G>(list, e, l, [&](int c) { return cw_fuse(cw[c]) > 0; });
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      const int c = l + LPE * k;
+      if (c < C) dng[c] = 0.0f;
+    }
+    const bool wave_bombs = __any(nb > 0);
+    if (wave_bombs) {
+      // weights; stage-A front = weight at every bomb (walls included: the
+      // reference's stage-A origins are not masked by passability)
+      for (int j = l; j < nb; j += LPE) {
+        const int c = list[j];
+        const float w0 = bomb_weight(cw_fuse(cw[c]), fmax_f);
+        wl[j] = w0;
+        fw[c] = w0;
+      }
+      // zero the per-direction ray buffers (4*C floats, 16-byte aligned)
+      {
+        float4* d4 = reinterpret_cast<float4*>(&dd[0][0]);
+        for (int i = l; i < C; i += LPE) d4[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+      if (cf.max_chain > 1) {
+        // in-edges, one (bomb, direction) per item: the first solid cell
+        // behind the bomb, kept if it is a bomb whose range reaches it
+        for (int it = l; it < 4 * nb; it += LPE) {
+          const int j = it >> 2, d = it & 3;
+          const int c = list[j];
+          uint16_t ed = 0;
+          if (!(cw[c] & F_WALL)) {
+            const int r0 = c / W, c0 = c % W;
+            const int dr = dir_dr(d), dc = dir_dc(d);
+            for (int k = 1; k < (H > W ? H : W); ++k) {
+              const int rr = r0 - k * dr, cc = c0 - k * dc;
+              if (rr < 0 || rr >= H || cc < 0 || cc >= W) break;
+              const int u = rr * W + cc;
+              const uint32_t wu = cw[u];
+              if (cw_fuse(wu) > 0) {
+                if (blast_of(wu, cf.blast) >= k) ed = (uint16_t)(u | (k << 8));
+                break;
+              }
+              if (wu & (F_WALL | F_BRICK)) break;
+            }
+          }
+          s.edge[e][j][d] = ed;
+        }
+        // stage A: synchronous relay rounds
+        const int rounds = min(cf.max_chain, cf.chain_cap_rounds);
+        for (int r = 0; r < rounds; ++r) {
+          __syncthreads();
+          float nf[KMAX];
+          bool upd = false;
+#pragma unroll
+          for (int i = 0; i < KMAX; ++i) {
+            const int j = l + LPE * i;
+            nf[i] = 0.0f;
+            if (j >= nb) continue;
+            float spread = 0.0f;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+              const uint16_t ed = s.edge[e][j][d];
+              if (ed) spread = fmaxf(spread, fw[ed & 0xFF]);
+            }
+            const float nv = spread > wl[j] ? spread : 0.0f;
+            nf[i] = nv;
+            upd |= nv > 0.0f;
+          }
+          __syncthreads();
+#pragma unroll
+          for (int i = 0; i < KMAX; ++i) {
+            const int j = l + LPE * i;
+            if (j >= nb) continue;
+            const float nv = nf[i];
+            if (nv > 0.0f) wl[j] = nv;
+            fw[list[j]] = nv;
+          }
+          if (!__any(upd)) break;
+        }
+      }
+      __syncthreads();
+      // stage B: every (bomb, direction) ray writes its own direction's
+      // buffer; within one direction rays never overlap, so plain stores
+      for (int it = l; it < 4 * nb; it += LPE) {
+        const int j = it >> 2, d = it & 3;
+        const int c = list[j];
+        const uint32_t wc = cw[c];
+        const float v = wl[j];
+        if (wc & F_WALL) continue;
+        if (d == 0) dng[c] = v;  // the bomb's own cell (seed)
+        const int b = blast_of(wc, cf.blast);
+        const int r0 = c / W, c0 = c % W;
+        const int dr = dir_dr(d), dc = dir_dc(d);
+        for (int k = 1; k <= b; ++k) {
+          const int rr = r0 + k * dr, cc = c0 + k * dc;
+          if (rr < 0 || rr >= H || cc < 0 || cc >= W) break;
+          const int x = rr * W + cc;
+          const uint32_t wx = cw[x];
+          if (wx & F_WALL) break;
+          dd[d][x] = v;
+          if (cw_solid(wx)) break;
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < KMAX; ++k) {
+        const int c = l + LPE * k;
+        if (c < C) {
+          const float m = fmaxf(fmaxf(dd[0][c], dd[1][c]), fmaxf(dd[2][c], dd[3][c]));
+          dng[c] = fmaxf(dng[c], m);
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  if (mode == QQT_MODE_STEP) {
+    // ---- 10. time, rewards, growth, combo, terminal terms; lane i < P is player i
+    {
+      const int i = l;
+      const bool me_ok = i < P;
+      const float alpha = a.explore_coef;
+      const int t = s.ev[e][QQT_E_T] + 1;
+      // env-wide sums over the players, read by every lane (LDS broadcasts)
+      int n_alive = 0, dsum_int = 0, hsum_int = 0;
+      bool any_stood = false;
+#pragma unroll
+      for (int o = 0; o < P; ++o) {
+        const int hpo = pl[o][QQT_P_HP];
+        n_alive += pl[o][QQT_P_ALIVE] != 0;
+        dsum_int += max(s.hp0[e][o] - hpo, 0);
+        hsum_int += hpo;
+        any_stood |= cf.corridor && (cw[s.fpost[e][o]] & F_CRATE);
+      }
+      const bool done = (n_alive <= 1) || (t >= cf.max_steps);
+      const int ip = me_ok ? i : 0;
+      const int hp_i = pl[ip][QQT_P_HP];
+      const float dmg = (float)max(s.hp0[e][ip] - hp_i, 0);
+      const int fp = s.fpost[e][ip];
+      const uint32_t wcell = cw[fp];
+      const int stood = (cf.corridor && me_ok) ? ((wcell & F_CRATE) != 0) : 0;
+      if (me_ok) {
+        const float a0 = (float)(s.alive0[e][i] != 0);
+        const float dsum = (float)dsum_int;  // exact: a sum of small integers
+        const float dealt = dsum - dmg;
+        float r = (-cf.step_penalty) * a0;
+        r = r + cf.hit_reward * dealt;
+        r = r - cf.hit_reward * dmg;
+        r = r + (alpha * s.pbonus[e][i]) * a0;
+        if (cf.hit_attr_penalty > 0 && dmg > 0.0f && s.alive0[e][i]) {
+          const int pen = cf.hit_attr_penalty;
+          const int bc = pl[i][QQT_P_BOMBS_CAP], zc = pl[i][QQT_P_BLAST_CAP];
+          const float sp = __int_as_float(pl[i][QQT_P_SPD]);
+          const int nbc = max(bc - pen, pl[i][QQT_P_LO_BOMBS]);
+          const int nzc = max(zc - pen, pl[i][QQT_P_LO_BLAST]);
+          const float ns = fmaxf(sp - cf.hit_speed_drop, __int_as_float(pl[i][QQT_P_LO_SPD]));
+          const float lost_f = (float)((bc - nbc) + (zc - nzc)) +
+                               rintf(__fdiv_rn(sp - ns, cf.growth_speed_step));
+          pl[i][QQT_P_BOMBS_CAP] = nbc;
+          pl[i][QQT_P_BLAST_CAP] = nzc;
+          pl[i][QQT_P_SPD] = __float_as_int(ns);
+          pl[i][QQT_P_PENDING_LOST] += (int)lost_f;
+        }
+        r = r + (alpha * 0.0f) * a0;  // chain_blast_bonus term (0 in every supported config)
+        if (cf.corridor) {
+          r = r + (cf.brick_reward * (float)stood) * a0;
+          if (any_stood) {
+            float uh = in_uh, ug = in_ug;
+            if (!a.crate_u) {
+              float u4[4];
+              philox_block(a.seed, (uint32_t)g, a.tick, STREAM_CRATE, (uint32_t)((2 * i) >> 2), u4);
+              uh = u4[(2 * i) & 3];
+              ug = u4[(2 * i + 1) & 3];
+            }
+            const float prob = (wcell & F_REC) ? cf.recycle_crate_prob
+                                               : __int_as_float(s.ev[e][QQT_E_CRATE_PROB]);
+            const int h = stood && (uh < prob) && s.alive0[e][i];
+            const int attr = (int)floorf(ug * 3.0f);
+            pl[i][QQT_P_BOMBS_CAP] = min(pl[i][QQT_P_BOMBS_CAP] + (attr == 0) * h, cf.growth_bombs_max);
+            pl[i][QQT_P_BLAST_CAP] = min(pl[i][QQT_P_BLAST_CAP] + (attr == 1) * h, cf.growth_blast_max);
+            const float sp = __int_as_float(pl[i][QQT_P_SPD]) + (float)((attr == 2) * h) * cf.growth_speed_step;
+            pl[i][QQT_P_SPD] = __float_as_int(fminf(sp, cf.growth_speed_max));
+          }
+          cw[fp] = wcell & ~(F_CRATE | F_REC);
+        }
+        r = r - (a.danger_coef * s.dng[e][fp]) * a0;
+        if (cf.combo_reward > 0.0f) {
+          const int c = pl[i][QQT_P_COMBO];
+          if (dealt > 0.0f) {
+            const int gap = t - pl[i][QQT_P_LAST_HIT];
+            const float factor = powf(cf.combo_gap_factor, (float)max(gap, 0));
+            const int combo_now = c + 1;
+            const float pts = (((float)combo_now * cf.combo_reward) * factor) * fminf(dealt, 1.0f);
+            r = r + pts * a0;
+            pl[i][QQT_P_LAST_HIT] = t;
+            pl[i][QQT_P_COMBO] = combo_now;
+          } else {
+            r = r + 0.0f * a0;
+          }
+          if (dmg > 0.0f) pl[i][QQT_P_COMBO] = 0;
+        }
+        const bool death_done = done && n_alive == 1;
+        const bool all_alive = done && n_alive == P;
+        const bool al = pl[i][QQT_P_ALIVE] != 0;
+        int win = death_done && al, lose = death_done && !al;
+        const float hpf = (float)hp_i;
+        float tscale = alpha;
+        if (!cf.timeout_draw) {
+          bool gt = true, lt = false;
+          for (int o = 0; o < P; ++o) {
+            if (o == i) continue;
+            const float ho = (float)pl[o][QQT_P_HP];
+            gt = gt && (hpf > ho);
+            lt = lt || (hpf < ho);
+          }
+          win |= all_alive && gt;
+          lose |= all_alive && lt;
+          tscale = 1.0f;
+        }
+        const float diff = hpf - __fdiv_rn((float)hsum_int - hpf, (float)(P - 1));
+        if (cf.win_hp_scaled) {
+          const float base = cf.win_per_hp * diff;
+          r = r + (base * (float)death_done + (base * (float)all_alive) * tscale);
+        } else {
+          r = r + cf.win_bonus * ((float)win - (float)lose);
+          if (cf.timeout_draw) r = r + ((cf.win_per_hp * diff) * (float)all_alive) * tscale;
+        }
+        if (valid) {
+          if (a.reward) a.reward[(size_t)g * P + i] = r;
+          if (a.winner) a.winner[(size_t)g * P + i] = win;
+        }
+      }
+      if (l == 0) {
+        s.ev[e][QQT_E_T] = t;
+        if (valid) {
+          if (a.done) a.done[g] = done;
+          if (a.n_alive) a.n_alive[g] = n_alive;
+        }
+        s.done[e] = done && a.auto_reset && valid;
+      }
+    }
+    __syncthreads();
+    if (s.done[e]) template_reset();
+    __syncthreads();
+  }
 
   // ---- observation + legality masks of the current state (sim/obs.py:25-229)
+  const int g0 = blockIdx.x * EPW;
+  const int opad = (int)(((uintptr_t)(a.obs + (size_t)g0 * OBS)) & 15u);  // staging offset
   {
-    int cnt[P];
+    // everything starts as zero; only nonzero values are written afterwards
+    {
+      uint4* z = reinterpret_cast<uint4*>(s.obs_raw);
+      constexpr int N16 = sizeof(s.obs_raw) / 16;
+      for (int i = lane; i < N16; i += 64) z[i] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    __syncthreads();
+    uint16_t* ob = reinterpret_cast<uint16_t*>(s.obs_raw + opad) + (size_t)e * OBS;
+    const float tplane = __fdiv_rn((float)s.ev[e][QQT_E_T], (float)cf.max_steps);
+    const uint16_t h_one = __half_as_ushort(__float2half_rn(1.0f));
+    const uint16_t h_t = __half_as_ushort(__float2half_rn(tplane));
 #pragma unroll
-    for (int i = 0; i < P; ++i) cnt[i] = 0;
-    for (int c = l; c < C; c += LPE) {
+    for (int k = 0; k < KMAX; ++k) {
+      const int c = l + LPE * k;
+      if (c >= C) continue;
       const uint32_t w = cw[c];
-      if (cw_fuse(w) > 0) {
-        const int o = cw_owner(w);
-#pragma unroll
-        for (int i = 0; i < P; ++i) cnt[i] += (o == i);
-      }
+      const float dv = s.dng[e][c];
+      if (w & (F_WALL | F_BRICK)) ob[(2 * P) * C + c] = h_one;
+      if (dv != 0.0f) ob[(2 * P + 1) * C + c] = __half_as_ushort(__float2half_rn(dv));
+      ob[(2 * P + 2) * C + c] = h_t;
+      if (w & F_CRATE) ob[(2 * P + 3) * C + c] = h_one;
+    }
+    // fuse channels from the bomb cells: list[] still holds them unless this
+    // env was reset (then it has no bombs)
+    const int nbo = build_list<G>(list, e, l, [&](int c) { return cw_fuse(cw[c]) > 0; });
+    for (int j = l; j < nbo; j += LPE) {
+      const int c = list[j];
+      const uint32_t w = cw[c];
+      const int o = cw_owner(w);
+      if (o >= 0 && o < P)
+        ob[(P + o) * C + c] = __half_as_ushort(__float2half_rn(__fdiv_rn((float)cw_fuse(w), fmax_f)));
     }
 #pragma unroll
     for (int i = 0; i < P; ++i) {
-      const int t = sum16(cnt[i]);
+      const int t = env_count<G>(e, l, [&](int c) {
+        const uint32_t w = cw[c];
+        return cw_fuse(w) > 0 && cw_owner(w) == i;
+      });
       if (l == 0) s.live[e][i] = t;
     }
+    __syncthreads();
     if (l < P) {
+      // splat: the four corner terms accumulate in order (0,0),(0,1),(1,0),(1,1)
       const int i = l;
       const float py = __int_as_float(pl[i][QQT_P_Y]), px = __int_as_float(pl[i][QQT_P_X]);
-      const float gate = (float)(pl[i][QQT_P_ALIVE] != 0);
+      const bool al = pl[i][QQT_P_ALIVE] != 0;
+      const float gate = (float)al;
       const float fy = fminf(fmaxf(py - 0.5f, 0.0f), (float)(H - 1));
       const float fx = fminf(fmaxf(px - 0.5f, 0.0f), (float)(W - 1));
       const int y0 = min(max((int)floorf(fy), 0), H - 1);
@@ -793,48 +911,27 @@ __global__ __launch_bounds__(64) void tick_kernel(const DevCfg dc, const qqt_tic
       const float wy = fminf(fmaxf(fy - (float)y0, 0.0f), 1.0f);
       const float wx = fminf(fmaxf(fx - (float)x0, 0.0f), 1.0f);
       const float ky0 = 1.0f - wy, kx0 = 1.0f - wx;
-      s.splat_i[e][i][0] = y0 * W + x0; s.splat_w[e][i][0] = (ky0 * kx0) * gate;
-      s.splat_i[e][i][1] = y0 * W + x1; s.splat_w[e][i][1] = (ky0 * wx) * gate;
-      s.splat_i[e][i][2] = y1 * W + x0; s.splat_w[e][i][2] = (wy * kx0) * gate;
-      s.splat_i[e][i][3] = y1 * W + x1; s.splat_w[e][i][3] = (wy * wx) * gate;
-      s.fpost[e][i] = min(max((int)floorf(py) * W + (int)floorf(px), 0), C - 1);
-    }
-    __syncthreads();
-
-    uint16_t* ob = s.obs[e];
-    const float tplane = __fdiv_rn((float)s.ev[e][QQT_E_T], (float)cf.max_steps);
-    for (int c = l; c < C; c += LPE) {
-      const uint32_t w = cw[c];
-      const int f = cw_fuse(w), o = cw_owner(w);
-      const float fnorm = __fdiv_rn((float)f, fmax_f);
+      const int id[4] = {y0 * W + x0, y0 * W + x1, y1 * W + x0, y1 * W + x1};
+      const float wt[4] = {(ky0 * kx0) * gate, (ky0 * wx) * gate, (wy * kx0) * gate, (wy * wx) * gate};
+      float run[4];
 #pragma unroll
-      for (int i = 0; i < P; ++i) {
-        float v = 0.0f;
+      for (int q = 0; q < 4; ++q) {
+        float prev = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-          if (s.splat_i[e][i][k] == c) v = v + s.splat_w[e][i][k];
-        ob[i * C + c] = __half_as_ushort(__float2half_rn(v));
-        ob[(P + i) * C + c] = __half_as_ushort(__float2half_rn((o == i && f > 0) ? fnorm : 0.0f));
+        for (int j = 0; j < q; ++j)
+          if (id[j] == id[q]) prev = run[j];
+        run[q] = prev + wt[q];
+        ob[i * C + id[q]] = __half_as_ushort(__float2half_rn(run[q]));
       }
-      ob[(2 * P) * C + c] = __half_as_ushort(__float2half_rn((w & (F_WALL | F_BRICK)) ? 1.0f : 0.0f));
-      ob[(2 * P + 1) * C + c] = __half_as_ushort(__float2half_rn(s.dng[e][c]));
-      ob[(2 * P + 2) * C + c] = __half_as_ushort(__float2half_rn(tplane));
-      ob[(2 * P + 3) * C + c] = __half_as_ushort(__float2half_rn((w & F_CRATE) ? 1.0f : 0.0f));
-#pragma unroll
-      for (int i = 0; i < P; ++i) {
-        const bool here = s.fpost[e][i] == c;
-        const bool al = pl[i][QQT_P_ALIVE] != 0;
-        const int capi = pl[i][QQT_P_BOMBS_CAP];
-        const float cap = fmaxf((float)capi, 1.0f);
-        const float avail = fmaxf((float)(capi - s.live[e][i]), 0.0f);
-        const float af = (float)al;
-        const float inv = (pl[i][QQT_P_INVULN] > 0 && al) ? 1.0f : 0.0f;
-        ob[(2 * P + 4 + i) * C + c] = __half_as_ushort(__float2half_rn(here ? inv : 0.0f));
-        ob[(3 * P + 4 + i) * C + c] =
-            __half_as_ushort(__float2half_rn(here ? __fdiv_rn(avail, cap) * af : 0.0f));
-        ob[(4 * P + 4 + i) * C + c] = __half_as_ushort(
-            __float2half_rn(here ? __fdiv_rn(cap, (float)cf.growth_bombs_max) * af : 0.0f));
-      }
+      const int cell = min(max((int)floorf(py) * W + (int)floorf(px), 0), C - 1);
+      const int capi = pl[i][QQT_P_BOMBS_CAP];
+      const float cap = fmaxf((float)capi, 1.0f);
+      const float avail = fmaxf((float)(capi - s.live[e][i]), 0.0f);
+      const float inv = (pl[i][QQT_P_INVULN] > 0 && al) ? 1.0f : 0.0f;
+      ob[(2 * P + 4 + i) * C + cell] = __half_as_ushort(__float2half_rn(inv));
+      ob[(3 * P + 4 + i) * C + cell] = __half_as_ushort(__float2half_rn(__fdiv_rn(avail, cap) * gate));
+      ob[(4 * P + 4 + i) * C + cell] =
+          __half_as_ushort(__float2half_rn(__fdiv_rn(cap, (float)cf.growth_bombs_max) * gate));
     }
 
     // masks: lane = me*4 + probe (up, down, left, right)
@@ -845,24 +942,19 @@ __global__ __launch_bounds__(64) void tick_kernel(const DevCfg dc, const qqt_tic
       const float st = cf.step_len;
       const float d = (pr & 1) ? st : -st;
       bool moved;
-      if (pr < 2) {
-        const float ny = resolve_axis<H, W>(cw, y + d, d, x, y, x, rad, true);
-        moved = fabsf(ny - y) > 2e-4f;
-      } else {
-        const float nx = resolve_axis<H, W>(cw, x + d, d, y, y, x, rad, false);
-        moved = fabsf(nx - x) > 2e-4f;
-      }
+      const bool vert = pr < 2;
+      const float own = vert ? y : x;
+      const float nv = resolve_axis<H, W>(cw, own + d, d, y, x, rad, vert);
+      moved = fabsf(nv - own) > 2e-4f;
       if (a.move_mask) {
         a.move_mask[((size_t)g * P + me) * 5 + pr] = al ? moved : 1;
         if (pr == 0) a.move_mask[((size_t)g * P + me) * 5 + 4] = 1;
       }
       if (pr == 0 && a.bomb_mask) {
-        const int cy = (int)floorf(y), cx = (int)floorf(x);
-        const int flat = min(max(cy * W + cx, 0), C - 1);
+        const int flat = min(max((int)floorf(y) * W + (int)floorf(x), 0), C - 1);
         const uint32_t wc = cw[flat];
         const bool under = cw_fuse(wc) > 0;
-        const bool blk = under || (wc & F_BRICK);
-        const bool can = !under && !blk && s.live[e][me] < pl[me][QQT_P_BOMBS_CAP];
+        const bool can = !under && !(wc & F_BRICK) && s.live[e][me] < pl[me][QQT_P_BOMBS_CAP];
         a.bomb_mask[((size_t)g * P + me) * 2 + 0] = 1;
         a.bomb_mask[((size_t)g * P + me) * 2 + 1] = (can && al) || !al;
       }
@@ -873,28 +965,33 @@ __global__ __launch_bounds__(64) void tick_kernel(const DevCfg dc, const qqt_tic
   // ---- store state and the staged observation
   if (mode == QQT_MODE_STEP || mode == QQT_MODE_RESET) {
     if (valid) {
-      for (int c = l; c < C; c += LPE) a.cells[(size_t)g * C + c] = (int32_t)cw[c];
+#pragma unroll
+      for (int k = 0; k < KMAX; ++k) {
+        const int c = l + LPE * k;
+        if (c < C) a.cells[(size_t)g * C + c] = (int32_t)cw[c];
+      }
       for (int i = l; i < P * QQT_P_SLOTS; i += LPE)
         a.players[(size_t)g * P * QQT_P_SLOTS + i] = pl[i / QQT_P_SLOTS][i % QQT_P_SLOTS];
       if (l < QQT_E_SLOTS) a.envs[(size_t)g * QQT_E_SLOTS + l] = s.ev[e][l];
     }
   }
   if (a.obs) {
-    const int g0 = blockIdx.x * EPW;
+    // staging and destination share their address mod 16: u16 head, 16-byte
+    // body, u16 tail
     const int nvalid = min(EPW, a.n_envs - g0);
-    const size_t bytes = (size_t)nvalid * OBS * 2;
+    const int bytes = nvalid * OBS * 2;
     uint8_t* dst = (uint8_t*)(a.obs + (size_t)g0 * OBS);
-    const uint8_t* src = (const uint8_t*)&s.obs[0][0];
-    if constexpr ((EPW * OBS * 2) % 16 == 0) {
-      const size_t n16 = bytes / 16;
-      for (size_t i = lane; i < n16; i += 64)
-        reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
-      for (size_t i = n16 * 16 + lane * 2; i < bytes; i += 128)
-        *reinterpret_cast<uint16_t*>(dst + i) = *reinterpret_cast<const uint16_t*>(src + i);
-    } else {
-      for (size_t i = lane * 2; i < bytes; i += 128)
-        *reinterpret_cast<uint16_t*>(dst + i) = *reinterpret_cast<const uint16_t*>(src + i);
-    }
+    const uint8_t* src = s.obs_raw + opad;
+    const int head = min((16 - opad) & 15, bytes);
+    const int n16 = (bytes - head) / 16;
+    if (lane * 2 < head)
+      *reinterpret_cast<uint16_t*>(dst + lane * 2) = *reinterpret_cast<const uint16_t*>(src + lane * 2);
+    for (int i = lane; i < n16; i += 64)
+      reinterpret_cast<uint4*>(dst + head)[i] = reinterpret_cast<const uint4*>(src + head)[i];
+    const int tail0 = head + n16 * 16;
+    if (tail0 + lane * 2 < bytes)
+      *reinterpret_cast<uint16_t*>(dst + tail0 + lane * 2) =
+          *reinterpret_cast<const uint16_t*>(src + tail0 + lane * 2);
   }
 }
 
@@ -906,12 +1003,16 @@ int fail(int code, const char* msg) {
   return code;
 }
 
+#ifndef QQT_LPE
+#define QQT_LPE 64
+#endif
+
 template <int H, int W, int P>
 int launch(const qqt_sim_config* cfg, const qqt_tick_args* a, hipStream_t st) {
+  constexpr int LPE = QQT_LPE;
+  constexpr int EPW = 64 / LPE;
   const int blocks = (a->n_envs + EPW - 1) / EPW;
-  DevCfg dc;
-  dc.c = *cfg;
-  hipLaunchKernelGGL((tick_kernel<H, W, P>), dim3(blocks), dim3(64), 0, st, dc, *a);
+  hipLaunchKernelGGL((tick_kernel<H, W, P, LPE>), dim3(blocks), dim3(64), 0, st, *cfg, *a);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     snprintf(g_err, sizeof(g_err), "tick launch failed: %s", hipGetErrorString(err));
