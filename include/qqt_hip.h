@@ -102,6 +102,38 @@ typedef struct qqt_tick_args {
   int32_t* probe_out;         /* PROBE: [N] largest bomb_blast */
 } qqt_tick_args;
 
+/* MLP actor/critic forward (+ masked sampling).  Weights are the packed
+ * device buffers built by qqtsim/policy.py from an ActorCritic "mlp"
+ * state_dict (train/model.py:121-165): fragment-ordered float16 matrices
+ * w0 (both players' view-permuted first layers), w1, wh (the three head
+ * hidden layers stacked), wf (the three output layers, block diagonal, 16
+ * padded rows), the float16 residuals of w1/wh/wf (the later layers run as
+ * hi/lo pairs), and float32 vectors.  Outputs are indexed [row][player slot]. */
+typedef struct qqt_mlp_args {
+  int32_t batch;             /* rows B */
+  int32_t npid;              /* 1: player pid0 only; 2: both players */
+  int32_t pid0;
+  int32_t sample;            /* 1: draw actions (needs masks) */
+  int32_t k0, kblocks0;      /* first-layer width (C*H*W) and ceil(k0/64) */
+  int32_t obs_stride;        /* elements between observation rows (even) */
+  int32_t mm_row_stride, mm_pid_stride;  /* move mask [row*rs + pid*ps + k] */
+  int32_t bm_row_stride, bm_pid_stride;  /* bomb mask */
+  uint64_t seed;             /* Philox key of the policy uniforms */
+  uint32_t tick, reserved;   /* counter word of the policy uniforms */
+  const uint16_t* obs;       /* [B][obs_stride] float16 bits, 4-byte aligned */
+  const uint16_t *w0, *w1, *wh, *wf;       /* float16 (hi) fragments */
+  const uint16_t *w1_lo, *wh_lo, *wf_lo;   /* float16 residuals w - hi */
+  const float *b0, *ln1_w, *ln1_b, *b1, *ln2_w, *ln2_b, *bh, *bf;
+  const uint8_t* move_mask;
+  const uint8_t* bomb_mask;
+  const float* uniforms;     /* [B][npid][2] (move, bomb) or NULL = Philox */
+  int64_t* actions;          /* [B][npid][2] or NULL */
+  int8_t* actions_i8;        /* [B][npid][2] or NULL */
+  float* logp_out;           /* [B][npid] or NULL */
+  float* value_out;          /* [B][npid] or NULL */
+  float* logits_out;         /* [B][npid][8]: 5 move, 2 bomb, value; or NULL */
+} qqt_mlp_args;
+
 /* ABI version (QQT_ABI_VERSION). */
 int qqt_abi_version(void);
 
@@ -113,6 +145,12 @@ const char* qqt_last_error(void);
  * BatchedSim.observe (:605-627) and BatchedSim.legal_mask (:636-645), plus
  * reset_ (:178-420) with template maps, per `mode`. */
 int qqt_tick(const qqt_sim_config* cfg, const qqt_tick_args* args, void* stream);
+
+/* One launch of the MLP forward with optional masked sampling.  Replaces
+ * ActorCritic.act (train/model.py:230-245) for one or both players (obs is
+ * shared, so both players' first layers are one GEMM), ActorCritic.forward
+ * (:167-196) when sample = 0. */
+int qqt_mlp_act(const qqt_mlp_args* args, void* stream);
 
 #ifdef __cplusplus
 }

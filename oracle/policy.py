@@ -134,21 +134,3 @@ def mlp_forward(params: dict, obs: torch.Tensor, pid: int, n_players: int = 2,
         return F.linear(y, P[f"{name}.2.weight"], P[f"{name}.2.bias"])
 
     return head("move_head"), head("bomb_head"), head("critic").squeeze(-1)
-
-
-def default_init_params(c: int = 14, hw: int = 169, n_moves: int = 5, n_bomb: int = 2,
-                        seed: int = 0) -> dict:
-    """PyTorch default init (nn.Linear: kaiming-uniform a=sqrt(5) weights,
-    U(+-1/sqrt(fan_in)) bias; LayerNorm gamma=1, beta=0) for the mlp
-    ActorCritic under torch.manual_seed(seed), layers created in module order."""
-    torch.manual_seed(seed)
-    shared = torch.nn.Sequential(torch.nn.Linear(c * hw, 128), torch.nn.LayerNorm(128),
-                                 torch.nn.ReLU(), torch.nn.Linear(128, 128),
-                                 torch.nn.LayerNorm(128), torch.nn.ReLU())
-    heads = {name: torch.nn.Sequential(torch.nn.Linear(128, 64), torch.nn.ReLU(),
-                                       torch.nn.Linear(64, k))
-             for name, k in (("move_head", n_moves), ("bomb_head", n_bomb), ("critic", 1))}
-    out = {f"shared.{k}": v for k, v in shared.state_dict().items()}
-    for name, mod in heads.items():
-        out.update({f"{name}.{k}": v for k, v in mod.state_dict().items()})
-    return {k: v.detach().clone() for k, v in out.items()}

@@ -48,6 +48,16 @@ class TickArgsC(ctypes.Structure):
                            "probe_out")]
 
 
+class MlpArgsC(ctypes.Structure):
+    _fields_ = [(n, _i32) for n in (
+        "batch", "npid", "pid0", "sample", "k0", "kblocks0", "obs_stride", "mm_row_stride",
+        "mm_pid_stride", "bm_row_stride", "bm_pid_stride")] + [
+        ("seed", _u64), ("tick", _u32), ("reserved", _u32)] + [
+        (n, _vp) for n in ("obs", "w0", "w1", "wh", "wf", "w1_lo", "wh_lo", "wf_lo", "b0", "ln1_w", "ln1_b", "b1",
+                           "ln2_w", "ln2_b", "bh", "bf", "move_mask", "bomb_mask", "uniforms",
+                           "actions", "actions_i8", "logp_out", "value_out", "logits_out")]
+
+
 _LIB = None
 
 
@@ -63,6 +73,8 @@ def lib():
         L.qqt_last_error.restype = ctypes.c_char_p
         L.qqt_tick.restype = ctypes.c_int
         L.qqt_tick.argtypes = [ctypes.POINTER(SimConfigC), ctypes.POINTER(TickArgsC), _vp]
+        L.qqt_mlp_act.restype = ctypes.c_int
+        L.qqt_mlp_act.argtypes = [ctypes.POINTER(MlpArgsC), _vp]
         if L.qqt_abi_version() != ABI_VERSION:
             raise RuntimeError("libqqt_hip.so ABI version mismatch; rebuild it")
         _LIB = L

@@ -1,0 +1,229 @@
+"""`HipActorCritic`: the reference's mlp `ActorCritic` on the MFMA kernel.
+
+Drop-in for `train/model.py::ActorCritic` (arch "mlp", :54-259) on the
+rollout path: `act(obs, move_mask, bomb_mask, pid)` -> (actions (B,2) int64,
+logp (B,), value (B,)) and `forward(obs, pid)` -> (move logits (B,5), bomb
+logits (B,2), value (B,)), plus `act_pair` which serves both players from one
+pass over the shared observation (the collect loop's learner + self-play
+opponent, train/ppo.py:213-249).
+
+Weights come from an ActorCritic mlp state_dict (keys `shared.0.weight`, ...,
+`critic.2.bias`) and are packed once into the kernel's layout: float16
+matrices in MFMA B-fragment order (see qqt-gpu-sim_amd/csrc/mlp.hip) with each
+player's view permutation folded into the first layer (train/model.py:121-139),
+float32 bias / LayerNorm vectors.
+
+Sampling replaces `Categorical.sample` (torch.multinomial, which cannot take
+injected randomness) with an inverse-CDF draw on uniforms: given the same
+logits, masks and uniforms it is reproducible bit for bit on the host.  The
+uniforms come from Philox(seed, row, tick) unless passed explicitly.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _capi
+from .config import n_obs_channels, view_perm
+
+KBLOCK = 64
+HID = 128
+HEAD = 64
+
+
+def column_permutation(pid: int, p: int, c: int, hw: int) -> torch.Tensor:
+    """First-layer columns of player `pid`'s view: block k of the permuted
+    weight is block argsort(view_perm)[k] of the original."""
+    inv = torch.argsort(torch.tensor(view_perm(pid, p, c)))
+    return (inv.view(c, 1) * hw + torch.arange(hw).view(1, hw)).reshape(-1)
+
+
+def _frag(w: torch.Tensor, kpad: int, residual: bool = False) -> torch.Tensor:
+    """(n_out, k) float matrix -> float16 B fragments [tile][kblock][lane][16]
+    (of w itself, or of its float16 residual w - float16(w))."""
+    n, k = w.shape
+    assert n % 16 == 0
+    out = torch.zeros((n, kpad), dtype=torch.float32)
+    out[:, :k] = w.float().cpu()
+    if residual:
+        out = out - out.half().float()
+    kb = kpad // KBLOCK
+    f = out.view(n // 16, 16, kb, 4, 16).permute(0, 2, 3, 1, 4).contiguous()
+    return f.half().reshape(-1)
+
+
+def pack_mlp(params: dict, n_players: int = 2, obs_shape=(14, 13, 13)) -> dict:
+    """Host-side packing of an ActorCritic mlp state_dict (CPU tensors out)."""
+    c, h, w = obs_shape
+    hw = h * w
+    k0 = c * hw
+    kpad = math.ceil(k0 / KBLOCK) * KBLOCK
+    W0 = params["shared.0.weight"].float().cpu()
+    if W0.shape != (HID, k0):
+        raise ValueError(f"shared.0.weight must be {(HID, k0)}, got {tuple(W0.shape)}")
+    per_pid = [W0[:, column_permutation(pid, n_players, c, hw)] for pid in range(n_players)]
+    w0 = torch.cat([_frag(wp, kpad) for wp in per_pid])
+    w1_src = params["shared.3.weight"]
+    w1, w1_lo = _frag(w1_src, HID), _frag(w1_src, HID, True)
+    heads = ("move_head", "bomb_head", "critic")
+    wh_src = torch.cat([params[f"{n}.0.weight"].float() for n in heads])
+    wh, wh_lo = _frag(wh_src, HID), _frag(wh_src, HID, True)
+    wfin = torch.zeros((16, 3 * HEAD), dtype=torch.float32)
+    outs = [params[f"{n}.2.weight"].float() for n in heads]
+    row = 0
+    for i, o in enumerate(outs):
+        wfin[row:row + o.shape[0], i * HEAD:(i + 1) * HEAD] = o
+        row += o.shape[0]
+    if row != 8:
+        raise ValueError("heads must produce 5 + 2 + 1 outputs")
+    wf, wf_lo = _frag(wfin, 3 * HEAD), _frag(wfin, 3 * HEAD, True)
+    vec = lambda k: params[k].float().cpu().contiguous()  # noqa: E731
+    return dict(
+        w0=w0, w1=w1, wh=wh, wf=wf, w1_lo=w1_lo, wh_lo=wh_lo, wf_lo=wf_lo,
+        b0=vec("shared.0.bias"), ln1_w=vec("shared.1.weight"), ln1_b=vec("shared.1.bias"),
+        b1=vec("shared.3.bias"), ln2_w=vec("shared.4.weight"), ln2_b=vec("shared.4.bias"),
+        bh=torch.cat([vec(f"{n}.0.bias") for n in heads]),
+        bf=torch.cat([vec(f"{n}.2.bias") for n in heads]),
+        k0=k0, kblocks0=kpad // KBLOCK)
+
+
+def default_init(obs_shape=(14, 13, 13), n_moves: int = 5, n_bomb: int = 2,
+                 seed: int = 0) -> dict:
+    """PyTorch default init of the mlp ActorCritic layers (nn.Linear
+    kaiming-uniform(a=sqrt(5)) weights, U(+-1/sqrt(fan_in)) biases, LayerNorm
+    1/0) under torch.manual_seed(seed), layers created in module order
+    (train/model.py:140-153).  The global RNG state is restored afterwards."""
+    c, h, w = obs_shape
+    nn = torch.nn
+    with torch.random.fork_rng(devices=[]):
+        torch.manual_seed(seed)
+        shared = nn.Sequential(nn.Linear(c * h * w, HID), nn.LayerNorm(HID), nn.ReLU(),
+                               nn.Linear(HID, HID), nn.LayerNorm(HID), nn.ReLU())
+        heads = {name: nn.Sequential(nn.Linear(HID, HEAD), nn.ReLU(), nn.Linear(HEAD, k))
+                 for name, k in (("move_head", n_moves), ("bomb_head", n_bomb), ("critic", 1))}
+    out = {f"shared.{k}": v for k, v in shared.state_dict().items()}
+    for name, mod in heads.items():
+        out.update({f"{name}.{k}": v for k, v in mod.state_dict().items()})
+    return {k: v.detach().clone() for k, v in out.items()}
+
+
+class HipActorCritic:
+    def __init__(self, state_dict: dict | None = None, obs_shape=(14, 13, 13),
+                 n_players: int = 2, device="cuda", seed: int = 0):
+        self.obs_shape = tuple(obs_shape)
+        self.n_players = n_players
+        if n_obs_channels(n_players) != self.obs_shape[0]:
+            raise ValueError("observation channels do not match n_players")
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise ValueError("HipActorCritic runs on a ROCm device")
+        self.seed = int(seed)
+        self.tick = 0
+        self._lib = _capi.lib()
+        self.load_state_dict(state_dict if state_dict is not None else default_init(obs_shape))
+
+    def load_state_dict(self, state_dict: dict) -> None:
+        self.params = {k: v.detach().float().cpu().clone() for k, v in state_dict.items()}
+        packed = pack_mlp(self.params, self.n_players, self.obs_shape)
+        self.k0, self.kblocks0 = packed.pop("k0"), packed.pop("kblocks0")
+        self._w = {k: v.to(self.device).contiguous() for k, v in packed.items()}
+
+    def n_params(self) -> int:
+        return sum(v.numel() for v in self.params.values())
+
+    # ------------------------------------------------------------ launch
+    def _run(self, obs, npid, pid0, sample, mm=None, bm=None, mm_strides=(0, 0),
+             bm_strides=(0, 0), uniforms=None, actions=None, actions_i8=None, logp=None,
+             value=None, logits=None, tick=None):
+        b = obs.shape[0]
+        flat = obs.reshape(b, -1) if obs.is_contiguous() else obs.contiguous().reshape(b, -1)
+        if flat.dtype != torch.float16:
+            flat = flat.half()
+        if flat.shape[1] != self.k0:
+            raise ValueError(f"observation rows must have {self.k0} values")
+        a = _capi.MlpArgsC()
+        a.batch, a.npid, a.pid0, a.sample = b, npid, pid0, int(sample)
+        a.k0, a.kblocks0, a.obs_stride = self.k0, self.kblocks0, flat.stride(0)
+        a.mm_row_stride, a.mm_pid_stride = mm_strides
+        a.bm_row_stride, a.bm_pid_stride = bm_strides
+        a.seed = self.seed & 0xFFFFFFFFFFFFFFFF
+        a.tick = (self.tick if tick is None else tick) & 0xFFFFFFFF
+        a.obs = flat.data_ptr()
+        for k, v in self._w.items():
+            setattr(a, k, v.data_ptr())
+        a.move_mask = _capi.ptr(mm)
+        a.bomb_mask = _capi.ptr(bm)
+        a.uniforms = _capi.ptr(uniforms)
+        a.actions = _capi.ptr(actions)
+        a.actions_i8 = _capi.ptr(actions_i8)
+        a.logp_out = _capi.ptr(logp)
+        a.value_out = _capi.ptr(value)
+        a.logits_out = _capi.ptr(logits)
+        _capi.check(self._lib.qqt_mlp_act(a, _capi.stream_handle(self.device)))
+        return flat
+
+    @staticmethod
+    def _u8(mask):
+        m = mask if mask.dtype == torch.uint8 else mask.to(torch.uint8)
+        return m.contiguous()
+
+    # ------------------------------------------------------------ API
+    def forward(self, obs, pid: int = 0):
+        """(move logits (B,5), bomb logits (B,2), value (B,)) of player `pid`."""
+        b = obs.shape[0]
+        out = torch.empty((b, 1, 8), dtype=torch.float32, device=self.device)
+        keep = self._run(obs, 1, pid, False, logits=out)  # noqa: F841
+        return out[:, 0, :5], out[:, 0, 5:7], out[:, 0, 7]
+
+    __call__ = forward
+
+    def act(self, obs, move_mask, bomb_mask, pid: int = 0, uniforms=None):
+        """Sample one step for player `pid` (train/model.py:230-245)."""
+        b = obs.shape[0]
+        mm = self._u8(move_mask)
+        bm = self._u8(bomb_mask)
+        acts = torch.empty((b, 1, 2), dtype=torch.int64, device=self.device)
+        logp = torch.empty((b, 1), dtype=torch.float32, device=self.device)
+        val = torch.empty((b, 1), dtype=torch.float32, device=self.device)
+        u = None if uniforms is None else uniforms.to(self.device, torch.float32).reshape(b, 1, 2).contiguous()
+        self._run(obs, 1, pid, True, mm=mm, bm=bm, mm_strides=(5, 0), bm_strides=(2, 0),
+                  uniforms=u, actions=acts, logp=logp, value=val)
+        if uniforms is None:
+            self.tick += 1
+        return acts[:, 0], logp[:, 0], val[:, 0]
+
+    def act_pair(self, obs, move_mask, bomb_mask, uniforms=None, out=None, logits=False):
+        """Both players from one pass: masks (B,P,5)/(B,P,2); returns
+        (actions (B,P,2) int64, logp (B,P), value (B,P)[, logits (B,P,8)])."""
+        b, p = obs.shape[0], self.n_players
+        if p != 2:
+            raise ValueError("act_pair serves two players")
+        mm = self._u8(move_mask)
+        bm = self._u8(bomb_mask)
+        if out is None:
+            out = dict(actions=torch.empty((b, p, 2), dtype=torch.int64, device=self.device),
+                       logp=torch.empty((b, p), dtype=torch.float32, device=self.device),
+                       value=torch.empty((b, p), dtype=torch.float32, device=self.device))
+        lg = torch.empty((b, p, 8), dtype=torch.float32, device=self.device) if logits else None
+        u = None if uniforms is None else uniforms.to(self.device, torch.float32).reshape(b, p, 2).contiguous()
+        self._run(obs, 2, 0, True, mm=mm, bm=bm, mm_strides=(5 * p, 5), bm_strides=(2 * p, 2),
+                  uniforms=u, actions=out.get("actions"), actions_i8=out.get("actions_i8"),
+                  logp=out.get("logp"), value=out.get("value"), logits=lg)
+        if uniforms is None:
+            self.tick += 1
+        res = (out.get("actions", out.get("actions_i8")), out.get("logp"), out.get("value"))
+        return res + ((lg,) if logits else ())
+
+    def evaluate(self, obs, move_mask, bomb_mask, actions, pid: int = 0):
+        """(logp, entropy, value) of given actions (train/model.py:247-256)."""
+        ml, bl, v = self.forward(obs, pid)
+        neg = torch.finfo(torch.float32).min
+        lp, ent = 0.0, 0.0
+        for logits, mask, act in ((ml, move_mask, actions[..., 0]), (bl, bomb_mask, actions[..., 1])):
+            d = torch.distributions.Categorical(
+                logits=torch.where(mask.bool(), logits, torch.full_like(logits, neg)))
+            lp = lp + d.log_prob(act)
+            ent = ent + d.entropy()
+        return lp, ent, v
