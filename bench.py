@@ -1,0 +1,237 @@
+#!/usr/bin/env python3
+"""Self-play rollout throughput on one MI355X: env-steps/s at 5632 envs.
+
+One step = one env-step of the collect loop for every env (train/ppo.py:213-249):
+both players' MLP actor/critic forward with masked factored sampling, then
+the tick (movement, bombs, chain explosion, danger map, rewards, auto-reset,
+14-channel float16 observation, legality masks).  On this path that is two
+kernel launches per step, `mlp_act_kernel` and `tick_kernel`, on torch's
+current stream.
+
+Workload: 5632 envs, 13x13 map with border walls, pillars at even/even
+cells and a brick on every other free cell outside the spawn L with p 0.7,
+two players spawning in opposite corners (random side swap), training corridor
+rules (0.3 cell/tick, 1800-tick episodes), MLP 2366->128->LN->ReLU->128->LN->
+ReLU->heads with PyTorch default init (manual_seed 0), auto-reset on done.
+Maps and weights are synthetic; everything is resident in HBM before timing.
+
+Prints ONE JSON line (rank 0).  `roofline` prices the dominant kernel against
+its bound: the tick kernel against HBM (algorithmic bytes per env-step below),
+the MLP kernel against dense float16 MFMA (algorithmic FLOP per env-step).
+Kernel durations come from HIP events recorded on the launch stream around
+every launch inside the timed region.  `traffic` is read from the committed
+rocprofv3 FETCH_SIZE/WRITE_SIZE summary when one exists.  `cpu_baseline`
+times the oracle (the CPU restatement of the reference path) on the host
+cores over a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "qqt-gpu-sim_amd"))
+
+METRIC = "env-steps/s at 5632 envs (step+obs+MLP act), 1 MI355X; % HBM/MFMA roofline"
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+# Algorithmic bytes of one env-step of the tick kernel: packed state read +
+# write (169 cells x 4 B + 2 players x 48 B + 16 B, twice), the float16
+# observation (14 x 169 x 2 B), actions (4 B), masks (14 B), reward (8 B),
+# done (1 B).
+TICK_BYTES_PER_ENV = 2 * (169 * 4 + 2 * 48 + 16) + 14 * 169 * 2 + 4 + 14 + 8 + 1
+# Algorithmic bytes of one env-step of the MLP kernel: observation read once
+# for both players, masks, int8 actions, logp and value.
+MLP_BYTES_PER_ENV = 14 * 169 * 2 + 14 + 4 + 16
+# Algorithmic FLOP of one env-step of the MLP: two players x 2 x MACs of
+# 2366x128 + 128x128 + 3 x 128x64 + 64x(5+2+1).
+MLP_FLOP_PER_ENV = 2 * 2 * (2366 * 128 + 128 * 128 + 3 * 128 * 64 + 64 * 8)
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_rollout_5632.json")
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--envs", type=int, default=5632)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="CPU work budget of the cpu_baseline sample (0 = skip)")
+    ap.add_argument("--copy-calibrate", action="store_true",
+                    help="after timing, run a 512 MiB device copy (HBM counter calibration)")
+    return ap.parse_args()
+
+
+def build_workload(n, seed, device):
+    from qqtsim.config import corridor_training_config
+    from qqtsim.maps import MapSpec
+    from qqtsim.policy import HipActorCritic, default_init
+    from qqtsim.rollout import Rollout
+    from qqtsim.sim import HipBatchedSim
+
+    cfg = corridor_training_config()
+    spec = MapSpec(kind="pillars", brick_p=0.7, swap_spawns=True)
+    sim = HipBatchedSim(cfg, n, device=device, seed=seed, map_spec=spec)
+    net = HipActorCritic(default_init(cfg.obs_shape), device=device, seed=seed)
+    return cfg, spec, Rollout(sim, net)
+
+
+def cpu_baseline(cfg, spec, n, seed, budget_s):
+    """The oracle's env-step on the host cores: observe, legal_mask, both
+    players' forward + masked sampling, step with auto-reset."""
+    import numpy as np
+    import torch
+
+    from oracle import philox
+    from oracle.policy import mlp_forward, sample_masked
+    from oracle.sim import OracleSim
+    from qqtsim.policy import default_init
+
+    cores = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        cores = min(cores, int(os.environ["OMP_NUM_THREADS"]))
+    torch.set_num_threads(max(1, cores))
+    params = default_init(cfg.obs_shape)
+    sim = OracleSim(cfg, n, spec, seed=seed)
+    envs = np.arange(n)
+
+    def env_step(t):
+        obs = sim.observe()
+        mm, bm = sim.legal_mask()
+        u = philox.uniforms(seed, envs, t, philox.STREAM_POLICY, 4)
+        acts = torch.zeros((n, 2, 2), dtype=torch.int64)
+        for pid in range(2):
+            ml, bl, _ = mlp_forward(params, obs, pid)
+            acts[:, pid, 0] = torch.from_numpy(
+                sample_masked(ml.numpy(), mm[:, pid].numpy(), u[:, 2 * pid])[0])
+            acts[:, pid, 1] = torch.from_numpy(
+                sample_masked(bl.numpy(), bm[:, pid].numpy(), u[:, 2 * pid + 1])[0])
+        sim.step(acts, auto_reset=True)
+
+    for t in range(2):
+        env_step(t)
+    ticks, t0 = 0, time.perf_counter()
+    while True:
+        env_step(2 + ticks)
+        ticks += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or ticks >= 256:
+            break
+    return {"value": n * ticks / el, "unit": "env-steps/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"oracle (torch CPU restatement) on the same workload, {n} envs x "
+                      f"{ticks} timed ticks after 2 warm-up ticks, {el:.1f} s"}
+
+
+def read_traffic(kernel):
+    try:
+        with open(TRAFFIC_FILE) as f:
+            d = json.load(f)
+        k = d["kernels"][kernel]
+        return int(round(k["fetch_bytes"] + k["write_bytes"]))
+    except (OSError, KeyError, ValueError, TypeError):
+        return None
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        sys.exit("bench.py measures one GPU: the rollout has no cross-GPU step and this "
+                 "build runs on a single MI355X (envs shard by index across GPUs with "
+                 "replicated weights; see the sharding notes). Run with --gpus 1.")
+    import torch
+
+    if not torch.cuda.is_available():
+        sys.exit("bench.py needs a ROCm GPU")
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    n, K, W = args.envs, args.steps, args.warmup
+    cfg, spec, roll = build_workload(n, args.seed, dev)
+    for _ in range(W):
+        roll.step()
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream(dev)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * K + 1)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev[0].record(stream)
+    for k in range(K):
+        roll.launch_act()
+        ev[2 * k + 1].record(stream)
+        roll.launch_tick()
+        ev[2 * k + 2].record(stream)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    act_ms = sum(ev[2 * k].elapsed_time(ev[2 * k + 1]) for k in range(K)) / K
+    tick_ms = sum(ev[2 * k + 1].elapsed_time(ev[2 * k + 2]) for k in range(K)) / K
+    done_frac = float(roll.done.float().mean())
+
+    if args.copy_calibrate:
+        src = torch.empty(256 << 20, dtype=torch.int16, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+
+    kernels = {
+        "tick_kernel": {"us": tick_ms * 1e3, "bound": "hbm",
+                        "achieved": TICK_BYTES_PER_ENV * n / (tick_ms * 1e-3) / 1e9,
+                        "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "bytes_per_env": TICK_BYTES_PER_ENV},
+        "mlp_act_kernel": {"us": act_ms * 1e3, "bound": "mfma",
+                           "achieved": MLP_FLOP_PER_ENV * n / (act_ms * 1e-3) / 1e12,
+                           "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                           "flop_per_env": MLP_FLOP_PER_ENV,
+                           "hbm_gbs": MLP_BYTES_PER_ENV * n / (act_ms * 1e-3) / 1e9},
+    }
+    for v in kernels.values():
+        v["frac"] = v["achieved"] / v["peak"]
+    dom = max(kernels, key=lambda k: kernels[k]["us"])
+    d = kernels[dom]
+    roofline = {"kernel": dom, "bound": d["bound"], "achieved": round(d["achieved"], 3),
+                "peak": d["peak"], "unit": d["unit"], "frac": round(d["frac"], 5),
+                "traffic": read_traffic(dom)}
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        cpu = cpu_baseline(cfg, spec, n, args.seed, args.cpu_seconds)
+
+    out = {
+        "metric": METRIC,
+        "value": n * K / el,
+        "unit": "env-steps/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": el / K * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 sim / f16 MFMA (f32 accumulate)",
+        "data": "synthetic: template maps from Philox draws, PyTorch default-init MLP weights",
+        "config": {"workload": "self-play rollout, 5632 envs, 13x13 pillars + 70% bricks, "
+                               "P=2, 14-ch f16 obs, MLP act both players + masked sampling, "
+                               "auto-reset",
+                   "envs": n, "grid": [cfg.height, cfg.width], "players": cfg.n_players,
+                   "brick_p": spec.brick_p, "step_len": cfg.step_len,
+                   "max_steps": cfg.max_steps, "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
+                        for kk, vv in v.items()} for k, v in kernels.items()},
+        "done_fraction_last_tick": done_frac,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,19 @@
+"""qqtsim: the self-play rollout hot path of the bomber simulator on MI355X.
+
+`HipBatchedSim` (the reference's `BatchedSim` API), `HipActorCritic` (the mlp
+`ActorCritic.act/forward/evaluate` API), `Rollout` (observe -> act -> step in
+two launches) and `make_sim`, all over hand-written HIP kernels in
+libqqt_hip.so (C ABI in include/qqt_hip.h).  Importing the package does not
+load the library; the first sim or policy does, and raises if it is missing.
+"""
+
+from .config import SimConfig, corridor_training_config
+from .factory import make_sim
+from .maps import BOMB_STRESS_40, CORRIDOR_70, OPEN_PILLARS, MapSpec
+from .policy import HipActorCritic, default_init
+from .rollout import Rollout
+from .sim import HipBatchedSim
+
+__all__ = ["SimConfig", "corridor_training_config", "make_sim", "MapSpec", "OPEN_PILLARS",
+           "CORRIDOR_70", "BOMB_STRESS_40", "HipActorCritic", "default_init", "Rollout",
+           "HipBatchedSim"]

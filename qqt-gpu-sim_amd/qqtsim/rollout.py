@@ -1,0 +1,114 @@
+"""`Rollout`: one env-step of the self-play collect loop in two launches.
+
+The reference's collect loop (train/ppo.py:213-249) does, per tick,
+`observe()` -> `legal_mask()` -> `act(obs, mm, bm, pid=0)` -> `act(..., pid=1)`
+-> `step(actions)` with auto-reset.  On the HIP path the observation and masks
+of the current state are already in the sim's persistent buffers (the tick
+kernel writes them after stepping and auto-resetting), so an env-step is
+
+    qqt_mlp_act  (both players, masked sampling, int8 actions)
+    qqt_tick     (step + auto-reset + observe + legal masks)
+
+with both argument blocks built once: a tick only updates the Philox counter
+words.  Rewards, done flags, log-probabilities and values land in persistent
+device buffers (`reward`, `done`, `logp`, `value`, `actions`), which callers
+that keep them across ticks copy.  Nothing here synchronises with the host
+except the sim's first tick (it measures the reference's explosion tier
+hint, see `HipBatchedSim`).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _capi
+from .policy import HipActorCritic
+from .sim import HipBatchedSim
+
+
+class Rollout:
+    def __init__(self, sim: HipBatchedSim, policy: HipActorCritic):
+        p = sim.cfg.n_players
+        if p != 2 or policy.n_players != 2:
+            raise ValueError("the self-play rollout serves two players")
+        if tuple(sim.cfg.obs_shape) != tuple(policy.obs_shape):
+            raise ValueError("sim observation and policy input shapes differ")
+        if sim.device != policy.device:
+            raise ValueError("sim and policy live on different devices")
+        self.sim, self.policy = sim, policy
+        n, d = sim.num_envs, sim.device
+        self.actions = torch.zeros((n, p, 2), dtype=torch.int8, device=d)
+        self.logp = torch.zeros((n, p), dtype=torch.float32, device=d)
+        self.value = torch.zeros((n, p), dtype=torch.float32, device=d)
+        self._stream = _capi.stream_handle(d)
+        self._lib = _capi.lib()
+
+        m = _capi.MlpArgsC()
+        m.batch, m.npid, m.pid0, m.sample = n, 2, 0, 1
+        m.k0, m.kblocks0, m.obs_stride = policy.k0, policy.kblocks0, policy.k0
+        m.mm_row_stride, m.mm_pid_stride = 5 * p, 5
+        m.bm_row_stride, m.bm_pid_stride = 2 * p, 2
+        m.seed = policy.seed & 0xFFFFFFFFFFFFFFFF
+        m.obs = sim._obs.data_ptr()
+        for k, v in policy._w.items():
+            setattr(m, k, v.data_ptr())
+        m.move_mask, m.bomb_mask = sim._mm.data_ptr(), sim._bm.data_ptr()
+        m.actions_i8 = self.actions.data_ptr()
+        m.logp_out, m.value_out = self.logp.data_ptr(), self.value.data_ptr()
+        self._mlp = m
+
+        t = _capi.TickArgsC()
+        t.n_envs, t.mode, t.auto_reset = n, _capi.MODE_STEP, 1
+        t.seed = sim.seed & 0xFFFFFFFFFFFFFFFF
+        t.cells, t.players, t.envs = (sim._cells.data_ptr(), sim._players.data_ptr(),
+                                      sim._envs.data_ptr())
+        t.actions_i8 = self.actions.data_ptr()
+        for k, buf in (("reward", sim._reward), ("done", sim._done), ("n_alive", sim._n_alive),
+                       ("died", sim._died), ("winner", sim._winner), ("covered", sim._cov),
+                       ("triggered", sim._trg), ("obs", sim._obs), ("move_mask", sim._mm),
+                       ("bomb_mask", sim._bm)):
+            setattr(t, k, buf.data_ptr())
+        self._tick = t
+
+    @property
+    def reward(self) -> torch.Tensor:
+        return self.sim._reward
+
+    @property
+    def done(self) -> torch.Tensor:
+        return self.sim._done.view(torch.bool)
+
+    def launch_act(self) -> None:
+        """Both players' actions for the current observation (train/model.py:230-245)."""
+        self.sim._refresh()
+        self._mlp.tick = self.policy.tick & 0xFFFFFFFF
+        _capi.check(self._lib.qqt_mlp_act(self._mlp, self._stream))
+        self.policy.tick += 1
+
+    def launch_tick(self) -> None:
+        """Step with the sampled actions, auto-reset, observe, masks
+        (sim/torch_sim.py:895-1261, :605-645)."""
+        sim = self.sim
+        if sim.resolve_tiers is None:
+            sim.resolve_tiers = sim._first_tick_tiers(self.actions) \
+                if sim.exact_reference_resolve else 255
+        t = self._tick
+        t.resolve_tiers = sim.resolve_tiers
+        t.explore_coef = float(sim.explore_coef)
+        t.danger_coef = float(sim.explore_coef * sim.cfg.danger_penalty)
+        t.tick = sim.tick & 0xFFFFFFFF
+        t.epoch = sim.epoch & 0xFFFFFFFF
+        _capi.check(self._lib.qqt_tick(sim._cfg_c, t, self._stream))
+        sim.tick += 1
+        sim.epoch += 1
+        sim._fresh = True
+
+    def step(self) -> None:
+        """One env-step for every env."""
+        self.launch_act()
+        self.launch_tick()
+
+    def run(self, ticks: int) -> None:
+        for _ in range(int(ticks)):
+            self.launch_act()
+            self.launch_tick()
