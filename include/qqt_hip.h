@@ -119,7 +119,8 @@ typedef struct qqt_mlp_args {
   int32_t mm_row_stride, mm_pid_stride;  /* move mask [row*rs + pid*ps + k] */
   int32_t bm_row_stride, bm_pid_stride;  /* bomb mask */
   uint64_t seed;             /* Philox key of the policy uniforms */
-  uint32_t tick, reserved;   /* counter word of the policy uniforms */
+  uint32_t tick;             /* counter word of the policy uniforms */
+  int32_t w0_players;        /* players whose first layers w0 holds (pid0, npid < it) */
   const uint16_t* obs;       /* [B][obs_stride] float16 bits, 4-byte aligned */
   const uint16_t *w0, *w1, *wh, *wf;       /* float16 (hi) fragments */
   const uint16_t *w1_lo, *wh_lo, *wf_lo;   /* float16 residuals w - hi */

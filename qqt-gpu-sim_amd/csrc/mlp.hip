@@ -3,21 +3,31 @@
 // Network (train/model.py:121-196, arch "mlp"): obs (B, C*H*W) float16 ->
 // Linear(2366,128) -> LayerNorm -> ReLU -> Linear(128,128) -> LayerNorm ->
 // ReLU -> three heads Linear(128,64) -> ReLU -> Linear(64, 5 | 2 | 1).
-// A player's view permutation is folded into the first-layer weights, so one
-// pass over the shared observation serves both players: layer 1 is a single
-// (B x 2366) x (2366 x 256) GEMM whose columns are [player 0 | player 1].
+// A player's view permutation is folded into the first-layer weights, so a
+// player is just a column block of one shared weight buffer.
 //
-// Workgroup = 4 wavefronts.  With both players, wavefront w computes rows
-// [0, 64) of the tile for player w/2, output columns 64*(w%2) .. +63; with
-// one player the four wavefronts cover 128 rows.  Every product runs on
-// v_mfma_f32_16x16x32_f16 with float32 accumulation; LayerNorm statistics of
-// a row are combined across the two wavefronts holding its 128 columns
-// through LDS.  The observation is exact in float16 and the first layer's
-// weights are rounded to float16 once; every later layer carries both its
-// activations and its weights as float16 hi/lo pairs (x = hi + lo) and sums
-// the three products hi*hi + hi*lo + lo*hi, which keeps logits within ~5e-4
-// of a float32 forward even for large (orthogonal, gain sqrt 2) weights.  B operands are pre-arranged on the host (qqtsim/policy.py)
-// so each lane reads 32 contiguous bytes per 64-deep K block:
+// Workgroup = 8 wavefronts (2 per SIMD) = one 64-row block of one player.
+// Both players' workgroups of a row block are dispatched back to back on the
+// same XCD (workgroups are dealt to the 8 XCDs round robin), so the second
+// read of the observation tile hits that XCD's L2.
+//
+// Layer 1 (K = 2366) is split over two groups of four wavefronts: group g
+// takes K blocks g, g+2, g+4, ...  Each group streams its 64 x 64 observation
+// tiles through its own double-buffered, XOR-swizzled LDS tile (loaded PD
+// steps ahead into registers); the weight fragments go straight from L2 into
+// registers, PD steps ahead.  Wavefront (g, c) owns output columns
+// 32c..32c+31.  The two groups' partial sums meet in an fp32 LDS tile, where
+// LayerNorm runs row-wise (8 lanes per row, 16 contiguous columns per lane).
+// The small layers split rows and columns over all eight wavefronts.
+//
+// Every product runs on v_mfma_f32_16x16x32_f16 with float32 accumulation.
+// The observation is exact in float16 and the first layer's weights are
+// rounded to float16 once; every later layer carries both its activations
+// and its weights as float16 hi/lo pairs (x = hi + lo) and sums the three
+// products hi*hi + hi*lo + lo*hi, which keeps logits within ~5e-4 of a
+// float32 forward even for large (orthogonal, gain sqrt 2) weights.  B
+// operands are pre-arranged on the host (qqtsim/policy.py) so each lane reads
+// 32 contiguous bytes per 64-deep K block:
 //   frag[tile][kblock][lane][16] = W[16*tile + lane%16][64*kblock + 16*(lane/16) + j].
 // The matching A fragment is the lane's 16 contiguous halves of its row, so
 // the K order inside a block is a permutation shared by A and B.
@@ -38,7 +48,18 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int HID = 128;           // hidden width
 constexpr int HEAD = 64;           // head hidden width
 constexpr int NOUT = 8;            // 5 move + 2 bomb + 1 value
-constexpr int ROWS = 64;           // rows per wavefront pair
+constexpr int ROWS = 64;           // rows per workgroup
+constexpr int NTHR = 512;          // 8 wavefronts
+constexpr int FST = HID + 4;       // fp32 row stride of the LayerNorm tile (bank spread)
+#ifndef QQT_MLP_PD
+#define QQT_MLP_PD 2
+#endif
+constexpr int PD = QQT_MLP_PD;     // K blocks of layer 1 in flight per group (even)
+static_assert(PD >= 2 && PD % 2 == 0, "the x tile ring pairs with an LDS double buffer");
+
+// parameter vectors staged in LDS (floats)
+constexpr int V_B0 = 0, V_G1 = 128, V_BE1 = 256, V_B1 = 384, V_G2 = 512, V_BE2 = 640;
+constexpr int V_BH = 768, V_BF = 960, V_N = 968;
 
 struct Frag16 { half8 lo, hi; };   // 16 halves of one lane in one K block
 
@@ -57,127 +78,166 @@ __device__ __forceinline__ Frag16 load_b(const uint16_t* p) {
   return f;
 }
 
-// 16 halves of an observation row starting at element k (4-byte aligned).
-__device__ __forceinline__ Frag16 load_a_global(const uint16_t* row, int k, int kmax) {
-  uint32_t v[8];
-  const uint32_t* p = reinterpret_cast<const uint32_t*>(row + k);
-  if (k + 16 <= kmax) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = __builtin_nontemporal_load(p + i);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = (k + 2 * i + 2 <= kmax) ? p[i] : 0u;
-  }
-  Frag16 f;
-  f.lo = as_h8(make_uint4(v[0], v[1], v[2], v[3]));
-  f.hi = as_h8(make_uint4(v[4], v[5], v[6], v[7]));
-  return f;
-}
-
 __device__ __forceinline__ floatx4 mfma(half8 a, half8 b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// Activations as float16 hi/lo planes: h1 and h2 ([slot][plane][row][128])
-// each fill 64 KB; the head hidden layer ([slot][plane][row][192], 96 KB)
-// reuses both once every wavefront has finished reading h2.
-constexpr int ACT_HALVES = 2 * 2 * ROWS * HID;   // one of h1 / h2
+// LDS tiles store rows of float16 in 16-byte chunks; chunk c of row r sits at
+// chunk position c ^ (r & 7), so the 16 rows of an A fragment read land on
+// distinct banks.
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ (row & 7); }
+
+constexpr int XT_HALVES = ROWS * 64;            // one 64 x 64 observation tile (8 KB)
+constexpr int H_HALVES = 2 * ROWS * HID;        // hi + lo planes of h1 or h2 (32 KB)
+constexpr int HY_HALVES = 2 * ROWS * 3 * HEAD;  // hi + lo planes of the head layer (48 KB)
+static_assert(HY_HALVES <= 4 * XT_HALVES + H_HALVES, "head layer reuses the x tiles and h1");
+static_assert(ROWS * HID * 2 <= 4 * XT_HALVES, "the second partial tile fits in the x tiles");
+
 struct __align__(16) MlpLds {
-  uint16_t act[2 * ACT_HALVES];
-  float logit[2][ROWS][NOUT];
-  float stat[2][2][ROWS];            // [slot][half][row] partial row sums
+  uint16_t xs_h1[4 * XT_HALVES + H_HALVES];   // x tiles [group][buffer] | h1; later the head layer
+  uint16_t h2[H_HALVES];
+  float f[ROWS][FST];                         // fp32 pre-LayerNorm tile
+  float vec[V_N];                             // biases and LayerNorm affine parameters
+  float logit[ROWS][NOUT];
 };
-__device__ __forceinline__ uint16_t* h_at(uint16_t* base, int slot, int plane, int row, int col) {
-  return base + ((slot * 2 + plane) * ROWS + row) * HID + col;
-}
-__device__ __forceinline__ uint16_t* hy_at(uint16_t* base, int slot, int plane, int row, int col) {
-  return base + ((slot * 2 + plane) * ROWS + row) * (3 * HEAD) + col;
+
+__device__ __forceinline__ uint16_t* h_at(uint16_t* base, int width, int plane, int row, int col) {
+  return base + (plane * ROWS + row) * width + (swz(row, col >> 3) << 3) + (col & 7);
 }
 __device__ __forceinline__ void split_store(uint16_t* hi, uint16_t* lo, float y) {
   const __half h = __float2half_rn(y);
   *hi = __half_as_ushort(h);
   *lo = __half_as_ushort(__float2half_rn(y - __half2float(h)));
 }
+// A fragment (16 halves) of row `row`, K block kb, from a swizzled tile.
+__device__ __forceinline__ Frag16 read_a(const uint16_t* plane, int width, int row, int kb, int q) {
+  const uint16_t* r = plane + row * width;
+  const int c = 8 * kb + 2 * q;
+  Frag16 f;
+  f.lo = as_h8(*reinterpret_cast<const uint4*>(r + (swz(row, c) << 3)));
+  f.hi = as_h8(*reinterpret_cast<const uint4*>(r + (swz(row, c + 1) << 3)));
+  return f;
+}
 
-// Sum over the 16 lanes that share lane/16 (they hold the same rows).
-__device__ __forceinline__ float sum16(float v) {
+// Sum over the 8 consecutive lanes that hold one row in the LayerNorm phase.
+__device__ __forceinline__ float sum8(float v) {
   v += __shfl_xor(v, 1, 64);
   v += __shfl_xor(v, 2, 64);
   v += __shfl_xor(v, 4, 64);
-  v += __shfl_xor(v, 8, 64);
   return v;
 }
 
-// Bias + LayerNorm(128) + ReLU of a 64 x 64 accumulator block (this wave's
-// half of one player's columns); writes float16 into dst[row][col].
-__device__ __forceinline__ void ln_relu_store(floatx4 (&acc)[4][4], const float* bias,
-                                              const float* gamma, const float* beta,
-                                              MlpLds& s, int slot, int half, int lane,
-                                              uint16_t* dst) {
+// fp32 partial-sum tile of layer 1's second K group, kept in the (dead) x
+// tiles: 64 rows x 128 floats, float4 j of row r stored at j ^ (r & 31).
+__device__ __forceinline__ float* f1_at(uint16_t* xs, int row, int col) {
+  float* base = reinterpret_cast<float*>(xs);
+  return base + row * HID + ((((col >> 2) ^ (row & 31))) << 2) + (col & 3);
+}
+
+// Row-wise bias + LayerNorm(128) + ReLU from the fp32 tile (plus the second
+// partial tile f1 when given): thread t owns row t/8, columns 16*(t%8)..+15;
+// writes float16 hi/lo planes of dst.
+__device__ __forceinline__ void layernorm_rows(MlpLds& s, const uint16_t* f1, int vb, int vg,
+                                               int vbe, uint16_t* dst) {
+  const int t = threadIdx.x, row = t >> 3, c0 = 16 * (t & 7);
+  float v[16], ga[16], be[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = c0 + 4 * i;
+    const float4 x = *reinterpret_cast<const float4*>(&s.f[row][c]);
+    const float4 b = *reinterpret_cast<const float4*>(&s.vec[vb + c]);
+    const float4 g = *reinterpret_cast<const float4*>(&s.vec[vg + c]);
+    const float4 e = *reinterpret_cast<const float4*>(&s.vec[vbe + c]);
+    float4 y = x;
+    if (f1) {
+      const float4 z = *reinterpret_cast<const float4*>(
+          f1_at(const_cast<uint16_t*>(f1), row, c));
+      y = make_float4(z.x + x.x, z.y + x.y, z.z + x.z, z.w + x.w);
+    }
+    v[4 * i + 0] = y.x + b.x;
+    v[4 * i + 1] = y.y + b.y;
+    v[4 * i + 2] = y.z + b.z;
+    v[4 * i + 3] = y.w + b.w;
+    ga[4 * i + 0] = g.x; ga[4 * i + 1] = g.y; ga[4 * i + 2] = g.z; ga[4 * i + 3] = g.w;
+    be[4 * i + 0] = e.x; be[4 * i + 1] = e.y; be[4 * i + 2] = e.z; be[4 * i + 3] = e.w;
+  }
+  float p = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) p += v[i];
+  const float mean = sum8(p) * (1.0f / HID);
+  float q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float d = v[i] - mean;
+    q += d * d;
+  }
+  const float rstd = 1.0f / sqrtf(sum8(q) * (1.0f / HID) + 1e-5f);
+  uint32_t hi[8], lo[8];
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    const float y0 = fmaxf((v[i] - mean) * rstd * ga[i] + be[i], 0.0f);
+    const float y1 = fmaxf((v[i + 1] - mean) * rstd * ga[i + 1] + be[i + 1], 0.0f);
+    const __half h0 = __float2half_rn(y0), h1 = __float2half_rn(y1);
+    const __half l0 = __float2half_rn(y0 - __half2float(h0));
+    const __half l1 = __float2half_rn(y1 - __half2float(h1));
+    hi[i / 2] = (uint32_t)__half_as_ushort(h0) | ((uint32_t)__half_as_ushort(h1) << 16);
+    lo[i / 2] = (uint32_t)__half_as_ushort(l0) | ((uint32_t)__half_as_ushort(l1) << 16);
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int chunk = (c0 >> 3) + k;
+    uint16_t* ph = dst + (0 * ROWS + row) * HID + (swz(row, chunk) << 3);
+    uint16_t* pl = dst + (1 * ROWS + row) * HID + (swz(row, chunk) << 3);
+    *reinterpret_cast<uint4*>(ph) = make_uint4(hi[4 * k], hi[4 * k + 1], hi[4 * k + 2], hi[4 * k + 3]);
+    *reinterpret_cast<uint4*>(pl) = make_uint4(lo[4 * k], lo[4 * k + 1], lo[4 * k + 2], lo[4 * k + 3]);
+  }
+}
+
+// hi and lo B fragments of CT column tiles x KB K blocks (tiles tile0..).
+template <int CT, int KB>
+struct SplitB { Frag16 hi[KB][CT], lo[KB][CT]; };
+template <int CT, int KB>
+__device__ __forceinline__ void load_split_b(SplitB<CT, KB>& b, const uint16_t* b_hi,
+                                             const uint16_t* b_lo, int tile0, int lane) {
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      const size_t off = ((size_t)((tile0 + ct) * KB + kb) * 64 + lane) * 16;
+      b.hi[kb][ct] = load_b(b_hi + off);
+      b.lo[kb][ct] = load_b(b_lo + off);
+    }
+}
+
+// RT row tiles (rows 16*(rt0+i) + lane%16) x CT column tiles of a hi/lo layer:
+// acc += A(hi,lo) * B(hi,lo) over KB K blocks.
+template <int RT, int CT, int KB>
+__device__ __forceinline__ void split_gemm(floatx4 (&acc)[RT][CT], const uint16_t* a_hi,
+                                           const uint16_t* a_lo, int width, int rt0,
+                                           const SplitB<CT, KB>& b, int lane) {
   const int r16 = lane & 15, q = lane >> 4;
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-    const float b = bias[64 * half + 16 * ct + r16];
+  for (int kb = 0; kb < KB; ++kb) {
+    Frag16 ah[RT], al[RT];
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[rt][ct][j] += b;
-  }
-  float mean[4][4], rstd[4][4];
-#pragma unroll
-  for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float p = 0.0f;
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) p += acc[rt][ct][j];
-      p = sum16(p);
-      if (r16 == 0) s.stat[slot][half][16 * rt + 4 * q + j] = p;
+    for (int i = 0; i < RT; ++i) {
+      ah[i] = read_a(a_hi, width, 16 * (rt0 + i) + r16, kb, q);
+      al[i] = read_a(a_lo, width, 16 * (rt0 + i) + r16, kb, q);
     }
-  __syncthreads();
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt)
+    for (int ct = 0; ct < CT; ++ct) {
+      const Frag16& bh = b.hi[kb][ct];
+      const Frag16& bl = b.lo[kb][ct];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = 16 * rt + 4 * q + j;
-      mean[rt][j] = (s.stat[slot][0][row] + s.stat[slot][1][row]) * (1.0f / HID);
-    }
-  __syncthreads();
-#pragma unroll
-  for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float p = 0.0f;
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
-        const float d = acc[rt][ct][j] - mean[rt][j];
-        p += d * d;
+      for (int i = 0; i < RT; ++i) {
+        acc[i][ct] = mfma(ah[i].lo, bh.lo, acc[i][ct]);
+        acc[i][ct] = mfma(ah[i].hi, bh.hi, acc[i][ct]);
+        acc[i][ct] = mfma(ah[i].lo, bl.lo, acc[i][ct]);
+        acc[i][ct] = mfma(ah[i].hi, bl.hi, acc[i][ct]);
+        acc[i][ct] = mfma(al[i].lo, bh.lo, acc[i][ct]);
+        acc[i][ct] = mfma(al[i].hi, bh.hi, acc[i][ct]);
       }
-      p = sum16(p);
-      if (r16 == 0) s.stat[slot][half][16 * rt + 4 * q + j] = p;
     }
-  __syncthreads();
-#pragma unroll
-  for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = 16 * rt + 4 * q + j;
-      const float var = (s.stat[slot][0][row] + s.stat[slot][1][row]) * (1.0f / HID);
-      rstd[rt][j] = 1.0f / sqrtf(var + 1e-5f);
-    }
-#pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-    const int col = 64 * half + 16 * ct + r16;
-    const float ga = gamma[col], be = beta[col];
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float y = (acc[rt][ct][j] - mean[rt][j]) * rstd[rt][j] * ga + be;
-        y = fmaxf(y, 0.0f);
-        const int row = 16 * rt + 4 * q + j;
-        split_store(h_at(dst, slot, 0, row, col), h_at(dst, slot, 1, row, col), y);
-      }
   }
 }
 
@@ -212,214 +272,265 @@ __device__ __forceinline__ int sample_masked(const float* logit, const uint8_t* 
   return a;
 }
 
-__global__ __launch_bounds__(256) void mlp_act_kernel(const qqt_mlp_args a) {
+__global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   __shared__ MlpLds s;
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nrb = (a.batch + ROWS - 1) / ROWS;
+  const int xcd = blockIdx.x & 7, seq = blockIdx.x >> 3;
+  const int slot = seq % a.npid;
+  const int rb = (seq / a.npid) * 8 + xcd;
+  if (rb >= nrb) return;                   // padding workgroup (uniform, before any barrier)
+  const int pid = a.npid == 2 ? slot : a.pid0;
+  const int row0 = rb * ROWS;
+  // wavefront index as a scalar: branches and addresses on it stay uniform
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int r16 = lane & 15, q = lane >> 4;
-  const int slot = w >> 1, half = w & 1;
-  const bool two = a.npid == 2;
-  const int pid = two ? slot : a.pid0;
-  const int rows_per_block = two ? ROWS : 2 * ROWS;
-  const int row0 = blockIdx.x * rows_per_block + (two ? 0 : slot * ROWS);
-  const int lslot = slot;  // LDS slot: player slot (two) or row block (one)
+  const int kg = w >> 2, cg = w & 3;       // layer-1 K group, column group
 
-  // ---------------- layer 1: (64 rows) x (64 columns of this player), K = 2366
-  floatx4 acc[4][4];
+  // Parameter vectors: two floats per thread, loaded before the first tiles
+  // (vmcnt retires in order) and written to LDS after they are issued.
+  auto vec_src = [&](int i) -> const float* {
+    return i < V_G1 ? a.b0 + (i - V_B0) : i < V_BE1 ? a.ln1_w + (i - V_G1)
+         : i < V_B1 ? a.ln1_b + (i - V_BE1) : i < V_G2 ? a.b1 + (i - V_B1)
+         : i < V_BE2 ? a.ln2_w + (i - V_G2) : i < V_BH ? a.ln2_b + (i - V_BE2)
+         : i < V_BF ? a.bh + (i - V_BH) : a.bf + (i - V_BF);
+  };
+  const int vi0 = threadIdx.x, vi1 = threadIdx.x + NTHR;   // vi1 < V_N for the first 456
+  const float vv0 = *vec_src(vi0);
+  const float vv1 = vi1 < V_N ? *vec_src(vi1) : 0.0f;
+
+  // ---------------- layer 1: group kg, K blocks kg, kg+2, ...; columns 32cg..32cg+31
+  floatx4 acc[4][2];
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) acc[rt][ct] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-  const uint16_t* rowp[4];
-  bool rowok[4];
+    for (int ct = 0; ct < 2; ++ct) acc[rt][ct] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // x loads: instruction i of wavefront (kg, cg) covers tile rows 16cg+2i,
+  // 16cg+2i+1; lane l reads dword l&31 (two halves) of row 16cg+2i+(l>>5).
+  const int nkb = a.kblocks0;
+  const int dw = lane & 31;
+  const uint32_t* xrow[8];
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt) {
-    const int row = row0 + 16 * rt + r16;
-    rowok[rt] = row < a.batch;
-    rowp[rt] = a.obs + (size_t)(rowok[rt] ? row : 0) * a.obs_stride;
+  for (int i = 0; i < 8; ++i) {
+    const int r = min(row0 + 16 * cg + 2 * i + (lane >> 5), a.batch - 1);
+    xrow[i] = reinterpret_cast<const uint32_t*>(a.obs + (size_t)r * a.obs_stride);
   }
-  const uint16_t* wb = a.w0 + (size_t)((pid * 8 + half * 4) * a.kblocks0) * 64 * 16;
-  for (int kb = 0; kb < a.kblocks0; ++kb) {
-    const int k = 64 * kb + 16 * q;
-    Frag16 af[4], bf[4];
+  const uint16_t* wb = a.w0 + (size_t)((pid * 8 + 2 * cg) * nkb) * 64 * 16 + lane * 16;
+  const size_t wtile = (size_t)nkb * 64 * 16;   // halves between B tiles
+  uint16_t* const xt = s.xs_h1 + kg * 2 * XT_HALVES;   // this group's two x tiles
+
+  // Loads run PD group steps ahead; the tail mask (elements >= k0) is applied
+  // when the registers are written to LDS, so no load is waited on early.
+  // Lanes past k0 read dword 0 of their row (in bounds).
+  auto load_x = [&](int kb, uint32_t (&xr)[8]) {
+    const int k = 64 * kb + 2 * dw;              // first half of this lane's pair
+    const int off = k < a.k0 ? (k >> 1) : 0;     // k0 is even: pairs never straddle
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xr[i] = __builtin_nontemporal_load(xrow[i] + off);
+  };
+  auto load_w = [&](int kb, Frag16 (&br)[2]) {
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) br[ct] = load_b(wb + ct * wtile + (size_t)kb * 64 * 16);
+  };
+  auto store_x = [&](const uint32_t (&xr)[8], int buf, int kb) {
+    const bool ok = 64 * kb + 2 * dw < a.k0;
+    uint32_t* t = reinterpret_cast<uint32_t*>(xt + buf * XT_HALVES);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 16 * cg + 2 * i + (lane >> 5);
+      t[r * 32 + (swz(r, dw >> 2) << 2) + (dw & 3)] = ok ? xr[i] : 0u;
+    }
+  };
+  auto compute = [&](int buf, const Frag16 (&br)[2]) {
+    const uint16_t* t = xt + buf * XT_HALVES;
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
-      af[rt] = rowok[rt] ? load_a_global(rowp[rt], k, a.k0) : Frag16{};
-    }
+      const Frag16 af = read_a(t, 64, 16 * rt + r16, 0, q);
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct)
-      bf[ct] = load_b(wb + ((size_t)(ct * a.kblocks0 + kb) * 64 + lane) * 16);
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
-        acc[rt][ct] = mfma(af[rt].lo, bf[ct].lo, acc[rt][ct]);
-        acc[rt][ct] = mfma(af[rt].hi, bf[ct].hi, acc[rt][ct]);
+      for (int ct = 0; ct < 2; ++ct) {
+        acc[rt][ct] = mfma(af.lo, br[ct].lo, acc[rt][ct]);
+        acc[rt][ct] = mfma(af.hi, br[ct].hi, acc[rt][ct]);
       }
-  }
-  uint16_t* const H1 = s.act;
-  uint16_t* const H2 = s.act + ACT_HALVES;
-  ln_relu_store(acc, a.b0, a.ln1_w, a.ln1_b, s, lslot, half, lane, H1);
-  __syncthreads();
+    }
+  };
 
-  // ---------------- layer 2: K = 128 from LDS
+  // Group step i handles K block 2i + kg.  Register ring of PD steps in
+  // flight, LDS double buffer per group, one barrier per step, no branches:
+  // prefetch indices are clamped to the last block, and the step count is
+  // padded to a multiple of PD with all-zero x tiles (store_x masks every
+  // element >= k0), which add exactly zero.
+  uint32_t xr[PD][8];
+  Frag16 br[PD][2];
+  const int last = nkb - 1;
+  const int nsteps = (((nkb + 1) / 2 + PD - 1) / PD) * PD;
+  auto kblk = [&](int i) { return 2 * i + kg; };
+#pragma unroll
+  for (int j = 0; j < PD; ++j) {
+    load_x(min(kblk(j), last), xr[j]);
+    load_w(min(kblk(j), last), br[j]);
+  }
+
+  const int srow = row0 + (int)threadIdx.x;          // sampling row of threads < 64
+  const bool sampler = threadIdx.x < ROWS && srow < a.batch && a.sample;
+  uint8_t mm[5] = {0, 0, 0, 0, 0}, bm[2] = {0, 0};
+  float um = 0.0f, ub = 0.0f;
+  if (sampler) {
+#pragma unroll
+    for (int k = 0; k < 5; ++k)
+      mm[k] = a.move_mask[(size_t)srow * a.mm_row_stride + (size_t)pid * a.mm_pid_stride + k];
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      bm[k] = a.bomb_mask[(size_t)srow * a.bm_row_stride + (size_t)pid * a.bm_pid_stride + k];
+    const size_t o = (size_t)srow * a.npid + (a.npid == 2 ? slot : 0);
+    if (a.uniforms) {
+      um = a.uniforms[o * 2 + 0];
+      ub = a.uniforms[o * 2 + 1];
+    } else {
+      float u4[4];
+      philox_block(a.seed, (uint32_t)srow, a.tick, STREAM_POLICY, (uint32_t)((2 * pid) >> 2), u4);
+      um = u4[(2 * pid) & 3];
+      ub = u4[(2 * pid + 1) & 3];
+    }
+  }
+
+  s.vec[vi0] = vv0;
+  if (vi1 < V_N) s.vec[vi1] = vv1;
+  store_x(xr[0], 0, kblk(0));
+  load_x(min(kblk(PD), last), xr[0]);
+  __syncthreads();
+  for (int i0 = 0; i0 < nsteps - PD; i0 += PD) {
+#pragma unroll
+    for (int j = 0; j < PD; ++j) {
+      const int i = i0 + j;                 // LDS buffer j&1 holds block kblk(i)
+      compute(j & 1, br[j]);
+      load_w(min(kblk(i + PD), last), br[j]);
+      store_x(xr[(j + 1) % PD], (j + 1) & 1, kblk(i + 1));
+      load_x(min(kblk(i + 1 + PD), last), xr[(j + 1) % PD]);
+      __syncthreads();
+    }
+  }
+  // last PD steps: everything they need is already in flight
+#pragma unroll
+  for (int j = 0; j < PD; ++j) {
+    compute(j & 1, br[j]);
+    if (j + 1 < PD) store_x(xr[(j + 1) % PD], (j + 1) & 1, kblk(nsteps - PD + j + 1));
+    __syncthreads();
+  }
+
+  // Combine the two groups' partial sums in the fp32 tile.
+  uint16_t* const H1 = s.xs_h1 + 4 * XT_HALVES;
+  SplitB<2, 2> w1b;                 // layer-2 weights: in flight during LayerNorm 1
+  const int rh = w >> 2;            // row half of the small layers
+  load_split_b(w1b, a.w1, a.w1_lo, 2 * cg, lane);
+  // The last loop step ended with a barrier, so the x tiles are free.
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) acc[rt][ct] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
-    Frag16 ah[4], al[4];
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
-      const uint4* ph = reinterpret_cast<const uint4*>(h_at(H1, lslot, 0, 16 * rt + r16, 64 * kb + 16 * q));
-      const uint4* pl = reinterpret_cast<const uint4*>(h_at(H1, lslot, 1, 16 * rt + r16, 64 * kb + 16 * q));
-      ah[rt].lo = as_h8(ph[0]); ah[rt].hi = as_h8(ph[1]);
-      al[rt].lo = as_h8(pl[0]); al[rt].hi = as_h8(pl[1]);
-    }
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-      const size_t off = ((size_t)((half * 4 + ct) * 2 + kb) * 64 + lane) * 16;
-      const Frag16 bh = load_b(a.w1 + off), bl = load_b(a.w1_lo + off);
-#pragma unroll
-      for (int rt = 0; rt < 4; ++rt) {
-        acc[rt][ct] = mfma(ah[rt].lo, bh.lo, acc[rt][ct]);
-        acc[rt][ct] = mfma(ah[rt].hi, bh.hi, acc[rt][ct]);
-        acc[rt][ct] = mfma(ah[rt].lo, bl.lo, acc[rt][ct]);
-        acc[rt][ct] = mfma(ah[rt].hi, bl.hi, acc[rt][ct]);
-        acc[rt][ct] = mfma(al[rt].lo, bh.lo, acc[rt][ct]);
-        acc[rt][ct] = mfma(al[rt].hi, bh.hi, acc[rt][ct]);
+      for (int j = 0; j < 4; ++j) {
+        const int row = 16 * rt + 4 * q + j, col = 32 * cg + 16 * ct + r16;
+        float* dstp = kg == 0 ? &s.f[row][col] : f1_at(s.xs_h1, row, col);
+        *dstp = acc[rt][ct][j];
       }
-    }
-  }
-  ln_relu_store(acc, a.b1, a.ln2_w, a.ln2_b, s, lslot, half, lane, H2);
+  __syncthreads();
+  layernorm_rows(s, s.xs_h1, V_B0, V_G1, V_BE1, H1);
   __syncthreads();
 
-  // ---------------- heads, first layer: 192 hidden columns (this wave: 96)
-  {
-    floatx4 hac[4][6];
+  // ---------------- layer 2: 128 -> 128; wavefront w: rows 32rh.., columns 32cg..
+  floatx4 acc2[2][2];
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int ct = 0; ct < 6; ++ct) hac[rt][ct] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int ct = 0; ct < 2; ++ct) acc2[i][ct] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  split_gemm<2, 2, 2>(acc2, H1, H1 + ROWS * HID, HID, 2 * rh, w1b, lane);
+  SplitB<3, 2> whb;                 // head weights: in flight during LayerNorm 2
+  load_split_b(whb, a.wh, a.wh_lo, 3 * cg, lane);
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      Frag16 ah[4], al[4];
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt) {
-        const uint4* ph = reinterpret_cast<const uint4*>(h_at(H2, lslot, 0, 16 * rt + r16, 64 * kb + 16 * q));
-        const uint4* pl = reinterpret_cast<const uint4*>(h_at(H2, lslot, 1, 16 * rt + r16, 64 * kb + 16 * q));
-        ah[rt].lo = as_h8(ph[0]); ah[rt].hi = as_h8(ph[1]);
-        al[rt].lo = as_h8(pl[0]); al[rt].hi = as_h8(pl[1]);
-      }
+    for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-      for (int ct = 0; ct < 6; ++ct) {
-        const size_t off = ((size_t)((half * 6 + ct) * 2 + kb) * 64 + lane) * 16;
-        const Frag16 bh = load_b(a.wh + off), bl = load_b(a.wh_lo + off);
-#pragma unroll
-        for (int rt = 0; rt < 4; ++rt) {
-          hac[rt][ct] = mfma(ah[rt].lo, bh.lo, hac[rt][ct]);
-          hac[rt][ct] = mfma(ah[rt].hi, bh.hi, hac[rt][ct]);
-          hac[rt][ct] = mfma(ah[rt].lo, bl.lo, hac[rt][ct]);
-          hac[rt][ct] = mfma(ah[rt].hi, bl.hi, hac[rt][ct]);
-          hac[rt][ct] = mfma(al[rt].lo, bh.lo, hac[rt][ct]);
-          hac[rt][ct] = mfma(al[rt].hi, bh.hi, hac[rt][ct]);
-        }
-      }
-    }
-    __syncthreads();  // every wavefront is done reading h2: the head layer reuses it
-#pragma unroll
-    for (int ct = 0; ct < 6; ++ct) {
-      const int col = 96 * half + 16 * ct + r16;
-      const float b = a.bh[col];
-#pragma unroll
-      for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int row = 16 * rt + 4 * q + j;
-          split_store(hy_at(s.act, lslot, 0, row, col), hy_at(s.act, lslot, 1, row, col),
-                      fmaxf(hac[rt][ct][j] + b, 0.0f));
-        }
-    }
-  }
+      for (int j = 0; j < 4; ++j)
+        s.f[32 * rh + 16 * i + 4 * q + j][32 * cg + 16 * ct + r16] = acc2[i][ct][j];
+  __syncthreads();
+  layernorm_rows(s, nullptr, V_B1, V_G2, V_BE2, s.h2);
   __syncthreads();
 
-  // ---------------- heads, output layer: 192 -> 8 (block diagonal), MFMA
+  // ---------------- heads, first layer: 128 -> 192; rows 32rh.., columns 48cg..
+  uint16_t* const HY = s.xs_h1;     // x tiles and h1 are dead from here on
   {
-    floatx4 oac[2] = {floatx4{0.0f, 0.0f, 0.0f, 0.0f}, floatx4{0.0f, 0.0f, 0.0f, 0.0f}};
+    floatx4 hac[2][3];
 #pragma unroll
-    for (int kb = 0; kb < 3; ++kb) {
-      const size_t off = ((size_t)kb * 64 + lane) * 16;
-      const Frag16 bh = load_b(a.wf + off), bl = load_b(a.wf_lo + off);
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int rt = 2 * half + i;
-        const uint4* ph = reinterpret_cast<const uint4*>(hy_at(s.act, lslot, 0, 16 * rt + r16, 64 * kb + 16 * q));
-        const uint4* pl = reinterpret_cast<const uint4*>(hy_at(s.act, lslot, 1, 16 * rt + r16, 64 * kb + 16 * q));
-        const half8 h0 = as_h8(ph[0]), h1 = as_h8(ph[1]), l0 = as_h8(pl[0]), l1 = as_h8(pl[1]);
-        oac[i] = mfma(h0, bh.lo, oac[i]);
-        oac[i] = mfma(h1, bh.hi, oac[i]);
-        oac[i] = mfma(h0, bl.lo, oac[i]);
-        oac[i] = mfma(h1, bl.hi, oac[i]);
-        oac[i] = mfma(l0, bh.lo, oac[i]);
-        oac[i] = mfma(l1, bh.hi, oac[i]);
-      }
-    }
-    if (r16 < NOUT) {
-      const float b = a.bf[r16];
+      for (int ct = 0; ct < 3; ++ct) hac[i][ct] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    split_gemm<2, 3, 2>(hac, s.h2, s.h2 + ROWS * HID, HID, 2 * rh, whb, lane);
+#pragma unroll
+    for (int ct = 0; ct < 3; ++ct) {
+      const int col = 48 * cg + 16 * ct + r16;
+      const float b = s.vec[V_BH + col];
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          s.logit[lslot][16 * (2 * half + i) + 4 * q + j][r16] = oac[i][j] + b;
+        for (int j = 0; j < 4; ++j) {
+          const int row = 32 * rh + 16 * i + 4 * q + j;
+          split_store(h_at(HY, 3 * HEAD, 0, row, col), h_at(HY, 3 * HEAD, 1, row, col),
+                      fmaxf(hac[i][ct][j] + b, 0.0f));
+        }
     }
   }
   __syncthreads();
 
-  // ---------------- outputs and sampling: one thread per (row, player slot)
-  if (threadIdx.x < 2 * ROWS) {
-    const int slot2 = threadIdx.x >> 6, rl = threadIdx.x & 63;
-    const int pid2 = two ? slot2 : a.pid0;
-    const int row = blockIdx.x * rows_per_block + (two ? rl : slot2 * ROWS + rl);
-    const int oslot = two ? slot2 : 0;
-    if (row < a.batch) {
-      const float* lg = s.logit[slot2][rl];
-      const size_t o = (size_t)row * a.npid + oslot;
-      if (a.logits_out) {
+  // ---------------- heads, output layer: 192 -> 8 (block diagonal); wavefronts 0-3: rows 16w..
+  if (w < 4) {
+    SplitB<1, 3> wfb;
+    load_split_b(wfb, a.wf, a.wf_lo, 0, lane);
+    floatx4 oac = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int k = 0; k < NOUT; ++k) a.logits_out[o * NOUT + k] = lg[k];
+    for (int kb = 0; kb < 3; ++kb) {
+      const Frag16& bh = wfb.hi[kb][0];
+      const Frag16& bl = wfb.lo[kb][0];
+      const int row = 16 * w + r16;
+      const Frag16 ah = read_a(HY, 3 * HEAD, row, kb, q);
+      const Frag16 al = read_a(HY + ROWS * 3 * HEAD, 3 * HEAD, row, kb, q);
+      oac = mfma(ah.lo, bh.lo, oac);
+      oac = mfma(ah.hi, bh.hi, oac);
+      oac = mfma(ah.lo, bl.lo, oac);
+      oac = mfma(ah.hi, bl.hi, oac);
+      oac = mfma(al.lo, bh.lo, oac);
+      oac = mfma(al.hi, bh.hi, oac);
+    }
+    if (r16 < NOUT) {
+      const float b = s.vec[V_BF + r16];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s.logit[16 * w + 4 * q + j][r16] = oac[j] + b;
+    }
+  }
+  __syncthreads();
+
+  // ---------------- outputs and sampling: one thread per row
+  if (threadIdx.x < ROWS && srow < a.batch) {
+    const float* lg = s.logit[threadIdx.x];
+    const size_t o = (size_t)srow * a.npid + (a.npid == 2 ? slot : 0);
+    if (a.logits_out) {
+#pragma unroll
+      for (int k = 0; k < NOUT; ++k) a.logits_out[o * NOUT + k] = lg[k];
+    }
+    if (a.value_out) a.value_out[o] = lg[7];
+    if (sampler) {
+      float lpm, lpb;
+      const int am = sample_masked<5>(lg, mm, um, &lpm);
+      const int ab = sample_masked<2>(lg + 5, bm, ub, &lpb);
+      if (a.actions) {
+        a.actions[o * 2 + 0] = am;
+        a.actions[o * 2 + 1] = ab;
       }
-      if (a.value_out) a.value_out[o] = lg[7];
-      if (a.sample) {
-        uint8_t mm[5], bm[2];
-#pragma unroll
-        for (int k = 0; k < 5; ++k)
-          mm[k] = a.move_mask[(size_t)row * a.mm_row_stride + (size_t)pid2 * a.mm_pid_stride + k];
-#pragma unroll
-        for (int k = 0; k < 2; ++k)
-          bm[k] = a.bomb_mask[(size_t)row * a.bm_row_stride + (size_t)pid2 * a.bm_pid_stride + k];
-        float um, ub;
-        if (a.uniforms) {
-          um = a.uniforms[o * 2 + 0];
-          ub = a.uniforms[o * 2 + 1];
-        } else {
-          float u4[4];
-          philox_block(a.seed, (uint32_t)row, a.tick, STREAM_POLICY, (uint32_t)((2 * pid2) >> 2), u4);
-          um = u4[(2 * pid2) & 3];
-          ub = u4[(2 * pid2 + 1) & 3];
-        }
-        float lpm, lpb;
-        const int am = sample_masked<5>(lg, mm, um, &lpm);
-        const int ab = sample_masked<2>(lg + 5, bm, ub, &lpb);
-        if (a.actions) {
-          a.actions[o * 2 + 0] = am;
-          a.actions[o * 2 + 1] = ab;
-        }
-        if (a.actions_i8) {
-          a.actions_i8[o * 2 + 0] = (int8_t)am;
-          a.actions_i8[o * 2 + 1] = (int8_t)ab;
-        }
-        if (a.logp_out) a.logp_out[o] = lpm + lpb;
+      if (a.actions_i8) {
+        a.actions_i8[o * 2 + 0] = (int8_t)am;
+        a.actions_i8[o * 2 + 1] = (int8_t)ab;
       }
+      if (a.logp_out) a.logp_out[o] = lpm + lpb;
     }
   }
 }
@@ -439,7 +550,8 @@ int qqt_mlp_act(const qqt_mlp_args* a, void* stream) {
     snprintf(g_err, sizeof(g_err), "qqt_mlp_act: null pointer argument");
     return QQT_E_ARG;
   }
-  if (a->batch <= 0 || (a->npid != 1 && a->npid != 2) || a->pid0 < 0 || a->pid0 > 3 ||
+  if (a->batch <= 0 || (a->npid != 1 && a->npid != 2) || a->w0_players < a->npid ||
+      a->w0_players > 4 || a->pid0 < 0 || (a->npid == 1 && a->pid0 >= a->w0_players) ||
       a->k0 <= 0 || a->k0 % 2 || a->kblocks0 != (a->k0 + 63) / 64 || a->obs_stride < a->k0 ||
       (a->obs_stride % 2) || (((uintptr_t)a->obs) & 3)) {
     snprintf(g_err, sizeof(g_err), "qqt_mlp_act: bad shape/stride/alignment");
@@ -449,9 +561,11 @@ int qqt_mlp_act(const qqt_mlp_args* a, void* stream) {
     snprintf(g_err, sizeof(g_err), "qqt_mlp_act: sampling needs masks");
     return QQT_E_ARG;
   }
-  const int rows_per_block = a->npid == 2 ? ROWS : 2 * ROWS;
-  const int blocks = (a->batch + rows_per_block - 1) / rows_per_block;
-  hipLaunchKernelGGL(mlp_act_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, *a);
+  // one workgroup per (64-row block, player); row blocks are dealt to the 8
+  // XCDs round robin with both players' workgroups adjacent on one XCD
+  const int nrb = (a->batch + ROWS - 1) / ROWS;
+  const int blocks = ((nrb + 7) / 8) * 8 * a->npid;
+  hipLaunchKernelGGL(mlp_act_kernel, dim3(blocks), dim3(NTHR), 0, (hipStream_t)stream, *a);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     snprintf(g_err, sizeof(g_err), "mlp launch failed: %s", hipGetErrorString(err));

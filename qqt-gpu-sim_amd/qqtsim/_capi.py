@@ -52,7 +52,7 @@ class MlpArgsC(ctypes.Structure):
     _fields_ = [(n, _i32) for n in (
         "batch", "npid", "pid0", "sample", "k0", "kblocks0", "obs_stride", "mm_row_stride",
         "mm_pid_stride", "bm_row_stride", "bm_pid_stride")] + [
-        ("seed", _u64), ("tick", _u32), ("reserved", _u32)] + [
+        ("seed", _u64), ("tick", _u32), ("w0_players", _i32)] + [
         (n, _vp) for n in ("obs", "w0", "w1", "wh", "wf", "w1_lo", "wh_lo", "wf_lo", "b0", "ln1_w", "ln1_b", "b1",
                            "ln2_w", "ln2_b", "bh", "bf", "move_mask", "bomb_mask", "uniforms",
                            "actions", "actions_i8", "logp_out", "value_out", "logits_out")]

@@ -150,6 +150,7 @@ class HipActorCritic:
         a.bm_row_stride, a.bm_pid_stride = bm_strides
         a.seed = self.seed & 0xFFFFFFFFFFFFFFFF
         a.tick = (self.tick if tick is None else tick) & 0xFFFFFFFF
+        a.w0_players = self.n_players
         a.obs = flat.data_ptr()
         for k, v in self._w.items():
             setattr(a, k, v.data_ptr())

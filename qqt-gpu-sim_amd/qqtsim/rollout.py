@@ -49,6 +49,7 @@ class Rollout:
         m.mm_row_stride, m.mm_pid_stride = 5 * p, 5
         m.bm_row_stride, m.bm_pid_stride = 2 * p, 2
         m.seed = policy.seed & 0xFFFFFFFFFFFFFFFF
+        m.w0_players = policy.n_players
         m.obs = sim._obs.data_ptr()
         for k, v in policy._w.items():
             setattr(m, k, v.data_ptr())
