@@ -38,10 +38,10 @@ def rays(sources, wall, bombed, blast, brick=None, blast_max_hint=None):
         b_top = blast
     else:
         per_cell = blast
+        b_top = int(per_cell.max()) if per_cell.numel() else 0
         if blast_max_hint is not None:
-            b_top = int(blast_max_hint)
-        else:
-            b_top = int(per_cell.max()) if per_cell.numel() else 0
+            # tiers above the largest range present have no sources
+            b_top = min(b_top, int(blast_max_hint))
     brk = brick if brick is not None else torch.zeros_like(sources)
     open_cell = ~wall
     passes = ~(bombed | brk)

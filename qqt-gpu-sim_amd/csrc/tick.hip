@@ -1038,6 +1038,8 @@ int qqt_tick(const qqt_sim_config* cfg, const qqt_tick_args* a, void* stream) {
   if (a->mode < QQT_MODE_STEP || a->mode > QQT_MODE_PROBE) return fail(QQT_E_ARG, "bad mode");
   if (a->mode == QQT_MODE_STEP && !a->actions && !a->actions_i8)
     return fail(QQT_E_ARG, "STEP needs actions");
+  if (a->mode == QQT_MODE_PROBE && !a->actions && !a->actions_i8)
+    return fail(QQT_E_ARG, "PROBE needs actions");
   if (a->mode == QQT_MODE_RESET && !a->reset_mask) return fail(QQT_E_ARG, "RESET needs reset_mask");
   if (a->mode == QQT_MODE_PROBE && !a->probe_out) return fail(QQT_E_ARG, "PROBE needs probe_out");
   if (a->obs && (((uintptr_t)a->obs) & 15)) return fail(QQT_E_ARG, "obs must be 16-byte aligned");

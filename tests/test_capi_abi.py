@@ -1,0 +1,198 @@
+"""The C ABI library (no GPU needed): it loads, exports every entry point the
+header declares, its structs have the layout the header gives them, and its
+argument checks reject bad calls before anything touches a device."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "qqt_hip.h")
+
+
+def _lib_path():
+    from qqtsim import _build
+
+    if not os.path.exists(_build.LIB):
+        _build.build(verbose=False)
+    return _build.LIB
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from qqtsim import _capi
+
+    _lib_path()
+    return _capi.lib()
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*[\w\s\*]+?\b(qqt_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_entry_points():
+    assert _declared_functions() == ["qqt_abi_version", "qqt_last_error", "qqt_mlp_act",
+                                     "qqt_tick"]
+
+
+def test_library_exports_every_declared_symbol():
+    path = _lib_path()
+    lib = ctypes.CDLL(path)
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    if shutil.which("nm"):
+        out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True,
+                             text=True, check=True).stdout
+        exported = set(re.findall(r"\bT (qqt_\w+)", out))
+        assert set(_declared_functions()) <= exported
+
+
+def test_abi_version(lib):
+    from qqtsim import _capi
+
+    m = re.search(r"#define QQT_ABI_VERSION (\d+)", open(HEADER).read())
+    assert lib.qqt_abi_version() == int(m.group(1)) == _capi.ABI_VERSION
+
+
+def test_header_constants_match_host_mirror():
+    from qqtsim import _capi, state as st
+
+    text = open(HEADER).read()
+    enum = dict((k, int(v)) for k, v in re.findall(r"\b(QQT_[PE]_\w+) = (\d+)", text))
+    assert enum["QQT_P_SLOTS"] == st.P_SLOTS and enum["QQT_E_SLOTS"] == st.E_SLOTS
+    host = dict(Y=st.P_Y, X=st.P_X, ALIVE=st.P_ALIVE, HP=st.P_HP, SINCE_BOMB=st.P_SINCE,
+                BOMBS_CAP=st.P_BOMBS, BLAST_CAP=st.P_BLAST, SPD=st.P_SPD, INVULN=st.P_INV,
+                COMBO=st.P_COMBO, LAST_HIT=st.P_LAST, PENDING_LOST=st.P_PEND,
+                LO_BOMBS=st.P_LOB, LO_BLAST=st.P_LOZ, LO_SPD=st.P_LOS)
+    for name, v in host.items():
+        assert enum["QQT_P_" + name] == v, name
+    for name, v in dict(T=st.E_T, CRATE_PROB=st.E_CRATE_PROB, MAP_KIND=st.E_KIND).items():
+        assert enum["QQT_E_" + name] == v, name
+    modes = dict((k, int(v)) for k, v in re.findall(r"#define QQT_MODE_(\w+) (\d+)", text))
+    assert (modes["STEP"], modes["OBSERVE"], modes["RESET"], modes["PROBE"]) == (
+        _capi.MODE_STEP, _capi.MODE_OBSERVE, _capi.MODE_RESET, _capi.MODE_PROBE)
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="needs gcc")
+def test_struct_layouts_match_the_header(tmp_path):
+    """offsetof/sizeof of every ctypes field, from a C program built against
+    the header, must equal the ctypes mirror's."""
+    from qqtsim import _capi
+
+    structs = {"qqt_sim_config": _capi.SimConfigC, "qqt_tick_args": _capi.TickArgsC,
+               "qqt_mlp_args": _capi.MlpArgsC}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "qqt_hip.h"',
+             'int main(void) {']
+    for cname, cls in structs.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in cls._fields_:
+            lines.append(f'  printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines += ['  return 0;', '}']
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)],
+                   check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout
+    got = {tuple(l.split()[:2]): int(l.split()[2]) for l in out.strip().splitlines()}
+    for cname, cls in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(cls), cname
+        for fname, _ in cls._fields_:
+            assert got[(cname, fname)] == getattr(cls, fname).offset, (cname, fname)
+
+
+def _tick_args(**kw):
+    from qqtsim import _capi
+
+    a = _capi.TickArgsC()
+    a.n_envs, a.mode = 4, _capi.MODE_OBSERVE
+    a.cells, a.players, a.envs = 0x1000, 0x2000, 0x3000   # never dereferenced on these paths
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def _cfg(**kw):
+    from qqtsim.config import corridor_training_config
+    from qqtsim.maps import MapSpec
+    from qqtsim.sim import config_struct
+
+    c = config_struct(corridor_training_config(), MapSpec())
+    for k, v in kw.items():
+        setattr(c, k, v)
+    return c
+
+
+@pytest.mark.parametrize("cfg_kw,args_kw,msg", [
+    ({}, dict(n_envs=0), "n_envs"),
+    ({}, dict(cells=None), "null state"),
+    ({}, dict(mode=7), "bad mode"),
+    ({}, dict(mode=0), "STEP needs actions"),
+    ({}, dict(mode=2), "RESET needs reset_mask"),
+    ({}, dict(mode=3), "PROBE"),
+    ({}, dict(obs=0x1008), "16-byte aligned"),
+    (dict(fuse=0), {}, "fuse"),
+    (dict(fuse=300), {}, "fuse"),
+    (dict(bombs_lo=3, bombs_hi=2), {}, "cap ranges"),
+])
+def test_tick_rejects_bad_arguments(lib, cfg_kw, args_kw, msg):
+    rc = lib.qqt_tick(_cfg(**cfg_kw), _tick_args(**args_kw), None)
+    assert rc == -1
+    assert msg in lib.qqt_last_error().decode()
+
+
+def test_tick_null_config(lib):
+    assert lib.qqt_tick(None, None, None) == -1
+    assert b"null" in lib.qqt_last_error()
+
+
+def test_tick_unsupported_grid(lib):
+    rc = lib.qqt_tick(_cfg(height=11, width=11), _tick_args(), None)
+    assert rc == -3
+    assert b"not compiled" in lib.qqt_last_error()
+
+
+def _mlp_args(**kw):
+    from qqtsim import _capi
+
+    a = _capi.MlpArgsC()
+    a.batch, a.npid, a.pid0, a.sample = 8, 2, 0, 0
+    a.k0, a.kblocks0, a.obs_stride, a.w0_players = 2366, 37, 2366, 2
+    for i, name in enumerate(("obs", "w0", "w1", "wh", "wf", "w1_lo", "wh_lo", "wf_lo", "b0",
+                              "ln1_w", "ln1_b", "b1", "ln2_w", "ln2_b", "bh", "bf")):
+        setattr(a, name, 0x10000 * (i + 1))
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(w1_lo=None), "null pointer"),
+    (dict(batch=0), "bad shape"),
+    (dict(npid=3), "bad shape"),
+    (dict(k0=2365), "bad shape"),
+    (dict(kblocks0=36), "bad shape"),
+    (dict(obs_stride=2000), "bad shape"),
+    (dict(obs=0x10002), "bad shape"),
+    (dict(npid=1, pid0=2), "bad shape"),
+    (dict(w0_players=1), "bad shape"),
+    (dict(sample=1), "sampling needs masks"),
+])
+def test_mlp_rejects_bad_arguments(lib, kw, msg):
+    assert lib.qqt_mlp_act(_mlp_args(**kw), None) == -1
+    assert msg in lib.qqt_last_error().decode()
+
+
+def test_errors_raise_in_python(lib):
+    from qqtsim import _capi
+
+    with pytest.raises(ValueError, match="n_envs"):
+        _capi.check(lib.qqt_tick(_cfg(), _tick_args(n_envs=-1), None))

@@ -1,0 +1,152 @@
+"""Host-side layout logic (CPU only): the packed device state, the MFMA
+fragment packing of the MLP weights, and the float32 rule constants."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from qqtsim import state as st
+from qqtsim.config import corridor_training_config
+from qqtsim.maps import MapSpec
+from qqtsim.policy import KBLOCK, _frag, default_init, pack_mlp
+from qqtsim.sim import config_struct
+
+
+def _random_state(n=5, h=13, w=13, p=2, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    ri = lambda lo, hi, shape, dt=torch.long: torch.randint(lo, hi, shape, generator=g).to(dt)  # noqa: E731
+    return dict(
+        wall=ri(0, 2, (n, h, w), torch.bool), brick=ri(0, 2, (n, h, w), torch.bool),
+        crate=ri(0, 2, (n, h, w), torch.bool), recycle=ri(0, 2, (n, h, w), torch.bool),
+        fuse=ri(0, 256, (n, h, w), torch.int16), owner=ri(-1, 4, (n, h, w), torch.int8),
+        bomb_blast=ri(0, 256, (n, h, w), torch.int16),
+        pos=torch.rand((n, p, 2), generator=g) * 12.0 + 0.3,
+        alive=ri(0, 2, (n, p), torch.bool), hp=ri(0, 6, (n, p), torch.uint8),
+        since_bomb=ri(-5, 100, (n, p), torch.int32), bombs_cap=ri(0, 11, (n, p)),
+        blast_cap=ri(0, 8, (n, p)), spd_g=torch.rand((n, p), generator=g) + 0.5,
+        invuln=ri(0, 31, (n, p)), combo=ri(0, 9, (n, p)), last_hit=ri(-1000, 2000, (n, p)),
+        pending_lost=ri(0, 7, (n, p)), lo_bombs=ri(0, 3, (n, p)), lo_blast=ri(0, 3, (n, p)),
+        lo_spd=torch.rand((n, p), generator=g), t=ri(0, 1800, (n,)),
+        crate_prob=torch.rand((n,), generator=g), map_kind=ri(0, 2, (n,)))
+
+
+def _packed(n=5, h=13, w=13, p=2):
+    return (torch.zeros((n, h * w), dtype=torch.int32),
+            torch.zeros((n, p, st.P_SLOTS), dtype=torch.int32),
+            torch.zeros((n, st.E_SLOTS), dtype=torch.int32))
+
+
+def test_state_round_trip_is_exact():
+    snap = _random_state()
+    cells, players, envs = _packed()
+    st.pack_into(cells, players, envs, snap, 13, 13)
+    back = st.unpack(cells, players, envs, 13, 13)
+    assert set(back) == set(st.ALL_KEYS)
+    for k, v in snap.items():
+        b = back[k]
+        if v.dtype.is_floating_point:
+            assert torch.equal(b.view(torch.int32), v.float().view(torch.int32)), k
+        else:
+            assert torch.equal(b.long(), v.long()), k
+
+
+def test_cell_word_bit_layout():
+    """bits 0-7 fuse, 8-15 owner (int8), 16-23 bomb_blast, 24 wall, 25 brick,
+    26 crate, 27 recycle-crate (the layout the C header documents)."""
+    snap = {k: torch.zeros(1, 13, 13, dtype=dt) for k, dt in (
+        ("wall", torch.bool), ("brick", torch.bool), ("crate", torch.bool),
+        ("recycle", torch.bool), ("fuse", torch.int16), ("owner", torch.int8),
+        ("bomb_blast", torch.int16))}
+    snap["fuse"][0, 2, 3] = 30
+    snap["owner"][0, 2, 3] = -1
+    snap["bomb_blast"][0, 2, 3] = 5
+    snap["wall"][0, 0, 0] = True
+    snap["recycle"][0, 12, 12] = True
+    cells, players, envs = _packed(n=1)
+    st.pack_into(cells, players, envs, snap, 13, 13)
+    assert int(cells[0, 2 * 13 + 3]) == 30 | (0xFF << 8) | (5 << 16)
+    assert int(cells[0, 0]) == 1 << 24
+    assert int(cells[0, 168]) == 1 << 27
+
+
+@pytest.mark.parametrize("key,val", [("fuse", 256), ("bomb_blast", -1), ("t", -3)])
+def test_pack_rejects_values_the_word_cannot_hold(key, val):
+    snap = _random_state(n=2)
+    snap[key] = torch.full_like(snap[key], val)
+    cells, players, envs = _packed(n=2)
+    with pytest.raises(ValueError):
+        st.pack_into(cells, players, envs, snap, 13, 13)
+
+
+def test_unpack_bits():
+    words = torch.zeros((2, 8), dtype=torch.int32)
+    words[0, 0] = 1 << 5
+    words[1, 5] = 1 << 8          # cell 168
+    m = st.unpack_bits(words, 13, 13)
+    assert m.shape == (2, 13, 13) and int(m.sum()) == 2
+    assert m[0, 0, 5] and m[1, 12, 12]
+
+
+def test_fragment_layout():
+    """frag[tile][kblock][lane][j] = W[16 tile + lane%16][64 kblock + 16 (lane/16) + j],
+    zero past the matrix's K."""
+    g = torch.Generator().manual_seed(3)
+    wm = torch.randn((32, 100), generator=g)
+    f = _frag(wm, 128).float().view(2, 2, 64, 16)
+    for tile in range(2):
+        for kb in range(2):
+            for lane in range(64):
+                for j in range(16):
+                    r, k = 16 * tile + lane % 16, KBLOCK * kb + 16 * (lane // 16) + j
+                    want = float(wm[r, k].half()) if k < 100 else 0.0
+                    assert float(f[tile, kb, lane, j]) == want
+
+
+def test_fragment_residual_split():
+    g = torch.Generator().manual_seed(4)
+    wm = torch.randn((16, 64), generator=g) * 0.3
+    hi = _frag(wm, 64).float()
+    lo = _frag(wm, 64, residual=True).float()
+    flat = wm.view(1, 16, 1, 4, 16).permute(0, 2, 3, 1, 4).reshape(-1)
+    assert torch.equal(lo, (flat - flat.half().float()).half().float())
+    # hi + lo carries ~22 significant bits; residuals below the float16
+    # normal range keep an absolute error of half the subnormal spacing
+    err = (flat - (hi + lo)).abs()
+    assert bool((err <= flat.abs() * 2.0 ** -22 + 2.0 ** -25).all())
+
+
+def test_pack_mlp_folds_each_players_view_into_w0():
+    from oracle.policy import column_permutation
+
+    params = default_init()
+    packed = pack_mlp(params)
+    assert packed["k0"] == 2366 and packed["kblocks0"] == 37
+    w0 = packed["w0"].float().view(2, 8, 37, 64, 16)
+    W0 = params["shared.0.weight"]
+    for pid in range(2):
+        cols = column_permutation(pid, 2, 14, 169)
+        # unpack the fragments back into a (128, 2368) matrix
+        f = w0[pid].view(8, 37, 4, 16, 16).permute(0, 3, 1, 2, 4).reshape(128, 37 * 64)
+        assert torch.equal(f[:, :2366], W0[:, cols].half().float())
+        assert float(f[:, 2366:].abs().max()) == 0.0
+    assert packed["bf"].numel() == 8 and packed["bh"].numel() == 192
+
+
+def test_config_struct_float32_constants():
+    c = config_struct(corridor_training_config(), MapSpec(kind="pillars", brick_p=0.7))
+    f32 = lambda x: float(np.float32(x))  # noqa: E731
+    assert c.step_len == f32(0.3)
+    assert c.pos_hi_y == f32(13 - 0.3) and c.pos_hi_x == f32(13 - 0.3)
+    assert c.chain_time_rest == f32(1.0 - 0.15)
+    assert c.win_per_hp == f32(10.0 / 5)
+    assert c.hit_speed_drop == f32(2 * 0.15)
+    assert c.fuse == 30 and c.blast == 2 and c.max_steps == 1800 and c.corridor == 1
+    assert c.brick_p == f32(0.7) and c.map_kind == 0
+
+
+@pytest.mark.parametrize("kw", [dict(kind="ring"), dict(brick_p=1.5), dict(bombs_cap=(3, 2))])
+def test_map_spec_validation(kw):
+    with pytest.raises(ValueError):
+        MapSpec(**kw)
