@@ -19,7 +19,7 @@ Prints ONE JSON line (rank 0).  `roofline` prices the dominant kernel against
 its bound: the tick kernel against HBM (algorithmic bytes per env-step below),
 the MLP kernel against dense float16 MFMA (algorithmic FLOP per env-step).
 Kernel durations come from HIP events recorded on the launch stream around
-every launch inside the timed region.  `traffic` is read from the committed
+both launches of every 8th step inside the timed region.  `traffic` is read from the committed
 rocprofv3 FETCH_SIZE/WRITE_SIZE summary when one exists.  `cpu_baseline`
 times the oracle (the CPU restatement of the reference path) on the host
 cores over a bounded sample of the same workload.
@@ -53,6 +53,7 @@ MLP_BYTES_PER_ENV = 14 * 169 * 2 + 14 + 4 + 16
 MLP_FLOP_PER_ENV = 2 * 2 * (2366 * 128 + 128 * 128 + 3 * 128 * 64 + 64 * 8)
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_rollout_5632.json")
+EVERY = 8   # kernel durations are sampled on every 8th timed step
 
 
 def parse_args():
@@ -159,20 +160,29 @@ def main():
         roll.step()
     torch.cuda.synchronize()
 
+    # HIP events bracket both launches of every EVERY-th timed step (on the
+    # stream the kernels run on); sampling keeps their cost out of `value`.
     stream = torch.cuda.current_stream(dev)
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * K + 1)]
+    sampled = list(range(0, K, EVERY))
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in sampled]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    ev[0].record(stream)
+    j = 0
     for k in range(K):
+        mark = k % EVERY == 0
+        if mark:
+            ev[j][0].record(stream)
         roll.launch_act()
-        ev[2 * k + 1].record(stream)
+        if mark:
+            ev[j][1].record(stream)
         roll.launch_tick()
-        ev[2 * k + 2].record(stream)
+        if mark:
+            ev[j][2].record(stream)
+            j += 1
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
-    act_ms = sum(ev[2 * k].elapsed_time(ev[2 * k + 1]) for k in range(K)) / K
-    tick_ms = sum(ev[2 * k + 1].elapsed_time(ev[2 * k + 2]) for k in range(K)) / K
+    act_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / len(ev)
+    tick_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / len(ev)
     done_frac = float(roll.done.float().mean())
 
     if args.copy_calibrate:
