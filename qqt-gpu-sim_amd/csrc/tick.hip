@@ -73,19 +73,28 @@ struct Geo {
   static constexpr int KMAX = (C + LPE - 1) / LPE;
 };
 
+template <class G>
+struct DangerScratch {
+  float dd[G::EPW][4][G::C];       // danger stage B: per-direction ray values
+  float fw[G::EPW][G::C];          // danger stage-A front (by cell)
+  float wl[G::EPW][G::C];          // per listed bomb: corrected weight
+  uint16_t edge[G::EPW][G::C][4];  // stage-A in-edge per listed bomb: sender | dist << 8
+};
+
 template <class G, int P>
 struct __align__(16) Lds {
-  float dd[G::EPW][4][G::C];  // danger stage B: per-direction ray values
-  // observation staging: envs back to back in output layout, placed at byte
-  // offset (output address mod 16) so that copy-out can use 16-byte units
-  uint8_t obs_raw[(G::EPW * G::OBS * 2 + 16 + 15) / 16 * 16];
+  // The danger map's scratch is dead before the observation is staged, so
+  // the two share LDS (fewer bytes per env -> more envs resident per CU).
+  union {
+    DangerScratch<G> dz;
+    // observation staging: envs back to back in output layout, placed at byte
+    // offset (output address mod 16) so that copy-out can use 16-byte units
+    uint8_t obs_raw[(G::EPW * G::OBS * 2 + 16 + 15) / 16 * 16];
+  };
   uint32_t cw[G::EPW][G::C];
-  float fw[G::EPW][G::C];    // danger stage-A front (by cell)
   float dng[G::EPW][G::C];   // danger map
-  float wl[G::EPW][G::C];    // per listed bomb: corrected weight
   uint32_t cov[G::EPW][G::CW4];  // byte maps viewed as dwords for clearing
   uint32_t trg[G::EPW][G::CW4];
-  uint16_t edge[G::EPW][G::C][4];  // stage-A in-edge per listed bomb: sender | dist << 8
   uint8_t list[G::EPW][G::C];
   int32_t nlist[G::EPW];
   int32_t pl[G::EPW][P][QQT_P_SLOTS];
@@ -605,9 +614,9 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
   // ---- danger map of the current state (sim/blast.py:158-317)
   {
     float* dng = s.dng[e];
-    float* fw = s.fw[e];
-    float* wl = s.wl[e];
-    float(*dd)[C] = s.dd[e];
+    float* fw = s.dz.fw[e];
+    float* wl = s.dz.wl[e];
+    float(*dd)[C] = s.dz.dd[e];
     const int nb = build_list<G>(list, e, l, [&](int c) { return cw_fuse(cw[c]) > 0; });
 #pragma unroll
     for (int k = 0; k < KMAX; ++k) {
@@ -651,7 +660,7 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
               if (wu & (F_WALL | F_BRICK)) break;
             }
           }
-          s.edge[e][j][d] = ed;
+          s.dz.edge[e][j][d] = ed;
         }
         // stage A: synchronous relay rounds
         const int rounds = min(cf.max_chain, cf.chain_cap_rounds);
@@ -667,7 +676,7 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
             float spread = 0.0f;
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
-              const uint16_t ed = s.edge[e][j][d];
+              const uint16_t ed = s.dz.edge[e][j][d];
               if (ed) spread = fmaxf(spread, fw[ed & 0xFF]);
             }
             const float nv = spread > wl[j] ? spread : 0.0f;
