@@ -65,6 +65,9 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="CPU work budget of the cpu_baseline sample (0 = skip)")
+    ap.add_argument("--workload", choices=("rollout", "stress"), default="rollout",
+                    help="rollout: the headline self-play rollout (default); stress: "
+                         "16384-env bomb-stress ticks with injected actions")
     ap.add_argument("--copy-calibrate", action="store_true",
                     help="after timing, run a 512 MiB device copy (HBM counter calibration)")
     return ap.parse_args()
@@ -84,6 +87,56 @@ def build_workload(n, seed, device):
     return cfg, spec, Rollout(sim, net)
 
 
+STRESS_ENVS = 16384
+
+
+def stress_actions(n, steps, seed, device):
+    """(steps, N, 2, 2) int8 injected actions: move ~ U{0..4} (unmasked), bomb ~
+    Bernoulli(0.5), generated on the device before timing."""
+    import torch
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    mv = torch.randint(0, 5, (steps, n, 2), generator=g, device=device, dtype=torch.int8)
+    bb = (torch.rand((steps, n, 2), generator=g, device=device) < 0.5).to(torch.int8)
+    return torch.stack([mv, bb], dim=-1).contiguous()
+
+
+def cpu_baseline_stress(cfg, spec, n, seed, budget_s):
+    """The oracle's tick on the host cores with the same injected-action rule."""
+    import torch
+
+    from oracle.sim import OracleSim
+
+    cores = _cores(torch)
+    sim = OracleSim(cfg, n, spec, seed=seed)
+    g = torch.Generator().manual_seed(seed)
+
+    def tick():
+        mv = torch.randint(0, 5, (n, 2), generator=g)
+        bb = (torch.rand((n, 2), generator=g) < 0.5).long()
+        sim.step(torch.stack([mv, bb], -1), auto_reset=True)
+
+    tick()
+    ticks, t0 = 0, time.perf_counter()
+    while True:
+        tick()
+        ticks += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or ticks >= 256:
+            break
+    return {"value": n * ticks / el, "unit": "env-steps/s", "cores": cores, "kind": "port",
+            "sample": f"oracle (torch CPU restatement) tick with injected actions, {n} envs x "
+                      f"{ticks} timed ticks after 1 warm-up tick, {el:.1f} s"}
+
+
+def _cores(torch):
+    cores = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        cores = min(cores, int(os.environ["OMP_NUM_THREADS"]))
+    torch.set_num_threads(max(1, cores))
+    return torch.get_num_threads()
+
+
 def cpu_baseline(cfg, spec, n, seed, budget_s):
     """The oracle's env-step on the host cores: observe, legal_mask, both
     players' forward + masked sampling, step with auto-reset."""
@@ -95,10 +148,7 @@ def cpu_baseline(cfg, spec, n, seed, budget_s):
     from oracle.sim import OracleSim
     from qqtsim.policy import default_init
 
-    cores = len(os.sched_getaffinity(0))
-    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
-        cores = min(cores, int(os.environ["OMP_NUM_THREADS"]))
-    torch.set_num_threads(max(1, cores))
+    cores = _cores(torch)
     params = default_init(cfg.obs_shape)
     sim = OracleSim(cfg, n, spec, seed=seed)
     envs = np.arange(n)
@@ -125,7 +175,7 @@ def cpu_baseline(cfg, spec, n, seed, budget_s):
         el = time.perf_counter() - t0
         if el >= budget_s or ticks >= 256:
             break
-    return {"value": n * ticks / el, "unit": "env-steps/s", "cores": torch.get_num_threads(),
+    return {"value": n * ticks / el, "unit": "env-steps/s", "cores": cores,
             "kind": "port",
             "sample": f"oracle (torch CPU restatement) on the same workload, {n} envs x "
                       f"{ticks} timed ticks after 2 warm-up ticks, {el:.1f} s"}
@@ -154,6 +204,8 @@ def main():
         sys.exit("bench.py needs a ROCm GPU")
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.workload == "stress":
+        return main_stress(args, torch, dev)
     n, K, W = args.envs, args.steps, args.warmup
     cfg, spec, roll = build_workload(n, args.seed, dev)
     for _ in range(W):
@@ -186,11 +238,7 @@ def main():
     done_frac = float(roll.done.float().mean())
 
     if args.copy_calibrate:
-        src = torch.empty(256 << 20, dtype=torch.int16, device=dev).fill_(1)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
+        _calibration_copy(torch, dev)
 
     kernels = {
         "tick_kernel": {"us": tick_ms * 1e3, "bound": "hbm",
@@ -239,6 +287,70 @@ def main():
         "kernels": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                         for kk, vv in v.items()} for k, v in kernels.items()},
         "done_fraction_last_tick": done_frac,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def _calibration_copy(torch, dev):
+    src = torch.empty(256 << 20, dtype=torch.int16, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def main_stress(args, torch, dev):
+    """Bomb-stress ticks: 16384 envs, corridor map with 40% bricks, per-player
+    bombs 1-4 and blast 2-5, injected unmasked actions (bomb w.p. 0.5)."""
+    from qqtsim.config import corridor_training_config
+    from qqtsim.maps import BOMB_STRESS_40
+    from qqtsim.rollout import TickLoop
+    from qqtsim.sim import HipBatchedSim
+
+    n = STRESS_ENVS if args.envs == 5632 else args.envs
+    K, W = args.steps, args.warmup
+    cfg = corridor_training_config()
+    sim = HipBatchedSim(cfg, n, device=dev, seed=args.seed, map_spec=BOMB_STRESS_40)
+    acts = stress_actions(n, K + W, args.seed, dev)
+    loop = TickLoop(sim)
+    for k in range(W):
+        loop.launch_tick(acts[k])
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(0, K, EVERY)]
+    t0 = time.perf_counter()
+    j = 0
+    for k in range(K):
+        mark = k % EVERY == 0
+        if mark:
+            ev[j][0].record(stream)
+        loop.launch_tick(acts[W + k])
+        if mark:
+            ev[j][1].record(stream)
+            j += 1
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    tick_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / len(ev)
+    if args.copy_calibrate:
+        _calibration_copy(torch, dev)
+    achieved = TICK_BYTES_PER_ENV * n / (tick_ms * 1e-3) / 1e9
+    cpu = cpu_baseline_stress(cfg, BOMB_STRESS_40, n, args.seed, args.cpu_seconds) \
+        if args.cpu_seconds > 0 else None
+    out = {
+        "metric": "env-steps/s at 16384 envs, bomb-stress tick (injected actions), 1 MI355X",
+        "value": n * K / el, "unit": "env-steps/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": el / K * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32 sim",
+        "data": "synthetic: template maps from Philox draws, actions from a seeded device generator",
+        "config": {"workload": "bomb-stress ticks, 16384 envs, 13x13 pillars + 40% bricks, "
+                               "bombs 1-4, blast 2-5, injected actions (bomb w.p. 0.5), auto-reset",
+                   "envs": n, "parallelism": "single GPU"},
+        "roofline": {"kernel": "tick_kernel", "bound": "hbm", "achieved": round(achieved, 3),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None},
+        "cpu_baseline": cpu,
+        "kernels": {"tick_kernel": {"us": round(tick_ms * 1e3, 4),
+                                    "bytes_per_env": TICK_BYTES_PER_ENV}},
     }
     print(json.dumps(out), flush=True)
 

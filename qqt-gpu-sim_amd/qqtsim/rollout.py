@@ -113,3 +113,45 @@ class Rollout:
         for _ in range(int(ticks)):
             self.launch_act()
             self.launch_tick()
+
+
+class TickLoop:
+    """Ticks driven by injected actions (the bomb-stress workload): one
+    `qqt_tick` launch per step with a prebuilt argument block; `actions` is
+    any (N, P, 2) int8 device tensor (a slice of a pre-generated batch)."""
+
+    def __init__(self, sim: HipBatchedSim):
+        self.sim = sim
+        self._stream = _capi.stream_handle(sim.device)
+        self._lib = _capi.lib()
+        t = _capi.TickArgsC()
+        t.n_envs, t.mode, t.auto_reset = sim.num_envs, _capi.MODE_STEP, 1
+        t.seed = sim.seed & 0xFFFFFFFFFFFFFFFF
+        t.cells, t.players, t.envs = (sim._cells.data_ptr(), sim._players.data_ptr(),
+                                      sim._envs.data_ptr())
+        for k, buf in (("reward", sim._reward), ("done", sim._done), ("n_alive", sim._n_alive),
+                       ("died", sim._died), ("winner", sim._winner), ("covered", sim._cov),
+                       ("triggered", sim._trg), ("obs", sim._obs), ("move_mask", sim._mm),
+                       ("bomb_mask", sim._bm)):
+            setattr(t, k, buf.data_ptr())
+        self._tick = t
+
+    def launch_tick(self, actions: torch.Tensor) -> None:
+        sim = self.sim
+        if actions.dtype != torch.int8 or not actions.is_contiguous() or \
+                tuple(actions.shape) != (sim.num_envs, sim.cfg.n_players, 2):
+            raise ValueError("actions must be a contiguous (N, P, 2) int8 tensor")
+        if sim.resolve_tiers is None:
+            sim.resolve_tiers = sim._first_tick_tiers(actions) \
+                if sim.exact_reference_resolve else 255
+        t = self._tick
+        t.actions_i8 = actions.data_ptr()
+        t.resolve_tiers = sim.resolve_tiers
+        t.explore_coef = float(sim.explore_coef)
+        t.danger_coef = float(sim.explore_coef * sim.cfg.danger_penalty)
+        t.tick = sim.tick & 0xFFFFFFFF
+        t.epoch = sim.epoch & 0xFFFFFFFF
+        _capi.check(self._lib.qqt_tick(sim._cfg_c, t, self._stream))
+        sim.tick += 1
+        sim.epoch += 1
+        sim._fresh = True

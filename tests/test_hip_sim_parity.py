@@ -151,3 +151,38 @@ def test_hip_matches_oracle_with_auto_reset(dev, spec_name, n, ticks):
                        INT_KEYS + FLOAT_KEYS + ("lo_bombs", "lo_blast", "lo_spd", "crate_prob"))
     assert resets > 0, "the run must exercise auto-reset"
     print(f"{spec_name}: {ticks} ticks x {n} envs bit-exact, {resets} resets")
+
+
+def test_hip_bomb_stress_injected_actions_match_oracle(dev):
+    """The bomb-stress workload: unmasked injected actions (bomb w.p. 0.5,
+    moves into walls included) through the lean TickLoop launch path, full
+    training-corridor rules, auto-reset: bit-exact state, exact done, reward
+    within tolerance, tick after tick."""
+    from oracle.sim import OracleSim
+    from qqtsim.config import corridor_training_config
+    from qqtsim.maps import BOMB_STRESS_40
+    from qqtsim.rollout import TickLoop
+    from qqtsim.sim import HipBatchedSim
+
+    cfg = corridor_training_config(max_hp=2, invuln_ticks=3, max_steps=50)
+    n, ticks, seed = 256, 64, 5
+    hip = HipBatchedSim(cfg, n, device=dev, seed=seed, map_spec=BOMB_STRESS_40)
+    ora = OracleSim(cfg, n, BOMB_STRESS_40, seed=seed)
+    loop = TickLoop(hip)
+    g = torch.Generator().manual_seed(seed)
+    keys = INT_KEYS + FLOAT_KEYS + ("lo_bombs", "lo_blast", "lo_spd", "crate_prob")
+    resets = 0
+    for t in range(ticks):
+        mv = torch.randint(0, 5, (n, 2), generator=g)
+        bb = (torch.rand((n, 2), generator=g) < 0.5).long()
+        act = torch.stack([mv, bb], -1)
+        r1, d1, _ = ora.step(act, auto_reset=True)
+        loop.launch_tick(act.to(torch.int8).to(dev).contiguous())
+        resets += int(d1.sum())
+        np.testing.assert_array_equal(loop.sim._done.cpu().numpy().astype(bool), d1.numpy(),
+                                      err_msg=f"done {t}")
+        assert float((loop.sim._reward.cpu() - r1).abs().max()) <= REWARD_ATOL, f"reward {t}"
+        _compare_state(hip.state_dict(), ora.state_dict(), t, keys)
+    np.testing.assert_array_equal(hip.observe().cpu().numpy().view(np.uint16),
+                                  ora.observe().numpy().view(np.uint16))
+    assert resets > 0
