@@ -24,6 +24,13 @@ permutation):
   observation of envs 0..3.
 * deep_chain.npz - single-tick states with chains longer than 8 rounds.
 * mlp.npz - MLP ActorCritic weights, inputs and forward/evaluate outputs.
+* astar_<name>.npz - the reference astar bot (sim/bots.py astar_attack, no
+  behaviour modes, no crate eating) as player 1 against random legal moves
+  for player 0: per tick the bot's inputs (state, observation, masks, the
+  noise uniforms its torch.rand(n, 5) draws, seeded per tick), its output,
+  and on every 4th tick its two cost fields (V_safe, V_opp).
+
+Run a subset by name: `python tests/golden/gen_reference_vectors.py astar`.
 """
 
 from __future__ import annotations
@@ -261,7 +268,109 @@ def mlp(traj_name="pillars70"):
     print("mlp: batch", b, "params", int(out["param_count"]))
 
 
-if __name__ == "__main__":
+def astar(name, spec, n=64, ticks=64, seed=11):
+    import sim.bots as ref_bots
+
+    s = ref_sim(n, spec, seed)
+    p = s.cfg.n_players
+    keys = ("wall", "brick", "fuse", "owner", "pos", "alive", "blast_cap")
+    rec = {k: [] for k in keys + ("obs", "mm1", "bm1", "u", "reach", "bot", "field_tick",
+                                  "v_safe", "v_opp")}
+    for tick in range(ticks):
+        snap = snapshot(s)
+        obs = s.observe()
+        mm, bm = s.legal_mask()
+        seed_t = seed * 100003 + tick
+        torch.manual_seed(seed_t)
+        u = torch.rand(n, 5)
+        torch.manual_seed(seed_t)
+        bot = ref_bots.astar_attack(s, obs, mm[:, 1], bm[:, 1], 1)
+        for k in keys:
+            rec[k].append(snap[k])
+        rec["obs"].append(obs.numpy().copy())
+        rec["mm1"].append(mm[:, 1].numpy().copy())
+        rec["bm1"].append(bm[:, 1].numpy().copy())
+        rec["u"].append(u.numpy().copy())
+        rec["reach"].append(np.int64(s.blast_cap[:, 1].max()))
+        rec["bot"].append(bot.numpy().copy())
+        if tick % 4 == 0:
+            danger = obs.float()[:, 2 * p + 1]
+            block_all = s.wall | s.brick | (s.fuse > 0)
+            rec["v_safe"].append(ref_bots._dijkstra_field(
+                s, danger < 0.35, danger, blocked=block_all).numpy().copy())
+            r0 = s.pos[:, 0, 0].floor().long().clamp(0, s.cfg.height - 1)
+            c0 = s.pos[:, 0, 1].floor().long().clamp(0, s.cfg.width - 1)
+            src = torch.zeros(n, s.cfg.height * s.cfg.width, dtype=torch.bool)
+            src[torch.arange(n), r0 * s.cfg.width + c0] = s.alive[:, 0]
+            rec["v_opp"].append(ref_bots._dijkstra_field(
+                s, src.view(n, s.cfg.height, s.cfg.width), danger,
+                blocked=block_all).numpy().copy())
+            rec["field_tick"].append(np.int64(tick))
+        a = actions_for("legal", mm.numpy(), bm.numpy(), n, seed, tick)
+        a[:, 1] = bot.numpy()
+        cu = philox.uniforms(seed, np.arange(n), tick, philox.STREAM_CRATE, 2 * p)
+        cu = cu.reshape(n, p, 2).transpose(1, 2, 0).copy()
+        s._rand_buf = torch.from_numpy(np.concatenate(
+            [cu[:, 0, :].T.reshape(-1), cu[:, 1, :].T.reshape(-1)]))
+        s.step(torch.from_numpy(a), auto_reset=False)
+    out = {k: np.stack(v) for k, v in rec.items()}
+    np.savez_compressed(os.path.join(HERE, f"astar_{name}.npz"), **out)
+    bots = out["bot"]
+    print(f"astar_{name}: ticks={ticks} moves={np.bincount(bots[..., 0].ravel(), minlength=5)} "
+          f"places={int(bots[..., 1].sum())} reach={sorted(set(out['reach'].tolist()))} "
+          f"alive1={int(out['alive'][-1][:, 1].sum())}")
+
+
+def astar_chain(seed=19):
+    """Hand-built states where the bot's chain check matters: the bot stands
+    in the open with a short-fuse bomb k cells away in a straight line; env 0's
+    bot has blast cap 5 (the batch max), the others cap 2, so bombs 3..5 cells
+    out are in reach only through the batch-max loop bound."""
+    import sim.bots as ref_bots
+
+    n = 16
+    s = ref_sim(n, MapSpec(kind="open"), seed)
+    s.pos[:, 1, 0] = 6.5
+    s.pos[:, 1, 1] = 6.5
+    s.pos[:, 0, 0] = 1.5            # opponent far away, not aligned
+    s.pos[:, 0, 1] = 11.5
+    s.blast_cap[:, 1] = 2
+    s.blast_cap[0, 1] = 5
+    for e in range(n):
+        k = 1 + e % 5                # bomb distance 1..5
+        d = (e // 5) % 4            # direction
+        dr, dc = ((-1, 0), (1, 0), (0, -1), (0, 1))[d]
+        s.fuse[e, 6 + dr * k, 6 + dc * k] = 3 + (e % 9)      # fuse 3..11
+        s.owner[e, 6 + dr * k, 6 + dc * k] = 0
+        s.bomb_blast[e, 6 + dr * k, 6 + dc * k] = 2
+    obs = s.observe()
+    mm, bm = s.legal_mask()
+    torch.manual_seed(seed)
+    u = torch.rand(n, 5)
+    torch.manual_seed(seed)
+    bot = ref_bots.astar_attack(s, obs, mm[:, 1], bm[:, 1], 1)
+    snap = snapshot(s)
+    out = {k: snap[k][None] for k in ("wall", "brick", "fuse", "owner", "pos", "alive",
+                                       "blast_cap")}
+    out.update(obs=obs.numpy()[None], mm1=mm[:, 1].numpy()[None], bm1=bm[:, 1].numpy()[None],
+               u=u.numpy()[None], reach=np.array([int(s.blast_cap[:, 1].max())]),
+               bot=bot.numpy()[None])
+    np.savez_compressed(os.path.join(HERE, "astar_chain.npz"), **out)
+    print("astar_chain: places", bot[:, 1].tolist())
+
+
+if __name__ == "__main__" and len(sys.argv) > 1:
+    for what in sys.argv[1:]:
+        if what == "astar":
+            astar("p70", MapSpec(kind="pillars", brick_p=0.7))
+            astar("p30", MapSpec(kind="pillars", brick_p=0.3, bombs_cap=(2, 4), blast_cap=(2, 5)),
+                  seed=13)
+            astar("open", MapSpec(kind="open", bombs_cap=(2, 3), blast_cap=(2, 4)), ticks=96,
+                  seed=17)
+            astar_chain()
+        else:
+            raise SystemExit(f"unknown fixture group {what!r}")
+elif __name__ == "__main__":
     rollout("pillars0", MapSpec(kind="pillars", brick_p=0.0), "legal", ticks=128, seed=0)
     rollout("pillars70", MapSpec(kind="pillars", brick_p=0.7), "legal", ticks=128, seed=3)
     rollout("stress40", MapSpec(kind="pillars", brick_p=0.4, bombs_cap=(1, 4),
@@ -271,3 +380,8 @@ if __name__ == "__main__":
             cfg_kw=dict(max_hp=2, invuln_ticks=4, max_steps=70))
     deep_chain()
     mlp()
+    astar("p70", MapSpec(kind="pillars", brick_p=0.7))
+    astar("p30", MapSpec(kind="pillars", brick_p=0.3, bombs_cap=(2, 4), blast_cap=(2, 5)),
+          seed=13)
+    astar("open", MapSpec(kind="open", bombs_cap=(2, 3), blast_cap=(2, 4)), ticks=96, seed=17)
+    astar_chain()
