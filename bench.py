@@ -65,9 +65,10 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="CPU work budget of the cpu_baseline sample (0 = skip)")
-    ap.add_argument("--workload", choices=("rollout", "stress"), default="rollout",
+    ap.add_argument("--workload", choices=("rollout", "stress", "astar"), default="rollout",
                     help="rollout: the headline self-play rollout (default); stress: "
-                         "16384-env bomb-stress ticks with injected actions")
+                         "16384-env bomb-stress ticks with injected actions; astar: "
+                         "learner (MLP) vs the astar bot, 5632 envs")
     ap.add_argument("--copy-calibrate", action="store_true",
                     help="after timing, run a 512 MiB device copy (HBM counter calibration)")
     return ap.parse_args()
@@ -206,6 +207,8 @@ def main():
     torch.cuda.set_device(dev)
     if args.workload == "stress":
         return main_stress(args, torch, dev)
+    if args.workload == "astar":
+        return main_astar(args, torch, dev)
     n, K, W = args.envs, args.steps, args.warmup
     cfg, spec, roll = build_workload(n, args.seed, dev)
     for _ in range(W):
@@ -351,6 +354,131 @@ def main_stress(args, torch, dev):
         "cpu_baseline": cpu,
         "kernels": {"tick_kernel": {"us": round(tick_ms * 1e3, 4),
                                     "bytes_per_env": TICK_BYTES_PER_ENV}},
+    }
+    print(json.dumps(out), flush=True)
+
+
+# Algorithmic bytes of one env-step of the bot kernel: cell words (169 x 4 B),
+# the danger channel of the observation (169 x 2 B), the player records
+# (2 x 64 B), the bot's masks (7 B) and its action (2 B).
+BOT_BYTES_PER_ENV = 169 * 4 + 169 * 2 + 2 * 64 + 7 + 2
+
+
+def cpu_baseline_astar(cfg, spec, n, seed, budget_s):
+    """The oracle's learner-vs-bot env-step on the host cores."""
+    import numpy as np
+    import torch
+
+    from oracle import philox
+    from oracle.bots import astar_act
+    from oracle.policy import mlp_forward, sample_masked
+    from oracle.sim import OracleSim
+    from qqtsim.policy import default_init
+
+    cores = _cores(torch)
+    params = default_init(cfg.obs_shape)
+    sim = OracleSim(cfg, n, spec, seed=seed)
+    envs = np.arange(n)
+
+    def env_step(t):
+        obs = sim.observe()
+        mm, bm = sim.legal_mask()
+        u = philox.uniforms(seed, envs, t, philox.STREAM_POLICY, 2)
+        ub = torch.from_numpy(philox.uniforms(seed, envs, t, philox.STREAM_BOT, 5))
+        acts = torch.zeros((n, 2, 2), dtype=torch.int64)
+        ml, bl, _ = mlp_forward(params, obs, 0)
+        acts[:, 0, 0] = torch.from_numpy(sample_masked(ml.numpy(), mm[:, 0].numpy(), u[:, 0])[0])
+        acts[:, 0, 1] = torch.from_numpy(sample_masked(bl.numpy(), bm[:, 0].numpy(), u[:, 1])[0])
+        acts[:, 1] = astar_act(cfg, sim.state_dict(), obs, mm[:, 1], bm[:, 1], 1, ub)
+        sim.step(acts, auto_reset=True)
+
+    env_step(0)
+    ticks, t0 = 0, time.perf_counter()
+    while True:
+        env_step(1 + ticks)
+        ticks += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or ticks >= 128:
+            break
+    return {"value": n * ticks / el, "unit": "env-steps/s", "cores": cores, "kind": "port",
+            "sample": f"oracle (torch CPU restatement) learner-vs-astar env-step, {n} envs x "
+                      f"{ticks} timed ticks after 1 warm-up tick, {el:.1f} s"}
+
+
+def main_astar(args, torch, dev):
+    """Learner vs astar bot: 5632 envs, 13x13 pillars + 70% bricks; player 0
+    = the MLP (masked sampling), player 1 = the astar bot (two cost fields per
+    env per tick); tick with auto-reset."""
+    from qqtsim.bots import HipAstarBot
+    from qqtsim.config import corridor_training_config
+    from qqtsim.maps import MapSpec
+    from qqtsim.policy import HipActorCritic, default_init
+    from qqtsim.rollout import Rollout
+    from qqtsim.sim import HipBatchedSim
+
+    n, K, W = args.envs, args.steps, args.warmup
+    cfg = corridor_training_config()
+    spec = MapSpec(kind="pillars", brick_p=0.7, swap_spawns=True)
+    sim = HipBatchedSim(cfg, n, device=dev, seed=args.seed, map_spec=spec)
+    net = HipActorCritic(default_init(cfg.obs_shape), device=dev, seed=args.seed)
+    bot = HipAstarBot(sim, pid=1)
+    roll = Rollout(sim, net, opponent=bot)
+    for _ in range(W):
+        roll.step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(0, K, EVERY)]
+    t0 = time.perf_counter()
+    j = 0
+    for k in range(K):
+        mark = k % EVERY == 0
+        if not mark:
+            roll.step()
+            continue
+        e = ev[j]
+        j += 1
+        e[0].record(stream)
+        roll.launch_policy()
+        e[1].record(stream)
+        roll.launch_opponent()
+        e[2].record(stream)
+        roll.launch_tick()
+        e[3].record(stream)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    us = [sum(e[i].elapsed_time(e[i + 1]) for e in ev) / len(ev) * 1e3 for i in range(3)]
+    kernels = {
+        "mlp_act_kernel": {"us": us[0], "bound": "mfma",
+                           "achieved": MLP_FLOP_PER_ENV / 2 * n / (us[0] * 1e-6) / 1e12,
+                           "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s"},
+        "bot_kernel": {"us": us[1], "bound": "hbm",
+                       "achieved": BOT_BYTES_PER_ENV * n / (us[1] * 1e-6) / 1e9,
+                       "peak": HBM_PEAK_GBS, "unit": "GB/s", "bytes_per_env": BOT_BYTES_PER_ENV},
+        "tick_kernel": {"us": us[2], "bound": "hbm",
+                        "achieved": TICK_BYTES_PER_ENV * n / (us[2] * 1e-6) / 1e9,
+                        "peak": HBM_PEAK_GBS, "unit": "GB/s", "bytes_per_env": TICK_BYTES_PER_ENV},
+    }
+    for v in kernels.values():
+        v["frac"] = v["achieved"] / v["peak"]
+    dom = max(kernels, key=lambda k: kernels[k]["us"])
+    d = kernels[dom]
+    cpu = cpu_baseline_astar(cfg, spec, n, args.seed, args.cpu_seconds) \
+        if args.cpu_seconds > 0 else None
+    out = {
+        "metric": "env-steps/s at 5632 envs, learner MLP vs astar bot (step+obs+act+bot), 1 MI355X",
+        "value": n * K / el, "unit": "env-steps/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": el / K * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32 sim and bot / f16 MFMA (f32 accumulate)",
+        "data": "synthetic: template maps from Philox draws, PyTorch default-init MLP weights",
+        "config": {"workload": "learner MLP (player 0) vs astar bot (player 1), 5632 envs, "
+                               "13x13 pillars + 70% bricks, auto-reset",
+                   "envs": n, "parallelism": "single GPU"},
+        "roofline": {"kernel": dom, "bound": d["bound"], "achieved": round(d["achieved"], 3),
+                     "peak": d["peak"], "unit": d["unit"], "frac": round(d["frac"], 5),
+                     "traffic": None},
+        "cpu_baseline": cpu,
+        "kernels": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
+                        for kk, vv in v.items()} for k, v in kernels.items()},
     }
     print(json.dumps(out), flush=True)
 

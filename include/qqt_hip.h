@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 1
+#define QQT_ABI_VERSION 2
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -127,13 +127,37 @@ typedef struct qqt_mlp_args {
   const float *b0, *ln1_w, *ln1_b, *b1, *ln2_w, *ln2_b, *bh, *bf;
   const uint8_t* move_mask;
   const uint8_t* bomb_mask;
-  const float* uniforms;     /* [B][npid][2] (move, bomb) or NULL = Philox */
-  int64_t* actions;          /* [B][npid][2] or NULL */
-  int8_t* actions_i8;        /* [B][npid][2] or NULL */
-  float* logp_out;           /* [B][npid] or NULL */
-  float* value_out;          /* [B][npid] or NULL */
-  float* logits_out;         /* [B][npid][8]: 5 move, 2 bomb, value; or NULL */
+  const float* uniforms;     /* [B][out_slots][2] (move, bomb) or NULL = Philox */
+  int64_t* actions;          /* [B][out_slots][2] or NULL */
+  int8_t* actions_i8;        /* [B][out_slots][2] or NULL */
+  float* logp_out;           /* [B][out_slots] or NULL */
+  float* value_out;          /* [B][out_slots] or NULL */
+  float* logits_out;         /* [B][out_slots][8]: 5 move, 2 bomb, value; or NULL */
+  int32_t out_slots;         /* player slots per output row (0 = npid) */
+  int32_t out_slot;          /* slot written when npid == 1 */
 } qqt_mlp_args;
+
+/* astar rule bot for one player (sim/bots.py:267-508, astar_attack with no
+ * behaviour modes and no crate eating).  Reads the sim state, the tick's
+ * float16 observation (danger channel 2P+1) and the player's legality masks;
+ * writes slot `pid` of the (N, P, 2) action buffer. */
+typedef struct qqt_bot_args {
+  int32_t n_envs;
+  int32_t pid;                /* the bot's player id */
+  uint64_t seed;              /* Philox key of the noise uniforms */
+  uint32_t tick;              /* counter word of the noise uniforms */
+  int32_t reserved;
+  const int32_t* cells;       /* sim state, layout above */
+  const int32_t* players;
+  const uint16_t* obs;        /* [N][5P+4][H][W] float16 bits */
+  const uint8_t* move_mask;   /* [N][P][5] */
+  const uint8_t* bomb_mask;   /* [N][P][2] */
+  const float* uniforms;      /* [N][5] noise uniforms, or NULL = Philox stream 7 */
+  const int32_t* reach;       /* device scalar: chain-check reach (the reference uses
+                                 the batch max of the bot's blast cap); NULL = own cap */
+  int64_t* actions;           /* [N][P][2], slot pid written; or NULL */
+  int8_t* actions_i8;         /* same as int8; or NULL */
+} qqt_bot_args;
 
 /* ABI version (QQT_ABI_VERSION). */
 int qqt_abi_version(void);
@@ -152,6 +176,12 @@ int qqt_tick(const qqt_sim_config* cfg, const qqt_tick_args* args, void* stream)
  * shared, so both players' first layers are one GEMM), ActorCritic.forward
  * (:167-196) when sample = 0. */
 int qqt_mlp_act(const qqt_mlp_args* args, void* stream);
+
+/* One launch of the astar bot for player args->pid.  Replaces
+ * astar_attack(sim, obs, mmask, bmask, pid) (sim/bots.py:267-508) with its
+ * two _dijkstra_field cost fields (:179-238); the 0.05 * torch.rand(n, 5)
+ * noise (:355) comes from `uniforms` or the Philox stream. */
+int qqt_bot_act(const qqt_sim_config* cfg, const qqt_bot_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,312 @@
+// The astar rule bot for gfx950 (sim/bots.py:179-238, :267-508): two
+// danger-weighted multi-source shortest-cost fields and steepest descent on
+// them, for one player of a batch of envs, in one launch.
+//
+// Mapping: one 64-lane wavefront (= one workgroup) per env.  The env's
+// obstacles, danger and threat maps and both cost fields live in LDS (~3 KB);
+// lane l owns cells l, l + 64, l + 128.
+//
+// Cost fields: dist = min(dist, min_4nbr(dist) + cost), cost = 1 + 2 danger
+// (inf on blocked cells), sources at 0 even when blocked, relaxed in place
+// until a full pass changes nothing (wavefront ballot).  float32 addition is
+// monotone, so the in-place order reaches the same fixed point as the
+// reference's synchronous passes, bit for bit.
+//
+// Decision: lane 0 scores the five candidate cells (4 moves + idle) exactly as
+// the reference does (approach on V_opp, escape on V_safe, danger and threat
+// penalties, 0.05-scaled noise, fallback to the least dangerous legal move);
+// the chain check (a short-fuse bomb within `reach` cells in line) runs one
+// (distance, direction) pair per lane.  The library is built with
+// -ffp-contract=off, so every product and sum rounds separately like the
+// reference's float32 tensor ops.
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "qqt_common.h"
+#include "qqt_hip.h"
+
+namespace qqt {
+
+namespace bot {
+
+constexpr uint32_t F_WALL = 1u << 24, F_BRICK = 1u << 25;
+__device__ __forceinline__ int fuse_of(uint32_t w) { return (int)(w & 0xFFu); }
+__device__ __forceinline__ int owner_of(uint32_t w) { return (int)(int8_t)((w >> 8) & 0xFFu); }
+
+template <int H, int W>
+struct BotLds {
+  static constexpr int C = H * W;
+  float dng[C];       // danger (the observation's float16 channel, widened)
+  float cost[C];      // 1 + 2 danger, inf where blocked
+  float vs[C];        // V_safe
+  float vo[C];        // V_opp
+  uint32_t cw[C];     // packed cell words
+  uint8_t thr[2][C];  // threat map, double buffer for the dilation
+};
+
+}  // namespace bot
+
+template <int H, int W, int P>
+__global__ __launch_bounds__(64) void bot_kernel(const qqt_sim_config cf, const qqt_bot_args a) {
+  constexpr int C = H * W;
+  constexpr int KMAX = (C + 63) / 64;
+  __shared__ bot::BotLds<H, W> s;
+  const int lane = threadIdx.x;
+  const int g = blockIdx.x;                  // grid = n_envs
+  const int pid = a.pid;
+  const float INF = __builtin_inff();
+  const uint16_t* obs = a.obs + (size_t)g * (5 * P + 4) * C + (size_t)(2 * P + 1) * C;
+  const int32_t* pl = a.players + (size_t)g * P * QQT_P_SLOTS;
+
+  // ---- load: cells, danger, cost, sources, threat
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) {
+    const int c = lane + 64 * k;
+    if (c < C) {
+      const uint32_t w = (uint32_t)a.cells[(size_t)g * C + c];
+      s.cw[c] = w;
+      const float d = __half2float(__ushort_as_half(obs[c]));
+      s.dng[c] = d;
+      const bool blocked = (w & (bot::F_WALL | bot::F_BRICK)) || bot::fuse_of(w) > 0;
+      s.cost[c] = blocked ? INF : 1.0f + 2.0f * d;
+      s.vs[c] = d < 0.35f ? 0.0f : INF;
+      s.vo[c] = INF;
+      s.thr[0][c] = (bot::owner_of(w) == pid && bot::fuse_of(w) > 0) ? 1 : 0;
+    }
+  }
+  // opponents' cells: a later opponent overwrites an earlier one's flag
+  // (the reference assigns alive[o] per opponent in id order)
+  if (lane == 0) {
+    for (int o = 0; o < P; ++o) {
+      if (o == pid) continue;
+      const float oy = __int_as_float(pl[o * QQT_P_SLOTS + QQT_P_Y]);
+      const float ox = __int_as_float(pl[o * QQT_P_SLOTS + QQT_P_X]);
+      const int ro = min(max((int)floorf(oy), 0), H - 1);
+      const int co = min(max((int)floorf(ox), 0), W - 1);
+      s.vo[ro * W + co] = pl[o * QQT_P_SLOTS + QQT_P_ALIVE] ? 0.0f : INF;
+    }
+  }
+  __syncthreads();
+
+  // ---- threat: the bot's live bombs dilated growth_blast_max times (4-neighbourhood)
+  int cur = 0;
+  for (int it = 0; it < cf.growth_blast_max; ++it) {
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      const int c = lane + 64 * k;
+      if (c < C) {
+        const int r = c / W, col = c % W;
+        uint8_t v = s.thr[cur][c];
+        if (r > 0) v |= s.thr[cur][c - W];
+        if (r < H - 1) v |= s.thr[cur][c + W];
+        if (col > 0) v |= s.thr[cur][c - 1];
+        if (col < W - 1) v |= s.thr[cur][c + 1];
+        s.thr[cur ^ 1][c] = v;
+      }
+    }
+    cur ^= 1;
+    __syncthreads();
+  }
+
+  // ---- both cost fields, relaxed in place to their fixed point
+  for (int pass = 0; pass < 4 * C; ++pass) {
+    bool changed = false;
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      const int c = lane + 64 * k;
+      if (c < C) {
+        const float cc = s.cost[c];
+        if (cc != INF) {
+          const int r = c / W, col = c % W;
+          float ns = INF, no = INF;
+          if (r > 0) { ns = fminf(ns, s.vs[c - W]); no = fminf(no, s.vo[c - W]); }
+          if (r < H - 1) { ns = fminf(ns, s.vs[c + W]); no = fminf(no, s.vo[c + W]); }
+          if (col > 0) { ns = fminf(ns, s.vs[c - 1]); no = fminf(no, s.vo[c - 1]); }
+          if (col < W - 1) { ns = fminf(ns, s.vs[c + 1]); no = fminf(no, s.vo[c + 1]); }
+          const float cs = ns + cc, co = no + cc;
+          if (cs < s.vs[c]) { s.vs[c] = cs; changed = true; }
+          if (co < s.vo[c]) { s.vo[c] = co; changed = true; }
+        }
+      }
+    }
+    if (__ballot(changed) == 0ull) break;
+    __syncthreads();
+  }
+  __syncthreads();
+
+  // ---- decision
+  const float by = __int_as_float(pl[pid * QQT_P_SLOTS + QQT_P_Y]);
+  const float bx = __int_as_float(pl[pid * QQT_P_SLOTS + QQT_P_X]);
+  const int r = min(max((int)floorf(by), 0), H - 1);
+  const int c = min(max((int)floorf(bx), 0), W - 1);
+  const bool alive = pl[pid * QQT_P_SLOTS + QQT_P_ALIVE] != 0;
+  const int cap = pl[pid * QQT_P_SLOTS + QQT_P_BLAST_CAP];
+  const int reach = a.reach ? *a.reach : cap;
+
+  // chain: a bomb with fuse 1..10 within `reach` cells in line (lane = step, direction)
+  bool chain_l = false;
+  for (int i = lane; i < 4 * reach; i += 64) {
+    const int k = i / 4 + 1, d = i % 4;
+    const int rr = r + (d == 0 ? -k : d == 1 ? k : 0);
+    const int cc2 = c + (d == 2 ? -k : d == 3 ? k : 0);
+    if (rr >= 0 && rr < H && cc2 >= 0 && cc2 < W) {
+      const int f = bot::fuse_of(s.cw[rr * W + cc2]);
+      chain_l |= f > 0 && f <= 10;
+    }
+  }
+  const bool chain = __ballot(chain_l) != 0ull;
+
+  if (lane == 0) {
+    float u[5];
+    if (a.uniforms) {
+#pragma unroll
+      for (int k = 0; k < 5; ++k) u[k] = a.uniforms[(size_t)g * 5 + k];
+    } else {
+      float u8[8];
+      philox_block(a.seed, (uint32_t)g, a.tick, STREAM_BOT, 0, u8);
+      philox_block(a.seed, (uint32_t)g, a.tick, STREAM_BOT, 1, u8 + 4);
+#pragma unroll
+      for (int k = 0; k < 5; ++k) u[k] = u8[k];
+    }
+    const uint8_t* mm = a.move_mask + ((size_t)g * P + pid) * 5;
+    const uint8_t* bm = a.bomb_mask + ((size_t)g * P + pid) * 2;
+    const float own_dng = s.dng[r * W + c];
+    int cell[5];
+    cell[0] = max(r - 1, 0) * W + c;
+    cell[1] = min(r + 1, H - 1) * W + c;
+    cell[2] = r * W + max(c - 1, 0);
+    cell[3] = r * W + min(c + 1, W - 1);
+    cell[4] = r * W + c;
+    float app[5], esc[5], dngc[5];
+    bool legal[5], thr[5];
+    bool app_ok = false;
+#pragma unroll
+    for (int k = 0; k < 5; ++k) {
+      const uint32_t w = s.cw[cell[k]];
+      legal[k] = mm[k] != 0 && !(w & (bot::F_WALL | bot::F_BRICK));
+      thr[k] = s.thr[cur][cell[k]] != 0;
+      const float thf = thr[k] ? 1.0f : 0.0f;
+      const float noise = 0.05f * u[k];
+      dngc[k] = s.dng[cell[k]];
+      float ap = ((s.vo[cell[k]] + 2.0f * dngc[k]) + 2.0f * thf) + noise;
+      if (dngc[k] >= 0.5f || !legal[k]) ap = INF;
+      app[k] = ap;
+      app_ok |= ap != INF;
+      esc[k] = ((s.vs[cell[k]] * 100.0f) + 2.0f * thf) + noise;
+    }
+    const bool use_esc = own_dng >= 0.35f || !app_ok;
+    float score[5];
+#pragma unroll
+    for (int k = 0; k < 5; ++k) {
+      float e = esc[k];
+      if ((use_esc && k == 4) || !legal[k]) e = INF;
+      score[k] = use_esc ? e : app[k];
+    }
+    // argmin with the first index winning ties (all-inf -> 0)
+    int move = 0;
+    bool finite = score[0] != INF;
+#pragma unroll
+    for (int k = 1; k < 5; ++k) {
+      if (score[k] < score[move]) move = k;
+      finite |= score[k] != INF;
+    }
+    bool any_legal = false;
+#pragma unroll
+    for (int k = 0; k < 5; ++k) any_legal |= legal[k];
+    if (!finite && any_legal) {
+      float dl[5];
+#pragma unroll
+      for (int k = 0; k < 5; ++k) dl[k] = legal[k] ? dngc[k] : INF;
+      int fm = 0, fi = 0;
+#pragma unroll
+      for (int k = 1; k < 4; ++k)
+        if (dl[k] < dl[fm]) fm = k;
+#pragma unroll
+      for (int k = 1; k < 5; ++k)
+        if (dl[k] < dl[fi]) fi = k;
+      move = dl[fm] != INF ? fm : fi;
+    }
+
+    // placement
+    long long dr_o = 1000000000LL, dc_o = 1000000000LL;
+    for (int o = 0; o < P; ++o) {
+      if (o == pid || !pl[o * QQT_P_SLOTS + QQT_P_ALIVE]) continue;
+      const float oy = __int_as_float(pl[o * QQT_P_SLOTS + QQT_P_Y]);
+      const float ox = __int_as_float(pl[o * QQT_P_SLOTS + QQT_P_X]);
+      const int ro = min(max((int)floorf(oy), 0), H - 1);
+      const int co = min(max((int)floorf(ox), 0), W - 1);
+      dr_o = r > ro ? r - ro : ro - r;
+      dc_o = c > co ? c - co : co - c;
+    }
+    const bool aligned = (dr_o == 0 && dc_o <= cap) || (dc_o == 0 && dr_o <= cap);
+    const long long manh = min(dr_o + dc_o, 100000000LL);
+    const bool near = manh <= (long long)max(cap + 1, 1);
+    bool can_escape = false;
+#pragma unroll
+    for (int k = 0; k < 5; ++k) can_escape |= legal[k] && dngc[k] < 0.35f && !thr[k];
+    int place = (bm[1] != 0 && (aligned || near || chain) && own_dng < 0.2f && can_escape) ? 1 : 0;
+    if (!alive) {
+      move = 4;
+      place = 0;
+    }
+    const size_t o = ((size_t)g * P + pid) * 2;
+    if (a.actions) {
+      a.actions[o] = move;
+      a.actions[o + 1] = place;
+    }
+    if (a.actions_i8) {
+      a.actions_i8[o] = (int8_t)move;
+      a.actions_i8[o + 1] = (int8_t)place;
+    }
+  }
+}
+
+extern thread_local char g_err[512];
+
+template <int H, int W, int P>
+static int launch_bot(const qqt_sim_config* cfg, const qqt_bot_args* a, hipStream_t st) {
+  hipLaunchKernelGGL((bot_kernel<H, W, P>), dim3(a->n_envs), dim3(64), 0, st, *cfg, *a);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    snprintf(g_err, sizeof(g_err), "bot launch failed: %s", hipGetErrorString(err));
+    return QQT_E_LAUNCH;
+  }
+  return QQT_OK;
+}
+
+}  // namespace qqt
+
+extern "C" {
+
+int qqt_bot_act(const qqt_sim_config* cfg, const qqt_bot_args* a, void* stream) {
+  using namespace qqt;
+  g_err[0] = 0;
+  if (!cfg || !a) {
+    snprintf(g_err, sizeof(g_err), "qqt_bot_act: null config or args");
+    return QQT_E_ARG;
+  }
+  if (a->n_envs <= 0 || !a->cells || !a->players || !a->obs || !a->move_mask ||
+      !a->bomb_mask || (!a->actions && !a->actions_i8)) {
+    snprintf(g_err, sizeof(g_err), "qqt_bot_act: null pointer or empty batch");
+    return QQT_E_ARG;
+  }
+  if (a->pid < 0 || a->pid >= cfg->n_players || cfg->growth_blast_max < 0 ||
+      cfg->growth_blast_max > 64) {
+    snprintf(g_err, sizeof(g_err), "qqt_bot_act: bad player id or dilation count");
+    return QQT_E_ARG;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  const int h = cfg->height, w = cfg->width, p = cfg->n_players;
+  if (h == 13 && w == 13 && p == 2) return launch_bot<13, 13, 2>(cfg, a, st);
+  if (h == 7 && w == 7 && p == 2) return launch_bot<7, 7, 2>(cfg, a, st);
+  if (h == 9 && w == 9 && p == 2) return launch_bot<9, 9, 2>(cfg, a, st);
+  if (h == 13 && w == 13 && p == 3) return launch_bot<13, 13, 3>(cfg, a, st);
+  if (h == 13 && w == 13 && p == 4) return launch_bot<13, 13, 4>(cfg, a, st);
+  snprintf(g_err, sizeof(g_err), "grid %dx%d with %d players is not compiled", h, w, p);
+  return QQT_E_UNSUPPORTED;
+}
+
+}  // extern "C"

@@ -285,6 +285,8 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int r16 = lane & 15, q = lane >> 4;
   const int kg = w >> 2, cg = w & 3;       // layer-1 K group, column group
+  const int oslots = a.out_slots > 0 ? a.out_slots : a.npid;   // output row width (slots)
+  const int oslot = a.npid == 2 ? slot : a.out_slot;
 
   // Parameter vectors: two floats per thread, loaded before the first tiles
   // (vmcnt retires in order) and written to LDS after they are issued.
@@ -381,7 +383,7 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
 #pragma unroll
     for (int k = 0; k < 2; ++k)
       bm[k] = a.bomb_mask[(size_t)srow * a.bm_row_stride + (size_t)pid * a.bm_pid_stride + k];
-    const size_t o = (size_t)srow * a.npid + (a.npid == 2 ? slot : 0);
+    const size_t o = (size_t)srow * oslots + oslot;
     if (a.uniforms) {
       um = a.uniforms[o * 2 + 0];
       ub = a.uniforms[o * 2 + 1];
@@ -512,7 +514,7 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   // ---------------- outputs and sampling: one thread per row
   if (threadIdx.x < ROWS && srow < a.batch) {
     const float* lg = s.logit[threadIdx.x];
-    const size_t o = (size_t)srow * a.npid + (a.npid == 2 ? slot : 0);
+    const size_t o = (size_t)srow * oslots + oslot;
     if (a.logits_out) {
 #pragma unroll
       for (int k = 0; k < NOUT; ++k) a.logits_out[o * NOUT + k] = lg[k];
@@ -556,6 +558,14 @@ int qqt_mlp_act(const qqt_mlp_args* a, void* stream) {
       (a->obs_stride % 2) || (((uintptr_t)a->obs) & 3)) {
     snprintf(g_err, sizeof(g_err), "qqt_mlp_act: bad shape/stride/alignment");
     return QQT_E_ARG;
+  }
+  {
+    const int oslots = a->out_slots > 0 ? a->out_slots : a->npid;
+    if (a->out_slots < 0 || oslots < a->npid || oslots > 4 || a->out_slot < 0 ||
+        (a->npid == 1 && a->out_slot >= oslots)) {
+      snprintf(g_err, sizeof(g_err), "qqt_mlp_act: bad output slots");
+      return QQT_E_ARG;
+    }
   }
   if (a->sample && (!a->move_mask || !a->bomb_mask)) {
     snprintf(g_err, sizeof(g_err), "qqt_mlp_act: sampling needs masks");

@@ -7,6 +7,7 @@ libqqt_hip.so (C ABI in include/qqt_hip.h).  Importing the package does not
 load the library; the first sim or policy does, and raises if it is missing.
 """
 
+from .bots import HipAstarBot
 from .config import SimConfig, corridor_training_config
 from .factory import make_sim
 from .maps import BOMB_STRESS_40, CORRIDOR_70, OPEN_PILLARS, MapSpec
@@ -14,6 +15,6 @@ from .policy import HipActorCritic, default_init
 from .rollout import Rollout
 from .sim import HipBatchedSim
 
-__all__ = ["SimConfig", "corridor_training_config", "make_sim", "MapSpec", "OPEN_PILLARS",
+__all__ = ["HipAstarBot", "SimConfig", "corridor_training_config", "make_sim", "MapSpec", "OPEN_PILLARS",
            "CORRIDOR_70", "BOMB_STRESS_40", "HipActorCritic", "default_init", "Rollout",
            "HipBatchedSim"]

@@ -14,7 +14,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 
 from ._build import LIB
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 MODE_STEP, MODE_OBSERVE, MODE_RESET, MODE_PROBE = 0, 1, 2, 3
 
@@ -55,7 +55,15 @@ class MlpArgsC(ctypes.Structure):
         ("seed", _u64), ("tick", _u32), ("w0_players", _i32)] + [
         (n, _vp) for n in ("obs", "w0", "w1", "wh", "wf", "w1_lo", "wh_lo", "wf_lo", "b0", "ln1_w", "ln1_b", "b1",
                            "ln2_w", "ln2_b", "bh", "bf", "move_mask", "bomb_mask", "uniforms",
-                           "actions", "actions_i8", "logp_out", "value_out", "logits_out")]
+                           "actions", "actions_i8", "logp_out", "value_out", "logits_out")] + [
+        ("out_slots", _i32), ("out_slot", _i32)]
+
+
+class BotArgsC(ctypes.Structure):
+    _fields_ = [("n_envs", _i32), ("pid", _i32), ("seed", _u64), ("tick", _u32),
+                ("reserved", _i32)] + [
+        (n, _vp) for n in ("cells", "players", "obs", "move_mask", "bomb_mask", "uniforms",
+                           "reach", "actions", "actions_i8")]
 
 
 _LIB = None
@@ -75,6 +83,8 @@ def lib():
         L.qqt_tick.argtypes = [ctypes.POINTER(SimConfigC), ctypes.POINTER(TickArgsC), _vp]
         L.qqt_mlp_act.restype = ctypes.c_int
         L.qqt_mlp_act.argtypes = [ctypes.POINTER(MlpArgsC), _vp]
+        L.qqt_bot_act.restype = ctypes.c_int
+        L.qqt_bot_act.argtypes = [ctypes.POINTER(SimConfigC), ctypes.POINTER(BotArgsC), _vp]
         if L.qqt_abi_version() != ABI_VERSION:
             raise RuntimeError("libqqt_hip.so ABI version mismatch; rebuild it")
         _LIB = L

@@ -1,0 +1,102 @@
+"""`HipAstarBot`: the reference's astar rule bot on the MI355X kernel.
+
+Drop-in for `partial(astar_attack)` wrapped by `BotWrapper` (sim/bots.py:
+267-508, :511-545) for the learner-vs-bot rollout: `act(obs, mmask, bmask,
+pid)` returns (N, 2) int64 actions like the reference bot, computed by one
+`qqt_bot_act` launch that reads the sim's device state directly.  Behaviour
+modes and crate eating are not on this path (the reference's defaults for
+the astar opponent are modes off, `eat_crates=False`).
+
+The noise uniforms come from Philox (stream 7, keyed by env and this bot's
+call counter) unless `uniforms=(N, 5)` is passed.  The chain check reaches
+out to the batch maximum of the bot's blast cap, as in the reference
+(`int(cap.max().item())`, sim/bots.py:477), computed on the device without a
+host round trip; `own_cap_reach=True` uses each bot's own cap instead.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _capi, state as st
+from .sim import HipBatchedSim
+
+
+class HipAstarBot:
+    is_bot = True
+
+    def __init__(self, sim: HipBatchedSim, pid: int = 1, seed: int | None = None,
+                 own_cap_reach: bool = False):
+        if not 0 <= pid < sim.cfg.n_players:
+            raise ValueError("pid out of range")
+        self.sim, self.pid = sim, int(pid)
+        self.seed = sim.seed if seed is None else int(seed)
+        self.own_cap_reach = own_cap_reach
+        self.tick = 0
+        self._lib = _capi.lib()
+        self._stream = _capi.stream_handle(sim.device)
+        self._reach = torch.zeros((), dtype=torch.int32, device=sim.device)
+        self._out = torch.zeros((sim.num_envs, sim.cfg.n_players, 2), dtype=torch.int64,
+                                device=sim.device)
+        b = _capi.BotArgsC()
+        b.n_envs, b.pid = sim.num_envs, self.pid
+        b.seed = self.seed & 0xFFFFFFFFFFFFFFFF
+        b.cells, b.players = sim._cells.data_ptr(), sim._players.data_ptr()
+        b.obs = sim._obs.data_ptr()
+        b.move_mask, b.bomb_mask = sim._mm.data_ptr(), sim._bm.data_ptr()
+        b.reach = None if own_cap_reach else self._reach.data_ptr()
+        self._args = b
+
+    def _update_reach(self):
+        if not self.own_cap_reach:
+            torch.amax(self.sim._players[:, self.pid, st.P_BLAST], out=self._reach)
+
+    def launch(self, actions: torch.Tensor) -> None:
+        """Write this bot's [move, place] into slot `pid` of an (N, P, 2)
+        int8 or int64 device action buffer (observation and masks are the
+        sim's current ones)."""
+        n, p = self.sim.num_envs, self.sim.cfg.n_players
+        if tuple(actions.shape) != (n, p, 2) or not actions.is_contiguous():
+            raise ValueError("actions must be a contiguous (N, P, 2) tensor")
+        self.sim._refresh()
+        self._update_reach()
+        b = self._args
+        b.tick = self.tick & 0xFFFFFFFF
+        b.uniforms = None
+        b.actions = actions.data_ptr() if actions.dtype == torch.int64 else None
+        b.actions_i8 = actions.data_ptr() if actions.dtype == torch.int8 else None
+        if b.actions is None and b.actions_i8 is None:
+            raise ValueError("actions must be int8 or int64")
+        _capi.check(self._lib.qqt_bot_act(self.sim._cfg_c, b, self._stream))
+        self.tick += 1
+
+    def act(self, obs, mmask, bmask, pid: int | None = None, uniforms=None):
+        """(N, 2) int64 [move, place] (BotWrapper.act, sim/bots.py:511-545).
+        `obs`/`mmask`/`bmask` are the observation and this player's masks;
+        the sim's own buffers are used when they are the ones passed."""
+        if pid is not None and int(pid) != self.pid:
+            raise ValueError("this bot plays pid %d" % self.pid)
+        sim, n, p = self.sim, self.sim.num_envs, self.sim.cfg.n_players
+        sim._refresh()
+        b = self._args
+        obs_t = obs.to(sim.device, torch.float16).contiguous()
+        if tuple(obs_t.shape) != tuple(sim._obs.shape):
+            raise ValueError("observation shape differs from the sim's")
+        mm = torch.zeros((n, p, 5), dtype=torch.uint8, device=sim.device)
+        bm = torch.zeros((n, p, 2), dtype=torch.uint8, device=sim.device)
+        mm[:, self.pid] = mmask.to(sim.device).to(torch.uint8)
+        bm[:, self.pid] = bmask.to(sim.device).to(torch.uint8)
+        u = None if uniforms is None else uniforms.to(sim.device, torch.float32).contiguous()
+        self._update_reach()
+        b.obs, b.move_mask, b.bomb_mask = obs_t.data_ptr(), mm.data_ptr(), bm.data_ptr()
+        b.tick = self.tick & 0xFFFFFFFF
+        b.uniforms = _capi.ptr(u)
+        b.actions, b.actions_i8 = self._out.data_ptr(), None
+        try:
+            _capi.check(self._lib.qqt_bot_act(sim._cfg_c, b, self._stream))
+        finally:
+            b.obs, b.move_mask, b.bomb_mask = sim._obs.data_ptr(), sim._mm.data_ptr(), \
+                sim._bm.data_ptr()
+        if uniforms is None:
+            self.tick += 1
+        return self._out[:, self.pid].clone()

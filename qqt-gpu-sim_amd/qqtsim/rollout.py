@@ -27,10 +27,19 @@ from .sim import HipBatchedSim
 
 
 class Rollout:
-    def __init__(self, sim: HipBatchedSim, policy: HipActorCritic):
+    """Self-play (both players from `policy`) or learner vs `opponent`: the
+    policy plays player 0 and an opponent with a `launch(actions)` method
+    (`qqtsim.bots.HipAstarBot`) writes player 1's slot of the same int8
+    action buffer before the tick."""
+
+    def __init__(self, sim: HipBatchedSim, policy: HipActorCritic, opponent=None):
         p = sim.cfg.n_players
         if p != 2 or policy.n_players != 2:
             raise ValueError("the self-play rollout serves two players")
+        if opponent is not None and (getattr(opponent, "pid", None) != 1
+                                     or getattr(opponent, "sim", None) is not sim):
+            raise ValueError("the opponent must play pid 1 on this sim")
+        self.opponent = opponent
         if tuple(sim.cfg.obs_shape) != tuple(policy.obs_shape):
             raise ValueError("sim observation and policy input shapes differ")
         if sim.device != policy.device:
@@ -44,7 +53,8 @@ class Rollout:
         self._lib = _capi.lib()
 
         m = _capi.MlpArgsC()
-        m.batch, m.npid, m.pid0, m.sample = n, 2, 0, 1
+        m.batch, m.npid, m.pid0, m.sample = n, (2 if opponent is None else 1), 0, 1
+        m.out_slots, m.out_slot = 2, 0
         m.k0, m.kblocks0, m.obs_stride = policy.k0, policy.kblocks0, policy.k0
         m.mm_row_stride, m.mm_pid_stride = 5 * p, 5
         m.bm_row_stride, m.bm_pid_stride = 2 * p, 2
@@ -79,12 +89,23 @@ class Rollout:
     def done(self) -> torch.Tensor:
         return self.sim._done.view(torch.bool)
 
-    def launch_act(self) -> None:
-        """Both players' actions for the current observation (train/model.py:230-245)."""
+    def launch_policy(self) -> None:
+        """The policy's actions (both players in self-play, player 0 against an
+        opponent) for the current observation (train/model.py:230-245)."""
         self.sim._refresh()
         self._mlp.tick = self.policy.tick & 0xFFFFFFFF
         _capi.check(self._lib.qqt_mlp_act(self._mlp, self._stream))
         self.policy.tick += 1
+
+    def launch_opponent(self) -> None:
+        """The opponent bot's actions (sim/bots.py:267-508), if there is one."""
+        if self.opponent is not None:
+            self.opponent.launch(self.actions)
+
+    def launch_act(self) -> None:
+        """Both players' actions for the current observation."""
+        self.launch_policy()
+        self.launch_opponent()
 
     def launch_tick(self) -> None:
         """Step with the sampled actions, auto-reset, observe, masks

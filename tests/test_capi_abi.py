@@ -39,8 +39,8 @@ def _declared_functions():
 
 
 def test_header_declares_the_entry_points():
-    assert _declared_functions() == ["qqt_abi_version", "qqt_last_error", "qqt_mlp_act",
-                                     "qqt_tick"]
+    assert _declared_functions() == ["qqt_abi_version", "qqt_bot_act", "qqt_last_error",
+                                     "qqt_mlp_act", "qqt_tick"]
 
 
 def test_library_exports_every_declared_symbol():
@@ -88,7 +88,7 @@ def test_struct_layouts_match_the_header(tmp_path):
     from qqtsim import _capi
 
     structs = {"qqt_sim_config": _capi.SimConfigC, "qqt_tick_args": _capi.TickArgsC,
-               "qqt_mlp_args": _capi.MlpArgsC}
+               "qqt_mlp_args": _capi.MlpArgsC, "qqt_bot_args": _capi.BotArgsC}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "qqt_hip.h"',
              'int main(void) {']
     for cname, cls in structs.items():
@@ -189,6 +189,44 @@ def _mlp_args(**kw):
 def test_mlp_rejects_bad_arguments(lib, kw, msg):
     assert lib.qqt_mlp_act(_mlp_args(**kw), None) == -1
     assert msg in lib.qqt_last_error().decode()
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(out_slot=2, npid=1, out_slots=2), "output slots"),
+    (dict(out_slots=1), "output slots"),
+    (dict(out_slots=-1), "output slots"),
+])
+def test_mlp_rejects_bad_output_slots(lib, kw, msg):
+    assert lib.qqt_mlp_act(_mlp_args(**kw), None) == -1
+    assert msg in lib.qqt_last_error().decode()
+
+
+def _bot_args(**kw):
+    from qqtsim import _capi
+
+    b = _capi.BotArgsC()
+    b.n_envs, b.pid = 4, 1
+    for i, name in enumerate(("cells", "players", "obs", "move_mask", "bomb_mask", "actions")):
+        setattr(b, name, 0x10000 * (i + 1))
+    for k, v in kw.items():
+        setattr(b, k, v)
+    return b
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(n_envs=0), "null pointer or empty"),
+    (dict(obs=None), "null pointer or empty"),
+    (dict(actions=None), "null pointer or empty"),
+    (dict(pid=2), "bad player id"),
+    (dict(pid=-1), "bad player id"),
+])
+def test_bot_rejects_bad_arguments(lib, kw, msg):
+    assert lib.qqt_bot_act(_cfg(), _bot_args(**kw), None) == -1
+    assert msg in lib.qqt_last_error().decode()
+
+
+def test_bot_unsupported_grid(lib):
+    assert lib.qqt_bot_act(_cfg(height=11, width=11), _bot_args(), None) == -3
 
 
 def test_errors_raise_in_python(lib):

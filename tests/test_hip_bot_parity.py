@@ -1,0 +1,95 @@
+"""HIP astar bot vs the reference's astar_attack vectors and the oracle
+(needs an MI355X).  Bar: actions bit-exact given the same state,
+observation, masks and noise uniforms."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from golden_io import GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+NAMES = ["p70", "p30", "open", "chain"]
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_hip_bot_matches_reference_vectors(dev, name):
+    from qqtsim import HipAstarBot, HipBatchedSim, MapSpec, corridor_training_config
+
+    z = np.load(f"{GOLDEN}/astar_{name}.npz")
+    n = z["bot"].shape[1]
+    cfg = corridor_training_config()
+    sim = HipBatchedSim(cfg, n, device=dev, seed=0, map_spec=MapSpec(kind="open"))
+    bot = HipAstarBot(sim, pid=1)
+    for t in range(z["bot"].shape[0]):
+        snap = {k: torch.from_numpy(np.ascontiguousarray(z[k][t]))
+                for k in ("wall", "brick", "fuse", "owner", "pos", "alive", "blast_cap")}
+        sim.load_state_dict(snap)
+        got = bot.act(torch.from_numpy(z["obs"][t]), torch.from_numpy(z["mm1"][t]),
+                      torch.from_numpy(z["bm1"][t]), 1, uniforms=torch.from_numpy(z["u"][t]))
+        np.testing.assert_array_equal(got.cpu().numpy(), z["bot"][t], err_msg=f"{name} tick {t}")
+
+
+def test_learner_vs_bot_rollout_matches_oracle(dev):
+    """Rollout(policy pid 0, astar bot pid 1): MLP actions, bot actions (Philox
+    noise) and the stepped state agree with the oracle tick after tick."""
+    from oracle import philox
+    from oracle.bots import astar_act
+    from oracle.policy import mlp_forward, sample_masked
+    from oracle.sim import OracleSim
+    from qqtsim import (HipActorCritic, HipAstarBot, HipBatchedSim, MapSpec, Rollout,
+                        corridor_training_config)
+    from qqtsim.policy import default_init
+
+    n, seed, ticks = 128, 9, 24
+    cfg = corridor_training_config()
+    spec = MapSpec(kind="pillars", brick_p=0.3, bombs_cap=(2, 3), blast_cap=(2, 4))
+    params = default_init(cfg.obs_shape)
+    sim = HipBatchedSim(cfg, n, device=dev, seed=seed, map_spec=spec)
+    net = HipActorCritic(params, device=dev, seed=seed)
+    bot = HipAstarBot(sim, pid=1)
+    roll = Rollout(sim, net, opponent=bot)
+    ora = OracleSim(cfg, n, spec, seed=seed)
+    rows = np.arange(n)
+    moved = placed = 0
+    for t in range(ticks):
+        o_obs = ora.observe()
+        mm, bm = ora.legal_mask()
+        u_pol = philox.uniforms(seed, rows, net.tick, philox.STREAM_POLICY, 4)
+        u_bot = torch.from_numpy(philox.uniforms(seed, rows, bot.tick, philox.STREAM_BOT, 5))
+        lg = torch.stack([torch.cat([a, b, c[:, None]], 1)
+                          for a, b, c in [net.forward(sim.observe(), 0)]], 1).cpu()
+        roll.launch_act()
+        acts = roll.actions.long().cpu()
+        ml, bl, v = mlp_forward(params, o_obs, 0)
+        ref = torch.cat([ml, bl, v[:, None]], 1)
+        assert float((lg[:, 0] - ref).abs().max()) <= 1e-3
+        want = torch.zeros((n, 2, 2), dtype=torch.int64)
+        want[:, 0, 0] = torch.from_numpy(sample_masked(lg[:, 0, :5].numpy(), mm[:, 0].numpy(),
+                                                       u_pol[:, 0])[0])
+        want[:, 0, 1] = torch.from_numpy(sample_masked(lg[:, 0, 5:7].numpy(), bm[:, 0].numpy(),
+                                                       u_pol[:, 1])[0])
+        st = ora.state_dict()
+        want[:, 1] = astar_act(cfg, st, o_obs, mm[:, 1], bm[:, 1], 1, u_bot)
+        np.testing.assert_array_equal(acts.numpy(), want.numpy(), err_msg=f"actions tick {t}")
+        moved += int((want[:, 1, 0] != 4).sum())
+        placed += int(want[:, 1, 1].sum())
+        roll.launch_tick()
+        ora.step(acts, auto_reset=True)
+        got, ref_sd = sim.state_dict(), ora.state_dict()
+        for k in sorted(set(got) & set(ref_sd)):
+            a = got[k].cpu().numpy()
+            np.testing.assert_array_equal(a, ref_sd[k].numpy().astype(a.dtype),
+                                          err_msg=f"{k} tick {t}")
+    assert moved > 0
+    print(f"learner vs bot: {ticks} ticks x {n} envs, bot moves {moved}, placements {placed}")
