@@ -65,10 +65,13 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="CPU work budget of the cpu_baseline sample (0 = skip)")
-    ap.add_argument("--workload", choices=("rollout", "stress", "astar"), default="rollout",
+    ap.add_argument("--workload", choices=("rollout", "stress", "astar", "evalfwd"),
+                    default="rollout",
                     help="rollout: the headline self-play rollout (default); stress: "
                          "16384-env bomb-stress ticks with injected actions; astar: "
-                         "learner (MLP) vs the astar bot, 5632 envs")
+                         "learner (MLP) vs the astar bot, 5632 envs; evalfwd: 32768-env x "
+                         "128-tick rollout into the observation slab, then the batched "
+                         "evaluation forward over all 4.19M observations")
     ap.add_argument("--copy-calibrate", action="store_true",
                     help="after timing, run a 512 MiB device copy (HBM counter calibration)")
     return ap.parse_args()
@@ -209,6 +212,8 @@ def main():
         return main_stress(args, torch, dev)
     if args.workload == "astar":
         return main_astar(args, torch, dev)
+    if args.workload == "evalfwd":
+        return main_evalfwd(args, torch, dev)
     n, K, W = args.envs, args.steps, args.warmup
     cfg, spec, roll = build_workload(n, args.seed, dev)
     for _ in range(W):
@@ -481,6 +486,107 @@ def main_astar(args, torch, dev):
                         for kk, vv in v.items()} for k, v in kernels.items()},
     }
     print(json.dumps(out), flush=True)
+
+
+EVAL_ENVS, EVAL_TICKS = 32768, 128
+EVAL_FLOP_PER_ROW = MLP_FLOP_PER_ENV // 2          # one player per row
+EVAL_BYTES_PER_ROW = 14 * 169 * 2 + 8 * 4          # observation in, 8 float32 logits out
+
+
+def cpu_baseline_forward(cfg, rows, seed, budget_s):
+    """The oracle's float32 forward (one player) on the host cores."""
+    import torch
+
+    from oracle.policy import mlp_forward
+    from qqtsim.policy import default_init
+
+    cores = _cores(torch)
+    params = default_init(cfg.obs_shape)
+    g = torch.Generator().manual_seed(seed)
+    obs = (torch.rand((rows,) + tuple(cfg.obs_shape), generator=g) < 0.3).half()
+    mlp_forward(params, obs[:1024], 0)
+    done, t0 = 0, time.perf_counter()
+    while True:
+        mlp_forward(params, obs, 0)
+        done += rows
+        el = time.perf_counter() - t0
+        if el >= budget_s or done >= 64 * rows:
+            break
+    return {"value": done / el, "unit": "obs/s", "cores": cores, "kind": "port",
+            "sample": f"oracle float32 forward, {done // rows} passes over {rows} synthetic "
+                      f"observations, {el:.1f} s"}
+
+
+def main_evalfwd(args, torch, dev):
+    """32768 envs x 128 ticks of self-play rollout writing the observation
+    slab (128, 32768, 14, 13, 13) float16 (19.85 GB) directly, then one
+    batched actor/critic forward (player 0: logits + value) over all
+    4,194,304 observations, as the PPO evaluation pass does."""
+    from qqtsim.config import corridor_training_config
+    from qqtsim.maps import MapSpec
+    from qqtsim.policy import HipActorCritic, default_init
+    from qqtsim.rollout import Rollout
+    from qqtsim.sim import HipBatchedSim
+
+    n = EVAL_ENVS if args.envs == 5632 else args.envs
+    T = EVAL_TICKS
+    cfg = corridor_training_config()
+    spec = MapSpec(kind="pillars", brick_p=0.7, swap_spawns=True)
+    params = default_init(cfg.obs_shape)
+    sim = HipBatchedSim(cfg, n, device=dev, seed=args.seed, map_spec=spec)
+    net = HipActorCritic(params, device=dev, seed=args.seed)
+    roll = Rollout(sim, net)
+    for _ in range(4):
+        roll.step()
+    buf = torch.empty((T, n) + tuple(cfg.obs_shape), dtype=torch.float16, device=dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    roll.run_into(buf)
+    torch.cuda.synchronize()
+    el_roll = time.perf_counter() - t0
+
+    rows = T * n
+    flat = buf.view(rows, -1)
+    out = torch.empty((rows, 1, 8), dtype=torch.float32, device=dev)
+    net._run(flat, 1, 0, False, logits=out)          # warm-up
+    torch.cuda.synchronize()
+    reps = max(1, args.steps // 64)
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t1 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(reps):
+        net._run(flat, 1, 0, False, logits=out)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    el_fwd = (time.perf_counter() - t1) / reps
+    fwd_ms = e0.elapsed_time(e1) / reps
+    gbs = EVAL_BYTES_PER_ROW * rows / (fwd_ms * 1e-3) / 1e9
+    tflops = EVAL_FLOP_PER_ROW * rows / (fwd_ms * 1e-3) / 1e12
+    cpu = cpu_baseline_forward(cfg, 32768, args.seed, args.cpu_seconds) \
+        if args.cpu_seconds > 0 else None
+    res = {
+        "metric": "obs/s of the batched actor/critic evaluation forward over a 128 x 32768 "
+                  "rollout slab (4.19M observations), 1 MI355X",
+        "value": rows / el_fwd, "unit": "obs/s", "n_gpus": 1, "steps": reps, "warmup": 1,
+        "ms_per_step": el_fwd * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16 MFMA (f32 accumulate; hi/lo f16 after layer 1)",
+        "data": "synthetic: observations from a self-play rollout on template maps, "
+                "PyTorch default-init MLP weights",
+        "config": {"workload": "rollout 32768 envs x 128 ticks into the float16 observation "
+                               "slab, then one forward (player 0) over all 4,194,304 rows",
+                   "envs": n, "ticks": T, "rows": rows, "parallelism": "single GPU"},
+        "roofline": {"kernel": "mlp_act_kernel (forward, 4.19M rows)", "bound": "hbm",
+                     "achieved": round(gbs, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 5), "traffic": None},
+        "mfma": {"achieved_tflops": round(tflops, 3), "peak_tflops": MFMA_F16_PEAK_TFLOPS,
+                 "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 5),
+                 "flop_per_row": EVAL_FLOP_PER_ROW},
+        "rollout": {"env_steps_per_s": n * T / el_roll, "ms": el_roll * 1e3,
+                    "slab_gb": buf.numel() * 2 / 1e9},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
 
 
 if __name__ == "__main__":

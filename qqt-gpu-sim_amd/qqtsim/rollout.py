@@ -130,6 +130,38 @@ class Rollout:
         self.launch_act()
         self.launch_tick()
 
+    def run_into(self, buf: torch.Tensor) -> None:
+        """T env-steps writing the observation each step acts on straight into
+        `buf` (T, N, C, H, W) float16, the rollout buffer's observation
+        slab (train/ppo.py:54-110): buf[0] is the current observation, the
+        tick of step t writes buf[t + 1] (the last one lands in the sim's own
+        buffer), and the policy of step t reads buf[t].  No copies besides
+        buf[0]."""
+        sim = self.sim
+        n = sim.num_envs
+        if buf.dtype != torch.float16 or not buf.is_contiguous() or buf.device != sim.device \
+                or tuple(buf.shape[1:]) != (n,) + tuple(sim.cfg.obs_shape):
+            raise ValueError("buf must be a contiguous (T, N, C, H, W) float16 device tensor")
+        if (n * buf[0, 0].numel() * 2) % 16:
+            raise ValueError("the number of envs must be a multiple of 4 (16-byte aligned slabs)")
+        T = buf.shape[0]
+        bot = self.opponent
+        buf[0].copy_(sim.observe())
+        try:
+            for t in range(T):
+                cur = buf[t].data_ptr()
+                self._mlp.obs = cur
+                if bot is not None:
+                    bot._args.obs = cur
+                self.launch_act()
+                self._tick.obs = buf[t + 1].data_ptr() if t + 1 < T else sim._obs.data_ptr()
+                self.launch_tick()
+        finally:
+            self._mlp.obs = sim._obs.data_ptr()
+            self._tick.obs = sim._obs.data_ptr()
+            if bot is not None:
+                bot._args.obs = sim._obs.data_ptr()
+
     def run(self, ticks: int) -> None:
         for _ in range(int(ticks)):
             self.launch_act()

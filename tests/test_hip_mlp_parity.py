@@ -139,3 +139,39 @@ def test_sampling_frequencies_follow_softmax(dev):
     exp = p * b
     chi2 = float(((cnt - exp) ** 2 / np.maximum(exp, 1e-9))[[0, 2, 3, 4]].sum())
     assert chi2 < 25.0, (cnt, exp)
+
+
+def test_rollout_into_buffer_and_batched_forward(dev):
+    """Rollout.run_into writes the observation each step acted on into a
+    (T, N, C, H, W) slab (identical to stepping and copying observe()), and
+    the batched evaluation forward over all T*N rows matches the oracle
+    forward on sampled rows."""
+    from oracle.policy import mlp_forward
+    from qqtsim import HipActorCritic, HipBatchedSim, MapSpec, Rollout, corridor_training_config
+    from qqtsim.policy import default_init
+
+    n, T, seed = 256, 12, 4
+    cfg = corridor_training_config()
+    spec = MapSpec(kind="pillars", brick_p=0.7, swap_spawns=True)
+    params = default_init(cfg.obs_shape)
+    a_sim = HipBatchedSim(cfg, n, device=dev, seed=seed, map_spec=spec)
+    a = Rollout(a_sim, HipActorCritic(params, device=dev, seed=seed))
+    buf = torch.empty((T, n) + tuple(cfg.obs_shape), dtype=torch.float16, device=dev)
+    a.run_into(buf)
+    b_sim = HipBatchedSim(cfg, n, device=dev, seed=seed, map_spec=spec)
+    b = Rollout(b_sim, HipActorCritic(params, device=dev, seed=seed))
+    for t in range(T):
+        assert torch.equal(b_sim.observe(), buf[t]), t
+        b.step()
+    assert torch.equal(a_sim.observe(), b_sim.observe())
+    for k, v in a_sim.state_dict().items():
+        assert torch.equal(v, b_sim.state_dict()[k]), k
+
+    net = HipActorCritic(params, device=dev)
+    flat = buf.view(T * n, *cfg.obs_shape)
+    ml, bl, v = net.forward(flat, 0)
+    idx = torch.randperm(T * n, generator=torch.Generator().manual_seed(0))[:512]
+    rml, rbl, rv = mlp_forward(params, flat[idx.to(dev)].cpu(), 0)
+    got = torch.cat([ml[idx.to(dev)], bl[idx.to(dev)], v[idx.to(dev)][:, None]], 1).cpu()
+    ref = torch.cat([rml, rbl, rv[:, None]], 1)
+    assert float((got - ref).abs().max()) <= LOGIT_ATOL
