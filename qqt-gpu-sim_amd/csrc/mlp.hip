@@ -135,15 +135,17 @@ __device__ __forceinline__ float* f1_at(uint16_t* xs, int row, int col) {
 }
 
 // Row-wise bias + LayerNorm(128) + ReLU from the fp32 tile (plus the second
-// partial tile f1 when given): thread t owns row t/8, columns 16*(t%8)..+15;
-// writes float16 hi/lo planes of dst.
+// partial tile f1 when given): thread t owns row t/8; lane j = t%8 of a row
+// owns columns 32i + 4j .. +3 (i = 0..3), so for each i the row's 8 lanes
+// read 128 contiguous bytes (no bank conflicts); writes float16 hi/lo planes
+// of dst as 8-byte stores.
 __device__ __forceinline__ void layernorm_rows(MlpLds& s, const uint16_t* f1, int vb, int vg,
                                                int vbe, uint16_t* dst) {
-  const int t = threadIdx.x, row = t >> 3, c0 = 16 * (t & 7);
+  const int t = threadIdx.x, row = t >> 3, j = t & 7;
   float v[16], ga[16], be[16];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int c = c0 + 4 * i;
+    const int c = 32 * i + 4 * j;
     const float4 x = *reinterpret_cast<const float4*>(&s.f[row][c]);
     const float4 b = *reinterpret_cast<const float4*>(&s.vec[vb + c]);
     const float4 g = *reinterpret_cast<const float4*>(&s.vec[vg + c]);
@@ -172,24 +174,24 @@ __device__ __forceinline__ void layernorm_rows(MlpLds& s, const uint16_t* f1, in
     q += d * d;
   }
   const float rstd = 1.0f / sqrtf(sum8(q) * (1.0f / HID) + 1e-5f);
-  uint32_t hi[8], lo[8];
 #pragma unroll
-  for (int i = 0; i < 16; i += 2) {
-    const float y0 = fmaxf((v[i] - mean) * rstd * ga[i] + be[i], 0.0f);
-    const float y1 = fmaxf((v[i + 1] - mean) * rstd * ga[i + 1] + be[i + 1], 0.0f);
-    const __half h0 = __float2half_rn(y0), h1 = __float2half_rn(y1);
-    const __half l0 = __float2half_rn(y0 - __half2float(h0));
-    const __half l1 = __float2half_rn(y1 - __half2float(h1));
-    hi[i / 2] = (uint32_t)__half_as_ushort(h0) | ((uint32_t)__half_as_ushort(h1) << 16);
-    lo[i / 2] = (uint32_t)__half_as_ushort(l0) | ((uint32_t)__half_as_ushort(l1) << 16);
-  }
+  for (int i = 0; i < 4; ++i) {
+    uint32_t hi[2], lo[2];
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int chunk = (c0 >> 3) + k;
-    uint16_t* ph = dst + (0 * ROWS + row) * HID + (swz(row, chunk) << 3);
-    uint16_t* pl = dst + (1 * ROWS + row) * HID + (swz(row, chunk) << 3);
-    *reinterpret_cast<uint4*>(ph) = make_uint4(hi[4 * k], hi[4 * k + 1], hi[4 * k + 2], hi[4 * k + 3]);
-    *reinterpret_cast<uint4*>(pl) = make_uint4(lo[4 * k], lo[4 * k + 1], lo[4 * k + 2], lo[4 * k + 3]);
+    for (int e = 0; e < 4; e += 2) {
+      const int k = 4 * i + e;
+      const float y0 = fmaxf((v[k] - mean) * rstd * ga[k] + be[k], 0.0f);
+      const float y1 = fmaxf((v[k + 1] - mean) * rstd * ga[k + 1] + be[k + 1], 0.0f);
+      const __half h0 = __float2half_rn(y0), h1 = __float2half_rn(y1);
+      const __half l0 = __float2half_rn(y0 - __half2float(h0));
+      const __half l1 = __float2half_rn(y1 - __half2float(h1));
+      hi[e / 2] = (uint32_t)__half_as_ushort(h0) | ((uint32_t)__half_as_ushort(h1) << 16);
+      lo[e / 2] = (uint32_t)__half_as_ushort(l0) | ((uint32_t)__half_as_ushort(l1) << 16);
+    }
+    const int c = 32 * i + 4 * j;                 // 4 halves = half of chunk c/8
+    const int off = (swz(row, c >> 3) << 3) + (c & 7);
+    *reinterpret_cast<uint2*>(dst + (0 * ROWS + row) * HID + off) = make_uint2(hi[0], hi[1]);
+    *reinterpret_cast<uint2*>(dst + (1 * ROWS + row) * HID + off) = make_uint2(lo[0], lo[1]);
   }
 }
 
