@@ -146,15 +146,17 @@ typedef struct qqt_bot_args {
   int32_t pid;                /* the bot's player id */
   uint64_t seed;              /* Philox key of the noise uniforms */
   uint32_t tick;              /* counter word of the noise uniforms */
-  int32_t reserved;
+  int32_t reach_mode;         /* chain-check reach: 0 = the bot's own blast cap;
+                                 1 = the batch max of the bot's blast cap (the
+                                 reference's rule), computed by this call into
+                                 *reach; 2 = the value already in *reach */
   const int32_t* cells;       /* sim state, layout above */
   const int32_t* players;
   const uint16_t* obs;        /* [N][5P+4][H][W] float16 bits */
   const uint8_t* move_mask;   /* [N][P][5] */
   const uint8_t* bomb_mask;   /* [N][P][2] */
   const float* uniforms;      /* [N][5] noise uniforms, or NULL = Philox stream 7 */
-  const int32_t* reach;       /* device scalar: chain-check reach (the reference uses
-                                 the batch max of the bot's blast cap); NULL = own cap */
+  int32_t* reach;             /* device int32 scalar for reach_mode 1 and 2 */
   int64_t* actions;           /* [N][P][2], slot pid written; or NULL */
   int8_t* actions_i8;         /* same as int8; or NULL */
 } qqt_bot_args;

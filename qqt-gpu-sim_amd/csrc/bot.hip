@@ -22,6 +22,7 @@
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
+#include <limits.h>
 #include <stdint.h>
 #include <stdio.h>
 
@@ -144,7 +145,7 @@ __global__ __launch_bounds__(64) void bot_kernel(const qqt_sim_config cf, const 
   const int c = min(max((int)floorf(bx), 0), W - 1);
   const bool alive = pl[pid * QQT_P_SLOTS + QQT_P_ALIVE] != 0;
   const int cap = pl[pid * QQT_P_SLOTS + QQT_P_BLAST_CAP];
-  const int reach = a.reach ? *a.reach : cap;
+  const int reach = a.reach_mode != 0 ? *a.reach : cap;
 
   // chain: a bomb with fuse 1..10 within `reach` cells in line (lane = step, direction)
   bool chain_l = false;
@@ -264,10 +265,32 @@ __global__ __launch_bounds__(64) void bot_kernel(const qqt_sim_config cf, const 
   }
 }
 
+// Batch max of the bot's blast cap (the chain-check reach of the reference,
+// `int(cap.max().item())`): one workgroup strides over the envs.
+__global__ __launch_bounds__(1024) void reach_kernel(const int32_t* players, int n, int p,
+                                                     int pid, int32_t* out) {
+  __shared__ int part[16];
+  int v = INT_MIN;
+  for (int g = threadIdx.x; g < n; g += 1024)
+    v = max(v, players[((size_t)g * p + pid) * QQT_P_SLOTS + QQT_P_BLAST_CAP]);
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = max(v, __shfl_xor(v, m, 64));
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int r = part[0];
+    for (int i = 1; i < 16; ++i) r = max(r, part[i]);
+    *out = r;
+  }
+}
+
 extern thread_local char g_err[512];
 
 template <int H, int W, int P>
 static int launch_bot(const qqt_sim_config* cfg, const qqt_bot_args* a, hipStream_t st) {
+  if (a->reach_mode == 1)
+    hipLaunchKernelGGL(reach_kernel, dim3(1), dim3(1024), 0, st, a->players, a->n_envs, P,
+                       a->pid, a->reach);
   hipLaunchKernelGGL((bot_kernel<H, W, P>), dim3(a->n_envs), dim3(64), 0, st, *cfg, *a);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
@@ -291,6 +314,10 @@ int qqt_bot_act(const qqt_sim_config* cfg, const qqt_bot_args* a, void* stream) 
   if (a->n_envs <= 0 || !a->cells || !a->players || !a->obs || !a->move_mask ||
       !a->bomb_mask || (!a->actions && !a->actions_i8)) {
     snprintf(g_err, sizeof(g_err), "qqt_bot_act: null pointer or empty batch");
+    return QQT_E_ARG;
+  }
+  if (a->reach_mode < 0 || a->reach_mode > 2 || (a->reach_mode != 0 && !a->reach)) {
+    snprintf(g_err, sizeof(g_err), "qqt_bot_act: reach_mode 1/2 needs a reach scalar");
     return QQT_E_ARG;
   }
   if (a->pid < 0 || a->pid >= cfg->n_players || cfg->growth_blast_max < 0 ||

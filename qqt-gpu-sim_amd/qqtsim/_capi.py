@@ -61,7 +61,7 @@ class MlpArgsC(ctypes.Structure):
 
 class BotArgsC(ctypes.Structure):
     _fields_ = [("n_envs", _i32), ("pid", _i32), ("seed", _u64), ("tick", _u32),
-                ("reserved", _i32)] + [
+                ("reach_mode", _i32)] + [
         (n, _vp) for n in ("cells", "players", "obs", "move_mask", "bomb_mask", "uniforms",
                            "reach", "actions", "actions_i8")]
 

@@ -11,14 +11,15 @@ The noise uniforms come from Philox (stream 7, keyed by env and this bot's
 call counter) unless `uniforms=(N, 5)` is passed.  The chain check reaches
 out to the batch maximum of the bot's blast cap, as in the reference
 (`int(cap.max().item())`, sim/bots.py:477), computed on the device without a
-host round trip; `own_cap_reach=True` uses each bot's own cap instead.
+host round trip (a one-workgroup reduction launched by `qqt_bot_act`);
+`own_cap_reach=True` uses each bot's own cap instead.
 """
 
 from __future__ import annotations
 
 import torch
 
-from . import _capi, state as st
+from . import _capi
 from .sim import HipBatchedSim
 
 
@@ -44,12 +45,9 @@ class HipAstarBot:
         b.cells, b.players = sim._cells.data_ptr(), sim._players.data_ptr()
         b.obs = sim._obs.data_ptr()
         b.move_mask, b.bomb_mask = sim._mm.data_ptr(), sim._bm.data_ptr()
-        b.reach = None if own_cap_reach else self._reach.data_ptr()
+        b.reach_mode = 0 if own_cap_reach else 1
+        b.reach = self._reach.data_ptr()
         self._args = b
-
-    def _update_reach(self):
-        if not self.own_cap_reach:
-            torch.amax(self.sim._players[:, self.pid, st.P_BLAST], out=self._reach)
 
     def launch(self, actions: torch.Tensor) -> None:
         """Write this bot's [move, place] into slot `pid` of an (N, P, 2)
@@ -59,7 +57,6 @@ class HipAstarBot:
         if tuple(actions.shape) != (n, p, 2) or not actions.is_contiguous():
             raise ValueError("actions must be a contiguous (N, P, 2) tensor")
         self.sim._refresh()
-        self._update_reach()
         b = self._args
         b.tick = self.tick & 0xFFFFFFFF
         b.uniforms = None
@@ -87,7 +84,6 @@ class HipAstarBot:
         mm[:, self.pid] = mmask.to(sim.device).to(torch.uint8)
         bm[:, self.pid] = bmask.to(sim.device).to(torch.uint8)
         u = None if uniforms is None else uniforms.to(sim.device, torch.float32).contiguous()
-        self._update_reach()
         b.obs, b.move_mask, b.bomb_mask = obs_t.data_ptr(), mm.data_ptr(), bm.data_ptr()
         b.tick = self.tick & 0xFFFFFFFF
         b.uniforms = _capi.ptr(u)

@@ -219,6 +219,8 @@ def _bot_args(**kw):
     (dict(actions=None), "null pointer or empty"),
     (dict(pid=2), "bad player id"),
     (dict(pid=-1), "bad player id"),
+    (dict(reach_mode=1), "reach scalar"),
+    (dict(reach_mode=3, reach=0x9000), "reach scalar"),
 ])
 def test_bot_rejects_bad_arguments(lib, kw, msg):
     assert lib.qqt_bot_act(_cfg(), _bot_args(**kw), None) == -1
