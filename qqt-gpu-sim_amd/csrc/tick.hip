@@ -75,7 +75,6 @@ struct Geo {
 
 template <class G>
 struct DangerScratch {
-  float dd[G::EPW][4][G::C];       // danger stage B: per-direction ray values
   float fw[G::EPW][G::C];          // danger stage-A front (by cell)
   float wl[G::EPW][G::C];          // per listed bomb: corrected weight
   uint16_t edge[G::EPW][G::C][4];  // stage-A in-edge per listed bomb: sender | dist << 8
@@ -107,6 +106,15 @@ struct __align__(16) Lds {
 };
 
 // ---------------------------------------------------------------- lane helpers
+// A workgroup is exactly one wavefront: its LDS accesses are performed in
+// program order, so a sync point only has to keep the compiler from moving
+// memory operations across it (wavefront-scope fences, no s_barrier and no
+// wait for the LDS queue to drain).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 template <int LPE>
 __device__ __forceinline__ int env_sum(int v) {
 #pragma unroll
@@ -246,7 +254,7 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
       }
     }
   }
-  __syncthreads();
+  wave_sync();
 
   if (mode == QQT_MODE_STEP || mode == QQT_MODE_PROBE) {
     // ---- 1. snapshots, actions, fuse countdown, live counts
@@ -275,7 +283,7 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
       });
       if (l == 0) s.live[e][i] = t;
     }
-    __syncthreads();
+    wave_sync();
 
     // ---- 2. placement, players in id order (sim/torch_sim.py:1357-1402)
     if (l == 0) {
@@ -288,7 +296,7 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
         if (ok) cw[idx] = cw_make(w, cf.fuse, me, pl[me][QQT_P_BLAST_CAP]);
       }
     }
-    __syncthreads();
+    wave_sync();
 
     if (mode == QQT_MODE_PROBE) {
       int mb = 0;
@@ -376,7 +384,7 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
         s.pbonus[e][me] = bonus * (float)s.alive0[e][me];
       }
     }
-    __syncthreads();
+    wave_sync();
 
     // ---- 4. since_bomb; 5. movement (sim/move.py:234-279); explosion list
     if (l < 2 * P) {  // lane = player * 2 + axis; both axes start from the pre-move box
@@ -411,7 +419,7 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
       const uint32_t w = cw[c];
       return cw_fuse(w) > 0 || cw_owner(w) >= 0;
     });
-    __syncthreads();
+    wave_sync();
 
     // ---- 6. explosions (sim/blast.py:101-155), fixed synchronous rounds
     auto fire = [&](int src) {  // rays of one seed cell into cov
@@ -445,7 +453,7 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
       }
     }
     const bool env_boom = env_bits<LPE>(boom, e) != 0;
-    __syncthreads();
+    wave_sync();
     if (__any(env_boom)) {
       for (int j = l; j < nl; j += LPE) {
         const int c = list[j];
@@ -453,7 +461,7 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
       }
       const int rounds = min(cf.max_chain - 1, cf.chain_cap_rounds);
       for (int r = 0; r < rounds; ++r) {
-        __syncthreads();
+        wave_sync();
         uint32_t newly = 0;  // bit i: list entry l + LPE*i
         int i = 0;
         for (int j = l; j < nl; j += LPE, ++i) {
@@ -461,7 +469,7 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
           if (cw_fuse(cw[c]) > 0 && cov[c] && !trg[c]) newly |= 1u << (i & 31);
         }
         if (!__any(newly != 0)) break;
-        __syncthreads();
+        wave_sync();
         i = 0;
         for (int j = l; j < nl; j += LPE, ++i) {
           if (newly & (1u << (i & 31))) {
@@ -471,7 +479,7 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
           }
         }
       }
-      __syncthreads();
+      wave_sync();
       // ---- 7. burnt bricks (corridor: into crates)
       if (env_boom) {
 #pragma unroll
@@ -533,7 +541,7 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
       const int c = list[j];
       if (trg[c]) cw[c] = cw_make(cw[c], 0, -1, 0);
     }
-    __syncthreads();
+    wave_sync();
   }
 
   bool do_reset = false;
@@ -608,7 +616,7 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
   if (mode == QQT_MODE_RESET) {
     do_reset = valid && a.reset_mask[g] != 0;
     if (do_reset) template_reset();
-    __syncthreads();
+    wave_sync();
   }
 
   // ---- danger map of the current state (sim/blast.py:158-317)
@@ -616,7 +624,6 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
     float* dng = s.dng[e];
     float* fw = s.dz.fw[e];
     float* wl = s.dz.wl[e];
-    float(*dd)[C] = s.dz.dd[e];
     const int nb = build_list<G>(list, e, l, [&](int c) { return cw_fuse(cw[c]) > 0; });
 #pragma unroll
     for (int k = 0; k < KMAX; ++k) {
@@ -632,11 +639,6 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
         const float w0 = bomb_weight(cw_fuse(cw[c]), fmax_f);
         wl[j] = w0;
         fw[c] = w0;
-      }
-      // zero the per-direction ray buffers (4*C floats, 16-byte aligned)
-      {
-        float4* d4 = reinterpret_cast<float4*>(&dd[0][0]);
-        for (int i = l; i < C; i += LPE) d4[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       }
       if (cf.max_chain > 1) {
         // in-edges, one (bomb, direction) per item: the first solid cell
@@ -665,7 +667,7 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
         // stage A: synchronous relay rounds
         const int rounds = min(cf.max_chain, cf.chain_cap_rounds);
         for (int r = 0; r < rounds; ++r) {
-          __syncthreads();
+          wave_sync();
           float nf[KMAX];
           bool upd = false;
 #pragma unroll
@@ -683,7 +685,7 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
             nf[i] = nv;
             upd |= nv > 0.0f;
           }
-          __syncthreads();
+          wave_sync();
 #pragma unroll
           for (int i = 0; i < KMAX; ++i) {
             const int j = l + LPE * i;
@@ -695,16 +697,18 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
           if (!__any(upd)) break;
         }
       }
-      __syncthreads();
-      // stage B: every (bomb, direction) ray writes its own direction's
-      // buffer; within one direction rays never overlap, so plain stores
+      wave_sync();
+      // stage B: every (bomb, direction) ray max-updates the danger map.
+      // Danger values are >= 0, so their float bits order like ints and an
+      // LDS integer atomic max is exact whatever the order of the rays.
+      int* dngi = reinterpret_cast<int*>(dng);
       for (int it = l; it < 4 * nb; it += LPE) {
         const int j = it >> 2, d = it & 3;
         const int c = list[j];
         const uint32_t wc = cw[c];
         const float v = wl[j];
         if (wc & F_WALL) continue;
-        if (d == 0) dng[c] = v;  // the bomb's own cell (seed)
+        if (d == 0) atomicMax(&dngi[c], __float_as_int(v));  // the bomb's own cell (seed)
         const int b = blast_of(wc, cf.blast);
         const int r0 = c / W, c0 = c % W;
         const int dr = dir_dr(d), dc = dir_dc(d);
@@ -714,21 +718,12 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
           const int x = rr * W + cc;
           const uint32_t wx = cw[x];
           if (wx & F_WALL) break;
-          dd[d][x] = v;
+          atomicMax(&dngi[x], __float_as_int(v));
           if (cw_solid(wx)) break;
         }
       }
-      __syncthreads();
-#pragma unroll
-      for (int k = 0; k < KMAX; ++k) {
-        const int c = l + LPE * k;
-        if (c < C) {
-          const float m = fmaxf(fmaxf(dd[0][c], dd[1][c]), fmaxf(dd[2][c], dd[3][c]));
-          dng[c] = fmaxf(dng[c], m);
-        }
-      }
     }
-    __syncthreads();
+    wave_sync();
   }
 
   if (mode == QQT_MODE_STEP) {
@@ -856,9 +851,9 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
         s.done[e] = done && a.auto_reset && valid;
       }
     }
-    __syncthreads();
+    wave_sync();
     if (s.done[e]) template_reset();
-    __syncthreads();
+    wave_sync();
   }
 
   // ---- observation + legality masks of the current state (sim/obs.py:25-229)
@@ -871,7 +866,7 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
       constexpr int N16 = sizeof(s.obs_raw) / 16;
       for (int i = lane; i < N16; i += 64) z[i] = make_uint4(0u, 0u, 0u, 0u);
     }
-    __syncthreads();
+    wave_sync();
     uint16_t* ob = reinterpret_cast<uint16_t*>(s.obs_raw + opad) + (size_t)e * OBS;
     const float tplane = __fdiv_rn((float)s.ev[e][QQT_E_T], (float)cf.max_steps);
     const uint16_t h_one = __half_as_ushort(__float2half_rn(1.0f));
@@ -905,7 +900,7 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
       });
       if (l == 0) s.live[e][i] = t;
     }
-    __syncthreads();
+    wave_sync();
     if (l < P) {
       // splat: the four corner terms accumulate in order (0,0),(0,1),(1,0),(1,1)
       const int i = l;
@@ -969,7 +964,7 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
       }
     }
   }
-  __syncthreads();
+  wave_sync();
 
   // ---- store state and the staged observation
   if (mode == QQT_MODE_STEP || mode == QQT_MODE_RESET) {
