@@ -1,10 +1,13 @@
 // Fused rollout tick for gfx950: step + auto-reset + danger + observation +
 // legality masks of a batch of envs in one launch.
 //
-// Mapping: one 64-lane wavefront (= one workgroup) owns EPW = 64 / LPE
-// consecutive envs; each env gets LPE lanes (LPE = 64 on MI355X: a wavefront
-// per env keeps ~5 waves per SIMD in flight at 5632 envs).  Lane l of an env
-// walks the cells c = l, l + LPE, ...  Per-env grids live in LDS for the
+// Mapping: one 64-lane wavefront owns EPW = 64 / LPE consecutive envs; each
+// env gets LPE lanes (LPE = 64 on MI355X: a wavefront per env).  Lane l of an
+// env walks the cells c = l, l + LPE, ...  A workgroup holds WPB independent
+// wavefronts (own envs, own LDS, wave-level syncs only): with WPB = 2 a CU
+// keeps 11 workgroups = 22 envs resident (LDS-bound, 6.8 KB per env), so a
+// 5632-env batch runs in one round on 256 CUs; one-wave workgroups would hit
+// the per-CU workgroup-slot limit first.  Per-env grids live in LDS for the
 // whole tick; the observation is staged in LDS in its final (N, C, H, W)
 // float16 layout and leaves with wide, fully coalesced stores.
 //
@@ -19,9 +22,9 @@
 // * danger stage A: each bomb gathers from its (at most four) in-neighbours,
 //   the first solid cell behind it in each direction, for a fixed number of
 //   synchronous rounds;
-// * danger stage B: bombs scatter their corrected weight one direction at a
-//   time.  Within one direction two rays never share a cell (the nearer bomb
-//   stops the farther one's ray), so a plain LDS max-update is race free.
+// * danger stage B: every (bomb, direction) ray scatters the bomb's corrected
+//   weight along its cells.  Rays of different bombs may share a cell; danger values are >= 0,
+//   so an LDS integer atomic max on their float bits is exact in any order.
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -202,19 +205,24 @@ __device__ __forceinline__ int build_list(uint8_t* list, int e, int l, Pred pred
 }
 
 // ---------------------------------------------------------------- kernel
-template <int H, int W, int P, int LPE>
-__global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const qqt_tick_args a) {
+template <int H, int W, int P, int LPE, int WPB>
+__global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf, const qqt_tick_args a) {
   using G = Geo<H, W, P, LPE>;
   constexpr int C = G::C;
   constexpr int EPW = G::EPW;
   constexpr int OBS = G::OBS;
   constexpr int KMAX = G::KMAX;
-  __shared__ Lds<G, P> s;
+  __shared__ Lds<G, P> sh[WPB];
 
-  const int lane = threadIdx.x;
+  // waves of one workgroup share nothing: each owns its envs and its LDS
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g0 = (blockIdx.x * WPB + wv) * EPW;
+  if (g0 >= a.n_envs) return;
+  Lds<G, P>& s = sh[wv];
+  const int lane = threadIdx.x & 63;
   const int e = lane / LPE;
   const int l = lane % LPE;
-  const int g = blockIdx.x * EPW + e;
+  const int g = g0 + e;
   const bool valid = g < a.n_envs;
   const int mode = a.mode;
   const float rad = cf.radius;
@@ -857,7 +865,6 @@ __global__ __launch_bounds__(64) void tick_kernel(const qqt_sim_config cf, const
   }
 
   // ---- observation + legality masks of the current state (sim/obs.py:25-229)
-  const int g0 = blockIdx.x * EPW;
   const int opad = (int)(((uintptr_t)(a.obs + (size_t)g0 * OBS)) & 15u);  // staging offset
   {
     // everything starts as zero; only nonzero values are written afterwards
@@ -1010,13 +1017,18 @@ int fail(int code, const char* msg) {
 #ifndef QQT_LPE
 #define QQT_LPE 64
 #endif
+#ifndef QQT_TICK_WPB
+#define QQT_TICK_WPB 2
+#endif
 
 template <int H, int W, int P>
 int launch(const qqt_sim_config* cfg, const qqt_tick_args* a, hipStream_t st) {
   constexpr int LPE = QQT_LPE;
+  constexpr int WPB = QQT_TICK_WPB;
   constexpr int EPW = 64 / LPE;
-  const int blocks = (a->n_envs + EPW - 1) / EPW;
-  hipLaunchKernelGGL((tick_kernel<H, W, P, LPE>), dim3(blocks), dim3(64), 0, st, *cfg, *a);
+  const int waves = (a->n_envs + EPW - 1) / EPW;
+  const int blocks = (waves + WPB - 1) / WPB;
+  hipLaunchKernelGGL((tick_kernel<H, W, P, LPE, WPB>), dim3(blocks), dim3(64 * WPB), 0, st, *cfg, *a);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     snprintf(g_err, sizeof(g_err), "tick launch failed: %s", hipGetErrorString(err));
