@@ -2,9 +2,11 @@
 // danger-weighted multi-source shortest-cost fields and steepest descent on
 // them, for one player of a batch of envs, in one launch.
 //
-// Mapping: one 64-lane wavefront (= one workgroup) per env.  The env's
-// obstacles, danger and threat maps and both cost fields live in LDS (~3 KB);
-// lane l owns cells l, l + 64, l + 128.
+// Mapping: one 64-lane wavefront per env, two independent wavefronts per
+// workgroup (a CU holds more waves than workgroups).  The env's obstacles,
+// danger and threat maps and both cost fields live in LDS (~3.5 KB); lane l
+// owns cells l, l + 64, l + 128.  Every global load (cells, danger, players,
+// masks, noise) is issued at the start.
 //
 // Cost fields: dist = min(dist, min_4nbr(dist) + cost), cost = 1 + 2 danger
 // (inf on blocked cells), sources at 0 even when blocked, relaxed in place
@@ -37,115 +39,171 @@ constexpr uint32_t F_WALL = 1u << 24, F_BRICK = 1u << 25;
 __device__ __forceinline__ int fuse_of(uint32_t w) { return (int)(w & 0xFFu); }
 __device__ __forceinline__ int owner_of(uint32_t w) { return (int)(int8_t)((w >> 8) & 0xFFu); }
 
-template <int H, int W>
+template <int H, int W, int P>
 struct BotLds {
   static constexpr int C = H * W;
   float dng[C];       // danger (the observation's float16 channel, widened)
-  float cost[C];      // 1 + 2 danger, inf where blocked
   float vs[C];        // V_safe
   float vo[C];        // V_opp
   uint32_t cw[C];     // packed cell words
-  uint8_t thr[2][C];  // threat map, double buffer for the dilation
+  uint8_t thr[C];     // threat map
+  int32_t pl[P * QQT_P_SLOTS];  // player slots of the env
+  float u[8];         // noise uniforms
+  uint8_t mm[5], bm[2];         // the bot's legality masks
 };
 
 }  // namespace bot
 
-template <int H, int W, int P>
-__global__ __launch_bounds__(64) void bot_kernel(const qqt_sim_config cf, const qqt_bot_args a) {
+template <int H, int W, int P, int WPB>
+__global__ __launch_bounds__(64 * WPB) void bot_kernel(const qqt_sim_config cf, const qqt_bot_args a) {
   constexpr int C = H * W;
   constexpr int KMAX = (C + 63) / 64;
-  __shared__ bot::BotLds<H, W> s;
-  const int lane = threadIdx.x;
-  const int g = blockIdx.x;                  // grid = n_envs
+  constexpr int NPL = P * QQT_P_SLOTS;
+  static_assert(NPL <= 64, "player slots must fit one wavefront");
+  __shared__ bot::BotLds<H, W, P> sh[WPB];
+  // the waves of a workgroup share nothing: each owns one env and its LDS
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = blockIdx.x * WPB + wv;
+  if (g >= a.n_envs) return;
+  bot::BotLds<H, W, P>& s = sh[wv];
+  const int lane = threadIdx.x & 63;
   const int pid = a.pid;
   const float INF = __builtin_inff();
   const uint16_t* obs = a.obs + (size_t)g * (5 * P + 4) * C + (size_t)(2 * P + 1) * C;
-  const int32_t* pl = a.players + (size_t)g * P * QQT_P_SLOTS;
 
-  // ---- load: cells, danger, cost, sources, threat
+  // ---- every global load is issued first; the Philox noise is computed
+  // (lane 0: words 0-3, lane 1: words 4-7) while they are in flight
+  uint32_t wreg[KMAX];
+  uint16_t dreg[KMAX];
 #pragma unroll
   for (int k = 0; k < KMAX; ++k) {
     const int c = lane + 64 * k;
+    wreg[k] = c < C ? (uint32_t)a.cells[(size_t)g * C + c] : 0u;
+    dreg[k] = c < C ? obs[c] : (uint16_t)0;
+  }
+  const int plv = lane < NPL ? a.players[(size_t)g * NPL + lane] : 0;
+  const int mv = lane < 5 ? a.move_mask[((size_t)g * P + pid) * 5 + lane] : 0;
+  const int bv = lane < 2 ? a.bomb_mask[((size_t)g * P + pid) * 2 + lane] : 0;
+  const float uv = (a.uniforms && lane < 5) ? a.uniforms[(size_t)g * 5 + lane] : 0.0f;
+  const int reach_in = a.reach_mode != 0 ? *a.reach : 0;
+  if (!a.uniforms && lane < 2) {
+    float ub[4];
+    philox_block(a.seed, (uint32_t)g, a.tick, STREAM_BOT, (uint32_t)lane, ub);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) s.u[lane * 4 + q] = ub[q];
+  }
+  if (a.uniforms && lane < 5) s.u[lane] = uv;
+  if (lane < NPL) s.pl[lane] = plv;
+  if (lane < 5) s.mm[lane] = (uint8_t)mv;
+  if (lane < 2) s.bm[lane] = (uint8_t)bv;
+
+  // ---- cells, danger, cost, V_safe sources
+  float cst[KMAX];
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) {
+    const int c = lane + 64 * k;
+    cst[k] = INF;
     if (c < C) {
-      const uint32_t w = (uint32_t)a.cells[(size_t)g * C + c];
+      const uint32_t w = wreg[k];
       s.cw[c] = w;
-      const float d = __half2float(__ushort_as_half(obs[c]));
+      const float d = __half2float(__ushort_as_half(dreg[k]));
       s.dng[c] = d;
       const bool blocked = (w & (bot::F_WALL | bot::F_BRICK)) || bot::fuse_of(w) > 0;
-      s.cost[c] = blocked ? INF : 1.0f + 2.0f * d;
+      cst[k] = blocked ? INF : 1.0f + 2.0f * d;
       s.vs[c] = d < 0.35f ? 0.0f : INF;
       s.vo[c] = INF;
-      s.thr[0][c] = (bot::owner_of(w) == pid && bot::fuse_of(w) > 0) ? 1 : 0;
     }
   }
+
+  // ---- threat: the bot's live bombs dilated growth_blast_max times with the
+  // 4-neighbourhood, clipped at the border.  On a rectangle that is the set
+  // of cells within L1 distance growth_blast_max of such a bomb (a monotone
+  // path never leaves the bounding box), tested bomb by bomb.
+  {
+    const int gr = cf.growth_blast_max;
+    bool thr[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) thr[k] = false;
+#pragma unroll
+    for (int kb = 0; kb < KMAX; ++kb) {
+      const int cb = lane + 64 * kb;
+      const uint32_t wb = wreg[kb];
+      uint64_t m = __ballot(cb < C && bot::owner_of(wb) == pid && bot::fuse_of(wb) > 0);
+      while (m) {
+        const int b = 64 * kb + __builtin_ctzll(m);
+        m &= m - 1;
+        const int rb = b / W, colb = b % W;
+#pragma unroll
+        for (int k = 0; k < KMAX; ++k) {
+          const int c = lane + 64 * k;
+          const int r = c / W, col = c % W;
+          thr[k] |= abs(r - rb) + abs(col - colb) <= gr;
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      const int c = lane + 64 * k;
+      if (c < C) s.thr[c] = thr[k] ? 1 : 0;
+    }
+  }
+  wave_sync();
+
   // opponents' cells: a later opponent overwrites an earlier one's flag
   // (the reference assigns alive[o] per opponent in id order)
   if (lane == 0) {
     for (int o = 0; o < P; ++o) {
       if (o == pid) continue;
-      const float oy = __int_as_float(pl[o * QQT_P_SLOTS + QQT_P_Y]);
-      const float ox = __int_as_float(pl[o * QQT_P_SLOTS + QQT_P_X]);
+      const float oy = __int_as_float(s.pl[o * QQT_P_SLOTS + QQT_P_Y]);
+      const float ox = __int_as_float(s.pl[o * QQT_P_SLOTS + QQT_P_X]);
       const int ro = min(max((int)floorf(oy), 0), H - 1);
       const int co = min(max((int)floorf(ox), 0), W - 1);
-      s.vo[ro * W + co] = pl[o * QQT_P_SLOTS + QQT_P_ALIVE] ? 0.0f : INF;
+      s.vo[ro * W + co] = s.pl[o * QQT_P_SLOTS + QQT_P_ALIVE] ? 0.0f : INF;
     }
   }
-  __syncthreads();
+  wave_sync();
 
-  // ---- threat: the bot's live bombs dilated growth_blast_max times (4-neighbourhood)
-  int cur = 0;
-  for (int it = 0; it < cf.growth_blast_max; ++it) {
+  // ---- both cost fields, relaxed in place to their fixed point; each lane
+  // keeps its own cells' values in registers (only it writes them)
+  float vsr[KMAX], vor[KMAX];
 #pragma unroll
-    for (int k = 0; k < KMAX; ++k) {
-      const int c = lane + 64 * k;
-      if (c < C) {
-        const int r = c / W, col = c % W;
-        uint8_t v = s.thr[cur][c];
-        if (r > 0) v |= s.thr[cur][c - W];
-        if (r < H - 1) v |= s.thr[cur][c + W];
-        if (col > 0) v |= s.thr[cur][c - 1];
-        if (col < W - 1) v |= s.thr[cur][c + 1];
-        s.thr[cur ^ 1][c] = v;
-      }
-    }
-    cur ^= 1;
-    __syncthreads();
+  for (int k = 0; k < KMAX; ++k) {
+    const int c = lane + 64 * k;
+    vsr[k] = c < C ? s.vs[c] : INF;
+    vor[k] = c < C ? s.vo[c] : INF;
   }
-
-  // ---- both cost fields, relaxed in place to their fixed point
   for (int pass = 0; pass < 4 * C; ++pass) {
     bool changed = false;
 #pragma unroll
     for (int k = 0; k < KMAX; ++k) {
       const int c = lane + 64 * k;
-      if (c < C) {
-        const float cc = s.cost[c];
-        if (cc != INF) {
-          const int r = c / W, col = c % W;
-          float ns = INF, no = INF;
-          if (r > 0) { ns = fminf(ns, s.vs[c - W]); no = fminf(no, s.vo[c - W]); }
-          if (r < H - 1) { ns = fminf(ns, s.vs[c + W]); no = fminf(no, s.vo[c + W]); }
-          if (col > 0) { ns = fminf(ns, s.vs[c - 1]); no = fminf(no, s.vo[c - 1]); }
-          if (col < W - 1) { ns = fminf(ns, s.vs[c + 1]); no = fminf(no, s.vo[c + 1]); }
-          const float cs = ns + cc, co = no + cc;
-          if (cs < s.vs[c]) { s.vs[c] = cs; changed = true; }
-          if (co < s.vo[c]) { s.vo[c] = co; changed = true; }
-        }
+      const float cc = cst[k];
+      if (c < C && cc != INF) {
+        const int r = c / W, col = c % W;
+        float ns = INF, no = INF;
+        if (r > 0) { ns = fminf(ns, s.vs[c - W]); no = fminf(no, s.vo[c - W]); }
+        if (r < H - 1) { ns = fminf(ns, s.vs[c + W]); no = fminf(no, s.vo[c + W]); }
+        if (col > 0) { ns = fminf(ns, s.vs[c - 1]); no = fminf(no, s.vo[c - 1]); }
+        if (col < W - 1) { ns = fminf(ns, s.vs[c + 1]); no = fminf(no, s.vo[c + 1]); }
+        const float cs = ns + cc, co = no + cc;
+        if (cs < vsr[k]) { vsr[k] = cs; s.vs[c] = cs; changed = true; }
+        if (co < vor[k]) { vor[k] = co; s.vo[c] = co; changed = true; }
       }
     }
     if (__ballot(changed) == 0ull) break;
-    __syncthreads();
+    wave_sync();
   }
-  __syncthreads();
+  wave_sync();
 
   // ---- decision
+  const int32_t* pl = s.pl;
   const float by = __int_as_float(pl[pid * QQT_P_SLOTS + QQT_P_Y]);
   const float bx = __int_as_float(pl[pid * QQT_P_SLOTS + QQT_P_X]);
   const int r = min(max((int)floorf(by), 0), H - 1);
   const int c = min(max((int)floorf(bx), 0), W - 1);
   const bool alive = pl[pid * QQT_P_SLOTS + QQT_P_ALIVE] != 0;
   const int cap = pl[pid * QQT_P_SLOTS + QQT_P_BLAST_CAP];
-  const int reach = a.reach_mode != 0 ? *a.reach : cap;
+  const int reach = a.reach_mode != 0 ? reach_in : cap;
 
   // chain: a bomb with fuse 1..10 within `reach` cells in line (lane = step, direction)
   bool chain_l = false;
@@ -161,19 +219,9 @@ __global__ __launch_bounds__(64) void bot_kernel(const qqt_sim_config cf, const 
   const bool chain = __ballot(chain_l) != 0ull;
 
   if (lane == 0) {
-    float u[5];
-    if (a.uniforms) {
-#pragma unroll
-      for (int k = 0; k < 5; ++k) u[k] = a.uniforms[(size_t)g * 5 + k];
-    } else {
-      float u8[8];
-      philox_block(a.seed, (uint32_t)g, a.tick, STREAM_BOT, 0, u8);
-      philox_block(a.seed, (uint32_t)g, a.tick, STREAM_BOT, 1, u8 + 4);
-#pragma unroll
-      for (int k = 0; k < 5; ++k) u[k] = u8[k];
-    }
-    const uint8_t* mm = a.move_mask + ((size_t)g * P + pid) * 5;
-    const uint8_t* bm = a.bomb_mask + ((size_t)g * P + pid) * 2;
+    const float* u = s.u;
+    const uint8_t* mm = s.mm;
+    const uint8_t* bm = s.bm;
     const float own_dng = s.dng[r * W + c];
     int cell[5];
     cell[0] = max(r - 1, 0) * W + c;
@@ -188,7 +236,7 @@ __global__ __launch_bounds__(64) void bot_kernel(const qqt_sim_config cf, const 
     for (int k = 0; k < 5; ++k) {
       const uint32_t w = s.cw[cell[k]];
       legal[k] = mm[k] != 0 && !(w & (bot::F_WALL | bot::F_BRICK));
-      thr[k] = s.thr[cur][cell[k]] != 0;
+      thr[k] = s.thr[cell[k]] != 0;
       const float thf = thr[k] ? 1.0f : 0.0f;
       const float noise = 0.05f * u[k];
       dngc[k] = s.dng[cell[k]];
@@ -271,8 +319,17 @@ __global__ __launch_bounds__(1024) void reach_kernel(const int32_t* players, int
                                                      int pid, int32_t* out) {
   __shared__ int part[16];
   int v = INT_MIN;
-  for (int g = threadIdx.x; g < n; g += 1024)
-    v = max(v, players[((size_t)g * p + pid) * QQT_P_SLOTS + QQT_P_BLAST_CAP]);
+  // eight independent loads in flight per thread
+  for (int base = 0; base < n; base += 8 * 1024) {
+    int r[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int g = base + q * 1024 + (int)threadIdx.x;
+      r[q] = g < n ? players[((size_t)g * p + pid) * QQT_P_SLOTS + QQT_P_BLAST_CAP] : INT_MIN;
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v = max(v, r[q]);
+  }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = max(v, __shfl_xor(v, m, 64));
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
@@ -291,7 +348,9 @@ static int launch_bot(const qqt_sim_config* cfg, const qqt_bot_args* a, hipStrea
   if (a->reach_mode == 1)
     hipLaunchKernelGGL(reach_kernel, dim3(1), dim3(1024), 0, st, a->players, a->n_envs, P,
                        a->pid, a->reach);
-  hipLaunchKernelGGL((bot_kernel<H, W, P>), dim3(a->n_envs), dim3(64), 0, st, *cfg, *a);
+  constexpr int WPB = 2;  // two independent waves per workgroup (workgroup slots per CU)
+  hipLaunchKernelGGL((bot_kernel<H, W, P, WPB>), dim3((a->n_envs + WPB - 1) / WPB), dim3(64 * WPB),
+                     0, st, *cfg, *a);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     snprintf(g_err, sizeof(g_err), "bot launch failed: %s", hipGetErrorString(err));

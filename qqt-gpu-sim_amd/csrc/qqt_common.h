@@ -85,4 +85,14 @@ __device__ __forceinline__ float log_q(float x) {
   return (float)k * 0.6931471805599453f + lm;
 }
 
+// Sync point of a wavefront that works alone on its own LDS region: one
+// wavefront's LDS accesses are performed in program order, so the sync only
+// has to keep the compiler from moving memory operations across it
+// (wavefront-scope fences, no s_barrier and no wait for the LDS queue).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 }  // namespace qqt

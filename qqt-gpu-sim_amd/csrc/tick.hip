@@ -109,15 +109,6 @@ struct __align__(16) Lds {
 };
 
 // ---------------------------------------------------------------- lane helpers
-// A workgroup is exactly one wavefront: its LDS accesses are performed in
-// program order, so a sync point only has to keep the compiler from moving
-// memory operations across it (wavefront-scope fences, no s_barrier and no
-// wait for the LDS queue to drain).
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 template <int LPE>
 __device__ __forceinline__ int env_sum(int v) {
 #pragma unroll
