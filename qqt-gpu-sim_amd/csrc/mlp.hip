@@ -93,12 +93,16 @@ constexpr int HY_HALVES = 2 * ROWS * 3 * HEAD;  // hi + lo planes of the head la
 static_assert(HY_HALVES <= 4 * XT_HALVES + H_HALVES, "head layer reuses the x tiles and h1");
 static_assert(ROWS * HID * 2 <= 4 * XT_HALVES, "the second partial tile fits in the x tiles");
 
+constexpr int WF_HALVES = 3 * 64 * 16;          // output layer: 1 column tile x 3 K blocks
+constexpr int WF_CHUNKS = 2 * WF_HALVES / 8;    // 16-byte chunks of both planes
+
 struct __align__(16) MlpLds {
   uint16_t xs_h1[4 * XT_HALVES + H_HALVES];   // x tiles [group][buffer] | h1; later the head layer
   uint16_t h2[H_HALVES];
   float f[ROWS][FST];                         // fp32 pre-LayerNorm tile
   float vec[V_N];                             // biases and LayerNorm affine parameters
   float logit[ROWS][NOUT];
+  uint16_t wf[2][WF_HALVES];                  // output-layer B fragments, hi and lo planes
 };
 
 __device__ __forceinline__ uint16_t* h_at(uint16_t* base, int width, int plane, int row, int col) {
@@ -301,6 +305,15 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   const int vi0 = threadIdx.x, vi1 = threadIdx.x + NTHR;   // vi1 < V_N for the first 456
   const float vv0 = *vec_src(vi0);
   const float vv1 = vi1 < V_N ? *vec_src(vi1) : 0.0f;
+  // output-layer weights (both planes, 16-byte chunks t and t + NTHR)
+  static_assert(WF_CHUNKS <= 2 * NTHR && WF_CHUNKS > NTHR, "two chunks per thread");
+  auto wf_src = [&](int c) {
+    const int plane = c / (WF_HALVES / 8), i = c % (WF_HALVES / 8);
+    return reinterpret_cast<const uint4*>(plane ? a.wf_lo : a.wf) + i;
+  };
+  const int wc1 = threadIdx.x + NTHR;
+  const uint4 wfv0 = *wf_src(threadIdx.x);
+  const uint4 wfv1 = wc1 < WF_CHUNKS ? *wf_src(wc1) : make_uint4(0u, 0u, 0u, 0u);
 
   // ---------------- layer 1: group kg, K blocks kg, kg+2, ...; columns 32cg..32cg+31
   floatx4 acc[4][2];
@@ -399,6 +412,8 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
 
   s.vec[vi0] = vv0;
   if (vi1 < V_N) s.vec[vi1] = vv1;
+  reinterpret_cast<uint4*>(&s.wf[0][0])[threadIdx.x] = wfv0;
+  if (wc1 < WF_CHUNKS) reinterpret_cast<uint4*>(&s.wf[0][0])[wc1] = wfv1;
   store_x(xr[0], 0, kblk(0));
   load_x(min(kblk(PD), last), xr[0]);
   __syncthreads();
@@ -427,16 +442,24 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   const int rh = w >> 2;            // row half of the small layers
   load_split_b(w1b, a.w1, a.w1_lo, 2 * cg, lane);
   // The last loop step ended with a barrier, so the x tiles are free.
+  // (kg is uniform: one branch around both store loops)
+  if (kg == 0) {
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt)
+    for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
+      for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int row = 16 * rt + 4 * q + j, col = 32 * cg + 16 * ct + r16;
-        float* dstp = kg == 0 ? &s.f[row][col] : f1_at(s.xs_h1, row, col);
-        *dstp = acc[rt][ct][j];
-      }
+        for (int j = 0; j < 4; ++j)
+          s.f[16 * rt + 4 * q + j][32 * cg + 16 * ct + r16] = acc[rt][ct][j];
+  } else {
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          *f1_at(s.xs_h1, 16 * rt + 4 * q + j, 32 * cg + 16 * ct + r16) = acc[rt][ct][j];
+  }
   __syncthreads();
   layernorm_rows(s, s.xs_h1, V_B0, V_G1, V_BE1, H1);
   __syncthreads();
@@ -488,13 +511,11 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
 
   // ---------------- heads, output layer: 192 -> 8 (block diagonal); wavefronts 0-3: rows 16w..
   if (w < 4) {
-    SplitB<1, 3> wfb;
-    load_split_b(wfb, a.wf, a.wf_lo, 0, lane);
     floatx4 oac = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int kb = 0; kb < 3; ++kb) {
-      const Frag16& bh = wfb.hi[kb][0];
-      const Frag16& bl = wfb.lo[kb][0];
+      const Frag16 bh = load_b(&s.wf[0][(kb * 64 + lane) * 16]);
+      const Frag16 bl = load_b(&s.wf[1][(kb * 64 + lane) * 16]);
       const int row = 16 * w + r16;
       const Frag16 ah = read_a(HY, 3 * HEAD, row, kb, q);
       const Frag16 al = read_a(HY + ROWS * 3 * HEAD, 3 * HEAD, row, kb, q);
