@@ -18,8 +18,9 @@ Maps and weights are synthetic; everything is resident in HBM before timing.
 Prints ONE JSON line (rank 0).  `roofline` prices the dominant kernel against
 its bound: the tick kernel against HBM (algorithmic bytes per env-step below),
 the MLP kernel against dense float16 MFMA (algorithmic FLOP per env-step).
-Kernel durations come from HIP events recorded on the launch stream around
-both launches of every 8th step inside the timed region.  `traffic` is read from the committed
+Kernel durations come from HIP event pairs that the library records on the
+dispatch packets of both launches of every 8th step inside the timed region
+(hipExtLaunchKernel on the launch stream), i.e. kernel begin to kernel end.  `traffic` is read from the committed
 rocprofv3 FETCH_SIZE/WRITE_SIZE summary when one exists.  `cpu_baseline`
 times the oracle (the CPU restatement of the reference path) on the host
 cores over a bounded sample of the same workload.
@@ -54,6 +55,14 @@ MLP_FLOP_PER_ENV = 2 * 2 * (2366 * 128 + 128 * 128 + 3 * 128 * 64 + 64 * 8)
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_rollout_5632.json")
 EVERY = 8   # kernel durations are sampled on every 8th timed step
+
+from qqtsim import _capi  # noqa: E402  (C ABI loader; loads the library lazily)
+
+
+def kernel_ms():
+    """{kernel: mean ms per timed dispatch} of the launches armed since the
+    last call (each timed by an event pair on its own dispatch packet)."""
+    return {k: ms / c for k, (ms, c) in _capi.timing_collect().items()}
 
 
 def parse_args():
@@ -220,29 +229,21 @@ def main():
         roll.step()
     torch.cuda.synchronize()
 
-    # HIP events bracket both launches of every EVERY-th timed step (on the
-    # stream the kernels run on); sampling keeps their cost out of `value`.
-    stream = torch.cuda.current_stream(dev)
-    sampled = list(range(0, K, EVERY))
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in sampled]
+    # Both launches of every EVERY-th timed step carry a HIP event pair on
+    # their own dispatch packet (the stream they run on); sampling keeps the
+    # cost out of `value`.
+    _capi.timing_arm(0)          # creates the event pool outside the timed region
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    j = 0
     for k in range(K):
-        mark = k % EVERY == 0
-        if mark:
-            ev[j][0].record(stream)
+        if k % EVERY == 0:
+            _capi.timing_arm(2)
         roll.launch_act()
-        if mark:
-            ev[j][1].record(stream)
         roll.launch_tick()
-        if mark:
-            ev[j][2].record(stream)
-            j += 1
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
-    act_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / len(ev)
-    tick_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / len(ev)
+    kms = kernel_ms()
+    act_ms, tick_ms = kms["mlp_act_kernel"], kms["tick_kernel"]
     done_frac = float(roll.done.float().mean())
 
     if args.copy_calibrate:
@@ -324,21 +325,16 @@ def main_stress(args, torch, dev):
     for k in range(W):
         loop.launch_tick(acts[k])
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(0, K, EVERY)]
+    _capi.timing_arm(0)          # creates the event pool outside the timed region
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
-    j = 0
     for k in range(K):
-        mark = k % EVERY == 0
-        if mark:
-            ev[j][0].record(stream)
+        if k % EVERY == 0:
+            _capi.timing_arm(1)
         loop.launch_tick(acts[W + k])
-        if mark:
-            ev[j][1].record(stream)
-            j += 1
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
-    tick_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / len(ev)
+    tick_ms = kernel_ms()["tick_kernel"]
     if args.copy_calibrate:
         _calibration_copy(torch, dev)
     achieved = TICK_BYTES_PER_ENV * n / (tick_ms * 1e-3) / 1e9
@@ -431,27 +427,19 @@ def main_astar(args, torch, dev):
     for _ in range(W):
         roll.step()
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(0, K, EVERY)]
+    _capi.timing_arm(0)          # creates the event pool outside the timed region
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
-    j = 0
     for k in range(K):
-        mark = k % EVERY == 0
-        if not mark:
-            roll.step()
-            continue
-        e = ev[j]
-        j += 1
-        e[0].record(stream)
-        roll.launch_policy()
-        e[1].record(stream)
-        roll.launch_opponent()
-        e[2].record(stream)
-        roll.launch_tick()
-        e[3].record(stream)
+        if k % EVERY == 0:
+            _capi.timing_arm(4)          # policy, bot reach, bot, tick
+        roll.step()
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
-    us = [sum(e[i].elapsed_time(e[i + 1]) for e in ev) / len(ev) * 1e3 for i in range(3)]
+    kms = kernel_ms()
+    # the bot's share is its two launches (batch-max reach, then the bot)
+    us = [kms["mlp_act_kernel"] * 1e3, (kms["bot_kernel"] + kms.get("reach_kernel", 0.0)) * 1e3,
+          kms["tick_kernel"] * 1e3]
     kernels = {
         "mlp_act_kernel": {"us": us[0], "bound": "mfma",
                            "achieved": MLP_FLOP_PER_ENV / 2 * n / (us[0] * 1e-6) / 1e12,
@@ -551,16 +539,15 @@ def main_evalfwd(args, torch, dev):
     net._run(flat, 1, 0, False, logits=out)          # warm-up
     torch.cuda.synchronize()
     reps = max(1, args.steps // 64)
-    stream = torch.cuda.current_stream(dev)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _capi.timing_arm(0)
+    torch.cuda.synchronize()
     t1 = time.perf_counter()
-    e0.record(stream)
+    _capi.timing_arm(reps)
     for _ in range(reps):
         net._run(flat, 1, 0, False, logits=out)
-    e1.record(stream)
     torch.cuda.synchronize()
     el_fwd = (time.perf_counter() - t1) / reps
-    fwd_ms = e0.elapsed_time(e1) / reps
+    fwd_ms = kernel_ms()["mlp_act_kernel"]
     gbs = EVAL_BYTES_PER_ROW * rows / (fwd_ms * 1e-3) / 1e9
     tflops = EVAL_FLOP_PER_ROW * rows / (fwd_ms * 1e-3) / 1e12
     cpu = cpu_baseline_forward(cfg, 32768, args.seed, args.cpu_seconds) \

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 2
+#define QQT_ABI_VERSION 3
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -149,14 +149,20 @@ typedef struct qqt_bot_args {
   int32_t reach_mode;         /* chain-check reach: 0 = the bot's own blast cap;
                                  1 = the batch max of the bot's blast cap (the
                                  reference's rule), computed by this call into
-                                 *reach; 2 = the value already in *reach */
+                                 reach[reach_slot & 1]; 2 = the value already in
+                                 reach[0] */
+  int32_t reach_slot;         /* mode 1: reach is int32[2], both INT32_MIN before
+                                 the first call; call k passes slot k (any
+                                 counter that alternates): the call max-reduces
+                                 into reach[slot & 1] and resets the other slot
+                                 to INT32_MIN for the next call */
   const int32_t* cells;       /* sim state, layout above */
   const int32_t* players;
   const uint16_t* obs;        /* [N][5P+4][H][W] float16 bits */
   const uint8_t* move_mask;   /* [N][P][5] */
   const uint8_t* bomb_mask;   /* [N][P][2] */
   const float* uniforms;      /* [N][5] noise uniforms, or NULL = Philox stream 7 */
-  int32_t* reach;             /* device int32 scalar for reach_mode 1 and 2 */
+  int32_t* reach;             /* device int32[2] (mode 1) or scalar (mode 2) */
   int64_t* actions;           /* [N][P][2], slot pid written; or NULL */
   int8_t* actions_i8;         /* same as int8; or NULL */
 } qqt_bot_args;
@@ -184,6 +190,20 @@ int qqt_mlp_act(const qqt_mlp_args* args, void* stream);
  * two _dijkstra_field cost fields (:179-238); the 0.05 * torch.rand(n, 5)
  * noise (:355) comes from `uniforms` or the Philox stream. */
 int qqt_bot_act(const qqt_sim_config* cfg, const qqt_bot_args* args, void* stream);
+
+/* Dispatch timing for benchmark harnesses (no counterpart in the reference:
+ * its bench times whole steps with host clocks).  qqt_timing_arm(n) times
+ * the next n kernel launches made through this library: each records a
+ * start/stop event pair on its own dispatch packet (hipExtLaunchKernel), so
+ * the pair spans that kernel alone.  qqt_timing_collect waits for the timed
+ * launches, writes per kernel kind (QQT_KERNEL_*, n_kinds entries) the
+ * summed duration in ms and the number of timed launches, and disarms.  At
+ * most 4096 launches are timed between collects.  Allocates no device
+ * memory (the event pool is created by the first arm). */
+enum { QQT_KERNEL_TICK = 0, QQT_KERNEL_MLP = 1, QQT_KERNEL_BOT = 2, QQT_KERNEL_REACH = 3,
+       QQT_KERNEL_KINDS = 4 };
+int qqt_timing_arm(int32_t launches);
+int qqt_timing_collect(double* ms, int32_t* count, int32_t n_kinds);
 
 #ifdef __cplusplus
 }

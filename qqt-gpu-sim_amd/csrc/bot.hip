@@ -85,7 +85,8 @@ __global__ __launch_bounds__(64 * WPB) void bot_kernel(const qqt_sim_config cf, 
   const int mv = lane < 5 ? a.move_mask[((size_t)g * P + pid) * 5 + lane] : 0;
   const int bv = lane < 2 ? a.bomb_mask[((size_t)g * P + pid) * 2 + lane] : 0;
   const float uv = (a.uniforms && lane < 5) ? a.uniforms[(size_t)g * 5 + lane] : 0.0f;
-  const int reach_in = a.reach_mode != 0 ? *a.reach : 0;
+  const int reach_in = a.reach_mode == 1 ? a.reach[a.reach_slot & 1]
+                       : a.reach_mode == 2 ? a.reach[0] : 0;
   if (!a.uniforms && lane < 2) {
     float ub[4];
     philox_block(a.seed, (uint32_t)g, a.tick, STREAM_BOT, (uint32_t)lane, ub);
@@ -314,30 +315,26 @@ __global__ __launch_bounds__(64 * WPB) void bot_kernel(const qqt_sim_config cf, 
 }
 
 // Batch max of the bot's blast cap (the chain-check reach of the reference,
-// `int(cap.max().item())`): one workgroup strides over the envs.
-__global__ __launch_bounds__(1024) void reach_kernel(const int32_t* players, int n, int p,
-                                                     int pid, int32_t* out) {
-  __shared__ int part[16];
-  int v = INT_MIN;
-  // eight independent loads in flight per thread
-  for (int base = 0; base < n; base += 8 * 1024) {
-    int r[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int g = base + q * 1024 + (int)threadIdx.x;
-      r[q] = g < n ? players[((size_t)g * p + pid) * QQT_P_SLOTS + QQT_P_BLAST_CAP] : INT_MIN;
-    }
-#pragma unroll
-    for (int q = 0; q < 8; ++q) v = max(v, r[q]);
-  }
+// `int(cap.max().item())`): one env per thread, a workgroup max, then one
+// atomic max per workgroup into out[slot].  Workgroup 0 also resets the
+// other slot, which the next call reduces into; the bot kernel that follows
+// in stream order reads out[slot].
+constexpr int REACH_THREADS = 256;
+__global__ __launch_bounds__(REACH_THREADS) void reach_kernel(const int32_t* players, int n, int p,
+                                                              int pid, int32_t* out, int slot) {
+  __shared__ int part[REACH_THREADS / 64];
+  const int g = blockIdx.x * REACH_THREADS + (int)threadIdx.x;
+  int v = g < n ? players[((size_t)g * p + pid) * QQT_P_SLOTS + QQT_P_BLAST_CAP] : INT_MIN;
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = max(v, __shfl_xor(v, m, 64));
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
   __syncthreads();
   if (threadIdx.x == 0) {
     int r = part[0];
-    for (int i = 1; i < 16; ++i) r = max(r, part[i]);
-    *out = r;
+#pragma unroll
+    for (int i = 1; i < REACH_THREADS / 64; ++i) r = max(r, part[i]);
+    atomicMax(&out[slot & 1], r);
+    if (blockIdx.x == 0) out[(slot & 1) ^ 1] = INT_MIN;
   }
 }
 
@@ -346,11 +343,11 @@ extern thread_local char g_err[512];
 template <int H, int W, int P>
 static int launch_bot(const qqt_sim_config* cfg, const qqt_bot_args* a, hipStream_t st) {
   if (a->reach_mode == 1)
-    hipLaunchKernelGGL(reach_kernel, dim3(1), dim3(1024), 0, st, a->players, a->n_envs, P,
-                       a->pid, a->reach);
+    QQT_LAUNCH(QQT_KERNEL_REACH, reach_kernel, dim3((a->n_envs + REACH_THREADS - 1) / REACH_THREADS),
+               dim3(REACH_THREADS), st, a->players, a->n_envs, P, a->pid, a->reach, a->reach_slot);
   constexpr int WPB = 2;  // two independent waves per workgroup (workgroup slots per CU)
-  hipLaunchKernelGGL((bot_kernel<H, W, P, WPB>), dim3((a->n_envs + WPB - 1) / WPB), dim3(64 * WPB),
-                     0, st, *cfg, *a);
+  QQT_LAUNCH(QQT_KERNEL_BOT, (bot_kernel<H, W, P, WPB>), dim3((a->n_envs + WPB - 1) / WPB),
+             dim3(64 * WPB), st, *cfg, *a);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     snprintf(g_err, sizeof(g_err), "bot launch failed: %s", hipGetErrorString(err));
@@ -376,7 +373,7 @@ int qqt_bot_act(const qqt_sim_config* cfg, const qqt_bot_args* a, void* stream) 
     return QQT_E_ARG;
   }
   if (a->reach_mode < 0 || a->reach_mode > 2 || (a->reach_mode != 0 && !a->reach)) {
-    snprintf(g_err, sizeof(g_err), "qqt_bot_act: reach_mode 1/2 needs a reach scalar");
+    snprintf(g_err, sizeof(g_err), "qqt_bot_act: reach_mode 1/2 needs a reach buffer");
     return QQT_E_ARG;
   }
   if (a->pid < 0 || a->pid >= cfg->n_players || cfg->growth_blast_max < 0 ||

@@ -598,7 +598,7 @@ int qqt_mlp_act(const qqt_mlp_args* a, void* stream) {
   // XCDs round robin with both players' workgroups adjacent on one XCD
   const int nrb = (a->batch + ROWS - 1) / ROWS;
   const int blocks = ((nrb + 7) / 8) * 8 * a->npid;
-  hipLaunchKernelGGL(mlp_act_kernel, dim3(blocks), dim3(NTHR), 0, (hipStream_t)stream, *a);
+  QQT_LAUNCH(QQT_KERNEL_MLP, mlp_act_kernel, dim3(blocks), dim3(NTHR), (hipStream_t)stream, *a);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     snprintf(g_err, sizeof(g_err), "mlp launch failed: %s", hipGetErrorString(err));

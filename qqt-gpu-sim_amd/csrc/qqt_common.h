@@ -1,6 +1,7 @@
 // Shared device helpers: Philox4x32-10, unit uniforms, the sampler's exp/log.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -84,6 +85,21 @@ __device__ __forceinline__ float log_q(float x) {
   const float lm = 2.0f * (s * q);
   return (float)k * 0.6931471805599453f + lm;
 }
+
+// Dispatch timing (timing.hip): true, with an event pair, when the next
+// launch of kernel kind `kind` (QQT_KERNEL_*) is to be timed.
+bool timing_take(int kind, hipEvent_t* e0, hipEvent_t* e1);
+
+// Kernel launch that records a start/stop event pair on the dispatch packet
+// itself (hipExtLaunchKernel) when timing is armed.
+#define QQT_LAUNCH(kind, kernel, grid, block, stream, ...)                              \
+  do {                                                                                  \
+    hipEvent_t qqt_e0_, qqt_e1_;                                                        \
+    if (::qqt::timing_take((kind), &qqt_e0_, &qqt_e1_))                                 \
+      hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, qqt_e0_, qqt_e1_, 0, __VA_ARGS__); \
+    else                                                                                \
+      hipLaunchKernelGGL(kernel, grid, block, 0, stream, __VA_ARGS__);                  \
+  } while (0)
 
 // Sync point of a wavefront that works alone on its own LDS region: one
 // wavefront's LDS accesses are performed in program order, so the sync only

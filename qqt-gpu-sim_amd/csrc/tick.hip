@@ -1019,7 +1019,8 @@ int launch(const qqt_sim_config* cfg, const qqt_tick_args* a, hipStream_t st) {
   constexpr int EPW = 64 / LPE;
   const int waves = (a->n_envs + EPW - 1) / EPW;
   const int blocks = (waves + WPB - 1) / WPB;
-  hipLaunchKernelGGL((tick_kernel<H, W, P, LPE, WPB>), dim3(blocks), dim3(64 * WPB), 0, st, *cfg, *a);
+  QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB>), dim3(blocks), dim3(64 * WPB), st, *cfg,
+             *a);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     snprintf(g_err, sizeof(g_err), "tick launch failed: %s", hipGetErrorString(err));

@@ -14,7 +14,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 
 from ._build import LIB
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 MODE_STEP, MODE_OBSERVE, MODE_RESET, MODE_PROBE = 0, 1, 2, 3
 
@@ -61,7 +61,7 @@ class MlpArgsC(ctypes.Structure):
 
 class BotArgsC(ctypes.Structure):
     _fields_ = [("n_envs", _i32), ("pid", _i32), ("seed", _u64), ("tick", _u32),
-                ("reach_mode", _i32)] + [
+                ("reach_mode", _i32), ("reach_slot", _i32)] + [
         (n, _vp) for n in ("cells", "players", "obs", "move_mask", "bomb_mask", "uniforms",
                            "reach", "actions", "actions_i8")]
 
@@ -85,10 +85,33 @@ def lib():
         L.qqt_mlp_act.argtypes = [ctypes.POINTER(MlpArgsC), _vp]
         L.qqt_bot_act.restype = ctypes.c_int
         L.qqt_bot_act.argtypes = [ctypes.POINTER(SimConfigC), ctypes.POINTER(BotArgsC), _vp]
+        L.qqt_timing_arm.restype = ctypes.c_int
+        L.qqt_timing_arm.argtypes = [_i32]
+        L.qqt_timing_collect.restype = ctypes.c_int
+        L.qqt_timing_collect.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i32), _i32]
         if L.qqt_abi_version() != ABI_VERSION:
             raise RuntimeError("libqqt_hip.so ABI version mismatch; rebuild it")
         _LIB = L
     return _LIB
+
+
+KERNEL_KINDS = ("tick_kernel", "mlp_act_kernel", "bot_kernel", "reach_kernel")  # QQT_KERNEL_*
+
+
+def timing_arm(launches: int) -> None:
+    """Time the next `launches` kernel launches of the library (each on its
+    own dispatch packet)."""
+    check(lib().qqt_timing_arm(int(launches)))
+
+
+def timing_collect() -> dict:
+    """{kernel name: (summed ms, timed launches)} of the armed launches since
+    the last collect (waits for them)."""
+    n = len(KERNEL_KINDS)
+    ms = (ctypes.c_double * n)()
+    cnt = (ctypes.c_int32 * n)()
+    check(lib().qqt_timing_collect(ms, cnt, n))
+    return {k: (ms[i], cnt[i]) for i, k in enumerate(KERNEL_KINDS) if cnt[i]}
 
 
 def check(rc: int) -> None:

@@ -36,7 +36,9 @@ class HipAstarBot:
         self.tick = 0
         self._lib = _capi.lib()
         self._stream = _capi.stream_handle(sim.device)
-        self._reach = torch.zeros((), dtype=torch.int32, device=sim.device)
+        # two reach slots (the batch-max reduction alternates between them)
+        self._reach = torch.full((2,), -2 ** 31, dtype=torch.int32, device=sim.device)
+        self._calls = 0
         self._out = torch.zeros((sim.num_envs, sim.cfg.n_players, 2), dtype=torch.int64,
                                 device=sim.device)
         b = _capi.BotArgsC()
@@ -59,6 +61,8 @@ class HipAstarBot:
         self.sim._refresh()
         b = self._args
         b.tick = self.tick & 0xFFFFFFFF
+        b.reach_slot = self._calls & 1
+        self._calls += 1
         b.uniforms = None
         b.actions = actions.data_ptr() if actions.dtype == torch.int64 else None
         b.actions_i8 = actions.data_ptr() if actions.dtype == torch.int8 else None
@@ -86,6 +90,8 @@ class HipAstarBot:
         u = None if uniforms is None else uniforms.to(sim.device, torch.float32).contiguous()
         b.obs, b.move_mask, b.bomb_mask = obs_t.data_ptr(), mm.data_ptr(), bm.data_ptr()
         b.tick = self.tick & 0xFFFFFFFF
+        b.reach_slot = self._calls & 1
+        self._calls += 1
         b.uniforms = _capi.ptr(u)
         b.actions, b.actions_i8 = self._out.data_ptr(), None
         try:

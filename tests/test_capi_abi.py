@@ -40,7 +40,8 @@ def _declared_functions():
 
 def test_header_declares_the_entry_points():
     assert _declared_functions() == ["qqt_abi_version", "qqt_bot_act", "qqt_last_error",
-                                     "qqt_mlp_act", "qqt_tick"]
+                                     "qqt_mlp_act", "qqt_tick", "qqt_timing_arm",
+                                     "qqt_timing_collect"]
 
 
 def test_library_exports_every_declared_symbol():
@@ -219,8 +220,8 @@ def _bot_args(**kw):
     (dict(actions=None), "null pointer or empty"),
     (dict(pid=2), "bad player id"),
     (dict(pid=-1), "bad player id"),
-    (dict(reach_mode=1), "reach scalar"),
-    (dict(reach_mode=3, reach=0x9000), "reach scalar"),
+    (dict(reach_mode=1), "reach buffer"),
+    (dict(reach_mode=3, reach=0x9000), "reach buffer"),
 ])
 def test_bot_rejects_bad_arguments(lib, kw, msg):
     assert lib.qqt_bot_act(_cfg(), _bot_args(**kw), None) == -1
@@ -229,6 +230,30 @@ def test_bot_rejects_bad_arguments(lib, kw, msg):
 
 def test_bot_unsupported_grid(lib):
     assert lib.qqt_bot_act(_cfg(height=11, width=11), _bot_args(), None) == -3
+
+
+def test_timing_rejects_bad_arguments(lib):
+    import ctypes as ct
+
+    assert lib.qqt_timing_arm(-1) == -1
+    assert lib.qqt_timing_arm(4097) == -1
+    assert b"launches" in lib.qqt_last_error()
+    ms, cnt = (ct.c_double * 4)(), (ct.c_int32 * 4)()
+    assert lib.qqt_timing_collect(None, cnt, 4) == -1
+    assert lib.qqt_timing_collect(ms, cnt, 0) == -1
+    # nothing armed or taken: collect succeeds without touching a device
+    assert lib.qqt_timing_collect(ms, cnt, 4) == 0
+    assert list(cnt) == [0, 0, 0, 0]
+
+
+def test_header_kernel_kinds_match_host_mirror():
+    from qqtsim import _capi
+
+    text = open(HEADER).read()
+    kinds = dict((k, int(v)) for k, v in re.findall(r"\bQQT_KERNEL_(\w+) = (\d+)", text))
+    assert kinds["KINDS"] == len(_capi.KERNEL_KINDS)
+    for name in ("TICK", "MLP", "BOT", "REACH"):
+        assert _capi.KERNEL_KINDS[kinds[name]].startswith(name.lower()), name
 
 
 def test_errors_raise_in_python(lib):

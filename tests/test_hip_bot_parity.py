@@ -93,3 +93,33 @@ def test_learner_vs_bot_rollout_matches_oracle(dev):
                                           err_msg=f"{k} tick {t}")
     assert moved > 0
     print(f"learner vs bot: {ticks} ticks x {n} envs, bot moves {moved}, placements {placed}")
+
+
+def test_hip_bot_reach_follows_the_batch_from_call_to_call(dev):
+    """The batch-max reach is recomputed on every call (two alternating
+    reduction slots): on the hand-built chain states (batch max 5) the bot
+    places as the reference does, after lowering every cap to 2 it acts as
+    the oracle with reach 2 (which differs), and back at 5 it matches again."""
+    from oracle.bots import astar_act
+    from qqtsim import HipAstarBot, HipBatchedSim, MapSpec, corridor_training_config
+
+    z = np.load(f"{GOLDEN}/astar_chain.npz")
+    n = z["bot"].shape[1]
+    cfg = corridor_training_config()
+    sim = HipBatchedSim(cfg, n, device=dev, seed=0, map_spec=MapSpec(kind="open"))
+    bot = HipAstarBot(sim, pid=1)
+    base = {k: torch.from_numpy(np.ascontiguousarray(z[k][0]))
+            for k in ("wall", "brick", "fuse", "owner", "pos", "alive", "blast_cap")}
+    low = dict(base)
+    low["blast_cap"] = base["blast_cap"].clone()
+    low["blast_cap"][:, 1] = 2
+    inputs = (torch.from_numpy(z["obs"][0]), torch.from_numpy(z["mm1"][0]),
+              torch.from_numpy(z["bm1"][0]))
+    u = torch.from_numpy(z["u"][0])
+    want_low = astar_act(cfg, low, *inputs, 1, u, reach=2)
+    assert not np.array_equal(want_low.numpy(), z["bot"][0])
+    for rep in range(2):
+        for state, want in ((base, z["bot"][0]), (low, want_low.numpy())):
+            sim.load_state_dict(state)
+            got = bot.act(*inputs, 1, uniforms=u)
+            np.testing.assert_array_equal(got.cpu().numpy(), want, err_msg=f"rep {rep}")
