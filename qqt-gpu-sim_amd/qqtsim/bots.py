@@ -1,11 +1,12 @@
 """`HipAstarBot`: the reference's astar rule bot on the MI355X kernel.
 
-Drop-in for `partial(astar_attack)` wrapped by `BotWrapper` (sim/bots.py:
-267-508, :511-545) for the learner-vs-bot rollout: `act(obs, mmask, bmask,
-pid)` returns (N, 2) int64 actions like the reference bot, computed by one
-`qqt_bot_act` launch that reads the sim's device state directly.  Behaviour
-modes and crate eating are not on this path (the reference's defaults for
-the astar opponent are modes off, `eat_crates=False`).
+Drop-in for `make_bot(sim, "astar", mode=False)` (sim/bots.py:538-560: the
+`astar_attack` policy of :267-508 in a `BotWrapper`, :511-535, without the
+approach/flee mode ticker) for the learner-vs-bot rollout: `act(obs, mmask,
+bmask, pid)` returns (N, 2) int64 actions like the reference bot, computed by
+one `qqt_bot_act` call that reads the sim's device state directly.  The mode
+ticker of `mode=True` and the crate-eating layer (`eat_crates=True`, the
+"hunter" bot) are not on this path.
 
 The noise uniforms come from Philox (stream 7, keyed by env and this bot's
 call counter) unless `uniforms=(N, 5)` is passed.  The chain check reaches
