@@ -65,6 +65,38 @@ __device__ __forceinline__ float bomb_weight(int f, float fuse_max) {
 __device__ __forceinline__ int dir_dr(int d) { return d == 0 ? -1 : (d == 1 ? 1 : 0); }
 __device__ __forceinline__ int dir_dc(int d) { return d == 2 ? -1 : (d == 3 ? 1 : 0); }
 
+// Walk up to `len` steps from `src` in direction sgn * d, four cells per LDS
+// round trip: the cell words of the next four steps are loaded together
+// (out-of-grid steps read as a plain wall), then step(k, x, w) runs for
+// k = 1, 2, ... in registers until it returns false.  Most rays end within
+// the first four cells.
+template <int H, int W, class F>
+__device__ __forceinline__ void walk_ray(const uint32_t* cw, int src, int d, int len, int sgn,
+                                         F&& step) {
+  constexpr int KR = (H > W ? H : W) - 1;   // longest ray inside the grid
+  constexpr int CH = 4;
+  const int r0 = src / W, c0 = src % W, dr = sgn * dir_dr(d), dc = sgn * dir_dc(d);
+  const int n = min(len, KR);
+  for (int k0 = 1; k0 <= n; k0 += CH) {
+    uint32_t w[CH];
+    int x[CH];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int k = k0 + i, rr = r0 + k * dr, cc = c0 + k * dc;
+      const bool in = k <= n && rr >= 0 && rr < H && cc >= 0 && cc < W;
+      const int xx = in ? rr * W + cc : src;
+      const uint32_t v = cw[xx];
+      x[i] = xx;
+      w[i] = in ? v : F_WALL;
+    }
+    bool go = true;
+#pragma unroll
+    for (int i = 0; i < CH; ++i)
+      if (go) go = step(k0 + i, x[i], w[i]);
+    if (!go) break;
+  }
+}
+
 template <int H, int W, int P, int LPE_>
 struct Geo {
   static constexpr int LPE = LPE_;
@@ -421,24 +453,20 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
     wave_sync();
 
     // ---- 6. explosions (sim/blast.py:101-155), fixed synchronous rounds
-    auto fire = [&](int src) {  // rays of one seed cell into cov
-      const uint32_t w = cw[src];
-      if (w & (F_WALL | F_BRICK)) return;
-      const int b = blast_of(w, cf.blast);
-      if (b > a.resolve_tiers) return;
-      const int r0 = src / W, c0 = src % W;
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const int dr = dir_dr(d), dc = dir_dc(d);
-        for (int k = 1; k <= b; ++k) {
-          const int rr = r0 + k * dr, cc = c0 + k * dc;
-          if (rr < 0 || rr >= H || cc < 0 || cc >= W) break;
-          const int x = rr * W + cc;
-          const uint32_t wx = cw[x];
-          if (wx & F_WALL) break;
+    // rays of the list entries whose trigger stamp is `stamp`, one
+    // (entry, direction) per lane: walls stop a ray before the cell, other
+    // solids after it
+    auto fire = [&](uint8_t stamp) {
+      for (int it = l; it < 4 * nl; it += LPE) {
+        const int src = list[it >> 2], d = it & 3;
+        const uint32_t w = cw[src];
+        const int b = blast_of(w, cf.blast);
+        if (trg[src] != stamp || (w & (F_WALL | F_BRICK)) || b > a.resolve_tiers) continue;
+        walk_ray<H, W>(cw, src, d, b, 1, [&](int, int x, uint32_t wx) {
+          if (wx & F_WALL) return false;
           cov[x] = 1;
-          if (cw_solid(wx)) break;
-        }
+          return !cw_solid(wx);
+        });
       }
     };
     bool boom = false;
@@ -454,29 +482,24 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
     const bool env_boom = env_bits<LPE>(boom, e) != 0;
     wave_sync();
     if (__any(env_boom)) {
-      for (int j = l; j < nl; j += LPE) {
-        const int c = list[j];
-        if (trg[c]) fire(c);
-      }
+      fire(1);
+      // chain rounds: entries triggered in round r carry stamp r + 2 (any
+      // nonzero stamp means triggered), so the rays of one round are spread
+      // over all lanes
       const int rounds = min(cf.max_chain - 1, cf.chain_cap_rounds);
       for (int r = 0; r < rounds; ++r) {
         wave_sync();
-        uint32_t newly = 0;  // bit i: list entry l + LPE*i
-        int i = 0;
-        for (int j = l; j < nl; j += LPE, ++i) {
+        bool newly = false;
+        for (int j = l; j < nl; j += LPE) {
           const int c = list[j];
-          if (cw_fuse(cw[c]) > 0 && cov[c] && !trg[c]) newly |= 1u << (i & 31);
-        }
-        if (!__any(newly != 0)) break;
-        wave_sync();
-        i = 0;
-        for (int j = l; j < nl; j += LPE, ++i) {
-          if (newly & (1u << (i & 31))) {
-            const int c = list[j];
-            trg[c] = 1;
-            fire(c);
+          if (cw_fuse(cw[c]) > 0 && cov[c] && !trg[c]) {
+            trg[c] = (uint8_t)(r + 2);
+            newly = true;
           }
         }
+        if (!__any(newly)) break;
+        wave_sync();
+        fire((uint8_t)(r + 2));
       }
       wave_sync();
       // ---- 7. burnt bricks (corridor: into crates)
@@ -647,19 +670,14 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
           const int c = list[j];
           uint16_t ed = 0;
           if (!(cw[c] & F_WALL)) {
-            const int r0 = c / W, c0 = c % W;
-            const int dr = dir_dr(d), dc = dir_dc(d);
-            for (int k = 1; k < (H > W ? H : W); ++k) {
-              const int rr = r0 - k * dr, cc = c0 - k * dc;
-              if (rr < 0 || rr >= H || cc < 0 || cc >= W) break;
-              const int u = rr * W + cc;
-              const uint32_t wu = cw[u];
+            // backwards from the bomb: the first solid cell behind it
+            walk_ray<H, W>(cw, c, d, H + W, -1, [&](int k, int u, uint32_t wu) {
               if (cw_fuse(wu) > 0) {
                 if (blast_of(wu, cf.blast) >= k) ed = (uint16_t)(u | (k << 8));
-                break;
+                return false;
               }
-              if (wu & (F_WALL | F_BRICK)) break;
-            }
+              return !(wu & (F_WALL | F_BRICK));
+            });
           }
           s.dz.edge[e][j][d] = ed;
         }
@@ -708,18 +726,11 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
         const float v = wl[j];
         if (wc & F_WALL) continue;
         if (d == 0) atomicMax(&dngi[c], __float_as_int(v));  // the bomb's own cell (seed)
-        const int b = blast_of(wc, cf.blast);
-        const int r0 = c / W, c0 = c % W;
-        const int dr = dir_dr(d), dc = dir_dc(d);
-        for (int k = 1; k <= b; ++k) {
-          const int rr = r0 + k * dr, cc = c0 + k * dc;
-          if (rr < 0 || rr >= H || cc < 0 || cc >= W) break;
-          const int x = rr * W + cc;
-          const uint32_t wx = cw[x];
-          if (wx & F_WALL) break;
+        walk_ray<H, W>(cw, c, d, blast_of(wc, cf.blast), 1, [&](int, int x, uint32_t wx) {
+          if (wx & F_WALL) return false;
           atomicMax(&dngi[x], __float_as_int(v));
-          if (cw_solid(wx)) break;
-        }
+          return !cw_solid(wx);
+        });
       }
     }
     wave_sync();
@@ -1052,6 +1063,8 @@ int qqt_tick(const qqt_sim_config* cfg, const qqt_tick_args* a, void* stream) {
   if (a->mode == QQT_MODE_PROBE && !a->probe_out) return fail(QQT_E_ARG, "PROBE needs probe_out");
   if (a->obs && (((uintptr_t)a->obs) & 15)) return fail(QQT_E_ARG, "obs must be 16-byte aligned");
   if (cfg->fuse < 1 || cfg->fuse > 255) return fail(QQT_E_ARG, "fuse must be in 1..255");
+  if (cfg->chain_cap_rounds < 0 || cfg->chain_cap_rounds > 64)
+    return fail(QQT_E_ARG, "chain_cap_rounds must be in 0..64");
   if (cfg->bombs_lo > cfg->bombs_hi || cfg->blast_lo > cfg->blast_hi)
     return fail(QQT_E_ARG, "bad cap ranges");
   hipStream_t st = (hipStream_t)stream;
