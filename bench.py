@@ -74,13 +74,15 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="CPU work budget of the cpu_baseline sample (0 = skip)")
-    ap.add_argument("--workload", choices=("rollout", "stress", "astar", "evalfwd"),
+    ap.add_argument("--workload", choices=("rollout", "stress", "astar", "evalfwd", "collect"),
                     default="rollout",
                     help="rollout: the headline self-play rollout (default); stress: "
                          "16384-env bomb-stress ticks with injected actions; astar: "
                          "learner (MLP) vs the astar bot, 5632 envs; evalfwd: 32768-env x "
                          "128-tick rollout into the observation slab, then the batched "
-                         "evaluation forward over all 4.19M observations")
+                         "evaluation forward over all 4.19M observations; collect: "
+                         "128-step self-play collects into the device rollout buffer "
+                         "(5632 envs) + last-value forward + GAE")
     ap.add_argument("--copy-calibrate", action="store_true",
                     help="after timing, run a 512 MiB device copy (HBM counter calibration)")
     return ap.parse_args()
@@ -223,6 +225,8 @@ def main():
         return main_astar(args, torch, dev)
     if args.workload == "evalfwd":
         return main_evalfwd(args, torch, dev)
+    if args.workload == "collect":
+        return main_collect(args, torch, dev)
     n, K, W = args.envs, args.steps, args.warmup
     cfg, spec, roll = build_workload(n, args.seed, dev)
     for _ in range(W):
@@ -575,6 +579,131 @@ def main_evalfwd(args, torch, dev):
     }
     print(json.dumps(res), flush=True)
 
+
+
+# Algorithmic bytes of the GAE scan per (step, env): reward, value, done read,
+# advantage and return written.
+GAE_BYTES = 4 + 4 + 1 + 4 + 4
+COLLECT_T = 128
+
+
+def cpu_baseline_collect(cfg, spec, n, seed, budget_s):
+    """The oracle's collect loop on the host cores: env-steps (observe,
+    masks, both players' forward + sampling, step) appended to host lists,
+    then the oracle's GAE over the sampled steps."""
+    import numpy as np
+    import torch
+
+    from oracle import philox
+    from oracle.policy import mlp_forward, sample_masked
+    from oracle.ppo import gae
+    from oracle.sim import OracleSim
+    from qqtsim.policy import default_init
+
+    cores = _cores(torch)
+    params = default_init(cfg.obs_shape)
+    sim = OracleSim(cfg, n, spec, seed=seed)
+    envs = np.arange(n)
+    rec = {k: [] for k in ("obs", "mm", "bm", "act", "val", "rew", "done")}
+
+    def env_step(t):
+        obs = sim.observe()
+        mm, bm = sim.legal_mask()
+        u = philox.uniforms(seed, envs, t, philox.STREAM_POLICY, 4)
+        acts = torch.zeros((n, 2, 2), dtype=torch.int64)
+        v0 = None
+        for pid in range(2):
+            ml, bl, v = mlp_forward(params, obs, pid)
+            v0 = v if pid == 0 else v0
+            acts[:, pid, 0] = torch.from_numpy(
+                sample_masked(ml.numpy(), mm[:, pid].numpy(), u[:, 2 * pid])[0])
+            acts[:, pid, 1] = torch.from_numpy(
+                sample_masked(bl.numpy(), bm[:, pid].numpy(), u[:, 2 * pid + 1])[0])
+        rew, done, _ = sim.step(acts, auto_reset=True)
+        for k, x in (("obs", obs), ("mm", mm[:, 0]), ("bm", bm[:, 0]), ("act", acts[:, 0]),
+                     ("val", v0), ("rew", rew[:, 0]), ("done", done)):
+            rec[k].append(np.array(x))
+
+    env_step(0)
+    for k in rec:
+        rec[k].clear()
+    ticks, t0 = 0, time.perf_counter()
+    while True:
+        env_step(1 + ticks)
+        ticks += 1
+        if time.perf_counter() - t0 >= budget_s or ticks >= COLLECT_T:
+            break
+    last = mlp_forward(params, sim.observe(), 0)[2].numpy()
+    gae(np.stack(rec["rew"]), np.stack(rec["val"]), np.stack(rec["done"]).astype(np.float32),
+        last, 0.995, 0.95)
+    el = time.perf_counter() - t0
+    return {"value": n * ticks / el, "unit": "env-steps/s", "cores": cores, "kind": "port",
+            "sample": f"oracle (torch CPU restatement) collect loop, {n} envs x {ticks} "
+                      f"steps into host buffers + GAE, after 1 warm-up step, {el:.1f} s"}
+
+
+def main_collect(args, torch, dev):
+    """Self-play collects into the device rollout buffer: 5632 envs x 128
+    steps per collect (observation slab, masks, actions, log-probs, values,
+    rewards, done and damage flags written by the kernels in place), then the
+    learner's value of the final observation and the GAE scan
+    (train/ppo.py:197-314, :101-110).  `--steps` counts env-steps per env
+    (rounded up to whole collects)."""
+    from qqtsim import HipRolloutBuffer, compute_gae
+
+    n, W = args.envs, args.warmup
+    reps = max(1, -(-args.steps // COLLECT_T))
+    cfg, spec, roll = build_workload(n, args.seed, dev)
+    for _ in range(W):
+        roll.step()
+    buf = HipRolloutBuffer(COLLECT_T, n, cfg.obs_shape, dev)
+    roll.collect(buf)                                    # warm-up collect
+    net = roll.policy
+    compute_gae(buf, net.forward(roll.sim.observe(), 0)[2], 0.995, 0.95)
+    _capi.timing_arm(0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        _capi.timing_arm(2 * 8)                          # the first 8 steps' launches
+        roll.collect(buf)
+        last_val = net.forward(roll.sim.observe(), 0)[2]
+        _capi.timing_arm(1)
+        adv, ret = compute_gae(buf, last_val, 0.995, 0.95)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    kms = kernel_ms()
+    steps = reps * COLLECT_T
+    gae_us = kms["gae_kernel"] * 1e3
+    gae_gbs = GAE_BYTES * COLLECT_T * n / (gae_us * 1e-6) / 1e9
+    act_ms, tick_ms = kms["mlp_act_kernel"], kms["tick_kernel"]
+    mlp_tf = MLP_FLOP_PER_ENV * n / (act_ms * 1e-3) / 1e12
+    cpu = cpu_baseline_collect(cfg, spec, n, args.seed, args.cpu_seconds) \
+        if args.cpu_seconds > 0 else None
+    res = {
+        "metric": "env-steps/s at 5632 envs, self-play collect into the device rollout "
+                  "buffer (128 steps) + last-value forward + GAE, 1 MI355X",
+        "value": n * steps / el, "unit": "env-steps/s", "n_gpus": 1, "steps": steps,
+        "warmup": W, "ms_per_step": el / steps * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 sim / f16 MFMA (f32 accumulate) / f32 GAE",
+        "data": "synthetic: template maps from Philox draws, PyTorch default-init MLP weights",
+        "config": {"workload": "self-play collect, 5632 envs x 128 steps into the rollout "
+                               "buffer (obs slab 3.4 GB per 128 steps), GAE gamma 0.995 "
+                               "lambda 0.95", "envs": n, "collect_steps": COLLECT_T,
+                   "collects": reps, "parallelism": "single GPU"},
+        "roofline": {"kernel": "mlp_act_kernel", "bound": "mfma", "achieved": round(mlp_tf, 3),
+                     "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(mlp_tf / MFMA_F16_PEAK_TFLOPS, 5),
+                     "traffic": read_traffic("mlp_act_kernel")},
+        "kernels": {"mlp_act_kernel": {"us": round(act_ms * 1e3, 3)},
+                    "tick_kernel": {"us": round(tick_ms * 1e3, 3)},
+                    "gae_kernel": {"us": round(gae_us, 3), "bound": "hbm",
+                                   "achieved": round(gae_gbs, 3), "peak": HBM_PEAK_GBS,
+                                   "unit": "GB/s", "bytes_per_step_env": GAE_BYTES,
+                                   "frac": round(gae_gbs / HBM_PEAK_GBS, 5)}},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
 
 if __name__ == "__main__":
     main()

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 3
+#define QQT_ABI_VERSION 4
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -100,6 +100,10 @@ typedef struct qqt_tick_args {
   uint8_t* move_mask;         /* [N][P][5] */
   uint8_t* bomb_mask;         /* [N][P][2] */
   int32_t* probe_out;         /* PROBE: [N] largest bomb_blast */
+  uint8_t* damaged;           /* STEP: [N][P] 1 if the player's hp fell this tick,
+                                 judged after the auto-reset like the collect
+                                 loop's (hp0 - sim.hp).clamp(min=0) > 0
+                                 (train/ppo.py:251); or NULL */
 } qqt_tick_args;
 
 /* MLP actor/critic forward (+ masked sampling).  Weights are the packed
@@ -191,6 +195,31 @@ int qqt_mlp_act(const qqt_mlp_args* args, void* stream);
  * noise (:355) comes from `uniforms` or the Philox stream. */
 int qqt_bot_act(const qqt_sim_config* cfg, const qqt_bot_args* args, void* stream);
 
+/* Generalised advantage estimation over a filled rollout buffer: the
+ * reverse-time scan of compute_gae (train/ppo.py:101-110) in the reference's
+ * float32 operation order, one thread per env:
+ *   delta = (rew[t] + (gamma * next_val) * nt) - val[t],  nt = 1 - done[t]
+ *   gae   = delta + (gamma_lam * nt) * gae;  adv[t] = gae;  ret[t] = gae + val[t]
+ * with next_val = last_val at t = steps - 1, val[t + 1] before. */
+typedef struct qqt_gae_args {
+  int32_t steps;              /* T */
+  int32_t n_envs;             /* N */
+  float gamma;                /* float32(gamma) */
+  float gamma_lam;            /* float32 rounding of gamma * lam taken in double
+                                 (the reference's Python expression) */
+  int64_t step_stride;        /* elements between steps of rew and val */
+  int64_t env_stride;         /* elements between envs of rew and val */
+  const float* rew;           /* e.g. player 0 of a [T][N][P] reward slab */
+  const float* val;
+  const uint8_t* done;        /* [T][N], 0 or 1 */
+  const float* last_val;      /* [N] */
+  float* adv;                 /* [T][N] */
+  float* ret;                 /* [T][N] */
+} qqt_gae_args;
+
+/* One launch of the GAE scan (replaces compute_gae, train/ppo.py:101-110). */
+int qqt_gae(const qqt_gae_args* args, void* stream);
+
 /* Dispatch timing for benchmark harnesses (no counterpart in the reference:
  * its bench times whole steps with host clocks).  qqt_timing_arm(n) times
  * the next n kernel launches made through this library: each records a
@@ -201,7 +230,7 @@ int qqt_bot_act(const qqt_sim_config* cfg, const qqt_bot_args* args, void* strea
  * most 4096 launches are timed between collects.  Allocates no device
  * memory (the event pool is created by the first arm). */
 enum { QQT_KERNEL_TICK = 0, QQT_KERNEL_MLP = 1, QQT_KERNEL_BOT = 2, QQT_KERNEL_REACH = 3,
-       QQT_KERNEL_KINDS = 4 };
+       QQT_KERNEL_GAE = 4, QQT_KERNEL_KINDS = 5 };
 int qqt_timing_arm(int32_t launches);
 int qqt_timing_collect(double* ms, int32_t* count, int32_t n_kinds);
 

@@ -864,6 +864,10 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
     wave_sync();
     if (s.done[e]) template_reset();
     wave_sync();
+    // hp fell this tick, judged on the post-reset record (the collect loop
+    // compares after step() returns)
+    if (a.damaged && valid && l < P)
+      a.damaged[(size_t)g * P + l] = s.hp0[e][l] - pl[l][QQT_P_HP] > 0 ? 1 : 0;
   }
 
   // ---- observation + legality masks of the current state (sim/obs.py:25-229)

@@ -14,7 +14,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 
 from ._build import LIB
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 MODE_STEP, MODE_OBSERVE, MODE_RESET, MODE_PROBE = 0, 1, 2, 3
 
@@ -45,7 +45,7 @@ class TickArgsC(ctypes.Structure):
         (n, _vp) for n in ("cells", "players", "envs", "actions", "actions_i8", "crate_u",
                            "reset_mask", "reward", "done", "n_alive", "died", "winner",
                            "covered", "triggered", "obs", "move_mask", "bomb_mask",
-                           "probe_out")]
+                           "probe_out", "damaged")]
 
 
 class MlpArgsC(ctypes.Structure):
@@ -64,6 +64,12 @@ class BotArgsC(ctypes.Structure):
                 ("reach_mode", _i32), ("reach_slot", _i32)] + [
         (n, _vp) for n in ("cells", "players", "obs", "move_mask", "bomb_mask", "uniforms",
                            "reach", "actions", "actions_i8")]
+
+
+class GaeArgsC(ctypes.Structure):
+    _fields_ = [("steps", _i32), ("n_envs", _i32), ("gamma", _f32), ("gamma_lam", _f32),
+                ("step_stride", ctypes.c_int64), ("env_stride", ctypes.c_int64)] + [
+        (n, _vp) for n in ("rew", "val", "done", "last_val", "adv", "ret")]
 
 
 _LIB = None
@@ -85,6 +91,8 @@ def lib():
         L.qqt_mlp_act.argtypes = [ctypes.POINTER(MlpArgsC), _vp]
         L.qqt_bot_act.restype = ctypes.c_int
         L.qqt_bot_act.argtypes = [ctypes.POINTER(SimConfigC), ctypes.POINTER(BotArgsC), _vp]
+        L.qqt_gae.restype = ctypes.c_int
+        L.qqt_gae.argtypes = [ctypes.POINTER(GaeArgsC), _vp]
         L.qqt_timing_arm.restype = ctypes.c_int
         L.qqt_timing_arm.argtypes = [_i32]
         L.qqt_timing_collect.restype = ctypes.c_int
@@ -95,7 +103,8 @@ def lib():
     return _LIB
 
 
-KERNEL_KINDS = ("tick_kernel", "mlp_act_kernel", "bot_kernel", "reach_kernel")  # QQT_KERNEL_*
+KERNEL_KINDS = ("tick_kernel", "mlp_act_kernel", "bot_kernel", "reach_kernel",
+                "gae_kernel")  # QQT_KERNEL_*
 
 
 def timing_arm(launches: int) -> None:

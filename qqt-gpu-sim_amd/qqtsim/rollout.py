@@ -107,12 +107,14 @@ class Rollout:
         self.launch_policy()
         self.launch_opponent()
 
-    def launch_tick(self) -> None:
-        """Step with the sampled actions, auto-reset, observe, masks
+    def launch_tick(self, actions: torch.Tensor | None = None) -> None:
+        """Step with the sampled actions (`self.actions`, or the int8 buffer
+        the tick arguments point at), auto-reset, observe, masks
         (sim/torch_sim.py:895-1261, :605-645)."""
         sim = self.sim
         if sim.resolve_tiers is None:
-            sim.resolve_tiers = sim._first_tick_tiers(self.actions) \
+            acts = self.actions if actions is None else actions
+            sim.resolve_tiers = sim._first_tick_tiers(acts) \
                 if sim.exact_reference_resolve else 255
         t = self._tick
         t.resolve_tiers = sim.resolve_tiers
@@ -161,6 +163,63 @@ class Rollout:
             self._tick.obs = sim._obs.data_ptr()
             if bot is not None:
                 bot._args.obs = sim._obs.data_ptr()
+
+    def collect(self, buf) -> None:
+        """`buf.steps` env-steps filling a `qqtsim.ppo.HipRolloutBuffer` in
+        place: the collect loop of train/ppo.py:213-276 with RolloutBuffer.add
+        fused into the launches.  Step t's policy (and opponent) read slot
+        t's observation and masks and write slot t's actions, log-probs and
+        values; its tick writes slot t's rewards, done and damage flags and
+        the next observation and masks into slot t + 1 (the sim's own
+        buffers after the last step).  Slot 0 is copied from the sim."""
+        sim = self.sim
+        n, p, T = sim.num_envs, sim.cfg.n_players, buf.steps
+        if buf.num_envs != n or buf.n_players != p or buf.device != sim.device \
+                or tuple(buf.obs.shape[2:]) != tuple(sim.cfg.obs_shape):
+            raise ValueError("buffer shape or device differs from the sim's")
+        if (n * buf.obs[0, 0].numel() * 2) % 16:
+            raise ValueError("the number of envs must be a multiple of 4 (16-byte aligned slabs)")
+        m, tk, bot = self._mlp, self._tick, self.opponent
+        saved_m = (m.obs, m.move_mask, m.bomb_mask, m.actions_i8, m.logp_out, m.value_out)
+        saved_t = (tk.actions_i8, tk.reward, tk.done, tk.damaged, tk.obs, tk.move_mask,
+                   tk.bomb_mask)
+        saved_b = None if bot is None else (bot._args.obs, bot._args.move_mask,
+                                            bot._args.bomb_mask)
+        sim._refresh()
+        buf.obs[0].copy_(sim._obs.view(buf.obs[0].shape))
+        buf._mm[0].copy_(sim._mm)
+        buf._bm[0].copy_(sim._bm)
+        try:
+            for k in range(T):
+                obs, mm, bm = buf.obs[k].data_ptr(), buf._mm[k].data_ptr(), buf._bm[k].data_ptr()
+                m.obs, m.move_mask, m.bomb_mask = obs, mm, bm
+                m.actions_i8, m.logp_out = buf._act[k].data_ptr(), buf._logp[k].data_ptr()
+                m.value_out = buf._val[k].data_ptr()
+                self.launch_policy()
+                if bot is not None:
+                    bot._args.obs, bot._args.move_mask, bot._args.bomb_mask = obs, mm, bm
+                    bot.launch(buf._act[k])
+                last = k + 1 == T
+                tk.actions_i8 = buf._act[k].data_ptr()
+                tk.reward, tk.done = buf._rew[k].data_ptr(), buf._done[k].data_ptr()
+                tk.damaged = buf._dmg[k].data_ptr()
+                tk.obs = (sim._obs if last else buf.obs[k + 1]).data_ptr()
+                tk.move_mask = (sim._mm if last else buf._mm[k + 1]).data_ptr()
+                tk.bomb_mask = (sim._bm if last else buf._bm[k + 1]).data_ptr()
+                self.launch_tick(buf._act[k])
+        finally:
+            (m.obs, m.move_mask, m.bomb_mask, m.actions_i8, m.logp_out, m.value_out) = saved_m
+            (tk.actions_i8, tk.reward, tk.done, tk.damaged, tk.obs, tk.move_mask,
+             tk.bomb_mask) = saved_t
+            if bot is not None:
+                bot._args.obs, bot._args.move_mask, bot._args.bomb_mask = saved_b
+        buf.ptr = T
+        # the sim's own outputs describe the last step, as after step()
+        sim._reward.copy_(buf._rew[T - 1])
+        sim._done.copy_(buf._done[T - 1])
+        self.actions.copy_(buf._act[T - 1])
+        self.logp.copy_(buf._logp[T - 1])
+        self.value.copy_(buf._val[T - 1])
 
     def run(self, ticks: int) -> None:
         for _ in range(int(ticks)):

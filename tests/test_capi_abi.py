@@ -39,9 +39,9 @@ def _declared_functions():
 
 
 def test_header_declares_the_entry_points():
-    assert _declared_functions() == ["qqt_abi_version", "qqt_bot_act", "qqt_last_error",
-                                     "qqt_mlp_act", "qqt_tick", "qqt_timing_arm",
-                                     "qqt_timing_collect"]
+    assert _declared_functions() == ["qqt_abi_version", "qqt_bot_act", "qqt_gae",
+                                     "qqt_last_error", "qqt_mlp_act", "qqt_tick",
+                                     "qqt_timing_arm", "qqt_timing_collect"]
 
 
 def test_library_exports_every_declared_symbol():
@@ -89,7 +89,8 @@ def test_struct_layouts_match_the_header(tmp_path):
     from qqtsim import _capi
 
     structs = {"qqt_sim_config": _capi.SimConfigC, "qqt_tick_args": _capi.TickArgsC,
-               "qqt_mlp_args": _capi.MlpArgsC, "qqt_bot_args": _capi.BotArgsC}
+               "qqt_mlp_args": _capi.MlpArgsC, "qqt_bot_args": _capi.BotArgsC,
+               "qqt_gae_args": _capi.GaeArgsC}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "qqt_hip.h"',
              'int main(void) {']
     for cname, cls in structs.items():
@@ -238,12 +239,12 @@ def test_timing_rejects_bad_arguments(lib):
     assert lib.qqt_timing_arm(-1) == -1
     assert lib.qqt_timing_arm(4097) == -1
     assert b"launches" in lib.qqt_last_error()
-    ms, cnt = (ct.c_double * 4)(), (ct.c_int32 * 4)()
-    assert lib.qqt_timing_collect(None, cnt, 4) == -1
+    ms, cnt = (ct.c_double * 5)(), (ct.c_int32 * 5)()
+    assert lib.qqt_timing_collect(None, cnt, 5) == -1
     assert lib.qqt_timing_collect(ms, cnt, 0) == -1
     # nothing armed or taken: collect succeeds without touching a device
-    assert lib.qqt_timing_collect(ms, cnt, 4) == 0
-    assert list(cnt) == [0, 0, 0, 0]
+    assert lib.qqt_timing_collect(ms, cnt, 5) == 0
+    assert list(cnt) == [0, 0, 0, 0, 0]
 
 
 def test_header_kernel_kinds_match_host_mirror():
@@ -252,8 +253,33 @@ def test_header_kernel_kinds_match_host_mirror():
     text = open(HEADER).read()
     kinds = dict((k, int(v)) for k, v in re.findall(r"\bQQT_KERNEL_(\w+) = (\d+)", text))
     assert kinds["KINDS"] == len(_capi.KERNEL_KINDS)
-    for name in ("TICK", "MLP", "BOT", "REACH"):
+    for name in ("TICK", "MLP", "BOT", "REACH", "GAE"):
         assert _capi.KERNEL_KINDS[kinds[name]].startswith(name.lower()), name
+
+
+def _gae_args(**kw):
+    from qqtsim import _capi
+
+    a = _capi.GaeArgsC()
+    a.steps, a.n_envs, a.gamma, a.gamma_lam, a.step_stride, a.env_stride = 8, 4, 0.99, 0.94, 8, 2
+    for i, name in enumerate(("rew", "val", "done", "last_val", "adv", "ret")):
+        setattr(a, name, 0x10000 * (i + 1))
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(rew=None), "null argument"),
+    (dict(ret=None), "null argument"),
+    (dict(steps=0), "positive"),
+    (dict(n_envs=-3), "positive"),
+    (dict(step_stride=0), "positive"),
+    (dict(env_stride=-1), "positive"),
+])
+def test_gae_rejects_bad_arguments(lib, kw, msg):
+    assert lib.qqt_gae(_gae_args(**kw), None) == -1
+    assert msg in lib.qqt_last_error().decode()
 
 
 def test_errors_raise_in_python(lib):
