@@ -144,6 +144,16 @@ def cpu_baseline_stress(cfg, spec, n, seed, budget_s):
                       f"{ticks} timed ticks after 1 warm-up tick, {el:.1f} s"}
 
 
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def _cores(torch):
     cores = len(os.sched_getaffinity(0))
     if os.environ.get("OMP_NUM_THREADS", "").isdigit():
@@ -190,10 +200,22 @@ def cpu_baseline(cfg, spec, n, seed, budget_s):
         el = time.perf_counter() - t0
         if el >= budget_s or ticks >= 256:
             break
+    # the same env-step on one thread, over a quarter of the budget
+    torch.set_num_threads(1)
+    ticks1, t1 = 0, time.perf_counter()
+    while True:
+        env_step(2 + ticks + ticks1)
+        ticks1 += 1
+        el1 = time.perf_counter() - t1
+        if el1 >= budget_s / 4 or ticks1 >= 64:
+            break
+    torch.set_num_threads(cores)
     return {"value": n * ticks / el, "unit": "env-steps/s", "cores": cores,
-            "kind": "port",
+            "kind": "port", "cpu_model": _cpu_model(),
+            "value_1thread": n * ticks1 / el1,
             "sample": f"oracle (torch CPU restatement) on the same workload, {n} envs x "
-                      f"{ticks} timed ticks after 2 warm-up ticks, {el:.1f} s"}
+                      f"{ticks} timed ticks after 2 warm-up ticks, {el:.1f} s; one thread: "
+                      f"{ticks1} ticks, {el1:.1f} s"}
 
 
 def read_traffic(kernel):
