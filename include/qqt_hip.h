@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 4
+#define QQT_ABI_VERSION 5
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -68,6 +68,8 @@ typedef struct qqt_sim_config {
 #define QQT_MODE_OBSERVE 1  /* observe + masks of the current state only */
 #define QQT_MODE_RESET 2    /* template reset where reset_mask, then observe */
 #define QQT_MODE_PROBE 3    /* largest bomb_blast after this tick's placement */
+#define QQT_MODE_FLUSH 4    /* recycle flush (each player's pending lost growth becomes
+                               recycle crates on random free cells), then observe */
 
 typedef struct qqt_tick_args {
   int32_t n_envs;
@@ -78,7 +80,8 @@ typedef struct qqt_tick_args {
   float danger_coef;          /* explore_coef * danger_penalty (rounded once) */
   uint64_t seed;              /* Philox key */
   uint32_t tick;              /* keys per-tick uniforms (crates) */
-  uint32_t epoch;             /* keys template draws of this call's resets */
+  uint32_t epoch;             /* keys template draws of this call's resets
+                                 (FLUSH: the flush counter keying the cell draws) */
   /* state (in/out) */
   int32_t* cells;
   int32_t* players;
@@ -104,6 +107,8 @@ typedef struct qqt_tick_args {
                                  judged after the auto-reset like the collect
                                  loop's (hp0 - sim.hp).clamp(min=0) > 0
                                  (train/ppo.py:251); or NULL */
+  const uint8_t* recycle_excl; /* FLUSH: [H*W] 1 = never a recycle crate (spawn
+                                 neighbourhoods, the open-mode cross band) */
 } qqt_tick_args;
 
 /* MLP actor/critic forward (+ masked sampling).  Weights are the packed

@@ -16,6 +16,10 @@ path:
   sim/torch_sim.py:732-833), with empty trailing rounds skipped.
 * Hazard waves and the reference's CUDA-graph mode are not modelled
   (`hazard_fraction` must be 0).
+* `flush_recycle` takes each player's recycle cells as the k free cells with
+  the smallest Philox keys (stream `STREAM_RECYCLE`, keyed by a flush
+  counter) where the reference takes the first k of `torch.randperm`: the
+  same uniform law over k-subsets, from injectable draws.
 
 Explosion tiers.  The reference resolves explosions through a function it
 builds once per sim with the first tick's blast hint bound as a default
@@ -35,6 +39,34 @@ from . import philox
 from .grid import danger_map, rays, resolve_explosions
 from .move import center_cell, move_players
 from .obs import encode_obs, legal_mask
+
+def recycle_exclusion(cfg) -> np.ndarray:
+    """(H*W,) bool: cells a recycle crate never lands on
+    (sim/torch_sim.py:455-533, `_recycle_excl`): the cell and 4-neighbours
+    of the open-mode spawns (the row through the middle, columns split
+    evenly), of `cfg.spawn_cells()` and of the ring-mode corner spawns, plus
+    the open-mode centre cross (rows and columns (n-1)//2 - 1 and (n-1)//2)."""
+    h, w, p = cfg.height, cfg.width, cfg.n_players
+    excl = set()
+    open_row = (h - 1) / 2.0 + 0.5
+    open_spawns = [(open_row, (w - 1) * (i + 1) / (p + 1) + 0.5) for i in range(p)]
+    spawn_sets = [open_spawns, [(float(r), float(c)) for r, c in cfg.spawn_cells()],
+                  [(float(r), float(c)) for r, c in cfg.ring_spawn_cells()]]
+    for spawns in spawn_sets:
+        for sy, sx in spawns:
+            r, c = int(sy), int(sx)
+            for dr, dc in ((0, 0), (-1, 0), (1, 0), (0, -1), (0, 1)):
+                if 0 <= r + dr < h and 0 <= c + dc < w:
+                    excl.add((r + dr) * w + (c + dc))
+    cy, cx = (h - 1) // 2, (w - 1) // 2
+    for r in range(h):
+        for c in range(w):
+            if r in (cy - 1, cy) or c in (cx - 1, cx):
+                excl.add(r * w + c)
+    m = np.zeros(h * w, dtype=bool)
+    m[sorted(excl)] = True
+    return m
+
 
 STATE_KEYS = (
     "wall", "brick", "crate", "recycle", "fuse", "owner", "bomb_blast",
@@ -178,6 +210,36 @@ class OracleSim:
         self.since_bomb[idx] = cfg.place_dist_cooldown
         self.invuln[idx] = 0
         self.t[idx] = 0
+
+    # ------------------------------------------------------------ recycle flush
+    def flush_recycle(self, flush_epoch: int) -> None:
+        """sim/torch_sim.py:549-596: for each env and each player in id order
+        with pending lost growth k > 0, min(k, free) distinct free cells (no
+        wall, no brick, not excluded) become recycle crates; then every
+        pending count resets.  The cells are the k free ones with the
+        smallest (key, cell) of Philox stream STREAM_RECYCLE, value p*C + c,
+        keyed by (seed, env, flush_epoch)."""
+        cfg = self.cfg
+        n, p, hw = self.num_envs, cfg.n_players, cfg.n_cells
+        excl = recycle_exclusion(cfg)
+        pend = self.pending_lost.numpy()
+        todo = np.flatnonzero(pend.sum(1) > 0)
+        if todo.size:
+            u = philox.uniforms(self.seed, todo, flush_epoch, philox.STREAM_RECYCLE, p * hw)
+            free = (~self.wall.view(n, hw) & ~self.brick.view(n, hw)).numpy()[todo] & ~excl
+            crate, rec = self.crate.view(n, hw), self.recycle.view(n, hw)
+            for row, e in enumerate(todo):
+                for i in range(p):
+                    k = int(pend[e, i])
+                    if k <= 0:
+                        continue
+                    cells = np.flatnonzero(free[row])
+                    keys = u[row, i * hw + cells]
+                    order = np.lexsort((cells, keys))        # by key, then cell
+                    pick = cells[order[:k]]
+                    crate[e, pick] = True
+                    rec[e, pick] = True
+        self.pending_lost.zero_()
 
     # ------------------------------------------------------------ state I/O
     def state_dict(self) -> dict:

@@ -10,7 +10,8 @@ namespace qqt {
 // Philox stream ids (third counter word); the host oracle uses the same ids.
 enum : uint32_t {
   STREAM_CRATE = 1, STREAM_RESET_CELL = 2, STREAM_RESET_MISC = 3,
-  STREAM_POLICY = 4, STREAM_RANDOM_ACT = 5, STREAM_INJECT_ACT = 6, STREAM_BOT = 7
+  STREAM_POLICY = 4, STREAM_RANDOM_ACT = 5, STREAM_INJECT_ACT = 6, STREAM_BOT = 7,
+  STREAM_RECYCLE = 8
 };
 
 // Philox4x32 with 10 rounds (Salmon et al., SC'11).  c holds the counter on

@@ -641,6 +641,61 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
     wave_sync();
   }
 
+  // ---- recycle flush (sim/torch_sim.py:549-596): player by player, the
+  // pending lost growth becomes that many recycle crates on distinct free
+  // cells (no wall, no brick, not excluded), then the counts reset.  The
+  // reference takes the first k of a random permutation of the free cells;
+  // here the k free cells with the smallest Philox keys (stream 8, value
+  // p*C + c) are taken, the same uniform k-subset law.
+  if (mode == QQT_MODE_FLUSH) {
+    bool freec[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      const int c = l + LPE * k;
+      freec[k] = c < C && !(cw[c] & (F_WALL | F_BRICK)) && !a.recycle_excl[c];
+    }
+    for (int i = 0; i < P; ++i) {
+      const int want = valid ? pl[i][QQT_P_PENDING_LOST] : 0;
+      uint64_t key[KMAX];
+#pragma unroll
+      for (int k = 0; k < KMAX; ++k) {
+        const int c = l + LPE * k;
+        key[k] = ~0ull;
+        if (want > 0 && freec[k]) {
+          const float u = philox_uniform(a.seed, (uint32_t)g, a.epoch, STREAM_RECYCLE,
+                                         (uint32_t)(i * C + c));
+          key[k] = ((uint64_t)__float_as_uint(u) << 32) | (uint32_t)c;   // u >= 0: bits order
+        }
+      }
+      // every lane runs the same number of rounds (the wave's largest count)
+      int rounds = want;
+#pragma unroll
+      for (int m = 1; m < 64; m <<= 1) rounds = max(rounds, __shfl_xor(rounds, m, 64));
+      for (int t = 0; t < rounds; ++t) {
+        uint64_t mn = key[0];
+#pragma unroll
+        for (int k = 1; k < KMAX; ++k) mn = key[k] < mn ? key[k] : mn;
+#pragma unroll
+        for (int m = 1; m < LPE; m <<= 1) {
+          const uint64_t o = __shfl_xor(mn, m, 64);
+          mn = o < mn ? o : mn;
+        }
+        if (t < want && mn != ~0ull) {
+          const int c = (int)(mn & 0xFFu);
+#pragma unroll
+          for (int k = 0; k < KMAX; ++k)
+            if (c == l + LPE * k) {
+              cw[c] |= F_CRATE | F_REC;
+              key[k] = ~0ull;
+            }
+        }
+      }
+    }
+    wave_sync();
+    if (l < P && valid) pl[l][QQT_P_PENDING_LOST] = 0;
+    wave_sync();
+  }
+
   // ---- danger map of the current state (sim/blast.py:158-317)
   {
     float* dng = s.dng[e];
@@ -980,7 +1035,7 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
   wave_sync();
 
   // ---- store state and the staged observation
-  if (mode == QQT_MODE_STEP || mode == QQT_MODE_RESET) {
+  if (mode == QQT_MODE_STEP || mode == QQT_MODE_RESET || mode == QQT_MODE_FLUSH) {
     if (valid) {
 #pragma unroll
       for (int k = 0; k < KMAX; ++k) {
@@ -1058,7 +1113,9 @@ int qqt_tick(const qqt_sim_config* cfg, const qqt_tick_args* a, void* stream) {
   if (!cfg || !a) return fail(QQT_E_ARG, "null config or args");
   if (a->n_envs <= 0) return fail(QQT_E_ARG, "n_envs must be positive");
   if (!a->cells || !a->players || !a->envs) return fail(QQT_E_ARG, "null state pointer");
-  if (a->mode < QQT_MODE_STEP || a->mode > QQT_MODE_PROBE) return fail(QQT_E_ARG, "bad mode");
+  if (a->mode < QQT_MODE_STEP || a->mode > QQT_MODE_FLUSH) return fail(QQT_E_ARG, "bad mode");
+  if (a->mode == QQT_MODE_FLUSH && !a->recycle_excl)
+    return fail(QQT_E_ARG, "FLUSH needs recycle_excl");
   if (a->mode == QQT_MODE_STEP && !a->actions && !a->actions_i8)
     return fail(QQT_E_ARG, "STEP needs actions");
   if (a->mode == QQT_MODE_PROBE && !a->actions && !a->actions_i8)

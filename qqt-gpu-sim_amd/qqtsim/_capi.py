@@ -14,9 +14,9 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 
 from ._build import LIB
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
-MODE_STEP, MODE_OBSERVE, MODE_RESET, MODE_PROBE = 0, 1, 2, 3
+MODE_STEP, MODE_OBSERVE, MODE_RESET, MODE_PROBE, MODE_FLUSH = 0, 1, 2, 3, 4
 
 _i32, _f32, _u32, _u64, _vp = (ctypes.c_int32, ctypes.c_float, ctypes.c_uint32,
                                ctypes.c_uint64, ctypes.c_void_p)
@@ -45,7 +45,7 @@ class TickArgsC(ctypes.Structure):
         (n, _vp) for n in ("cells", "players", "envs", "actions", "actions_i8", "crate_u",
                            "reset_mask", "reward", "done", "n_alive", "died", "winner",
                            "covered", "triggered", "obs", "move_mask", "bomb_mask",
-                           "probe_out", "damaged")]
+                           "probe_out", "damaged", "recycle_excl")]
 
 
 class MlpArgsC(ctypes.Structure):

@@ -63,3 +63,26 @@ def spawn_l_cells(h: int, w: int, p: int) -> set[tuple[int, int]]:
 OPEN_PILLARS = MapSpec(kind="pillars", brick_p=0.0)
 CORRIDOR_70 = MapSpec(kind="pillars", brick_p=0.7)
 BOMB_STRESS_40 = MapSpec(kind="pillars", brick_p=0.4, bombs_cap=(1, 4), blast_cap=(2, 5))
+
+
+def recycle_exclusion(cfg) -> list[int]:
+    """Flat cells a recycle crate never lands on (sim/torch_sim.py:455-533,
+    `_recycle_excl`): each spawn cell and its 4-neighbours for the open-mode
+    spawns (middle row, columns split evenly), `cfg.spawn_cells()` and the
+    ring-mode corners, plus the open-mode centre cross (rows and columns
+    (n-1)//2 - 1 and (n-1)//2), sorted."""
+    h, w, p = cfg.height, cfg.width, cfg.n_players
+    row = (h - 1) / 2.0 + 0.5
+    spawns = [(row, (w - 1) * (i + 1) / (p + 1) + 0.5) for i in range(p)]
+    spawns += [(float(r), float(c)) for r, c in cfg.spawn_cells()]
+    spawns += [(float(r), float(c)) for r, c in cfg.ring_spawn_cells()]
+    cells = set()
+    for sy, sx in spawns:
+        r0, c0 = int(sy), int(sx)
+        for r, c in ((r0, c0), (r0 - 1, c0), (r0 + 1, c0), (r0, c0 - 1), (r0, c0 + 1)):
+            if 0 <= r < h and 0 <= c < w:
+                cells.add(r * w + c)
+    cy, cx = (h - 1) // 2, (w - 1) // 2
+    cells |= {r * w + c for r in (cy - 1, cy) for c in range(w)}
+    cells |= {r * w + c for r in range(h) for c in (cx - 1, cx)}
+    return sorted(cells)

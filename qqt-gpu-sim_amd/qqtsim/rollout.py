@@ -81,6 +81,13 @@ class Rollout:
             setattr(t, k, buf.data_ptr())
         self._tick = t
 
+        f = _capi.TickArgsC()
+        f.n_envs, f.mode = n, _capi.MODE_FLUSH
+        f.seed = sim.seed & 0xFFFFFFFFFFFFFFFF
+        f.cells, f.players, f.envs = t.cells, t.players, t.envs
+        f.recycle_excl = sim.recycle_excl().data_ptr()
+        self._flush = f
+
     @property
     def reward(self) -> torch.Tensor:
         return self.sim._reward
@@ -164,14 +171,18 @@ class Rollout:
             if bot is not None:
                 bot._args.obs = sim._obs.data_ptr()
 
-    def collect(self, buf) -> None:
+    def collect(self, buf, flush_every: int = 16) -> None:
         """`buf.steps` env-steps filling a `qqtsim.ppo.HipRolloutBuffer` in
         place: the collect loop of train/ppo.py:213-276 with RolloutBuffer.add
         fused into the launches.  Step t's policy (and opponent) read slot
         t's observation and masks and write slot t's actions, log-probs and
         values; its tick writes slot t's rewards, done and damage flags and
         the next observation and masks into slot t + 1 (the sim's own
-        buffers after the last step).  Slot 0 is copied from the sim."""
+        buffers after the last step).  Slot 0 is copied from the sim.  Like
+        the reference loop (train/ppo.py:263-264, :292) the recycle flush
+        runs after every `flush_every`-th step and once after the last one
+        (0 = never); a flush rewrites the next slot's observation and
+        masks."""
         sim = self.sim
         n, p, T = sim.num_envs, sim.cfg.n_players, buf.steps
         if buf.num_envs != n or buf.n_players != p or buf.device != sim.device \
@@ -207,6 +218,10 @@ class Rollout:
                 tk.move_mask = (sim._mm if last else buf._mm[k + 1]).data_ptr()
                 tk.bomb_mask = (sim._bm if last else buf._bm[k + 1]).data_ptr()
                 self.launch_tick(buf._act[k])
+                if flush_every > 0 and k % flush_every == flush_every - 1 and not last:
+                    self._launch_flush(tk.obs, tk.move_mask, tk.bomb_mask)
+            if flush_every > 0:
+                self._launch_flush(sim._obs.data_ptr(), sim._mm.data_ptr(), sim._bm.data_ptr())
         finally:
             (m.obs, m.move_mask, m.bomb_mask, m.actions_i8, m.logp_out, m.value_out) = saved_m
             (tk.actions_i8, tk.reward, tk.done, tk.damaged, tk.obs, tk.move_mask,
@@ -220,6 +235,16 @@ class Rollout:
         self.actions.copy_(buf._act[T - 1])
         self.logp.copy_(buf._logp[T - 1])
         self.value.copy_(buf._val[T - 1])
+
+    def _launch_flush(self, obs: int, mm: int, bm: int) -> None:
+        """The sim's recycle flush, writing observation and masks to the given
+        device addresses (sim/torch_sim.py:549-596)."""
+        sim = self.sim
+        f = self._flush
+        f.epoch = sim.flushes & 0xFFFFFFFF
+        f.obs, f.move_mask, f.bomb_mask = obs, mm, bm
+        _capi.check(self._lib.qqt_tick(sim._cfg_c, f, self._stream))
+        sim.flushes += 1
 
     def run(self, ticks: int) -> None:
         for _ in range(int(ticks)):

@@ -32,7 +32,7 @@ import torch
 
 from . import _capi, state as st
 from .config import N_BOMB, N_MOVES, SimConfig
-from .maps import KIND_CODES, MapSpec
+from .maps import KIND_CODES, MapSpec, recycle_exclusion
 
 SUPPORTED = {(13, 13, 2), (7, 7, 2), (9, 9, 2), (13, 13, 3), (13, 13, 4)}
 
@@ -118,6 +118,8 @@ class HipBatchedSim:
         self.seed = int(seed)
         self.tick = 0
         self.epoch = 0
+        self.flushes = 0          # recycle flushes so far (keys their cell draws)
+        self._excl = None
         self.explore_coef = 1.0
         self.exact_reference_resolve = exact_reference_resolve
         self.resolve_tiers: int | None = None
@@ -145,7 +147,7 @@ class HipBatchedSim:
 
     # ---------------------------------------------------------------- launch
     def _launch(self, mode, actions=None, crate_u=None, reset_mask=None, auto_reset=True,
-                outputs=True):
+                outputs=True, epoch=None):
         a = _capi.TickArgsC()
         a.n_envs = self.num_envs
         a.mode = mode
@@ -155,7 +157,7 @@ class HipBatchedSim:
         a.danger_coef = float(self.explore_coef * self.cfg.danger_penalty)
         a.seed = self.seed & 0xFFFFFFFFFFFFFFFF
         a.tick = self.tick & 0xFFFFFFFF
-        a.epoch = self.epoch & 0xFFFFFFFF
+        a.epoch = (self.epoch if epoch is None else epoch) & 0xFFFFFFFF
         a.cells = self._cells.data_ptr()
         a.players = self._players.data_ptr()
         a.envs = self._envs.data_ptr()
@@ -180,6 +182,8 @@ class HipBatchedSim:
             a.bomb_mask = self._bm.data_ptr()
         if mode == _capi.MODE_PROBE:
             a.probe_out = self._probe.data_ptr()
+        if mode == _capi.MODE_FLUSH:
+            a.recycle_excl = self.recycle_excl().data_ptr()
         _capi.check(self._lib.qqt_tick(self._cfg_c, a, _capi.stream_handle(self.device)))
 
     def _as_device(self, t, dtype, shape):
@@ -262,10 +266,24 @@ class HipBatchedSim:
         """Accepted for API parity; template resets draw caps from the MapSpec."""
         self._opp_boost = int(v)
 
+    def recycle_excl(self) -> torch.Tensor:
+        """(H*W,) uint8 device mask of the cells recycle crates avoid."""
+        if self._excl is None:
+            m = torch.zeros(self.cfg.height * self.cfg.width, dtype=torch.uint8)
+            m[recycle_exclusion(self.cfg)] = 1
+            self._excl = m.to(self.device)
+        return self._excl
+
     def flush_recycle(self) -> None:
-        """Deferred recycle-crate placement is not on the rollout hot path; the
-        pending counts stay in `pending_lost` (sim/torch_sim.py:580-596)."""
-        return None
+        """BatchedSim.flush_recycle (sim/torch_sim.py:549-596) as one launch:
+        every player's pending lost growth becomes that many recycle crates on
+        distinct free cells (the k smallest Philox keys among them, the
+        uniform k-subset law of the reference's randperm), the counts reset,
+        and the observation and masks are refreshed.  No host sync: envs with
+        nothing pending are left as they are."""
+        self._launch(_capi.MODE_FLUSH, epoch=self.flushes)
+        self.flushes += 1
+        self._fresh = True
 
     def __getattr__(self, name):
         if name in st.ALL_KEYS:
