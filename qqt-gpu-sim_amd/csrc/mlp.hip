@@ -48,7 +48,8 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int HID = 128;           // hidden width
 constexpr int HEAD = 64;           // head hidden width
 constexpr int NOUT = 8;            // 5 move + 2 bomb + 1 value
-constexpr int ROWS = 64;           // rows per workgroup
+constexpr int ROWS = 64;           // rows per block (a workgroup takes one or two)
+constexpr int MLP_TWO_BLOCK_ROWS = 1 << 16;   // forward batches from here use two blocks
 constexpr int NTHR = 512;          // 8 wavefronts
 constexpr int FST = HID + 4;       // fp32 row stride of the LayerNorm tile (bank spread)
 #ifndef QQT_MLP_PD
@@ -91,14 +92,21 @@ constexpr int XT_HALVES = ROWS * 64;            // one 64 x 64 observation tile 
 constexpr int H_HALVES = 2 * ROWS * HID;        // hi + lo planes of h1 or h2 (32 KB)
 constexpr int HY_HALVES = 2 * ROWS * 3 * HEAD;  // hi + lo planes of the head layer (48 KB)
 static_assert(HY_HALVES <= 4 * XT_HALVES + H_HALVES, "head layer reuses the x tiles and h1");
+static_assert(HY_HALVES <= 8 * XT_HALVES, "two-block head layer fits in the x tiles alone");
 static_assert(ROWS * HID * 2 <= 4 * XT_HALVES, "the second partial tile fits in the x tiles");
 
 constexpr int WF_HALVES = 3 * 64 * 16;          // output layer: 1 column tile x 3 K blocks
 constexpr int WF_CHUNKS = 2 * WF_HALVES / 8;    // 16-byte chunks of both planes
 
+// LDS of a workgroup of RB 64-row blocks.  xs_h1 holds the layer-1 x tiles
+// (RB x 32 KB), then h1; the tail reuses the x tiles for the second partial
+// tile and the head layer.  With RB = 1 the head layer spills over into the
+// dead h1 and h2 has its own region; with RB = 2 the x tiles alone hold the
+// head layer and h2 reuses h1 (dead once layer 2 has read it).
+template <int RB>
 struct __align__(16) MlpLds {
-  uint16_t xs_h1[4 * XT_HALVES + H_HALVES];   // x tiles [group][buffer] | h1; later the head layer
-  uint16_t h2[H_HALVES];
+  uint16_t xs_h1[RB * 4 * XT_HALVES + H_HALVES];   // x tiles [group][buffer] | h1
+  uint16_t h2[RB == 1 ? H_HALVES : 8];
   float f[ROWS][FST];                         // fp32 pre-LayerNorm tile
   float vec[V_N];                             // biases and LayerNorm affine parameters
   float logit[ROWS][NOUT];
@@ -143,7 +151,8 @@ __device__ __forceinline__ float* f1_at(uint16_t* xs, int row, int col) {
 // owns columns 32i + 4j .. +3 (i = 0..3), so for each i the row's 8 lanes
 // read 128 contiguous bytes (no bank conflicts); writes float16 hi/lo planes
 // of dst as 8-byte stores.
-__device__ __forceinline__ void layernorm_rows(MlpLds& s, const uint16_t* f1, int vb, int vg,
+template <class L>
+__device__ __forceinline__ void layernorm_rows(L& s, const uint16_t* f1, int vb, int vg,
                                                int vbe, uint16_t* dst) {
   const int t = threadIdx.x, row = t >> 3, j = t & 7;
   float v[16], ga[16], be[16];
@@ -278,15 +287,22 @@ __device__ __forceinline__ int sample_masked(const float* logit, const uint8_t* 
   return a;
 }
 
+// RB row blocks of 64 per workgroup: RB = 2 halves the W0 bytes each row
+// costs (large forward batches, no sampling); the tail runs once per block.
+template <int RB>
 __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
-  __shared__ MlpLds s;
-  const int nrb = (a.batch + ROWS - 1) / ROWS;
+  static_assert(RB == 1 || RB == 2, "one or two row blocks per workgroup");
+  constexpr int RT = 4 * RB;               // layer-1 row tiles per wavefront
+  constexpr int NX = 8 * RB;               // x load instructions per wavefront and K block
+  constexpr int XT = RB * XT_HALVES;       // one x tile of the workgroup
+  __shared__ MlpLds<RB> s;
+  const int nrb = (a.batch + RB * ROWS - 1) / (RB * ROWS);
   const int xcd = blockIdx.x & 7, seq = blockIdx.x >> 3;
   const int slot = seq % a.npid;
   const int rb = (seq / a.npid) * 8 + xcd;
   if (rb >= nrb) return;                   // padding workgroup (uniform, before any barrier)
   const int pid = a.npid == 2 ? slot : a.pid0;
-  const int row0 = rb * ROWS;
+  const int row0 = rb * RB * ROWS;
   // wavefront index as a scalar: branches and addresses on it stay uniform
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int r16 = lane & 15, q = lane >> 4;
@@ -316,52 +332,55 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   const uint4 wfv1 = wc1 < WF_CHUNKS ? *wf_src(wc1) : make_uint4(0u, 0u, 0u, 0u);
 
   // ---------------- layer 1: group kg, K blocks kg, kg+2, ...; columns 32cg..32cg+31
-  floatx4 acc[4][2];
+  floatx4 acc[RT][2];
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt)
+  for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) acc[rt][ct] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // x loads: instruction i of wavefront (kg, cg) covers tile rows 16cg+2i,
-  // 16cg+2i+1; lane l reads dword l&31 (two halves) of row 16cg+2i+(l>>5).
+  // x loads: instruction i of wavefront (kg, cg) covers tile rows
+  // 16RBcg+2i, 16RBcg+2i+1; lane l reads dword l&31 (two halves) of row
+  // 16RBcg+2i+(l>>5).
   const int nkb = a.kblocks0;
   const int dw = lane & 31;
-  const uint32_t* xrow[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = min(row0 + 16 * cg + 2 * i + (lane >> 5), a.batch - 1);
-    xrow[i] = reinterpret_cast<const uint32_t*>(a.obs + (size_t)r * a.obs_stride);
-  }
+  // row addresses are formed at each load from one base row (clamped to
+  // the batch for a ragged last block), not held as NX pointers
+  const int xrow0 = row0 + 16 * RB * cg + (lane >> 5);
+  const uint32_t* const xbase = reinterpret_cast<const uint32_t*>(a.obs);
+  const size_t xstride = (size_t)a.obs_stride / 2;    // dwords per row
   const uint16_t* wb = a.w0 + (size_t)((pid * 8 + 2 * cg) * nkb) * 64 * 16 + lane * 16;
   const size_t wtile = (size_t)nkb * 64 * 16;   // halves between B tiles
-  uint16_t* const xt = s.xs_h1 + kg * 2 * XT_HALVES;   // this group's two x tiles
+  uint16_t* const xt = s.xs_h1 + kg * 2 * XT;   // this group's two x tiles
 
   // Loads run PD group steps ahead; the tail mask (elements >= k0) is applied
   // when the registers are written to LDS, so no load is waited on early.
   // Lanes past k0 read dword 0 of their row (in bounds).
-  auto load_x = [&](int kb, uint32_t (&xr)[8]) {
+  auto load_x = [&](int kb, uint32_t (&xr)[NX]) {
     const int k = 64 * kb + 2 * dw;              // first half of this lane's pair
     const int off = k < a.k0 ? (k >> 1) : 0;     // k0 is even: pairs never straddle
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xr[i] = __builtin_nontemporal_load(xrow[i] + off);
+    for (int i = 0; i < NX; ++i) {
+      const int r = min(xrow0 + 2 * i, a.batch - 1);
+      xr[i] = xbase[(size_t)r * xstride + off];   // cached: two workgroups read each row
+    }
   };
   auto load_w = [&](int kb, Frag16 (&br)[2]) {
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) br[ct] = load_b(wb + ct * wtile + (size_t)kb * 64 * 16);
   };
-  auto store_x = [&](const uint32_t (&xr)[8], int buf, int kb) {
+  auto store_x = [&](const uint32_t (&xr)[NX], int buf, int kb) {
     const bool ok = 64 * kb + 2 * dw < a.k0;
-    uint32_t* t = reinterpret_cast<uint32_t*>(xt + buf * XT_HALVES);
+    uint32_t* t = reinterpret_cast<uint32_t*>(xt + buf * XT);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = 16 * cg + 2 * i + (lane >> 5);
+    for (int i = 0; i < NX; ++i) {
+      const int r = 16 * RB * cg + 2 * i + (lane >> 5);
       t[r * 32 + (swz(r, dw >> 2) << 2) + (dw & 3)] = ok ? xr[i] : 0u;
     }
   };
   auto compute = [&](int buf, const Frag16 (&br)[2]) {
-    const uint16_t* t = xt + buf * XT_HALVES;
+    const uint16_t* t = xt + buf * XT;
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       const Frag16 af = read_a(t, 64, 16 * rt + r16, 0, q);
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
@@ -376,7 +395,7 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   // prefetch indices are clamped to the last block, and the step count is
   // padded to a multiple of PD with all-zero x tiles (store_x masks every
   // element >= k0), which add exactly zero.
-  uint32_t xr[PD][8];
+  uint32_t xr[PD][NX];
   Frag16 br[PD][2];
   const int last = nkb - 1;
   const int nsteps = (((nkb + 1) / 2 + PD - 1) / PD) * PD;
@@ -388,7 +407,7 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   }
 
   const int srow = row0 + (int)threadIdx.x;          // sampling row of threads < 64
-  const bool sampler = threadIdx.x < ROWS && srow < a.batch && a.sample;
+  const bool sampler = RB == 1 && threadIdx.x < ROWS && srow < a.batch && a.sample;
   uint8_t mm[5] = {0, 0, 0, 0, 0}, bm[2] = {0, 0};
   float um = 0.0f, ub = 0.0f;
   if (sampler) {
@@ -437,9 +456,13 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   }
 
   // Combine the two groups' partial sums in the fp32 tile.
-  uint16_t* const H1 = s.xs_h1 + 4 * XT_HALVES;
-  SplitB<2, 2> w1b;                 // layer-2 weights: in flight during LayerNorm 1
+  uint16_t* const H1 = s.xs_h1 + RB * 4 * XT_HALVES;
+  uint16_t* const H2 = RB == 1 ? s.h2 : H1;
   const int rh = w >> 2;            // row half of the small layers
+#pragma unroll
+  for (int hb = 0; hb < RB; ++hb) {   // one 64-row block at a time
+  const int brow0 = row0 + ROWS * hb;
+  SplitB<2, 2> w1b;                 // layer-2 weights: in flight during LayerNorm 1
   load_split_b(w1b, a.w1, a.w1_lo, 2 * cg, lane);
   // The last loop step ended with a barrier, so the x tiles are free.
   // (kg is uniform: one branch around both store loops)
@@ -450,7 +473,7 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
       for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          s.f[16 * rt + 4 * q + j][32 * cg + 16 * ct + r16] = acc[rt][ct][j];
+          s.f[16 * rt + 4 * q + j][32 * cg + 16 * ct + r16] = acc[4 * hb + rt][ct][j];
   } else {
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt)
@@ -458,7 +481,7 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
       for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          *f1_at(s.xs_h1, 16 * rt + 4 * q + j, 32 * cg + 16 * ct + r16) = acc[rt][ct][j];
+          *f1_at(s.xs_h1, 16 * rt + 4 * q + j, 32 * cg + 16 * ct + r16) = acc[4 * hb + rt][ct][j];
   }
   __syncthreads();
   layernorm_rows(s, s.xs_h1, V_B0, V_G1, V_BE1, H1);
@@ -481,18 +504,18 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
       for (int j = 0; j < 4; ++j)
         s.f[32 * rh + 16 * i + 4 * q + j][32 * cg + 16 * ct + r16] = acc2[i][ct][j];
   __syncthreads();
-  layernorm_rows(s, nullptr, V_B1, V_G2, V_BE2, s.h2);
+  layernorm_rows(s, nullptr, V_B1, V_G2, V_BE2, H2);
   __syncthreads();
 
   // ---------------- heads, first layer: 128 -> 192; rows 32rh.., columns 48cg..
-  uint16_t* const HY = s.xs_h1;     // x tiles and h1 are dead from here on
+  uint16_t* const HY = s.xs_h1;     // the x tiles (and with RB = 1 h1) are dead from here on
   {
     floatx4 hac[2][3];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int ct = 0; ct < 3; ++ct) hac[i][ct] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    split_gemm<2, 3, 2>(hac, s.h2, s.h2 + ROWS * HID, HID, 2 * rh, whb, lane);
+    split_gemm<2, 3, 2>(hac, H2, H2 + ROWS * HID, HID, 2 * rh, whb, lane);
 #pragma unroll
     for (int ct = 0; ct < 3; ++ct) {
       const int col = 48 * cg + 16 * ct + r16;
@@ -535,9 +558,10 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   __syncthreads();
 
   // ---------------- outputs and sampling: one thread per row
-  if (threadIdx.x < ROWS && srow < a.batch) {
+  const int orow = brow0 + (int)threadIdx.x;
+  if (threadIdx.x < ROWS && orow < a.batch) {
     const float* lg = s.logit[threadIdx.x];
-    const size_t o = (size_t)srow * oslots + oslot;
+    const size_t o = (size_t)orow * oslots + oslot;
     if (a.logits_out) {
 #pragma unroll
       for (int k = 0; k < NOUT; ++k) a.logits_out[o * NOUT + k] = lg[k];
@@ -557,6 +581,8 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
       }
       if (a.logp_out) a.logp_out[o] = lpm + lpb;
     }
+  }
+  if (hb + 1 < RB) __syncthreads();   // the next block reuses every tail buffer
   }
 }
 
@@ -594,11 +620,18 @@ int qqt_mlp_act(const qqt_mlp_args* a, void* stream) {
     snprintf(g_err, sizeof(g_err), "qqt_mlp_act: sampling needs masks");
     return QQT_E_ARG;
   }
-  // one workgroup per (64-row block, player); row blocks are dealt to the 8
-  // XCDs round robin with both players' workgroups adjacent on one XCD
-  const int nrb = (a->batch + ROWS - 1) / ROWS;
+  // one workgroup per (row block, player); row blocks are dealt to the 8
+  // XCDs round robin with both players' workgroups adjacent on one XCD.
+  // Large forward batches take two 64-row blocks per workgroup (half the
+  // W0 bytes per row); rollouts keep one, for twice the workgroups.
+  const bool two = !a->sample && a->batch >= MLP_TWO_BLOCK_ROWS;
+  const int rows_wg = (two ? 2 : 1) * ROWS;
+  const int nrb = (a->batch + rows_wg - 1) / rows_wg;
   const int blocks = ((nrb + 7) / 8) * 8 * a->npid;
-  QQT_LAUNCH(QQT_KERNEL_MLP, mlp_act_kernel, dim3(blocks), dim3(NTHR), (hipStream_t)stream, *a);
+  if (two)
+    QQT_LAUNCH(QQT_KERNEL_MLP, mlp_act_kernel<2>, dim3(blocks), dim3(NTHR), (hipStream_t)stream, *a);
+  else
+    QQT_LAUNCH(QQT_KERNEL_MLP, mlp_act_kernel<1>, dim3(blocks), dim3(NTHR), (hipStream_t)stream, *a);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     snprintf(g_err, sizeof(g_err), "mlp launch failed: %s", hipGetErrorString(err));

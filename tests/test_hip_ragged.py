@@ -117,3 +117,23 @@ def test_bot_ragged_envs_match_oracle(dev, n):
         got = bot.act(*args, 1, uniforms=u)
         want = astar_act(cfg, snap, *args, 1, u)          # reach = this batch's max cap
         np.testing.assert_array_equal(got.cpu().numpy(), want.numpy(), err_msg=f"tick {t}")
+
+
+@pytest.mark.parametrize("b", [65536, 70001])
+def test_large_forward_matches_oracle(dev, b):
+    """Forward batches from 65536 rows take two 64-row blocks per workgroup;
+    a ragged one (70001 rows) ends in a half-filled workgroup."""
+    from oracle.policy import mlp_forward
+    from qqtsim.policy import HipActorCritic, default_init
+
+    params = default_init()
+    net = HipActorCritic(params, device=dev)
+    g = torch.Generator().manual_seed(b)
+    obs = (torch.rand((b, 14, 13, 13), generator=g) < 0.3).half()
+    sel = torch.cat([torch.arange(0, 300), torch.arange(b - 300, b)])
+    for pid in range(2):
+        ml, bl, v = net.forward(obs.to(dev), pid)
+        got = torch.cat([ml, bl, v[:, None]], 1).cpu()[sel].numpy()
+        rml, rbl, rv = mlp_forward(params, obs[sel], pid)
+        ref = np.concatenate([rml.numpy(), rbl.numpy(), rv.numpy()[:, None]], 1)
+        assert float(np.abs(got - ref).max()) <= 1e-3
