@@ -228,7 +228,9 @@ __device__ __forceinline__ int build_list(uint8_t* list, int e, int l, Pred pred
 }
 
 // ---------------------------------------------------------------- kernel
-template <int H, int W, int P, int LPE, int WPB>
+// FLUSH selects the instantiation that serves QQT_MODE_FLUSH: the flush code
+// lives only there, so the step kernel carries none of it.
+template <int H, int W, int P, int LPE, int WPB, bool FLUSH>
 __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf, const qqt_tick_args a) {
   using G = Geo<H, W, P, LPE>;
   constexpr int C = G::C;
@@ -647,7 +649,7 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
   // reference takes the first k of a random permutation of the free cells;
   // here the k free cells with the smallest Philox keys (stream 8, value
   // p*C + c) are taken, the same uniform k-subset law.
-  if (mode == QQT_MODE_FLUSH) {
+  if constexpr (FLUSH) {
     bool freec[KMAX];
 #pragma unroll
     for (int k = 0; k < KMAX; ++k) {
@@ -1089,8 +1091,12 @@ int launch(const qqt_sim_config* cfg, const qqt_tick_args* a, hipStream_t st) {
   constexpr int EPW = 64 / LPE;
   const int waves = (a->n_envs + EPW - 1) / EPW;
   const int blocks = (waves + WPB - 1) / WPB;
-  QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB>), dim3(blocks), dim3(64 * WPB), st, *cfg,
-             *a);
+  if (a->mode == QQT_MODE_FLUSH)
+    QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB, true>), dim3(blocks), dim3(64 * WPB), st,
+               *cfg, *a);
+  else
+    QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB, false>), dim3(blocks), dim3(64 * WPB), st,
+               *cfg, *a);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     snprintf(g_err, sizeof(g_err), "tick launch failed: %s", hipGetErrorString(err));
