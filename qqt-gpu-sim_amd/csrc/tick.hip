@@ -228,9 +228,11 @@ __device__ __forceinline__ int build_list(uint8_t* list, int e, int l, Pred pred
 }
 
 // ---------------------------------------------------------------- kernel
-// FLUSH selects the instantiation that serves QQT_MODE_FLUSH: the flush code
-// lives only there, so the step kernel carries none of it.
-template <int H, int W, int P, int LPE, int WPB, bool FLUSH>
+// KMODE fixes the mode at compile time for the two modes with an
+// instantiation of their own: QQT_MODE_STEP (the hot one, which then carries
+// no code of the other modes) and QQT_MODE_FLUSH (whose code lives only
+// there).  KMODE = -1 serves the other modes from a.mode.
+template <int H, int W, int P, int LPE, int WPB, int KMODE>
 __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf, const qqt_tick_args a) {
   using G = Geo<H, W, P, LPE>;
   constexpr int C = G::C;
@@ -249,7 +251,7 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
   const int l = lane % LPE;
   const int g = g0 + e;
   const bool valid = g < a.n_envs;
-  const int mode = a.mode;
+  const int mode = KMODE >= 0 ? KMODE : a.mode;
   const float rad = cf.radius;
   const float fmax_f = (float)cf.fuse;
 
@@ -568,10 +570,11 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
     wave_sync();
   }
 
-  bool do_reset = false;
   auto template_reset = [&]() {  // qqtsim/maps.py; re-init of sim/torch_sim.py:178-420
     const uint32_t env_id = (uint32_t)g;
-#pragma unroll
+    // rolled: one copy of the per-cell Philox draw (this code runs rarely,
+    // and its size slows every tick)
+#pragma unroll 1
     for (int k = 0; k < KMAX; ++k) {
       const int c = l + LPE * k;
       if (c >= C) continue;
@@ -593,11 +596,13 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
       cw[c] = (wall ? F_WALL : 0u) | (brick ? F_BRICK : 0u) | EMPTY_CELL;
       s.dng[e][c] = 0.0f;
     }
+    // the misc values 0..11: lane j draws block min(j, 2), lane 0 gathers
+    float ub[4];
+    philox_block(a.seed, env_id, a.epoch, STREAM_RESET_MISC, (uint32_t)min(l, 2), ub);
+    float u[12];
+#pragma unroll
+    for (int j = 0; j < 12; ++j) u[j] = __shfl(ub[j % 4], j / 4, LPE);
     if (l == 0) {
-      float u[12];
-      philox_block(a.seed, env_id, a.epoch, STREAM_RESET_MISC, 0, u);
-      philox_block(a.seed, env_id, a.epoch, STREAM_RESET_MISC, 1, u + 4);
-      philox_block(a.seed, env_id, a.epoch, STREAM_RESET_MISC, 2, u + 8);
       float py[P], px[P];
 #pragma unroll
       for (int i = 0; i < P; ++i) {
@@ -637,11 +642,10 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
     }
   };
 
-  if (mode == QQT_MODE_RESET) {
-    do_reset = valid && a.reset_mask[g] != 0;
-    if (do_reset) template_reset();
-    wave_sync();
-  }
+  // RESET mode marks its envs here and resets them at the auto-reset site
+  // below (one inline copy of the reset code); their danger map, computed
+  // in between from the old state, is cleared by the reset.
+  if (mode == QQT_MODE_RESET && l == 0) s.done[e] = valid && a.reset_mask[g] != 0;
 
   // ---- recycle flush (sim/torch_sim.py:549-596): player by player, the
   // pending lost growth becomes that many recycle crates on distinct free
@@ -649,7 +653,7 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
   // reference takes the first k of a random permutation of the free cells;
   // here the k free cells with the smallest Philox keys (stream 8, value
   // p*C + c) are taken, the same uniform k-subset law.
-  if constexpr (FLUSH) {
+  if constexpr (KMODE == QQT_MODE_FLUSH) {
     bool freec[KMAX];
 #pragma unroll
     for (int k = 0; k < KMAX; ++k) {
@@ -918,12 +922,14 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
         s.done[e] = done && a.auto_reset && valid;
       }
     }
+  }
+  if (mode == QQT_MODE_STEP || mode == QQT_MODE_RESET) {
     wave_sync();
     if (s.done[e]) template_reset();
     wave_sync();
     // hp fell this tick, judged on the post-reset record (the collect loop
     // compares after step() returns)
-    if (a.damaged && valid && l < P)
+    if (mode == QQT_MODE_STEP && a.damaged && valid && l < P)
       a.damaged[(size_t)g * P + l] = s.hp0[e][l] - pl[l][QQT_P_HP] > 0 ? 1 : 0;
   }
 
@@ -1091,11 +1097,14 @@ int launch(const qqt_sim_config* cfg, const qqt_tick_args* a, hipStream_t st) {
   constexpr int EPW = 64 / LPE;
   const int waves = (a->n_envs + EPW - 1) / EPW;
   const int blocks = (waves + WPB - 1) / WPB;
-  if (a->mode == QQT_MODE_FLUSH)
-    QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB, true>), dim3(blocks), dim3(64 * WPB), st,
-               *cfg, *a);
+  if (a->mode == QQT_MODE_STEP)
+    QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB, QQT_MODE_STEP>), dim3(blocks),
+               dim3(64 * WPB), st, *cfg, *a);
+  else if (a->mode == QQT_MODE_FLUSH)
+    QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB, QQT_MODE_FLUSH>), dim3(blocks),
+               dim3(64 * WPB), st, *cfg, *a);
   else
-    QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB, false>), dim3(blocks), dim3(64 * WPB), st,
+    QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB, -1>), dim3(blocks), dim3(64 * WPB), st,
                *cfg, *a);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
