@@ -23,7 +23,9 @@ dispatch packets of both launches of every 8th step inside the timed region
 (hipExtLaunchKernel on the launch stream), i.e. kernel begin to kernel end.  `traffic` is read from the committed
 rocprofv3 FETCH_SIZE/WRITE_SIZE summary when one exists.  `cpu_baseline`
 times the oracle (the CPU restatement of the reference path) on the host
-cores over a bounded sample of the same workload.
+cores over a bounded sample of the same workload.  `torch_gpu_bound` bounds
+the reference's own PyTorch-on-GPU step from above: its launch count per tick
+times the eager launch cost measured on this GPU.
 """
 
 from __future__ import annotations
@@ -297,10 +299,12 @@ def main():
     cpu = None
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(cfg, spec, n, args.seed, args.cpu_seconds)
+    value = n * K / el
+    tgb = torch_gpu_bound(torch, dev, n, value)
 
     out = {
         "metric": METRIC,
-        "value": n * K / el,
+        "value": value,
         "unit": "env-steps/s",
         "n_gpus": 1,
         "steps": K,
@@ -319,11 +323,60 @@ def main():
                    "max_steps": cfg.max_steps, "parallelism": "single GPU"},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "torch_gpu_bound": tgb,
         "kernels": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                         for kk, vv in v.items()} for k, v in kernels.items()},
         "done_fraction_last_tick": done_frac,
     }
     print(json.dumps(out), flush=True)
+
+
+# Kernel launches of one eager BatchedSim.step of the reference on a GPU, as
+# its authors counted them (HANDOFF_20260810.md:209, n = 20000; observe,
+# legal_mask and both act() calls come on top and are left out here).
+REF_LAUNCHES_PER_TICK = 5145
+
+
+def torch_gpu_bound(torch, dev, n, value, reps=4):
+    """Upper bound on the reference PyTorch-on-GPU path at n envs: its step
+    issues REF_LAUNCHES_PER_TICK eager kernel launches, so one tick takes at
+    least that many times the cost of one eager elementwise op on (n,13,13)
+    tensors, measured here on the same GPU and host.  The reference itself
+    does not run here; this is a floor on its tick time (an upper bound on
+    its env-steps/s), so value / bound is a lower bound on the speedup."""
+    f = torch.rand((n, 13, 13), device=dev)
+    g = torch.rand((n, 13, 13), device=dev)
+    m = f > 0.5
+    b = torch.zeros_like(m)
+
+    def cycle():                      # eight ops, one kernel launch each
+        nonlocal f, m, b
+        f = f * 0.9
+        m = f > 0.3
+        f = torch.where(m, f, g)
+        b = b | m
+        f = f + g
+        f = f.clamp(0.0, 4.0)
+        f = torch.maximum(f, g)
+        f = f * 0.5
+    for _ in range(64):
+        cycle()
+    torch.cuda.synchronize()
+    ops = 8 * (REF_LAUNCHES_PER_TICK // 8)
+    best = float("inf")
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        for _ in range(ops // 8):
+            cycle()
+        torch.cuda.synchronize()
+        best = min(best, (time.perf_counter() - t0) / ops)
+    upper = n / (REF_LAUNCHES_PER_TICK * best)
+    return {"us_per_eager_launch": round(best * 1e6, 3),
+            "ref_launches_per_tick": REF_LAUNCHES_PER_TICK,
+            "ref_env_steps_per_s_upper": round(upper, 1),
+            "speedup_lower": round(value / upper, 1),
+            "note": "floor of the reference eager step on this GPU: launch count x measured "
+                    "eager launch cost (observe/legal_mask/act launches not counted)"}
 
 
 def _calibration_copy(torch, dev):
