@@ -10,7 +10,9 @@ path:
   (sim/torch_sim.py:1135-1138); when none is given they come from Philox
   stream `STREAM_CRATE` keyed by (seed, env, tick).
 * Resets draw synthetic template maps (`qqtsim.maps.MapSpec`) from Philox
-  uniforms instead of the reference's host map generators.
+  uniforms, or with `MapSpec(kind="reference")` the reference's own map
+  modes (oracle/maps_ref.py) from Philox uniforms instead of the
+  reference's host generator.
 * The chain explosion and danger stage A run exactly `chain_cap_rounds`
   rounds (the sync-free mode the reference's tick uses,
   sim/torch_sim.py:732-833), with empty trailing rounds skipped.
@@ -37,6 +39,7 @@ import torch
 
 from . import philox
 from .grid import danger_map, rays, resolve_explosions
+from .maps_ref import reference_maps
 from .move import center_cell, move_players
 from .obs import encode_obs, legal_mask
 
@@ -138,6 +141,7 @@ class OracleSim:
         self.tick = 0           # steps taken (keys the per-tick uniforms)
         self.epoch = 0          # reset calls made (keys the template draws)
         self.explore_coef = 1.0
+        self.opp_boost = 0      # set_opp_boost (reference map modes only)
         self.exact_reference_resolve = exact_reference_resolve
         self.resolve_tiers = None
         n, h, w, p = num_envs, cfg.height, cfg.width, cfg.n_players
@@ -183,21 +187,45 @@ class OracleSim:
             return
         cfg = self.cfg
         ids = idx.cpu().numpy()
-        wall, brick, pos, bombs, blast, spd = template_maps(
-            cfg, self.spec, ids, self.seed, epoch)
         dev = self.device
-        self.wall[idx] = torch.from_numpy(wall).to(dev)
-        self.brick[idx] = torch.from_numpy(brick).to(dev)
-        self.pos[idx] = torch.from_numpy(pos).to(dev)
-        self.bombs_cap[idx] = torch.from_numpy(bombs).to(dev)
-        self.blast_cap[idx] = torch.from_numpy(blast).to(dev)
-        self.spd_g[idx] = torch.from_numpy(spd).to(dev)
-        self.lo_bombs[idx] = torch.from_numpy(bombs).to(dev)
-        self.lo_blast[idx] = torch.from_numpy(blast).to(dev)
-        self.lo_spd[idx] = torch.from_numpy(spd).to(dev)
-        self.crate_prob[idx] = cfg.growth_crate_prob
-        self.map_kind[idx] = 0
+        ref = None
+        if self.spec.kind == "reference":
+            ref = reference_maps(cfg, ids, self.seed, epoch, self.opp_boost)
+            self.wall[idx] = torch.from_numpy(ref["wall"]).to(dev)
+            self.brick[idx] = torch.from_numpy(ref["brick"]).to(dev)
+            self.pos[idx] = torch.from_numpy(ref["pos"]).to(dev)
+            c = ref["caps01"]
+            for i in range(2):          # players 2 and 3 keep theirs
+                bi = torch.from_numpy(c[:, i, 0].astype(np.int64)).to(dev)
+                zi = torch.from_numpy(c[:, i, 1].astype(np.int64)).to(dev)
+                si = torch.from_numpy(c[:, i, 2].copy()).to(dev)
+                self.bombs_cap[idx, i] = bi
+                self.blast_cap[idx, i] = zi
+                self.spd_g[idx, i] = si
+                self.lo_bombs[idx, i] = bi
+                self.lo_blast[idx, i] = zi
+                self.lo_spd[idx, i] = si
+            cp = torch.from_numpy(ref["crate_prob"]).to(dev)
+            keep = torch.isnan(cp)
+            self.crate_prob[idx] = torch.where(keep, self.crate_prob[idx], cp)
+            self.map_kind[idx] = torch.from_numpy(ref["map_kind"]).to(dev)
+        else:
+            wall, brick, pos, bombs, blast, spd = template_maps(
+                cfg, self.spec, ids, self.seed, epoch)
+            self.wall[idx] = torch.from_numpy(wall).to(dev)
+            self.brick[idx] = torch.from_numpy(brick).to(dev)
+            self.pos[idx] = torch.from_numpy(pos).to(dev)
+            self.bombs_cap[idx] = torch.from_numpy(bombs).to(dev)
+            self.blast_cap[idx] = torch.from_numpy(blast).to(dev)
+            self.spd_g[idx] = torch.from_numpy(spd).to(dev)
+            self.lo_bombs[idx] = torch.from_numpy(bombs).to(dev)
+            self.lo_blast[idx] = torch.from_numpy(blast).to(dev)
+            self.lo_spd[idx] = torch.from_numpy(spd).to(dev)
+            self.crate_prob[idx] = cfg.growth_crate_prob
+            self.map_kind[idx] = 0
         self.crate[idx] = False
+        if ref is not None:             # the open-mode start crates, after the clear
+            self.crate[idx] = torch.from_numpy(ref["crate"]).to(dev)
         self.recycle[idx] = False
         self.pending_lost[idx] = 0
         self.combo[idx] = 0
@@ -210,6 +238,11 @@ class OracleSim:
         self.since_bomb[idx] = cfg.place_dist_cooldown
         self.invuln[idx] = 0
         self.t[idx] = 0
+
+    def set_opp_boost(self, v: int) -> None:
+        """sim/torch_sim.py:422-426: player 1's starting caps tier (0, 1, 2)
+        for the reference map modes."""
+        self.opp_boost = int(v)
 
     # ------------------------------------------------------------ recycle flush
     def flush_recycle(self, flush_epoch: int) -> None:

@@ -9,9 +9,17 @@ reset needs no host round trip and is reproducible on the host:
   cells; with `brick_p > 0` every free cell outside the spawn L (the spawn
   cell and its two in-map neighbours) is a brick with that probability.
 * `open`: no walls and no bricks.
+* `reference`: the reference's own map modes, configured by the SimConfig
+  (`map_mode`, `pure_open_fraction` / `open_fraction` / `ring_fraction`,
+  `random_wall_rows`, `top_wall_rows`, `corridor_width`, `wall_density`,
+  `open_obstacle_max`, the ring and start-cap fields) and the sim's
+  `set_opp_boost` tier: corridor maps with random top/bottom wall rows and
+  side bricks, open maps with the centre cross crates, ring maps
+  (sim/torch_sim.py:178-420, sim/mapgen.py), drawn from Philox uniforms
+  on the device.  The MapSpec's other fields are unused for this kind.
 
-Spawns sit in opposite corners ((1.5, 1.5) and (h-1.5, w-1.5) for two
-players; the other two corners for players 3 and 4).  Per-player starting
+Template spawns sit in opposite corners ((1.5, 1.5) and (h-1.5, w-1.5) for
+two players; the other two corners for players 3 and 4).  Per-player starting
 caps are drawn uniformly from the inclusive ranges `bombs_cap` and
 `blast_cap`; the hit-penalty floors (`_lo_*`) are set to the drawn starts,
 matching the reference's rule that a player is clamped back to its own
@@ -22,7 +30,7 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
-KIND_CODES = {"pillars": 0, "open": 1}
+KIND_CODES = {"pillars": 0, "open": 1, "reference": 2}
 
 
 @dataclass(frozen=True)
