@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 5
+#define QQT_ABI_VERSION 6
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -61,12 +61,32 @@ typedef struct qqt_sim_config {
   /* reset template (qqtsim/maps.py MapSpec) */
   int32_t map_kind, swap_spawns, bombs_lo, bombs_hi, blast_lo, blast_hi, spawn_cooldown;
   float brick_p, spawn_speed;
+  /* the reference's map modes (map_kind QQT_MAP_REFERENCE; BatchedSim.reset_,
+   * sim/torch_sim.py:178-420, and sim/mapgen.py:15-242) */
+  int32_t top_wall_rows, random_wall_rows, corridor_width, open_obstacle_max;
+  int32_t ring_center_h, ring_center_w, open_crate_cross, max_bombs;
+  int32_t growth_bombs_start, growth_blast_start, open_growth_bombs, open_growth_blast;
+  int32_t opp_growth_bombs, opp_growth_blast;
+  float thr_pure, thr_open, thr_ring;   /* map-type thresholds: float32 of the cumulative
+                                           fractions pure, +open, +ring (corridor mode) */
+  float wall_density, ring_brick_density, ring_crate_prob;
+  float growth_speed_start, open_growth_speed, opp_growth_speed, opp_hist_mult;
+  /* spawns of the corridor, open and ring layouts (SimConfig.spawn_pos /
+   * ring_spawns, float32) and their cells r*W + c (taken from the double
+   * values, like cfg.spawn_cells()) */
+  float ref_spawn_y[3][4], ref_spawn_x[3][4];
+  int32_t ref_spawn_cell[3][4];
 } qqt_sim_config;
+
+/* map_kind values */
+#define QQT_MAP_PILLARS 0    /* template: border + even/even pillars, bricks w.p. brick_p */
+#define QQT_MAP_OPEN 1       /* template: empty grid */
+#define QQT_MAP_REFERENCE 2  /* the reference's corridor / open / ring modes */
 
 /* modes of qqt_tick */
 #define QQT_MODE_STEP 0     /* one tick, then auto-reset, observe and masks */
 #define QQT_MODE_OBSERVE 1  /* observe + masks of the current state only */
-#define QQT_MODE_RESET 2    /* template reset where reset_mask, then observe */
+#define QQT_MODE_RESET 2    /* map reset (map_kind) where reset_mask, then observe */
 #define QQT_MODE_PROBE 3    /* largest bomb_blast after this tick's placement */
 #define QQT_MODE_FLUSH 4    /* recycle flush (each player's pending lost growth becomes
                                recycle crates on random free cells), then observe */
@@ -109,6 +129,9 @@ typedef struct qqt_tick_args {
                                  (train/ppo.py:251); or NULL */
   const uint8_t* recycle_excl; /* FLUSH: [H*W] 1 = never a recycle crate (spawn
                                  neighbourhoods, the open-mode cross band) */
+  int32_t opp_boost;          /* QQT_MAP_REFERENCE resets: player 1's start tier
+                                 (0 as player 0, 1 x opp_hist_mult, 2 opp_growth_*;
+                                 BatchedSim.set_opp_boost, sim/torch_sim.py:422-453) */
 } qqt_tick_args;
 
 /* MLP actor/critic forward (+ masked sampling).  Weights are the packed

@@ -231,8 +231,10 @@ __device__ __forceinline__ int build_list(uint8_t* list, int e, int l, Pred pred
 // KMODE fixes the mode at compile time for the two modes with an
 // instantiation of their own: QQT_MODE_STEP (the hot one, which then carries
 // no code of the other modes) and QQT_MODE_FLUSH (whose code lives only
-// there).  KMODE = -1 serves the other modes from a.mode.
-template <int H, int W, int P, int LPE, int WPB, int KMODE>
+// there).  KMODE = -1 serves the other modes from a.mode.  MAPS selects the
+// reset's map source: 0 the templates, 1 the reference's map modes (each
+// kernel carries one of the two).
+template <int H, int W, int P, int LPE, int WPB, int KMODE, int MAPS>
 __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf, const qqt_tick_args a) {
   using G = Geo<H, W, P, LPE>;
   constexpr int C = G::C;
@@ -642,6 +644,179 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
     }
   };
 
+  // The reference's reset map modes (BatchedSim.reset_, sim/torch_sim.py:
+  // 178-420; generators sim/mapgen.py:15-242).  Every lane of the env runs
+  // it.  Draws: STREAM_RESET_MISC values 0 map type, 1 top wall rows,
+  // 2 spawn swap, 3 obstacle count, 4.. the corridor edge segments (start,
+  // length, on) x 4 columns then the horizontal one; STREAM_RESET_CELL value
+  // c the ring band's brick draw, C + c the open obstacles' keys (the n
+  // cells with the smallest (key, cell)).
+  auto reference_reset = [&]() {
+    const uint32_t env_id = (uint32_t)g;
+    float ub[4];
+    philox_block(a.seed, env_id, a.epoch, STREAM_RESET_MISC, (uint32_t)min(l, 4), ub);
+    float u[19];
+#pragma unroll
+    for (int j = 0; j < 19; ++j) u[j] = __shfl(ub[j % 4], j / 4, LPE);
+    // map kind (uniform over the env's lanes): 0 corridor, 1 open, 2 ring
+    int kind = 1;
+    bool pure = false;
+    if (cf.corridor) {
+      kind = u[0] < cf.thr_open ? 1 : u[0] < cf.thr_ring ? 2 : 0;
+      pure = u[0] < cf.thr_pure;
+    }
+    const int T = cf.top_wall_rows;
+    const int top = cf.random_wall_rows ? min((int)floorf(u[1] * (float)(T + 1)), T) : T;
+    const int bot = cf.random_wall_rows ? T - top : 0;
+    const int sp_mode = cf.corridor ? 0 : 1;    // cfg.spawn_cells(): the mode's own spawns
+    const int sp_kind = kind == 0 ? 0 : kind == 2 ? 2 : 1;
+    auto near_spawn = [&](int set, int r, int col) {
+      bool nb = false;
+#pragma unroll
+      for (int i = 0; i < P; ++i) {
+        const int sc = cf.ref_spawn_cell[set][i];
+        const int dr = r - sc / W, dc = col - sc % W;
+        nb |= (dr == 0 && (dc == 0 || dc == 1 || dc == -1)) || (dc == 0 && (dr == 1 || dr == -1));
+      }
+      return nb;
+    };
+    // open obstacles: bit k marks cell l + LPE k
+    uint32_t obst = 0;
+    const int nmax = cf.open_obstacle_max;
+    const int nobst = nmax > 0 ? min((int)floorf(u[3] * (float)(nmax + 1)), nmax) : 0;
+    if (kind == 1 && !pure && nobst > 0) {
+      uint64_t key[KMAX];
+#pragma unroll
+      for (int k = 0; k < KMAX; ++k) {
+        const int c = l + LPE * k;
+        key[k] = ~0ull;
+        if (c < C) {
+          const float uk = philox_uniform(a.seed, env_id, a.epoch, STREAM_RESET_CELL,
+                                          (uint32_t)(C + c));
+          key[k] = ((uint64_t)__float_as_uint(uk) << 32) | (uint32_t)c;
+        }
+      }
+      for (int t = 0; t < nobst; ++t) {
+        uint64_t mn = key[0];
+#pragma unroll
+        for (int k = 1; k < KMAX; ++k) mn = key[k] < mn ? key[k] : mn;
+#pragma unroll
+        for (int m = 1; m < LPE; m <<= 1) {
+          const uint64_t o = __shfl_xor(mn, m, LPE);
+          mn = o < mn ? o : mn;
+        }
+#pragma unroll
+        for (int k = 0; k < KMAX; ++k)
+          if (key[k] == mn) {
+            obst |= 1u << k;
+            key[k] = ~0ull;
+          }
+      }
+    }
+    // corridor geometry and edge segments (sim/mapgen.py:101-199)
+    const int c0 = (W - cf.corridor_width) / 2, c1 = c0 + cf.corridor_width;
+    const bool segs = kind == 0 && cf.wall_density > 0.0f;
+    const int ecol[4] = {c0, c0 + 1, c1 - 2, c1 - 1};
+    int vs[4], vl[4];
+    bool va[4];
+#pragma unroll
+    for (int ci = 0; ci < 4; ++ci) {
+      const float us = u[4 + 3 * ci], ul = u[5 + 3 * ci], ua = u[6 + 3 * ci];
+      vs[ci] = cf.random_wall_rows
+          ? (int)(us * (float)max(H - bot - 4 - top, 1) + (float)top)
+          : (int)(us * (float)(H - T - 4) + (float)T);
+      vl[ci] = 2 + (int)(ul * 3.0f);
+      va[ci] = segs && ua < cf.wall_density && ecol[ci] >= c0 && ecol[ci] < c1;
+    }
+    const int hs = (int)(u[16] * (float)(c1 - c0 - 4) + (float)c0);
+    const int hl = 2 + (int)(u[17] * 3.0f);
+    const bool ha = segs && c1 - c0 > 4 && u[18] < cf.wall_density;
+    const int hr0 = cf.random_wall_rows ? top : T;
+    const int hr1 = cf.random_wall_rows ? top + 2 : T + min(2, H - T);
+    // ring geometry (sim/mapgen.py:202-242)
+    const int r0 = (H - cf.ring_center_h) / 2, q0 = (W - cf.ring_center_w) / 2;
+    const int r1 = r0 + cf.ring_center_h, q1 = q0 + cf.ring_center_w;
+    const int cy = (H - 1) / 2, cx = (W - 1) / 2;
+#pragma unroll 1
+    for (int k = 0; k < KMAX; ++k) {
+      const int c = l + LPE * k;
+      if (c >= C) continue;
+      const int r = c / W, col = c % W;
+      bool wall = false, brick = false, crate = false;
+      if (kind == 0) {
+        wall = cf.random_wall_rows ? (r < top || r >= H - bot) : r < T;
+        brick = (col < c0 || col >= c1) && r >= (cf.random_wall_rows ? top : T);
+#pragma unroll
+        for (int ci = 0; ci < 4; ++ci)
+          brick |= va[ci] && col == ecol[ci] && r >= vs[ci] && r < vs[ci] + vl[ci];
+        brick |= ha && r >= hr0 && r < hr1 && col >= c0 && col < c1 && col >= hs && col < hs + hl;
+        if (near_spawn(sp_mode, r, col)) wall = brick = false;
+      } else if (kind == 2) {
+        wall = r >= r0 && r < r1 && col >= q0 && col < q1;
+        const bool band = !wall && r >= r0 - 1 && r <= r1 && col >= q0 - 1 && col <= q1;
+        if (band && !near_spawn(2, r, col))
+          brick = philox_uniform(a.seed, env_id, a.epoch, STREAM_RESET_CELL, (uint32_t)c) <
+                  cf.ring_brick_density;
+      } else {
+        wall = ((obst >> k) & 1u) && !near_spawn(sp_mode, r, col);
+        crate = cf.corridor && cf.open_crate_cross &&
+                (r == cy - 1 || r == cy || col == cx - 1 || col == cx) && !near_spawn(1, r, col);
+      }
+      cw[c] = (wall ? F_WALL : 0u) | (brick ? F_BRICK : 0u) | (crate ? F_CRATE : 0u) | EMPTY_CELL;
+      s.dng[e][c] = 0.0f;
+    }
+    if (l == 0) {
+      int b0, z0;
+      float s0;
+      if (!cf.corridor) {
+        b0 = cf.max_bombs; z0 = cf.blast; s0 = 1.0f;
+      } else if (kind == 1) {
+        b0 = cf.open_growth_bombs; z0 = cf.open_growth_blast; s0 = cf.open_growth_speed;
+      } else {
+        b0 = cf.growth_bombs_start; z0 = cf.growth_blast_start; s0 = cf.growth_speed_start;
+      }
+      int b1 = b0, z1 = z0;
+      float s1 = s0;
+      if (a.opp_boost == 2) {
+        b1 = cf.opp_growth_bombs; z1 = cf.opp_growth_blast; s1 = cf.opp_growth_speed;
+      } else if (a.opp_boost == 1) {
+        b1 = (int)fminf(rintf((float)b0 * cf.opp_hist_mult), (float)cf.growth_bombs_max);
+        z1 = (int)fminf(rintf((float)z0 * cf.opp_hist_mult), (float)cf.growth_blast_max);
+        s1 = fminf(s0 * cf.opp_hist_mult, cf.growth_speed_max);
+      }
+      const bool swap = u[2] < 0.5f;
+#pragma unroll
+      for (int i = 0; i < P; ++i) {
+        const int si = (swap && i < 2) ? 1 - i : i;
+        int32_t* q = pl[i];
+        q[QQT_P_Y] = __float_as_int(cf.ref_spawn_y[sp_kind][si]);
+        q[QQT_P_X] = __float_as_int(cf.ref_spawn_x[sp_kind][si]);
+        q[QQT_P_ALIVE] = 1;
+        q[QQT_P_HP] = cf.max_hp;
+        q[QQT_P_SINCE_BOMB] = cf.spawn_cooldown;
+        q[QQT_P_INVULN] = 0;
+        q[QQT_P_COMBO] = 0;
+        q[QQT_P_LAST_HIT] = -1000000000;
+        q[QQT_P_PENDING_LOST] = 0;
+        if (i < 2) {            // players 2 and 3 keep caps, speed and floors
+          const int bc = i == 0 ? b0 : b1, zc = i == 0 ? z0 : z1;
+          const float sp = i == 0 ? s0 : s1;
+          q[QQT_P_BOMBS_CAP] = bc;
+          q[QQT_P_BLAST_CAP] = zc;
+          q[QQT_P_SPD] = __float_as_int(sp);
+          q[QQT_P_LO_BOMBS] = bc;
+          q[QQT_P_LO_BLAST] = zc;
+          q[QQT_P_LO_SPD] = __float_as_int(sp);
+        }
+      }
+      s.ev[e][QQT_E_T] = 0;
+      if (cf.corridor)
+        s.ev[e][QQT_E_CRATE_PROB] = __float_as_int(
+            kind == 1 ? 1.0f : kind == 2 ? cf.ring_crate_prob : cf.growth_crate_prob);
+      s.ev[e][QQT_E_MAP_KIND] = kind;
+    }
+  };
+
   // RESET mode marks its envs here and resets them at the auto-reset site
   // below (one inline copy of the reset code); their danger map, computed
   // in between from the old state, is cleared by the reset.
@@ -925,7 +1100,10 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
   }
   if (mode == QQT_MODE_STEP || mode == QQT_MODE_RESET) {
     wave_sync();
-    if (s.done[e]) template_reset();
+    if (s.done[e]) {
+      if constexpr (MAPS == 1) reference_reset();
+      else template_reset();
+    }
     wave_sync();
     // hp fell this tick, judged on the post-reset record (the collect loop
     // compares after step() returns)
@@ -1097,15 +1275,21 @@ int launch(const qqt_sim_config* cfg, const qqt_tick_args* a, hipStream_t st) {
   constexpr int EPW = 64 / LPE;
   const int waves = (a->n_envs + EPW - 1) / EPW;
   const int blocks = (waves + WPB - 1) / WPB;
-  if (a->mode == QQT_MODE_STEP)
-    QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB, QQT_MODE_STEP>), dim3(blocks),
-               dim3(64 * WPB), st, *cfg, *a);
-  else if (a->mode == QQT_MODE_FLUSH)
-    QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB, QQT_MODE_FLUSH>), dim3(blocks),
-               dim3(64 * WPB), st, *cfg, *a);
-  else
-    QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB, -1>), dim3(blocks), dim3(64 * WPB), st,
+  const bool ref = cfg->map_kind == QQT_MAP_REFERENCE;
+  const dim3 grid(blocks), block(64 * WPB);
+  if (a->mode == QQT_MODE_FLUSH)     // no reset in a flush
+    QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB, QQT_MODE_FLUSH, 0>), grid, block, st,
                *cfg, *a);
+  else if (a->mode == QQT_MODE_STEP && !ref)
+    QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB, QQT_MODE_STEP, 0>), grid, block, st,
+               *cfg, *a);
+  else if (a->mode == QQT_MODE_STEP)
+    QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB, QQT_MODE_STEP, 1>), grid, block, st,
+               *cfg, *a);
+  else if (!ref)
+    QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB, -1, 0>), grid, block, st, *cfg, *a);
+  else
+    QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB, -1, 1>), grid, block, st, *cfg, *a);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     snprintf(g_err, sizeof(g_err), "tick launch failed: %s", hipGetErrorString(err));
@@ -1143,6 +1327,20 @@ int qqt_tick(const qqt_sim_config* cfg, const qqt_tick_args* a, void* stream) {
     return fail(QQT_E_ARG, "chain_cap_rounds must be in 0..64");
   if (cfg->bombs_lo > cfg->bombs_hi || cfg->blast_lo > cfg->blast_hi)
     return fail(QQT_E_ARG, "bad cap ranges");
+  if (cfg->map_kind < QQT_MAP_PILLARS || cfg->map_kind > QQT_MAP_REFERENCE)
+    return fail(QQT_E_ARG, "bad map_kind");
+  if (cfg->map_kind == QQT_MAP_REFERENCE) {
+    const int h = cfg->height, w = cfg->width, p = cfg->n_players;
+    if (cfg->corridor_width < 3 || cfg->corridor_width > w - 2 || cfg->top_wall_rows < 1 ||
+        cfg->top_wall_rows > h - 3 || cfg->ring_center_h < 3 || cfg->ring_center_h > h - 4 ||
+        cfg->ring_center_w < 3 || cfg->ring_center_w > w - 4 || cfg->open_obstacle_max < 0 ||
+        cfg->open_obstacle_max > h * w || a->opp_boost < 0 || a->opp_boost > 2)
+      return fail(QQT_E_ARG, "reference map mode geometry out of range");
+    for (int k = 0; k < 3; ++k)
+      for (int i = 0; i < p; ++i)
+        if (cfg->ref_spawn_cell[k][i] < 0 || cfg->ref_spawn_cell[k][i] >= h * w)
+          return fail(QQT_E_ARG, "reference spawn cell outside the grid");
+  }
   hipStream_t st = (hipStream_t)stream;
   const int h = cfg->height, w = cfg->width, p = cfg->n_players;
   if (h == 13 && w == 13 && p == 2) return launch<13, 13, 2>(cfg, a, st);

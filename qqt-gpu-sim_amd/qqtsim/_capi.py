@@ -14,9 +14,10 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 
 from ._build import LIB
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 MODE_STEP, MODE_OBSERVE, MODE_RESET, MODE_PROBE, MODE_FLUSH = 0, 1, 2, 3, 4
+MAP_PILLARS, MAP_OPEN, MAP_REFERENCE = 0, 1, 2
 
 _i32, _f32, _u32, _u64, _vp = (ctypes.c_int32, ctypes.c_float, ctypes.c_uint32,
                                ctypes.c_uint64, ctypes.c_void_p)
@@ -35,7 +36,17 @@ class SimConfigC(ctypes.Structure):
         "growth_speed_max", "hit_speed_drop", "recycle_crate_prob", "growth_crate_prob")] + [
         (n, _i32) for n in ("map_kind", "swap_spawns", "bombs_lo", "bombs_hi", "blast_lo",
                             "blast_hi", "spawn_cooldown")] + [
-        (n, _f32) for n in ("brick_p", "spawn_speed")]
+        (n, _f32) for n in ("brick_p", "spawn_speed")] + [
+        (n, _i32) for n in ("top_wall_rows", "random_wall_rows", "corridor_width",
+                            "open_obstacle_max", "ring_center_h", "ring_center_w",
+                            "open_crate_cross", "max_bombs", "growth_bombs_start",
+                            "growth_blast_start", "open_growth_bombs", "open_growth_blast",
+                            "opp_growth_bombs", "opp_growth_blast")] + [
+        (n, _f32) for n in ("thr_pure", "thr_open", "thr_ring", "wall_density",
+                            "ring_brick_density", "ring_crate_prob", "growth_speed_start",
+                            "open_growth_speed", "opp_growth_speed", "opp_hist_mult")] + [
+        ("ref_spawn_y", (_f32 * 4) * 3), ("ref_spawn_x", (_f32 * 4) * 3),
+        ("ref_spawn_cell", (_i32 * 4) * 3)]
 
 
 class TickArgsC(ctypes.Structure):
@@ -45,7 +56,7 @@ class TickArgsC(ctypes.Structure):
         (n, _vp) for n in ("cells", "players", "envs", "actions", "actions_i8", "crate_u",
                            "reset_mask", "reward", "done", "n_alive", "died", "winner",
                            "covered", "triggered", "obs", "move_mask", "bomb_mask",
-                           "probe_out", "damaged", "recycle_excl")]
+                           "probe_out", "damaged", "recycle_excl")] + [("opp_boost", _i32)]
 
 
 class MlpArgsC(ctypes.Structure):

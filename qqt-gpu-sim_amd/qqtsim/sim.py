@@ -17,7 +17,9 @@ Randomness is injected (see `oracle/philox.py` for the shared layout):
 crate-hit / growth uniforms per tick come from Philox(seed, env, tick) unless
 `step(..., crate_u=(P,2,N) float32)` passes them, as the reference's
 `torch.rand(2PN).view(P,2,N)` would (sim/torch_sim.py:1135-1138).  Resets
-draw template maps (`MapSpec`) from Philox(seed, env, epoch).
+draw template maps (`MapSpec`), or with `MapSpec(kind="reference")` the
+reference's own corridor / open / ring map modes, from Philox(seed, env,
+epoch).
 
 Explosion tiers: the reference binds the first tick's blast hint into its
 explosion resolver (sim/torch_sim.py:809-833, `_h=hint`), so later ticks
@@ -74,7 +76,41 @@ def config_struct(cfg: SimConfig, spec: MapSpec) -> _capi.SimConfigC:
         setattr(c, k, int(v))
     for k, v in floats.items():
         setattr(c, k, float(v))
+    _reference_map_fields(c, cfg)
     return c
+
+
+def _reference_map_fields(c, cfg: SimConfig) -> None:
+    """Fields of the reference map modes (sim/torch_sim.py:178-420): the
+    cumulative map-type thresholds as the reference's Python sums, and the
+    corridor / open / ring spawn tables with their cells taken from the
+    double values (cfg.spawn_cells())."""
+    h, w, p = cfg.height, cfg.width, cfg.n_players
+    for k in ("top_wall_rows", "corridor_width", "open_obstacle_max", "ring_center_h",
+              "ring_center_w", "max_bombs", "growth_bombs_start", "growth_blast_start",
+              "open_growth_bombs", "open_growth_blast", "opp_growth_bombs", "opp_growth_blast"):
+        setattr(c, k, int(getattr(cfg, k)))
+    c.random_wall_rows = int(bool(cfg.random_wall_rows))
+    c.open_crate_cross = int(bool(cfg.open_crate_cross))
+    for k in ("wall_density", "ring_brick_density", "ring_crate_prob", "growth_speed_start",
+              "open_growth_speed", "opp_growth_speed", "opp_hist_mult"):
+        setattr(c, k, float(getattr(cfg, k)))
+    pf = cfg.pure_open_fraction
+    c.thr_pure = pf
+    c.thr_open = pf + cfg.open_fraction
+    c.thr_ring = pf + cfg.open_fraction + cfg.ring_fraction
+    row_c = (cfg.top_wall_rows + (h - 1)) / 2.0 + 0.5
+    c0 = (w - cfg.corridor_width) / 2.0 + 0.5
+    step = (cfg.corridor_width - 2) / max(1, p - 1)
+    row_o = (h - 1) / 2.0 + 0.5
+    tables = ([(row_c, c0 + 1.0 + i * step) for i in range(p)],
+              [(row_o, (w - 1) * (i + 1) / (p + 1) + 0.5) for i in range(p)],
+              [(1.5, 1.5), (1.5, w - 0.5), (h - 0.5, w - 0.5), (h - 0.5, 1.5)][:p])
+    for k, spawns in enumerate(tables):
+        for i, (y, x) in enumerate(spawns):
+            c.ref_spawn_y[k][i] = y
+            c.ref_spawn_x[k][i] = x
+            c.ref_spawn_cell[k][i] = int(y) * w + int(x)
 
 
 class _Info(dict):
@@ -131,6 +167,16 @@ class HipBatchedSim:
         self._cells = torch.zeros((n, h * w), **i32)
         self._players = torch.zeros((n, p, st.P_SLOTS), **i32)
         self._envs = torch.zeros((n, st.E_SLOTS), **i32)
+        # the reference's initial values where no reset writes (sim/torch_sim.py:
+        # 80-87, 105, 147-149): speed 1, penalty floors at the growth starts,
+        # crate probability growth_crate_prob
+        f32bits = lambda v: torch.tensor([v], dtype=torch.float32).view(torch.int32).item()  # noqa: E731
+        self._players[..., st.P_SPD] = f32bits(1.0)
+        self._players[..., st.P_LOB] = cfg.growth_bombs_start
+        self._players[..., st.P_LOZ] = cfg.growth_blast_start
+        self._players[..., st.P_LOS] = f32bits(cfg.growth_speed_start)
+        self._envs[:, st.E_CRATE_PROB] = f32bits(cfg.growth_crate_prob)
+        self._opp_boost = 0
         self._obs = torch.zeros((n, cfg.n_channels, h, w), dtype=torch.float16, device=d)
         self._mm = torch.zeros((n, p, N_MOVES), dtype=torch.uint8, device=d)
         self._bm = torch.zeros((n, p, N_BOMB), dtype=torch.uint8, device=d)
@@ -156,6 +202,7 @@ class HipBatchedSim:
         a.explore_coef = float(self.explore_coef)
         a.danger_coef = float(self.explore_coef * self.cfg.danger_penalty)
         a.seed = self.seed & 0xFFFFFFFFFFFFFFFF
+        a.opp_boost = self._opp_boost
         a.tick = self.tick & 0xFFFFFFFF
         a.epoch = (self.epoch if epoch is None else epoch) & 0xFFFFFFFF
         a.cells = self._cells.data_ptr()
@@ -197,7 +244,8 @@ class HipBatchedSim:
         self.reset_(torch.ones(self.num_envs, dtype=torch.bool, device=self.device))
 
     def reset_(self, mask: torch.Tensor) -> None:
-        """Template reset of the envs where `mask` is True (sim/torch_sim.py:178-420)."""
+        """Reset of the envs where `mask` is True (sim/torch_sim.py:178-420):
+        template maps, or the reference's map modes for MapSpec("reference")."""
         m = self._as_device(mask, torch.uint8, (self.num_envs,))
         self._launch(_capi.MODE_RESET, reset_mask=m)
         self.epoch += 1
@@ -263,7 +311,11 @@ class HipBatchedSim:
         self.explore_coef = float(v)
 
     def set_opp_boost(self, v: int) -> None:
-        """Accepted for API parity; template resets draw caps from the MapSpec."""
+        """Player 1's starting tier for the reference map modes
+        (sim/torch_sim.py:422-426; 0, 1 or 2).  Template resets draw caps
+        from the MapSpec instead."""
+        if int(v) not in (0, 1, 2):
+            raise ValueError("opp boost must be 0, 1 or 2")
         self._opp_boost = int(v)
 
     def recycle_excl(self) -> torch.Tensor:
