@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 6
+#define QQT_ABI_VERSION 7
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -167,6 +167,11 @@ typedef struct qqt_mlp_args {
   float* logits_out;         /* [B][out_slots][8]: 5 move, 2 bomb, value; or NULL */
   int32_t out_slots;         /* player slots per output row (0 = npid) */
   int32_t out_slot;          /* slot written when npid == 1 */
+  float* z1_out;             /* [B][128] or NULL.  When set (npid 1, sample 0) the
+                                launch computes the first layer only,
+                                z1 = obs W0[pid]^T + b0 in float32 (the training
+                                forward's input to LayerNorm 1), and writes
+                                nothing else */
 } qqt_mlp_args;
 
 /* astar rule bot for one player (sim/bots.py:267-508, astar_attack with no
@@ -248,6 +253,30 @@ typedef struct qqt_gae_args {
 /* One launch of the GAE scan (replaces compute_gae, train/ppo.py:101-110). */
 int qqt_gae(const qqt_gae_args* args, void* stream);
 
+/* First-layer weight gradient of the PPO update's backward pass (the
+ * product loss.backward() forms for shared.0.weight, train/ppo.py:364-437
+ * through train/model.py:121-147), for the view-permuted first layer of
+ * one player:  dw0[h][k] = sum_b dz1[b][h] * obs[b][k]  (h < 128, k < k0).
+ * float16 MFMA with float32 accumulation; dz1 is multiplied by *dz_scale
+ * (a power of two chosen by the caller so that max|dz1| * scale <= 2^14;
+ * NULL = 1) before its float16 hi/lo split and the result is divided by it.
+ * Deterministic: fixed batch chunks summed in chunk order.  The caller
+ * provides the workspace (qqt_l1_grad_workspace_floats floats). */
+typedef struct qqt_l1_grad_args {
+  int32_t batch;              /* rows B */
+  int32_t k0;                 /* observation width C*H*W (even) */
+  int32_t obs_stride;         /* elements between observation rows (even) */
+  int32_t reserved;
+  int64_t workspace_floats;   /* size of workspace */
+  const uint16_t* obs;        /* [B][obs_stride] float16 bits, 4-byte aligned */
+  const float* dz1;           /* [B][128], 8-byte aligned */
+  const float* dz_scale;      /* [1] device float, or NULL */
+  float* workspace;
+  float* dw0;                 /* [128][k0] */
+} qqt_l1_grad_args;
+int64_t qqt_l1_grad_workspace_floats(int32_t batch, int32_t k0);
+int qqt_l1_grad(const qqt_l1_grad_args* args, void* stream);
+
 /* Dispatch timing for benchmark harnesses (no counterpart in the reference:
  * its bench times whole steps with host clocks).  qqt_timing_arm(n) times
  * the next n kernel launches made through this library: each records a
@@ -258,7 +287,7 @@ int qqt_gae(const qqt_gae_args* args, void* stream);
  * most 4096 launches are timed between collects.  Allocates no device
  * memory (the event pool is created by the first arm). */
 enum { QQT_KERNEL_TICK = 0, QQT_KERNEL_MLP = 1, QQT_KERNEL_BOT = 2, QQT_KERNEL_REACH = 3,
-       QQT_KERNEL_GAE = 4, QQT_KERNEL_KINDS = 5 };
+       QQT_KERNEL_GAE = 4, QQT_KERNEL_L1GRAD = 5, QQT_KERNEL_KINDS = 6 };
 int qqt_timing_arm(int32_t launches);
 int qqt_timing_collect(double* ms, int32_t* count, int32_t n_kinds);
 

@@ -289,7 +289,8 @@ __device__ __forceinline__ int sample_masked(const float* logit, const uint8_t* 
 
 // RB row blocks of 64 per workgroup: RB = 2 halves the W0 bytes each row
 // costs (large forward batches, no sampling); the tail runs once per block.
-template <int RB>
+// Z1: the first-layer-only instantiation of the training forward (z1_out).
+template <int RB, bool Z1>
 __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   static_assert(RB == 1 || RB == 2, "one or two row blocks per workgroup");
   constexpr int RT = 4 * RB;               // layer-1 row tiles per wavefront
@@ -484,6 +485,23 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
           *f1_at(s.xs_h1, 16 * rt + 4 * q + j, 32 * cg + 16 * ct + r16) = acc[4 * hb + rt][ct][j];
   }
   __syncthreads();
+  if constexpr (Z1) {   // first layer only (the training forward): z1 = (f1 + f) + b0
+    const int t = threadIdx.x, row = t >> 3, j = t & 7, orow = brow0 + row;
+    if (orow < a.batch) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = 32 * i + 4 * j;
+        const float4 x = *reinterpret_cast<const float4*>(&s.f[row][c]);
+        const float4 z = *reinterpret_cast<const float4*>(f1_at(s.xs_h1, row, c));
+        const float4 b = *reinterpret_cast<const float4*>(&s.vec[V_B0 + c]);
+        *reinterpret_cast<float4*>(a.z1_out + (size_t)orow * HID + c) =
+            make_float4((z.x + x.x) + b.x, (z.y + x.y) + b.y, (z.z + x.z) + b.z,
+                        (z.w + x.w) + b.w);
+      }
+    }
+    if (hb + 1 < RB) __syncthreads();   // the next block rewrites both tiles
+    continue;
+  }
   layernorm_rows(s, s.xs_h1, V_B0, V_G1, V_BE1, H1);
   __syncthreads();
 
@@ -620,6 +638,10 @@ int qqt_mlp_act(const qqt_mlp_args* a, void* stream) {
     snprintf(g_err, sizeof(g_err), "qqt_mlp_act: sampling needs masks");
     return QQT_E_ARG;
   }
+  if (a->z1_out && (a->npid != 1 || a->sample || (((uintptr_t)a->z1_out) & 15))) {
+    snprintf(g_err, sizeof(g_err), "qqt_mlp_act: z1_out needs npid 1, no sampling, 16-byte alignment");
+    return QQT_E_ARG;
+  }
   // one workgroup per (row block, player); row blocks are dealt to the 8
   // XCDs round robin with both players' workgroups adjacent on one XCD.
   // Large forward batches take two 64-row blocks per workgroup (half the
@@ -628,10 +650,15 @@ int qqt_mlp_act(const qqt_mlp_args* a, void* stream) {
   const int rows_wg = (two ? 2 : 1) * ROWS;
   const int nrb = (a->batch + rows_wg - 1) / rows_wg;
   const int blocks = ((nrb + 7) / 8) * 8 * a->npid;
-  if (two)
-    QQT_LAUNCH(QQT_KERNEL_MLP, mlp_act_kernel<2>, dim3(blocks), dim3(NTHR), (hipStream_t)stream, *a);
+  hipStream_t st = (hipStream_t)stream;
+  if (a->z1_out && two)
+    QQT_LAUNCH(QQT_KERNEL_MLP, (mlp_act_kernel<2, true>), dim3(blocks), dim3(NTHR), st, *a);
+  else if (a->z1_out)
+    QQT_LAUNCH(QQT_KERNEL_MLP, (mlp_act_kernel<1, true>), dim3(blocks), dim3(NTHR), st, *a);
+  else if (two)
+    QQT_LAUNCH(QQT_KERNEL_MLP, (mlp_act_kernel<2, false>), dim3(blocks), dim3(NTHR), st, *a);
   else
-    QQT_LAUNCH(QQT_KERNEL_MLP, mlp_act_kernel<1>, dim3(blocks), dim3(NTHR), (hipStream_t)stream, *a);
+    QQT_LAUNCH(QQT_KERNEL_MLP, (mlp_act_kernel<1, false>), dim3(blocks), dim3(NTHR), st, *a);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     snprintf(g_err, sizeof(g_err), "mlp launch failed: %s", hipGetErrorString(err));

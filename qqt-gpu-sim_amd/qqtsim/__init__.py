@@ -2,12 +2,15 @@
 
 `HipBatchedSim` (the reference's `BatchedSim` API), `HipActorCritic` (the mlp
 `ActorCritic.act/forward/evaluate` API), `Rollout` (observe -> act -> step in
-two launches) and `make_sim`, all over hand-written HIP kernels in
+two launches), `HipRolloutBuffer` / `compute_gae`, `HipMlpActorCritic` /
+`ppo_update` (the PPO update with the first layer's forward and weight
+gradient on MFMA) and `make_sim`, all over hand-written HIP kernels in
 libqqt_hip.so (C ABI in include/qqt_hip.h).  Importing the package does not
 load the library; the first sim or policy does, and raises if it is missing.
 """
 
 from .bots import HipAstarBot
+from .learn import HipMlpActorCritic, PPOConfig, ppo_update
 from .config import SimConfig, corridor_training_config
 from .factory import make_sim
 from .maps import BOMB_STRESS_40, CORRIDOR_70, OPEN_PILLARS, MapSpec
@@ -18,4 +21,5 @@ from .sim import HipBatchedSim
 
 __all__ = ["HipAstarBot", "SimConfig", "corridor_training_config", "make_sim", "MapSpec", "OPEN_PILLARS",
            "CORRIDOR_70", "BOMB_STRESS_40", "HipActorCritic", "default_init", "Rollout",
-           "HipBatchedSim", "HipRolloutBuffer", "compute_gae"]
+           "HipBatchedSim", "HipRolloutBuffer", "compute_gae", "HipMlpActorCritic", "PPOConfig",
+           "ppo_update"]

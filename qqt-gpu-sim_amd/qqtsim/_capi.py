@@ -14,7 +14,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 
 from ._build import LIB
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 MODE_STEP, MODE_OBSERVE, MODE_RESET, MODE_PROBE, MODE_FLUSH = 0, 1, 2, 3, 4
 MAP_PILLARS, MAP_OPEN, MAP_REFERENCE = 0, 1, 2
@@ -67,7 +67,7 @@ class MlpArgsC(ctypes.Structure):
         (n, _vp) for n in ("obs", "w0", "w1", "wh", "wf", "w1_lo", "wh_lo", "wf_lo", "b0", "ln1_w", "ln1_b", "b1",
                            "ln2_w", "ln2_b", "bh", "bf", "move_mask", "bomb_mask", "uniforms",
                            "actions", "actions_i8", "logp_out", "value_out", "logits_out")] + [
-        ("out_slots", _i32), ("out_slot", _i32)]
+        ("out_slots", _i32), ("out_slot", _i32), ("z1_out", _vp)]
 
 
 class BotArgsC(ctypes.Structure):
@@ -75,6 +75,12 @@ class BotArgsC(ctypes.Structure):
                 ("reach_mode", _i32), ("reach_slot", _i32)] + [
         (n, _vp) for n in ("cells", "players", "obs", "move_mask", "bomb_mask", "uniforms",
                            "reach", "actions", "actions_i8")]
+
+
+class L1GradArgsC(ctypes.Structure):
+    _fields_ = [("batch", _i32), ("k0", _i32), ("obs_stride", _i32), ("reserved", _i32),
+                ("workspace_floats", ctypes.c_int64)] + [
+        (n, _vp) for n in ("obs", "dz1", "dz_scale", "workspace", "dw0")]
 
 
 class GaeArgsC(ctypes.Structure):
@@ -104,6 +110,10 @@ def lib():
         L.qqt_bot_act.argtypes = [ctypes.POINTER(SimConfigC), ctypes.POINTER(BotArgsC), _vp]
         L.qqt_gae.restype = ctypes.c_int
         L.qqt_gae.argtypes = [ctypes.POINTER(GaeArgsC), _vp]
+        L.qqt_l1_grad.restype = ctypes.c_int
+        L.qqt_l1_grad.argtypes = [ctypes.POINTER(L1GradArgsC), _vp]
+        L.qqt_l1_grad_workspace_floats.restype = ctypes.c_int64
+        L.qqt_l1_grad_workspace_floats.argtypes = [_i32, _i32]
         L.qqt_timing_arm.restype = ctypes.c_int
         L.qqt_timing_arm.argtypes = [_i32]
         L.qqt_timing_collect.restype = ctypes.c_int
@@ -115,7 +125,7 @@ def lib():
 
 
 KERNEL_KINDS = ("tick_kernel", "mlp_act_kernel", "bot_kernel", "reach_kernel",
-                "gae_kernel")  # QQT_KERNEL_*
+                "gae_kernel", "l1grad_kernels")  # QQT_KERNEL_*
 
 
 def timing_arm(launches: int) -> None:

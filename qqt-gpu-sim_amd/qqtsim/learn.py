@@ -1,0 +1,235 @@
+"""`HipMlpActorCritic`: the reference's mlp ActorCritic as a trainable module
+whose first layer runs forward and backward on the MFMA kernels.
+
+Drop-in for `train/model.py::ActorCritic(arch="mlp")` (:54-259) where the PPO
+update uses it (`ppo_update`, train/ppo.py:364-437): same submodules and
+state_dict keys (`shared.{0,1,3,4}`, `move_head.{0,2}`, `bomb_head.{0,2}`,
+`critic.{0,2}`), `forward(obs, pid)`, `dists`, `evaluate(obs, move_mask,
+bomb_mask, actions, pid)`, `n_params`, `arch == "mlp"`, so
+`loss.backward()`, `clip_grad_norm_` and the optimizer work unchanged.
+
+The first layer, x (B, 2366) float16 @ W0[:, view columns of pid]^T + b0,
+carries nearly all of the update's work and bytes.  Its forward is the
+first-layer part of `mlp_act_kernel` (float16 MFMA, W0 rounded to float16
+as in acting, float32 accumulation; `qqt_mlp_act` with `z1_out`), its weight
+gradient `qqt_l1_grad` (float16 MFMA over the batch, dz1 split hi/lo after
+a power-of-two scale, float32 accumulation).  No input gradient is formed
+(the observation is data).  LayerNorm, the 128-wide layers and the heads
+run as torch ops on the same device (about 8 % of the FLOPs).
+
+`ppo_update` is the reference's update loop (train/ppo.py:364-437) over a
+device rollout buffer, with the GAE scan on `qqt_gae`.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+from torch import nn
+
+from . import _capi
+from .config import n_obs_channels
+from .policy import HEAD, HID, KBLOCK, column_permutation, default_init, pack_mlp
+from .ppo import compute_gae
+
+
+def _w0_fragments(w: torch.Tensor, kpad: int) -> torch.Tensor:
+    """(128, k) float weight on the device -> float16 B fragments
+    [tile][kblock][lane][16] (the layout of qqtsim.policy._frag)."""
+    n, k = w.shape
+    out = torch.zeros((n, kpad), dtype=torch.float32, device=w.device)
+    out[:, :k] = w
+    kb = kpad // KBLOCK
+    f = out.view(n // 16, 16, kb, 4, 16).permute(0, 2, 3, 1, 4).contiguous()
+    return f.half().reshape(-1)
+
+
+class _FirstLayer(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x16, w0, b0, pid, owner):
+        z1 = owner._l1_forward(x16, w0, b0, pid)
+        ctx.save_for_backward(x16)
+        ctx.pid, ctx.owner = pid, owner
+        return z1
+
+    @staticmethod
+    def backward(ctx, dz1):
+        (x16,) = ctx.saved_tensors
+        dw0 = ctx.owner._l1_weight_grad(x16, dz1.contiguous().float(), ctx.pid)
+        return None, dw0, dz1.sum(0), None, None
+
+
+class HipMlpActorCritic(nn.Module):
+    arch = "mlp"
+
+    def __init__(self, obs_shape=(14, 13, 13), n_moves: int = 5, n_bomb: int = 2,
+                 n_players: int = 2, device="cuda", state_dict: dict | None = None):
+        super().__init__()
+        self.obs_shape = tuple(obs_shape)
+        self.n_players = n_players
+        if n_obs_channels(n_players) != self.obs_shape[0]:
+            raise ValueError("observation channels do not match n_players")
+        dev = torch.device(device)
+        if dev.type != "cuda":
+            raise ValueError("HipMlpActorCritic runs on a ROCm device")
+        c, h, w = self.obs_shape
+        self.k0 = c * h * w
+        self.kpad = -(-self.k0 // KBLOCK) * KBLOCK
+        self.shared = nn.Sequential(nn.Linear(self.k0, HID), nn.LayerNorm(HID), nn.ReLU(),
+                                    nn.Linear(HID, HID), nn.LayerNorm(HID), nn.ReLU())
+        self.move_head = nn.Sequential(nn.Linear(HID, HEAD), nn.ReLU(), nn.Linear(HEAD, n_moves))
+        self.bomb_head = nn.Sequential(nn.Linear(HID, HEAD), nn.ReLU(), nn.Linear(HEAD, n_bomb))
+        self.critic = nn.Sequential(nn.Linear(HID, HEAD), nn.ReLU(), nn.Linear(HEAD, 1))
+        self.load_state_dict(state_dict if state_dict is not None
+                             else default_init(obs_shape, n_moves, n_bomb))
+        self.to(dev)
+        self._lib = _capi.lib()
+        perms = [column_permutation(pid, n_players, c, h * w) for pid in range(n_players)]
+        self._perm = [p.to(dev) for p in perms]
+        self._inv = [torch.argsort(p).to(dev) for p in perms]
+        # the first-layer launch reads the later layers' buffers in its
+        # prologue; zero stand-ins of the packed sizes
+        packed = pack_mlp(default_init(obs_shape, n_moves, n_bomb), n_players, obs_shape)
+        self._stub = {k: torch.zeros_like(v).to(dev) for k, v in packed.items()
+                      if torch.is_tensor(v) and k not in ("w0", "b0")}
+        self._ws = None
+
+    def n_params(self) -> int:
+        return sum(p.numel() for p in self.parameters())
+
+    # ------------------------------------------------------------ kernels
+    def _l1_forward(self, x16, w0, b0, pid):
+        b = x16.shape[0]
+        z1 = torch.empty((b, HID), dtype=torch.float32, device=x16.device)
+        frag = _w0_fragments(w0.detach()[:, self._perm[pid]].float(), self.kpad)
+        bias = b0.detach().float().contiguous()
+        a = _capi.MlpArgsC()
+        a.batch, a.npid, a.pid0, a.sample = b, 1, 0, 0
+        a.k0, a.kblocks0, a.obs_stride = self.k0, self.kpad // KBLOCK, x16.stride(0)
+        a.w0_players = 1
+        a.obs, a.w0, a.b0 = x16.data_ptr(), frag.data_ptr(), bias.data_ptr()
+        for k, v in self._stub.items():
+            setattr(a, k, v.data_ptr())
+        a.z1_out = z1.data_ptr()
+        _capi.check(self._lib.qqt_mlp_act(a, _capi.stream_handle(x16.device)))
+        return z1
+
+    def _l1_weight_grad(self, x16, dz1, pid):
+        b = x16.shape[0]
+        need = int(self._lib.qqt_l1_grad_workspace_floats(b, self.k0))
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(need, dtype=torch.float32, device=x16.device)
+        amax = dz1.abs().amax().clamp_min(1e-30)
+        scale = torch.exp2(torch.clamp(14.0 - torch.ceil(torch.log2(amax)), -100.0, 100.0))
+        dw0p = torch.empty((HID, self.k0), dtype=torch.float32, device=x16.device)
+        a = _capi.L1GradArgsC()
+        a.batch, a.k0, a.obs_stride = b, self.k0, x16.stride(0)
+        a.workspace_floats = self._ws.numel()
+        a.obs, a.dz1, a.dz_scale = x16.data_ptr(), dz1.data_ptr(), scale.data_ptr()
+        a.workspace, a.dw0 = self._ws.data_ptr(), dw0p.data_ptr()
+        _capi.check(self._lib.qqt_l1_grad(a, _capi.stream_handle(x16.device)))
+        return dw0p[:, self._inv[pid]]
+
+    # ------------------------------------------------------------ API
+    def forward(self, obs, pid: int = 0):
+        """(move logits, bomb logits, value) like train/model.py:167-196."""
+        b = obs.shape[0]
+        x16 = obs.reshape(b, -1)
+        if x16.dtype != torch.float16:
+            x16 = x16.half()
+        x16 = x16.contiguous()
+        if x16.shape[1] != self.k0:
+            raise ValueError(f"observation rows must have {self.k0} values")
+        lin = self.shared[0]
+        x = _FirstLayer.apply(x16, lin.weight, lin.bias, int(pid), self)
+        x = self.shared[1:](x)
+        return self.move_head(x), self.bomb_head(x), self.critic(x).squeeze(-1)
+
+    @staticmethod
+    def masked_dist(logits, mask):
+        neg_inf = torch.finfo(logits.dtype).min
+        masked = torch.where(mask, logits, torch.full_like(logits, neg_inf))
+        return torch.distributions.Categorical(logits=masked)
+
+    def dists(self, obs, move_mask, bomb_mask, pid: int = 0):
+        ml, bl, val = self(obs, pid)
+        return (self.masked_dist(ml, move_mask.bool()), self.masked_dist(bl, bomb_mask.bool()),
+                val)
+
+    def evaluate(self, obs, move_mask, bomb_mask, actions, pid: int = 0):
+        """(logp, entropy, value) of given actions (train/model.py:247-256)."""
+        dm, db, val = self.dists(obs, move_mask, bomb_mask, pid)
+        logp = dm.log_prob(actions[..., 0]) + db.log_prob(actions[..., 1])
+        return logp, dm.entropy() + db.entropy(), val
+
+
+@dataclass
+class PPOConfig:
+    """train/ppo.py:38-51."""
+    rollout_steps: int = 128
+    epochs: int = 4
+    minibatches: int = 4
+    gamma: float = 0.995
+    gae_lambda: float = 0.95
+    clip_eps: float = 0.2
+    value_coef: float = 0.5
+    entropy_coef: float = 0.05
+    entropy_final: float = 0.03
+    max_grad_norm: float = 0.5
+    lr: float = 3e-4
+    oversample_dying: int = 3
+    bptt_window: int = 0
+
+
+def ppo_update(learner, opt, buf, last_val, cfg: PPOConfig, entropy_coef: float) -> dict:
+    """One PPO update over a filled rollout buffer, as train/ppo.py:364-437
+    (GAE, advantage normalisation, dying-frame oversampling, epochs x
+    minibatches of clipped policy loss + clipped value loss - entropy bonus,
+    gradient-norm clipping, optimizer step).  `buf` is a HipRolloutBuffer
+    (or any buffer with the reference's fields); the GAE scan is
+    `qqt_gae`.  The statistics are summed on the device and read once at the
+    end (the reference reads them after every minibatch)."""
+    adv, ret = compute_gae(buf, last_val, cfg.gamma, cfg.gae_lambda)
+    flat = lambda x: x.reshape(-1, *x.shape[2:])  # noqa: E731
+    obs = flat(buf.obs)
+    mmask, bmask = flat(buf.mmask), flat(buf.bmask)
+    act, old_logp = flat(buf.act), flat(buf.logp)
+    adv, ret, old_val = flat(adv), flat(ret), flat(buf.val)
+    adv = (adv - adv.mean()) / (adv.std() + 1e-8)
+    total = obs.shape[0]
+    dev = obs.device
+    base = torch.arange(total, device=dev)
+    pool = base
+    if cfg.oversample_dying > 1:
+        rare = flat(buf.dmg) | flat(buf.done).bool()
+        if bool(rare.any()):
+            rare_idx = rare.nonzero(as_tuple=False).squeeze(1)
+            pool = torch.cat([base, rare_idx.repeat(cfg.oversample_dying - 1)])
+    mb = max(1, total // cfg.minibatches)
+    keys = ("pg", "vf", "ent", "kl", "clipfrac")
+    acc = torch.zeros(len(keys), dtype=torch.float32, device=dev)
+    n_updates = 0
+    for _ in range(cfg.epochs):
+        perm = pool[torch.randperm(pool.numel(), device=dev)][:total]
+        for start in range(0, total, mb):
+            sel = perm[start:start + mb]
+            logp, entropy, value = learner.evaluate(obs[sel], mmask[sel], bmask[sel], act[sel])
+            ratio = (logp - old_logp[sel]).exp()
+            pg = -torch.min(ratio * adv[sel],
+                            ratio.clamp(1 - cfg.clip_eps, 1 + cfg.clip_eps) * adv[sel]).mean()
+            v_clipped = old_val[sel] + (value - old_val[sel]).clamp(-cfg.clip_eps, cfg.clip_eps)
+            vf = 0.5 * torch.max((value - ret[sel]) ** 2, (v_clipped - ret[sel]) ** 2).mean()
+            ent = entropy.mean()
+            loss = pg + cfg.value_coef * vf - entropy_coef * ent
+            opt.zero_grad(set_to_none=True)
+            loss.backward()
+            torch.nn.utils.clip_grad_norm_(learner.parameters(), cfg.max_grad_norm)
+            opt.step()
+            with torch.no_grad():
+                acc += torch.stack([pg.detach(), vf.detach(), ent.detach(),
+                                    (old_logp[sel] - logp).mean().detach(),
+                                    ((ratio - 1).abs() > cfg.clip_eps).float().mean()])
+            n_updates += 1
+    vals = (acc / max(1, n_updates)).tolist()
+    return dict(zip(keys, vals))

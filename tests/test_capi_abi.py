@@ -40,6 +40,7 @@ def _declared_functions():
 
 def test_header_declares_the_entry_points():
     assert _declared_functions() == ["qqt_abi_version", "qqt_bot_act", "qqt_gae",
+                                     "qqt_l1_grad", "qqt_l1_grad_workspace_floats",
                                      "qqt_last_error", "qqt_mlp_act", "qqt_tick",
                                      "qqt_timing_arm", "qqt_timing_collect"]
 
@@ -90,7 +91,7 @@ def test_struct_layouts_match_the_header(tmp_path):
 
     structs = {"qqt_sim_config": _capi.SimConfigC, "qqt_tick_args": _capi.TickArgsC,
                "qqt_mlp_args": _capi.MlpArgsC, "qqt_bot_args": _capi.BotArgsC,
-               "qqt_gae_args": _capi.GaeArgsC}
+               "qqt_gae_args": _capi.GaeArgsC, "qqt_l1_grad_args": _capi.L1GradArgsC}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "qqt_hip.h"',
              'int main(void) {']
     for cname, cls in structs.items():
@@ -253,7 +254,7 @@ def test_header_kernel_kinds_match_host_mirror():
     text = open(HEADER).read()
     kinds = dict((k, int(v)) for k, v in re.findall(r"\bQQT_KERNEL_(\w+) = (\d+)", text))
     assert kinds["KINDS"] == len(_capi.KERNEL_KINDS)
-    for name in ("TICK", "MLP", "BOT", "REACH", "GAE"):
+    for name in ("TICK", "MLP", "BOT", "REACH", "GAE", "L1GRAD"):
         assert _capi.KERNEL_KINDS[kinds[name]].startswith(name.lower()), name
 
 
@@ -287,3 +288,21 @@ def test_errors_raise_in_python(lib):
 
     with pytest.raises(ValueError, match="n_envs"):
         _capi.check(lib.qqt_tick(_cfg(), _tick_args(n_envs=-1), None))
+
+
+def test_l1_grad_rejects_bad_arguments(lib):
+    """Argument checks run before any launch (no GPU needed)."""
+    from qqtsim import _capi
+
+    assert lib.qqt_l1_grad_workspace_floats(0, 2366) == -1
+    n = lib.qqt_l1_grad_workspace_floats(5000, 2366)
+    assert n == 3 * 128 * 10 * 256          # 3 chunks of 1696 rows, 10 column tiles
+    a = _capi.L1GradArgsC()
+    assert lib.qqt_l1_grad(ctypes.byref(a), None) == -1
+    assert b"null" in lib.qqt_last_error()
+    a.batch, a.k0, a.obs_stride, a.workspace_floats = 5000, 2366, 2366, n - 1
+    a.obs = a.dz1 = a.workspace = a.dw0 = 1 << 20
+    assert lib.qqt_l1_grad(ctypes.byref(a), None) == -1
+    assert b"workspace" in lib.qqt_last_error()
+    a.workspace_floats, a.k0 = n, 2367
+    assert lib.qqt_l1_grad(ctypes.byref(a), None) == -1
