@@ -76,7 +76,8 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="CPU work budget of the cpu_baseline sample (0 = skip)")
-    ap.add_argument("--workload", choices=("rollout", "stress", "astar", "evalfwd", "collect"),
+    ap.add_argument("--workload", choices=("rollout", "stress", "astar", "evalfwd", "collect",
+                                           "ppo"),
                     default="rollout",
                     help="rollout: the headline self-play rollout (default); stress: "
                          "16384-env bomb-stress ticks with injected actions; astar: "
@@ -84,7 +85,8 @@ def parse_args():
                          "128-tick rollout into the observation slab, then the batched "
                          "evaluation forward over all 4.19M observations; collect: "
                          "128-step self-play collects into the device rollout buffer "
-                         "(5632 envs) + last-value forward + GAE")
+                         "(5632 envs) + last-value forward + GAE; ppo: one PPO update "
+                         "(4 epochs x 4 minibatches) over a 5632 x 128 collected buffer")
     ap.add_argument("--copy-calibrate", action="store_true",
                     help="after timing, run a 512 MiB device copy (HBM counter calibration)")
     return ap.parse_args()
@@ -251,6 +253,8 @@ def main():
         return main_evalfwd(args, torch, dev)
     if args.workload == "collect":
         return main_collect(args, torch, dev)
+    if args.workload == "ppo":
+        return main_ppo(args, torch, dev)
     n, K, W = args.envs, args.steps, args.warmup
     cfg, spec, roll = build_workload(n, args.seed, dev)
     for _ in range(W):
@@ -779,6 +783,160 @@ def main_collect(args, torch, dev):
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
+
+def _torch_mlp(torch, sd, dev):
+    """The reference's mlp ActorCritic as plain torch modules (float32,
+    eager): forward and evaluate of train/model.py:140-153, 192-196,
+    215-256.  The PyTorch-on-GPU baseline of the PPO update."""
+    nn = torch.nn
+    from qqtsim.policy import column_permutation
+
+    class Mlp(nn.Module):
+        arch = "mlp"
+
+        def __init__(self):
+            super().__init__()
+            self.shared = nn.Sequential(nn.Linear(2366, 128), nn.LayerNorm(128), nn.ReLU(),
+                                        nn.Linear(128, 128), nn.LayerNorm(128), nn.ReLU())
+            self.move_head = nn.Sequential(nn.Linear(128, 64), nn.ReLU(), nn.Linear(64, 5))
+            self.bomb_head = nn.Sequential(nn.Linear(128, 64), nn.ReLU(), nn.Linear(64, 2))
+            self.critic = nn.Sequential(nn.Linear(128, 64), nn.ReLU(), nn.Linear(64, 1))
+            self.cols = [column_permutation(p, 2, 14, 169).to(dev) for p in range(2)]
+
+        def forward(self, obs, pid=0):
+            x = obs.to(self.shared[0].weight.dtype).reshape(obs.shape[0], -1)
+            x = torch.nn.functional.linear(x, self.shared[0].weight[:, self.cols[pid]],
+                                           self.shared[0].bias)
+            x = self.shared[1:](x)
+            return self.move_head(x), self.bomb_head(x), self.critic(x).squeeze(-1)
+
+        def evaluate(self, obs, mm, bm, act, pid=0):
+            ml, bl, v = self(obs, pid)
+            neg = torch.finfo(ml.dtype).min
+            dm = torch.distributions.Categorical(
+                logits=torch.where(mm.bool(), ml, torch.full_like(ml, neg)))
+            db = torch.distributions.Categorical(
+                logits=torch.where(bm.bool(), bl, torch.full_like(bl, neg)))
+            logp = dm.log_prob(act[..., 0]) + db.log_prob(act[..., 1])
+            return logp, dm.entropy() + db.entropy(), v
+
+    m = Mlp()
+    m.load_state_dict(sd)
+    return m.to(dev)
+
+
+# Algorithmic bytes and FLOP per row of the first-layer weight gradient:
+# the float16 observation row and the float32 dz1 row read once; 2 x 128 x
+# 2366 multiply-adds, twice (the hi and lo halves of dz1).
+L1G_BYTES_PER_ROW = 2366 * 2 + 128 * 4
+L1G_FLOP_PER_ROW = 2 * 2 * 128 * 2366
+
+
+def main_ppo(args, torch, dev):
+    """One PPO update (train/ppo.py:364-437: GAE, 4 epochs x 4 minibatches of
+    the clipped loss, backward, gradient clipping, Adam) over a buffer of
+    5632 envs x 128 self-play steps collected by the kernels.  `value` counts
+    rows processed per second (rows x epochs / update time).  The learner is
+    HipMlpActorCritic (first layer forward and weight gradient on MFMA);
+    `torch_gpu_baseline` runs the same update with the reference's network
+    as float32 eager torch modules on the same GPU."""
+    from qqtsim import HipMlpActorCritic, HipRolloutBuffer, PPOConfig, ppo_update
+    from qqtsim.policy import default_init
+
+    n = args.envs
+    cfg, spec, roll = build_workload(n, args.seed, dev)
+    for _ in range(max(1, args.warmup)):
+        roll.step()
+    buf = HipRolloutBuffer(COLLECT_T, n, cfg.obs_shape, dev)
+    roll.collect(buf)
+    last_val = roll.policy.forward(roll.sim.observe(), 0)[2]
+    pcfg = PPOConfig()
+    sd = default_init(cfg.obs_shape)
+    rows = COLLECT_T * n
+    reps = 2 if args.steps >= 256 else max(1, min(args.steps, 3))   # whole updates timed
+
+    def run(learner, timed_launches=0):
+        opt = torch.optim.Adam(learner.parameters(), lr=pcfg.lr)
+        torch.manual_seed(0)
+        ppo_update(learner, opt, buf, last_val, pcfg, pcfg.entropy_coef)     # warm-up
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(reps):
+            torch.manual_seed(0)
+            if timed_launches:
+                _capi.timing_arm(timed_launches)
+            t0 = time.perf_counter()
+            ppo_update(learner, opt, buf, last_val, pcfg, pcfg.entropy_coef)
+            torch.cuda.synchronize()
+            best = min(best, time.perf_counter() - t0)
+        return best
+
+    _capi.timing_arm(0)
+    learner = HipMlpActorCritic(cfg.obs_shape, device=dev, state_dict=sd)
+    el = run(learner, timed_launches=1 + 3)    # GAE, then the first minibatch's three launches
+    tim = _capi.timing_collect()
+    mb_rows = rows // pcfg.minibatches
+    fwd_ms = tim["mlp_act_kernel"][0] / tim["mlp_act_kernel"][1]
+    # weight-gradient kernel + chunk reduction, per minibatch
+    l1g_ms = tim["l1grad_kernels"][0] / (tim["l1grad_kernels"][1] / 2)
+    l1g_gbs = L1G_BYTES_PER_ROW * mb_rows / (l1g_ms * 1e-3) / 1e9
+    l1g_tf = L1G_FLOP_PER_ROW * mb_rows / (l1g_ms * 1e-3) / 1e12
+    fwd_gbs = 2366 * 2 * mb_rows / (fwd_ms * 1e-3) / 1e9
+    ref = _torch_mlp(torch, sd, dev)
+    el_ref = run(ref)
+    samples = rows * pcfg.epochs
+    cpu = None
+    if args.cpu_seconds > 0:
+        cores = _cores(torch)
+        cpu_net = _torch_mlp(torch, sd, torch.device("cpu"))
+        opt = torch.optim.Adam(cpu_net.parameters(), lr=pcfg.lr)
+        b = 4096
+        obs = buf.obs.reshape(-1, 14, 13, 13)[:b].cpu()
+        mm, bm = buf.mmask.reshape(-1, 5)[:b].cpu(), buf.bmask.reshape(-1, 2)[:b].cpu()
+        act = buf.act.reshape(-1, 2)[:b].cpu()
+        done, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < min(args.cpu_seconds, 10.0) or done == 0:
+            logp, ent, v = cpu_net.evaluate(obs, mm, bm, act)
+            loss = -(logp.mean()) + 0.5 * (v ** 2).mean() - 0.05 * ent.mean()
+            opt.zero_grad(set_to_none=True)
+            loss.backward()
+            opt.step()
+            done += 1
+        elc = time.perf_counter() - t0
+        cpu = {"value": b * done / elc, "unit": "samples/s", "cores": cores, "kind": "port",
+               "sample": f"the reference's mlp ActorCritic as float32 torch modules on the "
+                         f"host: {done} minibatches of {b} rows (evaluate + loss + backward + "
+                         f"Adam), {elc:.1f} s"}
+    res = {
+        "metric": "PPO update samples/s (5632 envs x 128 steps, 4 epochs x 4 minibatches), "
+                  "1 MI355X",
+        "value": samples / el, "unit": "samples/s", "n_gpus": 1, "steps": reps,
+        "warmup": 1, "ms_per_step": el * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16 MFMA first layer (f32 accumulate) / f32 torch rest",
+        "data": "synthetic: a buffer collected by the kernels from template maps, PyTorch "
+                "default-init MLP weights",
+        "config": {"workload": "PPO update over a 5632 x 128 rollout buffer "
+                               "(train/ppo.py:364-437)", "rows": rows,
+                   "epochs": pcfg.epochs, "minibatches": pcfg.minibatches,
+                   "minibatch_rows": mb_rows, "parallelism": "single GPU"},
+        "roofline": {"kernel": "l1_grad_kernel + l1_grad_reduce", "bound": "hbm",
+                     "achieved": round(l1g_gbs, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(l1g_gbs / HBM_PEAK_GBS, 5), "traffic": None},
+        "kernels": {"l1_grad (per minibatch)": {"us": round(l1g_ms * 1e3, 3),
+                                                "achieved_gbs": round(l1g_gbs, 3),
+                                                "tflops": round(l1g_tf, 3),
+                                                "bytes_per_row": L1G_BYTES_PER_ROW},
+                    "first-layer forward (per minibatch)": {
+                        "us": round(fwd_ms * 1e3, 3), "obs_gbs": round(fwd_gbs, 3)}},
+        "torch_gpu_baseline": {"value": samples / el_ref, "unit": "samples/s",
+                               "ms_per_update": el_ref * 1e3,
+                               "speedup": round(el_ref / el, 3),
+                               "note": "same update, the reference's network as float32 "
+                                       "eager torch modules"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+
 
 if __name__ == "__main__":
     main()

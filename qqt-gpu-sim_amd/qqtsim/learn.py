@@ -15,7 +15,10 @@ as in acting, float32 accumulation; `qqt_mlp_act` with `z1_out`), its weight
 gradient `qqt_l1_grad` (float16 MFMA over the batch, dz1 split hi/lo after
 a power-of-two scale, float32 accumulation).  No input gradient is formed
 (the observation is data).  LayerNorm, the 128-wide layers and the heads
-run as torch ops on the same device (about 8 % of the FLOPs).
+run as torch ops on the same device (about 8 % of the FLOPs); their weight
+gradients, whose reduction runs over the whole minibatch, are batched
+products over row chunks (a single batch-long reduction lands on a few
+workgroups).
 
 `ppo_update` is the reference's update loop (train/ppo.py:364-437) over a
 device rollout buffer, with the GAE scan on `qqt_gae`.
@@ -58,6 +61,44 @@ class _FirstLayer(torch.autograd.Function):
         (x16,) = ctx.saved_tensors
         dw0 = ctx.owner._l1_weight_grad(x16, dz1.contiguous().float(), ctx.pid)
         return None, dw0, dz1.sum(0), None, None
+
+
+def _weight_grad(dy: torch.Tensor, x: torch.Tensor, chunk: int = 4096) -> torch.Tensor:
+    """dy^T x with the batch as the reduction, as batched products over row
+    chunks summed in chunk order.  A single product with a batch-long
+    reduction runs on a handful of workgroups (the weight is 128 x 128 or
+    smaller); chunking spreads it over the GPU."""
+    b = dy.shape[0]
+    c = b // chunk
+    out = None
+    if c >= 2:
+        n = c * chunk
+        dyt = dy[:n].reshape(c, chunk, dy.shape[1]).transpose(1, 2).contiguous()
+        out = torch.bmm(dyt, x[:n].reshape(c, chunk, x.shape[1]).contiguous()).sum(0)
+        dy, x = dy[n:], x[n:]
+    if dy.shape[0]:
+        r = dy.t() @ x
+        out = r if out is None else out + r
+    return out
+
+
+class _Linear(torch.autograd.Function):
+    """F.linear whose weight gradient reduces over the batch in chunks."""
+
+    @staticmethod
+    def forward(ctx, x, w, b):
+        ctx.save_for_backward(x, w)
+        return torch.nn.functional.linear(x, w, b)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w = ctx.saved_tensors
+        dy = dy.contiguous()
+        return dy @ w, _weight_grad(dy, x), dy.sum(0)
+
+
+def _lin(mod: nn.Linear, x):
+    return _Linear.apply(x, mod.weight, mod.bias)
 
 
 class HipMlpActorCritic(nn.Module):
@@ -143,8 +184,11 @@ class HipMlpActorCritic(nn.Module):
             raise ValueError(f"observation rows must have {self.k0} values")
         lin = self.shared[0]
         x = _FirstLayer.apply(x16, lin.weight, lin.bias, int(pid), self)
-        x = self.shared[1:](x)
-        return self.move_head(x), self.bomb_head(x), self.critic(x).squeeze(-1)
+        x = torch.relu(self.shared[1](x))
+        x = torch.relu(self.shared[4](_lin(self.shared[3], x)))
+        heads = [_lin(h[2], torch.relu(_lin(h[0], x)))
+                 for h in (self.move_head, self.bomb_head, self.critic)]
+        return heads[0], heads[1], heads[2].squeeze(-1)
 
     @staticmethod
     def masked_dist(logits, mask):
