@@ -837,7 +837,8 @@ def main_ppo(args, torch, dev):
     the clipped loss, backward, gradient clipping, Adam) over a buffer of
     5632 envs x 128 self-play steps collected by the kernels.  `value` counts
     rows processed per second (rows x epochs / update time).  The learner is
-    HipMlpActorCritic (first layer forward and weight gradient on MFMA);
+    HipMlpActorCritic (first layer forward and weight gradient on MFMA, the
+    loss and the backward above the first layer fused in one kernel);
     `torch_gpu_baseline` runs the same update with the reference's network
     as float32 eager torch modules on the same GPU."""
     from qqtsim import HipMlpActorCritic, HipRolloutBuffer, PPOConfig, ppo_update
@@ -873,7 +874,9 @@ def main_ppo(args, torch, dev):
 
     _capi.timing_arm(0)
     learner = HipMlpActorCritic(cfg.obs_shape, device=dev, state_dict=sd)
-    el = run(learner, timed_launches=1 + 3)    # GAE, then the first minibatch's three launches
+    # GAE, then the first minibatch's four launches (forward, fused loss +
+    # backward, weight gradient and its chunk reduction)
+    el = run(learner, timed_launches=1 + 4)
     tim = _capi.timing_collect()
     mb_rows = rows // pcfg.minibatches
     fwd_ms = tim["mlp_act_kernel"][0] / tim["mlp_act_kernel"][1]
@@ -882,6 +885,7 @@ def main_ppo(args, torch, dev):
     l1g_gbs = L1G_BYTES_PER_ROW * mb_rows / (l1g_ms * 1e-3) / 1e9
     l1g_tf = L1G_FLOP_PER_ROW * mb_rows / (l1g_ms * 1e-3) / 1e12
     fwd_gbs = 2366 * 2 * mb_rows / (fwd_ms * 1e-3) / 1e9
+    ppo_ms = tim["ppo_grad_kernel"][0] / tim["ppo_grad_kernel"][1]
     ref = _torch_mlp(torch, sd, dev)
     el_ref = run(ref)
     samples = rows * pcfg.epochs
@@ -912,7 +916,9 @@ def main_ppo(args, torch, dev):
                   "1 MI355X",
         "value": samples / el, "unit": "samples/s", "n_gpus": 1, "steps": reps,
         "warmup": 1, "ms_per_step": el * 1e3, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f16 MFMA first layer (f32 accumulate) / f32 torch rest",
+        "vs_baseline": None,
+        "dtype": "f16 MFMA first layer (f32 accumulate) / f32 fused loss + backward / f32 torch "
+                 "weight-gradient products and Adam",
         "data": "synthetic: a buffer collected by the kernels from template maps, PyTorch "
                 "default-init MLP weights",
         "config": {"workload": "PPO update over a 5632 x 128 rollout buffer "
@@ -927,7 +933,8 @@ def main_ppo(args, torch, dev):
                                                 "tflops": round(l1g_tf, 3),
                                                 "bytes_per_row": L1G_BYTES_PER_ROW},
                     "first-layer forward (per minibatch)": {
-                        "us": round(fwd_ms * 1e3, 3), "obs_gbs": round(fwd_gbs, 3)}},
+                        "us": round(fwd_ms * 1e3, 3), "obs_gbs": round(fwd_gbs, 3)},
+                    "ppo_grad_kernel (per minibatch)": {"us": round(ppo_ms * 1e3, 3)}},
         "torch_gpu_baseline": {"value": samples / el_ref, "unit": "samples/s",
                                "ms_per_update": el_ref * 1e3,
                                "speedup": round(el_ref / el, 3),

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 7
+#define QQT_ABI_VERSION 8
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -277,6 +277,44 @@ typedef struct qqt_l1_grad_args {
 int64_t qqt_l1_grad_workspace_floats(int32_t batch, int32_t k0);
 int qqt_l1_grad(const qqt_l1_grad_args* args, void* stream);
 
+/* The PPO minibatch loss and its backward above the first layer, fused
+ * (train/ppo.py:401-421 through train/model.py:140-153, 192-196, 215-256):
+ * from z1 = x W0^T + b0 per row, LayerNorm/ReLU, Linear(128,128),
+ * LayerNorm/ReLU, the three heads, the masked log-probs and entropies, the
+ * clipped policy loss, the clipped value loss and the entropy bonus, back to
+ * dz1.  float32.  Row outputs feed the weight gradients the caller forms
+ * over the minibatch (dW1 = dz2^T h1, dWh = dhy^T h2, output layers from dl
+ * and hy, dW0 via qqt_l1_grad on dz1); per 16-row block sums of the
+ * LayerNorm parameter gradients and of the loss statistics. */
+typedef struct qqt_ppo_args {
+  int32_t batch;              /* rows B of the minibatch (the means' divisor) */
+  float clip_eps;             /* float32(clip_eps): value clip and clip fraction */
+  float ratio_lo, ratio_hi;   /* float32(1 - clip_eps), float32(1 + clip_eps) */
+  float value_coef, entropy_coef;
+  const float* z1;            /* [B][128] */
+  const float *ln1_w, *ln1_b; /* [128] */
+  const float *w1, *w1t;      /* shared.3.weight [128][128] and its transpose */
+  const float* b1;
+  const float *ln2_w, *ln2_b;
+  const float *wh, *wht;      /* the heads' hidden layers stacked [192][128] and transpose */
+  const float* bh;            /* [192] */
+  const float* wf;            /* [8][64]: move rows 0-4, bomb 5-6, critic 7 (each head's
+                                 output layer over its own 64 hidden units) */
+  const float* bf;            /* [8] */
+  const int64_t* actions;     /* [B][2] */
+  const uint8_t* move_mask;   /* [B][5] */
+  const uint8_t* bomb_mask;   /* [B][2] */
+  const float *old_logp, *adv, *ret, *old_val;   /* [B]; adv normalised by the caller */
+  float* dz1;                 /* [B][128] */
+  float *h1, *dz2, *h2;       /* [B][128] */
+  float *hy, *dhy;            /* [B][192] */
+  float* dl;                  /* [B][8]: d loss / d (5 move logits, 2 bomb logits, value) */
+  float* ln_part;             /* [ceil(B/16)][4][128]: dgamma1, dbeta1, dgamma2, dbeta2 */
+  float* stats_part;          /* [ceil(B/16)][5]: sums of -min(surrogates), 0.5 max(value
+                                 errors), entropy, old_logp - logp, clipped indicator */
+} qqt_ppo_args;
+int qqt_ppo_grad(const qqt_ppo_args* args, void* stream);
+
 /* Dispatch timing for benchmark harnesses (no counterpart in the reference:
  * its bench times whole steps with host clocks).  qqt_timing_arm(n) times
  * the next n kernel launches made through this library: each records a
@@ -287,7 +325,7 @@ int qqt_l1_grad(const qqt_l1_grad_args* args, void* stream);
  * most 4096 launches are timed between collects.  Allocates no device
  * memory (the event pool is created by the first arm). */
 enum { QQT_KERNEL_TICK = 0, QQT_KERNEL_MLP = 1, QQT_KERNEL_BOT = 2, QQT_KERNEL_REACH = 3,
-       QQT_KERNEL_GAE = 4, QQT_KERNEL_L1GRAD = 5, QQT_KERNEL_KINDS = 6 };
+       QQT_KERNEL_GAE = 4, QQT_KERNEL_L1GRAD = 5, QQT_KERNEL_PPO = 6, QQT_KERNEL_KINDS = 7 };
 int qqt_timing_arm(int32_t launches);
 int qqt_timing_collect(double* ms, int32_t* count, int32_t n_kinds);
 

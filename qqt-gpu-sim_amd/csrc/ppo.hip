@@ -1,0 +1,383 @@
+// The PPO minibatch loss and its backward through the mlp ActorCritic above
+// the first layer (train/ppo.py:401-421 on train/model.py:140-153, 192-196,
+// 215-256), fused: from z1 = x W0^T + b0 of each row to the gradient dz1
+// that the first layer's weight gradient (csrc/mlp_grad.hip) consumes.
+//
+// Forward, per row: LayerNorm 1 + ReLU -> Linear(128,128) -> LayerNorm 2 +
+// ReLU -> the three heads' Linear(128,64) + ReLU -> move (5), bomb (2) and
+// value (1) outputs; masked log-softmax, log-prob of the taken actions,
+// entropies.  Loss terms (the reference's, with torch's gradient rules:
+// min/max ties split the gradient in halves, clamp passes it at its bounds):
+//   ratio = exp(logp - old_logp)
+//   pg    = -mean(min(ratio A, clamp(ratio, 1-e, 1+e) A))
+//   vf    = 0.5 mean(max((v - R)^2, (old_v + clamp(v - old_v, -e, e) - R)^2))
+//   loss  = pg + value_coef vf - entropy_coef mean(H_move + H_bomb)
+// Backward, per row, through the heads, LayerNorm 2, Linear(128,128) and
+// LayerNorm 1.  Float32 throughout; the four products (K and N of 128 and
+// 192) on v_mfma_f32_16x16x4_f32, the 16 rows as one M tile.
+//
+// One workgroup of 512 threads takes 16 rows; activations live in LDS
+// (rows padded by 4 floats against bank conflicts; two workgroups per CU).  Outputs: dz1, and for the weight
+// gradients the caller forms as batched products (their reduction runs over
+// the whole minibatch): h1, dz2, h2, hy, dhy and the output-layer gradients
+// dl; per-workgroup sums of the LayerNorm parameter gradients and of the
+// loss statistics.
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "qqt_common.h"
+#include "qqt_hip.h"
+
+namespace qqt {
+
+extern thread_local char g_err[512];
+
+namespace ppo {
+
+constexpr int R = 16;        // rows per workgroup
+constexpr int T = 512;       // threads: 8 wavefronts (one per column tile of a 128-wide product)
+constexpr int TR = 256;      // threads of the row-wise phases (16 per row)
+constexpr int H = 128;       // hidden width
+constexpr int HY = 192;      // three heads x 64
+constexpr int HP = H + 4, HYP = HY + 4;   // padded LDS row strides
+constexpr float LN_EPS = 1e-5f;
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+struct __align__(16) Lds {
+  float xh1[R][HP], h1[R][HP], xh2[R][HP], h2[R][HP], g[R][HP], z[R][HP];
+  float hy[R][HYP], dhy[R][HYP];
+  float logit[R][8], dl[R][8];
+  float rstd1[R], rstd2[R];
+  float stat[R][5];
+};
+
+// Y[r][n] = sum_k X[r][k] W[k][n] (+ bias[n]) for the 16 rows; W row-major
+// [K][N] in global memory, X and Y in LDS.  MFMA 16x16x4 f32: lane l feeds
+// A[l%16][k0 + l/16] and B[k0 + l/16][n0 + l%16] and holds D[4(l/16)+q][l%16].
+// Wavefront w takes column tiles w, w+4, ...
+template <int K, int N, int LDX, int LDY>
+__device__ __forceinline__ void gemm(const float (*X)[LDX], const float* __restrict__ W,
+                                     const float* __restrict__ bias, float (*Y)[LDY]) {
+  constexpr int CT = N / 16;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i16 = lane & 15, kq = lane >> 4;
+  for (int ct = w; ct < CT; ct += T / 64) {
+    const int col = 16 * ct + i16;
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 16
+    for (int k0 = 0; k0 < K; k0 += 4)
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(X[i16][k0 + kq], W[(size_t)(k0 + kq) * N + col],
+                                                 acc, 0, 0, 0);
+    const float b = bias ? bias[col] : 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) Y[4 * kq + q][col] = acc[q] + b;
+  }
+}
+
+// Sum over the 16 lanes of one row (threads 16r .. 16r+15).
+__device__ __forceinline__ float sum16(float v) {
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) v += __shfl_xor(v, m, 16);
+  return v;
+}
+
+// LayerNorm + ReLU of Z[r] (in place into xh = normalised, h = output);
+// 16 threads per row, feature c = lane + 16 i.
+__device__ __forceinline__ void ln_forward(const float (*Z)[HP], const float* __restrict__ gam,
+                                           const float* __restrict__ bet, float (*xh)[HP],
+                                           float (*h)[HP], float* rstd_out) {
+  const int r = threadIdx.x >> 4, j = threadIdx.x & 15;
+  float v[8];
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    v[i] = Z[r][j + 16 * i];
+    s += v[i];
+  }
+  const float mean = sum16(s) / (float)H;
+  float q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float d = v[i] - mean;
+    q += d * d;
+  }
+  const float rstd = 1.0f / sqrtf(sum16(q) / (float)H + LN_EPS);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = j + 16 * i;
+    const float x = (v[i] - mean) * rstd;
+    xh[r][c] = x;
+    h[r][c] = fmaxf(x * gam[c] + bet[c], 0.0f);
+  }
+  if (j == 0) rstd_out[r] = rstd;
+}
+
+// LayerNorm backward with the ReLU after it: dy = G (gradient of the ReLU
+// output) where h > 0; dz = rstd (dx - mean(dx) - xh mean(dx xh)), dx =
+// dy gamma.  Writes dz over G.
+__device__ __forceinline__ void ln_backward(float (*G)[HP], const float (*xh)[HP],
+                                            const float (*h)[HP], const float* __restrict__ gam,
+                                            const float* rstd) {
+  const int r = threadIdx.x >> 4, j = threadIdx.x & 15;
+  float dx[8], x[8];
+  float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = j + 16 * i;
+    const float dy = h[r][c] > 0.0f ? G[r][c] : 0.0f;
+    x[i] = xh[r][c];
+    dx[i] = dy * gam[c];
+    s1 += dx[i];
+    s2 += dx[i] * x[i];
+  }
+  const float m1 = sum16(s1) / (float)H, m2 = sum16(s2) / (float)H;
+  const float rs = rstd[r];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) G[r][j + 16 * i] = rs * ((dx[i] - m1) - x[i] * m2);
+}
+
+// Per-workgroup sums over the rows of dgamma = dy xh and dbeta = dy, where
+// dy = G (before ln_backward overwrote it) masked by h > 0.
+__device__ __forceinline__ void ln_param_sums(const float (*G)[HP], const float (*xh)[HP],
+                                              const float (*h)[HP], float* out_g, float* out_b) {
+  const int c = threadIdx.x;
+  if (c < H) {
+    float sg = 0.0f, sb = 0.0f;
+    for (int r = 0; r < R; ++r) {
+      const float dy = h[r][c] > 0.0f ? G[r][c] : 0.0f;
+      sg += dy * xh[r][c];
+      sb += dy;
+    }
+    out_g[c] = sg;
+    out_b[c] = sb;
+  }
+}
+
+// Masked categorical over K logits: log-softmax (masked entries at the
+// float32 minimum, as torch.where(mask, logits, finfo.min)), probabilities,
+// entropy H = -sum p log p over the clamped normalised logits.
+template <int K>
+__device__ __forceinline__ void masked_cat(const float* lg, const uint8_t* mask, float* lp, float* p,
+                                           float* ent) {
+  const float NEG = -3.4028234663852886e38f;
+  float z[K];
+  float m = NEG;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    z[k] = mask[k] ? lg[k] : NEG;
+    m = fmaxf(m, z[k]);
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) s += expf(z[k] - m);
+  const float lse = m + logf(s);
+  float h = 0.0f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    lp[k] = fmaxf(z[k] - lse, NEG);
+    p[k] = expf(z[k] - lse);
+    h -= lp[k] * p[k];
+  }
+  *ent = h;
+}
+
+__global__ __launch_bounds__(T) void ppo_grad_kernel(const qqt_ppo_args a) {
+  __shared__ Lds s;
+  const int t = threadIdx.x;
+  const int row0 = blockIdx.x * R;
+  const int nrows = min(R, a.batch - row0);
+
+  // ---- z1 tile (rows past the batch are zero and masked out of every sum)
+  for (int i = t; i < R * H / 4; i += T) {
+    const int r = i / (H / 4), c4 = i % (H / 4);
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (r < nrows) v = reinterpret_cast<const float4*>(a.z1 + (size_t)(row0 + r) * H)[c4];
+    *reinterpret_cast<float4*>(&s.z[r][4 * c4]) = v;
+  }
+  __syncthreads();
+  if (t < TR) ln_forward(s.z, a.ln1_w, a.ln1_b, s.xh1, s.h1, s.rstd1);
+  __syncthreads();
+  gemm<H, H, HP, HP>(s.h1, a.w1t, a.b1, s.z);               // z2 = h1 W1^T + b1
+  __syncthreads();
+  if (t < TR) ln_forward(s.z, a.ln2_w, a.ln2_b, s.xh2, s.h2, s.rstd2);
+  __syncthreads();
+  gemm<H, HY, HP, HYP>(s.h2, a.wht, a.bh, s.hy);            // heads' hidden layers
+  __syncthreads();
+  for (int i = t; i < R * HY; i += T) {
+    const int r = i / HY, c = i % HY;
+    s.hy[r][c] = fmaxf(s.hy[r][c], 0.0f);
+  }
+  __syncthreads();
+  if (t < R * 8) {                                            // outputs: 5 move, 2 bomb, value
+    const int r = t >> 3, j = t & 7;
+    const int base = j < 5 ? 0 : j < 7 ? 64 : 128;
+    float acc = a.bf[j];
+    for (int k = 0; k < 64; ++k) acc += s.hy[r][base + k] * a.wf[j * 64 + k];
+    s.logit[r][j] = acc;
+  }
+  __syncthreads();
+
+  // ---- loss terms and output gradients, one thread per row
+  if (t < R) {
+    const int r = t;
+    float dl[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float st[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+    if (r < nrows) {
+      const size_t g = (size_t)(row0 + r);
+      uint8_t mm[5], bm[2];
+#pragma unroll
+      for (int k = 0; k < 5; ++k) mm[k] = a.move_mask[g * 5 + k];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) bm[k] = a.bomb_mask[g * 2 + k];
+      const int am = (int)a.actions[g * 2 + 0], ab = (int)a.actions[g * 2 + 1];
+      float lpm[5], pm[5], lpb[2], pb[2], hm, hb;
+      masked_cat<5>(&s.logit[r][0], mm, lpm, pm, &hm);
+      masked_cat<2>(&s.logit[r][5], bm, lpb, pb, &hb);
+      float lpa = 0.0f, lpb_a = 0.0f;                          // select, not index (registers)
+#pragma unroll
+      for (int k = 0; k < 5; ++k) lpa = k == am ? lpm[k] : lpa;
+#pragma unroll
+      for (int k = 0; k < 2; ++k) lpb_a = k == ab ? lpb[k] : lpb_a;
+      const float logp = lpa + lpb_a;
+      const float v = s.logit[r][7];
+      const float B = (float)a.batch;
+      // policy term
+      const float ratio = expf(logp - a.old_logp[g]);
+      const float adv = a.adv[g];
+      const float cr = fminf(fmaxf(ratio, a.ratio_lo), a.ratio_hi);
+      const float s1 = ratio * adv, s2 = cr * adv;
+      const float w1 = s1 < s2 ? 1.0f : s1 == s2 ? 0.5f : 0.0f;
+      const float w2 = 1.0f - w1;
+      const float pass = (ratio >= a.ratio_lo && ratio <= a.ratio_hi) ? 1.0f : 0.0f;
+      const float gmin = -1.0f / B;                           // d loss / d min_i
+      const float glogp = gmin * (w1 * adv + w2 * adv * pass) * ratio;
+      // value term
+      const float ov = a.old_val[g], ret = a.ret[g];
+      const float dvc = v - ov;
+      const float vc = ov + fminf(fmaxf(dvc, -a.clip_eps), a.clip_eps);
+      const float e1 = (v - ret) * (v - ret), e2 = (vc - ret) * (vc - ret);
+      const float u1 = e1 > e2 ? 1.0f : e1 == e2 ? 0.5f : 0.0f;
+      const float u2 = 1.0f - u1;
+      const float vpass = (dvc >= -a.clip_eps && dvc <= a.clip_eps) ? 1.0f : 0.0f;
+      const float gmax = a.value_coef * 0.5f / B;             // d loss / d max_i
+      dl[7] = gmax * (u1 * 2.0f * (v - ret) + u2 * 2.0f * (vc - ret) * vpass);
+      // entropy term
+      const float gh = -a.entropy_coef / B;
+#pragma unroll
+      for (int k = 0; k < 5; ++k)
+        if (mm[k]) dl[k] = glogp * ((k == am ? 1.0f : 0.0f) - pm[k]) - gh * pm[k] * (lpm[k] + hm);
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        if (bm[k]) dl[5 + k] = glogp * ((k == ab ? 1.0f : 0.0f) - pb[k]) - gh * pb[k] * (lpb[k] + hb);
+      st[0] = -fminf(s1, s2);
+      st[1] = 0.5f * fmaxf(e1, e2);
+      st[2] = hm + hb;
+      st[3] = a.old_logp[g] - logp;
+      st[4] = fabsf(ratio - 1.0f) > a.clip_eps ? 1.0f : 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) a.dl[g * 8 + k] = dl[k];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s.dl[r][k] = dl[k];
+#pragma unroll
+    for (int k = 0; k < 5; ++k) s.stat[r][k] = st[k];
+  }
+  __syncthreads();
+  if (t < 5) {
+    float sum = 0.0f;
+    for (int r = 0; r < R; ++r) sum += s.stat[r][t];
+    a.stats_part[(size_t)blockIdx.x * 5 + t] = sum;
+  }
+
+  // ---- backward: output layer -> heads' hidden (ReLU)
+  for (int i = t; i < R * HY; i += T) {
+    const int r = i / HY, c = i % HY;
+    const int head = c >> 6, k = c & 63;
+    float d = 0.0f;
+    if (head == 0) {
+#pragma unroll
+      for (int j = 0; j < 5; ++j) d += s.dl[r][j] * a.wf[j * 64 + k];
+    } else if (head == 1) {
+      d = s.dl[r][5] * a.wf[5 * 64 + k] + s.dl[r][6] * a.wf[6 * 64 + k];
+    } else {
+      d = s.dl[r][7] * a.wf[7 * 64 + k];
+    }
+    s.dhy[r][c] = s.hy[r][c] > 0.0f ? d : 0.0f;
+  }
+  __syncthreads();
+  gemm<HY, H, HYP, HP>(s.dhy, a.wh, nullptr, s.g);          // dh2 = dhy Wh
+  __syncthreads();
+  if (t < H)
+    ln_param_sums(s.g, s.xh2, s.h2, a.ln_part + ((size_t)blockIdx.x * 4 + 2) * H,
+                  a.ln_part + ((size_t)blockIdx.x * 4 + 3) * H);
+  __syncthreads();
+  if (t < TR) ln_backward(s.g, s.xh2, s.h2, a.ln2_w, s.rstd2);   // s.g = dz2
+  __syncthreads();
+  gemm<H, H, HP, HP>(s.g, a.w1, nullptr, s.z);              // dh1 = dz2 W1
+  __syncthreads();
+  if (t < H)
+    ln_param_sums(s.z, s.xh1, s.h1, a.ln_part + ((size_t)blockIdx.x * 4 + 0) * H,
+                  a.ln_part + ((size_t)blockIdx.x * 4 + 1) * H);
+  __syncthreads();
+  if (t < TR) ln_backward(s.z, s.xh1, s.h1, a.ln1_w, s.rstd1);   // s.z = dz1
+  __syncthreads();
+
+  // ---- row outputs
+  for (int i = t; i < R * H; i += T) {
+    const int r = i / H, c = i % H;
+    if (r < nrows) {
+      const size_t o = (size_t)(row0 + r) * H + c;
+      a.dz1[o] = s.z[r][c];
+      a.dz2[o] = s.g[r][c];
+      a.h1[o] = s.h1[r][c];
+      a.h2[o] = s.h2[r][c];
+    }
+  }
+  for (int i = t; i < R * HY; i += T) {
+    const int r = i / HY, c = i % HY;
+    if (r < nrows) {
+      const size_t o = (size_t)(row0 + r) * HY + c;
+      a.hy[o] = s.hy[r][c];
+      a.dhy[o] = s.dhy[r][c];
+    }
+  }
+}
+
+}  // namespace ppo
+}  // namespace qqt
+
+extern "C" {
+
+int qqt_ppo_grad(const qqt_ppo_args* a, void* stream) {
+  using namespace qqt;
+  using namespace qqt::ppo;
+  g_err[0] = 0;
+  if (!a || !a->z1 || !a->ln1_w || !a->ln1_b || !a->w1 || !a->w1t || !a->b1 || !a->ln2_w ||
+      !a->ln2_b || !a->wh || !a->wht || !a->bh || !a->wf || !a->bf || !a->actions ||
+      !a->move_mask || !a->bomb_mask || !a->old_logp || !a->adv || !a->ret || !a->old_val ||
+      !a->dz1 || !a->h1 || !a->dz2 || !a->h2 || !a->hy || !a->dhy || !a->dl || !a->ln_part ||
+      !a->stats_part) {
+    snprintf(g_err, sizeof(g_err), "qqt_ppo_grad: null argument");
+    return QQT_E_ARG;
+  }
+  const uintptr_t al = (uintptr_t)a->z1 | (uintptr_t)a->w1 | (uintptr_t)a->w1t | (uintptr_t)a->b1 |
+                       (uintptr_t)a->wh | (uintptr_t)a->wht | (uintptr_t)a->bh;
+  if (a->batch <= 0 || (al & 15) || !(a->clip_eps >= 0.0f)) {
+    snprintf(g_err, sizeof(g_err), "qqt_ppo_grad: bad batch, clip or 16-byte alignment");
+    return QQT_E_ARG;
+  }
+  const int blocks = (a->batch + R - 1) / R;
+  QQT_LAUNCH(QQT_KERNEL_PPO, ppo_grad_kernel, dim3(blocks), dim3(T), (hipStream_t)stream, *a);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    snprintf(g_err, sizeof(g_err), "ppo grad launch failed: %s", hipGetErrorString(err));
+    return QQT_E_LAUNCH;
+  }
+  return QQT_OK;
+}
+
+}  // extern "C"

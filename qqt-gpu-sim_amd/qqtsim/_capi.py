@@ -14,7 +14,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 
 from ._build import LIB
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 MODE_STEP, MODE_OBSERVE, MODE_RESET, MODE_PROBE, MODE_FLUSH = 0, 1, 2, 3, 4
 MAP_PILLARS, MAP_OPEN, MAP_REFERENCE = 0, 1, 2
@@ -83,6 +83,15 @@ class L1GradArgsC(ctypes.Structure):
         (n, _vp) for n in ("obs", "dz1", "dz_scale", "workspace", "dw0")]
 
 
+class PpoArgsC(ctypes.Structure):
+    _fields_ = [("batch", _i32)] + [(n, _f32) for n in (
+        "clip_eps", "ratio_lo", "ratio_hi", "value_coef", "entropy_coef")] + [
+        (n, _vp) for n in ("z1", "ln1_w", "ln1_b", "w1", "w1t", "b1", "ln2_w", "ln2_b", "wh",
+                           "wht", "bh", "wf", "bf", "actions", "move_mask", "bomb_mask",
+                           "old_logp", "adv", "ret", "old_val", "dz1", "h1", "dz2", "h2", "hy",
+                           "dhy", "dl", "ln_part", "stats_part")]
+
+
 class GaeArgsC(ctypes.Structure):
     _fields_ = [("steps", _i32), ("n_envs", _i32), ("gamma", _f32), ("gamma_lam", _f32),
                 ("step_stride", ctypes.c_int64), ("env_stride", ctypes.c_int64)] + [
@@ -114,6 +123,8 @@ def lib():
         L.qqt_l1_grad.argtypes = [ctypes.POINTER(L1GradArgsC), _vp]
         L.qqt_l1_grad_workspace_floats.restype = ctypes.c_int64
         L.qqt_l1_grad_workspace_floats.argtypes = [_i32, _i32]
+        L.qqt_ppo_grad.restype = ctypes.c_int
+        L.qqt_ppo_grad.argtypes = [ctypes.POINTER(PpoArgsC), _vp]
         L.qqt_timing_arm.restype = ctypes.c_int
         L.qqt_timing_arm.argtypes = [_i32]
         L.qqt_timing_collect.restype = ctypes.c_int
@@ -125,7 +136,7 @@ def lib():
 
 
 KERNEL_KINDS = ("tick_kernel", "mlp_act_kernel", "bot_kernel", "reach_kernel",
-                "gae_kernel", "l1grad_kernels")  # QQT_KERNEL_*
+                "gae_kernel", "l1grad_kernels", "ppo_grad_kernel")  # QQT_KERNEL_*
 
 
 def timing_arm(launches: int) -> None:

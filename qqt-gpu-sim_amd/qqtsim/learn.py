@@ -201,6 +201,76 @@ class HipMlpActorCritic(nn.Module):
         return (self.masked_dist(ml, move_mask.bool()), self.masked_dist(bl, bomb_mask.bool()),
                 val)
 
+    def ppo_grads(self, obs, move_mask, bomb_mask, actions, old_logp, adv, ret, old_val,
+                  cfg, entropy_coef: float) -> torch.Tensor:
+        """Gradients of the reference's minibatch PPO loss (train/ppo.py:401-421,
+        player 0's view) written into every parameter's `.grad`, as
+        `loss.backward()` through `evaluate` would leave them; returns the
+        five statistics (pg, vf, ent, kl, clipfrac) as a device tensor.
+        Three launches: the first layer's forward, `qqt_ppo_grad` (the loss
+        and the backward above the first layer) and `qqt_l1_grad`; the weight
+        gradients of the 128-wide layers are batched products of its row
+        outputs."""
+        b = obs.shape[0]
+        dev = obs.device
+        x16 = obs.reshape(b, -1)
+        x16 = (x16 if x16.dtype == torch.float16 else x16.half()).contiguous()
+        l0 = self.shared[0]
+        z1 = self._l1_forward(x16, l0.weight, l0.bias, 0)
+        heads = (self.move_head, self.bomb_head, self.critic)
+        w1 = self.shared[3].weight.detach().contiguous()
+        wh = torch.cat([h[0].weight.detach() for h in heads]).contiguous()
+        wf = torch.cat([h[2].weight.detach() for h in heads]).contiguous()      # (8, 64)
+        bf = torch.cat([h[2].bias.detach() for h in heads]).contiguous()
+        bh = torch.cat([h[0].bias.detach() for h in heads]).contiguous()
+        f32 = dict(dtype=torch.float32, device=dev)
+        nb = -(-b // 16)
+        out = dict(dz1=torch.empty((b, HID), **f32), h1=torch.empty((b, HID), **f32),
+                   dz2=torch.empty((b, HID), **f32), h2=torch.empty((b, HID), **f32),
+                   hy=torch.empty((b, 3 * HEAD), **f32), dhy=torch.empty((b, 3 * HEAD), **f32),
+                   dl=torch.empty((b, 8), **f32), ln_part=torch.empty((nb, 4, HID), **f32),
+                   stats_part=torch.empty((nb, 5), **f32))
+        keep = dict(z1=z1, ln1_w=self.shared[1].weight.detach().contiguous(),
+                    ln1_b=self.shared[1].bias.detach().contiguous(), w1=w1,
+                    w1t=w1.t().contiguous(), b1=self.shared[3].bias.detach().contiguous(),
+                    ln2_w=self.shared[4].weight.detach().contiguous(),
+                    ln2_b=self.shared[4].bias.detach().contiguous(), wh=wh,
+                    wht=wh.t().contiguous(), bh=bh, wf=wf, bf=bf,
+                    actions=actions.to(torch.int64).contiguous(),
+                    move_mask=move_mask.to(torch.uint8).contiguous(),
+                    bomb_mask=bomb_mask.to(torch.uint8).contiguous(),
+                    old_logp=old_logp.float().contiguous(), adv=adv.float().contiguous(),
+                    ret=ret.float().contiguous(), old_val=old_val.float().contiguous())
+        a = _capi.PpoArgsC()
+        a.batch = b
+        a.clip_eps = cfg.clip_eps
+        a.ratio_lo, a.ratio_hi = 1 - cfg.clip_eps, 1 + cfg.clip_eps
+        a.value_coef, a.entropy_coef = cfg.value_coef, entropy_coef
+        for k, v in list(keep.items()) + list(out.items()):
+            setattr(a, k, v.data_ptr())
+        _capi.check(self._lib.qqt_ppo_grad(a, _capi.stream_handle(dev)))
+        dz1, dz2, dhy, dl = out["dz1"], out["dz2"], out["dhy"], out["dl"]
+        h1, h2, hy = out["h1"], out["h2"], out["hy"]
+        l0.weight.grad = self._l1_weight_grad(x16, dz1, 0)
+        l0.bias.grad = dz1.sum(0)
+        ln = out["ln_part"].sum(0)
+        self.shared[1].weight.grad, self.shared[1].bias.grad = ln[0], ln[1]
+        self.shared[4].weight.grad, self.shared[4].bias.grad = ln[2], ln[3]
+        self.shared[3].weight.grad = _weight_grad(dz2, h1)
+        self.shared[3].bias.grad = dz2.sum(0)
+        dwh = _weight_grad(dhy, h2)
+        dbh = dhy.sum(0)
+        rows = 0
+        for i, h in enumerate(heads):
+            h[0].weight.grad = dwh[HEAD * i:HEAD * (i + 1)].contiguous()
+            h[0].bias.grad = dbh[HEAD * i:HEAD * (i + 1)].contiguous()
+            n_out = h[2].weight.shape[0]
+            h[2].weight.grad = _weight_grad(dl[:, rows:rows + n_out].contiguous(),
+                                            hy[:, HEAD * i:HEAD * (i + 1)].contiguous())
+            h[2].bias.grad = dl[:, rows:rows + n_out].sum(0)
+            rows += n_out
+        return out["stats_part"].sum(0) / b
+
     def evaluate(self, obs, move_mask, bomb_mask, actions, pid: int = 0):
         """(logp, entropy, value) of given actions (train/model.py:247-256)."""
         dm, db, val = self.dists(obs, move_mask, bomb_mask, pid)
@@ -232,8 +302,10 @@ def ppo_update(learner, opt, buf, last_val, cfg: PPOConfig, entropy_coef: float)
     minibatches of clipped policy loss + clipped value loss - entropy bonus,
     gradient-norm clipping, optimizer step).  `buf` is a HipRolloutBuffer
     (or any buffer with the reference's fields); the GAE scan is
-    `qqt_gae`.  The statistics are summed on the device and read once at the
-    end (the reference reads them after every minibatch)."""
+    `qqt_gae`.  A learner with `ppo_grads` (HipMlpActorCritic) takes the
+    fused loss + backward; any other learner the reference's autograd
+    path.  The statistics are summed on the device and read once at the end
+    (the reference reads them after every minibatch)."""
     adv, ret = compute_gae(buf, last_val, cfg.gamma, cfg.gae_lambda)
     flat = lambda x: x.reshape(-1, *x.shape[2:])  # noqa: E731
     obs = flat(buf.obs)
@@ -258,6 +330,15 @@ def ppo_update(learner, opt, buf, last_val, cfg: PPOConfig, entropy_coef: float)
         perm = pool[torch.randperm(pool.numel(), device=dev)][:total]
         for start in range(0, total, mb):
             sel = perm[start:start + mb]
+            if hasattr(learner, "ppo_grads"):       # the fused loss + backward
+                opt.zero_grad(set_to_none=True)
+                st = learner.ppo_grads(obs[sel], mmask[sel], bmask[sel], act[sel], old_logp[sel],
+                                       adv[sel], ret[sel], old_val[sel], cfg, entropy_coef)
+                torch.nn.utils.clip_grad_norm_(learner.parameters(), cfg.max_grad_norm)
+                opt.step()
+                acc += st
+                n_updates += 1
+                continue
             logp, entropy, value = learner.evaluate(obs[sel], mmask[sel], bmask[sel], act[sel])
             ratio = (logp - old_logp[sel]).exp()
             pg = -torch.min(ratio * adv[sel],

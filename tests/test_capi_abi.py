@@ -41,7 +41,7 @@ def _declared_functions():
 def test_header_declares_the_entry_points():
     assert _declared_functions() == ["qqt_abi_version", "qqt_bot_act", "qqt_gae",
                                      "qqt_l1_grad", "qqt_l1_grad_workspace_floats",
-                                     "qqt_last_error", "qqt_mlp_act", "qqt_tick",
+                                     "qqt_last_error", "qqt_mlp_act", "qqt_ppo_grad", "qqt_tick",
                                      "qqt_timing_arm", "qqt_timing_collect"]
 
 
@@ -91,7 +91,8 @@ def test_struct_layouts_match_the_header(tmp_path):
 
     structs = {"qqt_sim_config": _capi.SimConfigC, "qqt_tick_args": _capi.TickArgsC,
                "qqt_mlp_args": _capi.MlpArgsC, "qqt_bot_args": _capi.BotArgsC,
-               "qqt_gae_args": _capi.GaeArgsC, "qqt_l1_grad_args": _capi.L1GradArgsC}
+               "qqt_gae_args": _capi.GaeArgsC, "qqt_l1_grad_args": _capi.L1GradArgsC,
+               "qqt_ppo_args": _capi.PpoArgsC}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "qqt_hip.h"',
              'int main(void) {']
     for cname, cls in structs.items():
@@ -254,7 +255,7 @@ def test_header_kernel_kinds_match_host_mirror():
     text = open(HEADER).read()
     kinds = dict((k, int(v)) for k, v in re.findall(r"\bQQT_KERNEL_(\w+) = (\d+)", text))
     assert kinds["KINDS"] == len(_capi.KERNEL_KINDS)
-    for name in ("TICK", "MLP", "BOT", "REACH", "GAE", "L1GRAD"):
+    for name in ("TICK", "MLP", "BOT", "REACH", "GAE", "L1GRAD", "PPO"):
         assert _capi.KERNEL_KINDS[kinds[name]].startswith(name.lower()), name
 
 

@@ -225,3 +225,50 @@ def test_ppo_update_runs_on_a_collected_buffer(dev):
     after = learner.state_dict()
     for k, v in before.items():
         assert not torch.equal(v, after[k]), k
+
+
+def test_fused_ppo_grads_match_autograd(dev):
+    """qqt_ppo_grad (+ the first layer's kernels): every parameter gradient
+    and the five statistics equal what loss.backward() through evaluate()
+    gives on the same module (float32, summation order aside), on a ragged
+    batch (3001 rows: the last 16-row block is partial) with masked moves,
+    masked bombs, clipped and unclipped ratios and value errors."""
+    from qqtsim.learn import HipMlpActorCritic, PPOConfig
+
+    sd = _ortho_init(11)
+    net = HipMlpActorCritic(device=dev, state_dict=sd)
+    g = torch.Generator().manual_seed(5)
+    b = 3001
+    obs = _obs(b, g).reshape(b, 14, 13, 13).to(dev)
+    mm = (torch.rand((b, 5), generator=g) < 0.6).to(dev)
+    mm[:, 4] = True
+    bm = torch.ones((b, 2), dtype=torch.bool, device=dev)
+    bm[:, 1] = (torch.rand(b, generator=g) < 0.5).to(dev)
+    act = torch.stack([torch.multinomial(mm.float().cpu(), 1, generator=g)[:, 0],
+                       torch.multinomial(bm.float().cpu(), 1, generator=g)[:, 0]], 1).to(dev)
+    with torch.no_grad():
+        lp0, _, v0 = net.evaluate(obs, mm, bm, act)
+    # old log-probs and values around the current ones: ratios and value
+    # moves on both sides of the clip range
+    old_logp = lp0 + (torch.randn(b, generator=g) * 0.3).to(dev)
+    old_val = v0 + (torch.randn(b, generator=g) * 0.3).to(dev)
+    adv = torch.randn(b, generator=g).to(dev)
+    ret = old_val + torch.randn(b, generator=g).to(dev)
+    cfg = PPOConfig()
+
+    loss, (lp, ent, v) = _loss(net, obs, mm, bm, act, old_logp, adv, ret, old_val, 0)
+    loss.backward()
+    want = {k: p.grad.detach().clone() for k, p in net.named_parameters()}
+    ratio = (lp - old_logp).exp()
+    want_st = torch.stack([
+        -torch.min(ratio * adv, ratio.clamp(0.8, 1.2) * adv).mean(),
+        0.5 * torch.max((v - ret) ** 2, (old_val + (v - old_val).clamp(-0.2, 0.2) - ret) ** 2).mean(),
+        ent.mean(), (old_logp - lp).mean(), ((ratio - 1).abs() > 0.2).float().mean()]).detach()
+    clipped = float(((ratio - 1).abs() > 0.2).float().mean())
+    assert 0.1 < clipped < 0.9, clipped
+    net.zero_grad(set_to_none=True)
+    st = net.ppo_grads(obs, mm, bm, act, old_logp, adv, ret, old_val, cfg, 0.05)
+    for k, p in net.named_parameters():
+        err = float((p.grad - want[k]).norm() / want[k].norm().clamp_min(1e-12))
+        assert err <= 2e-4, (k, err)
+    assert float((st - want_st).abs().max()) <= 1e-5 * max(1.0, float(want_st.abs().max()))
