@@ -77,7 +77,7 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="CPU work budget of the cpu_baseline sample (0 = skip)")
     ap.add_argument("--workload", choices=("rollout", "stress", "astar", "evalfwd", "collect",
-                                           "ppo"),
+                                           "ppo", "train"),
                     default="rollout",
                     help="rollout: the headline self-play rollout (default); stress: "
                          "16384-env bomb-stress ticks with injected actions; astar: "
@@ -86,7 +86,9 @@ def parse_args():
                          "evaluation forward over all 4.19M observations; collect: "
                          "128-step self-play collects into the device rollout buffer "
                          "(5632 envs) + last-value forward + GAE; ppo: one PPO update "
-                         "(4 epochs x 4 minibatches) over a 5632 x 128 collected buffer")
+                         "(4 epochs x 4 minibatches) over a 5632 x 128 collected buffer; "
+                         "train: whole training iterations (collect 128 steps + PPO update "
+                         "+ weight sync to the acting network)")
     ap.add_argument("--copy-calibrate", action="store_true",
                     help="after timing, run a 512 MiB device copy (HBM counter calibration)")
     return ap.parse_args()
@@ -255,6 +257,8 @@ def main():
         return main_collect(args, torch, dev)
     if args.workload == "ppo":
         return main_ppo(args, torch, dev)
+    if args.workload == "train":
+        return main_train(args, torch, dev)
     n, K, W = args.envs, args.steps, args.warmup
     cfg, spec, roll = build_workload(n, args.seed, dev)
     for _ in range(W):
@@ -941,6 +945,62 @@ def main_ppo(args, torch, dev):
                                "note": "same update, the reference's network as float32 "
                                        "eager torch modules"},
         "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+
+
+def main_train(args, torch, dev):
+    """Whole training iterations of the reference's loop (train/ppo.py:197-314
+    collect + :364-437 update): 128 self-play steps of 5632 envs into the
+    device rollout buffer (both players acted by the current network), the
+    learner's value of the last observation, one PPO update (4 epochs x 4
+    minibatches) and the copy of the updated weights into the acting
+    network.  `value` is env-steps per second of the whole iteration (the
+    reference's "sps")."""
+    from qqtsim import HipMlpActorCritic, HipRolloutBuffer, PPOConfig, ppo_update
+    from qqtsim.policy import default_init
+
+    n = args.envs
+    cfg, spec, roll = build_workload(n, args.seed, dev)
+    for _ in range(max(1, args.warmup)):
+        roll.step()
+    buf = HipRolloutBuffer(COLLECT_T, n, cfg.obs_shape, dev)
+    pcfg = PPOConfig()
+    learner = HipMlpActorCritic(cfg.obs_shape, device=dev, state_dict=default_init(cfg.obs_shape))
+    opt = torch.optim.Adam(learner.parameters(), lr=pcfg.lr)
+    actor = roll.policy
+
+    def iteration():
+        roll.collect(buf)
+        last_val = actor.forward(roll.sim.observe(), 0)[2]
+        st = ppo_update(learner, opt, buf, last_val, pcfg, pcfg.entropy_coef)
+        actor.load_state_dict(learner.state_dict())
+        return st
+
+    torch.manual_seed(0)
+    iteration()                                      # warm-up iteration
+    torch.cuda.synchronize()
+    iters = 3 if args.steps >= 256 else max(1, min(args.steps, 3))
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        st = iteration()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    steps = iters * COLLECT_T * n
+    res = {
+        "metric": "training env-steps/s (collect 128 steps x 5632 envs + PPO update + weight "
+                  "sync), 1 MI355X",
+        "value": steps / el, "unit": "env-steps/s", "n_gpus": 1, "steps": iters, "warmup": 1,
+        "ms_per_step": el / iters * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 sim / f16 MFMA acting / f16 MFMA first layer + f32 fused loss and "
+                 "backward in the update",
+        "data": "synthetic: template maps from Philox draws, PyTorch default-init weights",
+        "config": {"workload": "training iteration: collect (5632 envs x 128 steps) + PPO "
+                               "update (4 epochs x 4 minibatches) + weight sync",
+                   "envs": n, "collect_steps": COLLECT_T, "parallelism": "single GPU"},
+        "last_update_stats": st,
+        "cpu_baseline": None,
     }
     print(json.dumps(res), flush=True)
 
