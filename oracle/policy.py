@@ -134,3 +134,34 @@ def mlp_forward(params: dict, obs: torch.Tensor, pid: int, n_players: int = 2,
         return F.linear(y, P[f"{name}.2.weight"], P[f"{name}.2.bias"])
 
     return head("move_head"), head("bomb_head"), head("critic").squeeze(-1)
+
+
+def cnn_forward(params: dict, obs: torch.Tensor, pid: int, n_players: int = 2,
+                dtype=torch.float32):
+    """(move_logits, bomb_logits, value) of the cnn ActorCritic for player
+    `pid` (train/model.py:79-96, 186-190): conv0 reads the observation
+    through the view permutation of its input channels, then 3x3 convs
+    16 -> 32 -> 64 and a 1x1 conv to 8 channels, each followed by a
+    per-sample LayerNorm over [C, H, W] and ReLU, then the shared MLP
+    (1352 -> 128 -> 128) and the heads."""
+    P = {k: v.to(dtype) for k, v in params.items()}
+    c, h, w = obs.shape[1:]
+    inv = torch.argsort(torch.tensor(view_perm(pid, n_players, c)))
+    x = F.conv2d(obs.to(dtype), P["conv0.weight"][:, inv], P["conv0.bias"], padding=1)
+    for ln, conv in (("conv.0", "conv.2"), ("conv.3", "conv.5"), ("conv.6", "conv.8"),
+                     ("conv.9", None)):
+        x = F.relu(F.layer_norm(x, tuple(x.shape[1:]), P[f"{ln}.weight"], P[f"{ln}.bias"]))
+        if conv is not None:
+            k = P[f"{conv}.weight"].shape[-1]
+            x = F.conv2d(x, P[f"{conv}.weight"], P[f"{conv}.bias"], padding=k // 2)
+    x = x.flatten(1)
+    x = F.linear(x, P["shared.0.weight"], P["shared.0.bias"])
+    x = F.relu(F.layer_norm(x, (x.shape[-1],), P["shared.1.weight"], P["shared.1.bias"]))
+    x = F.linear(x, P["shared.3.weight"], P["shared.3.bias"])
+    x = F.relu(F.layer_norm(x, (x.shape[-1],), P["shared.4.weight"], P["shared.4.bias"]))
+
+    def head(name):
+        y = F.relu(F.linear(x, P[f"{name}.0.weight"], P[f"{name}.0.bias"]))
+        return F.linear(y, P[f"{name}.2.weight"], P[f"{name}.2.bias"])
+
+    return head("move_head"), head("bomb_head"), head("critic").squeeze(-1)

@@ -24,6 +24,8 @@ permutation):
   observation of envs 0..3.
 * deep_chain.npz - single-tick states with chains longer than 8 rounds.
 * mlp.npz - MLP ActorCritic weights, inputs and forward/evaluate outputs.
+* cnn.npz - the same for ActorCritic(arch="cnn") (conv trunk with the view
+  permutation on conv0's input channels, per-sample LayerNorms).
 * astar_<name>.npz - the reference astar bot (sim/bots.py astar_attack, no
   behaviour modes, no crate eating) as player 1 against random legal moves
   for player 0: per tick the bot's inputs (state, observation, masks, the
@@ -233,14 +235,15 @@ def deep_chain():
     print("deep_chain: trig per env", info["trig"].flatten(1).sum(1).tolist())
 
 
-def mlp(traj_name="pillars70"):
+def mlp(traj_name="pillars70", arch="mlp"):
     torch.manual_seed(0)
-    net = ActorCritic((14, 13, 13), arch="mlp", n_players=2)
+    net = ActorCritic((14, 13, 13), arch=arch, n_players=2)
     # Perturb biases and LayerNorm affine terms so every parameter matters.
     g = torch.Generator().manual_seed(1)
     with torch.no_grad():
         for name, prm in net.named_parameters():
-            if name.endswith("bias") or ".1." in name or ".4." in name:
+            if name.endswith("bias") or ".1." in name or ".4." in name or (
+                    arch == "cnn" and name.startswith("conv.")):
                 prm.add_(0.1 * torch.randn(prm.shape, generator=g))
     z = np.load(os.path.join(HERE, f"traj_{traj_name}.npz"))
     obs = torch.from_numpy(z["obs"][::4].reshape(-1, 14, 13, 13)[:96].copy())
@@ -264,8 +267,8 @@ def mlp(traj_name="pillars70"):
             out[f"logp_{pid}"] = lp.numpy()
             out[f"entropy_{pid}"] = ent.numpy()
     out["param_count"] = np.int64(sum(p.numel() for p in net.parameters()))
-    np.savez_compressed(os.path.join(HERE, "mlp.npz"), **out)
-    print("mlp: batch", b, "params", int(out["param_count"]))
+    np.savez_compressed(os.path.join(HERE, f"{arch}.npz"), **out)
+    print(f"{arch}: batch", b, "params", int(out["param_count"]))
 
 
 def astar(name, spec, n=64, ticks=64, seed=11):
@@ -368,6 +371,8 @@ if __name__ == "__main__" and len(sys.argv) > 1:
             astar("open", MapSpec(kind="open", bombs_cap=(2, 3), blast_cap=(2, 4)), ticks=96,
                   seed=17)
             astar_chain()
+        elif what == "cnn":
+            mlp(arch="cnn")
         else:
             raise SystemExit(f"unknown fixture group {what!r}")
 elif __name__ == "__main__":
@@ -380,6 +385,7 @@ elif __name__ == "__main__":
             cfg_kw=dict(max_hp=2, invuln_ticks=4, max_steps=70))
     deep_chain()
     mlp()
+    mlp(arch="cnn")
     astar("p70", MapSpec(kind="pillars", brick_p=0.7))
     astar("p30", MapSpec(kind="pillars", brick_p=0.3, bombs_cap=(2, 4), blast_cap=(2, 5)),
           seed=13)

@@ -76,3 +76,14 @@ def mlp_params(z):
             if name.startswith(pre):
                 out[pre + "." + name[len(pre) + 1:].replace("_", ".")] = torch.from_numpy(z[k])
     return out
+
+
+def cnn_params(z):
+    """state_dict of the cnn ActorCritic from cnn.npz's w_* arrays."""
+    out = mlp_params(z)
+    for k in z.files:
+        if k.startswith("w_conv0_"):
+            out["conv0." + k[len("w_conv0_"):]] = torch.from_numpy(z[k])
+        elif k.startswith("w_conv_"):
+            out["conv." + k[len("w_conv_"):].replace("_", ".")] = torch.from_numpy(z[k])
+    return out

@@ -173,3 +173,24 @@ def test_oracle_logp_matches_reference_evaluate():
             s = exp_f32(lg - m[:, None]).sum(1).astype(np.float32)
             total += (lg[np.arange(len(act)), act] - m) - log_f32(s)
         np.testing.assert_allclose(total, z[f"logp_{pid}"], atol=2e-6)
+
+
+def test_oracle_cnn_matches_reference_forward():
+    """ActorCritic(arch="cnn") (train/model.py:79-96, 186-190): the oracle's
+    restatement equals the reference module's forward on 96 recorded
+    observations for both players (view permutation on conv0's inputs)."""
+    from golden_io import cnn_params
+    from oracle.policy import cnn_forward
+
+    z = np.load(__import__("golden_io").GOLDEN + "/cnn.npz")
+    params = cnn_params(z)
+    assert sum(v.numel() for v in params.values()) == 281744 == int(z["param_count"])
+    obs = torch.from_numpy(z["obs"])
+    for pid in range(2):
+        ml, bl, v = cnn_forward(params, obs, pid)
+        np.testing.assert_allclose(ml.numpy(), z[f"move_logits_{pid}"], rtol=0, atol=1e-5)
+        np.testing.assert_allclose(bl.numpy(), z[f"bomb_logits_{pid}"], rtol=0, atol=1e-5)
+        np.testing.assert_allclose(v.numpy(), z[f"value_{pid}"], rtol=0, atol=1e-5)
+    ml0 = cnn_forward(params, obs, 0)[0]
+    ml1 = cnn_forward(params, obs, 1)[0]
+    assert float((ml0 - ml1).abs().max()) > 1e-3, "the two views differ"
