@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 8
+#define QQT_ABI_VERSION 9
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -315,6 +315,51 @@ typedef struct qqt_ppo_args {
 } qqt_ppo_args;
 int qqt_ppo_grad(const qqt_ppo_args* args, void* stream);
 
+/* Forward of the cnn actor/critic (train/model.py:79-96, 186-190) with
+ * optional masked factored sampling, one workgroup per (row, player).
+ * Replaces ActorCritic.act / forward for arch "cnn" (:167-196, 230-245) as
+ * qqt_mlp_act does for the MLP: the same masks, uniforms and output layout.
+ * Every LayerNorm normalises one sample over all of its values (eps 1e-5)
+ * with an elementwise affine of that shape; weights are float32, K-major
+ * (index [k][out]); a 3x3 conv's k is ci * 9 + 3 dy + dx. */
+typedef struct qqt_cnn_args {
+  int32_t batch;              /* rows B */
+  int32_t npid;               /* 1: player pid0 only; 2: both players */
+  int32_t pid0;
+  int32_t sample;             /* 1: draw actions (needs masks) */
+  int32_t obs_stride;         /* elements between observation rows (>= 14*169) */
+  int32_t mm_row_stride, mm_pid_stride;  /* move mask [row*rs + pid*ps + k] */
+  int32_t bm_row_stride, bm_pid_stride;  /* bomb mask */
+  int32_t w_players;          /* player views c0w holds (pid0, npid < it) */
+  uint64_t seed;              /* Philox key of the policy uniforms */
+  uint32_t tick;              /* counter word of the policy uniforms */
+  int32_t out_slots;          /* player slots per output row (0 = npid) */
+  int32_t out_slot;           /* slot written when npid == 1 */
+  int32_t reserved;
+  const uint16_t* obs;        /* [B][obs_stride] float16 bits, [14][13][13] per row */
+  const float* c0w;           /* [w_players][126][16]: conv0 with player p's view
+                                 permutation folded into its input channels */
+  const float *c0b, *ln0w, *ln0b;   /* [16], [16*169] x 2 */
+  const float *c1w, *c1b, *ln1w, *ln1b;   /* [144][32], [32], [32*169] x 2 */
+  const float *c2w, *c2b, *ln2w, *ln2b;   /* [288][64], [64], [64*169] x 2 */
+  const float *c3w, *c3b, *ln3w, *ln3b;   /* 1x1: [64][8], [8], [8*169] x 2 */
+  const float *s0wt, *s0b;    /* [1352][128], [128] */
+  const float *s1w, *s1b;     /* LayerNorm(128) */
+  const float *s3wt, *s3b;    /* [128][128], [128] */
+  const float *s4w, *s4b;     /* LayerNorm(128) */
+  const float *hwt, *hb;      /* [128][192] (move | bomb | critic hidden), [192] */
+  const float *fw, *fb;       /* [8][64]: move rows 0-4, bomb 5-6, critic 7; [8] */
+  const uint8_t* move_mask;
+  const uint8_t* bomb_mask;
+  const float* uniforms;      /* [B][out_slots][2] (move, bomb) or NULL = Philox */
+  int64_t* actions;           /* [B][out_slots][2] or NULL */
+  int8_t* actions_i8;         /* [B][out_slots][2] or NULL */
+  float* logp_out;            /* [B][out_slots] or NULL */
+  float* value_out;           /* [B][out_slots] or NULL */
+  float* logits_out;          /* [B][out_slots][8]: 5 move, 2 bomb, value; or NULL */
+} qqt_cnn_args;
+int qqt_cnn_act(const qqt_cnn_args* args, void* stream);
+
 /* Dispatch timing for benchmark harnesses (no counterpart in the reference:
  * its bench times whole steps with host clocks).  qqt_timing_arm(n) times
  * the next n kernel launches made through this library: each records a
@@ -325,7 +370,8 @@ int qqt_ppo_grad(const qqt_ppo_args* args, void* stream);
  * most 4096 launches are timed between collects.  Allocates no device
  * memory (the event pool is created by the first arm). */
 enum { QQT_KERNEL_TICK = 0, QQT_KERNEL_MLP = 1, QQT_KERNEL_BOT = 2, QQT_KERNEL_REACH = 3,
-       QQT_KERNEL_GAE = 4, QQT_KERNEL_L1GRAD = 5, QQT_KERNEL_PPO = 6, QQT_KERNEL_KINDS = 7 };
+       QQT_KERNEL_GAE = 4, QQT_KERNEL_L1GRAD = 5, QQT_KERNEL_PPO = 6, QQT_KERNEL_CNN = 7,
+       QQT_KERNEL_KINDS = 8 };
 int qqt_timing_arm(int32_t launches);
 int qqt_timing_collect(double* ms, int32_t* count, int32_t n_kinds);
 

@@ -256,37 +256,6 @@ __device__ __forceinline__ void split_gemm(floatx4 (&acc)[RT][CT], const uint16_
   }
 }
 
-// Masked categorical draw by inverse CDF on injected uniforms; same float32
-// operation sequence as the host sampler (oracle/policy.py).
-template <int K>
-__device__ __forceinline__ int sample_masked(const float* logit, const uint8_t* mask, float u,
-                                             float* logp) {
-  const float NEG = -3.4028234663852886e38f;
-  float ml[K], ex[K];
-#pragma unroll
-  for (int k = 0; k < K; ++k) ml[k] = mask[k] ? logit[k] : NEG;
-  float m = ml[0];
-#pragma unroll
-  for (int k = 1; k < K; ++k) m = fmaxf(m, ml[k]);
-#pragma unroll
-  for (int k = 0; k < K; ++k) ex[k] = exp_q(ml[k] - m);
-  float sum = ex[0];
-#pragma unroll
-  for (int k = 1; k < K; ++k) sum = sum + ex[k];
-  const float t = u * sum;
-  float run = 0.0f;
-  int count = 0, last = 0;
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    run = run + ex[k];
-    count += run <= t;
-    if (ex[k] > 0.0f) last = k;
-  }
-  const int a = count >= K ? last : count;
-  *logp = (ml[a] - m) - log_q(sum);
-  return a;
-}
-
 // RB row blocks of 64 per workgroup: RB = 2 halves the W0 bytes each row
 // costs (large forward batches, no sampling); the tail runs once per block.
 // Z1: the first-layer-only instantiation of the training forward (z1_out).

@@ -14,12 +14,12 @@ from .learn import HipMlpActorCritic, PPOConfig, ppo_update
 from .config import SimConfig, corridor_training_config
 from .factory import make_sim
 from .maps import BOMB_STRESS_40, CORRIDOR_70, OPEN_PILLARS, MapSpec
-from .policy import HipActorCritic, default_init
+from .policy import HipActorCritic, HipCnnActorCritic, default_init, default_init_cnn
 from .ppo import HipRolloutBuffer, compute_gae
 from .rollout import Rollout
 from .sim import HipBatchedSim
 
 __all__ = ["HipAstarBot", "SimConfig", "corridor_training_config", "make_sim", "MapSpec", "OPEN_PILLARS",
-           "CORRIDOR_70", "BOMB_STRESS_40", "HipActorCritic", "default_init", "Rollout",
+           "CORRIDOR_70", "BOMB_STRESS_40", "HipActorCritic", "HipCnnActorCritic", "default_init", "default_init_cnn", "Rollout",
            "HipBatchedSim", "HipRolloutBuffer", "compute_gae", "HipMlpActorCritic", "PPOConfig",
            "ppo_update"]

@@ -14,7 +14,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 
 from ._build import LIB
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 MODE_STEP, MODE_OBSERVE, MODE_RESET, MODE_PROBE, MODE_FLUSH = 0, 1, 2, 3, 4
 MAP_PILLARS, MAP_OPEN, MAP_REFERENCE = 0, 1, 2
@@ -92,6 +92,19 @@ class PpoArgsC(ctypes.Structure):
                            "dhy", "dl", "ln_part", "stats_part")]
 
 
+class CnnArgsC(ctypes.Structure):
+    _fields_ = [(n, _i32) for n in (
+        "batch", "npid", "pid0", "sample", "obs_stride", "mm_row_stride", "mm_pid_stride",
+        "bm_row_stride", "bm_pid_stride", "w_players")] + [
+        ("seed", _u64), ("tick", _u32), ("out_slots", _i32), ("out_slot", _i32),
+        ("reserved", _i32)] + [
+        (n, _vp) for n in ("obs", "c0w", "c0b", "ln0w", "ln0b", "c1w", "c1b", "ln1w", "ln1b",
+                           "c2w", "c2b", "ln2w", "ln2b", "c3w", "c3b", "ln3w", "ln3b", "s0wt",
+                           "s0b", "s1w", "s1b", "s3wt", "s3b", "s4w", "s4b", "hwt", "hb", "fw",
+                           "fb", "move_mask", "bomb_mask", "uniforms", "actions", "actions_i8",
+                           "logp_out", "value_out", "logits_out")]
+
+
 class GaeArgsC(ctypes.Structure):
     _fields_ = [("steps", _i32), ("n_envs", _i32), ("gamma", _f32), ("gamma_lam", _f32),
                 ("step_stride", ctypes.c_int64), ("env_stride", ctypes.c_int64)] + [
@@ -125,6 +138,8 @@ def lib():
         L.qqt_l1_grad_workspace_floats.argtypes = [_i32, _i32]
         L.qqt_ppo_grad.restype = ctypes.c_int
         L.qqt_ppo_grad.argtypes = [ctypes.POINTER(PpoArgsC), _vp]
+        L.qqt_cnn_act.restype = ctypes.c_int
+        L.qqt_cnn_act.argtypes = [ctypes.POINTER(CnnArgsC), _vp]
         L.qqt_timing_arm.restype = ctypes.c_int
         L.qqt_timing_arm.argtypes = [_i32]
         L.qqt_timing_collect.restype = ctypes.c_int
@@ -136,7 +151,7 @@ def lib():
 
 
 KERNEL_KINDS = ("tick_kernel", "mlp_act_kernel", "bot_kernel", "reach_kernel",
-                "gae_kernel", "l1grad_kernels", "ppo_grad_kernel")  # QQT_KERNEL_*
+                "gae_kernel", "l1grad_kernels", "ppo_grad_kernel", "cnn_act_kernel")  # QQT_KERNEL_*
 
 
 def timing_arm(launches: int) -> None:

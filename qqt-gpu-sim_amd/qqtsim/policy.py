@@ -134,6 +134,22 @@ class HipActorCritic:
         return sum(v.numel() for v in self.params.values())
 
     # ------------------------------------------------------------ launch
+    def _args(self, b, npid, pid0, sample, obs_ptr, obs_stride):
+        """Kernel argument block with the weights, sizes and Philox key set
+        (masks, uniforms and outputs left NULL)."""
+        a = _capi.MlpArgsC()
+        a.batch, a.npid, a.pid0, a.sample = b, npid, pid0, int(sample)
+        a.k0, a.kblocks0, a.obs_stride = self.k0, self.kblocks0, obs_stride
+        a.seed = self.seed & 0xFFFFFFFFFFFFFFFF
+        a.w0_players = self.n_players
+        a.obs = obs_ptr
+        for k, v in self._w.items():
+            setattr(a, k, v.data_ptr())
+        return a
+
+    def _launch(self, a, stream) -> None:
+        _capi.check(self._lib.qqt_mlp_act(a, stream))
+
     def _run(self, obs, npid, pid0, sample, mm=None, bm=None, mm_strides=(0, 0),
              bm_strides=(0, 0), uniforms=None, actions=None, actions_i8=None, logp=None,
              value=None, logits=None, tick=None):
@@ -143,17 +159,10 @@ class HipActorCritic:
             flat = flat.half()
         if flat.shape[1] != self.k0:
             raise ValueError(f"observation rows must have {self.k0} values")
-        a = _capi.MlpArgsC()
-        a.batch, a.npid, a.pid0, a.sample = b, npid, pid0, int(sample)
-        a.k0, a.kblocks0, a.obs_stride = self.k0, self.kblocks0, flat.stride(0)
+        a = self._args(b, npid, pid0, sample, flat.data_ptr(), flat.stride(0))
         a.mm_row_stride, a.mm_pid_stride = mm_strides
         a.bm_row_stride, a.bm_pid_stride = bm_strides
-        a.seed = self.seed & 0xFFFFFFFFFFFFFFFF
         a.tick = (self.tick if tick is None else tick) & 0xFFFFFFFF
-        a.w0_players = self.n_players
-        a.obs = flat.data_ptr()
-        for k, v in self._w.items():
-            setattr(a, k, v.data_ptr())
         a.move_mask = _capi.ptr(mm)
         a.bomb_mask = _capi.ptr(bm)
         a.uniforms = _capi.ptr(uniforms)
@@ -162,7 +171,7 @@ class HipActorCritic:
         a.logp_out = _capi.ptr(logp)
         a.value_out = _capi.ptr(value)
         a.logits_out = _capi.ptr(logits)
-        _capi.check(self._lib.qqt_mlp_act(a, _capi.stream_handle(self.device)))
+        self._launch(a, _capi.stream_handle(self.device))
         return flat
 
     @staticmethod
@@ -228,3 +237,113 @@ class HipActorCritic:
             lp = lp + d.log_prob(act)
             ent = ent + d.entropy()
         return lp, ent, v
+
+
+# ---------------------------------------------------------------- cnn arch
+CNN_CHANNELS = (16, 32, 64, 8)
+
+
+def pack_cnn(params: dict, n_players: int = 2, obs_shape=(14, 13, 13)) -> dict:
+    """Host-side packing of an ActorCritic cnn state_dict (train/model.py:79-96)
+    into the layout of qqt_cnn_act: conv weights K-major [ci*taps + tap][out]
+    with each player's view permutation folded into conv0's input channels
+    (conv0.weight[:, argsort(view_perm)], :186-190), Linear weights
+    transposed, LayerNorm affines flattened."""
+    c, h, w = obs_shape
+    if (c, h, w) != (14, 13, 13) or n_players != 2:
+        raise ValueError("the cnn kernel is built for 2 players on a 13 x 13 grid (14 channels)")
+    f = lambda k: params[k].float().cpu()  # noqa: E731
+
+    def kmajor(wt):                       # [out][in][kh][kw] -> [in*kh*kw][out]
+        return wt.permute(1, 2, 3, 0).reshape(-1, wt.shape[0]).contiguous()
+
+    w0 = f("conv0.weight")
+    if tuple(w0.shape) != (16, c, 3, 3):
+        raise ValueError(f"conv0.weight must be {(16, c, 3, 3)}, got {tuple(w0.shape)}")
+    c0w = torch.stack([kmajor(w0[:, torch.argsort(torch.tensor(view_perm(pid, n_players, c)))])
+                       for pid in range(n_players)])
+    heads = ("move_head", "bomb_head", "critic")
+    fw = torch.cat([f(f"{n}.2.weight") for n in heads])
+    if fw.shape != (8, HEAD):
+        raise ValueError("heads must produce 5 + 2 + 1 outputs from 64 hidden units")
+    out = dict(
+        c0w=c0w.reshape(-1).contiguous(), c0b=f("conv0.bias"),
+        ln0w=f("conv.0.weight").reshape(-1), ln0b=f("conv.0.bias").reshape(-1),
+        c1w=kmajor(f("conv.2.weight")), c1b=f("conv.2.bias"),
+        ln1w=f("conv.3.weight").reshape(-1), ln1b=f("conv.3.bias").reshape(-1),
+        c2w=kmajor(f("conv.5.weight")), c2b=f("conv.5.bias"),
+        ln2w=f("conv.6.weight").reshape(-1), ln2b=f("conv.6.bias").reshape(-1),
+        c3w=kmajor(f("conv.8.weight")), c3b=f("conv.8.bias"),
+        ln3w=f("conv.9.weight").reshape(-1), ln3b=f("conv.9.bias").reshape(-1),
+        s0wt=f("shared.0.weight").t().contiguous(), s0b=f("shared.0.bias"),
+        s1w=f("shared.1.weight"), s1b=f("shared.1.bias"),
+        s3wt=f("shared.3.weight").t().contiguous(), s3b=f("shared.3.bias"),
+        s4w=f("shared.4.weight"), s4b=f("shared.4.bias"),
+        hwt=torch.cat([f(f"{n}.0.weight") for n in heads]).t().contiguous(),
+        hb=torch.cat([f(f"{n}.0.bias") for n in heads]),
+        fw=fw.contiguous(), fb=torch.cat([f(f"{n}.2.bias") for n in heads]))
+    expect = dict(c1w=(144, 32), c2w=(288, 64), c3w=(64, 8), s0wt=(8 * h * w, HID),
+                  s3wt=(HID, HID), hwt=(HID, 3 * HEAD))
+    for k, shp in expect.items():
+        if tuple(out[k].shape) != shp:
+            raise ValueError(f"{k} packs to {tuple(out[k].shape)}, expected {shp}")
+    return {k: v.contiguous() for k, v in out.items()}
+
+
+def default_init_cnn(obs_shape=(14, 13, 13), n_moves: int = 5, n_bomb: int = 2,
+                     seed: int = 0) -> dict:
+    """PyTorch default init of the cnn ActorCritic layers (Conv2d / Linear
+    kaiming-uniform(a=sqrt(5)), LayerNorm 1/0) under torch.manual_seed(seed),
+    layers created in module order (train/model.py:79-96, 140-153).  The
+    global RNG state is restored afterwards."""
+    c, h, w = obs_shape
+    nn = torch.nn
+    with torch.random.fork_rng(devices=[]):
+        torch.manual_seed(seed)
+        conv0 = nn.Conv2d(c, 16, 3, padding=1)
+        conv = nn.Sequential(nn.LayerNorm([16, h, w]), nn.ReLU(), nn.Conv2d(16, 32, 3, padding=1),
+                             nn.LayerNorm([32, h, w]), nn.ReLU(), nn.Conv2d(32, 64, 3, padding=1),
+                             nn.LayerNorm([64, h, w]), nn.ReLU(), nn.Conv2d(64, 8, 1),
+                             nn.LayerNorm([8, h, w]), nn.ReLU())
+        shared = nn.Sequential(nn.Linear(8 * h * w, HID), nn.LayerNorm(HID), nn.ReLU(),
+                               nn.Linear(HID, HID), nn.LayerNorm(HID), nn.ReLU())
+        heads = {name: nn.Sequential(nn.Linear(HID, HEAD), nn.ReLU(), nn.Linear(HEAD, k))
+                 for name, k in (("move_head", n_moves), ("bomb_head", n_bomb), ("critic", 1))}
+    out = {f"conv0.{k}": v for k, v in conv0.state_dict().items()}
+    out.update({f"conv.{k}": v for k, v in conv.state_dict().items()})
+    out.update({f"shared.{k}": v for k, v in shared.state_dict().items()})
+    for name, mod in heads.items():
+        out.update({f"{name}.{k}": v for k, v in mod.state_dict().items()})
+    return {k: v.detach().clone() for k, v in out.items()}
+
+
+class HipCnnActorCritic(HipActorCritic):
+    """The reference's cnn `ActorCritic` (train/model.py:79-96, 186-190) on
+    qqt_cnn_act: the same forward / act / act_pair / evaluate as the mlp
+    class, with float32 weights (the trunk computes in float32 on MFMA)."""
+
+    def __init__(self, state_dict: dict | None = None, obs_shape=(14, 13, 13),
+                 n_players: int = 2, device="cuda", seed: int = 0):
+        if state_dict is None:
+            state_dict = default_init_cnn(obs_shape)
+        super().__init__(state_dict, obs_shape, n_players, device, seed)
+
+    def load_state_dict(self, state_dict: dict) -> None:
+        self.params = {k: v.detach().float().cpu().clone() for k, v in state_dict.items()}
+        packed = pack_cnn(self.params, self.n_players, self.obs_shape)
+        self.k0 = self.obs_shape[0] * self.obs_shape[1] * self.obs_shape[2]
+        self._w = {k: v.to(self.device).contiguous() for k, v in packed.items()}
+
+    def _args(self, b, npid, pid0, sample, obs_ptr, obs_stride):
+        a = _capi.CnnArgsC()
+        a.batch, a.npid, a.pid0, a.sample = b, npid, pid0, int(sample)
+        a.obs_stride = obs_stride
+        a.w_players = self.n_players
+        a.seed = self.seed & 0xFFFFFFFFFFFFFFFF
+        a.obs = obs_ptr
+        for k, v in self._w.items():
+            setattr(a, k, v.data_ptr())
+        return a
+
+    def _launch(self, a, stream) -> None:
+        _capi.check(self._lib.qqt_cnn_act(a, stream))

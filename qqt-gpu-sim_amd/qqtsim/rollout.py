@@ -6,7 +6,8 @@ The reference's collect loop (train/ppo.py:213-249) does, per tick,
 of the current state are already in the sim's persistent buffers (the tick
 kernel writes them after stepping and auto-resetting), so an env-step is
 
-    qqt_mlp_act  (both players, masked sampling, int8 actions)
+    qqt_mlp_act  (both players, masked sampling, int8 actions; qqt_cnn_act
+                  for the cnn policy)
     qqt_tick     (step + auto-reset + observe + legal masks)
 
 with both argument blocks built once: a tick only updates the Philox counter
@@ -18,6 +19,8 @@ hint, see `HipBatchedSim`).
 """
 
 from __future__ import annotations
+
+import math
 
 import torch
 
@@ -52,21 +55,15 @@ class Rollout:
         self._stream = _capi.stream_handle(d)
         self._lib = _capi.lib()
 
-        m = _capi.MlpArgsC()
-        m.batch, m.npid, m.pid0, m.sample = n, (2 if opponent is None else 1), 0, 1
+        m = policy._args(n, 2 if opponent is None else 1, 0, 1, sim._obs.data_ptr(),
+                         math.prod(policy.obs_shape))
         m.out_slots, m.out_slot = 2, 0
-        m.k0, m.kblocks0, m.obs_stride = policy.k0, policy.kblocks0, policy.k0
         m.mm_row_stride, m.mm_pid_stride = 5 * p, 5
         m.bm_row_stride, m.bm_pid_stride = 2 * p, 2
-        m.seed = policy.seed & 0xFFFFFFFFFFFFFFFF
-        m.w0_players = policy.n_players
-        m.obs = sim._obs.data_ptr()
-        for k, v in policy._w.items():
-            setattr(m, k, v.data_ptr())
         m.move_mask, m.bomb_mask = sim._mm.data_ptr(), sim._bm.data_ptr()
         m.actions_i8 = self.actions.data_ptr()
         m.logp_out, m.value_out = self.logp.data_ptr(), self.value.data_ptr()
-        self._mlp = m
+        self._act = m
 
         t = _capi.TickArgsC()
         t.n_envs, t.mode, t.auto_reset = n, _capi.MODE_STEP, 1
@@ -100,8 +97,8 @@ class Rollout:
         """The policy's actions (both players in self-play, player 0 against an
         opponent) for the current observation (train/model.py:230-245)."""
         self.sim._refresh()
-        self._mlp.tick = self.policy.tick & 0xFFFFFFFF
-        _capi.check(self._lib.qqt_mlp_act(self._mlp, self._stream))
+        self._act.tick = self.policy.tick & 0xFFFFFFFF
+        self.policy._launch(self._act, self._stream)
         self.policy.tick += 1
 
     def launch_opponent(self) -> None:
@@ -159,14 +156,14 @@ class Rollout:
         try:
             for t in range(T):
                 cur = buf[t].data_ptr()
-                self._mlp.obs = cur
+                self._act.obs = cur
                 if bot is not None:
                     bot._args.obs = cur
                 self.launch_act()
                 self._tick.obs = buf[t + 1].data_ptr() if t + 1 < T else sim._obs.data_ptr()
                 self.launch_tick()
         finally:
-            self._mlp.obs = sim._obs.data_ptr()
+            self._act.obs = sim._obs.data_ptr()
             self._tick.obs = sim._obs.data_ptr()
             if bot is not None:
                 bot._args.obs = sim._obs.data_ptr()
@@ -190,7 +187,7 @@ class Rollout:
             raise ValueError("buffer shape or device differs from the sim's")
         if (n * buf.obs[0, 0].numel() * 2) % 16:
             raise ValueError("the number of envs must be a multiple of 4 (16-byte aligned slabs)")
-        m, tk, bot = self._mlp, self._tick, self.opponent
+        m, tk, bot = self._act, self._tick, self.opponent
         saved_m = (m.obs, m.move_mask, m.bomb_mask, m.actions_i8, m.logp_out, m.value_out)
         saved_t = (tk.actions_i8, tk.reward, tk.done, tk.damaged, tk.obs, tk.move_mask,
                    tk.bomb_mask)

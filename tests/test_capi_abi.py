@@ -39,7 +39,7 @@ def _declared_functions():
 
 
 def test_header_declares_the_entry_points():
-    assert _declared_functions() == ["qqt_abi_version", "qqt_bot_act", "qqt_gae",
+    assert _declared_functions() == ["qqt_abi_version", "qqt_bot_act", "qqt_cnn_act", "qqt_gae",
                                      "qqt_l1_grad", "qqt_l1_grad_workspace_floats",
                                      "qqt_last_error", "qqt_mlp_act", "qqt_ppo_grad", "qqt_tick",
                                      "qqt_timing_arm", "qqt_timing_collect"]
@@ -92,7 +92,7 @@ def test_struct_layouts_match_the_header(tmp_path):
     structs = {"qqt_sim_config": _capi.SimConfigC, "qqt_tick_args": _capi.TickArgsC,
                "qqt_mlp_args": _capi.MlpArgsC, "qqt_bot_args": _capi.BotArgsC,
                "qqt_gae_args": _capi.GaeArgsC, "qqt_l1_grad_args": _capi.L1GradArgsC,
-               "qqt_ppo_args": _capi.PpoArgsC}
+               "qqt_ppo_args": _capi.PpoArgsC, "qqt_cnn_args": _capi.CnnArgsC}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "qqt_hip.h"',
              'int main(void) {']
     for cname, cls in structs.items():
@@ -205,6 +205,40 @@ def test_mlp_rejects_bad_output_slots(lib, kw, msg):
     assert msg in lib.qqt_last_error().decode()
 
 
+_CNN_PTRS = ("obs", "c0w", "c0b", "ln0w", "ln0b", "c1w", "c1b", "ln1w", "ln1b", "c2w", "c2b",
+             "ln2w", "ln2b", "c3w", "c3b", "ln3w", "ln3b", "s0wt", "s0b", "s1w", "s1b", "s3wt",
+             "s3b", "s4w", "s4b", "hwt", "hb", "fw", "fb")
+
+
+def _cnn_args(**kw):
+    from qqtsim import _capi
+
+    a = _capi.CnnArgsC()
+    a.batch, a.npid, a.obs_stride, a.w_players = 4, 2, 14 * 169, 2
+    for i, name in enumerate(_CNN_PTRS):
+        setattr(a, name, 0x10000 * (i + 1))
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(s3wt=None), "null pointer"),
+    (dict(obs=None), "null pointer"),
+    (dict(batch=0), "bad batch"),
+    (dict(npid=3), "bad batch"),
+    (dict(obs_stride=2365), "bad batch"),
+    (dict(npid=1, pid0=2), "bad batch"),
+    (dict(w_players=1), "bad batch"),
+    (dict(out_slots=1), "output slots"),
+    (dict(npid=1, out_slots=2, out_slot=2), "output slots"),
+    (dict(sample=1), "sampling needs masks"),
+])
+def test_cnn_rejects_bad_arguments(lib, kw, msg):
+    assert lib.qqt_cnn_act(_cnn_args(**kw), None) == -1
+    assert msg in lib.qqt_last_error().decode()
+
+
 def _bot_args(**kw):
     from qqtsim import _capi
 
@@ -255,7 +289,7 @@ def test_header_kernel_kinds_match_host_mirror():
     text = open(HEADER).read()
     kinds = dict((k, int(v)) for k, v in re.findall(r"\bQQT_KERNEL_(\w+) = (\d+)", text))
     assert kinds["KINDS"] == len(_capi.KERNEL_KINDS)
-    for name in ("TICK", "MLP", "BOT", "REACH", "GAE", "L1GRAD", "PPO"):
+    for name in ("TICK", "MLP", "BOT", "REACH", "GAE", "L1GRAD", "PPO", "CNN"):
         assert _capi.KERNEL_KINDS[kinds[name]].startswith(name.lower()), name
 
 

@@ -1,0 +1,183 @@
+"""cnn actor/critic kernel (qqt_cnn_act) vs the reference forward and the host sampler.
+
+Bars: logits and value within 1e-3 absolute of the float32 forward (the
+kernel computes the trunk in float32 on MFMA, in another summation order,
+from float16 observations); sampled actions bit-exact against the host
+sampler given the kernel's own logits and the same uniforms, with logp within
+1e-6; Philox-drawn actions bit-exact against the host sampler on the
+oracle's Philox uniforms.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from golden_io import GOLDEN, cnn_params, traj
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_ATOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+def _logits(net, obs, pid):
+    ml, bl, v = net.forward(obs, pid)
+    return torch.cat([ml, bl, v[:, None]], 1).cpu()
+
+
+def test_cnn_forward_matches_reference_golden(dev):
+    """Weights and outputs recorded from the reference's ActorCritic(arch="cnn"),
+    and evaluate()'s log-probabilities and entropies of the recorded actions."""
+    from qqtsim.policy import HipCnnActorCritic
+
+    z = np.load(GOLDEN + "/cnn.npz")
+    net = HipCnnActorCritic(cnn_params(z), device=dev)
+    assert net.n_params() == int(z["param_count"]) == 281744
+    obs = torch.from_numpy(z["obs"]).to(dev)
+    mm = torch.from_numpy(z["mm"]).to(dev)
+    bm = torch.from_numpy(z["bm"]).to(dev)
+    acts = torch.from_numpy(z["actions"]).to(dev)
+    for pid in range(2):
+        ml, bl, v = net.forward(obs, pid)
+        for got, key in ((ml, "move_logits"), (bl, "bomb_logits"), (v, "value")):
+            err = float(np.abs(got.cpu().numpy() - z[f"{key}_{pid}"]).max())
+            print(f"pid {pid} {key}: max |err| {err:.2e}")
+            assert err <= LOGIT_ATOL
+        lp, ent, _ = net.evaluate(obs, mm[:, pid], bm[:, pid], acts[:, pid], pid)
+        np.testing.assert_allclose(lp.cpu().numpy(), z[f"logp_{pid}"], atol=2e-3, rtol=0)
+        np.testing.assert_allclose(ent.cpu().numpy(), z[f"entropy_{pid}"], atol=2e-3, rtol=0)
+
+
+@pytest.mark.parametrize("name", ["pillars70", "stress40"])
+def test_cnn_forward_matches_oracle_default_init(dev, name):
+    """PyTorch default init on observations from reference trajectories, both
+    players from one pass, against the oracle in float64."""
+    from oracle.policy import cnn_forward
+    from qqtsim.policy import HipCnnActorCritic, default_init_cnn
+
+    params = default_init_cnn(seed=1)
+    net = HipCnnActorCritic(params, device=dev)
+    z = traj(name)
+    obs = torch.from_numpy(z["obs"].reshape(-1, 14, 13, 13)[:600].copy())
+    b = obs.shape[0]
+    mm = torch.ones((b, 2, 5), dtype=torch.bool)
+    bm = torch.ones((b, 2, 2), dtype=torch.bool)
+    _, _, val, lg = net.act_pair(obs.to(dev), mm.to(dev), bm.to(dev), logits=True)
+    lg = lg.cpu().numpy()
+    worst = 0.0
+    for pid in range(2):
+        ml, bl, v = cnn_forward(params, obs, pid, dtype=torch.float64)
+        ref = np.concatenate([ml.numpy(), bl.numpy(), v.numpy()[:, None]], 1)
+        worst = max(worst, float(np.abs(lg[:, pid] - ref).max()))
+        np.testing.assert_array_equal(val.cpu().numpy()[:, pid], lg[:, pid, 7])
+        np.testing.assert_array_equal(lg[:, pid], _logits(net, obs.to(dev), pid).numpy())
+    print(f"{name}: {b} rows x 2 players, max |logit err| {worst:.2e}")
+    assert worst <= LOGIT_ATOL
+
+
+def test_cnn_sampling_bit_exact_given_logits(dev):
+    """Same logits, masks and uniforms -> same actions as the host sampler,
+    including all-masked rows and the uniforms' end points."""
+    from oracle.policy import sample_masked
+    from qqtsim.policy import HipCnnActorCritic
+
+    net = HipCnnActorCritic(device=dev, seed=3)
+    z = traj("deathmatch")
+    obs = torch.from_numpy(z["obs"].reshape(-1, 14, 13, 13)[:800].copy())
+    b = obs.shape[0]
+    g = torch.Generator().manual_seed(0)
+    mm = torch.rand((b, 2, 5), generator=g) < 0.6
+    bm = torch.rand((b, 2, 2), generator=g) < 0.6
+    mm[..., 4] |= torch.rand((b, 2), generator=g) < 0.5
+    u = torch.rand((b, 2, 2), generator=g)
+    u[:7] = torch.tensor([0.0, 1.0 - 2 ** -24]).repeat(7, 2, 1)
+    acts, logp, val, lg = net.act_pair(obs.to(dev), mm.to(dev), bm.to(dev), uniforms=u.to(dev),
+                                       logits=True)
+    acts, logp, lg = acts.cpu().numpy(), logp.cpu().numpy(), lg.cpu().numpy()
+    for pid in range(2):
+        am, lpm = sample_masked(lg[:, pid, :5], mm[:, pid].numpy(), u[:, pid, 0].numpy())
+        ab, lpb = sample_masked(lg[:, pid, 5:7], bm[:, pid].numpy(), u[:, pid, 1].numpy())
+        np.testing.assert_array_equal(acts[:, pid, 0], am)
+        np.testing.assert_array_equal(acts[:, pid, 1], ab)
+        np.testing.assert_allclose(logp[:, pid], lpm + lpb, atol=1e-6, rtol=0)
+
+
+def test_cnn_philox_draws_match_oracle_uniforms(dev):
+    """Without injected uniforms the kernel draws Philox(seed, row, tick,
+    policy stream): the actions equal the host sampler's on the oracle's
+    Philox uniforms, tick after tick."""
+    from oracle import philox
+    from oracle.policy import sample_masked
+    from qqtsim.policy import HipCnnActorCritic
+
+    seed = 11
+    net = HipCnnActorCritic(device=dev, seed=seed)
+    z = traj("pillars70")
+    obs = torch.from_numpy(z["obs"].reshape(-1, 14, 13, 13)[:512].copy()).to(dev)
+    b = obs.shape[0]
+    g = torch.Generator().manual_seed(2)
+    mm = (torch.rand((b, 2, 5), generator=g) < 0.7).to(dev)
+    bm = (torch.rand((b, 2, 2), generator=g) < 0.7).to(dev)
+    rows = np.arange(b)
+    for _ in range(3):
+        u = philox.uniforms(seed, rows, net.tick, philox.STREAM_POLICY, 4)
+        acts, _, _, lg = net.act_pair(obs, mm, bm, logits=True)
+        lg = lg.cpu().numpy()
+        for pid in range(2):
+            am, _ = sample_masked(lg[:, pid, :5], mm[:, pid].cpu().numpy(), u[:, 2 * pid])
+            ab, _ = sample_masked(lg[:, pid, 5:7], bm[:, pid].cpu().numpy(), u[:, 2 * pid + 1])
+            np.testing.assert_array_equal(acts[:, pid, 0].cpu().numpy(), am)
+            np.testing.assert_array_equal(acts[:, pid, 1].cpu().numpy(), ab)
+
+
+def test_cnn_single_player_act_matches_pair(dev):
+    """act(pid) on one player equals that player's slot of act_pair."""
+    from qqtsim.policy import HipCnnActorCritic
+
+    net = HipCnnActorCritic(device=dev, seed=5)
+    z = traj("pillars70")
+    obs = torch.from_numpy(z["obs"].reshape(-1, 14, 13, 13)[:300].copy()).to(dev)
+    b = obs.shape[0]
+    mm = torch.from_numpy(np.ascontiguousarray(z["mm"][:75, :4].reshape(-1, 2, 5)[:b])).to(dev)
+    bm = torch.from_numpy(np.ascontiguousarray(z["bm"][:75, :4].reshape(-1, 2, 2)[:b])).to(dev)
+    u = torch.rand((b, 2, 2), generator=torch.Generator().manual_seed(1)).to(dev)
+    pa, pl, pv = net.act_pair(obs, mm, bm, uniforms=u)
+    for pid in range(2):
+        a, lp, v = net.act(obs, mm[:, pid], bm[:, pid], pid, uniforms=u[:, pid])
+        torch.testing.assert_close(a, pa[:, pid], rtol=0, atol=0)
+        torch.testing.assert_close(lp, pl[:, pid], rtol=0, atol=0)
+        torch.testing.assert_close(v, pv[:, pid], rtol=0, atol=0)
+
+
+def test_cnn_rollout_self_play(dev):
+    """The collect loop with the cnn policy: Rollout's per-tick actions equal
+    act_pair on the same observation, masks and Philox tick, and the sim
+    state equals a second sim stepped with those actions."""
+    from qqtsim import HipBatchedSim, MapSpec, Rollout, corridor_training_config
+    from qqtsim.policy import HipCnnActorCritic, default_init_cnn
+
+    n, T, seed = 128, 6, 9
+    cfg = corridor_training_config()
+    spec = MapSpec(kind="pillars", brick_p=0.7, swap_spawns=True)
+    params = default_init_cnn(cfg.obs_shape, seed=2)
+    a_sim = HipBatchedSim(cfg, n, device=dev, seed=seed, map_spec=spec)
+    a = Rollout(a_sim, HipCnnActorCritic(params, device=dev, seed=seed))
+    b_sim = HipBatchedSim(cfg, n, device=dev, seed=seed, map_spec=spec)
+    b_net = HipCnnActorCritic(params, device=dev, seed=seed)
+    for t in range(T):
+        obs = b_sim.observe()
+        mm, bm = b_sim.legal_mask()
+        want, lp, v = b_net.act_pair(obs, mm, bm)
+        a.step()
+        assert torch.equal(a.actions.long(), want), t
+        assert torch.equal(a.logp, lp) and torch.equal(a.value, v), t
+        b_sim.step(want)
+        assert torch.equal(a_sim.observe(), b_sim.observe()), t

@@ -150,3 +150,47 @@ def test_config_struct_float32_constants():
 def test_map_spec_validation(kw):
     with pytest.raises(ValueError):
         MapSpec(**kw)
+
+
+def test_pack_cnn_kmajor_convs_equal_conv2d():
+    """The cnn kernel's implicit GEMM on the packed weights (A[p][k] = the
+    zero-padded input plane ci at position p shifted by tap k % 9, k = ci * 9
+    + 3 dy + dx; B = the packed [k][out] matrix) equals F.conv2d with the
+    reference's weights, conv0 through each player's view permutation; the
+    1x1 conv reads the centre tap."""
+    import torch.nn.functional as F
+
+    from qqtsim.config import view_perm
+    from qqtsim.policy import default_init_cnn, pack_cnn
+
+    params = default_init_cnn(seed=3)
+    pk = pack_cnn(params)
+    g = torch.Generator().manual_seed(0)
+
+    def implicit_gemm(x, wk, bias, ks):
+        cin = x.shape[0]
+        xp = F.pad(x, (1, 1, 1, 1))
+        cols = []
+        for ci in range(cin):
+            for t in range(ks * ks):
+                dy, dx = (t // 3, t % 3) if ks == 3 else (1, 1)
+                cols.append(xp[ci, dy:dy + 13, dx:dx + 13].reshape(-1))
+        a = torch.stack(cols, 1)                       # [169][K]
+        return (a.double() @ wk.double() + bias.double()).t().reshape(-1, 13, 13)
+
+    x = torch.rand((14, 13, 13), generator=g, dtype=torch.float64)
+    for pid in range(2):
+        inv = torch.argsort(torch.tensor(view_perm(pid, 2, 14)))
+        want = F.conv2d(x[None], params["conv0.weight"].double()[:, inv],
+                        params["conv0.bias"].double(), padding=1)[0]
+        got = implicit_gemm(x, pk["c0w"].view(2, 126, 16)[pid], pk["c0b"], 3)
+        torch.testing.assert_close(got, want, rtol=1e-12, atol=1e-12)
+    for key, wk, bk, cin, ks in (("conv.2", "c1w", "c1b", 16, 3), ("conv.5", "c2w", "c2b", 32, 3),
+                                 ("conv.8", "c3w", "c3b", 64, 1)):
+        x = torch.rand((cin, 13, 13), generator=g, dtype=torch.float64)
+        want = F.conv2d(x[None], params[f"{key}.weight"].double(), params[f"{key}.bias"].double(),
+                        padding=ks // 2)[0]
+        torch.testing.assert_close(implicit_gemm(x, pk[wk], pk[bk], ks), want, rtol=1e-12, atol=1e-12)
+    assert pk["s0wt"].shape == (1352, 128) and torch.equal(pk["s0wt"].t(), params["shared.0.weight"])
+    assert torch.equal(pk["fw"][5:7], params["bomb_head.2.weight"])
+    assert sum(v.numel() for v in params.values()) == 281744
