@@ -77,7 +77,7 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="CPU work budget of the cpu_baseline sample (0 = skip)")
     ap.add_argument("--workload", choices=("rollout", "stress", "astar", "evalfwd", "collect",
-                                           "ppo", "train"),
+                                           "ppo", "train", "cnn"),
                     default="rollout",
                     help="rollout: the headline self-play rollout (default); stress: "
                          "16384-env bomb-stress ticks with injected actions; astar: "
@@ -88,7 +88,8 @@ def parse_args():
                          "(5632 envs) + last-value forward + GAE; ppo: one PPO update "
                          "(4 epochs x 4 minibatches) over a 5632 x 128 collected buffer; "
                          "train: whole training iterations (collect 128 steps + PPO update "
-                         "+ weight sync to the acting network)")
+                         "+ weight sync to the acting network); cnn: the self-play rollout "
+                         "with the reference's cnn actor/critic, 5632 envs")
     ap.add_argument("--copy-calibrate", action="store_true",
                     help="after timing, run a 512 MiB device copy (HBM counter calibration)")
     return ap.parse_args()
@@ -168,19 +169,23 @@ def _cores(torch):
     return torch.get_num_threads()
 
 
-def cpu_baseline(cfg, spec, n, seed, budget_s):
+def cpu_baseline(cfg, spec, n, seed, budget_s, arch="mlp"):
     """The oracle's env-step on the host cores: observe, legal_mask, both
-    players' forward + masked sampling, step with auto-reset."""
+    players' forward (mlp or cnn network) + masked sampling, step with
+    auto-reset."""
     import numpy as np
     import torch
 
     from oracle import philox
-    from oracle.policy import mlp_forward, sample_masked
+    from oracle.policy import cnn_forward, mlp_forward, sample_masked
     from oracle.sim import OracleSim
-    from qqtsim.policy import default_init
+    from qqtsim.policy import default_init, default_init_cnn
 
     cores = _cores(torch)
-    params = default_init(cfg.obs_shape)
+    if arch == "cnn":
+        params, forward = default_init_cnn(cfg.obs_shape), cnn_forward
+    else:
+        params, forward = default_init(cfg.obs_shape), mlp_forward
     sim = OracleSim(cfg, n, spec, seed=seed)
     envs = np.arange(n)
 
@@ -190,7 +195,7 @@ def cpu_baseline(cfg, spec, n, seed, budget_s):
         u = philox.uniforms(seed, envs, t, philox.STREAM_POLICY, 4)
         acts = torch.zeros((n, 2, 2), dtype=torch.int64)
         for pid in range(2):
-            ml, bl, _ = mlp_forward(params, obs, pid)
+            ml, bl, _ = forward(params, obs, pid)
             acts[:, pid, 0] = torch.from_numpy(
                 sample_masked(ml.numpy(), mm[:, pid].numpy(), u[:, 2 * pid])[0])
             acts[:, pid, 1] = torch.from_numpy(
@@ -219,8 +224,8 @@ def cpu_baseline(cfg, spec, n, seed, budget_s):
     return {"value": n * ticks / el, "unit": "env-steps/s", "cores": cores,
             "kind": "port", "cpu_model": _cpu_model(),
             "value_1thread": n * ticks1 / el1,
-            "sample": f"oracle (torch CPU restatement) on the same workload, {n} envs x "
-                      f"{ticks} timed ticks after 2 warm-up ticks, {el:.1f} s; one thread: "
+            "sample": f"oracle (torch CPU restatement, {arch} network) on the same workload, "
+                      f"{n} envs x {ticks} timed ticks after 2 warm-up ticks, {el:.1f} s; one thread: "
                       f"{ticks1} ticks, {el1:.1f} s"}
 
 
@@ -259,6 +264,8 @@ def main():
         return main_ppo(args, torch, dev)
     if args.workload == "train":
         return main_train(args, torch, dev)
+    if args.workload == "cnn":
+        return main_cnn(args, torch, dev)
     n, K, W = args.envs, args.steps, args.warmup
     cfg, spec, roll = build_workload(n, args.seed, dev)
     for _ in range(W):
@@ -1003,6 +1010,153 @@ def main_train(args, torch, dev):
         "cpu_baseline": None,
     }
     print(json.dumps(res), flush=True)
+
+
+
+# Algorithmic FLOP of the cnn actor/critic for one player view: 2 x MACs of
+# conv0 14->16 3x3, conv 16->32 3x3, conv 32->64 3x3, conv 64->8 1x1 on
+# 169 positions, Linear 1352->128, 128->128, three 128->64 heads and their
+# 64->(5+2+1) outputs.
+CNN_MACS = (169 * (14 * 9 * 16 + 16 * 9 * 32 + 32 * 9 * 64 + 64 * 8)
+            + 1352 * 128 + 128 * 128 + 3 * 128 * 64 + 64 * 8)
+CNN_FLOP_PER_ENV = 2 * 2 * CNN_MACS            # both players
+MFMA_F32_PEAK_TFLOPS = 157.3
+
+
+def _torch_cnn(torch, sd, dev):
+    """The reference's cnn ActorCritic as plain float32 eager torch modules
+    (train/model.py:79-96, 140-153, 186-196, 230-245): forward through the
+    view-permuted conv0 and act() with masked Categorical sampling."""
+    nn = torch.nn
+    F = torch.nn.functional
+    from qqtsim.config import view_perm
+
+    class Cnn(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.conv0 = nn.Conv2d(14, 16, 3, padding=1)
+            self.conv = nn.Sequential(
+                nn.LayerNorm([16, 13, 13]), nn.ReLU(), nn.Conv2d(16, 32, 3, padding=1),
+                nn.LayerNorm([32, 13, 13]), nn.ReLU(), nn.Conv2d(32, 64, 3, padding=1),
+                nn.LayerNorm([64, 13, 13]), nn.ReLU(), nn.Conv2d(64, 8, 1),
+                nn.LayerNorm([8, 13, 13]), nn.ReLU())
+            self.shared = nn.Sequential(nn.Linear(1352, 128), nn.LayerNorm(128), nn.ReLU(),
+                                        nn.Linear(128, 128), nn.LayerNorm(128), nn.ReLU())
+            self.move_head = nn.Sequential(nn.Linear(128, 64), nn.ReLU(), nn.Linear(64, 5))
+            self.bomb_head = nn.Sequential(nn.Linear(128, 64), nn.ReLU(), nn.Linear(64, 2))
+            self.critic = nn.Sequential(nn.Linear(128, 64), nn.ReLU(), nn.Linear(64, 1))
+            self.inv = [torch.argsort(torch.tensor(view_perm(p, 2, 14))).to(dev) for p in range(2)]
+
+        def forward(self, obs, pid=0):
+            x = F.conv2d(obs.float(), self.conv0.weight[:, self.inv[pid]], self.conv0.bias,
+                         padding=1)
+            x = self.shared(self.conv(x).flatten(1))
+            return self.move_head(x), self.bomb_head(x), self.critic(x).squeeze(-1)
+
+        @torch.no_grad()
+        def act(self, obs, mm, bm, pid=0):
+            ml, bl, v = self(obs, pid)
+            neg = torch.finfo(ml.dtype).min
+            dm = torch.distributions.Categorical(logits=torch.where(mm, ml, torch.full_like(ml, neg)))
+            db = torch.distributions.Categorical(logits=torch.where(bm, bl, torch.full_like(bl, neg)))
+            a = torch.stack([dm.sample(), db.sample()], -1)
+            return a, dm.log_prob(a[:, 0]) + db.log_prob(a[:, 1]), v
+
+    m = Cnn()
+    m.load_state_dict(sd)
+    return m.to(dev)
+
+
+def main_cnn(args, torch, dev):
+    """The self-play rollout of the headline workload with the reference's cnn
+    actor/critic as the policy (both players, one cnn_act_kernel launch, then
+    the tick).  `torch_gpu_baseline` times the reference's act() for both
+    players with the same network as float32 eager torch modules (MIOpen
+    convolutions) on the same GPU and observations."""
+    from qqtsim.config import corridor_training_config
+    from qqtsim.maps import MapSpec
+    from qqtsim.policy import HipCnnActorCritic, default_init_cnn
+    from qqtsim.rollout import Rollout
+    from qqtsim.sim import HipBatchedSim
+
+    n, K, W = args.envs, args.steps, args.warmup
+    cfg = corridor_training_config()
+    spec = MapSpec(kind="pillars", brick_p=0.7, swap_spawns=True)
+    sim = HipBatchedSim(cfg, n, device=dev, seed=args.seed, map_spec=spec)
+    sd = default_init_cnn(cfg.obs_shape)
+    roll = Rollout(sim, HipCnnActorCritic(sd, device=dev, seed=args.seed))
+    for _ in range(W):
+        roll.step()
+    torch.cuda.synchronize()
+    _capi.timing_arm(0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(K):
+        if k % EVERY == 0:
+            _capi.timing_arm(2)
+        roll.launch_act()
+        roll.launch_tick()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    kms = kernel_ms()
+    act_ms, tick_ms = kms["cnn_act_kernel"], kms["tick_kernel"]
+    kernels = {
+        "cnn_act_kernel": {"us": act_ms * 1e3, "bound": "mfma",
+                           "achieved": CNN_FLOP_PER_ENV * n / (act_ms * 1e-3) / 1e12,
+                           "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                           "flop_per_env": CNN_FLOP_PER_ENV},
+        "tick_kernel": {"us": tick_ms * 1e3, "bound": "hbm",
+                        "achieved": TICK_BYTES_PER_ENV * n / (tick_ms * 1e-3) / 1e9,
+                        "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "bytes_per_env": TICK_BYTES_PER_ENV},
+    }
+    for v in kernels.values():
+        v["frac"] = v["achieved"] / v["peak"]
+    d = kernels["cnn_act_kernel"]
+
+    # the reference's act() for both players, eager float32 torch on this GPU
+    ref = _torch_cnn(torch, sd, dev)
+    obs = sim.observe().clone()
+    mm, bm = (m.bool().clone() for m in sim.legal_mask())
+    for _ in range(3):
+        for pid in range(2):
+            ref.act(obs, mm[:, pid], bm[:, pid], pid)
+    torch.cuda.synchronize()
+    reps = 10
+    t1 = time.perf_counter()
+    for _ in range(reps):
+        for pid in range(2):
+            ref.act(obs, mm[:, pid], bm[:, pid], pid)
+    torch.cuda.synchronize()
+    ref_ms = (time.perf_counter() - t1) / reps * 1e3
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        cpu = cpu_baseline(cfg, spec, 512, args.seed, args.cpu_seconds, arch="cnn")
+    value = n * K / el
+    out = {
+        "metric": "env-steps/s at 5632 envs (step+obs+cnn act), 1 MI355X; % MFMA roofline",
+        "value": value, "unit": "env-steps/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": el / K * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32 sim / f32 MFMA cnn trunk",
+        "data": "synthetic: template maps from Philox draws, PyTorch default-init cnn weights",
+        "config": {"workload": "self-play rollout, 5632 envs, 13x13 pillars + 70% bricks, "
+                               "P=2, 14-ch f16 obs, cnn act both players + masked sampling, "
+                               "auto-reset", "envs": n, "parallelism": "single GPU"},
+        "roofline": {"kernel": "cnn_act_kernel", "bound": d["bound"],
+                     "achieved": round(d["achieved"], 3), "peak": d["peak"], "unit": d["unit"],
+                     "frac": round(d["frac"], 5), "traffic": None},
+        "torch_gpu_baseline": {"act_ms_both_players": round(ref_ms, 3),
+                               "hip_act_ms_both_players": round(act_ms, 4),
+                               "speedup": round(ref_ms / act_ms, 2),
+                               "note": "the reference's act() (forward + masked Categorical "
+                                       "sampling) for both players, float32 eager torch with "
+                                       "MIOpen convolutions, same observations"},
+        "cpu_baseline": cpu,
+        "kernels": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
+                        for kk, vv in v.items()} for k, v in kernels.items()},
+    }
+    print(json.dumps(out), flush=True)
 
 
 if __name__ == "__main__":

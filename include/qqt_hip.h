@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 9
+#define QQT_ABI_VERSION 10
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -316,12 +316,18 @@ typedef struct qqt_ppo_args {
 int qqt_ppo_grad(const qqt_ppo_args* args, void* stream);
 
 /* Forward of the cnn actor/critic (train/model.py:79-96, 186-190) with
- * optional masked factored sampling, one workgroup per (row, player).
- * Replaces ActorCritic.act / forward for arch "cnn" (:167-196, 230-245) as
- * qqt_mlp_act does for the MLP: the same masks, uniforms and output layout.
- * Every LayerNorm normalises one sample over all of its values (eps 1e-5)
- * with an elementwise affine of that shape; weights are float32, K-major
- * (index [k][out]); a 3x3 conv's k is ci * 9 + 3 dy + dx. */
+ * optional masked factored sampling.  Replaces ActorCritic.act / forward for
+ * arch "cnn" (:167-196, 230-245) as qqt_mlp_act does for the MLP: the same
+ * masks, uniforms and output layout.  Every LayerNorm normalises one sample
+ * over all of its values (eps 1e-5) with an elementwise affine of that shape.
+ * Weights are float32 in the kernel's operand order ("packed" below: index
+ * [tile][step][lane], lane l holding output 16 tile + l % 16 and input
+ * 4 step + l / 16 of the K order); a 3x3 conv's K order is, for channel
+ * blocks cb of 4 (inputs padded to a multiple of 4 with zero weights) and
+ * taps t = 3 dy + dx, step 9 cb + t = channels 4 cb .. 4 cb + 3 at tap t.
+ * LayerNorm tables are packed [tile][11 position tiles][lane][4] (value q of
+ * lane l: channel 16 tile + l % 16, position 16 ptile + 4 (l / 16) + q;
+ * zero past 169 positions or the channel count), 16-byte aligned. */
 typedef struct qqt_cnn_args {
   int32_t batch;              /* rows B */
   int32_t npid;               /* 1: player pid0 only; 2: both players */
@@ -330,24 +336,28 @@ typedef struct qqt_cnn_args {
   int32_t obs_stride;         /* elements between observation rows (>= 14*169) */
   int32_t mm_row_stride, mm_pid_stride;  /* move mask [row*rs + pid*ps + k] */
   int32_t bm_row_stride, bm_pid_stride;  /* bomb mask */
-  int32_t w_players;          /* player views c0w holds (pid0, npid < it) */
+  int32_t w_players;          /* player views view_perm holds (pid0, npid < it) */
   uint64_t seed;              /* Philox key of the policy uniforms */
   uint32_t tick;              /* counter word of the policy uniforms */
   int32_t out_slots;          /* player slots per output row (0 = npid) */
   int32_t out_slot;           /* slot written when npid == 1 */
   int32_t reserved;
   const uint16_t* obs;        /* [B][obs_stride] float16 bits, [14][13][13] per row */
-  const float* c0w;           /* [w_players][126][16]: conv0 with player p's view
-                                 permutation folded into its input channels */
-  const float *c0b, *ln0w, *ln0b;   /* [16], [16*169] x 2 */
-  const float *c1w, *c1b, *ln1w, *ln1b;   /* [144][32], [32], [32*169] x 2 */
-  const float *c2w, *c2b, *ln2w, *ln2b;   /* [288][64], [64], [64*169] x 2 */
-  const float *c3w, *c3b, *ln3w, *ln3b;   /* 1x1: [64][8], [8], [8*169] x 2 */
-  const float *s0wt, *s0b;    /* [1352][128], [128] */
+  const int32_t* view_perm;   /* [w_players][14]: conv0 input channel j of player p is
+                                 observation channel view_perm[p][j] (the reference's
+                                 conv0.weight[:, argsort(view_perm)] on the stored obs) */
+  const float *c0w, *c0b, *ln0w, *ln0b;   /* conv0 packed [1][36][64]; [16]; LN [1][11][64][4] */
+  const float *c1w, *c1b, *ln1w, *ln1b;   /* packed [2][36][64]; [32]; LN [2][11][64][4] */
+  const float *c2w, *c2b, *ln2w, *ln2b;   /* packed [4][72][64]; [64]; LN [4][11][64][4] */
+  const float *c3w, *c3b, *ln3w, *ln3b;   /* 1x1: packed [1][16][64] (outputs 8..15 zero);
+                                             [16] (8..15 zero); LN [1][11][64][4] */
+  const float *s0p, *s0b;     /* Linear(1352,128) packed [8][338][64] (input index
+                                 c * 169 + p of the flattened [8][13][13]); [128] */
   const float *s1w, *s1b;     /* LayerNorm(128) */
-  const float *s3wt, *s3b;    /* [128][128], [128] */
+  const float *s3p, *s3b;     /* Linear(128,128) packed [8][32][64]; [128] */
   const float *s4w, *s4b;     /* LayerNorm(128) */
-  const float *hwt, *hb;      /* [128][192] (move | bomb | critic hidden), [192] */
+  const float *hp, *hb;       /* heads' hidden layers (move | bomb | critic, 192 outputs)
+                                 packed [12][32][64]; [192] */
   const float *fw, *fb;       /* [8][64]: move rows 0-4, bomb 5-6, critic 7; [8] */
   const uint8_t* move_mask;
   const uint8_t* bomb_mask;

@@ -1,27 +1,42 @@
 // cnn actor/critic forward + masked factored sampling for gfx950 (the
 // reference's ActorCritic(arch="cnn"), train/model.py:79-96, 186-190).
 //
-// Network per player view: conv0 3x3 (C=14 -> 16, the view permutation
-// folded into its input channels) -> LayerNorm([16,13,13]) -> ReLU -> conv
-// 3x3 16 -> 32 -> LN -> ReLU -> conv 3x3 32 -> 64 -> LN -> ReLU -> conv 1x1
-// 64 -> 8 -> LN -> ReLU -> flatten (1352) -> Linear(1352,128) -> LN ->
-// ReLU -> Linear(128,128) -> LN -> ReLU -> three heads 128 -> 64 -> ReLU ->
-// 5 | 2 | 1.  Every LayerNorm normalises one sample over all of its values
-// with an elementwise affine of the same shape.
+// Network per (observation row, player): conv0 3x3 (14 -> 16 channels, the
+// player's view permutation applied to the input planes) -> LayerNorm([16,
+// 13,13]) -> ReLU -> conv 3x3 16 -> 32 -> LN -> ReLU -> conv 3x3 32 -> 64 ->
+// LN -> ReLU -> conv 1x1 64 -> 8 -> LN -> ReLU -> flatten (1352) ->
+// Linear(1352,128) -> LN -> ReLU -> Linear(128,128) -> LN -> ReLU -> three
+// heads 128 -> 64 -> ReLU -> 5 | 2 | 1.  Every LayerNorm normalises one
+// sample over all of its values (eps 1e-5) with an elementwise affine.
 //
-// One workgroup (8 wavefronts) per (observation row, player).  The feature
-// maps live in LDS: the conv input as zero-padded 15 x 15 planes [C][225],
-// the conv output as [C][176] (169 positions padded to 11 row tiles of 16).
-// Each conv is an implicit GEMM on v_mfma_f32_16x16x4_f32 (float32 operands,
-// so the trunk is float32 throughout): M = positions (11 tiles), N = output
-// channels (16 per tile), K = C_in x taps with k = ci * 9 + 3 dy + dx; lane l
-// reads its A element from the padded plane at the position of row l % 16
-// shifted by the tap of K row k0 + l / 16, and its B element from the K-major
-// weight [K][C_out] in global memory (L2-resident, shared by every
-// workgroup).  The per-sample LayerNorms reduce over the workgroup (two
-// passes: mean, then squared deviations).  The MLP head runs as
-// matrix-vector products on the vector units, four (or two, eight) threads
-// per output with a shuffle reduction; sampling as in the mlp kernel.
+// Persistent kernel: one workgroup (4 wavefronts, one per SIMD, so each
+// wavefront may hold 512 registers) per CU walks a contiguous
+// range of items (row, player).  All arithmetic is float32; every product
+// with weights runs on v_mfma_f32_16x16x4_f32 (A[i][k]: lane l holds row
+// l % 16, k = l / 16; B[k][j]: lane l holds k = l / 16, column l % 16;
+// D[i][j]: lane l holds rows 4 (l / 16) + q, column l % 16).
+//
+// Trunk, one item at a time, feature maps in LDS as zero-bordered 15 x 15
+// planes (row stride 15, plane stride PL):
+//   * convolutions are implicit GEMMs with M = positions (11 tiles of 16),
+//     N = output channels, K in steps of 4 channels: step j covers channels
+//     4 (j / 9) + l / 16 at tap j % 9 (1x1: channels 4 j + l / 16), so lane
+//     l's A address is a per-lane base (its channel and position) plus a
+//     per-step constant, the immediate offset of a ds_read_b32;
+//   * the B operands of the two wide convolutions stay in registers for the
+//     whole kernel (wavefront w owns output tile w % NT of each, 108
+//     registers), those of conv0 and the 1x1 conv (one output tile, shared
+//     by all wavefronts) in LDS; all are packed on the host as
+//     [tile][step][lane]; the K loop is step-outer, tile-inner, so one
+//     step's A loads feed independent accumulators;
+//   * the accumulators of a layer are its output: the LayerNorm reduces them
+//     across the workgroup (mean, then squared deviations), and the
+//     normalised, rectified values are written over the input planes (after
+//     the last conv, into this item's row of the flat buffer).
+// Head, per batch of up to 16 items: Linear(1352,128), Linear(128,128) and
+// the heads' hidden layer are MFMA GEMMs with M = the 16 items (B streamed
+// from L2 once per batch), LayerNorm(128) by 16 threads per item, then the
+// output layer and the masked sampling per item.
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -40,25 +55,35 @@ namespace cnn {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int T = 512;                 // threads
-constexpr int NW = T / 64;             // wavefronts
-constexpr int HW = 13, NP = 169, NPT = 176, PL = 225;   // grid, positions, padded
-constexpr int C0 = 14, F0 = 16, F1 = 32, F2 = 64, F3 = 8;
-constexpr int FLAT = F3 * NP;          // 1352
-constexpr int HID = 128, HEAD = 64;
+constexpr int T = 256, NW = 4;
+constexpr int HW = 13, NP = 169, MT = 11;
+constexpr int PL = 240;                     // plane stride (15 x 15 = 225 used); 16 mod 32 banks
+constexpr int C0 = 14;
+constexpr int SB = 16;                      // items per head batch
+constexpr int FLAT = 8 * NP;                // 1352
+constexpr int FS = 1378;                    // flat row stride (2 mod 32 banks)
+constexpr int HID = 128, HS = 130, HYS = 194;
+constexpr int S0 = 36, S1 = 36, S2 = 72, S3 = 16;   // K steps of the four convolutions
+constexpr int L0 = FLAT / 4, L1 = HID / 4;          // K steps of the head GEMMs
 
 struct __align__(16) Lds {
-  float in[F2][PL];                    // padded conv input planes
-  float out[F2][NPT];                  // conv output [channel][position]
+  float plane[64 * PL];
+  float flat[SB * FS];                      // trunk outputs; head scratch after GEMM 1
+  float wc0[S0 * 64], wc3[S3 * 64];         // conv0 / conv1x1 B operands (shared by all waves)
   float red[NW];
-  float h[HID], h2[HID], hy[3 * HEAD], logit[8];
 };
+// head scratch inside flat (free once Linear(1352,128) has read it)
+constexpr int H_OFF = 0, H2_OFF = SB * HS, HY_OFF = 2 * SB * HS, LG_OFF = 2 * SB * HS + SB * HYS;
+static_assert(LG_OFF + SB * 8 <= SB * FS, "head scratch fits in the flat buffer");
+
+__device__ __forceinline__ floatx4 mfma(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
 
 __device__ __forceinline__ float block_sum(float v, float* red) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  const int wv = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) red[wv] = v;
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   float s = 0.0f;
 #pragma unroll
@@ -67,195 +92,350 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return s;
 }
 
-// out[n][p] = bias[n] + sum_k A[p][k] W[k][n]; A[p][k] = in[ci][pad(p) + tap(k)].
-template <int CIN, int COUT, int KS>
-__device__ __forceinline__ void conv(const float (*in)[PL], const float* __restrict__ w,
-                                     const float* __restrict__ bias, float (*out)[NPT]) {
-  constexpr int TAPS = KS * KS, K = CIN * TAPS, KP = (K + 3) & ~3;
-  constexpr int NT = (COUT + 15) / 16, MT = NPT / 16;
-  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int i16 = lane & 15, kq = lane >> 4;
-  for (int tile = wv; tile < MT * NT; tile += NW) {
-    const int mt = tile % MT, nt = tile / MT;
-    const int p = min(16 * mt + i16, NP - 1);        // A row: position (rows past 168 unused)
-    const int pbase = (p / HW) * 15 + (p % HW);      // padded (y, x) of tap (0, 0)
-    const int n = 16 * nt + i16;                     // B column: output channel
-    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 4
-    for (int k0 = 0; k0 < KP; k0 += 4) {
-      const int k = k0 + kq;
-      float av = 0.0f, bv = 0.0f;
-      if (k < K) {
-        const int ci = k / TAPS, tap = k % TAPS;
-        const int off = KS == 3 ? (tap / 3) * 15 + (tap % 3) : 16;   // 1x1: the centre
-        av = in[ci][pbase + off];
-        if (n < COUT) bv = w[k * COUT + n];
-      }
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
-    }
-    if (n < COUT) {
-      const float b = bias[n];
+// LDS offset of step j's A element relative to the lane base.
+template <bool K1>
+__device__ __forceinline__ constexpr int step_off(int j) {
+  return K1 ? 4 * j * PL + 16 : 4 * (j / 9) * PL + ((j % 9) / 3) * 15 + (j % 9) % 3;
+}
+
+// One conv layer for this wavefront: position tiles min(mt0 + t ms, 10),
+// t < NTL (duplicates of tile 10 are computed and later ignored);
+// acc[t] = bias + sum_j A B[j].
+template <int STEPS, int NTL, bool K1>
+__device__ __forceinline__ void conv(const float* plane, const float (&b)[STEPS], float bias,
+                                     int mt0, int ms, floatx4 (&acc)[NTL]) {
+  const int lane = threadIdx.x & 63, i16 = lane & 15, kq = lane >> 4;
+  const float* base[NTL];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) out[n][16 * mt + 4 * kq + q] = acc[q] + b;
-    }
+  for (int t = 0; t < NTL; ++t) {
+    const int p = min(16 * min(mt0 + t * ms, MT - 1) + i16, NP - 1);
+    base[t] = plane + kq * PL + (p / HW) * 15 + (p % HW);
+    acc[t] = floatx4{bias, bias, bias, bias};
+  }
+#pragma unroll
+  for (int j = 0; j < STEPS; ++j) {
+#pragma unroll
+    for (int t = 0; t < NTL; ++t) acc[t] = mfma(base[t][step_off<K1>(j)], b[j], acc[t]);
   }
 }
 
-// LayerNorm over out[0..C)[0..169) with elementwise affine gamma/beta [C*169],
-// ReLU; results to the padded planes (or, flat, to dst[c*169 + p]).
-template <int C>
-__device__ __forceinline__ void ln_relu(float (*out)[NPT], const float* __restrict__ gam,
-                                        const float* __restrict__ bet, float (*dst)[PL],
-                                        float* flat, float* red) {
+// As conv, with B read from LDS (packed [step][lane]).
+template <int STEPS, int NTL, bool K1>
+__device__ __forceinline__ void conv_lds(const float* plane, const float* wl, float bias,
+                                         int mt0, int ms, floatx4 (&acc)[NTL]) {
+  const int lane = threadIdx.x & 63, i16 = lane & 15, kq = lane >> 4;
+  const float* base[NTL];
+#pragma unroll
+  for (int t = 0; t < NTL; ++t) {
+    const int p = min(16 * min(mt0 + t * ms, MT - 1) + i16, NP - 1);
+    base[t] = plane + kq * PL + (p / HW) * 15 + (p % HW);
+    acc[t] = floatx4{bias, bias, bias, bias};
+  }
+#pragma unroll
+  for (int j = 0; j < STEPS; ++j) {
+    const float bv = wl[j * 64 + lane];
+#pragma unroll
+    for (int t = 0; t < NTL; ++t) acc[t] = mfma(base[t][step_off<K1>(j)], bv, acc[t]);
+  }
+}
+
+// LayerNorm statistics over the valid outputs of a layer (n < cout, p < 169).
+template <int NTL>
+__device__ __forceinline__ void ln_stats(const floatx4 (&acc)[NTL], int mt0, int ms,
+                                         bool nvalid, float* red, float inv_count,
+                                         float& mean, float& rstd) {
+  const int kq = (threadIdx.x & 63) >> 4;
   float s = 0.0f;
-  for (int i = threadIdx.x; i < C * NP; i += T) s += out[i / NP][i % NP];
-  const float mean = block_sum(s, red) / (float)(C * NP);
+#pragma unroll
+  for (int t = 0; t < NTL; ++t)
+    if (mt0 + t * ms < MT && nvalid) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (16 * (mt0 + t * ms) + 4 * kq + q < NP) s += acc[t][q];
+    }
+  mean = block_sum(s, red) * inv_count;
+  float v = 0.0f;
+#pragma unroll
+  for (int t = 0; t < NTL; ++t)
+    if (mt0 + t * ms < MT && nvalid) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (16 * (mt0 + t * ms) + 4 * kq + q < NP) {
+          const float d = acc[t][q] - mean;
+          v += d * d;
+        }
+    }
+  rstd = 1.0f / sqrtf(block_sum(v, red) * inv_count + 1e-5f);
+}
+
+// relu(LN affine) of this wavefront's outputs: into the padded planes, or
+// (flat != nullptr) into flat[n * 169 + p].  g / bt: [NT][11][64][4] packed.
+template <int NTL>
+__device__ __forceinline__ void ln_write(const floatx4 (&acc)[NTL], int mt0, int ms, int ntile,
+                                         bool nvalid, float mean, float rstd,
+                                         const float* __restrict__ g, const float* __restrict__ bt,
+                                         float* plane, float* flat) {
+  const int lane = threadIdx.x & 63, i16 = lane & 15, kq = lane >> 4;
+  const int n = 16 * ntile + i16;
+#pragma unroll
+  for (int t = 0; t < NTL; ++t)
+    if (mt0 + t * ms < MT && nvalid) {
+      const int mt = mt0 + t * ms;
+      const size_t gi = ((size_t)(ntile * MT + mt) * 64 + lane) * 4;
+      const float4 gg = *reinterpret_cast<const float4*>(g + gi);
+      const float4 bb = *reinterpret_cast<const float4*>(bt + gi);
+      const float gv[4] = {gg.x, gg.y, gg.z, gg.w}, bv[4] = {bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int p = 16 * mt + 4 * kq + q;
+        if (p < NP) {
+          const float y = fmaxf((acc[t][q] - mean) * rstd * gv[q] + bv[q], 0.0f);
+          if (flat) flat[n * NP + p] = y;
+          else plane[n * PL + (p / HW + 1) * 15 + (p % HW) + 1] = y;
+        }
+      }
+    }
+}
+
+// Head GEMM for tiles nt0 + i (i < NTW): D[m][n] = sum_k A[m * as + k] W[k][n],
+// A in LDS, W packed [tile][step][lane] in global memory.
+template <int STEPS, int NTW>
+__device__ __forceinline__ void head_gemm(const float* A, int as, const float* __restrict__ w,
+                                          int nt0, floatx4 (&c)[NTW]) {
+  const int lane = threadIdx.x & 63, i16 = lane & 15, kq = lane >> 4;
+  const float* a = A + i16 * as + kq;
+  const float* b = w + (size_t)nt0 * STEPS * 64 + lane;
+#pragma unroll
+  for (int i = 0; i < NTW; ++i) c[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 2
+  for (int j = 0; j < STEPS; ++j) {
+    const float av = a[4 * j];
+#pragma unroll
+    for (int i = 0; i < NTW; ++i) c[i] = mfma(av, b[(i * STEPS + j) * 64], c[i]);
+  }
+}
+
+// D tile -> dst[m * ds + 16 * ntile + i16] for the 16 rows m (+ bias, optional ReLU).
+__device__ __forceinline__ void head_store(floatx4 c, float* dst, int ds, int ntile,
+                                           const float* __restrict__ bias, bool relu) {
+  const int lane = threadIdx.x & 63, i16 = lane & 15, kq = lane >> 4;
+  const int n = 16 * ntile + i16;
+  const float bv = bias[n];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float y = c[q] + bv;
+    dst[(4 * kq + q) * ds + n] = relu ? fmaxf(y, 0.0f) : y;
+  }
+}
+
+// LayerNorm(128) + ReLU of rows m < nb of h (stride HS), 16 threads per row.
+__device__ __forceinline__ void head_ln(float* h, int nb, const float* __restrict__ g,
+                                        const float* __restrict__ bt) {
+  const int m = threadIdx.x >> 4, c = threadIdx.x & 15;
+  float v[8];
+  float s = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    v[r] = h[m * HS + c + 16 * r];
+    s += v[r];
+  }
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+  const float mean = s * (1.0f / HID);
   float q = 0.0f;
-  for (int i = threadIdx.x; i < C * NP; i += T) {
-    const float d = out[i / NP][i % NP] - mean;
-    q += d * d;
-  }
-  const float rstd = 1.0f / sqrtf(block_sum(q, red) / (float)(C * NP) + 1e-5f);
-  for (int i = threadIdx.x; i < C * NP; i += T) {
-    const int c = i / NP, p = i % NP;
-    const float y = fmaxf((out[c][p] - mean) * rstd * gam[i] + bet[i], 0.0f);
-    if (flat) flat[i] = y;
-    else dst[c][(p / HW + 1) * 15 + (p % HW) + 1] = y;
-  }
-}
-
-// LayerNorm(128) + ReLU of v in place, by the first wavefront (2 values per lane).
-__device__ __forceinline__ void ln128(float* v, const float* __restrict__ gam,
-                                      const float* __restrict__ bet) {
-  if (threadIdx.x < 64) {
-    const int l = threadIdx.x;
-    float a = v[l], b = v[l + 64];
-    float s = a + b;
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
-    const float mean = s / (float)HID;
-    float q = (a - mean) * (a - mean) + (b - mean) * (b - mean);
+  for (int r = 0; r < 8; ++r) q += (v[r] - mean) * (v[r] - mean);
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) q += __shfl_xor(q, m, 64);
-    const float rstd = 1.0f / sqrtf(q / (float)HID + 1e-5f);
-    v[l] = fmaxf((a - mean) * rstd * gam[l] + bet[l], 0.0f);
-    v[l + 64] = fmaxf((b - mean) * rstd * gam[l + 64] + bet[l + 64], 0.0f);
+  for (int o = 8; o >= 1; o >>= 1) q += __shfl_xor(q, o, 64);
+  const float rstd = 1.0f / sqrtf(q * (1.0f / HID) + 1e-5f);
+  if (m < nb) {
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int k = c + 16 * r;
+      h[m * HS + k] = fmaxf((v[r] - mean) * rstd * g[k] + bt[k], 0.0f);
+    }
   }
 }
 
-// y[o] = b[o] + sum_k x[k] wt[k][o] for o < NO, with G threads per output
-// (a power of two, consecutive lanes) summing k = j, j + G, ...
-template <int NI, int NO, int G>
-__device__ __forceinline__ void matvec(const float* x, const float* __restrict__ wt,
-                                       const float* __restrict__ b, float* y) {
-  const int o = threadIdx.x / G, j = threadIdx.x % G;
-  float acc = 0.0f;
-  if (o < NO)
-    for (int k = j; k < NI; k += G) acc += x[k] * wt[k * NO + o];
-#pragma unroll
-  for (int m = G / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
-  if (o < NO && j == 0) y[o] = acc + b[o];
-}
-
-__global__ __launch_bounds__(T) void cnn_act_kernel(const qqt_cnn_args a) {
+__global__ __launch_bounds__(T, 1) void cnn_act_kernel(const qqt_cnn_args a, int items, int per) {
   __shared__ Lds s;
-  const int row = blockIdx.x / a.npid, slot = blockIdx.x % a.npid;
-  const int pid = a.npid == 2 ? slot : a.pid0;
   const int t = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int lane = t & 63, i16 = lane & 15;
 
-  // zero the padded planes, then the observation row into channels 0..13
-  for (int i = t; i < F2 * PL; i += T) (&s.in[0][0])[i] = 0.0f;
-  __syncthreads();
-  const uint16_t* ob = a.obs + (size_t)row * a.obs_stride;
-  for (int i = t; i < C0 * NP; i += T) {
-    const int c = i / NP, p = i % NP;
-    s.in[c][(p / HW + 1) * 15 + (p % HW) + 1] = __half2float(__ushort_as_half(ob[i]));
-  }
-  __syncthreads();
-
-  conv<C0, F0, 3>(s.in, a.c0w + (size_t)pid * C0 * 9 * F0, a.c0b, s.out);
-  __syncthreads();
-  ln_relu<F0>(s.out, a.ln0w, a.ln0b, s.in, nullptr, s.red);
-  __syncthreads();
-  conv<F0, F1, 3>(s.in, a.c1w, a.c1b, s.out);
-  __syncthreads();
-  ln_relu<F1>(s.out, a.ln1w, a.ln1b, s.in, nullptr, s.red);
-  __syncthreads();
-  conv<F1, F2, 3>(s.in, a.c2w, a.c2b, s.out);
-  __syncthreads();
-  ln_relu<F2>(s.out, a.ln2w, a.ln2b, s.in, nullptr, s.red);
-  __syncthreads();
-  conv<F2, F3, 1>(s.in, a.c3w, a.c3b, s.out);
-  __syncthreads();
-  float* const flat = &s.in[0][0];                    // the planes are free now
-  ln_relu<F3>(s.out, a.ln3w, a.ln3b, s.in, flat, s.red);
-  __syncthreads();
-
-  // shared MLP and heads
-  matvec<FLAT, HID, 4>(flat, a.s0wt, a.s0b, s.h);
-  __syncthreads();
-  ln128(s.h, a.s1w, a.s1b);
-  __syncthreads();
-  matvec<HID, HID, 4>(s.h, a.s3wt, a.s3b, s.h2);
-  __syncthreads();
-  ln128(s.h2, a.s4w, a.s4b);
-  __syncthreads();
-  matvec<HID, 3 * HEAD, 2>(s.h2, a.hwt, a.hb, s.hy);
-  __syncthreads();
-  for (int i = t; i < 3 * HEAD; i += T) s.hy[i] = fmaxf(s.hy[i], 0.0f);
-  __syncthreads();
-  if (t < 8 * 8) {                                     // outputs: 8 threads each, 8 terms
-    const int o = t >> 3, j = t & 7;
-    const int base = o < 5 ? 0 : o < 7 ? HEAD : 2 * HEAD;
-    float acc = 0.0f;
-    for (int k = j; k < HEAD; k += 8) acc += s.hy[base + k] * a.fw[o * HEAD + k];
+  // conv B operands, resident for the whole kernel
+  float b1[S1], b2[S2];
+  const int n1 = w & 1, n2 = w;
 #pragma unroll
-    for (int m = 4; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
-    if (j == 0) s.logit[o] = acc + a.fb[o];
-  }
-  __syncthreads();
-
-  if (t == 0) {
-    const int oslots = a.out_slots > 0 ? a.out_slots : a.npid;
-    const int oslot = a.npid == 2 ? slot : a.out_slot;
-    const size_t o = (size_t)row * oslots + oslot;
-    if (a.logits_out) {
+  for (int j = 0; j < S1; ++j) b1[j] = a.c1w[(n1 * S1 + j) * 64 + lane];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) a.logits_out[o * 8 + k] = s.logit[k];
+  for (int j = 0; j < S2; ++j) b2[j] = a.c2w[(n2 * S2 + j) * 64 + lane];
+  const float bias0 = a.c0b[i16], bias1 = a.c1b[16 * n1 + i16], bias2 = a.c2b[16 * n2 + i16];
+  const float bias3 = a.c3b[i16];
+
+  // position tiles per wavefront: conv0 / conv3 {w + 4i}, i < 3; conv1
+  // {w/2 + 2i}, i < 6; conv2 all 11
+  const int mt1 = w >> 1;
+
+  for (int i = t; i < 64 * PL; i += T) s.plane[i] = 0.0f;
+  for (int i = t; i < S0 * 64; i += T) s.wc0[i] = a.c0w[i];
+  for (int i = t; i < S3 * 64; i += T) s.wc3[i] = a.c3w[i];
+
+  const int start = blockIdx.x * per, end = min(items, start + per);
+  for (int ib = start; ib < end; ib += SB) {
+    const int nb = min(SB, end - ib);
+    for (int ii = 0; ii < nb; ++ii) {
+      const int item = ib + ii;
+      const int row = item / a.npid, slot = item % a.npid;
+      const int pid = a.npid == 2 ? slot : a.pid0;
+      __syncthreads();                                  // planes 0..13 free
+      const uint16_t* ob = a.obs + (size_t)row * a.obs_stride;
+      const int32_t* perm = a.view_perm + pid * C0;
+      for (int i = t; i < C0 * NP; i += T) {
+        const int c = i / NP, p = i - c * NP;
+        s.plane[c * PL + (p / HW + 1) * 15 + (p % HW) + 1] =
+            __half2float(__ushort_as_half(ob[perm[c] * NP + p]));
+      }
+      __syncthreads();
+
+      float mean, rstd;
+      {
+        floatx4 acc[3];
+        conv_lds<S0, 3, false>(s.plane, s.wc0, bias0, w, 4, acc);
+        ln_stats<3>(acc, w, 4, true, s.red, 1.0f / (16 * NP), mean, rstd);
+        ln_write<3>(acc, w, 4, 0, true, mean, rstd, a.ln0w, a.ln0b, s.plane, nullptr);
+      }
+      __syncthreads();
+      {
+        floatx4 acc[6];
+        conv<S1, 6, false>(s.plane, b1, bias1, mt1, 2, acc);
+        ln_stats<6>(acc, mt1, 2, true, s.red, 1.0f / (32 * NP), mean, rstd);
+        ln_write<6>(acc, mt1, 2, n1, true, mean, rstd, a.ln1w, a.ln1b, s.plane, nullptr);
+      }
+      __syncthreads();
+      {
+        floatx4 acc[MT];
+        conv<S2, MT, false>(s.plane, b2, bias2, 0, 1, acc);
+        ln_stats<MT>(acc, 0, 1, true, s.red, 1.0f / (64 * NP), mean, rstd);
+        ln_write<MT>(acc, 0, 1, n2, true, mean, rstd, a.ln2w, a.ln2b, s.plane, nullptr);
+      }
+      __syncthreads();
+      {
+        floatx4 acc[3];
+        conv_lds<S3, 3, true>(s.plane, s.wc3, bias3, w, 4, acc);
+        const bool nv = i16 < 8;
+        ln_stats<3>(acc, w, 4, nv, s.red, 1.0f / (8 * NP), mean, rstd);
+        ln_write<3>(acc, w, 4, 0, nv, mean, rstd, a.ln3w, a.ln3b, s.plane, s.flat + ii * FS);
+      }
     }
-    if (a.value_out) a.value_out[o] = s.logit[7];
-    if (a.sample) {
-      uint8_t mm[5], bm[2];
+    __syncthreads();
+
+    // ---------------- head over the batch's nb items (rows m of the GEMMs;
+    // rows >= nb carry stale values that only reach their own rows)
+    float* const h = s.flat + H_OFF;
+    float* const h2 = s.flat + H2_OFF;
+    float* const hy = s.flat + HY_OFF;
+    float* const lg = s.flat + LG_OFF;
+    {
+      floatx4 c[2];
+      head_gemm<L0, 2>(s.flat, FS, a.s0p, 2 * w, c);
+      __syncthreads();                                  // flat fully read
+      head_store(c[0], h, HS, 2 * w, a.s0b, false);
+      head_store(c[1], h, HS, 2 * w + 1, a.s0b, false);
+    }
+    __syncthreads();
+    head_ln(h, nb, a.s1w, a.s1b);
+    __syncthreads();
+    {
+      floatx4 c[2];
+      head_gemm<L1, 2>(h, HS, a.s3p, 2 * w, c);
+      head_store(c[0], h2, HS, 2 * w, a.s3b, false);
+      head_store(c[1], h2, HS, 2 * w + 1, a.s3b, false);
+    }
+    __syncthreads();
+    head_ln(h2, nb, a.s4w, a.s4b);
+    __syncthreads();
+    {
+      floatx4 c[3];
+      head_gemm<L1, 3>(h2, HS, a.hp, 3 * w, c);
 #pragma unroll
-      for (int k = 0; k < 5; ++k)
-        mm[k] = a.move_mask[(size_t)row * a.mm_row_stride + (size_t)pid * a.mm_pid_stride + k];
+      for (int i = 0; i < 3; ++i) head_store(c[i], hy, HYS, 3 * w + i, a.hb, true);
+    }
+    __syncthreads();
+    if (t < SB * 8) {                                   // output layer: item m, output o
+      const int m = t >> 3, o = t & 7;
+      const int base = o < 5 ? 0 : o < 7 ? 64 : 128;
+      const float* x = hy + m * HYS + base;
+      const float* wf = a.fw + o * 64;
+      float acc = 0.0f;
+#pragma unroll 8
+      for (int k = 0; k < 64; ++k) acc += x[k] * wf[k];
+      lg[m * 8 + o] = acc + a.fb[o];
+    }
+    __syncthreads();
+    if (t < nb) {
+      const int item = ib + t;
+      const int row = item / a.npid, slot = item % a.npid;
+      const int pid = a.npid == 2 ? slot : a.pid0;
+      float l8[8];
 #pragma unroll
-      for (int k = 0; k < 2; ++k)
-        bm[k] = a.bomb_mask[(size_t)row * a.bm_row_stride + (size_t)pid * a.bm_pid_stride + k];
-      float um, ub;
-      if (a.uniforms) {
-        um = a.uniforms[o * 2 + 0];
-        ub = a.uniforms[o * 2 + 1];
-      } else {
-        float u4[4];
-        philox_block(a.seed, (uint32_t)row, a.tick, STREAM_POLICY, (uint32_t)((2 * pid) >> 2), u4);
-        um = u4[(2 * pid) & 3];
-        ub = u4[(2 * pid + 1) & 3];
+      for (int k = 0; k < 8; ++k) l8[k] = lg[t * 8 + k];
+      const int oslots = a.out_slots > 0 ? a.out_slots : a.npid;
+      const int oslot = a.npid == 2 ? slot : a.out_slot;
+      const size_t o = (size_t)row * oslots + oslot;
+      if (a.logits_out) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) a.logits_out[o * 8 + k] = l8[k];
       }
-      float lpm, lpb;
-      const int am = sample_masked<5>(s.logit, mm, um, &lpm);
-      const int ab = sample_masked<2>(s.logit + 5, bm, ub, &lpb);
-      if (a.actions) {
-        a.actions[o * 2 + 0] = am;
-        a.actions[o * 2 + 1] = ab;
+      if (a.value_out) a.value_out[o] = l8[7];
+      if (a.sample) {
+        uint8_t mm[5], bm[2];
+#pragma unroll
+        for (int k = 0; k < 5; ++k)
+          mm[k] = a.move_mask[(size_t)row * a.mm_row_stride + (size_t)pid * a.mm_pid_stride + k];
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+          bm[k] = a.bomb_mask[(size_t)row * a.bm_row_stride + (size_t)pid * a.bm_pid_stride + k];
+        float um, ub;
+        if (a.uniforms) {
+          um = a.uniforms[o * 2 + 0];
+          ub = a.uniforms[o * 2 + 1];
+        } else {
+          float u4[4];
+          philox_block(a.seed, (uint32_t)row, a.tick, STREAM_POLICY, (uint32_t)((2 * pid) >> 2),
+                       u4);
+          um = u4[(2 * pid) & 3];
+          ub = u4[(2 * pid + 1) & 3];
+        }
+        float lpm, lpb;
+        const int am = sample_masked<5>(l8, mm, um, &lpm);
+        const int ab = sample_masked<2>(l8 + 5, bm, ub, &lpb);
+        if (a.actions) {
+          a.actions[o * 2 + 0] = am;
+          a.actions[o * 2 + 1] = ab;
+        }
+        if (a.actions_i8) {
+          a.actions_i8[o * 2 + 0] = (int8_t)am;
+          a.actions_i8[o * 2 + 1] = (int8_t)ab;
+        }
+        if (a.logp_out) a.logp_out[o] = lpm + lpb;
       }
-      if (a.actions_i8) {
-        a.actions_i8[o * 2 + 0] = (int8_t)am;
-        a.actions_i8[o * 2 + 1] = (int8_t)ab;
-      }
-      if (a.logp_out) a.logp_out[o] = lpm + lpb;
     }
   }
+}
+
+int cu_count() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        c <= 0)
+      c = 256;
+    cus[dev] = c;
+  }
+  return cus[dev];
 }
 
 }  // namespace cnn
@@ -267,16 +447,22 @@ int qqt_cnn_act(const qqt_cnn_args* a, void* stream) {
   using namespace qqt;
   using namespace qqt::cnn;
   g_err[0] = 0;
-  if (!a || !a->obs || !a->c0w || !a->c0b || !a->ln0w || !a->ln0b || !a->c1w || !a->c1b ||
-      !a->ln1w || !a->ln1b || !a->c2w || !a->c2b || !a->ln2w || !a->ln2b || !a->c3w ||
-      !a->c3b || !a->ln3w || !a->ln3b || !a->s0wt || !a->s0b || !a->s1w || !a->s1b ||
-      !a->s3wt || !a->s3b || !a->s4w || !a->s4b || !a->hwt || !a->hb || !a->fw || !a->fb) {
+  if (!a || !a->obs || !a->view_perm || !a->c0w || !a->c0b || !a->ln0w || !a->ln0b ||
+      !a->c1w || !a->c1b || !a->ln1w || !a->ln1b || !a->c2w || !a->c2b || !a->ln2w ||
+      !a->ln2b || !a->c3w || !a->c3b || !a->ln3w || !a->ln3b || !a->s0p || !a->s0b ||
+      !a->s1w || !a->s1b || !a->s3p || !a->s3b || !a->s4w || !a->s4b || !a->hp || !a->hb ||
+      !a->fw || !a->fb) {
     snprintf(g_err, sizeof(g_err), "qqt_cnn_act: null pointer argument");
+    return QQT_E_ARG;
+  }
+  if (((uintptr_t)a->ln0w | (uintptr_t)a->ln0b | (uintptr_t)a->ln1w | (uintptr_t)a->ln1b |
+       (uintptr_t)a->ln2w | (uintptr_t)a->ln2b | (uintptr_t)a->ln3w | (uintptr_t)a->ln3b) & 15) {
+    snprintf(g_err, sizeof(g_err), "qqt_cnn_act: LayerNorm tables must be 16-byte aligned");
     return QQT_E_ARG;
   }
   if (a->batch <= 0 || (a->npid != 1 && a->npid != 2) || a->w_players < a->npid ||
       a->w_players > 4 || a->pid0 < 0 || (a->npid == 1 && a->pid0 >= a->w_players) ||
-      a->obs_stride < C0 * NP) {
+      a->obs_stride < C0 * NP || (int64_t)a->batch * a->npid > INT32_MAX) {
     snprintf(g_err, sizeof(g_err), "qqt_cnn_act: bad batch, players or observation stride");
     return QQT_E_ARG;
   }
@@ -290,8 +476,11 @@ int qqt_cnn_act(const qqt_cnn_args* a, void* stream) {
     snprintf(g_err, sizeof(g_err), "qqt_cnn_act: sampling needs masks");
     return QQT_E_ARG;
   }
-  QQT_LAUNCH(QQT_KERNEL_CNN, cnn_act_kernel, dim3(a->batch * a->npid), dim3(T),
-             (hipStream_t)stream, *a);
+  const int items = a->batch * a->npid;
+  const int grid = min(cu_count(), (items + SB - 1) / SB);
+  const int per = (items + grid - 1) / grid;
+  QQT_LAUNCH(QQT_KERNEL_CNN, cnn_act_kernel, dim3(grid), dim3(T), (hipStream_t)stream, *a,
+             items, per);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     snprintf(g_err, sizeof(g_err), "cnn launch failed: %s", hipGetErrorString(err));

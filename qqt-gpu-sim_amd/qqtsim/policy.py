@@ -243,50 +243,85 @@ class HipActorCritic:
 CNN_CHANNELS = (16, 32, 64, 8)
 
 
+def _pack_conv(w: torch.Tensor, n_tiles: int) -> torch.Tensor:
+    """[out][in][k][k] conv weight -> the cnn kernel's B operand [tile][step][lane]:
+    lane l of step j holds output 16 tile + l % 16 and, for a 3x3 conv, input
+    channel 4 (j // 9) + l // 16 at tap j % 9 (dy = tap // 3, dx = tap % 3);
+    for a 1x1 conv input channel 4 j + l // 16.  Inputs are padded to a
+    multiple of 4 and outputs to 16 n_tiles with zeros."""
+    cout, cin, kh, kw = w.shape
+    taps = kh * kw
+    cinp = -(-cin // 4) * 4
+    wp = torch.zeros((n_tiles * 16, cinp, taps), dtype=torch.float32)
+    wp[:cout, :cin] = w.float().reshape(cout, cin, taps)
+    x = wp.view(n_tiles, 16, cinp // 4, 4, taps)              # [tile][i16][cb][kq][tap]
+    return x.permute(0, 2, 4, 3, 1).reshape(-1).contiguous()  # [tile][cb*taps+tap][kq*16+i16]
+
+
+def _pack_linear(w: torch.Tensor) -> torch.Tensor:
+    """[out][in] Linear weight -> [tile][step][lane]: lane l of step j holds
+    output 16 tile + l % 16, input 4 j + l // 16."""
+    n, k = w.shape
+    x = w.float().reshape(n // 16, 16, k // 4, 4)             # [tile][i16][j][kq]
+    return x.permute(0, 2, 3, 1).reshape(-1).contiguous()
+
+
+def _pack_ln(g: torch.Tensor, n_tiles: int) -> torch.Tensor:
+    """[C][13][13] LayerNorm affine -> [tile][11][lane][4]: value q of lane l
+    in position tile mt is channel 16 tile + l % 16, position 16 mt +
+    4 (l // 16) + q (zero past 169 positions or C channels)."""
+    c = g.shape[0]
+    gp = torch.zeros((n_tiles * 16, 176), dtype=torch.float32)
+    gp[:c, :169] = g.float().reshape(c, 169)
+    x = gp.view(n_tiles, 16, 11, 4, 4)                        # [tile][i16][mt][kq][q]
+    return x.permute(0, 2, 3, 1, 4).reshape(-1).contiguous()
+
+
 def pack_cnn(params: dict, n_players: int = 2, obs_shape=(14, 13, 13)) -> dict:
     """Host-side packing of an ActorCritic cnn state_dict (train/model.py:79-96)
-    into the layout of qqt_cnn_act: conv weights K-major [ci*taps + tap][out]
-    with each player's view permutation folded into conv0's input channels
-    (conv0.weight[:, argsort(view_perm)], :186-190), Linear weights
-    transposed, LayerNorm affines flattened."""
+    into the operand layout of qqt_cnn_act (CPU tensors out), plus the view
+    permutation table: conv0 input plane j of player p is observation channel
+    view_perm(p)[j], which equals the reference's conv0.weight[:,
+    argsort(view_perm)] over the stored observation (:186-190)."""
     c, h, w = obs_shape
     if (c, h, w) != (14, 13, 13) or n_players != 2:
         raise ValueError("the cnn kernel is built for 2 players on a 13 x 13 grid (14 channels)")
     f = lambda k: params[k].float().cpu()  # noqa: E731
-
-    def kmajor(wt):                       # [out][in][kh][kw] -> [in*kh*kw][out]
-        return wt.permute(1, 2, 3, 0).reshape(-1, wt.shape[0]).contiguous()
-
-    w0 = f("conv0.weight")
-    if tuple(w0.shape) != (16, c, 3, 3):
-        raise ValueError(f"conv0.weight must be {(16, c, 3, 3)}, got {tuple(w0.shape)}")
-    c0w = torch.stack([kmajor(w0[:, torch.argsort(torch.tensor(view_perm(pid, n_players, c)))])
-                       for pid in range(n_players)])
+    shapes = {"conv0.weight": (16, c, 3, 3), "conv.2.weight": (32, 16, 3, 3),
+              "conv.5.weight": (64, 32, 3, 3), "conv.8.weight": (8, 64, 1, 1),
+              "shared.0.weight": (HID, 8 * h * w), "shared.3.weight": (HID, HID)}
+    for k, shp in shapes.items():
+        if tuple(params[k].shape) != shp:
+            raise ValueError(f"{k} must be {shp}, got {tuple(params[k].shape)}")
     heads = ("move_head", "bomb_head", "critic")
     fw = torch.cat([f(f"{n}.2.weight") for n in heads])
     if fw.shape != (8, HEAD):
         raise ValueError("heads must produce 5 + 2 + 1 outputs from 64 hidden units")
+    c3b = torch.zeros(16)
+    c3b[:8] = f("conv.8.bias")
     out = dict(
-        c0w=c0w.reshape(-1).contiguous(), c0b=f("conv0.bias"),
-        ln0w=f("conv.0.weight").reshape(-1), ln0b=f("conv.0.bias").reshape(-1),
-        c1w=kmajor(f("conv.2.weight")), c1b=f("conv.2.bias"),
-        ln1w=f("conv.3.weight").reshape(-1), ln1b=f("conv.3.bias").reshape(-1),
-        c2w=kmajor(f("conv.5.weight")), c2b=f("conv.5.bias"),
-        ln2w=f("conv.6.weight").reshape(-1), ln2b=f("conv.6.bias").reshape(-1),
-        c3w=kmajor(f("conv.8.weight")), c3b=f("conv.8.bias"),
-        ln3w=f("conv.9.weight").reshape(-1), ln3b=f("conv.9.bias").reshape(-1),
-        s0wt=f("shared.0.weight").t().contiguous(), s0b=f("shared.0.bias"),
+        view_perm=torch.tensor([view_perm(p, n_players, c) for p in range(n_players)],
+                               dtype=torch.int32).reshape(-1),
+        c0w=_pack_conv(f("conv0.weight"), 1), c0b=f("conv0.bias"),
+        ln0w=_pack_ln(f("conv.0.weight"), 1), ln0b=_pack_ln(f("conv.0.bias"), 1),
+        c1w=_pack_conv(f("conv.2.weight"), 2), c1b=f("conv.2.bias"),
+        ln1w=_pack_ln(f("conv.3.weight"), 2), ln1b=_pack_ln(f("conv.3.bias"), 2),
+        c2w=_pack_conv(f("conv.5.weight"), 4), c2b=f("conv.5.bias"),
+        ln2w=_pack_ln(f("conv.6.weight"), 4), ln2b=_pack_ln(f("conv.6.bias"), 4),
+        c3w=_pack_conv(f("conv.8.weight"), 1), c3b=c3b,
+        ln3w=_pack_ln(f("conv.9.weight"), 1), ln3b=_pack_ln(f("conv.9.bias"), 1),
+        s0p=_pack_linear(f("shared.0.weight")), s0b=f("shared.0.bias"),
         s1w=f("shared.1.weight"), s1b=f("shared.1.bias"),
-        s3wt=f("shared.3.weight").t().contiguous(), s3b=f("shared.3.bias"),
+        s3p=_pack_linear(f("shared.3.weight")), s3b=f("shared.3.bias"),
         s4w=f("shared.4.weight"), s4b=f("shared.4.bias"),
-        hwt=torch.cat([f(f"{n}.0.weight") for n in heads]).t().contiguous(),
+        hp=_pack_linear(torch.cat([f(f"{n}.0.weight") for n in heads])),
         hb=torch.cat([f(f"{n}.0.bias") for n in heads]),
-        fw=fw.contiguous(), fb=torch.cat([f(f"{n}.2.bias") for n in heads]))
-    expect = dict(c1w=(144, 32), c2w=(288, 64), c3w=(64, 8), s0wt=(8 * h * w, HID),
-                  s3wt=(HID, HID), hwt=(HID, 3 * HEAD))
-    for k, shp in expect.items():
-        if tuple(out[k].shape) != shp:
-            raise ValueError(f"{k} packs to {tuple(out[k].shape)}, expected {shp}")
+        fw=fw, fb=torch.cat([f(f"{n}.2.bias") for n in heads]))
+    expect = dict(c0w=36 * 64, c1w=2 * 36 * 64, c2w=4 * 72 * 64, c3w=16 * 64,
+                  s0p=8 * 338 * 64, s3p=8 * 32 * 64, hp=12 * 32 * 64, ln2w=4 * 11 * 64 * 4)
+    for k, numel in expect.items():
+        if out[k].numel() != numel:
+            raise ValueError(f"{k} packs to {out[k].numel()} values, expected {numel}")
     return {k: v.contiguous() for k, v in out.items()}
 
 

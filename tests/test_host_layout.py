@@ -152,45 +152,69 @@ def test_map_spec_validation(kw):
         MapSpec(**kw)
 
 
-def test_pack_cnn_kmajor_convs_equal_conv2d():
-    """The cnn kernel's implicit GEMM on the packed weights (A[p][k] = the
-    zero-padded input plane ci at position p shifted by tap k % 9, k = ci * 9
-    + 3 dy + dx; B = the packed [k][out] matrix) equals F.conv2d with the
-    reference's weights, conv0 through each player's view permutation; the
-    1x1 conv reads the centre tap."""
+def test_pack_cnn_operands_reproduce_the_reference_layers():
+    """The cnn kernel's operand addressing over the packed tensors reproduces
+    the reference's layers: for each conv, A[p][k] read from zero-bordered
+    15 x 15 planes at the kernel's offsets (step j: plane 4 (j // 9) + kq,
+    tap j % 9; 1x1: plane 4 j + kq, centre) times B[k][n] = packed[tile][j]
+    [kq * 16 + n % 16] equals F.conv2d, conv0 on the planes permuted by the
+    view table; the Linear packing gives W[n][4 j + kq]; the LayerNorm tables
+    give gamma[n][16 mt + 4 kq + q]."""
     import torch.nn.functional as F
 
-    from qqtsim.config import view_perm
     from qqtsim.policy import default_init_cnn, pack_cnn
 
     params = default_init_cnn(seed=3)
     pk = pack_cnn(params)
     g = torch.Generator().manual_seed(0)
 
-    def implicit_gemm(x, wk, bias, ks):
-        cin = x.shape[0]
-        xp = F.pad(x, (1, 1, 1, 1))
-        cols = []
-        for ci in range(cin):
-            for t in range(ks * ks):
-                dy, dx = (t // 3, t % 3) if ks == 3 else (1, 1)
-                cols.append(xp[ci, dy:dy + 13, dx:dx + 13].reshape(-1))
-        a = torch.stack(cols, 1)                       # [169][K]
-        return (a.double() @ wk.double() + bias.double()).t().reshape(-1, 13, 13)
+    def kernel_conv(planes, packed, bias, n_tiles, steps, k1):
+        cin_p = planes.shape[0]
+        flat = F.pad(planes, (1, 1, 1, 1)).reshape(cin_p, 225)
+        b = packed.double().view(n_tiles, steps, 4, 16)        # [tile][j][kq][i16]
+        out = torch.zeros((n_tiles * 16, 169), dtype=torch.float64)
+        pos = torch.arange(169)
+        pbase = (pos // 13) * 15 + pos % 13
+        for j in range(steps):
+            for kq in range(4):
+                if k1:
+                    ci, off = 4 * j + kq, 16
+                else:
+                    ci, tap = 4 * (j // 9) + kq, j % 9
+                    off = (tap // 3) * 15 + tap % 3
+                if ci >= cin_p:
+                    assert float(b[:, j, kq].abs().max()) == 0.0
+                    continue
+                a = flat[ci, pbase + off]                        # [169]
+                out += b[:, j, kq].reshape(-1)[:, None] * a[None, :]
+        return out.view(-1, 13, 13)[: bias.numel()] + bias.double()[:, None, None]
 
     x = torch.rand((14, 13, 13), generator=g, dtype=torch.float64)
+    vp = pk["view_perm"].view(2, 14)
     for pid in range(2):
-        inv = torch.argsort(torch.tensor(view_perm(pid, 2, 14)))
+        inv = torch.argsort(vp[pid].long())
         want = F.conv2d(x[None], params["conv0.weight"].double()[:, inv],
                         params["conv0.bias"].double(), padding=1)[0]
-        got = implicit_gemm(x, pk["c0w"].view(2, 126, 16)[pid], pk["c0b"], 3)
+        planes = torch.zeros((16, 13, 13), dtype=torch.float64)
+        planes[:14] = x[vp[pid].long()]
+        got = kernel_conv(planes, pk["c0w"], pk["c0b"], 1, 36, False)
         torch.testing.assert_close(got, want, rtol=1e-12, atol=1e-12)
-    for key, wk, bk, cin, ks in (("conv.2", "c1w", "c1b", 16, 3), ("conv.5", "c2w", "c2b", 32, 3),
-                                 ("conv.8", "c3w", "c3b", 64, 1)):
+    for key, wk, bk, cin, nt, steps, k1 in (("conv.2", "c1w", "c1b", 16, 2, 36, False),
+                                            ("conv.5", "c2w", "c2b", 32, 4, 72, False),
+                                            ("conv.8", "c3w", "c3b", 64, 1, 16, True)):
         x = torch.rand((cin, 13, 13), generator=g, dtype=torch.float64)
-        want = F.conv2d(x[None], params[f"{key}.weight"].double(), params[f"{key}.bias"].double(),
-                        padding=ks // 2)[0]
-        torch.testing.assert_close(implicit_gemm(x, pk[wk], pk[bk], ks), want, rtol=1e-12, atol=1e-12)
-    assert pk["s0wt"].shape == (1352, 128) and torch.equal(pk["s0wt"].t(), params["shared.0.weight"])
+        w = params[f"{key}.weight"].double()
+        want = F.conv2d(x[None], w, params[f"{key}.bias"].double(), padding=w.shape[-1] // 2)[0]
+        got = kernel_conv(x, pk[wk], pk[bk][: w.shape[0]], nt, steps, k1)
+        torch.testing.assert_close(got, want, rtol=1e-12, atol=1e-12)
+    for key, pkey, n, k in (("shared.0.weight", "s0p", 128, 1352),
+                            ("shared.3.weight", "s3p", 128, 128)):
+        p = pk[pkey].view(n // 16, k // 4, 4, 16)                 # [tile][j][kq][i16]
+        dense = p.permute(0, 3, 1, 2).reshape(n, k)
+        assert torch.equal(dense, params[key])
+    ln = pk["ln2w"].view(4, 11, 4, 16, 4)                        # [tile][mt][kq][i16][q]
+    gam = params["conv.6.weight"].reshape(64, 169)
+    assert float(ln[1, 3, 2, 5, 1]) == float(gam[16 + 5, 16 * 3 + 4 * 2 + 1])
+    assert float(ln[0, 10, 3, 0, 3]) == 0.0                      # position 175 >= 169
     assert torch.equal(pk["fw"][5:7], params["bomb_head.2.weight"])
     assert sum(v.numel() for v in params.values()) == 281744
