@@ -70,7 +70,7 @@ struct __align__(16) Lds {
   float plane[64 * PL];
   float flat[SB * FS];                      // trunk outputs; head scratch after GEMM 1
   float wc0[S0 * 64], wc3[S3 * 64];         // conv0 / conv1x1 B operands (shared by all waves)
-  float red[NW];
+  float red[2][NW];
 };
 // head scratch inside flat (free once Linear(1352,128) has read it)
 constexpr int H_OFF = 0, H2_OFF = SB * HS, HY_OFF = 2 * SB * HS, LG_OFF = 2 * SB * HS + SB * HYS;
@@ -80,15 +80,18 @@ __device__ __forceinline__ floatx4 mfma(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float block_sum(float v, float* red) {
+// Workgroup sum through red[slot][wave]: one barrier.  Consecutive calls
+// alternate slots, so a slot is rewritten only after a later barrier has
+// ordered every read of it.
+__device__ __forceinline__ float block_sum(float v, float (*red)[NW], int& slot) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  if ((threadIdx.x & 63) == 0) red[slot][threadIdx.x >> 6] = v;
   __syncthreads();
   float s = 0.0f;
 #pragma unroll
-  for (int i = 0; i < NW; ++i) s += red[i];
-  __syncthreads();
+  for (int i = 0; i < NW; ++i) s += red[slot][i];
+  slot ^= 1;
   return s;
 }
 
@@ -142,8 +145,8 @@ __device__ __forceinline__ void conv_lds(const float* plane, const float* wl, fl
 // LayerNorm statistics over the valid outputs of a layer (n < cout, p < 169).
 template <int NTL>
 __device__ __forceinline__ void ln_stats(const floatx4 (&acc)[NTL], int mt0, int ms,
-                                         bool nvalid, float* red, float inv_count,
-                                         float& mean, float& rstd) {
+                                         bool nvalid, float (*red)[NW], int& slot,
+                                         float inv_count, float& mean, float& rstd) {
   const int kq = (threadIdx.x & 63) >> 4;
   float s = 0.0f;
 #pragma unroll
@@ -153,7 +156,7 @@ __device__ __forceinline__ void ln_stats(const floatx4 (&acc)[NTL], int mt0, int
       for (int q = 0; q < 4; ++q)
         if (16 * (mt0 + t * ms) + 4 * kq + q < NP) s += acc[t][q];
     }
-  mean = block_sum(s, red) * inv_count;
+  mean = block_sum(s, red, slot) * inv_count;
   float v = 0.0f;
 #pragma unroll
   for (int t = 0; t < NTL; ++t)
@@ -165,7 +168,7 @@ __device__ __forceinline__ void ln_stats(const floatx4 (&acc)[NTL], int mt0, int
           v += d * d;
         }
     }
-  rstd = 1.0f / sqrtf(block_sum(v, red) * inv_count + 1e-5f);
+  rstd = 1.0f / sqrtf(block_sum(v, red, slot) * inv_count + 1e-5f);
 }
 
 // relu(LN affine) of this wavefront's outputs: into the padded planes, or
@@ -281,6 +284,7 @@ __global__ __launch_bounds__(T, 1) void cnn_act_kernel(const qqt_cnn_args a, int
   for (int i = t; i < S0 * 64; i += T) s.wc0[i] = a.c0w[i];
   for (int i = t; i < S3 * 64; i += T) s.wc3[i] = a.c3w[i];
 
+  int rslot = 0;                                   // reduction slot
   const int start = blockIdx.x * per, end = min(items, start + per);
   for (int ib = start; ib < end; ib += SB) {
     const int nb = min(SB, end - ib);
@@ -302,21 +306,21 @@ __global__ __launch_bounds__(T, 1) void cnn_act_kernel(const qqt_cnn_args a, int
       {
         floatx4 acc[3];
         conv_lds<S0, 3, false>(s.plane, s.wc0, bias0, w, 4, acc);
-        ln_stats<3>(acc, w, 4, true, s.red, 1.0f / (16 * NP), mean, rstd);
+        ln_stats<3>(acc, w, 4, true, s.red, rslot, 1.0f / (16 * NP), mean, rstd);
         ln_write<3>(acc, w, 4, 0, true, mean, rstd, a.ln0w, a.ln0b, s.plane, nullptr);
       }
       __syncthreads();
       {
         floatx4 acc[6];
         conv<S1, 6, false>(s.plane, b1, bias1, mt1, 2, acc);
-        ln_stats<6>(acc, mt1, 2, true, s.red, 1.0f / (32 * NP), mean, rstd);
+        ln_stats<6>(acc, mt1, 2, true, s.red, rslot, 1.0f / (32 * NP), mean, rstd);
         ln_write<6>(acc, mt1, 2, n1, true, mean, rstd, a.ln1w, a.ln1b, s.plane, nullptr);
       }
       __syncthreads();
       {
         floatx4 acc[MT];
         conv<S2, MT, false>(s.plane, b2, bias2, 0, 1, acc);
-        ln_stats<MT>(acc, 0, 1, true, s.red, 1.0f / (64 * NP), mean, rstd);
+        ln_stats<MT>(acc, 0, 1, true, s.red, rslot, 1.0f / (64 * NP), mean, rstd);
         ln_write<MT>(acc, 0, 1, n2, true, mean, rstd, a.ln2w, a.ln2b, s.plane, nullptr);
       }
       __syncthreads();
@@ -324,7 +328,7 @@ __global__ __launch_bounds__(T, 1) void cnn_act_kernel(const qqt_cnn_args a, int
         floatx4 acc[3];
         conv_lds<S3, 3, true>(s.plane, s.wc3, bias3, w, 4, acc);
         const bool nv = i16 < 8;
-        ln_stats<3>(acc, w, 4, nv, s.red, 1.0f / (8 * NP), mean, rstd);
+        ln_stats<3>(acc, w, 4, nv, s.red, rslot, 1.0f / (8 * NP), mean, rstd);
         ln_write<3>(acc, w, 4, 0, nv, mean, rstd, a.ln3w, a.ln3b, s.plane, s.flat + ii * FS);
       }
     }
