@@ -181,3 +181,63 @@ def test_cnn_rollout_self_play(dev):
         assert torch.equal(a.logp, lp) and torch.equal(a.value, v), t
         b_sim.step(want)
         assert torch.equal(a_sim.observe(), b_sim.observe()), t
+
+
+def test_cnn_ragged_batches_are_row_independent(dev):
+    """The persistent kernel splits items over workgroups and batches of 16 by
+    the launch size; each item's outputs must not depend on that split.
+    Forwards over ragged slices (1 to 4099 rows, both players and one) equal
+    the same rows of one large launch bit for bit, and the small ones match
+    the oracle."""
+    from oracle.policy import cnn_forward
+    from qqtsim.policy import HipCnnActorCritic, default_init_cnn
+
+    params = default_init_cnn(seed=4)
+    net = HipCnnActorCritic(params, device=dev)
+    z = traj("pillars70")
+    base = torch.from_numpy(z["obs"].reshape(-1, 14, 13, 13).copy())
+    obs = base.repeat((5000 + base.shape[0] - 1) // base.shape[0], 1, 1, 1)[:5000].to(dev)
+    b = obs.shape[0]
+    ones_m = torch.ones((b, 2, 5), dtype=torch.bool, device=dev)
+    ones_b = torch.ones((b, 2, 2), dtype=torch.bool, device=dev)
+    _, _, _, full = net.act_pair(obs, ones_m, ones_b, logits=True)
+    start = 0
+    for n in (1, 5, 17, 33, 100, 255, 4099):
+        sl = slice(start, start + n)
+        _, _, _, lg = net.act_pair(obs[sl], ones_m[sl], ones_b[sl], logits=True)
+        assert torch.equal(lg, full[sl]), n
+        for pid in range(2):
+            ml, bl, v = net.forward(obs[sl], pid)
+            assert torch.equal(torch.cat([ml, bl, v[:, None]], 1), full[sl, pid]), (n, pid)
+        if n <= 33:
+            for pid in range(2):
+                ml, bl, v = cnn_forward(params, obs[sl].cpu(), pid, dtype=torch.float64)
+                ref = torch.cat([ml, bl, v[:, None]], 1)
+                assert float((full[sl, pid].cpu().double() - ref).abs().max()) <= LOGIT_ATOL
+        start = (start + n) % (b - 4100)
+
+
+def test_cnn_learner_vs_astar_rollout(dev):
+    """The cnn policy as the learner (player 0) against the astar bot: the
+    rollout's player-0 actions equal act(pid=0) on the same observation,
+    masks and Philox tick, and player 1's slot is the bot's."""
+    from qqtsim import HipAstarBot, HipBatchedSim, MapSpec, Rollout, corridor_training_config
+    from qqtsim.policy import HipCnnActorCritic, default_init_cnn
+
+    n, T, seed = 96, 5, 13
+    cfg = corridor_training_config()
+    spec = MapSpec(kind="pillars", brick_p=0.5, swap_spawns=True)
+    params = default_init_cnn(cfg.obs_shape, seed=5)
+    sim = HipBatchedSim(cfg, n, device=dev, seed=seed, map_spec=spec)
+    net = HipCnnActorCritic(params, device=dev, seed=seed)
+    bot = HipAstarBot(sim, pid=1)
+    roll = Rollout(sim, net, opponent=bot)
+    ref_net = HipCnnActorCritic(params, device=dev, seed=seed)
+    for t in range(T):
+        obs = sim.observe().clone()
+        mm, bm = (m.clone() for m in sim.legal_mask())
+        want, lp, v = ref_net.act(obs, mm[:, 0], bm[:, 0], 0)
+        roll.launch_act()
+        assert torch.equal(roll.actions[:, 0].long(), want), t
+        assert torch.equal(roll.logp[:, 0], lp) and torch.equal(roll.value[:, 0], v), t
+        roll.launch_tick()
