@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 10
+#define QQT_ABI_VERSION 11
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -320,11 +320,15 @@ int qqt_ppo_grad(const qqt_ppo_args* args, void* stream);
  * arch "cnn" (:167-196, 230-245) as qqt_mlp_act does for the MLP: the same
  * masks, uniforms and output layout.  Every LayerNorm normalises one sample
  * over all of its values (eps 1e-5) with an elementwise affine of that shape.
- * Weights are float32 in the kernel's operand order ("packed" below: index
- * [tile][step][lane], lane l holding output 16 tile + l % 16 and input
- * 4 step + l / 16 of the K order); a 3x3 conv's K order is, for channel
- * blocks cb of 4 (inputs padded to a multiple of 4 with zero weights) and
- * taps t = 3 dy + dx, step 9 cb + t = channels 4 cb .. 4 cb + 3 at tap t.
+ * Weights come in the kernel's operand order.  Conv weights are float16
+ * hi / lo planes (w = hi + lo), index [tile][step][lane][8]: lane l holds
+ * output 16 tile + l % 16 and 8 consecutive input channels at one tap, the
+ * block of lane group g = l / 16: for 16 input channels (conv0 padded from
+ * 14 with zero weights, and conv 16->32) combination c = 4 step + g, tap
+ * c / 2 (taps 3 dy + dx; combinations 18, 19 are zero), channels 8 (c % 2)..;
+ * for 32 input channels tap = step, channels 8 g..; for the 1x1 conv
+ * channels 8 (4 step + g)...  Linear weights are float32 [tile][step][lane],
+ * lane l holding output 16 tile + l % 16, input 4 step + l / 16.
  * LayerNorm tables are packed [tile][11 position tiles][lane][4] (value q of
  * lane l: channel 16 tile + l % 16, position 16 ptile + 4 (l / 16) + q;
  * zero past 169 positions or the channel count), 16-byte aligned. */
@@ -346,11 +350,14 @@ typedef struct qqt_cnn_args {
   const int32_t* view_perm;   /* [w_players][14]: conv0 input channel j of player p is
                                  observation channel view_perm[p][j] (the reference's
                                  conv0.weight[:, argsort(view_perm)] on the stored obs) */
-  const float *c0w, *c0b, *ln0w, *ln0b;   /* conv0 packed [1][36][64]; [16]; LN [1][11][64][4] */
-  const float *c1w, *c1b, *ln1w, *ln1b;   /* packed [2][36][64]; [32]; LN [2][11][64][4] */
-  const float *c2w, *c2b, *ln2w, *ln2b;   /* packed [4][72][64]; [64]; LN [4][11][64][4] */
-  const float *c3w, *c3b, *ln3w, *ln3b;   /* 1x1: packed [1][16][64] (outputs 8..15 zero);
-                                             [16] (8..15 zero); LN [1][11][64][4] */
+  const uint16_t *c0w, *c0w_lo;           /* conv0 [1][5][64][8] */
+  const float *c0b, *ln0w, *ln0b;         /* [16]; LN [1][11][64][4] */
+  const uint16_t *c1w, *c1w_lo;           /* conv 16->32 [2][5][64][8] */
+  const float *c1b, *ln1w, *ln1b;         /* [32]; LN [2][11][64][4] */
+  const uint16_t *c2w, *c2w_lo;           /* conv 32->64 [4][9][64][8] */
+  const float *c2b, *ln2w, *ln2b;         /* [64]; LN [4][11][64][4] */
+  const uint16_t *c3w, *c3w_lo;           /* 1x1 64->8 [1][2][64][8] (outputs 8..15 zero) */
+  const float *c3b, *ln3w, *ln3b;         /* [16] (8..15 zero); LN [1][11][64][4] */
   const float *s0p, *s0b;     /* Linear(1352,128) packed [8][338][64] (input index
                                  c * 169 + p of the flattened [8][13][13]); [128] */
   const float *s1w, *s1b;     /* LayerNorm(128) */

@@ -10,33 +10,36 @@
 // sample over all of its values (eps 1e-5) with an elementwise affine.
 //
 // Persistent kernel: one workgroup (4 wavefronts, one per SIMD, so each
-// wavefront may hold 512 registers) per CU walks a contiguous
-// range of items (row, player).  All arithmetic is float32; every product
-// with weights runs on v_mfma_f32_16x16x4_f32 (A[i][k]: lane l holds row
-// l % 16, k = l / 16; B[k][j]: lane l holds k = l / 16, column l % 16;
-// D[i][j]: lane l holds rows 4 (l / 16) + q, column l % 16).
+// wavefront may hold 512 registers) per CU walks a contiguous range of items
+// (row, player).
 //
-// Trunk, one item at a time, feature maps in LDS as zero-bordered 15 x 15
-// planes (row stride 15, plane stride PL):
-//   * convolutions are implicit GEMMs with M = positions (11 tiles of 16),
-//     N = output channels, K in steps of 4 channels: step j covers channels
-//     4 (j / 9) + l / 16 at tap j % 9 (1x1: channels 4 j + l / 16), so lane
-//     l's A address is a per-lane base (its channel and position) plus a
-//     per-step constant, the immediate offset of a ds_read_b32;
-//   * the B operands of the two wide convolutions stay in registers for the
-//     whole kernel (wavefront w owns output tile w % NT of each, 108
-//     registers), those of conv0 and the 1x1 conv (one output tile, shared
-//     by all wavefronts) in LDS; all are packed on the host as
-//     [tile][step][lane]; the K loop is step-outer, tile-inner, so one
-//     step's A loads feed independent accumulators;
-//   * the accumulators of a layer are its output: the LayerNorm reduces them
-//     across the workgroup (mean, then squared deviations), and the
-//     normalised, rectified values are written over the input planes (after
-//     the last conv, into this item's row of the flat buffer).
-// Head, per batch of up to 16 items: Linear(1352,128), Linear(128,128) and
-// the heads' hidden layer are MFMA GEMMs with M = the 16 items (B streamed
-// from L2 once per batch), LayerNorm(128) by 16 threads per item, then the
-// output layer and the masked sampling per item.
+// Trunk, one item at a time.  Feature maps live in LDS as zero-bordered
+// 15 x 15 grids of positions with the channels of a position contiguous
+// (72 halves per position), as float16 hi and lo planes (x = hi + lo).
+// Convolutions are implicit GEMMs on v_mfma_f32_16x16x32_f16 with float32
+// accumulation: M = positions (11 tiles of 16), N = output channels, K in
+// steps of 32 = four 8-channel blocks, so lane l's A operand (8 halves) is
+// one 16-byte LDS read of 8 channels at one position and tap:
+//   16 input channels (conv0, conv 16->32): step s, lane group g = l / 16
+//     takes combination c = 4 s + g: tap min(c / 2, 8), channels 8 (c % 2)..;
+//     combinations 18, 19 carry zero weights;
+//   32 input channels (conv 32->64): step s = tap, channels 8 g..;
+//   64 input channels (1x1): step s, channels 8 (4 s + g)...
+// Each product is hi*hi + hi*lo + lo*hi of the activation and weight
+// planes (the observation is exact in float16, so conv0 skips its lo
+// plane), which keeps the layer outputs within ~1e-6 relative of float32.
+// The B operands of the 16->32 and 32->64 convs stay in registers for the
+// whole kernel (wavefront w owns output tile w % NT of each); those of conv0
+// and the 1x1 conv (one output tile, used by every wavefront) sit in LDS; all
+// are packed on the host as [tile][step][lane][8] halves.  The accumulators
+// are the layer's output: the per-sample LayerNorm reduces them across the
+// workgroup (mean, then squared deviations) and the rectified, normalised
+// values are written over the input planes as hi/lo halves (after the last
+// conv, into this item's row of the float32 flat buffer).
+// Head, per batch of up to 15 items: Linear(1352,128), Linear(128,128) and
+// the heads' hidden layer are v_mfma_f32_16x16x4_f32 GEMMs with M = the items
+// (B streamed from L2 once per batch), LayerNorm(128) by 16 threads per item,
+// then the output layer and the masked sampling per item.
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -54,27 +57,31 @@ extern thread_local char g_err[512];
 namespace cnn {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 
 constexpr int T = 256, NW = 4;
 constexpr int HW = 13, NP = 169, MT = 11;
-constexpr int PL = 240;                     // plane stride (15 x 15 = 225 used); 16 mod 32 banks
+constexpr int PP = 225;                     // padded positions (15 x 15)
+constexpr int CS = 72;                      // halves per position (64 channels + 8: bank spread)
 constexpr int C0 = 14;
-constexpr int SB = 16;                      // items per head batch
+constexpr int SB = 15;                      // items per head batch (<= the 16 MFMA rows)
 constexpr int FLAT = 8 * NP;                // 1352
 constexpr int FS = 1378;                    // flat row stride (2 mod 32 banks)
 constexpr int HID = 128, HS = 130, HYS = 194;
-constexpr int S0 = 36, S1 = 36, S2 = 72, S3 = 16;   // K steps of the four convolutions
+constexpr int S0 = 5, S1 = 5, S2 = 9, S3 = 2;       // 32-deep K steps of the four convolutions
 constexpr int L0 = FLAT / 4, L1 = HID / 4;          // K steps of the head GEMMs
+constexpr int BFRAG = 64 * 8;                       // halves of one step's B fragments
 
-struct __align__(16) Lds {
-  float plane[64 * PL];
+struct __align__(16) Lds {                 // every member a multiple of 16 bytes long
+  uint16_t act[2][PP * CS];                 // hi, lo planes [position][channel]
+  uint16_t wc0[2][S0 * BFRAG], wc3[2][S3 * BFRAG];   // conv0 / 1x1 B (hi, lo), all waves
   float flat[SB * FS];                      // trunk outputs; head scratch after GEMM 1
-  float wc0[S0 * 64], wc3[S3 * 64];         // conv0 / conv1x1 B operands (shared by all waves)
   float red[2][NW];
 };
+static_assert(sizeof(uint16_t) * 2 * PP * CS % 16 == 0, "16-byte fragment reads stay aligned");
 // head scratch inside flat (free once Linear(1352,128) has read it)
 constexpr int H_OFF = 0, H2_OFF = SB * HS, HY_OFF = 2 * SB * HS, LG_OFF = 2 * SB * HS + SB * HYS;
-static_assert(LG_OFF + SB * 8 <= SB * FS, "head scratch fits in the flat buffer");
+static_assert(LG_OFF + 16 * 8 <= SB * FS, "head scratch (16 rows) fits in the flat buffer");
 
 __device__ __forceinline__ floatx4 mfma(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -95,50 +102,53 @@ __device__ __forceinline__ float block_sum(float v, float (*red)[NW], int& slot)
   return s;
 }
 
-// LDS offset of step j's A element relative to the lane base.
-template <bool K1>
-__device__ __forceinline__ constexpr int step_off(int j) {
-  return K1 ? 4 * j * PL + 16 : 4 * (j / 9) * PL + ((j % 9) / 3) * 15 + (j % 9) % 3;
+__device__ __forceinline__ half8 ld8(const uint16_t* p) {
+  union { uint4 u; half8 h; } c;
+  c.u = *reinterpret_cast<const uint4*>(p);
+  return c.h;
 }
+__device__ __forceinline__ floatx4 mfma16(half8 a, half8 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+struct BFrag { half8 hi, lo; };
 
-// One conv layer for this wavefront: position tiles min(mt0 + t ms, 10),
-// t < NTL (duplicates of tile 10 are computed and later ignored);
-// acc[t] = bias + sum_j A B[j].
-template <int STEPS, int NTL, bool K1>
-__device__ __forceinline__ void conv(const float* plane, const float (&b)[STEPS], float bias,
-                                     int mt0, int ms, floatx4 (&acc)[NTL]) {
+__device__ __forceinline__ constexpr int tap_off(int tap) { return (tap / 3) * 15 + tap % 3; }
+
+// One conv layer for this wavefront (KIND 0: 3x3 over 16 channels, 1: 3x3
+// over 32, 2: 1x1 over 64): position tiles min(mt0 + t ms, 10), t < NTL
+// (duplicates of tile 10 are computed and later ignored); acc[t] = bias +
+// sum over steps of A B, three float16 products per step (two without the
+// activations' lo plane).  bfrag(s) returns step s's B fragments.
+template <int KIND, int STEPS, int NTL, bool ALO, class BF>
+__device__ __forceinline__ void conv(const uint16_t* act_hi, const uint16_t* act_lo, BF bfrag,
+                                     float bias, int mt0, int ms, floatx4 (&acc)[NTL]) {
   const int lane = threadIdx.x & 63, i16 = lane & 15, kq = lane >> 4;
-  const float* base[NTL];
+  int base[NTL];
 #pragma unroll
   for (int t = 0; t < NTL; ++t) {
     const int p = min(16 * min(mt0 + t * ms, MT - 1) + i16, NP - 1);
-    base[t] = plane + kq * PL + (p / HW) * 15 + (p % HW);
+    const int pb = (p / HW) * 15 + (p % HW);          // padded position of tap (0, 0)
+    base[t] = KIND == 0 ? pb * CS + 8 * (kq & 1) : KIND == 1 ? pb * CS + 8 * kq
+                        : (pb + 16) * CS + 8 * kq;
     acc[t] = floatx4{bias, bias, bias, bias};
   }
 #pragma unroll
-  for (int j = 0; j < STEPS; ++j) {
+  for (int st = 0; st < STEPS; ++st) {
+    int off;
+    if constexpr (KIND == 0)
+      off = ((kq >> 1) ? tap_off(min(2 * st + 1, 8)) : tap_off(min(2 * st, 8))) * CS;
+    else if constexpr (KIND == 1)
+      off = tap_off(st) * CS;
+    else
+      off = 32 * st;
+    const BFrag b = bfrag(st);
 #pragma unroll
-    for (int t = 0; t < NTL; ++t) acc[t] = mfma(base[t][step_off<K1>(j)], b[j], acc[t]);
-  }
-}
-
-// As conv, with B read from LDS (packed [step][lane]).
-template <int STEPS, int NTL, bool K1>
-__device__ __forceinline__ void conv_lds(const float* plane, const float* wl, float bias,
-                                         int mt0, int ms, floatx4 (&acc)[NTL]) {
-  const int lane = threadIdx.x & 63, i16 = lane & 15, kq = lane >> 4;
-  const float* base[NTL];
-#pragma unroll
-  for (int t = 0; t < NTL; ++t) {
-    const int p = min(16 * min(mt0 + t * ms, MT - 1) + i16, NP - 1);
-    base[t] = plane + kq * PL + (p / HW) * 15 + (p % HW);
-    acc[t] = floatx4{bias, bias, bias, bias};
-  }
-#pragma unroll
-  for (int j = 0; j < STEPS; ++j) {
-    const float bv = wl[j * 64 + lane];
-#pragma unroll
-    for (int t = 0; t < NTL; ++t) acc[t] = mfma(base[t][step_off<K1>(j)], bv, acc[t]);
+    for (int t = 0; t < NTL; ++t) {
+      const half8 ah = ld8(act_hi + base[t] + off);
+      acc[t] = mfma16(ah, b.hi, acc[t]);
+      acc[t] = mfma16(ah, b.lo, acc[t]);
+      if constexpr (ALO) acc[t] = mfma16(ld8(act_lo + base[t] + off), b.hi, acc[t]);
+    }
   }
 }
 
@@ -171,13 +181,14 @@ __device__ __forceinline__ void ln_stats(const floatx4 (&acc)[NTL], int mt0, int
   rstd = 1.0f / sqrtf(block_sum(v, red, slot) * inv_count + 1e-5f);
 }
 
-// relu(LN affine) of this wavefront's outputs: into the padded planes, or
-// (flat != nullptr) into flat[n * 169 + p].  g / bt: [NT][11][64][4] packed.
+// relu(LN affine) of this wavefront's outputs: into the hi/lo activation
+// planes, or (flat != nullptr) into flat[n * 169 + p].  g / bt: [NT][11][64][4]
+// packed.
 template <int NTL>
 __device__ __forceinline__ void ln_write(const floatx4 (&acc)[NTL], int mt0, int ms, int ntile,
                                          bool nvalid, float mean, float rstd,
                                          const float* __restrict__ g, const float* __restrict__ bt,
-                                         float* plane, float* flat) {
+                                         uint16_t* act_hi, uint16_t* act_lo, float* flat) {
   const int lane = threadIdx.x & 63, i16 = lane & 15, kq = lane >> 4;
   const int n = 16 * ntile + i16;
 #pragma unroll
@@ -193,8 +204,14 @@ __device__ __forceinline__ void ln_write(const floatx4 (&acc)[NTL], int mt0, int
         const int p = 16 * mt + 4 * kq + q;
         if (p < NP) {
           const float y = fmaxf((acc[t][q] - mean) * rstd * gv[q] + bv[q], 0.0f);
-          if (flat) flat[n * NP + p] = y;
-          else plane[n * PL + (p / HW + 1) * 15 + (p % HW) + 1] = y;
+          if (flat) {
+            flat[n * NP + p] = y;
+          } else {
+            const int i = ((p / HW + 1) * 15 + (p % HW) + 1) * CS + n;
+            const __half h = __float2half_rn(y);
+            act_hi[i] = __half_as_ushort(h);
+            act_lo[i] = __half_as_ushort(__float2half_rn(y - __half2float(h)));
+          }
         }
       }
     }
@@ -206,7 +223,7 @@ template <int STEPS, int NTW>
 __device__ __forceinline__ void head_gemm(const float* A, int as, const float* __restrict__ w,
                                           int nt0, floatx4 (&c)[NTW]) {
   const int lane = threadIdx.x & 63, i16 = lane & 15, kq = lane >> 4;
-  const float* a = A + i16 * as + kq;
+  const float* a = A + min(i16, SB - 1) * as + kq;   // rows past the batch repeat its last
   const float* b = w + (size_t)nt0 * STEPS * 64 + lane;
 #pragma unroll
   for (int i = 0; i < NTW; ++i) c[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -266,13 +283,21 @@ __global__ __launch_bounds__(T, 1) void cnn_act_kernel(const qqt_cnn_args a, int
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int lane = t & 63, i16 = lane & 15;
 
-  // conv B operands, resident for the whole kernel
-  float b1[S1], b2[S2];
+  // B operands of the 16->32 and 32->64 convs, resident for the whole kernel
+  half8 b1h[S1], b1l[S1], b2h[S2], b2l[S2];
   const int n1 = w & 1, n2 = w;
 #pragma unroll
-  for (int j = 0; j < S1; ++j) b1[j] = a.c1w[(n1 * S1 + j) * 64 + lane];
+  for (int j = 0; j < S1; ++j) {
+    const size_t o = ((size_t)(n1 * S1 + j) * 64 + lane) * 8;
+    b1h[j] = ld8(a.c1w + o);
+    b1l[j] = ld8(a.c1w_lo + o);
+  }
 #pragma unroll
-  for (int j = 0; j < S2; ++j) b2[j] = a.c2w[(n2 * S2 + j) * 64 + lane];
+  for (int j = 0; j < S2; ++j) {
+    const size_t o = ((size_t)(n2 * S2 + j) * 64 + lane) * 8;
+    b2h[j] = ld8(a.c2w + o);
+    b2l[j] = ld8(a.c2w_lo + o);
+  }
   const float bias0 = a.c0b[i16], bias1 = a.c1b[16 * n1 + i16], bias2 = a.c2b[16 * n2 + i16];
   const float bias3 = a.c3b[i16];
 
@@ -280,9 +305,23 @@ __global__ __launch_bounds__(T, 1) void cnn_act_kernel(const qqt_cnn_args a, int
   // {w/2 + 2i}, i < 6; conv2 all 11
   const int mt1 = w >> 1;
 
-  for (int i = t; i < 64 * PL; i += T) s.plane[i] = 0.0f;
-  for (int i = t; i < S0 * 64; i += T) s.wc0[i] = a.c0w[i];
-  for (int i = t; i < S3 * 64; i += T) s.wc3[i] = a.c3w[i];
+  for (int i = t; i < PP * CS; i += T) s.act[0][i] = s.act[1][i] = 0;
+  for (int i = t; i < S0 * BFRAG; i += T) {
+    s.wc0[0][i] = a.c0w[i];
+    s.wc0[1][i] = a.c0w_lo[i];
+  }
+  for (int i = t; i < S3 * BFRAG; i += T) {
+    s.wc3[0][i] = a.c3w[i];
+    s.wc3[1][i] = a.c3w_lo[i];
+  }
+  auto breg1 = [&](int j) { return BFrag{b1h[j], b1l[j]}; };
+  auto breg2 = [&](int j) { return BFrag{b2h[j], b2l[j]}; };
+  auto blds0 = [&](int j) {
+    return BFrag{ld8(s.wc0[0] + (j * 64 + lane) * 8), ld8(s.wc0[1] + (j * 64 + lane) * 8)};
+  };
+  auto blds3 = [&](int j) {
+    return BFrag{ld8(s.wc3[0] + (j * 64 + lane) * 8), ld8(s.wc3[1] + (j * 64 + lane) * 8)};
+  };
 
   int rslot = 0;                                   // reduction slot
   const int start = blockIdx.x * per, end = min(items, start + per);
@@ -292,44 +331,46 @@ __global__ __launch_bounds__(T, 1) void cnn_act_kernel(const qqt_cnn_args a, int
       const int item = ib + ii;
       const int row = item / a.npid, slot = item % a.npid;
       const int pid = a.npid == 2 ? slot : a.pid0;
-      __syncthreads();                                  // planes 0..13 free
+      __syncthreads();                                  // channels 0..13 free
       const uint16_t* ob = a.obs + (size_t)row * a.obs_stride;
       const int32_t* perm = a.view_perm + pid * C0;
-      for (int i = t; i < C0 * NP; i += T) {
+      for (int i = t; i < C0 * NP; i += T) {          // exact in float16: hi plane only
         const int c = i / NP, p = i - c * NP;
-        s.plane[c * PL + (p / HW + 1) * 15 + (p % HW) + 1] =
-            __half2float(__ushort_as_half(ob[perm[c] * NP + p]));
+        s.act[0][((p / HW + 1) * 15 + (p % HW) + 1) * CS + c] = ob[perm[c] * NP + p];
       }
       __syncthreads();
 
       float mean, rstd;
       {
         floatx4 acc[3];
-        conv_lds<S0, 3, false>(s.plane, s.wc0, bias0, w, 4, acc);
+        conv<0, S0, 3, false>(s.act[0], s.act[1], blds0, bias0, w, 4, acc);
         ln_stats<3>(acc, w, 4, true, s.red, rslot, 1.0f / (16 * NP), mean, rstd);
-        ln_write<3>(acc, w, 4, 0, true, mean, rstd, a.ln0w, a.ln0b, s.plane, nullptr);
+        ln_write<3>(acc, w, 4, 0, true, mean, rstd, a.ln0w, a.ln0b, s.act[0], s.act[1], nullptr);
       }
       __syncthreads();
       {
         floatx4 acc[6];
-        conv<S1, 6, false>(s.plane, b1, bias1, mt1, 2, acc);
+        conv<0, S1, 6, true>(s.act[0], s.act[1], breg1, bias1, mt1, 2, acc);
         ln_stats<6>(acc, mt1, 2, true, s.red, rslot, 1.0f / (32 * NP), mean, rstd);
-        ln_write<6>(acc, mt1, 2, n1, true, mean, rstd, a.ln1w, a.ln1b, s.plane, nullptr);
+        ln_write<6>(acc, mt1, 2, n1, true, mean, rstd, a.ln1w, a.ln1b, s.act[0], s.act[1],
+                    nullptr);
       }
       __syncthreads();
       {
         floatx4 acc[MT];
-        conv<S2, MT, false>(s.plane, b2, bias2, 0, 1, acc);
+        conv<1, S2, MT, true>(s.act[0], s.act[1], breg2, bias2, 0, 1, acc);
         ln_stats<MT>(acc, 0, 1, true, s.red, rslot, 1.0f / (64 * NP), mean, rstd);
-        ln_write<MT>(acc, 0, 1, n2, true, mean, rstd, a.ln2w, a.ln2b, s.plane, nullptr);
+        ln_write<MT>(acc, 0, 1, n2, true, mean, rstd, a.ln2w, a.ln2b, s.act[0], s.act[1],
+                     nullptr);
       }
       __syncthreads();
       {
         floatx4 acc[3];
-        conv_lds<S3, 3, true>(s.plane, s.wc3, bias3, w, 4, acc);
+        conv<2, S3, 3, true>(s.act[0], s.act[1], blds3, bias3, w, 4, acc);
         const bool nv = i16 < 8;
         ln_stats<3>(acc, w, 4, nv, s.red, rslot, 1.0f / (8 * NP), mean, rstd);
-        ln_write<3>(acc, w, 4, 0, nv, mean, rstd, a.ln3w, a.ln3b, s.plane, s.flat + ii * FS);
+        ln_write<3>(acc, w, 4, 0, nv, mean, rstd, a.ln3w, a.ln3b, s.act[0], s.act[1],
+                    s.flat + ii * FS);
       }
     }
     __syncthreads();
@@ -451,17 +492,20 @@ int qqt_cnn_act(const qqt_cnn_args* a, void* stream) {
   using namespace qqt;
   using namespace qqt::cnn;
   g_err[0] = 0;
-  if (!a || !a->obs || !a->view_perm || !a->c0w || !a->c0b || !a->ln0w || !a->ln0b ||
-      !a->c1w || !a->c1b || !a->ln1w || !a->ln1b || !a->c2w || !a->c2b || !a->ln2w ||
-      !a->ln2b || !a->c3w || !a->c3b || !a->ln3w || !a->ln3b || !a->s0p || !a->s0b ||
+  if (!a || !a->obs || !a->view_perm || !a->c0w || !a->c0w_lo || !a->c0b || !a->ln0w ||
+      !a->ln0b || !a->c1w || !a->c1w_lo || !a->c1b || !a->ln1w || !a->ln1b || !a->c2w ||
+      !a->c2w_lo || !a->c2b || !a->ln2w || !a->ln2b || !a->c3w || !a->c3w_lo || !a->c3b ||
+      !a->ln3w || !a->ln3b || !a->s0p || !a->s0b ||
       !a->s1w || !a->s1b || !a->s3p || !a->s3b || !a->s4w || !a->s4b || !a->hp || !a->hb ||
       !a->fw || !a->fb) {
     snprintf(g_err, sizeof(g_err), "qqt_cnn_act: null pointer argument");
     return QQT_E_ARG;
   }
   if (((uintptr_t)a->ln0w | (uintptr_t)a->ln0b | (uintptr_t)a->ln1w | (uintptr_t)a->ln1b |
-       (uintptr_t)a->ln2w | (uintptr_t)a->ln2b | (uintptr_t)a->ln3w | (uintptr_t)a->ln3b) & 15) {
-    snprintf(g_err, sizeof(g_err), "qqt_cnn_act: LayerNorm tables must be 16-byte aligned");
+       (uintptr_t)a->ln2w | (uintptr_t)a->ln2b | (uintptr_t)a->ln3w | (uintptr_t)a->ln3b |
+       (uintptr_t)a->c1w | (uintptr_t)a->c1w_lo | (uintptr_t)a->c2w | (uintptr_t)a->c2w_lo) & 15) {
+    snprintf(g_err, sizeof(g_err),
+             "qqt_cnn_act: LayerNorm tables and conv weights must be 16-byte aligned");
     return QQT_E_ARG;
   }
   if (a->batch <= 0 || (a->npid != 1 && a->npid != 2) || a->w_players < a->npid ||

@@ -14,7 +14,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 
 from ._build import LIB
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 MODE_STEP, MODE_OBSERVE, MODE_RESET, MODE_PROBE, MODE_FLUSH = 0, 1, 2, 3, 4
 MAP_PILLARS, MAP_OPEN, MAP_REFERENCE = 0, 1, 2
@@ -98,9 +98,9 @@ class CnnArgsC(ctypes.Structure):
         "bm_row_stride", "bm_pid_stride", "w_players")] + [
         ("seed", _u64), ("tick", _u32), ("out_slots", _i32), ("out_slot", _i32),
         ("reserved", _i32)] + [
-        (n, _vp) for n in ("obs", "view_perm", "c0w", "c0b", "ln0w", "ln0b", "c1w", "c1b",
-                           "ln1w", "ln1b", "c2w", "c2b", "ln2w", "ln2b", "c3w", "c3b", "ln3w",
-                           "ln3b", "s0p", "s0b", "s1w", "s1b", "s3p", "s3b", "s4w", "s4b", "hp",
+        (n, _vp) for n in ("obs", "view_perm", "c0w", "c0w_lo", "c0b", "ln0w", "ln0b", "c1w",
+                           "c1w_lo", "c1b", "ln1w", "ln1b", "c2w", "c2w_lo", "c2b", "ln2w",
+                           "ln2b", "c3w", "c3w_lo", "c3b", "ln3w", "ln3b", "s0p", "s0b", "s1w", "s1b", "s3p", "s3b", "s4w", "s4b", "hp",
                            "hb", "fw", "fb", "move_mask", "bomb_mask", "uniforms", "actions", "actions_i8",
                            "logp_out", "value_out", "logits_out")]
 

@@ -243,19 +243,47 @@ class HipActorCritic:
 CNN_CHANNELS = (16, 32, 64, 8)
 
 
-def _pack_conv(w: torch.Tensor, n_tiles: int) -> torch.Tensor:
-    """[out][in][k][k] conv weight -> the cnn kernel's B operand [tile][step][lane]:
-    lane l of step j holds output 16 tile + l % 16 and, for a 3x3 conv, input
-    channel 4 (j // 9) + l // 16 at tap j % 9 (dy = tap // 3, dx = tap % 3);
-    for a 1x1 conv input channel 4 j + l // 16.  Inputs are padded to a
-    multiple of 4 and outputs to 16 n_tiles with zeros."""
+def _conv_operand(w: torch.Tensor, n_tiles: int) -> torch.Tensor:
+    """[out][in][k][k] conv weight -> float32 [tile][step][lane][8] in the cnn
+    kernel's K order: lane l holds output 16 tile + l % 16 and the 8 input
+    channels of its lane group g = l // 16 at one tap: 16 inputs (conv0's 14
+    padded with zeros): combination c = 4 step + g, tap c // 2 (zero past
+    tap 8), channels 8 (c % 2)..; 32 inputs: tap = step, channels 8 g..; a
+    1x1 conv over 64 inputs: channels 8 (4 step + g)...  Outputs past `out`
+    are zero."""
     cout, cin, kh, kw = w.shape
     taps = kh * kw
-    cinp = -(-cin // 4) * 4
+    if taps == 1:
+        cinp, steps = 64, 2
+    elif cin <= 16:
+        cinp, steps = 16, 5
+    else:
+        cinp, steps = 32, 9
+    if cin > cinp:
+        raise ValueError(f"{cin} input channels do not fit the kernel's layout")
     wp = torch.zeros((n_tiles * 16, cinp, taps), dtype=torch.float32)
     wp[:cout, :cin] = w.float().reshape(cout, cin, taps)
-    x = wp.view(n_tiles, 16, cinp // 4, 4, taps)              # [tile][i16][cb][kq][tap]
-    return x.permute(0, 2, 4, 3, 1).reshape(-1).contiguous()  # [tile][cb*taps+tap][kq*16+i16]
+    out = torch.zeros((n_tiles, 16, steps, 4, 8), dtype=torch.float32)   # [tile][i16][step][g][j]
+    wt = wp.view(n_tiles, 16, cinp, taps)
+    for st in range(steps):
+        for g in range(4):
+            if taps == 1:
+                tap, cb = 0, 4 * st + g
+            elif cinp == 16:
+                c = 4 * st + g
+                tap, cb = c // 2, c % 2
+                if tap >= taps:
+                    continue
+            else:
+                tap, cb = st, g
+            out[:, :, st, g, :] = wt[:, :, 8 * cb:8 * cb + 8, tap]
+    return out.permute(0, 2, 3, 1, 4).reshape(-1).contiguous()          # [tile][step][g*16+i16][j]
+
+
+def _split16(x: torch.Tensor):
+    """float32 -> float16 hi and lo (x = hi + lo to ~2^-22 relative)."""
+    hi = x.half()
+    return hi, (x - hi.float()).half()
 
 
 def _pack_linear(w: torch.Tensor) -> torch.Tensor:
@@ -279,7 +307,8 @@ def _pack_ln(g: torch.Tensor, n_tiles: int) -> torch.Tensor:
 
 def pack_cnn(params: dict, n_players: int = 2, obs_shape=(14, 13, 13)) -> dict:
     """Host-side packing of an ActorCritic cnn state_dict (train/model.py:79-96)
-    into the operand layout of qqt_cnn_act (CPU tensors out), plus the view
+    into the operand layout of qqt_cnn_act (CPU tensors out: conv weights as
+    float16 hi / lo planes, the rest float32), plus the view
     permutation table: conv0 input plane j of player p is observation channel
     view_perm(p)[j], which equals the reference's conv0.weight[:,
     argsort(view_perm)] over the stored observation (:186-190)."""
@@ -302,13 +331,13 @@ def pack_cnn(params: dict, n_players: int = 2, obs_shape=(14, 13, 13)) -> dict:
     out = dict(
         view_perm=torch.tensor([view_perm(p, n_players, c) for p in range(n_players)],
                                dtype=torch.int32).reshape(-1),
-        c0w=_pack_conv(f("conv0.weight"), 1), c0b=f("conv0.bias"),
+        c0b=f("conv0.bias"),
         ln0w=_pack_ln(f("conv.0.weight"), 1), ln0b=_pack_ln(f("conv.0.bias"), 1),
-        c1w=_pack_conv(f("conv.2.weight"), 2), c1b=f("conv.2.bias"),
+        c1b=f("conv.2.bias"),
         ln1w=_pack_ln(f("conv.3.weight"), 2), ln1b=_pack_ln(f("conv.3.bias"), 2),
-        c2w=_pack_conv(f("conv.5.weight"), 4), c2b=f("conv.5.bias"),
+        c2b=f("conv.5.bias"),
         ln2w=_pack_ln(f("conv.6.weight"), 4), ln2b=_pack_ln(f("conv.6.bias"), 4),
-        c3w=_pack_conv(f("conv.8.weight"), 1), c3b=c3b,
+        c3b=c3b,
         ln3w=_pack_ln(f("conv.9.weight"), 1), ln3b=_pack_ln(f("conv.9.bias"), 1),
         s0p=_pack_linear(f("shared.0.weight")), s0b=f("shared.0.bias"),
         s1w=f("shared.1.weight"), s1b=f("shared.1.bias"),
@@ -317,7 +346,10 @@ def pack_cnn(params: dict, n_players: int = 2, obs_shape=(14, 13, 13)) -> dict:
         hp=_pack_linear(torch.cat([f(f"{n}.0.weight") for n in heads])),
         hb=torch.cat([f(f"{n}.0.bias") for n in heads]),
         fw=fw, fb=torch.cat([f(f"{n}.2.bias") for n in heads]))
-    expect = dict(c0w=36 * 64, c1w=2 * 36 * 64, c2w=4 * 72 * 64, c3w=16 * 64,
+    for key, src, nt in (("c0w", "conv0.weight", 1), ("c1w", "conv.2.weight", 2),
+                         ("c2w", "conv.5.weight", 4), ("c3w", "conv.8.weight", 1)):
+        out[key], out[key + "_lo"] = _split16(_conv_operand(f(src), nt))
+    expect = dict(c0w=5 * 64 * 8, c1w=2 * 5 * 64 * 8, c2w=4 * 9 * 64 * 8, c3w=2 * 64 * 8,
                   s0p=8 * 338 * 64, s3p=8 * 32 * 64, hp=12 * 32 * 64, ln2w=4 * 11 * 64 * 4)
     for k, numel in expect.items():
         if out[k].numel() != numel:

@@ -205,9 +205,10 @@ def test_mlp_rejects_bad_output_slots(lib, kw, msg):
     assert msg in lib.qqt_last_error().decode()
 
 
-_CNN_PTRS = ("obs", "view_perm", "c0w", "c0b", "ln0w", "ln0b", "c1w", "c1b", "ln1w", "ln1b",
-             "c2w", "c2b", "ln2w", "ln2b", "c3w", "c3b", "ln3w", "ln3b", "s0p", "s0b", "s1w",
-             "s1b", "s3p", "s3b", "s4w", "s4b", "hp", "hb", "fw", "fb")
+_CNN_PTRS = ("obs", "view_perm", "c0w", "c0w_lo", "c0b", "ln0w", "ln0b", "c1w", "c1w_lo", "c1b",
+             "ln1w", "ln1b", "c2w", "c2w_lo", "c2b", "ln2w", "ln2b", "c3w", "c3w_lo", "c3b",
+             "ln3w", "ln3b", "s0p", "s0b", "s1w", "s1b", "s3p", "s3b", "s4w", "s4b", "hp", "hb",
+             "fw", "fb")
 
 
 def _cnn_args(**kw):
@@ -226,6 +227,8 @@ def _cnn_args(**kw):
     (dict(s3p=None), "null pointer"),
     (dict(view_perm=None), "null pointer"),
     (dict(ln2b=0x10004), "16-byte aligned"),
+    (dict(c2w_lo=0x10008), "16-byte aligned"),
+    (dict(c1w_lo=None), "null pointer"),
     (dict(obs=None), "null pointer"),
     (dict(batch=0), "bad batch"),
     (dict(npid=3), "bad batch"),

@@ -154,12 +154,16 @@ def test_map_spec_validation(kw):
 
 def test_pack_cnn_operands_reproduce_the_reference_layers():
     """The cnn kernel's operand addressing over the packed tensors reproduces
-    the reference's layers: for each conv, A[p][k] read from zero-bordered
-    15 x 15 planes at the kernel's offsets (step j: plane 4 (j // 9) + kq,
-    tap j % 9; 1x1: plane 4 j + kq, centre) times B[k][n] = packed[tile][j]
-    [kq * 16 + n % 16] equals F.conv2d, conv0 on the planes permuted by the
-    view table; the Linear packing gives W[n][4 j + kq]; the LayerNorm tables
-    give gamma[n][16 mt + 4 kq + q]."""
+    the reference's layers.  Each conv: the activations as zero-bordered
+    15 x 15 grids of positions with contiguous channels; lane group g of step
+    s reads the 8 channels of its block at its tap (16 inputs: combination
+    4 s + g -> tap c // 2 (clamped to 8), block c % 2; 32 inputs: tap s,
+    block g; 1x1: block 4 s + g, centre) and multiplies them with the packed
+    B values [tile][s][g * 16 + n % 16][8] (hi + lo); the sum over steps
+    equals F.conv2d with the same (hi + lo) weights in float64, which differ
+    from the reference's by <= 2^-22 relative + 2^-24; conv0 runs on the observation
+    channels permuted by the view table.  The Linear packing gives W[n][4 j +
+    kq]; the LayerNorm tables give gamma[n][16 mt + 4 kq + q]."""
     import torch.nn.functional as F
 
     from qqtsim.policy import default_init_cnn, pack_cnn
@@ -168,44 +172,77 @@ def test_pack_cnn_operands_reproduce_the_reference_layers():
     pk = pack_cnn(params)
     g = torch.Generator().manual_seed(0)
 
-    def kernel_conv(planes, packed, bias, n_tiles, steps, k1):
-        cin_p = planes.shape[0]
-        flat = F.pad(planes, (1, 1, 1, 1)).reshape(cin_p, 225)
-        b = packed.double().view(n_tiles, steps, 4, 16)        # [tile][j][kq][i16]
-        out = torch.zeros((n_tiles * 16, 169), dtype=torch.float64)
+    def tap_off(tap):
+        return (tap // 3) * 15 + tap % 3
+
+    def kernel_conv(x, key, n_tiles, steps, kind, cout):
+        cin = x.shape[0]
+        grid = torch.zeros((225, 64), dtype=torch.float64)       # [padded position][channel]
+        grid[:, :cin] = F.pad(x, (1, 1, 1, 1)).reshape(cin, 225).t()
+        w = (pk[key].double() + pk[key + "_lo"].double()).view(n_tiles, steps, 4, 16, 8)
         pos = torch.arange(169)
-        pbase = (pos // 13) * 15 + pos % 13
-        for j in range(steps):
-            for kq in range(4):
-                if k1:
-                    ci, off = 4 * j + kq, 16
+        pb = (pos // 13) * 15 + pos % 13
+        out = torch.zeros((n_tiles * 16, 169), dtype=torch.float64)
+        for st in range(steps):
+            for gq in range(4):
+                if kind == 0:
+                    c = 4 * st + gq
+                    tap, cb = min(c // 2, 8), c % 2
+                    off = tap_off(tap)
+                elif kind == 1:
+                    cb, off = gq, tap_off(st)
                 else:
-                    ci, tap = 4 * (j // 9) + kq, j % 9
-                    off = (tap // 3) * 15 + tap % 3
-                if ci >= cin_p:
-                    assert float(b[:, j, kq].abs().max()) == 0.0
-                    continue
-                a = flat[ci, pbase + off]                        # [169]
-                out += b[:, j, kq].reshape(-1)[:, None] * a[None, :]
-        return out.view(-1, 13, 13)[: bias.numel()] + bias.double()[:, None, None]
+                    cb, off = 4 * st + gq, 16
+                a = grid[pb + off, 8 * cb:8 * cb + 8]                   # [169][8]
+                bw = w[:, st, gq]                                        # [tile][16][8]
+                out += torch.einsum("pj,tnj->tnp", a, bw).reshape(n_tiles * 16, 169)
+        return out[:cout].view(cout, 13, 13)
+
+    def dense(key, src, n_tiles, steps, kind):
+        """The reference weight rounded as the kernel holds it (hi + lo)."""
+        w = params[src].double()
+        cout, cin, kh, _ = w.shape
+        back = torch.zeros_like(w)
+        pw = (pk[key].double() + pk[key + "_lo"].double()).view(n_tiles, steps, 4, 16, 8)
+        for st in range(steps):
+            for gq in range(4):
+                if kind == 0:
+                    c = 4 * st + gq
+                    tap, cb = c // 2, c % 2
+                    if tap > 8:
+                        assert float(pw[:, st, gq].abs().max()) == 0.0
+                        continue
+                elif kind == 1:
+                    tap, cb = st, gq
+                else:
+                    tap, cb = 0, 4 * st + gq
+                blk = pw[:, st, gq].reshape(n_tiles * 16, 8)[:cout]
+                for j in range(8):
+                    ci = 8 * cb + j
+                    if ci < cin:
+                        back[:, ci, tap // kh, tap % kh] = blk[:, j]
+                    else:
+                        assert float(blk[:, j].abs().max()) == 0.0
+        # hi + lo keeps ~22 bits; a lo below float16's normal range keeps 2^-24 absolute
+        assert bool(((back - w).abs() <= 2.0 ** -22 * w.abs() + 2.0 ** -24).all())
+        return back
 
     x = torch.rand((14, 13, 13), generator=g, dtype=torch.float64)
     vp = pk["view_perm"].view(2, 14)
+    w0 = dense("c0w", "conv0.weight", 1, 5, 0)
     for pid in range(2):
         inv = torch.argsort(vp[pid].long())
-        want = F.conv2d(x[None], params["conv0.weight"].double()[:, inv],
-                        params["conv0.bias"].double(), padding=1)[0]
-        planes = torch.zeros((16, 13, 13), dtype=torch.float64)
-        planes[:14] = x[vp[pid].long()]
-        got = kernel_conv(planes, pk["c0w"], pk["c0b"], 1, 36, False)
+        want = F.conv2d(x[None], w0[:, inv], params["conv0.bias"].double(), padding=1)[0]
+        got = kernel_conv(x[vp[pid].long()], "c0w", 1, 5, 0, 16) + \
+            params["conv0.bias"].double()[:, None, None]
         torch.testing.assert_close(got, want, rtol=1e-12, atol=1e-12)
-    for key, wk, bk, cin, nt, steps, k1 in (("conv.2", "c1w", "c1b", 16, 2, 36, False),
-                                            ("conv.5", "c2w", "c2b", 32, 4, 72, False),
-                                            ("conv.8", "c3w", "c3b", 64, 1, 16, True)):
+    for key, src, bk, cin, nt, steps, kind in (("c1w", "conv.2.weight", "conv.2.bias", 16, 2, 5, 0),
+                                               ("c2w", "conv.5.weight", "conv.5.bias", 32, 4, 9, 1),
+                                               ("c3w", "conv.8.weight", "conv.8.bias", 64, 1, 2, 2)):
         x = torch.rand((cin, 13, 13), generator=g, dtype=torch.float64)
-        w = params[f"{key}.weight"].double()
-        want = F.conv2d(x[None], w, params[f"{key}.bias"].double(), padding=w.shape[-1] // 2)[0]
-        got = kernel_conv(x, pk[wk], pk[bk][: w.shape[0]], nt, steps, k1)
+        wd = dense(key, src, nt, steps, kind)
+        want = F.conv2d(x[None], wd, params[bk].double(), padding=wd.shape[-1] // 2)[0]
+        got = kernel_conv(x, key, nt, steps, kind, wd.shape[0]) + params[bk].double()[:, None, None]
         torch.testing.assert_close(got, want, rtol=1e-12, atol=1e-12)
     for key, pkey, n, k in (("shared.0.weight", "s0p", 128, 1352),
                             ("shared.3.weight", "s3p", 128, 128)):
