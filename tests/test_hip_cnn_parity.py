@@ -241,3 +241,28 @@ def test_cnn_learner_vs_astar_rollout(dev):
         assert torch.equal(roll.actions[:, 0].long(), want), t
         assert torch.equal(roll.logp[:, 0], lp) and torch.equal(roll.value[:, 0], v), t
         roll.launch_tick()
+
+
+def test_cnn_strided_observation_rows(dev):
+    """Observation rows inside a wider buffer (obs_stride > 14 * 169, as a
+    slab with padding would hand them over) give the same outputs as the
+    contiguous rows, through the C ABI directly."""
+    from qqtsim import _capi
+    from qqtsim.policy import HipCnnActorCritic
+
+    net = HipCnnActorCritic(device=dev, seed=2)
+    z = traj("stress40")
+    obs = torch.from_numpy(z["obs"].reshape(-1, 14 * 169)[:200].copy()).half().to(dev)
+    b = obs.shape[0]
+    wide = torch.zeros((b, 14 * 169 + 40), dtype=torch.float16, device=dev)
+    wide[:, :14 * 169] = obs
+    outs = []
+    for src, stride in ((obs, 14 * 169), (wide, 14 * 169 + 40)):
+        lg = torch.full((b, 2, 8), float("nan"), device=dev)
+        a = net._args(b, 2, 0, 0, src.data_ptr(), stride)
+        a.logits_out = lg.data_ptr()
+        net._launch(a, _capi.stream_handle(dev))
+        outs.append(lg)
+    torch.cuda.synchronize()
+    assert torch.isfinite(outs[0]).all()
+    assert torch.equal(outs[0], outs[1])
