@@ -1,7 +1,7 @@
 """The reference's rollout buffer and advantage estimation on the device.
 
 `HipRolloutBuffer` mirrors `RolloutBuffer` (train/ppo.py:54-99) for the mlp
-arch: the same attribute names, shapes and dtypes (`obs`, `mmask`, `bmask`,
+and cnn archs (both store the shared observation): the same attribute names, shapes and dtypes (`obs`, `mmask`, `bmask`,
 `act`, `logp`, `val`, `rew`, `done`, `dmg`, `steps`, `ptr`, `add`, `reset`).
 Underneath, every per-step field is a slab in the layout the kernels write
 (`[T][N][P]` for per-player values, int8 actions, uint8 flags), so
@@ -27,8 +27,9 @@ class HipRolloutBuffer:
 
     def __init__(self, steps: int, num_envs: int, obs_shape, device,
                  obs_dtype=torch.float16, arch: str = "mlp", n_players: int = 2) -> None:
-        if arch != "mlp":
-            raise ValueError("HipRolloutBuffer serves the mlp arch (shared full-map observation)")
+        if arch not in ("mlp", "cnn"):
+            raise ValueError("HipRolloutBuffer serves the mlp and cnn archs (the shared full-map "
+                             "observation); the lstm arch keeps per-player local features")
         if obs_dtype != torch.float16:
             raise ValueError("the device rollout keeps float16 observations")
         c, h, w = obs_shape

@@ -266,3 +266,89 @@ def test_cnn_strided_observation_rows(dev):
     torch.cuda.synchronize()
     assert torch.isfinite(outs[0]).all()
     assert torch.equal(outs[0], outs[1])
+
+
+def _torch_cnn_learner(sd, dev):
+    """The reference's cnn ActorCritic as float32 torch modules with its
+    evaluate() for player 0 (train/model.py:79-96, 186-196, 215-256): the
+    autograd learner of a cnn training iteration."""
+    import torch.nn as nn
+    import torch.nn.functional as F
+
+    from qqtsim.config import view_perm
+
+    class Cnn(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.conv0 = nn.Conv2d(14, 16, 3, padding=1)
+            self.conv = nn.Sequential(
+                nn.LayerNorm([16, 13, 13]), nn.ReLU(), nn.Conv2d(16, 32, 3, padding=1),
+                nn.LayerNorm([32, 13, 13]), nn.ReLU(), nn.Conv2d(32, 64, 3, padding=1),
+                nn.LayerNorm([64, 13, 13]), nn.ReLU(), nn.Conv2d(64, 8, 1),
+                nn.LayerNorm([8, 13, 13]), nn.ReLU())
+            self.shared = nn.Sequential(nn.Linear(1352, 128), nn.LayerNorm(128), nn.ReLU(),
+                                        nn.Linear(128, 128), nn.LayerNorm(128), nn.ReLU())
+            self.move_head = nn.Sequential(nn.Linear(128, 64), nn.ReLU(), nn.Linear(64, 5))
+            self.bomb_head = nn.Sequential(nn.Linear(128, 64), nn.ReLU(), nn.Linear(64, 2))
+            self.critic = nn.Sequential(nn.Linear(128, 64), nn.ReLU(), nn.Linear(64, 1))
+            self.inv = torch.argsort(torch.tensor(view_perm(0, 2, 14))).to(dev)
+
+        def forward(self, obs):
+            x = F.conv2d(obs.float(), self.conv0.weight[:, self.inv], self.conv0.bias, padding=1)
+            x = self.shared(self.conv(x).flatten(1))
+            return self.move_head(x), self.bomb_head(x), self.critic(x).squeeze(-1)
+
+        def evaluate(self, obs, mm, bm, act):
+            ml, bl, v = self(obs)
+            neg = torch.finfo(ml.dtype).min
+            dm = torch.distributions.Categorical(logits=torch.where(mm.bool(), ml, torch.full_like(ml, neg)))
+            db = torch.distributions.Categorical(logits=torch.where(bm.bool(), bl, torch.full_like(bl, neg)))
+            return (dm.log_prob(act[..., 0]) + db.log_prob(act[..., 1]),
+                    dm.entropy() + db.entropy(), v)
+
+    m = Cnn()
+    m.load_state_dict(sd)
+    return m.to(dev)
+
+
+def test_cnn_training_iteration(dev):
+    """A cnn training iteration of the reference's loop: collect 32 steps of
+    64 envs with HipCnnActorCritic into the device buffer (arch "cnn"),
+    ppo_update on the reference network as an autograd learner, and the
+    updated weights loaded back into the acting network, whose forward then
+    matches the learner's (1e-4)."""
+    from qqtsim import (HipBatchedSim, HipCnnActorCritic, HipRolloutBuffer, MapSpec, PPOConfig,
+                        Rollout, corridor_training_config, ppo_update)
+    from qqtsim.policy import default_init_cnn
+
+    cfg = corridor_training_config(max_steps=40)
+    n, t = 64, 32
+    sd = default_init_cnn(cfg.obs_shape, seed=6)
+    sim = HipBatchedSim(cfg, n, device=dev, seed=3,
+                        map_spec=MapSpec(kind="pillars", brick_p=0.5, bombs_cap=(2, 3)))
+    actor = HipCnnActorCritic(sd, device=dev, seed=3)
+    roll = Rollout(sim, actor)
+    buf = HipRolloutBuffer(t, n, cfg.obs_shape, dev, arch="cnn")
+    roll.collect(buf)
+    learner = _torch_cnn_learner(sd, dev)
+    with torch.no_grad():                      # the buffer's log-probs are the acting network's
+        lp, _, v = learner.evaluate(buf.obs[:4].reshape(-1, 14, 13, 13), buf.mmask[:4].reshape(-1, 5),
+                                    buf.bmask[:4].reshape(-1, 2), buf.act[:4].reshape(-1, 2))
+    assert float((lp - buf.logp[:4].reshape(-1)).abs().max()) <= 2e-4
+    assert float((v - buf.val[:4].reshape(-1)).abs().max()) <= 1e-4
+    before = {k: v.detach().clone() for k, v in learner.state_dict().items()}
+    opt = torch.optim.Adam(learner.parameters(), lr=3e-4)
+    last_val = actor.forward(sim.observe(), 0)[2]
+    torch.manual_seed(0)
+    stats = ppo_update(learner, opt, buf, last_val, PPOConfig(minibatches=2, epochs=2), 0.05)
+    assert all(np.isfinite(x) for x in stats.values()), stats
+    after = {k: v.detach().cpu() for k, v in learner.state_dict().items()}
+    assert any(not torch.equal(before[k].cpu(), after[k]) for k in after)
+    actor.load_state_dict(after)
+    obs = sim.observe()
+    ml, bl, v = actor.forward(obs, 0)
+    with torch.no_grad():
+        rml, rbl, rv = learner(obs)
+    got = torch.cat([ml, bl, v[:, None]], 1)
+    ref = torch.cat([rml, rbl, rv[:, None]], 1)
+    assert float((got - ref).abs().max()) <= 1e-4
