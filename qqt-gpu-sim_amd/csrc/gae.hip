@@ -6,9 +6,9 @@
 // sum rounds separately (the library is built with -ffp-contract=off), and
 // gamma * lam arrives pre-rounded from the double product the reference's
 // Python expression forms.  Loads do not depend on the running sum, so each
-// block of 8 steps is loaded before its arithmetic.  Algorithmic bytes:
+// block of 32 steps is loaded before its arithmetic.  Algorithmic bytes:
 // 4 + 4 + 1 read and 8 written per (step, env); with one thread per env the
-// kernel is bound by T / 8 rounds of memory latency, not by bandwidth (it
+// kernel is bound by T / 32 rounds of memory latency, not by bandwidth (it
 // runs once per collected rollout).
 
 #include <hip/hip_runtime.h>
@@ -22,8 +22,8 @@ namespace qqt {
 
 extern thread_local char g_err[512];
 
-constexpr int GAE_THREADS = 256;
-constexpr int GAE_BLOCK = 8;    // steps whose loads are in flight together
+constexpr int GAE_THREADS = 64;  // one wavefront per workgroup: the envs spread over more CUs
+constexpr int GAE_BLOCK = 32;   // steps whose loads are in flight together
 
 // Steps t1-1 .. t1-B of one env: loads first (indices clamped at 0), then the
 // recurrence; steps below 0 (a partial last block) are skipped by predicate.
