@@ -296,6 +296,18 @@ class PPOConfig:
     bptt_window: int = 0
 
 
+def _gather_rows(x: torch.Tensor, sel: torch.Tensor) -> torch.Tensor:
+    """x[sel] for a contiguous tensor; rows of 2-byte elements with an even
+    width are gathered as 4-byte words (the same bytes; torch's row gather
+    moves them ~1.7x faster than as halves)."""
+    n = x.shape[0]
+    row = x[0].numel() if n else 0
+    if x.is_contiguous() and x.element_size() == 2 and row % 2 == 0 and row > 0:
+        words = x.view(n, row).view(torch.int32)
+        return words.index_select(0, sel).view(x.dtype).view(sel.shape[0], *x.shape[1:])
+    return x[sel]
+
+
 def ppo_update(learner, opt, buf, last_val, cfg: PPOConfig, entropy_coef: float) -> dict:
     """One PPO update over a filled rollout buffer, as train/ppo.py:364-437
     (GAE, advantage normalisation, dying-frame oversampling, epochs x
@@ -332,14 +344,16 @@ def ppo_update(learner, opt, buf, last_val, cfg: PPOConfig, entropy_coef: float)
             sel = perm[start:start + mb]
             if hasattr(learner, "ppo_grads"):       # the fused loss + backward
                 opt.zero_grad(set_to_none=True)
-                st = learner.ppo_grads(obs[sel], mmask[sel], bmask[sel], act[sel], old_logp[sel],
-                                       adv[sel], ret[sel], old_val[sel], cfg, entropy_coef)
+                st = learner.ppo_grads(_gather_rows(obs, sel), mmask[sel], bmask[sel], act[sel],
+                                       old_logp[sel], adv[sel], ret[sel], old_val[sel], cfg,
+                                       entropy_coef)
                 torch.nn.utils.clip_grad_norm_(learner.parameters(), cfg.max_grad_norm)
                 opt.step()
                 acc += st
                 n_updates += 1
                 continue
-            logp, entropy, value = learner.evaluate(obs[sel], mmask[sel], bmask[sel], act[sel])
+            logp, entropy, value = learner.evaluate(_gather_rows(obs, sel), mmask[sel], bmask[sel],
+                                                    act[sel])
             ratio = (logp - old_logp[sel]).exp()
             pg = -torch.min(ratio * adv[sel],
                             ratio.clamp(1 - cfg.clip_eps, 1 + cfg.clip_eps) * adv[sel]).mean()

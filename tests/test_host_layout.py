@@ -255,3 +255,19 @@ def test_pack_cnn_operands_reproduce_the_reference_layers():
     assert float(ln[0, 10, 3, 0, 3]) == 0.0                      # position 175 >= 169
     assert torch.equal(pk["fw"][5:7], params["bomb_head.2.weight"])
     assert sum(v.numel() for v in params.values()) == 281744
+
+
+def test_gather_rows_equals_advanced_indexing():
+    """The minibatch row gather of ppo_update (4-byte words for float16 rows
+    of even width) returns exactly obs[sel], and falls back for other rows."""
+    from qqtsim.learn import _gather_rows
+
+    g = torch.Generator().manual_seed(0)
+    obs = torch.rand((50, 14, 13, 13), generator=g).half()
+    sel = torch.randint(0, 50, (37,), generator=g)
+    assert torch.equal(_gather_rows(obs, sel), obs[sel])
+    odd = torch.rand((20, 3), generator=g).half()
+    s2 = torch.tensor([4, 1, 1, 19])
+    assert torch.equal(_gather_rows(odd, s2), odd[s2])
+    f32 = torch.rand((20, 6), generator=g)
+    assert torch.equal(_gather_rows(f32, s2), f32[s2])
