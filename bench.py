@@ -32,6 +32,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -843,6 +844,15 @@ L1G_BYTES_PER_ROW = 2366 * 2 + 128 * 4
 L1G_FLOP_PER_ROW = 2 * 2 * 128 * 2366
 
 
+def _require_finite(what, stats):
+    """Exit non-zero when an update's statistics are not all finite (a
+    diverged learner makes the timing meaningless)."""
+    bad = {k: v for k, v in stats.items() if not math.isfinite(v)}
+    if bad:
+        print(f"{what}: non-finite statistics {bad}", file=sys.stderr, flush=True)
+        sys.exit(3)
+
+
 def main_ppo(args, torch, dev):
     """One PPO update (train/ppo.py:364-437: GAE, 4 epochs x 4 minibatches of
     the clipped loss, backward, gradient clipping, Adam) over a buffer of
@@ -853,41 +863,49 @@ def main_ppo(args, torch, dev):
     `torch_gpu_baseline` runs the same update with the reference's network
     as float32 eager torch modules on the same GPU."""
     from qqtsim import HipMlpActorCritic, HipRolloutBuffer, PPOConfig, ppo_update
-    from qqtsim.policy import default_init
+    from qqtsim.policy import reference_init
 
     n = args.envs
     cfg, spec, roll = build_workload(n, args.seed, dev)
+    sd = reference_init(cfg.obs_shape)
+    roll.policy.load_state_dict(sd)           # the learner acts (and is cloned as the opponent)
     for _ in range(max(1, args.warmup)):
         roll.step()
     buf = HipRolloutBuffer(COLLECT_T, n, cfg.obs_shape, dev)
     roll.collect(buf)
     last_val = roll.policy.forward(roll.sim.observe(), 0)[2]
     pcfg = PPOConfig()
-    sd = default_init(cfg.obs_shape)
     rows = COLLECT_T * n
     reps = 2 if args.steps >= 256 else max(1, min(args.steps, 3))   # whole updates timed
 
     def run(learner, timed_launches=0):
+        """Warm-up update, then `reps` timed updates, each from the same
+        weights and optimizer state (the first update's statistics on a
+        buffer the weights acted are the ones a training run sees)."""
+        start = {k: v.detach().clone() for k, v in learner.state_dict().items()}
         opt = torch.optim.Adam(learner.parameters(), lr=pcfg.lr)
         torch.manual_seed(0)
         ppo_update(learner, opt, buf, last_val, pcfg, pcfg.entropy_coef)     # warm-up
         torch.cuda.synchronize()
-        best = float("inf")
+        best, stats = float("inf"), None
         for _ in range(reps):
+            learner.load_state_dict(start)
+            opt = torch.optim.Adam(learner.parameters(), lr=pcfg.lr)
             torch.manual_seed(0)
+            torch.cuda.synchronize()
             if timed_launches:
                 _capi.timing_arm(timed_launches)
             t0 = time.perf_counter()
-            ppo_update(learner, opt, buf, last_val, pcfg, pcfg.entropy_coef)
+            stats = ppo_update(learner, opt, buf, last_val, pcfg, pcfg.entropy_coef)
             torch.cuda.synchronize()
             best = min(best, time.perf_counter() - t0)
-        return best
+        return best, stats
 
     _capi.timing_arm(0)
     learner = HipMlpActorCritic(cfg.obs_shape, device=dev, state_dict=sd)
     # GAE, then the first minibatch's four launches (forward, fused loss +
     # backward, weight gradient and its chunk reduction)
-    el = run(learner, timed_launches=1 + 4)
+    el, stats = run(learner, timed_launches=1 + 4)
     tim = _capi.timing_collect()
     mb_rows = rows // pcfg.minibatches
     fwd_ms = tim["mlp_act_kernel"][0] / tim["mlp_act_kernel"][1]
@@ -898,7 +916,7 @@ def main_ppo(args, torch, dev):
     fwd_gbs = 2366 * 2 * mb_rows / (fwd_ms * 1e-3) / 1e9
     ppo_ms = tim["ppo_grad_kernel"][0] / tim["ppo_grad_kernel"][1]
     ref = _torch_mlp(torch, sd, dev)
-    el_ref = run(ref)
+    el_ref, ref_stats = run(ref)
     samples = rows * pcfg.epochs
     cpu = None
     if args.cpu_seconds > 0:
@@ -930,8 +948,8 @@ def main_ppo(args, torch, dev):
         "vs_baseline": None,
         "dtype": "f16 MFMA first layer (f32 accumulate) / f32 fused loss + backward / f32 torch "
                  "weight-gradient products and Adam",
-        "data": "synthetic: a buffer collected by the kernels from template maps, PyTorch "
-                "default-init MLP weights",
+        "data": "synthetic: a buffer collected by the kernels from template maps, acted by "
+                "the learner's weights (the reference ActorCritic's orthogonal init)",
         "config": {"workload": "PPO update over a 5632 x 128 rollout buffer "
                                "(train/ppo.py:364-437)", "rows": rows,
                    "epochs": pcfg.epochs, "minibatches": pcfg.minibatches,
@@ -949,11 +967,14 @@ def main_ppo(args, torch, dev):
         "torch_gpu_baseline": {"value": samples / el_ref, "unit": "samples/s",
                                "ms_per_update": el_ref * 1e3,
                                "speedup": round(el_ref / el, 3),
+                               "update_stats": ref_stats,
                                "note": "same update, the reference's network as float32 "
                                        "eager torch modules"},
+        "update_stats": stats,
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
+    _require_finite("ppo update", stats)
 
 
 def main_train(args, torch, dev):
@@ -965,17 +986,19 @@ def main_train(args, torch, dev):
     network.  `value` is env-steps per second of the whole iteration (the
     reference's "sps")."""
     from qqtsim import HipMlpActorCritic, HipRolloutBuffer, PPOConfig, ppo_update
-    from qqtsim.policy import default_init
+    from qqtsim.policy import reference_init
 
     n = args.envs
     cfg, spec, roll = build_workload(n, args.seed, dev)
+    sd = reference_init(cfg.obs_shape)
+    actor = roll.policy
+    actor.load_state_dict(sd)                 # the learner acts (and is cloned as the opponent)
     for _ in range(max(1, args.warmup)):
         roll.step()
     buf = HipRolloutBuffer(COLLECT_T, n, cfg.obs_shape, dev)
     pcfg = PPOConfig()
-    learner = HipMlpActorCritic(cfg.obs_shape, device=dev, state_dict=default_init(cfg.obs_shape))
+    learner = HipMlpActorCritic(cfg.obs_shape, device=dev, state_dict=sd)
     opt = torch.optim.Adam(learner.parameters(), lr=pcfg.lr)
-    actor = roll.policy
 
     def iteration():
         roll.collect(buf)
@@ -985,14 +1008,15 @@ def main_train(args, torch, dev):
         return st
 
     torch.manual_seed(0)
-    iteration()                                      # warm-up iteration
+    history = [iteration()]                          # warm-up iteration
     torch.cuda.synchronize()
     iters = 3 if args.steps >= 256 else max(1, min(args.steps, 3))
     t0 = time.perf_counter()
     for _ in range(iters):
-        st = iteration()
+        history.append(iteration())
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
+    st = history[-1]
     steps = iters * COLLECT_T * n
     res = {
         "metric": "training env-steps/s (collect 128 steps x 5632 envs + PPO update + weight "
@@ -1002,14 +1026,18 @@ def main_train(args, torch, dev):
         "vs_baseline": None,
         "dtype": "f32 sim / f16 MFMA acting / f16 MFMA first layer + f32 fused loss and "
                  "backward in the update",
-        "data": "synthetic: template maps from Philox draws, PyTorch default-init weights",
+        "data": "synthetic: template maps from Philox draws, the reference ActorCritic's "
+                "orthogonal init for the learner (acting for both players)",
         "config": {"workload": "training iteration: collect (5632 envs x 128 steps) + PPO "
                                "update (4 epochs x 4 minibatches) + weight sync",
                    "envs": n, "collect_steps": COLLECT_T, "parallelism": "single GPU"},
         "last_update_stats": st,
+        "update_stats_per_iteration": history,
         "cpu_baseline": None,
     }
     print(json.dumps(res), flush=True)
+    for i, h in enumerate(history):
+        _require_finite(f"training iteration {i}", h)
 
 
 

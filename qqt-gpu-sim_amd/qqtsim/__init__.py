@@ -14,12 +14,13 @@ from .learn import HipMlpActorCritic, PPOConfig, ppo_update
 from .config import SimConfig, corridor_training_config
 from .factory import make_sim
 from .maps import BOMB_STRESS_40, CORRIDOR_70, OPEN_PILLARS, MapSpec
-from .policy import HipActorCritic, HipCnnActorCritic, default_init, default_init_cnn
+from .policy import (HipActorCritic, HipCnnActorCritic, default_init, default_init_cnn,
+                     reference_init)
 from .ppo import HipRolloutBuffer, compute_gae
 from .rollout import Rollout
 from .sim import HipBatchedSim
 
 __all__ = ["HipAstarBot", "SimConfig", "corridor_training_config", "make_sim", "MapSpec", "OPEN_PILLARS",
-           "CORRIDOR_70", "BOMB_STRESS_40", "HipActorCritic", "HipCnnActorCritic", "default_init", "default_init_cnn", "Rollout",
+           "CORRIDOR_70", "BOMB_STRESS_40", "HipActorCritic", "HipCnnActorCritic", "default_init", "default_init_cnn", "reference_init", "Rollout",
            "HipBatchedSim", "HipRolloutBuffer", "compute_gae", "HipMlpActorCritic", "PPOConfig",
            "ppo_update"]

@@ -42,11 +42,12 @@ def column_permutation(pid: int, p: int, c: int, hw: int) -> torch.Tensor:
 
 def _frag(w: torch.Tensor, kpad: int, residual: bool = False) -> torch.Tensor:
     """(n_out, k) float matrix -> float16 B fragments [tile][kblock][lane][16]
-    (of w itself, or of its float16 residual w - float16(w))."""
+    (of w itself, or of its float16 residual w - float16(w)), on w's
+    device."""
     n, k = w.shape
     assert n % 16 == 0
-    out = torch.zeros((n, kpad), dtype=torch.float32)
-    out[:, :k] = w.float().cpu()
+    out = torch.zeros((n, kpad), dtype=torch.float32, device=w.device)
+    out[:, :k] = w.float()
     if residual:
         out = out - out.half().float()
     kb = kpad // KBLOCK
@@ -55,23 +56,26 @@ def _frag(w: torch.Tensor, kpad: int, residual: bool = False) -> torch.Tensor:
 
 
 def pack_mlp(params: dict, n_players: int = 2, obs_shape=(14, 13, 13)) -> dict:
-    """Host-side packing of an ActorCritic mlp state_dict (CPU tensors out)."""
+    """Packing of an ActorCritic mlp state_dict into the kernel's operand
+    layout, on the device the weights live on."""
     c, h, w = obs_shape
     hw = h * w
     k0 = c * hw
     kpad = math.ceil(k0 / KBLOCK) * KBLOCK
-    W0 = params["shared.0.weight"].float().cpu()
+    W0 = params["shared.0.weight"].float()
+    dev = W0.device
     if W0.shape != (HID, k0):
         raise ValueError(f"shared.0.weight must be {(HID, k0)}, got {tuple(W0.shape)}")
-    per_pid = [W0[:, column_permutation(pid, n_players, c, hw)] for pid in range(n_players)]
+    per_pid = [W0[:, column_permutation(pid, n_players, c, hw).to(dev)]
+               for pid in range(n_players)]
     w0 = torch.cat([_frag(wp, kpad) for wp in per_pid])
-    w1_src = params["shared.3.weight"]
+    w1_src = params["shared.3.weight"].to(dev)
     w1, w1_lo = _frag(w1_src, HID), _frag(w1_src, HID, True)
     heads = ("move_head", "bomb_head", "critic")
-    wh_src = torch.cat([params[f"{n}.0.weight"].float() for n in heads])
+    wh_src = torch.cat([params[f"{n}.0.weight"].to(dev).float() for n in heads])
     wh, wh_lo = _frag(wh_src, HID), _frag(wh_src, HID, True)
-    wfin = torch.zeros((16, 3 * HEAD), dtype=torch.float32)
-    outs = [params[f"{n}.2.weight"].float() for n in heads]
+    wfin = torch.zeros((16, 3 * HEAD), dtype=torch.float32, device=dev)
+    outs = [params[f"{n}.2.weight"].to(dev).float() for n in heads]
     row = 0
     for i, o in enumerate(outs):
         wfin[row:row + o.shape[0], i * HEAD:(i + 1) * HEAD] = o
@@ -79,7 +83,7 @@ def pack_mlp(params: dict, n_players: int = 2, obs_shape=(14, 13, 13)) -> dict:
     if row != 8:
         raise ValueError("heads must produce 5 + 2 + 1 outputs")
     wf, wf_lo = _frag(wfin, 3 * HEAD), _frag(wfin, 3 * HEAD, True)
-    vec = lambda k: params[k].float().cpu().contiguous()  # noqa: E731
+    vec = lambda k: params[k].to(dev).float().contiguous()  # noqa: E731
     return dict(
         w0=w0, w1=w1, wh=wh, wf=wf, w1_lo=w1_lo, wh_lo=wh_lo, wf_lo=wf_lo,
         b0=vec("shared.0.bias"), ln1_w=vec("shared.1.weight"), ln1_b=vec("shared.1.bias"),
@@ -89,27 +93,80 @@ def pack_mlp(params: dict, n_players: int = 2, obs_shape=(14, 13, 13)) -> dict:
         k0=k0, kblocks0=kpad // KBLOCK)
 
 
+def _layer_tree(arch: str, obs_shape, n_moves: int, n_bomb: int) -> torch.nn.Module:
+    """The ActorCritic layers of `arch` as plain torch modules, created (and
+    so drawing their PyTorch default init) in the reference's registration
+    order: the cnn trunk `conv0`, `conv` (train/model.py:76-93), then
+    `shared`, `move_head`, `bomb_head`, `critic` (:140-153)."""
+    c, h, w = obs_shape
+    nn = torch.nn
+    tree = nn.Module()
+    if arch == "cnn":
+        tree.conv0 = nn.Conv2d(c, 16, 3, padding=1)
+        tree.conv = nn.Sequential(
+            nn.LayerNorm([16, h, w]), nn.ReLU(), nn.Conv2d(16, 32, 3, padding=1),
+            nn.LayerNorm([32, h, w]), nn.ReLU(), nn.Conv2d(32, 64, 3, padding=1),
+            nn.LayerNorm([64, h, w]), nn.ReLU(), nn.Conv2d(64, 8, 1),
+            nn.LayerNorm([8, h, w]), nn.ReLU())
+        flat = 8 * h * w
+    elif arch == "mlp":
+        flat = c * h * w
+    else:
+        raise ValueError(f"no layer tree for arch {arch!r}")
+    tree.shared = nn.Sequential(nn.Linear(flat, HID), nn.LayerNorm(HID), nn.ReLU(),
+                                nn.Linear(HID, HID), nn.LayerNorm(HID), nn.ReLU())
+    tree.move_head = nn.Sequential(nn.Linear(HID, HEAD), nn.ReLU(), nn.Linear(HEAD, n_moves))
+    tree.bomb_head = nn.Sequential(nn.Linear(HID, HEAD), nn.ReLU(), nn.Linear(HEAD, n_bomb))
+    tree.critic = nn.Sequential(nn.Linear(HID, HEAD), nn.ReLU(), nn.Linear(HEAD, 1))
+    return tree
+
+
+def _tree_state(tree: torch.nn.Module) -> dict:
+    return {k: v.detach().clone() for k, v in tree.state_dict().items()}
+
+
 def default_init(obs_shape=(14, 13, 13), n_moves: int = 5, n_bomb: int = 2,
                  seed: int = 0) -> dict:
     """PyTorch default init of the mlp ActorCritic layers (nn.Linear
     kaiming-uniform(a=sqrt(5)) weights, U(+-1/sqrt(fan_in)) biases, LayerNorm
     1/0) under torch.manual_seed(seed), layers created in module order
-    (train/model.py:140-153).  The global RNG state is restored afterwards."""
-    c, h, w = obs_shape
+    (train/model.py:140-153).  The global RNG state is restored afterwards.
+    This is not what the reference's ActorCritic holds after construction
+    (see `reference_init`); benchmark workloads that name PyTorch default
+    init use it."""
+    with torch.random.fork_rng(devices=[]):
+        torch.manual_seed(seed)
+        return _tree_state(_layer_tree("mlp", obs_shape, n_moves, n_bomb))
+
+
+def reference_init(obs_shape=(14, 13, 13), n_moves: int = 5, n_bomb: int = 2,
+                   seed: int = 0, arch: str = "mlp") -> dict:
+    """The weights `torch.manual_seed(seed); ActorCritic(obs_shape, arch=arch)`
+    holds (train/model.py:154-165): every Conv2d / Linear weight orthogonal
+    with gain sqrt(2) and its bias zero, visited in module order after all
+    layers were created, then the move and bomb heads' output weights drawn
+    again orthogonal with gain 0.01 (biases zero); LayerNorm 1 / 0.  The
+    random draws follow the reference's order, so the result equals the
+    reference module's state_dict bit for bit.  The global RNG state is
+    restored afterwards."""
     nn = torch.nn
     with torch.random.fork_rng(devices=[]):
         torch.manual_seed(seed)
-        shared = nn.Sequential(nn.Linear(c * h * w, HID), nn.LayerNorm(HID), nn.ReLU(),
-                               nn.Linear(HID, HID), nn.LayerNorm(HID), nn.ReLU())
-        heads = {name: nn.Sequential(nn.Linear(HID, HEAD), nn.ReLU(), nn.Linear(HEAD, k))
-                 for name, k in (("move_head", n_moves), ("bomb_head", n_bomb), ("critic", 1))}
-    out = {f"shared.{k}": v for k, v in shared.state_dict().items()}
-    for name, mod in heads.items():
-        out.update({f"{name}.{k}": v for k, v in mod.state_dict().items()})
-    return {k: v.detach().clone() for k, v in out.items()}
+        tree = _layer_tree(arch, obs_shape, n_moves, n_bomb)
+        with torch.no_grad():
+            for mod in tree.modules():
+                if isinstance(mod, (nn.Conv2d, nn.Linear)):
+                    nn.init.orthogonal_(mod.weight, gain=2 ** 0.5)
+                    nn.init.zeros_(mod.bias)
+            for head in (tree.move_head, tree.bomb_head):
+                nn.init.orthogonal_(head[-1].weight, gain=0.01)
+                nn.init.zeros_(head[-1].bias)
+        return _tree_state(tree)
 
 
 class HipActorCritic:
+    arch = "mlp"
+
     def __init__(self, state_dict: dict | None = None, obs_shape=(14, 13, 13),
                  n_players: int = 2, device="cuda", seed: int = 0):
         self.obs_shape = tuple(obs_shape)
@@ -122,13 +179,36 @@ class HipActorCritic:
         self.seed = int(seed)
         self.tick = 0
         self._lib = _capi.lib()
-        self.load_state_dict(state_dict if state_dict is not None else default_init(obs_shape))
+        self._w = None
+        self.load_state_dict(state_dict if state_dict is not None
+                             else reference_init(obs_shape, seed=0, arch=self.arch))
+
+    def _pack(self, params: dict) -> dict:
+        packed = pack_mlp(params, self.n_players, self.obs_shape)
+        self.k0, self.kblocks0 = packed.pop("k0"), packed.pop("kblocks0")
+        return packed
 
     def load_state_dict(self, state_dict: dict) -> None:
-        self.params = {k: v.detach().float().cpu().clone() for k, v in state_dict.items()}
-        packed = pack_mlp(self.params, self.n_players, self.obs_shape)
-        self.k0, self.kblocks0 = packed.pop("k0"), packed.pop("kblocks0")
-        self._w = {k: v.to(self.device).contiguous() for k, v in packed.items()}
+        """Repack the weights (on the device) and copy them over the packed
+        buffers in place.  Argument blocks built before (a `Rollout`'s) keep
+        the buffers' addresses, so they stay valid and the next launch uses
+        the new weights; the copies are ordered on the current stream."""
+        params = {k: v.detach().to(self.device, torch.float32).clone()
+                  for k, v in state_dict.items()}
+        packed = self._pack(params)
+        if self._w is None:
+            self._w = {k: v.to(self.device).contiguous() for k, v in packed.items()}
+        else:
+            if set(packed) != set(self._w) or any(
+                    packed[k].shape != self._w[k].shape for k in packed):
+                raise ValueError("state_dict does not match the network's layer shapes")
+            for k, v in packed.items():
+                self._w[k].copy_(v)
+        self.params = params
+
+    def state_dict(self) -> dict:
+        """The float32 weights last loaded, under the reference's keys."""
+        return {k: v.clone() for k, v in self.params.items()}
 
     def n_params(self) -> int:
         return sum(v.numel() for v in self.params.values())
@@ -363,25 +443,9 @@ def default_init_cnn(obs_shape=(14, 13, 13), n_moves: int = 5, n_bomb: int = 2,
     kaiming-uniform(a=sqrt(5)), LayerNorm 1/0) under torch.manual_seed(seed),
     layers created in module order (train/model.py:79-96, 140-153).  The
     global RNG state is restored afterwards."""
-    c, h, w = obs_shape
-    nn = torch.nn
     with torch.random.fork_rng(devices=[]):
         torch.manual_seed(seed)
-        conv0 = nn.Conv2d(c, 16, 3, padding=1)
-        conv = nn.Sequential(nn.LayerNorm([16, h, w]), nn.ReLU(), nn.Conv2d(16, 32, 3, padding=1),
-                             nn.LayerNorm([32, h, w]), nn.ReLU(), nn.Conv2d(32, 64, 3, padding=1),
-                             nn.LayerNorm([64, h, w]), nn.ReLU(), nn.Conv2d(64, 8, 1),
-                             nn.LayerNorm([8, h, w]), nn.ReLU())
-        shared = nn.Sequential(nn.Linear(8 * h * w, HID), nn.LayerNorm(HID), nn.ReLU(),
-                               nn.Linear(HID, HID), nn.LayerNorm(HID), nn.ReLU())
-        heads = {name: nn.Sequential(nn.Linear(HID, HEAD), nn.ReLU(), nn.Linear(HEAD, k))
-                 for name, k in (("move_head", n_moves), ("bomb_head", n_bomb), ("critic", 1))}
-    out = {f"conv0.{k}": v for k, v in conv0.state_dict().items()}
-    out.update({f"conv.{k}": v for k, v in conv.state_dict().items()})
-    out.update({f"shared.{k}": v for k, v in shared.state_dict().items()})
-    for name, mod in heads.items():
-        out.update({f"{name}.{k}": v for k, v in mod.state_dict().items()})
-    return {k: v.detach().clone() for k, v in out.items()}
+        return _tree_state(_layer_tree("cnn", obs_shape, n_moves, n_bomb))
 
 
 class HipCnnActorCritic(HipActorCritic):
@@ -389,17 +453,14 @@ class HipCnnActorCritic(HipActorCritic):
     qqt_cnn_act: the same forward / act / act_pair / evaluate as the mlp
     class, with float32 weights (the trunk computes in float32 on MFMA)."""
 
-    def __init__(self, state_dict: dict | None = None, obs_shape=(14, 13, 13),
-                 n_players: int = 2, device="cuda", seed: int = 0):
-        if state_dict is None:
-            state_dict = default_init_cnn(obs_shape)
-        super().__init__(state_dict, obs_shape, n_players, device, seed)
+    arch = "cnn"
 
-    def load_state_dict(self, state_dict: dict) -> None:
-        self.params = {k: v.detach().float().cpu().clone() for k, v in state_dict.items()}
-        packed = pack_cnn(self.params, self.n_players, self.obs_shape)
+    def _pack(self, params: dict) -> dict:
+        # the conv operand layout is built on the host (a few hundred KB)
+        packed = pack_cnn({k: v.cpu() for k, v in params.items()}, self.n_players,
+                          self.obs_shape)
         self.k0 = self.obs_shape[0] * self.obs_shape[1] * self.obs_shape[2]
-        self._w = {k: v.to(self.device).contiguous() for k, v in packed.items()}
+        return packed
 
     def _args(self, b, npid, pid0, sample, obs_ptr, obs_stride):
         a = _capi.CnnArgsC()

@@ -346,3 +346,12 @@ def test_l1_grad_rejects_bad_arguments(lib):
     assert b"workspace" in lib.qqt_last_error()
     a.workspace_floats, a.k0 = n, 2367
     assert lib.qqt_l1_grad(ctypes.byref(a), None) == -1
+
+
+def test_integration_doc_lists_every_source():
+    """INTEGRATION.md's build section names every source the build compiles."""
+    from qqtsim import _build
+
+    doc = open(os.path.join(os.path.dirname(os.path.dirname(__file__)), "INTEGRATION.md")).read()
+    missing = [s for s in _build.SOURCES if f"csrc/{s}" not in doc]
+    assert missing == [], missing

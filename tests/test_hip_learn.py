@@ -138,21 +138,10 @@ class RefMlp(torch.nn.Module):
 
 
 def _ortho_init(seed):
-    """The reference's ActorCritic init (train/model.py:154-165): orthogonal
-    gain sqrt 2, zero biases, policy heads' last layers gain 0.01."""
-    from qqtsim.policy import default_init
+    """The reference's ActorCritic init (train/model.py:154-165)."""
+    from qqtsim.policy import reference_init
 
-    sd = default_init()
-    g = torch.Generator().manual_seed(seed)
-    for k, v in sd.items():
-        if k.endswith("weight") and v.dim() == 2:
-            gain = 0.01 if k in ("move_head.2.weight", "bomb_head.2.weight") else math.sqrt(2)
-            q = torch.empty_like(v)
-            torch.nn.init.orthogonal_(q, gain=gain, generator=g)
-            sd[k] = q
-        elif k.endswith("bias") and not k.startswith("shared.1") and not k.startswith("shared.4"):
-            sd[k] = torch.zeros_like(v)
-    return sd
+    return reference_init(seed=seed)
 
 
 def _loss(net, obs, mm, bm, act, old_logp, adv, ret, old_val, pid):
