@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 11
+#define QQT_ABI_VERSION 12
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -132,6 +132,9 @@ typedef struct qqt_tick_args {
   int32_t opp_boost;          /* QQT_MAP_REFERENCE resets: player 1's start tier
                                  (0 as player 0, 1 x opp_hist_mult, 2 opp_growth_*;
                                  BatchedSim.set_opp_boost, sim/torch_sim.py:422-453) */
+  float* danger_out;          /* OBSERVE: [N][H][W] float32 danger map of the current
+                                 state (blast.danger_map as BatchedSim._danger_c
+                                 computes it, sim/torch_sim.py:732-762), or NULL */
 } qqt_tick_args;
 
 /* MLP actor/critic forward (+ masked sampling).  Weights are the packed

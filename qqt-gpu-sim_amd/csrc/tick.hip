@@ -979,6 +979,17 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
     }
     wave_sync();
   }
+  // the float32 danger map itself, for callers that read it (OBSERVE launches;
+  // the STEP and FLUSH instantiations carry no such code)
+  if constexpr (KMODE < 0) {
+    if (mode == QQT_MODE_OBSERVE && a.danger_out && valid) {
+#pragma unroll
+      for (int k = 0; k < KMAX; ++k) {
+        const int c = l + LPE * k;
+        if (c < C) a.danger_out[(size_t)g * C + c] = s.dng[e][c];
+      }
+    }
+  }
 
   if (mode == QQT_MODE_STEP) {
     // ---- 10. time, rewards, growth, combo, terminal terms; lane i < P is player i

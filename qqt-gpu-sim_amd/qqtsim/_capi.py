@@ -14,7 +14,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 
 from ._build import LIB
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 MODE_STEP, MODE_OBSERVE, MODE_RESET, MODE_PROBE, MODE_FLUSH = 0, 1, 2, 3, 4
 MAP_PILLARS, MAP_OPEN, MAP_REFERENCE = 0, 1, 2
@@ -56,7 +56,8 @@ class TickArgsC(ctypes.Structure):
         (n, _vp) for n in ("cells", "players", "envs", "actions", "actions_i8", "crate_u",
                            "reset_mask", "reward", "done", "n_alive", "died", "winner",
                            "covered", "triggered", "obs", "move_mask", "bomb_mask",
-                           "probe_out", "damaged", "recycle_excl")] + [("opp_boost", _i32)]
+                           "probe_out", "damaged", "recycle_excl")] + [("opp_boost", _i32),
+                                                                        ("danger_out", _vp)]
 
 
 class MlpArgsC(ctypes.Structure):

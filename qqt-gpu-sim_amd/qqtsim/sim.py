@@ -193,7 +193,7 @@ class HipBatchedSim:
 
     # ---------------------------------------------------------------- launch
     def _launch(self, mode, actions=None, crate_u=None, reset_mask=None, auto_reset=True,
-                outputs=True, epoch=None):
+                outputs=True, epoch=None, danger_out=None):
         a = _capi.TickArgsC()
         a.n_envs = self.num_envs
         a.mode = mode
@@ -231,6 +231,7 @@ class HipBatchedSim:
             a.probe_out = self._probe.data_ptr()
         if mode == _capi.MODE_FLUSH:
             a.recycle_excl = self.recycle_excl().data_ptr()
+        a.danger_out = _capi.ptr(danger_out)
         _capi.check(self._lib.qqt_tick(self._cfg_c, a, _capi.stream_handle(self.device)))
 
     def _as_device(self, t, dtype, shape):
@@ -294,6 +295,18 @@ class HipBatchedSim:
         """(move_mask (N,P,5) bool, bomb_mask (N,P,2) bool) of the current state."""
         self._refresh()
         return self._mm.view(torch.bool), self._bm.view(torch.bool)
+
+    def danger(self) -> torch.Tensor:
+        """(N, H, W) float32 danger map of the current state, as the
+        reference's `_danger_c()` / `blast.danger_map` gives it
+        (sim/torch_sim.py:732-762, sim/blast.py:158-317); the observation's
+        danger channel is its float16 rounding.  One OBSERVE launch, which
+        also refreshes the observation and masks."""
+        out = torch.empty((self.num_envs, self.cfg.height, self.cfg.width),
+                          dtype=torch.float32, device=self.device)
+        self._launch(_capi.MODE_OBSERVE, danger_out=out)
+        self._fresh = True
+        return out
 
     # ---------------------------------------------------------------- state
     def state_dict(self) -> dict:
