@@ -280,6 +280,20 @@ typedef struct qqt_l1_grad_args {
 int64_t qqt_l1_grad_workspace_floats(int32_t batch, int32_t k0);
 int qqt_l1_grad(const qqt_l1_grad_args* args, void* stream);
 
+/* qqt_l1_grad without a caller workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  The chunk partials
+ * go to a file-scope device array of 32 x 128 x QQT_L1_GRAD_NOALLOC_MAX_K0
+ * floats (40 MiB, one per GPU, held until the process ends); `workspace`
+ * and `workspace_floats` are ignored.  Any batch size; k0 at most
+ * QQT_L1_GRAD_NOALLOC_MAX_K0 (larger is QQT_E_ARG).  The result equals
+ * qqt_l1_grad's bit for bit (same plan, same kernels).  The call allocates
+ * nothing: its first call on a device looks up the array's address there.
+ * Every element of the array that a call reads, the same call wrote first;
+ * calls that overlap on one GPU (different streams) race on the array. */
+#define QQT_L1_GRAD_NOALLOC_MAX_K0 2560
+int qqt_l1_grad_noalloc(const qqt_l1_grad_args* args, void* stream);
+
 /* The PPO minibatch loss and its backward above the first layer, fused
  * (train/ppo.py:401-421 through train/model.py:140-153, 192-196, 215-256):
  * from z1 = x W0^T + b0 per row, LayerNorm/ReLU, Linear(128,128),

@@ -28,6 +28,8 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "qqt_common.h"
 #include "qqt_hip.h"
 
@@ -198,6 +200,44 @@ __host__ inline void plan(int batch, int& chunks, int& chunk_rows) {
 }
 
 }  // namespace l1g
+
+// Scratch of qqt_l1_grad_noalloc: the chunk partials of the largest plan
+// (MAX_CHUNKS chunks of 128 x QQT_L1_GRAD_NOALLOC_MAX_K0 columns), one copy
+// per GPU, held until the process ends.  Host code never passes this name
+// to a kernel (on the host it is only a stand-in for the symbol): it uses
+// the device address hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) float
+    l1g_scratch[l1g::MAX_CHUNKS * l1g::HID * QQT_L1_GRAD_NOALLOC_MAX_K0];
+
+namespace l1g {
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[MAX_DEVICES] = {};
+
+// The scratch's device address on the current device, looked up once per
+// device (with that device current); nullptr with g_err set on failure.
+float* scratch_on_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
+    snprintf(g_err, sizeof(g_err), "qqt_l1_grad_noalloc: no usable current device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(l1g_scratch));
+    if (err != hipSuccess || !p) {
+      snprintf(g_err, sizeof(g_err), "qqt_l1_grad_noalloc: hipGetSymbolAddress failed: %s",
+               hipGetErrorString(err));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace l1g
 }  // namespace qqt
 
 extern "C" {
@@ -211,34 +251,39 @@ int64_t qqt_l1_grad_workspace_floats(int32_t batch, int32_t k0) {
   return (int64_t)chunks * HID * tiles * NCOL;
 }
 
-int qqt_l1_grad(const qqt_l1_grad_args* a, void* stream) {
+namespace {
+
+// Shape checks shared by both entry points (the workspace is checked by the
+// caller of each).
+int l1_grad_check(const qqt_l1_grad_args* a, const char* who) {
   using namespace qqt;
-  using namespace qqt::l1g;
-  g_err[0] = 0;
-  if (!a || !a->obs || !a->dz1 || !a->workspace || !a->dw0) {
-    snprintf(g_err, sizeof(g_err), "qqt_l1_grad: null argument");
+  if (!a || !a->obs || !a->dz1 || !a->dw0) {
+    snprintf(g_err, sizeof(g_err), "%s: null argument", who);
     return QQT_E_ARG;
   }
   if (a->batch <= 0 || a->k0 <= 0 || (a->k0 & 1) || a->obs_stride < a->k0 ||
       (a->obs_stride & 1) || (((uintptr_t)a->obs) & 3) || (((uintptr_t)a->dz1) & 7)) {
-    snprintf(g_err, sizeof(g_err), "qqt_l1_grad: bad shape/stride/alignment");
+    snprintf(g_err, sizeof(g_err), "%s: bad shape/stride/alignment", who);
     return QQT_E_ARG;
   }
-  if (a->workspace_floats < qqt_l1_grad_workspace_floats(a->batch, a->k0)) {
-    snprintf(g_err, sizeof(g_err), "qqt_l1_grad: workspace too small");
-    return QQT_E_ARG;
-  }
+  return QQT_OK;
+}
+
+// Both launches over a checked argument block whose workspace holds the
+// plan's partials.
+int l1_grad_launch(const qqt_l1_grad_args& a, hipStream_t st) {
+  using namespace qqt;
+  using namespace qqt::l1g;
   int chunks, rows;
-  plan(a->batch, chunks, rows);
-  const int tiles = (a->k0 + NCOL - 1) / NCOL;
+  plan(a.batch, chunks, rows);
+  const int tiles = (a.k0 + NCOL - 1) / NCOL;
   const int ws_cols = tiles * NCOL;
-  hipStream_t st = (hipStream_t)stream;
-  QQT_LAUNCH(QQT_KERNEL_L1GRAD, l1_grad_kernel, dim3(tiles, chunks), dim3(NT), st, *a, rows,
+  QQT_LAUNCH(QQT_KERNEL_L1GRAD, l1_grad_kernel, dim3(tiles, chunks), dim3(NT), st, a, rows,
              ws_cols);
   hipError_t err = hipGetLastError();
   if (err == hipSuccess) {
-    const int n = HID * a->k0;
-    QQT_LAUNCH(QQT_KERNEL_L1GRAD, l1_grad_reduce, dim3((n + 255) / 256), dim3(256), st, *a,
+    const int n = HID * a.k0;
+    QQT_LAUNCH(QQT_KERNEL_L1GRAD, l1_grad_reduce, dim3((n + 255) / 256), dim3(256), st, a,
                chunks, ws_cols);
     err = hipGetLastError();
   }
@@ -247,6 +292,45 @@ int qqt_l1_grad(const qqt_l1_grad_args* a, void* stream) {
     return QQT_E_LAUNCH;
   }
   return QQT_OK;
+}
+
+}  // namespace
+
+int qqt_l1_grad(const qqt_l1_grad_args* a, void* stream) {
+  using namespace qqt;
+  g_err[0] = 0;
+  if (const int rc = l1_grad_check(a, "qqt_l1_grad")) return rc;
+  if (!a->workspace) {
+    snprintf(g_err, sizeof(g_err), "qqt_l1_grad: null workspace");
+    return QQT_E_ARG;
+  }
+  if (a->workspace_floats < qqt_l1_grad_workspace_floats(a->batch, a->k0)) {
+    snprintf(g_err, sizeof(g_err), "qqt_l1_grad: workspace too small");
+    return QQT_E_ARG;
+  }
+  return l1_grad_launch(*a, (hipStream_t)stream);
+}
+
+int qqt_l1_grad_noalloc(const qqt_l1_grad_args* a, void* stream) {
+  using namespace qqt;
+  g_err[0] = 0;
+  if (const int rc = l1_grad_check(a, "qqt_l1_grad_noalloc")) return rc;
+  if (a->k0 > QQT_L1_GRAD_NOALLOC_MAX_K0) {
+    snprintf(g_err, sizeof(g_err),
+             "qqt_l1_grad_noalloc: k0 = %d exceeds the static scratch's maximum of %d columns",
+             a->k0, QQT_L1_GRAD_NOALLOC_MAX_K0);
+    return QQT_E_ARG;
+  }
+  float* const ptr = l1g::scratch_on_current_device();
+  if (!ptr) return QQT_E_LAUNCH;
+  qqt_l1_grad_args b = *a;          // the caller's workspace fields are ignored
+  b.workspace = ptr;
+  b.workspace_floats = (int64_t)l1g::MAX_CHUNKS * l1g::HID * QQT_L1_GRAD_NOALLOC_MAX_K0;
+  if (b.workspace_floats < qqt_l1_grad_workspace_floats(b.batch, b.k0)) {
+    snprintf(g_err, sizeof(g_err), "qqt_l1_grad_noalloc: plan exceeds the static scratch");
+    return QQT_E_ARG;
+  }
+  return l1_grad_launch(b, (hipStream_t)stream);
 }
 
 }  // extern "C"

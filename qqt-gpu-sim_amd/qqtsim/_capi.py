@@ -135,6 +135,8 @@ def lib():
         L.qqt_gae.argtypes = [ctypes.POINTER(GaeArgsC), _vp]
         L.qqt_l1_grad.restype = ctypes.c_int
         L.qqt_l1_grad.argtypes = [ctypes.POINTER(L1GradArgsC), _vp]
+        L.qqt_l1_grad_noalloc.restype = ctypes.c_int
+        L.qqt_l1_grad_noalloc.argtypes = [ctypes.POINTER(L1GradArgsC), _vp]
         L.qqt_l1_grad_workspace_floats.restype = ctypes.c_int64
         L.qqt_l1_grad_workspace_floats.argtypes = [_i32, _i32]
         L.qqt_ppo_grad.restype = ctypes.c_int

@@ -40,7 +40,8 @@ def _declared_functions():
 
 def test_header_declares_the_entry_points():
     assert _declared_functions() == ["qqt_abi_version", "qqt_bot_act", "qqt_cnn_act", "qqt_gae",
-                                     "qqt_l1_grad", "qqt_l1_grad_workspace_floats",
+                                     "qqt_l1_grad", "qqt_l1_grad_noalloc",
+                                     "qqt_l1_grad_workspace_floats",
                                      "qqt_last_error", "qqt_mlp_act", "qqt_ppo_grad", "qqt_tick",
                                      "qqt_timing_arm", "qqt_timing_collect"]
 
