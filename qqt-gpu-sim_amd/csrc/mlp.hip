@@ -239,19 +239,170 @@ __device__ __forceinline__ void split_gemm(floatx4 (&acc)[RT][CT], const uint16_
       ah[i] = read_a(a_hi, width, 16 * (rt0 + i) + r16, kb, q);
       al[i] = read_a(a_lo, width, 16 * (rt0 + i) + r16, kb, q);
     }
+    // the six products of each (row tile, column tile) pair in turn over all
+    // pairs: consecutive MFMAs never wait for each other's accumulator
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      const Frag16& bh = b.hi[kb][ct];
-      const Frag16& bl = b.lo[kb][ct];
+    for (int p = 0; p < 6; ++p)
 #pragma unroll
-      for (int i = 0; i < RT; ++i) {
-        acc[i][ct] = mfma(ah[i].lo, bh.lo, acc[i][ct]);
-        acc[i][ct] = mfma(ah[i].hi, bh.hi, acc[i][ct]);
-        acc[i][ct] = mfma(ah[i].lo, bl.lo, acc[i][ct]);
-        acc[i][ct] = mfma(ah[i].hi, bl.hi, acc[i][ct]);
-        acc[i][ct] = mfma(al[i].lo, bh.lo, acc[i][ct]);
-        acc[i][ct] = mfma(al[i].hi, bh.hi, acc[i][ct]);
+      for (int ct = 0; ct < CT; ++ct) {
+        const Frag16& bv = (p == 2 || p == 3) ? b.lo[kb][ct] : b.hi[kb][ct];
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+          const Frag16& av = p < 4 ? ah[i] : al[i];
+          acc[i][ct] = (p & 1) ? mfma(av.hi, bv.hi, acc[i][ct]) : mfma(av.lo, bv.lo, acc[i][ct]);
+        }
       }
+  }
+}
+
+// Sampling inputs of one row (threads < 64 of a row block): masks and the
+// two uniforms (move, bomb).
+struct RowSampler {
+  bool on;
+  uint8_t mm[5], bm[2];
+  float um, ub;
+};
+
+// Masks and uniforms of output row `row` for player pid (Philox when the
+// caller passes no uniforms).
+__device__ __forceinline__ RowSampler load_sampler(const qqt_mlp_args& a, bool on, int row, int pid,
+                                                   int oslots, int oslot) {
+  RowSampler r;
+  r.on = on;
+#pragma unroll
+  for (int k = 0; k < 5; ++k) r.mm[k] = 0;
+  r.bm[0] = r.bm[1] = 0;
+  r.um = r.ub = 0.0f;
+  if (on) {
+#pragma unroll
+    for (int k = 0; k < 5; ++k)
+      r.mm[k] = a.move_mask[(size_t)row * a.mm_row_stride + (size_t)pid * a.mm_pid_stride + k];
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      r.bm[k] = a.bomb_mask[(size_t)row * a.bm_row_stride + (size_t)pid * a.bm_pid_stride + k];
+    const size_t o = (size_t)row * oslots + oslot;
+    if (a.uniforms) {
+      r.um = a.uniforms[o * 2 + 0];
+      r.ub = a.uniforms[o * 2 + 1];
+    } else {
+      float u4[4];
+      philox_block(a.seed, (uint32_t)row, a.tick, STREAM_POLICY, (uint32_t)((2 * pid) >> 2), u4);
+      r.um = u4[(2 * pid) & 3];
+      r.ub = u4[(2 * pid + 1) & 3];
+    }
+  }
+  return r;
+}
+
+// Everything after the first layer for one 64-row block (512 threads):
+// bias + LayerNorm 1 (s.f plus the second partial tile f1 when given) +
+// ReLU, Linear(128,128), LayerNorm 2 + ReLU, the heads' hidden and output
+// layers, then the outputs and the masked sampling, one thread per row.
+// w1b holds the layer-2 B fragments, already in flight.  H1, H2 and HY are
+// LDS planes; HY may overlay f1 and H1 (both dead by then).
+template <class L>
+__device__ __forceinline__ void mlp_tail(L& s, const qqt_mlp_args& a, const uint16_t* f1,
+                                         uint16_t* H1, uint16_t* H2, uint16_t* HY, int brow0,
+                                         int oslots, int oslot, const RowSampler& rs,
+                                         const SplitB<2, 2>& w1b) {
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int r16 = lane & 15, q = lane >> 4;
+  const int cg = w & 3, rh = w >> 2;      // column group, row half of the small layers
+  layernorm_rows(s, f1, V_B0, V_G1, V_BE1, H1);
+  __syncthreads();
+
+  // ---------------- layer 2: 128 -> 128; wavefront w: rows 32rh.., columns 32cg..
+  floatx4 acc2[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) acc2[i][ct] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  split_gemm<2, 2, 2>(acc2, H1, H1 + ROWS * HID, HID, 2 * rh, w1b, lane);
+  SplitB<3, 2> whb;                 // head weights: in flight during LayerNorm 2
+  load_split_b(whb, a.wh, a.wh_lo, 3 * cg, lane);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        s.f[32 * rh + 16 * i + 4 * q + j][32 * cg + 16 * ct + r16] = acc2[i][ct][j];
+  __syncthreads();
+  layernorm_rows(s, nullptr, V_B1, V_G2, V_BE2, H2);
+  __syncthreads();
+
+  // ---------------- heads, first layer: 128 -> 192; rows 32rh.., columns 48cg..
+  {
+    floatx4 hac[2][3];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int ct = 0; ct < 3; ++ct) hac[i][ct] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    split_gemm<2, 3, 2>(hac, H2, H2 + ROWS * HID, HID, 2 * rh, whb, lane);
+#pragma unroll
+    for (int ct = 0; ct < 3; ++ct) {
+      const int col = 48 * cg + 16 * ct + r16;
+      const float b = s.vec[V_BH + col];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int row = 32 * rh + 16 * i + 4 * q + j;
+          split_store(h_at(HY, 3 * HEAD, 0, row, col), h_at(HY, 3 * HEAD, 1, row, col),
+                      fmaxf(hac[i][ct][j] + b, 0.0f));
+        }
+    }
+  }
+  __syncthreads();
+
+  // ---------------- heads, output layer: 192 -> 8 (block diagonal); wavefronts 0-3: rows 16w..
+  if (w < 4) {
+    floatx4 oac = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kb = 0; kb < 3; ++kb) {
+      const Frag16 bh = load_b(&s.wf[0][(kb * 64 + lane) * 16]);
+      const Frag16 bl = load_b(&s.wf[1][(kb * 64 + lane) * 16]);
+      const int row = 16 * w + r16;
+      const Frag16 ah = read_a(HY, 3 * HEAD, row, kb, q);
+      const Frag16 al = read_a(HY + ROWS * 3 * HEAD, 3 * HEAD, row, kb, q);
+      oac = mfma(ah.lo, bh.lo, oac);
+      oac = mfma(ah.hi, bh.hi, oac);
+      oac = mfma(ah.lo, bl.lo, oac);
+      oac = mfma(ah.hi, bl.hi, oac);
+      oac = mfma(al.lo, bh.lo, oac);
+      oac = mfma(al.hi, bh.hi, oac);
+    }
+    if (r16 < NOUT) {
+      const float b = s.vec[V_BF + r16];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s.logit[16 * w + 4 * q + j][r16] = oac[j] + b;
+    }
+  }
+  __syncthreads();
+
+  // ---------------- outputs and sampling: one thread per row
+  const int orow = brow0 + (int)threadIdx.x;
+  if (threadIdx.x < ROWS && orow < a.batch) {
+    const float* lg = s.logit[threadIdx.x];
+    const size_t o = (size_t)orow * oslots + oslot;
+    if (a.logits_out) {
+#pragma unroll
+      for (int k = 0; k < NOUT; ++k) a.logits_out[o * NOUT + k] = lg[k];
+    }
+    if (a.value_out) a.value_out[o] = lg[7];
+    if (rs.on) {
+      float lpm, lpb;
+      const int am = sample_masked<5>(lg, rs.mm, rs.um, &lpm);
+      const int ab = sample_masked<2>(lg + 5, rs.bm, rs.ub, &lpb);
+      if (a.actions) {
+        a.actions[o * 2 + 0] = am;
+        a.actions[o * 2 + 1] = ab;
+      }
+      if (a.actions_i8) {
+        a.actions_i8[o * 2 + 0] = (int8_t)am;
+        a.actions_i8[o * 2 + 1] = (int8_t)ab;
+      }
+      if (a.logp_out) a.logp_out[o] = lpm + lpb;
     }
   }
 }
@@ -349,15 +500,18 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   };
   auto compute = [&](int buf, const Frag16 (&br)[2]) {
     const uint16_t* t = xt + buf * XT;
+    Frag16 af[RT];
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      const Frag16 af = read_a(t, 64, 16 * rt + r16, 0, q);
+    for (int rt = 0; rt < RT; ++rt) af[rt] = read_a(t, 64, 16 * rt + r16, 0, q);
+    // low K halves over every tile pair, then the high halves
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        acc[rt][ct] = mfma(af.lo, br[ct].lo, acc[rt][ct]);
-        acc[rt][ct] = mfma(af.hi, br[ct].hi, acc[rt][ct]);
-      }
-    }
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+          acc[rt][ct] = h ? mfma(af[rt].hi, br[ct].hi, acc[rt][ct])
+                          : mfma(af[rt].lo, br[ct].lo, acc[rt][ct]);
   };
 
   // Group step i handles K block 2i + kg.  Register ring of PD steps in
@@ -377,27 +531,8 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   }
 
   const int srow = row0 + (int)threadIdx.x;          // sampling row of threads < 64
-  const bool sampler = RB == 1 && threadIdx.x < ROWS && srow < a.batch && a.sample;
-  uint8_t mm[5] = {0, 0, 0, 0, 0}, bm[2] = {0, 0};
-  float um = 0.0f, ub = 0.0f;
-  if (sampler) {
-#pragma unroll
-    for (int k = 0; k < 5; ++k)
-      mm[k] = a.move_mask[(size_t)srow * a.mm_row_stride + (size_t)pid * a.mm_pid_stride + k];
-#pragma unroll
-    for (int k = 0; k < 2; ++k)
-      bm[k] = a.bomb_mask[(size_t)srow * a.bm_row_stride + (size_t)pid * a.bm_pid_stride + k];
-    const size_t o = (size_t)srow * oslots + oslot;
-    if (a.uniforms) {
-      um = a.uniforms[o * 2 + 0];
-      ub = a.uniforms[o * 2 + 1];
-    } else {
-      float u4[4];
-      philox_block(a.seed, (uint32_t)srow, a.tick, STREAM_POLICY, (uint32_t)((2 * pid) >> 2), u4);
-      um = u4[(2 * pid) & 3];
-      ub = u4[(2 * pid + 1) & 3];
-    }
-  }
+  const RowSampler rs = load_sampler(a, RB == 1 && threadIdx.x < ROWS && srow < a.batch && a.sample,
+                                     srow, pid, oslots, oslot);
 
   s.vec[vi0] = vv0;
   if (vi1 < V_N) s.vec[vi1] = vv1;
@@ -471,104 +606,7 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
     if (hb + 1 < RB) __syncthreads();   // the next block rewrites both tiles
     continue;
   }
-  layernorm_rows(s, s.xs_h1, V_B0, V_G1, V_BE1, H1);
-  __syncthreads();
-
-  // ---------------- layer 2: 128 -> 128; wavefront w: rows 32rh.., columns 32cg..
-  floatx4 acc2[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) acc2[i][ct] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-  split_gemm<2, 2, 2>(acc2, H1, H1 + ROWS * HID, HID, 2 * rh, w1b, lane);
-  SplitB<3, 2> whb;                 // head weights: in flight during LayerNorm 2
-  load_split_b(whb, a.wh, a.wh_lo, 3 * cg, lane);
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        s.f[32 * rh + 16 * i + 4 * q + j][32 * cg + 16 * ct + r16] = acc2[i][ct][j];
-  __syncthreads();
-  layernorm_rows(s, nullptr, V_B1, V_G2, V_BE2, H2);
-  __syncthreads();
-
-  // ---------------- heads, first layer: 128 -> 192; rows 32rh.., columns 48cg..
-  uint16_t* const HY = s.xs_h1;     // the x tiles (and with RB = 1 h1) are dead from here on
-  {
-    floatx4 hac[2][3];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int ct = 0; ct < 3; ++ct) hac[i][ct] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    split_gemm<2, 3, 2>(hac, H2, H2 + ROWS * HID, HID, 2 * rh, whb, lane);
-#pragma unroll
-    for (int ct = 0; ct < 3; ++ct) {
-      const int col = 48 * cg + 16 * ct + r16;
-      const float b = s.vec[V_BH + col];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int row = 32 * rh + 16 * i + 4 * q + j;
-          split_store(h_at(HY, 3 * HEAD, 0, row, col), h_at(HY, 3 * HEAD, 1, row, col),
-                      fmaxf(hac[i][ct][j] + b, 0.0f));
-        }
-    }
-  }
-  __syncthreads();
-
-  // ---------------- heads, output layer: 192 -> 8 (block diagonal); wavefronts 0-3: rows 16w..
-  if (w < 4) {
-    floatx4 oac = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int kb = 0; kb < 3; ++kb) {
-      const Frag16 bh = load_b(&s.wf[0][(kb * 64 + lane) * 16]);
-      const Frag16 bl = load_b(&s.wf[1][(kb * 64 + lane) * 16]);
-      const int row = 16 * w + r16;
-      const Frag16 ah = read_a(HY, 3 * HEAD, row, kb, q);
-      const Frag16 al = read_a(HY + ROWS * 3 * HEAD, 3 * HEAD, row, kb, q);
-      oac = mfma(ah.lo, bh.lo, oac);
-      oac = mfma(ah.hi, bh.hi, oac);
-      oac = mfma(ah.lo, bl.lo, oac);
-      oac = mfma(ah.hi, bl.hi, oac);
-      oac = mfma(al.lo, bh.lo, oac);
-      oac = mfma(al.hi, bh.hi, oac);
-    }
-    if (r16 < NOUT) {
-      const float b = s.vec[V_BF + r16];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) s.logit[16 * w + 4 * q + j][r16] = oac[j] + b;
-    }
-  }
-  __syncthreads();
-
-  // ---------------- outputs and sampling: one thread per row
-  const int orow = brow0 + (int)threadIdx.x;
-  if (threadIdx.x < ROWS && orow < a.batch) {
-    const float* lg = s.logit[threadIdx.x];
-    const size_t o = (size_t)orow * oslots + oslot;
-    if (a.logits_out) {
-#pragma unroll
-      for (int k = 0; k < NOUT; ++k) a.logits_out[o * NOUT + k] = lg[k];
-    }
-    if (a.value_out) a.value_out[o] = lg[7];
-    if (sampler) {
-      float lpm, lpb;
-      const int am = sample_masked<5>(lg, mm, um, &lpm);
-      const int ab = sample_masked<2>(lg + 5, bm, ub, &lpb);
-      if (a.actions) {
-        a.actions[o * 2 + 0] = am;
-        a.actions[o * 2 + 1] = ab;
-      }
-      if (a.actions_i8) {
-        a.actions_i8[o * 2 + 0] = (int8_t)am;
-        a.actions_i8[o * 2 + 1] = (int8_t)ab;
-      }
-      if (a.logp_out) a.logp_out[o] = lpm + lpb;
-    }
-  }
+  mlp_tail(s, a, s.xs_h1, H1, H2, s.xs_h1, brow0, oslots, oslot, rs, w1b);
   if (hb + 1 < RB) __syncthreads();   // the next block reuses every tail buffer
   }
 }
