@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 12
+#define QQT_ABI_VERSION 13
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -143,7 +143,10 @@ typedef struct qqt_tick_args {
  * w0 (both players' view-permuted first layers), w1, wh (the three head
  * hidden layers stacked), wf (the three output layers, block diagonal, 16
  * padded rows), the float16 residuals of w1/wh/wf (the later layers run as
- * hi/lo pairs), and float32 vectors.  Outputs are indexed [row][player slot]. */
+ * hi/lo pairs), and float32 vectors.  w0 is [tile][64-deep K block][lane][16];
+ * w1/wh/wf are [tile][32-deep K step][lane][8] in the K order in which one
+ * layer's MFMA output tiles feed the next (csrc/mlp.hip documents both).
+ * Outputs are indexed [row][player slot]. */
 typedef struct qqt_mlp_args {
   int32_t batch;             /* rows B */
   int32_t npid;              /* 1: player pid0 only; 2: both players */

@@ -6,31 +6,49 @@
 // A player's view permutation is folded into the first-layer weights, so a
 // player is just a column block of one shared weight buffer.
 //
-// Workgroup = 8 wavefronts (2 per SIMD) = one 64-row block of one player.
-// Both players' workgroups of a row block are dispatched back to back on the
-// same XCD (workgroups are dealt to the 8 XCDs round robin), so the second
-// read of the observation tile hits that XCD's L2.
+// Workgroup = 8 wavefronts (2 per SIMD) = RB 64-row blocks of one player
+// (RB = 1 for rollout batches, 2 for large forward batches).  Both players'
+// workgroups of a row block are dispatched back to back on the same XCD
+// (workgroups are dealt to the 8 XCDs round robin), so the second read of
+// the observation tile hits that XCD's L2.
+//
+// Every product is v_mfma_f32_16x16x32_f16 (float32 accumulation) with the
+// weights as the A operand and the activations as the B operand, so a 16 x 16
+// output tile holds features 4q..4q+3 of batch row r in lane 16q + r
+// (q = lane / 16).
 //
 // Layer 1 (K = 2366) is split over two groups of four wavefronts: group g
-// takes K blocks g, g+2, g+4, ...  Each group streams its 64 x 64 observation
-// tiles through its own double-buffered, XOR-swizzled LDS tile (loaded PD
-// steps ahead into registers); the weight fragments go straight from L2 into
-// registers, PD steps ahead.  Wavefront (g, c) owns output columns
-// 32c..32c+31.  The two groups' partial sums meet in an fp32 LDS tile, where
-// LayerNorm runs row-wise (8 lanes per row, 16 contiguous columns per lane).
-// The small layers split rows and columns over all eight wavefronts.
+// takes K blocks g, g+2, g+4, ...  Each group streams its observation tiles
+// (RB*64 rows x 64 K) through its own double-buffered, XOR-swizzled LDS tile
+// (loaded PD steps ahead into registers); the weight fragments go straight
+// from L2 into registers, PD steps ahead.  Wavefront (g, c) owns features
+// 32c..32c+31 of every row.  The groups' partial sums meet in LDS (group 1
+// writes, group 0 adds), laid out by (row tile, feature tile, lane).
 //
-// Every product runs on v_mfma_f32_16x16x32_f16 with float32 accumulation.
-// The observation is exact in float16 and the first layer's weights are
-// rounded to float16 once; every later layer carries both its activations
-// and its weights as float16 hi/lo pairs (x = hi + lo) and sums the three
-// products hi*hi + hi*lo + lo*hi, which keeps logits within ~5e-4 of a
-// float32 forward even for large (orthogonal, gain sqrt 2) weights.  B
-// operands are pre-arranged on the host (qqtsim/policy.py) so each lane reads
-// 32 contiguous bytes per 64-deep K block:
-//   frag[tile][kblock][lane][16] = W[16*tile + lane%16][64*kblock + 16*(lane/16) + j].
-// The matching A fragment is the lane's 16 contiguous halves of its row, so
-// the K order inside a block is a permutation shared by A and B.
+// Everything after layer 1 runs per 16-row tile inside one wavefront, in
+// registers (wavefront w takes row tile w; with RB = 1 wavefronts 4-7 only
+// help stage weights).  A row's 128 features sit in lanes r, r+16, r+32,
+// r+48, so LayerNorm reduces with two cross-lane exchanges, and the output
+// tiles of one product are, unchanged, the B operand of the next: K step s
+// of the next product reads feature tiles 2s and 2s+1, i.e. MFMA K index
+// 8q + i is feature 32s + 4q + i (i < 4) or 32s + 16 + 4q + (i - 4) (i >= 4);
+// the host stores the later layers' weights in that K order.  Those layers
+// carry activations and weights as float16 hi/lo pairs (x = hi + lo) and sum
+// hi*hi + hi*lo + lo*hi, which keeps logits within ~5e-4 of a float32 forward
+// even for large (orthogonal, gain sqrt 2) weights.  Their weights are read
+// from LDS: layer 2's (64 KB, both planes) is staged in the prologue; the
+// heads' (96 KB) is loaded into registers while layer 2 runs and written over
+// layer 2's weights and the dead observation tiles once every tail wavefront
+// is past layer 2.
+//
+// Fragment layouts (built by qqtsim/policy.py):
+//   w0:          frag[tile][kblock][lane][16] =
+//                  W[16*tile + lane%16][64*kblock + 16*(lane/16) + j];
+//                the observation row's 16 halves at the same K offsets form
+//                the B operand (a K order inside the block shared by both);
+//   w1, wh, wf:  frag[tile][kstep][lane][8] =
+//   (hi and lo)    W[16*tile + lane%16][32*kstep + perm(lane/16, i)],
+//                perm(q, i) = 4q + i (i < 4), 16 + 4q + (i - 4) (i >= 4).
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -44,6 +62,7 @@ namespace qqt {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // 16 bytes staged global -> LDS
 
 constexpr int HID = 128;           // hidden width
 constexpr int HEAD = 64;           // head hidden width
@@ -51,7 +70,6 @@ constexpr int NOUT = 8;            // 5 move + 2 bomb + 1 value
 constexpr int ROWS = 64;           // rows per block (a workgroup takes one or two)
 constexpr int MLP_TWO_BLOCK_ROWS = 1 << 16;   // forward batches from here use two blocks
 constexpr int NTHR = 512;          // 8 wavefronts
-constexpr int FST = HID + 4;       // fp32 row stride of the LayerNorm tile (bank spread)
 #ifndef QQT_MLP_PD
 #define QQT_MLP_PD 2
 #endif
@@ -62,6 +80,11 @@ static_assert(PD >= 2 && PD % 2 == 0, "the x tile ring pairs with an LDS double 
 constexpr int V_B0 = 0, V_G1 = 128, V_BE1 = 256, V_B1 = 384, V_G2 = 512, V_BE2 = 640;
 constexpr int V_BH = 768, V_BF = 960, V_N = 968;
 
+constexpr int XT_HALVES = ROWS * 64;         // one 64-row x 64-K observation tile (8 KB)
+constexpr int W1_HALVES = HID * HID;         // one plane of the layer-2 fragments (32 KB)
+constexpr int WH_HALVES = 3 * HEAD * HID;    // one plane of the head-layer fragments (48 KB)
+constexpr int WF_HALVES = 16 * 3 * HEAD;     // one plane of the output-layer fragments (6 KB)
+
 struct Frag16 { half8 lo, hi; };   // 16 halves of one lane in one K block
 
 __device__ __forceinline__ half8 as_h8(uint4 v) {
@@ -70,7 +93,7 @@ __device__ __forceinline__ half8 as_h8(uint4 v) {
   return c.h;
 }
 
-// 32 bytes of a B fragment (32-byte aligned in the packed weight buffers).
+// 32 bytes of a first-layer weight fragment (32-byte aligned in w0).
 __device__ __forceinline__ Frag16 load_b(const uint16_t* p) {
   const uint4* q = reinterpret_cast<const uint4*>(p);
   Frag16 f;
@@ -79,343 +102,222 @@ __device__ __forceinline__ Frag16 load_b(const uint16_t* p) {
   return f;
 }
 
+// d = A B + c; A: weights (16 features x 32 K), B: activations (32 K x 16 rows).
 __device__ __forceinline__ floatx4 mfma(half8 a, half8 b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// LDS tiles store rows of float16 in 16-byte chunks; chunk c of row r sits at
-// chunk position c ^ (r & 7), so the 16 rows of an A fragment read land on
-// distinct banks.
-__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ (row & 7); }
+// Observation tiles store rows of 64 float16 as eight 16-byte chunks; chunk c
+// of row r sits at position c ^ (r & 7) ^ ((r >> 3) & 1).  The 16 rows of one
+// fragment read then land on 16 distinct 16-byte bank groups of a 256-byte
+// bank window (row r's window half is r & 1), and any 8 consecutive rows on 8
+// distinct groups of a 128-byte window.
+__device__ __forceinline__ int swz(int row, int chunk) {
+  return chunk ^ (row & 7) ^ ((row >> 3) & 1);
+}
 
-constexpr int XT_HALVES = ROWS * 64;            // one 64 x 64 observation tile (8 KB)
-constexpr int H_HALVES = 2 * ROWS * HID;        // hi + lo planes of h1 or h2 (32 KB)
-constexpr int HY_HALVES = 2 * ROWS * 3 * HEAD;  // hi + lo planes of the head layer (48 KB)
-static_assert(HY_HALVES <= 4 * XT_HALVES + H_HALVES, "head layer reuses the x tiles and h1");
-static_assert(HY_HALVES <= 8 * XT_HALVES, "two-block head layer fits in the x tiles alone");
-static_assert(ROWS * HID * 2 <= 4 * XT_HALVES, "the second partial tile fits in the x tiles");
-
-constexpr int WF_HALVES = 3 * 64 * 16;          // output layer: 1 column tile x 3 K blocks
-constexpr int WF_CHUNKS = 2 * WF_HALVES / 8;    // 16-byte chunks of both planes
-
-// LDS of a workgroup of RB 64-row blocks.  xs_h1 holds the layer-1 x tiles
-// (RB x 32 KB), then h1; the tail reuses the x tiles for the second partial
-// tile and the head layer.  With RB = 1 the head layer spills over into the
-// dead h1 and h2 has its own region; with RB = 2 the x tiles alone hold the
-// head layer and h2 reuses h1 (dead once layer 2 has read it).
+// LDS of a workgroup of RB 64-row blocks.  xw holds the layer-1 x tiles
+// [group][buffer] and then layer 2's weight planes; after layer 1 the
+// partial-sum exchange reuses the x tiles, and after layer 2 the head
+// weights overwrite the x tiles and layer 2's weights.
 template <int RB>
 struct __align__(16) MlpLds {
-  uint16_t xs_h1[RB * 4 * XT_HALVES + H_HALVES];   // x tiles [group][buffer] | h1
-  uint16_t h2[RB == 1 ? H_HALVES : 8];
-  float f[ROWS][FST];                         // fp32 pre-LayerNorm tile
+  uint16_t xw[RB * 4 * XT_HALVES + 2 * W1_HALVES];
+  uint16_t wf[2 * WF_HALVES];                 // output-layer fragments, hi and lo planes
   float vec[V_N];                             // biases and LayerNorm affine parameters
-  float logit[ROWS][NOUT];
-  uint16_t wf[2][WF_HALVES];                  // output-layer B fragments, hi and lo planes
 };
+static_assert(2 * WH_HALVES <= 4 * XT_HALVES + 2 * W1_HALVES, "head weights fit over x | W1");
+static_assert(4 * 8 * 64 * 4 * sizeof(float) <= 4 * XT_HALVES * sizeof(uint16_t),
+              "the partial-sum exchange of a 64-row block fits in its x tiles");
 
-__device__ __forceinline__ uint16_t* h_at(uint16_t* base, int width, int plane, int row, int col) {
-  return base + (plane * ROWS + row) * width + (swz(row, col >> 3) << 3) + (col & 7);
-}
-__device__ __forceinline__ void split_store(uint16_t* hi, uint16_t* lo, float y) {
-  const __half h = __float2half_rn(y);
-  *hi = __half_as_ushort(h);
-  *lo = __half_as_ushort(__float2half_rn(y - __half2float(h)));
-}
-// A fragment (16 halves) of row `row`, K block kb, from a swizzled tile.
-__device__ __forceinline__ Frag16 read_a(const uint16_t* plane, int width, int row, int kb, int q) {
-  const uint16_t* r = plane + row * width;
-  const int c = 8 * kb + 2 * q;
+// The B fragment (16 halves of row `row`, K 16q..16q+15 of the block) from a
+// swizzled 64-K observation tile.
+__device__ __forceinline__ Frag16 read_x(const uint16_t* tile, int row, int q) {
+  const uint16_t* r = tile + row * 64;
   Frag16 f;
-  f.lo = as_h8(*reinterpret_cast<const uint4*>(r + (swz(row, c) << 3)));
-  f.hi = as_h8(*reinterpret_cast<const uint4*>(r + (swz(row, c + 1) << 3)));
+  f.lo = as_h8(*reinterpret_cast<const uint4*>(r + (swz(row, 2 * q) << 3)));
+  f.hi = as_h8(*reinterpret_cast<const uint4*>(r + (swz(row, 2 * q + 1) << 3)));
   return f;
 }
 
-// Sum over the 8 consecutive lanes that hold one row in the LayerNorm phase.
-__device__ __forceinline__ float sum8(float v) {
-  v += __shfl_xor(v, 1, 64);
-  v += __shfl_xor(v, 2, 64);
-  v += __shfl_xor(v, 4, 64);
-  return v;
+// This lane's four values of feature tile t of an LDS parameter vector
+// (features 16t + 4q .. +3).
+__device__ __forceinline__ floatx4 vec4(const float* v, int t, int q) {
+  return *reinterpret_cast<const floatx4*>(v + 16 * t + 4 * q);
 }
 
-// fp32 partial-sum tile of layer 1's second K group, kept in the (dead) x
-// tiles: 64 rows x 128 floats, float4 j of row r stored at j ^ (r & 31).
-__device__ __forceinline__ float* f1_at(uint16_t* xs, int row, int col) {
-  float* base = reinterpret_cast<float*>(xs);
-  return base + row * HID + ((((col >> 2) ^ (row & 31))) << 2) + (col & 3);
+// y (>= 0) -> element e of the float16 hi/lo fragment pair (y = hi + lo).
+__device__ __forceinline__ void split_into(float y, half8& fh, half8& fl, int e) {
+  const _Float16 h = (_Float16)y;
+  fh[e] = h;
+  fl[e] = (_Float16)(y - (float)h);
 }
 
-// Row-wise bias + LayerNorm(128) + ReLU from the fp32 tile (plus the second
-// partial tile f1 when given): thread t owns row t/8; lane j = t%8 of a row
-// owns columns 32i + 4j .. +3 (i = 0..3), so for each i the row's 8 lanes
-// read 128 contiguous bytes (no bank conflicts); writes float16 hi/lo planes
-// of dst as 8-byte stores.
-template <class L>
-__device__ __forceinline__ void layernorm_rows(L& s, const uint16_t* f1, int vb, int vg,
-                                               int vbe, uint16_t* dst) {
-  const int t = threadIdx.x, row = t >> 3, j = t & 7;
-  float v[16], ga[16], be[16];
+// LayerNorm(128) + ReLU of one 16-row tile in output layout (v[t] = features
+// 16t + 4q .. +3 of row lane%16, bias included), then the float16 hi/lo B
+// fragments of the next product (K step s = feature tiles 2s, 2s+1).  The
+// affine parameters are read before the reductions so their LDS latency
+// overlaps them.
+__device__ __forceinline__ void ln_relu_split(const floatx4 (&v)[8], const float* gam,
+                                              const float* bet, int q, half8 (&fh)[4],
+                                              half8 (&fl)[4]) {
+  floatx4 g[8], e[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = 32 * i + 4 * j;
-    const float4 x = *reinterpret_cast<const float4*>(&s.f[row][c]);
-    const float4 b = *reinterpret_cast<const float4*>(&s.vec[vb + c]);
-    const float4 g = *reinterpret_cast<const float4*>(&s.vec[vg + c]);
-    const float4 e = *reinterpret_cast<const float4*>(&s.vec[vbe + c]);
-    float4 y = x;
-    if (f1) {
-      const float4 z = *reinterpret_cast<const float4*>(
-          f1_at(const_cast<uint16_t*>(f1), row, c));
-      y = make_float4(z.x + x.x, z.y + x.y, z.z + x.z, z.w + x.w);
-    }
-    v[4 * i + 0] = y.x + b.x;
-    v[4 * i + 1] = y.y + b.y;
-    v[4 * i + 2] = y.z + b.z;
-    v[4 * i + 3] = y.w + b.w;
-    ga[4 * i + 0] = g.x; ga[4 * i + 1] = g.y; ga[4 * i + 2] = g.z; ga[4 * i + 3] = g.w;
-    be[4 * i + 0] = e.x; be[4 * i + 1] = e.y; be[4 * i + 2] = e.z; be[4 * i + 3] = e.w;
+  for (int t = 0; t < 8; ++t) {
+    g[t] = vec4(gam, t, q);
+    e[t] = vec4(bet, t, q);
   }
   float p = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) p += v[i];
-  const float mean = sum8(p) * (1.0f / HID);
-  float q = 0.0f;
+  for (int t = 0; t < 8; ++t)
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const float d = v[i] - mean;
-    q += d * d;
-  }
-  const float rstd = 1.0f / sqrtf(sum8(q) * (1.0f / HID) + 1e-5f);
+    for (int j = 0; j < 4; ++j) p += v[t][j];
+  p += __shfl_xor(p, 16, 64);
+  p += __shfl_xor(p, 32, 64);
+  const float mean = p * (1.0f / HID);
+  float d2 = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    uint32_t hi[2], lo[2];
+  for (int t = 0; t < 8; ++t)
 #pragma unroll
-    for (int e = 0; e < 4; e += 2) {
-      const int k = 4 * i + e;
-      const float y0 = fmaxf((v[k] - mean) * rstd * ga[k] + be[k], 0.0f);
-      const float y1 = fmaxf((v[k + 1] - mean) * rstd * ga[k + 1] + be[k + 1], 0.0f);
-      const __half h0 = __float2half_rn(y0), h1 = __float2half_rn(y1);
-      const __half l0 = __float2half_rn(y0 - __half2float(h0));
-      const __half l1 = __float2half_rn(y1 - __half2float(h1));
-      hi[e / 2] = (uint32_t)__half_as_ushort(h0) | ((uint32_t)__half_as_ushort(h1) << 16);
-      lo[e / 2] = (uint32_t)__half_as_ushort(l0) | ((uint32_t)__half_as_ushort(l1) << 16);
+    for (int j = 0; j < 4; ++j) {
+      const float d = v[t][j] - mean;
+      d2 += d * d;
     }
-    const int c = 32 * i + 4 * j;                 // 4 halves = half of chunk c/8
-    const int off = (swz(row, c >> 3) << 3) + (c & 7);
-    *reinterpret_cast<uint2*>(dst + (0 * ROWS + row) * HID + off) = make_uint2(hi[0], hi[1]);
-    *reinterpret_cast<uint2*>(dst + (1 * ROWS + row) * HID + off) = make_uint2(lo[0], lo[1]);
-  }
+  d2 += __shfl_xor(d2, 16, 64);
+  d2 += __shfl_xor(d2, 32, 64);
+  const float rstd = 1.0f / sqrtf(d2 * (1.0f / HID) + 1e-5f);
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      split_into(fmaxf((v[t][j] - mean) * rstd * g[t][j] + e[t][j], 0.0f), fh[t >> 1],
+                 fl[t >> 1], 4 * (t & 1) + j);
 }
 
-// hi and lo B fragments of CT column tiles x KB K blocks (tiles tile0..).
-template <int CT, int KB>
-struct SplitB { Frag16 hi[KB][CT], lo[KB][CT]; };
-template <int CT, int KB>
-__device__ __forceinline__ void load_split_b(SplitB<CT, KB>& b, const uint16_t* b_hi,
-                                             const uint16_t* b_lo, int tile0, int lane) {
+// acc[t] += W(tile t) h over KS K steps: weight fragments from the LDS planes
+// a_hi, a_lo ([tile][kstep][lane][8]), activation fragments bh, bl in
+// registers.  Work goes in chunks of G tiles at one K step; the weight
+// fragments of the next chunk are read while the current one multiplies,
+// and each product runs over the chunk's G independent accumulators before
+// the next product touches them.
+template <int NT, int KS>
+__device__ __forceinline__ void tail_gemm(floatx4 (&acc)[NT], const uint16_t* a_hi,
+                                          const uint16_t* a_lo, const half8 (&bh)[KS],
+                                          const half8 (&bl)[KS], int lane) {
+  constexpr int G = NT < 4 ? NT : 4;
+  static_assert(NT % G == 0, "whole chunks");
+  constexpr int NG = NT / G, NC = KS * NG;   // chunk c: K step c / NG, tiles G * (c % NG) ..
+  half8 fa[2][2][G];                          // [buffer][plane][tile of the chunk]
+  auto fetch = [&](int c, half8 (&f)[2][G]) {
 #pragma unroll
-  for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      const size_t off = ((size_t)((tile0 + ct) * KB + kb) * 64 + lane) * 16;
-      b.hi[kb][ct] = load_b(b_hi + off);
-      b.lo[kb][ct] = load_b(b_lo + off);
+    for (int g = 0; g < G; ++g) {
+      const int off = (((G * (c % NG) + g) * KS + c / NG) * 64 + lane) * 8;
+      f[0][g] = *reinterpret_cast<const half8*>(a_hi + off);
+      f[1][g] = *reinterpret_cast<const half8*>(a_lo + off);
     }
-}
-
-// RT row tiles (rows 16*(rt0+i) + lane%16) x CT column tiles of a hi/lo layer:
-// acc += A(hi,lo) * B(hi,lo) over KB K blocks.
-template <int RT, int CT, int KB>
-__device__ __forceinline__ void split_gemm(floatx4 (&acc)[RT][CT], const uint16_t* a_hi,
-                                           const uint16_t* a_lo, int width, int rt0,
-                                           const SplitB<CT, KB>& b, int lane) {
-  const int r16 = lane & 15, q = lane >> 4;
+  };
+  fetch(0, fa[0]);
 #pragma unroll
-  for (int kb = 0; kb < KB; ++kb) {
-    Frag16 ah[RT], al[RT];
+  for (int c = 0; c < NC; ++c) {
+    if (c + 1 < NC) fetch(c + 1, fa[(c + 1) & 1]);
+    const int s = c / NG, t0 = G * (c % NG);
+    const half8 (&f)[2][G] = fa[c & 1];
 #pragma unroll
-    for (int i = 0; i < RT; ++i) {
-      ah[i] = read_a(a_hi, width, 16 * (rt0 + i) + r16, kb, q);
-      al[i] = read_a(a_lo, width, 16 * (rt0 + i) + r16, kb, q);
-    }
-    // the six products of each (row tile, column tile) pair in turn over all
-    // pairs: consecutive MFMAs never wait for each other's accumulator
+    for (int g = 0; g < G; ++g) acc[t0 + g] = mfma(f[0][g], bh[s], acc[t0 + g]);
 #pragma unroll
-    for (int p = 0; p < 6; ++p)
+    for (int g = 0; g < G; ++g) acc[t0 + g] = mfma(f[0][g], bl[s], acc[t0 + g]);
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        const Frag16& bv = (p == 2 || p == 3) ? b.lo[kb][ct] : b.hi[kb][ct];
-#pragma unroll
-        for (int i = 0; i < RT; ++i) {
-          const Frag16& av = p < 4 ? ah[i] : al[i];
-          acc[i][ct] = (p & 1) ? mfma(av.hi, bv.hi, acc[i][ct]) : mfma(av.lo, bv.lo, acc[i][ct]);
-        }
-      }
+    for (int g = 0; g < G; ++g) acc[t0 + g] = mfma(f[1][g], bh[s], acc[t0 + g]);
   }
 }
 
-// Sampling inputs of one row (threads < 64 of a row block): masks and the
-// two uniforms (move, bomb).
+// sample_masked<5> restricted to the first n entries: entries k >= n get
+// probability exactly zero (even when every real entry is masked), so their
+// terms add exact zeros to the sums and the draw and log-probability equal
+// sample_masked<n>'s.  Lets the move (n = 5) and bomb (n = 2) draws of a row
+// run as one instruction stream on two lanes.
+__device__ __forceinline__ int sample_masked_n(const float (&logit)[5], const uint8_t (&mask)[5],
+                                               int n, float u, float* logp) {
+  const float NEG = -3.4028234663852886e38f;
+  float ml[5], ex[5];
+#pragma unroll
+  for (int k = 0; k < 5; ++k) ml[k] = mask[k] && k < n ? logit[k] : NEG;
+  float m = ml[0];
+#pragma unroll
+  for (int k = 1; k < 5; ++k) m = fmaxf(m, ml[k]);
+#pragma unroll
+  for (int k = 0; k < 5; ++k) ex[k] = k < n ? exp_q(ml[k] - m) : 0.0f;
+  float sum = ex[0];
+#pragma unroll
+  for (int k = 1; k < 5; ++k) sum = sum + ex[k];
+  const float t = u * sum;
+  float run = 0.0f;
+  int count = 0, last = 0;
+#pragma unroll
+  for (int k = 0; k < 5; ++k) {
+    run = run + ex[k];
+    count += run <= t;
+    if (ex[k] > 0.0f) last = k;
+  }
+  const int a = count >= n ? last : count;
+  *logp = (ml[a] - m) - log_q(sum);
+  return a;
+}
+
+// Sampling inputs of one row, drawn by two lanes of its tail wavefront:
+// half 0 (lane r) the move, half 1 (lane r + 16) the bomb.
 struct RowSampler {
   bool on;
-  uint8_t mm[5], bm[2];
-  float um, ub;
+  uint8_t m[5];
+  float u;
 };
 
-// Masks and uniforms of output row `row` for player pid (Philox when the
-// caller passes no uniforms).
-__device__ __forceinline__ RowSampler load_sampler(const qqt_mlp_args& a, bool on, int row, int pid,
-                                                   int oslots, int oslot) {
+// Mask and uniform of one half of output row `row` for player pid (Philox
+// when the caller passes no uniforms).
+__device__ __forceinline__ RowSampler load_sampler(const qqt_mlp_args& a, bool on, int half,
+                                                   int row, int pid, int oslots, int oslot) {
   RowSampler r;
   r.on = on;
 #pragma unroll
-  for (int k = 0; k < 5; ++k) r.mm[k] = 0;
-  r.bm[0] = r.bm[1] = 0;
-  r.um = r.ub = 0.0f;
+  for (int k = 0; k < 5; ++k) r.m[k] = 0;
+  r.u = 0.0f;
   if (on) {
+    if (half == 0) {
 #pragma unroll
-    for (int k = 0; k < 5; ++k)
-      r.mm[k] = a.move_mask[(size_t)row * a.mm_row_stride + (size_t)pid * a.mm_pid_stride + k];
+      for (int k = 0; k < 5; ++k)
+        r.m[k] = a.move_mask[(size_t)row * a.mm_row_stride + (size_t)pid * a.mm_pid_stride + k];
+    } else {
 #pragma unroll
-    for (int k = 0; k < 2; ++k)
-      r.bm[k] = a.bomb_mask[(size_t)row * a.bm_row_stride + (size_t)pid * a.bm_pid_stride + k];
+      for (int k = 0; k < 2; ++k)
+        r.m[k] = a.bomb_mask[(size_t)row * a.bm_row_stride + (size_t)pid * a.bm_pid_stride + k];
+    }
     const size_t o = (size_t)row * oslots + oslot;
     if (a.uniforms) {
-      r.um = a.uniforms[o * 2 + 0];
-      r.ub = a.uniforms[o * 2 + 1];
+      r.u = a.uniforms[o * 2 + half];
     } else {
       float u4[4];
       philox_block(a.seed, (uint32_t)row, a.tick, STREAM_POLICY, (uint32_t)((2 * pid) >> 2), u4);
-      r.um = u4[(2 * pid) & 3];
-      r.ub = u4[(2 * pid + 1) & 3];
+      r.u = u4[(2 * pid + half) & 3];
     }
   }
   return r;
 }
 
-// Everything after the first layer for one 64-row block (512 threads):
-// bias + LayerNorm 1 (s.f plus the second partial tile f1 when given) +
-// ReLU, Linear(128,128), LayerNorm 2 + ReLU, the heads' hidden and output
-// layers, then the outputs and the masked sampling, one thread per row.
-// w1b holds the layer-2 B fragments, already in flight.  H1, H2 and HY are
-// LDS planes; HY may overlay f1 and H1 (both dead by then).
-template <class L>
-__device__ __forceinline__ void mlp_tail(L& s, const qqt_mlp_args& a, const uint16_t* f1,
-                                         uint16_t* H1, uint16_t* H2, uint16_t* HY, int brow0,
-                                         int oslots, int oslot, const RowSampler& rs,
-                                         const SplitB<2, 2>& w1b) {
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int r16 = lane & 15, q = lane >> 4;
-  const int cg = w & 3, rh = w >> 2;      // column group, row half of the small layers
-  layernorm_rows(s, f1, V_B0, V_G1, V_BE1, H1);
-  __syncthreads();
-
-  // ---------------- layer 2: 128 -> 128; wavefront w: rows 32rh.., columns 32cg..
-  floatx4 acc2[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) acc2[i][ct] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-  split_gemm<2, 2, 2>(acc2, H1, H1 + ROWS * HID, HID, 2 * rh, w1b, lane);
-  SplitB<3, 2> whb;                 // head weights: in flight during LayerNorm 2
-  load_split_b(whb, a.wh, a.wh_lo, 3 * cg, lane);
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        s.f[32 * rh + 16 * i + 4 * q + j][32 * cg + 16 * ct + r16] = acc2[i][ct][j];
-  __syncthreads();
-  layernorm_rows(s, nullptr, V_B1, V_G2, V_BE2, H2);
-  __syncthreads();
-
-  // ---------------- heads, first layer: 128 -> 192; rows 32rh.., columns 48cg..
-  {
-    floatx4 hac[2][3];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int ct = 0; ct < 3; ++ct) hac[i][ct] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    split_gemm<2, 3, 2>(hac, H2, H2 + ROWS * HID, HID, 2 * rh, whb, lane);
-#pragma unroll
-    for (int ct = 0; ct < 3; ++ct) {
-      const int col = 48 * cg + 16 * ct + r16;
-      const float b = s.vec[V_BH + col];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int row = 32 * rh + 16 * i + 4 * q + j;
-          split_store(h_at(HY, 3 * HEAD, 0, row, col), h_at(HY, 3 * HEAD, 1, row, col),
-                      fmaxf(hac[i][ct][j] + b, 0.0f));
-        }
-    }
-  }
-  __syncthreads();
-
-  // ---------------- heads, output layer: 192 -> 8 (block diagonal); wavefronts 0-3: rows 16w..
-  if (w < 4) {
-    floatx4 oac = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int kb = 0; kb < 3; ++kb) {
-      const Frag16 bh = load_b(&s.wf[0][(kb * 64 + lane) * 16]);
-      const Frag16 bl = load_b(&s.wf[1][(kb * 64 + lane) * 16]);
-      const int row = 16 * w + r16;
-      const Frag16 ah = read_a(HY, 3 * HEAD, row, kb, q);
-      const Frag16 al = read_a(HY + ROWS * 3 * HEAD, 3 * HEAD, row, kb, q);
-      oac = mfma(ah.lo, bh.lo, oac);
-      oac = mfma(ah.hi, bh.hi, oac);
-      oac = mfma(ah.lo, bl.lo, oac);
-      oac = mfma(ah.hi, bl.hi, oac);
-      oac = mfma(al.lo, bh.lo, oac);
-      oac = mfma(al.hi, bh.hi, oac);
-    }
-    if (r16 < NOUT) {
-      const float b = s.vec[V_BF + r16];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) s.logit[16 * w + 4 * q + j][r16] = oac[j] + b;
-    }
-  }
-  __syncthreads();
-
-  // ---------------- outputs and sampling: one thread per row
-  const int orow = brow0 + (int)threadIdx.x;
-  if (threadIdx.x < ROWS && orow < a.batch) {
-    const float* lg = s.logit[threadIdx.x];
-    const size_t o = (size_t)orow * oslots + oslot;
-    if (a.logits_out) {
-#pragma unroll
-      for (int k = 0; k < NOUT; ++k) a.logits_out[o * NOUT + k] = lg[k];
-    }
-    if (a.value_out) a.value_out[o] = lg[7];
-    if (rs.on) {
-      float lpm, lpb;
-      const int am = sample_masked<5>(lg, rs.mm, rs.um, &lpm);
-      const int ab = sample_masked<2>(lg + 5, rs.bm, rs.ub, &lpb);
-      if (a.actions) {
-        a.actions[o * 2 + 0] = am;
-        a.actions[o * 2 + 1] = ab;
-      }
-      if (a.actions_i8) {
-        a.actions_i8[o * 2 + 0] = (int8_t)am;
-        a.actions_i8[o * 2 + 1] = (int8_t)ab;
-      }
-      if (a.logp_out) a.logp_out[o] = lpm + lpb;
-    }
-  }
-}
-
 // RB row blocks of 64 per workgroup: RB = 2 halves the W0 bytes each row
-// costs (large forward batches, no sampling); the tail runs once per block.
+// costs (large forward batches, no sampling).
 // Z1: the first-layer-only instantiation of the training forward (z1_out).
 template <int RB, bool Z1>
 __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   static_assert(RB == 1 || RB == 2, "one or two row blocks per workgroup");
-  constexpr int RT = 4 * RB;               // layer-1 row tiles per wavefront
+  constexpr int RT = 4 * RB;               // row tiles: per layer-1 wavefront, and tail wavefronts
   constexpr int NX = 8 * RB;               // x load instructions per wavefront and K block
   constexpr int XT = RB * XT_HALVES;       // one x tile of the workgroup
+  constexpr int W1_CH = 2 * W1_HALVES / 8 / NTHR;   // 16-byte chunks of W1 per thread
+  constexpr int WH_CH = 2 * WH_HALVES / 8 / NTHR;   // ... of the head weights
+  constexpr int WF_CH = 2 * WF_HALVES / 8;          // 16-byte chunks of the output layer
+  static_assert(W1_CH * NTHR * 8 == 2 * W1_HALVES && WH_CH * NTHR * 8 == 2 * WH_HALVES,
+                "weight staging divides over the threads");
+  static_assert(WF_CH <= 2 * NTHR && WF_CH > NTHR, "two output-layer chunks per thread");
   __shared__ MlpLds<RB> s;
   const int nrb = (a.batch + RB * ROWS - 1) / (RB * ROWS);
   const int xcd = blockIdx.x & 7, seq = blockIdx.x >> 3;
@@ -430,9 +332,11 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   const int kg = w >> 2, cg = w & 3;       // layer-1 K group, column group
   const int oslots = a.out_slots > 0 ? a.out_slots : a.npid;   // output row width (slots)
   const int oslot = a.npid == 2 ? slot : a.out_slot;
+  uint16_t* const w1s = s.xw + RB * 4 * XT_HALVES;             // layer-2 weights in LDS
 
-  // Parameter vectors: two floats per thread, loaded before the first tiles
-  // (vmcnt retires in order) and written to LDS after they are issued.
+  // Parameter vectors (two floats per thread), the output layer's and layer
+  // 2's weights: loaded before the first tiles (vmcnt retires in order) and
+  // written to LDS after those are issued.
   auto vec_src = [&](int i) -> const float* {
     return i < V_G1 ? a.b0 + (i - V_B0) : i < V_BE1 ? a.ln1_w + (i - V_G1)
          : i < V_B1 ? a.ln1_b + (i - V_BE1) : i < V_G2 ? a.b1 + (i - V_B1)
@@ -442,17 +346,28 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   const int vi0 = threadIdx.x, vi1 = threadIdx.x + NTHR;   // vi1 < V_N for the first 456
   const float vv0 = *vec_src(vi0);
   const float vv1 = vi1 < V_N ? *vec_src(vi1) : 0.0f;
-  // output-layer weights (both planes, 16-byte chunks t and t + NTHR)
-  static_assert(WF_CHUNKS <= 2 * NTHR && WF_CHUNKS > NTHR, "two chunks per thread");
-  auto wf_src = [&](int c) {
-    const int plane = c / (WF_HALVES / 8), i = c % (WF_HALVES / 8);
-    return reinterpret_cast<const uint4*>(plane ? a.wf_lo : a.wf) + i;
+  auto plane_src = [](const uint16_t* hi, const uint16_t* lo, int halves, int c) {
+    const int per = halves / 8;
+    return c < per ? reinterpret_cast<const u32x4*>(hi) + c
+                   : reinterpret_cast<const u32x4*>(lo) + (c - per);
   };
+  u32x4 wfv[2];
   const int wc1 = threadIdx.x + NTHR;
-  const uint4 wfv0 = *wf_src(threadIdx.x);
-  const uint4 wfv1 = wc1 < WF_CHUNKS ? *wf_src(wc1) : make_uint4(0u, 0u, 0u, 0u);
+  if constexpr (!Z1) {
+    wfv[0] = *plane_src(a.wf, a.wf_lo, WF_HALVES, threadIdx.x);
+    wfv[1] = wc1 < WF_CH ? *plane_src(a.wf, a.wf_lo, WF_HALVES, wc1) : u32x4{0u, 0u, 0u, 0u};
+  }
+  // Layer 2's weights (64 KB) go to LDS in the prologue.  Staging them one
+  // chunk per K step instead was measured 1.3 us slower: the conditional
+  // stores split the K loop's body and the extra requests slow its stream.
+  u32x4 w1v[W1_CH];
+  if constexpr (!Z1) {
+#pragma unroll
+    for (int c = 0; c < W1_CH; ++c)
+      w1v[c] = *plane_src(a.w1, a.w1_lo, W1_HALVES, threadIdx.x + NTHR * c);
+  }
 
-  // ---------------- layer 1: group kg, K blocks kg, kg+2, ...; columns 32cg..32cg+31
+  // ---------------- layer 1: group kg, K blocks kg, kg+2, ...; features 32cg..32cg+31
   floatx4 acc[RT][2];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
@@ -470,8 +385,8 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   const uint32_t* const xbase = reinterpret_cast<const uint32_t*>(a.obs);
   const size_t xstride = (size_t)a.obs_stride / 2;    // dwords per row
   const uint16_t* wb = a.w0 + (size_t)((pid * 8 + 2 * cg) * nkb) * 64 * 16 + lane * 16;
-  const size_t wtile = (size_t)nkb * 64 * 16;   // halves between B tiles
-  uint16_t* const xt = s.xs_h1 + kg * 2 * XT;   // this group's two x tiles
+  const size_t wtile = (size_t)nkb * 64 * 16;   // halves between weight tiles
+  uint16_t* const xt = s.xw + kg * 2 * XT;      // this group's two x tiles
 
   // Loads run PD group steps ahead; the tail mask (elements >= k0) is applied
   // when the registers are written to LDS, so no load is waited on early.
@@ -500,9 +415,9 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   };
   auto compute = [&](int buf, const Frag16 (&br)[2]) {
     const uint16_t* t = xt + buf * XT;
-    Frag16 af[RT];
+    Frag16 xf[RT];
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) af[rt] = read_a(t, 64, 16 * rt + r16, 0, q);
+    for (int rt = 0; rt < RT; ++rt) xf[rt] = read_x(t, 16 * rt + r16, q);
     // low K halves over every tile pair, then the high halves
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -510,8 +425,8 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct)
-          acc[rt][ct] = h ? mfma(af[rt].hi, br[ct].hi, acc[rt][ct])
-                          : mfma(af[rt].lo, br[ct].lo, acc[rt][ct]);
+          acc[rt][ct] = h ? mfma(br[ct].hi, xf[rt].hi, acc[rt][ct])
+                          : mfma(br[ct].lo, xf[rt].lo, acc[rt][ct]);
   };
 
   // Group step i handles K block 2i + kg.  Register ring of PD steps in
@@ -530,14 +445,19 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
     load_w(min(kblk(j), last), br[j]);
   }
 
-  const int srow = row0 + (int)threadIdx.x;          // sampling row of threads < 64
-  const RowSampler rs = load_sampler(a, RB == 1 && threadIdx.x < ROWS && srow < a.batch && a.sample,
-                                     srow, pid, oslots, oslot);
+  // output row of lanes l and l + 16 (l < 16) of tail wavefront w: row0 + 16w + l
+  const int srow = row0 + 16 * w + r16;
+  const RowSampler rs = load_sampler(a, !Z1 && a.sample && w < RT && lane < 32 && srow < a.batch,
+                                     q & 1, srow, pid, oslots, oslot);
 
   s.vec[vi0] = vv0;
   if (vi1 < V_N) s.vec[vi1] = vv1;
-  reinterpret_cast<uint4*>(&s.wf[0][0])[threadIdx.x] = wfv0;
-  if (wc1 < WF_CHUNKS) reinterpret_cast<uint4*>(&s.wf[0][0])[wc1] = wfv1;
+  if constexpr (!Z1) {
+    reinterpret_cast<u32x4*>(s.wf)[threadIdx.x] = wfv[0];
+    if (wc1 < WF_CH) reinterpret_cast<u32x4*>(s.wf)[wc1] = wfv[1];
+#pragma unroll
+    for (int c = 0; c < W1_CH; ++c) reinterpret_cast<u32x4*>(w1s)[threadIdx.x + NTHR * c] = w1v[c];
+  }
   store_x(xr[0], 0, kblk(0));
   load_x(min(kblk(PD), last), xr[0]);
   __syncthreads();
@@ -560,54 +480,118 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
     __syncthreads();
   }
 
-  // Combine the two groups' partial sums in the fp32 tile.
-  uint16_t* const H1 = s.xs_h1 + RB * 4 * XT_HALVES;
-  uint16_t* const H2 = RB == 1 ? s.h2 : H1;
-  const int rh = w >> 2;            // row half of the small layers
+  // Head weights: in flight through the partial-sum exchange and layer 2.
+  u32x4 whv[WH_CH];
+  if constexpr (!Z1) {
 #pragma unroll
-  for (int hb = 0; hb < RB; ++hb) {   // one 64-row block at a time
-  const int brow0 = row0 + ROWS * hb;
-  SplitB<2, 2> w1b;                 // layer-2 weights: in flight during LayerNorm 1
-  load_split_b(w1b, a.w1, a.w1_lo, 2 * cg, lane);
-  // The last loop step ended with a barrier, so the x tiles are free.
-  // (kg is uniform: one branch around both store loops)
-  if (kg == 0) {
+    for (int i = 0; i < WH_CH; ++i)
+      whv[i] = *plane_src(a.wh, a.wh_lo, WH_HALVES, threadIdx.x + NTHR * i);
+  }
+
+  // ---------------- the groups' partial sums meet in the (now free) x tiles:
+  // ex[(row tile * 8 + feature tile) * 64 + lane]; group 1 writes, group 0 adds.
+  floatx4* const ex = reinterpret_cast<floatx4*>(s.xw);
+  if (kg == 1) {
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          s.f[16 * rt + 4 * q + j][32 * cg + 16 * ct + r16] = acc[4 * hb + rt][ct][j];
-  } else {
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          *f1_at(s.xs_h1, 16 * rt + 4 * q + j, 32 * cg + 16 * ct + r16) = acc[4 * hb + rt][ct][j];
+      for (int ct = 0; ct < 2; ++ct) ex[(rt * 8 + 2 * cg + ct) * 64 + lane] = acc[rt][ct];
   }
   __syncthreads();
-  if constexpr (Z1) {   // first layer only (the training forward): z1 = (f1 + f) + b0
-    const int t = threadIdx.x, row = t >> 3, j = t & 7, orow = brow0 + row;
-    if (orow < a.batch) {
+  if (kg == 0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int c = 32 * i + 4 * j;
-        const float4 x = *reinterpret_cast<const float4*>(&s.f[row][c]);
-        const float4 z = *reinterpret_cast<const float4*>(f1_at(s.xs_h1, row, c));
-        const float4 b = *reinterpret_cast<const float4*>(&s.vec[V_B0 + c]);
-        *reinterpret_cast<float4*>(a.z1_out + (size_t)orow * HID + c) =
-            make_float4((z.x + x.x) + b.x, (z.y + x.y) + b.y, (z.z + x.z) + b.z,
-                        (z.w + x.w) + b.w);
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        floatx4& e = ex[(rt * 8 + 2 * cg + ct) * 64 + lane];
+        e = acc[rt][ct] + e;
+      }
+  }
+  __syncthreads();
+
+  if constexpr (Z1) {   // first layer only (the training forward): z1 = (f + f1) + b0
+#pragma unroll
+    for (int hb = 0; hb < RB; ++hb) {
+      // thread t: row t/8 of the block, features 16(t%8) .. +15 as four float4
+      const int row = ROWS * hb + (threadIdx.x >> 3), ft = threadIdx.x & 7;
+      const int orow = row0 + row;
+      if (orow < a.batch) {
+#pragma unroll
+        for (int q2 = 0; q2 < 4; ++q2) {
+          const floatx4 e = ex[((row >> 4) * 8 + ft) * 64 + 16 * q2 + (row & 15)];
+          const float4 b = *reinterpret_cast<const float4*>(&s.vec[V_B0 + 16 * ft + 4 * q2]);
+          *reinterpret_cast<float4*>(a.z1_out + (size_t)orow * HID + 16 * ft + 4 * q2) =
+              make_float4(e[0] + b.x, e[1] + b.y, e[2] + b.z, e[3] + b.w);
+        }
       }
     }
-    if (hb + 1 < RB) __syncthreads();   // the next block rewrites both tiles
-    continue;
+    return;
   }
-  mlp_tail(s, a, s.xs_h1, H1, H2, s.xs_h1, brow0, oslots, oslot, rs, w1b);
-  if (hb + 1 < RB) __syncthreads();   // the next block reuses every tail buffer
+
+  // ---------------- LayerNorm 1, layer 2, LayerNorm 2: tail wavefront w, row tile w
+  const bool tail = w < RT;
+  half8 hh[4], hl[4];
+  if (tail) {
+    floatx4 v[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) v[t] = ex[(w * 8 + t) * 64 + lane];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) v[t] = v[t] + vec4(s.vec + V_B0, t, q);   // z1 = (f + f1) + b0
+    ln_relu_split(v, s.vec + V_G1, s.vec + V_BE1, q, hh, hl);
+    // layer 2: the accumulators start at the bias
+#pragma unroll
+    for (int t = 0; t < 8; ++t) v[t] = vec4(s.vec + V_B1, t, q);
+    tail_gemm<8, 4>(v, w1s, w1s + W1_HALVES, hh, hl, lane);
+    ln_relu_split(v, s.vec + V_G2, s.vec + V_BE2, q, hh, hl);
+  }
+  __syncthreads();   // every tail wavefront is past layer 2: x tiles and W1 are dead
+#pragma unroll
+  for (int i = 0; i < WH_CH; ++i) reinterpret_cast<u32x4*>(s.xw)[threadIdx.x + NTHR * i] = whv[i];
+  __syncthreads();
+  if (!tail) return;   // no barrier below
+
+  // ---------------- heads: 128 -> 192 (+ bias, ReLU), then 192 -> 8 (block diagonal)
+  // (accumulators start at the biases; lanes q >= 2 of the output tile hold
+  // its 8 padding rows, seeded with bf[0..7] and never read)
+  half8 yh[6], yl[6];
+  floatx4 o[1] = {vec4(s.vec + V_BF, 0, q & 1)};
+  {
+    floatx4 a3[12];
+#pragma unroll
+    for (int t = 0; t < 12; ++t) a3[t] = vec4(s.vec + V_BH, t, q);
+    tail_gemm<12, 4>(a3, s.xw, s.xw + WH_HALVES, hh, hl, lane);
+#pragma unroll
+    for (int t = 0; t < 12; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        split_into(fmaxf(a3[t][j], 0.0f), yh[t >> 1], yl[t >> 1], 4 * (t & 1) + j);
+  }
+  tail_gemm<1, 6>(o, s.wf, s.wf + WF_HALVES, yh, yl, lane);
+
+  // ---------------- outputs and sampling: lanes r and r + 16 own row 16w + r
+  // (outputs 0-3 in lane r, 4-7 in lane r + 16)
+  const float out4 = __shfl(o[0][0], lane + 16, 64);
+  const bool half0 = q == 0;
+  float lp = 0.0f;
+  int act = 0;
+  if (rs.on) {
+    const float lg[5] = {half0 ? o[0][0] : o[0][1], half0 ? o[0][1] : o[0][2],
+                         half0 ? o[0][2] : 0.0f, half0 ? o[0][3] : 0.0f, half0 ? out4 : 0.0f};
+    act = sample_masked_n(lg, rs.m, half0 ? 5 : 2, rs.u, &lp);
+  }
+  const float lpb = __shfl(lp, lane + 16, 64);
+  if (lane < 32 && srow < a.batch) {
+    const size_t oo = (size_t)srow * oslots + oslot;
+    if (a.logits_out) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a.logits_out[oo * NOUT + 4 * q + j] = o[0][j];
+    }
+    if (!half0 && a.value_out) a.value_out[oo] = o[0][3];
+    if (rs.on) {
+      if (a.actions) a.actions[oo * 2 + q] = act;
+      if (a.actions_i8) a.actions_i8[oo * 2 + q] = (int8_t)act;
+      if (half0 && a.logp_out) a.logp_out[oo] = lp + lpb;
+    }
   }
 }
 

@@ -45,14 +45,7 @@ def flags() -> list[str]:
 HOST_FEATURE_NOTICE = "'-packed-fp32-ops' is not a recognized feature for this target"
 
 
-def build(verbose: bool = True) -> str:
-    os.makedirs(LIBDIR, exist_ok=True)
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    missing = [s for s in srcs if not os.path.exists(s)]
-    if missing:
-        raise FileNotFoundError(f"HIP sources missing: {missing}")
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), *flags(), "-shared", "-o", tmp, *srcs]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
@@ -61,6 +54,27 @@ def build(verbose: bool = True) -> str:
         print(out, flush=True)
     if res.returncode:
         raise subprocess.CalledProcessError(res.returncode, cmd)
+
+
+def build(verbose: bool = True) -> str:
+    """Compile every source to an object (in parallel), then link."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    os.makedirs(LIBDIR, exist_ok=True)
+    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    missing = [s for s in srcs if not os.path.exists(s)]
+    if missing:
+        raise FileNotFoundError(f"HIP sources missing: {missing}")
+    objdir = os.path.join(LIBDIR, "obj")
+    os.makedirs(objdir, exist_ok=True)
+    objs = [os.path.join(objdir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+    jobs = max(1, min(len(srcs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with ThreadPoolExecutor(jobs) as ex:
+        for f in [ex.submit(_run, [hipcc(), *flags(), "-c", "-o", o, s], verbose)
+                  for s, o in zip(srcs, objs)]:
+            f.result()
+    tmp = LIB + ".tmp"
+    _run([hipcc(), f"--offload-arch={ARCH}", "-fPIC", "-shared", "-o", tmp, *objs], verbose)
     os.replace(tmp, LIB)
     return LIB
 

@@ -55,6 +55,28 @@ def _frag(w: torch.Tensor, kpad: int, residual: bool = False) -> torch.Tensor:
     return f.half().reshape(-1)
 
 
+# K order of one 32-deep step of the later layers: MFMA K index 8q + i
+# (lane group q, element i) reads input feature 32 s + CHAIN_KPERM[8q + i],
+# the order in which the previous product's output tiles 2s, 2s+1 sit in a
+# lane (features 4q..4q+3 of each).
+CHAIN_KPERM = [4 * q + i if i < 4 else 16 + 4 * q + (i - 4) for q in range(4) for i in range(8)]
+
+
+def _chain_frag(w: torch.Tensor, residual: bool = False) -> torch.Tensor:
+    """(n_out, k) float matrix (n_out % 16 == 0, k % 32 == 0) -> float16 A
+    fragments [tile][kstep][lane][8] = W[16 tile + lane%16][32 kstep +
+    CHAIN_KPERM[8 (lane/16) + i]] (of w itself, or of its float16 residual)."""
+    n, k = w.shape
+    assert n % 16 == 0 and k % 32 == 0
+    out = w.float()
+    if residual:
+        out = out - out.half().float()
+    perm = torch.tensor(CHAIN_KPERM, device=w.device)
+    f = out.reshape(n // 16, 16, k // 32, 32)[..., perm]           # [tile][r][s][8q + i]
+    f = f.reshape(n // 16, 16, k // 32, 4, 8).permute(0, 2, 3, 1, 4).contiguous()
+    return f.half().reshape(-1)                                     # [tile][s][16q + r][i]
+
+
 def pack_mlp(params: dict, n_players: int = 2, obs_shape=(14, 13, 13)) -> dict:
     """Packing of an ActorCritic mlp state_dict into the kernel's operand
     layout, on the device the weights live on."""
@@ -70,10 +92,10 @@ def pack_mlp(params: dict, n_players: int = 2, obs_shape=(14, 13, 13)) -> dict:
                for pid in range(n_players)]
     w0 = torch.cat([_frag(wp, kpad) for wp in per_pid])
     w1_src = params["shared.3.weight"].to(dev)
-    w1, w1_lo = _frag(w1_src, HID), _frag(w1_src, HID, True)
+    w1, w1_lo = _chain_frag(w1_src), _chain_frag(w1_src, True)
     heads = ("move_head", "bomb_head", "critic")
     wh_src = torch.cat([params[f"{n}.0.weight"].to(dev).float() for n in heads])
-    wh, wh_lo = _frag(wh_src, HID), _frag(wh_src, HID, True)
+    wh, wh_lo = _chain_frag(wh_src), _chain_frag(wh_src, True)
     wfin = torch.zeros((16, 3 * HEAD), dtype=torch.float32, device=dev)
     outs = [params[f"{n}.2.weight"].to(dev).float() for n in heads]
     row = 0
@@ -82,7 +104,7 @@ def pack_mlp(params: dict, n_players: int = 2, obs_shape=(14, 13, 13)) -> dict:
         row += o.shape[0]
     if row != 8:
         raise ValueError("heads must produce 5 + 2 + 1 outputs")
-    wf, wf_lo = _frag(wfin, 3 * HEAD), _frag(wfin, 3 * HEAD, True)
+    wf, wf_lo = _chain_frag(wfin), _chain_frag(wfin, True)
     vec = lambda k: params[k].to(dev).float().contiguous()  # noqa: E731
     return dict(
         w0=w0, w1=w1, wh=wh, wf=wf, w1_lo=w1_lo, wh_lo=wh_lo, wf_lo=wf_lo,

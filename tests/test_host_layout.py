@@ -117,6 +117,55 @@ def test_fragment_residual_split():
     assert bool((err <= flat.abs() * 2.0 ** -22 + 2.0 ** -25).all())
 
 
+def _mfma_16x16x32(a_lanes, b_lanes, c_lanes):
+    """v_mfma_f32_16x16x32_f16 on lane registers (float64 here): lane l holds
+    A[l%16][8(l/16) + i], B[8(l/16) + i][l%16] (i < 8) and D[4(l/16) + j][l%16]
+    (j < 4)."""
+    lane = np.arange(64)
+    A = np.zeros((16, 32))
+    B = np.zeros((32, 16))
+    for i in range(8):
+        A[lane % 16, 8 * (lane // 16) + i] = a_lanes[:, i]
+        B[8 * (lane // 16) + i, lane % 16] = b_lanes[:, i]
+    D = A @ B
+    return c_lanes + np.stack([D[4 * (lane // 16) + j, lane % 16] for j in range(4)], 1)
+
+
+def test_chain_fragments_take_the_previous_output_tiles_as_is():
+    """The later layers' A fragments (_chain_frag) against activations held in
+    the MFMA output layout (lane 16q + r: features 16t + 4q + j of row r): K
+    step s of the next product packs output tiles 2s, 2s+1 of a lane into its
+    8-element B fragment, and the products equal W h^T."""
+    from qqtsim.policy import CHAIN_KPERM, _chain_frag
+
+    g = torch.Generator().manual_seed(5)
+    n_out, k_in = 48, 64
+    W = torch.randn((n_out, k_in), generator=g).double()
+    h = torch.randn((16, k_in), generator=g).double()       # 16 batch rows
+    frag = _chain_frag(W).double().view(n_out // 16, k_in // 32, 64, 8).numpy()
+    lane = np.arange(64)
+    q, r = lane // 16, lane % 16
+    # previous product's output tiles: v[t][lane][j] = h[r][16t + 4q + j]
+    v = np.stack([np.stack([h.numpy()[r, 16 * t + 4 * q + j] for j in range(4)], 1)
+                  for t in range(k_in // 16)])
+    want = (W.half().double() @ h.numpy().T)                  # [feature][row]
+    for T in range(n_out // 16):
+        acc = np.zeros((64, 4))
+        for s in range(k_in // 32):
+            b = np.concatenate([v[2 * s], v[2 * s + 1]], 1)   # element i: tile 2s + i // 4
+            acc = _mfma_16x16x32(frag[T, s], b, acc)
+        for j in range(4):
+            assert np.allclose(acc[:, j], want.numpy()[16 * T + 4 * q + j, r], atol=1e-12)
+    assert sorted(CHAIN_KPERM) == list(range(32))
+    # hi + lo planes carry W to ~22 bits in the same element order
+    lo = _chain_frag(W, residual=True).double().view(frag.shape).numpy()
+    kperm = np.array(CHAIN_KPERM)
+    for T in range(n_out // 16):
+        for s in range(k_in // 32):
+            exact = W.numpy()[16 * T + r[:, None], 32 * s + kperm[8 * q[:, None] + np.arange(8)]]
+            assert np.all(np.abs(frag[T, s] + lo[T, s] - exact) <= np.abs(exact) * 2.0 ** -21 + 2.0 ** -24)
+
+
 def test_pack_mlp_folds_each_players_view_into_w0():
     from oracle.policy import column_permutation
 
