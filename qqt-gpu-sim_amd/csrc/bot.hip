@@ -62,14 +62,15 @@ __global__ __launch_bounds__(64 * WPB) void bot_kernel(const qqt_sim_config cf, 
   static_assert(NPL <= 64, "player slots must fit one wavefront");
   __shared__ bot::BotLds<H, W, P> sh[WPB];
   // the waves of a workgroup share nothing: each owns one env and its LDS.
-  // 64-env row blocks are dealt to the XCDs as in the tick and act kernels
-  // (block b: row block (b / 8 / WGRB) * 8 + b % 8), so the env's state,
-  // observation and masks are read from the L2 that the tick wrote them to.
-  constexpr int WGRB = 64 / WPB;                    // workgroups per row block
-  static_assert(WGRB * WPB == 64, "row blocks of 64 envs");
+  // XCD_ROWS-env row blocks are dealt to the XCDs as in the tick and act
+  // kernels (block b: row block (b / 8 / WGRB) * 8 + b % 8), so the env's
+  // state, observation and masks are read from the L2 that the tick wrote
+  // them to.
+  constexpr int WGRB = XCD_ROWS / WPB;              // workgroups per row block
+  static_assert(WGRB * WPB == XCD_ROWS, "whole workgroups per row block");
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int seq = blockIdx.x >> 3;
-  const int g = ((seq / WGRB) * 8 + (blockIdx.x & 7)) * 64 + (seq % WGRB) * WPB + wv;
+  const int g = ((seq / WGRB) * 8 + (blockIdx.x & 7)) * XCD_ROWS + (seq % WGRB) * WPB + wv;
   if (g >= a.n_envs) return;
   bot::BotLds<H, W, P>& s = sh[wv];
   const int lane = threadIdx.x & 63;
@@ -352,8 +353,8 @@ static int launch_bot(const qqt_sim_config* cfg, const qqt_bot_args* a, hipStrea
     QQT_LAUNCH(QQT_KERNEL_REACH, reach_kernel, dim3((a->n_envs + REACH_THREADS - 1) / REACH_THREADS),
                dim3(REACH_THREADS), st, a->players, a->n_envs, P, a->pid, a->reach, a->reach_slot);
   constexpr int WPB = 2;  // two independent waves per workgroup (workgroup slots per CU)
-  const int nrb = (a->n_envs + 63) / 64;     // row blocks, a multiple of 8 of them
-  QQT_LAUNCH(QQT_KERNEL_BOT, (bot_kernel<H, W, P, WPB>), dim3(((nrb + 7) / 8) * 8 * (64 / WPB)),
+  const int nrb = (a->n_envs + XCD_ROWS - 1) / XCD_ROWS;   // row blocks, a multiple of 8 of them
+  QQT_LAUNCH(QQT_KERNEL_BOT, (bot_kernel<H, W, P, WPB>), dim3(((nrb + 7) / 8) * 8 * (XCD_ROWS / WPB)),
              dim3(64 * WPB), st, *cfg, *a);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {

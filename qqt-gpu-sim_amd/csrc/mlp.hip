@@ -6,11 +6,12 @@
 // A player's view permutation is folded into the first-layer weights, so a
 // player is just a column block of one shared weight buffer.
 //
-// Workgroup = 8 wavefronts (2 per SIMD) = RB 64-row blocks of one player
-// (RB = 1 for rollout batches, 2 for large forward batches).  Both players'
+// Workgroup = 8 wavefronts (2 per SIMD) = one row block of one player: an
+// XCD row block of 44 rows (three 16-row tiles) for rollout-sized batches,
+// 128 rows (eight tiles) for large forward batches.  Both players'
 // workgroups of a row block are dispatched back to back on the same XCD
 // (workgroups are dealt to the 8 XCDs round robin), so the second read of
-// the observation tile hits that XCD's L2.
+// the observation tile hits that XCD's L2, where the tick kernel wrote it.
 //
 // Every product is v_mfma_f32_16x16x32_f16 (float32 accumulation) with the
 // weights as the A operand and the activations as the B operand, so a 16 x 16
@@ -19,15 +20,15 @@
 //
 // Layer 1 (K = 2366) is split over two groups of four wavefronts: group g
 // takes K blocks g, g+2, g+4, ...  Each group streams its observation tiles
-// (RB*64 rows x 64 K) through its own double-buffered, XOR-swizzled LDS tile
+// (16RT rows x 64 K) through its own double-buffered, XOR-swizzled LDS tile
 // (loaded PD steps ahead into registers); the weight fragments go straight
 // from L2 into registers, PD steps ahead.  Wavefront (g, c) owns features
 // 32c..32c+31 of every row.  The groups' partial sums meet in LDS (group 1
 // writes, group 0 adds), laid out by (row tile, feature tile, lane).
 //
 // Everything after layer 1 runs per 16-row tile inside one wavefront, in
-// registers (wavefront w takes row tile w; with RB = 1 wavefronts 4-7 only
-// help stage weights).  A row's 128 features sit in lanes r, r+16, r+32,
+// registers (wavefront w takes row tile w; wavefronts past the last tile
+// only help stage weights).  A row's 128 features sit in lanes r, r+16, r+32,
 // r+48, so LayerNorm reduces with two cross-lane exchanges, and the output
 // tiles of one product are, unchanged, the B operand of the next: K step s
 // of the next product reads feature tiles 2s and 2s+1, i.e. MFMA K index
@@ -67,8 +68,14 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // 16 bytes staged
 constexpr int HID = 128;           // hidden width
 constexpr int HEAD = 64;           // head hidden width
 constexpr int NOUT = 8;            // 5 move + 2 bomb + 1 value
-constexpr int ROWS = 64;           // rows per block (a workgroup takes one or two)
-constexpr int MLP_TWO_BLOCK_ROWS = 1 << 16;   // forward batches from here use two blocks
+// Row tiles (16 rows each) per workgroup.  Rollout-sized batches take RT = 3
+// tiles over an XCD row block of 44 rows: 5632 rows make 128 row blocks x 2
+// players = 256 workgroups, one per CU (64-row blocks left 80 of the 256 CUs
+// idle and put a third more MFMA work on each busy one).  Forward batches
+// from MLP_BIG_ROWS rows take RT = 8 (128 rows), which streams W0 once per
+// 128 rows.
+constexpr int RT_SMALL = (XCD_ROWS + 15) / 16, RT_BIG = 8;
+constexpr int MLP_BIG_ROWS = 1 << 16;
 constexpr int NTHR = 512;          // 8 wavefronts
 #ifndef QQT_MLP_PD
 #define QQT_MLP_PD 2
@@ -80,7 +87,6 @@ static_assert(PD >= 2 && PD % 2 == 0, "the x tile ring pairs with an LDS double 
 constexpr int V_B0 = 0, V_G1 = 128, V_BE1 = 256, V_B1 = 384, V_G2 = 512, V_BE2 = 640;
 constexpr int V_BH = 768, V_BF = 960, V_N = 968;
 
-constexpr int XT_HALVES = ROWS * 64;         // one 64-row x 64-K observation tile (8 KB)
 constexpr int W1_HALVES = HID * HID;         // one plane of the layer-2 fragments (32 KB)
 constexpr int WH_HALVES = 3 * HEAD * HID;    // one plane of the head-layer fragments (48 KB)
 constexpr int WF_HALVES = 16 * 3 * HEAD;     // one plane of the output-layer fragments (6 KB)
@@ -116,19 +122,20 @@ __device__ __forceinline__ int swz(int row, int chunk) {
   return chunk ^ (row & 7) ^ ((row >> 3) & 1);
 }
 
-// LDS of a workgroup of RB 64-row blocks.  xw holds the layer-1 x tiles
-// [group][buffer] and then layer 2's weight planes; after layer 1 the
-// partial-sum exchange reuses the x tiles, and after layer 2 the head
-// weights overwrite the x tiles and layer 2's weights.
-template <int RB>
+// LDS of a workgroup of RT row tiles.  xw holds the layer-1 x tiles
+// [group][buffer] (16RT rows x 64 K each) and then layer 2's weight planes;
+// after layer 1 the partial-sum exchange ([row tile][feature tile][lane]
+// floatx4, exactly the x tiles' bytes) reuses the x tiles, and after layer 2
+// the head weights overwrite the front of xw.
+template <int RT>
 struct __align__(16) MlpLds {
-  uint16_t xw[RB * 4 * XT_HALVES + 2 * W1_HALVES];
+  static constexpr int XT = RT * 16 * 64;     // halves of one x tile
+  static constexpr int XW = 4 * XT + 2 * W1_HALVES > 2 * WH_HALVES ? 4 * XT + 2 * W1_HALVES
+                                                                   : 2 * WH_HALVES;
+  uint16_t xw[XW];
   uint16_t wf[2 * WF_HALVES];                 // output-layer fragments, hi and lo planes
   float vec[V_N];                             // biases and LayerNorm affine parameters
 };
-static_assert(2 * WH_HALVES <= 4 * XT_HALVES + 2 * W1_HALVES, "head weights fit over x | W1");
-static_assert(4 * 8 * 64 * 4 * sizeof(float) <= 4 * XT_HALVES * sizeof(uint16_t),
-              "the partial-sum exchange of a 64-row block fits in its x tiles");
 
 // The B fragment (16 halves of row `row`, K 16q..16q+15 of the block) from a
 // swizzled 64-K observation tile.
@@ -303,36 +310,39 @@ __device__ __forceinline__ RowSampler load_sampler(const qqt_mlp_args& a, bool o
   return r;
 }
 
-// RB row blocks of 64 per workgroup: RB = 2 halves the W0 bytes each row
-// costs (large forward batches, no sampling).
+// RT row tiles (16RT rows) per workgroup.
 // Z1: the first-layer-only instantiation of the training forward (z1_out).
-template <int RB, bool Z1>
+template <int RT, bool Z1>
 __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
-  static_assert(RB == 1 || RB == 2, "one or two row blocks per workgroup");
-  constexpr int RT = 4 * RB;               // row tiles: per layer-1 wavefront, and tail wavefronts
-  constexpr int NX = 8 * RB;               // x load instructions per wavefront and K block
-  constexpr int XT = RB * XT_HALVES;       // one x tile of the workgroup
+  static_assert(RT >= 1 && RT <= 8, "tail wavefronts take one row tile each");
+  constexpr int ROWS = 16 * RT;            // rows of the workgroup's tiles
+  // rows the workgroup owns: an XCD row block for rollout-sized batches (the
+  // last tile's rows past it are computed on the next block's rows and dropped)
+  constexpr int BROWS = RT == RT_SMALL ? XCD_ROWS : ROWS;
+  static_assert(BROWS <= ROWS && BROWS > ROWS - 16, "the tiles cover the block");
+  constexpr int NX = 2 * RT;               // x load instructions per wavefront and K block
+  constexpr int XT = MlpLds<RT>::XT;       // one x tile of the workgroup
   constexpr int W1_CH = 2 * W1_HALVES / 8 / NTHR;   // 16-byte chunks of W1 per thread
   constexpr int WH_CH = 2 * WH_HALVES / 8 / NTHR;   // ... of the head weights
   constexpr int WF_CH = 2 * WF_HALVES / 8;          // 16-byte chunks of the output layer
   static_assert(W1_CH * NTHR * 8 == 2 * W1_HALVES && WH_CH * NTHR * 8 == 2 * WH_HALVES,
                 "weight staging divides over the threads");
   static_assert(WF_CH <= 2 * NTHR && WF_CH > NTHR, "two output-layer chunks per thread");
-  __shared__ MlpLds<RB> s;
-  const int nrb = (a.batch + RB * ROWS - 1) / (RB * ROWS);
+  __shared__ MlpLds<RT> s;
+  const int nrb = (a.batch + BROWS - 1) / BROWS;
   const int xcd = blockIdx.x & 7, seq = blockIdx.x >> 3;
   const int slot = seq % a.npid;
   const int rb = (seq / a.npid) * 8 + xcd;
   if (rb >= nrb) return;                   // padding workgroup (uniform, before any barrier)
   const int pid = a.npid == 2 ? slot : a.pid0;
-  const int row0 = rb * RB * ROWS;
+  const int row0 = rb * BROWS;
   // wavefront index as a scalar: branches and addresses on it stay uniform
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int r16 = lane & 15, q = lane >> 4;
   const int kg = w >> 2, cg = w & 3;       // layer-1 K group, column group
   const int oslots = a.out_slots > 0 ? a.out_slots : a.npid;   // output row width (slots)
   const int oslot = a.npid == 2 ? slot : a.out_slot;
-  uint16_t* const w1s = s.xw + RB * 4 * XT_HALVES;             // layer-2 weights in LDS
+  uint16_t* const w1s = s.xw + 4 * XT;                         // layer-2 weights in LDS
 
   // Parameter vectors (two floats per thread), the output layer's and layer
   // 2's weights: loaded before the first tiles (vmcnt retires in order) and
@@ -375,13 +385,13 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
     for (int ct = 0; ct < 2; ++ct) acc[rt][ct] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
   // x loads: instruction i of wavefront (kg, cg) covers tile rows
-  // 16RBcg+2i, 16RBcg+2i+1; lane l reads dword l&31 (two halves) of row
-  // 16RBcg+2i+(l>>5).
+  // 4RTcg+2i, 4RTcg+2i+1; lane l reads dword l&31 (two halves) of row
+  // 4RTcg+2i+(l>>5).
   const int nkb = a.kblocks0;
   const int dw = lane & 31;
   // row addresses are formed at each load from one base row (clamped to
   // the batch for a ragged last block), not held as NX pointers
-  const int xrow0 = row0 + 16 * RB * cg + (lane >> 5);
+  const int xrow0 = row0 + 4 * RT * cg + (lane >> 5);
   const uint32_t* const xbase = reinterpret_cast<const uint32_t*>(a.obs);
   const size_t xstride = (size_t)a.obs_stride / 2;    // dwords per row
   const uint16_t* wb = a.w0 + (size_t)((pid * 8 + 2 * cg) * nkb) * 64 * 16 + lane * 16;
@@ -409,7 +419,7 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
     uint32_t* t = reinterpret_cast<uint32_t*>(xt + buf * XT);
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
-      const int r = 16 * RB * cg + 2 * i + (lane >> 5);
+      const int r = 4 * RT * cg + 2 * i + (lane >> 5);
       t[r * 32 + (swz(r, dw >> 2) << 2) + (dw & 3)] = ok ? xr[i] : 0u;
     }
   };
@@ -447,8 +457,8 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
 
   // output row of lanes l and l + 16 (l < 16) of tail wavefront w: row0 + 16w + l
   const int srow = row0 + 16 * w + r16;
-  const RowSampler rs = load_sampler(a, !Z1 && a.sample && w < RT && lane < 32 && srow < a.batch,
-                                     q & 1, srow, pid, oslots, oslot);
+  const bool sown = w < RT && lane < 32 && 16 * w + r16 < BROWS && srow < a.batch;
+  const RowSampler rs = load_sampler(a, !Z1 && a.sample && sown, q & 1, srow, pid, oslots, oslot);
 
   s.vec[vi0] = vv0;
   if (vi1 < V_N) s.vec[vi1] = vv1;
@@ -511,11 +521,11 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
 
   if constexpr (Z1) {   // first layer only (the training forward): z1 = (f + f1) + b0
 #pragma unroll
-    for (int hb = 0; hb < RB; ++hb) {
-      // thread t: row t/8 of the block, features 16(t%8) .. +15 as four float4
-      const int row = ROWS * hb + (threadIdx.x >> 3), ft = threadIdx.x & 7;
+    for (int hb = 0; hb < (ROWS + 63) / 64; ++hb) {
+      // thread t: row 64hb + t/8 of the workgroup, features 16(t%8) .. +15 as four float4
+      const int row = 64 * hb + (threadIdx.x >> 3), ft = threadIdx.x & 7;
       const int orow = row0 + row;
-      if (orow < a.batch) {
+      if (row < BROWS && orow < a.batch) {
 #pragma unroll
         for (int q2 = 0; q2 < 4; ++q2) {
           const floatx4 e = ex[((row >> 4) * 8 + ft) * 64 + 16 * q2 + (row & 15)];
@@ -580,7 +590,7 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
     act = sample_masked_n(lg, rs.m, half0 ? 5 : 2, rs.u, &lp);
   }
   const float lpb = __shfl(lp, lane + 16, 64);
-  if (lane < 32 && srow < a.batch) {
+  if (sown) {
     const size_t oo = (size_t)srow * oslots + oslot;
     if (a.logits_out) {
 #pragma unroll
@@ -635,21 +645,22 @@ int qqt_mlp_act(const qqt_mlp_args* a, void* stream) {
   }
   // one workgroup per (row block, player); row blocks are dealt to the 8
   // XCDs round robin with both players' workgroups adjacent on one XCD.
-  // Large forward batches take two 64-row blocks per workgroup (half the
-  // W0 bytes per row); rollouts keep one, for twice the workgroups.
-  const bool two = !a->sample && a->batch >= MLP_TWO_BLOCK_ROWS;
-  const int rows_wg = (two ? 2 : 1) * ROWS;
+  // Large forward batches take 128-row blocks (W0 streamed once per 128
+  // rows); everything else XCD row blocks.
+  const bool big = !a->sample && a->batch >= MLP_BIG_ROWS;
+  const int rows_wg = big ? 16 * RT_BIG : XCD_ROWS;
   const int nrb = (a->batch + rows_wg - 1) / rows_wg;
   const int blocks = ((nrb + 7) / 8) * 8 * a->npid;
   hipStream_t st = (hipStream_t)stream;
-  if (a->z1_out && two)
-    QQT_LAUNCH(QQT_KERNEL_MLP, (mlp_act_kernel<2, true>), dim3(blocks), dim3(NTHR), st, *a);
+  if (a->z1_out && big)
+    QQT_LAUNCH(QQT_KERNEL_MLP, (mlp_act_kernel<RT_BIG, true>), dim3(blocks), dim3(NTHR), st, *a);
   else if (a->z1_out)
-    QQT_LAUNCH(QQT_KERNEL_MLP, (mlp_act_kernel<1, true>), dim3(blocks), dim3(NTHR), st, *a);
-  else if (two)
-    QQT_LAUNCH(QQT_KERNEL_MLP, (mlp_act_kernel<2, false>), dim3(blocks), dim3(NTHR), st, *a);
+    QQT_LAUNCH(QQT_KERNEL_MLP, (mlp_act_kernel<RT_SMALL, true>), dim3(blocks), dim3(NTHR), st, *a);
+  else if (big)
+    QQT_LAUNCH(QQT_KERNEL_MLP, (mlp_act_kernel<RT_BIG, false>), dim3(blocks), dim3(NTHR), st, *a);
   else
-    QQT_LAUNCH(QQT_KERNEL_MLP, (mlp_act_kernel<1, false>), dim3(blocks), dim3(NTHR), st, *a);
+    QQT_LAUNCH(QQT_KERNEL_MLP, (mlp_act_kernel<RT_SMALL, false>), dim3(blocks), dim3(NTHR), st,
+               *a);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     snprintf(g_err, sizeof(g_err), "mlp launch failed: %s", hipGetErrorString(err));

@@ -7,6 +7,15 @@
 
 namespace qqt {
 
+// Rows (envs) of one XCD row block.  The act kernel's rollout-sized
+// workgroups take this many rows, and the tick and bot kernels deal blocks
+// of this many envs to the 8 XCDs the same way (block b: row block
+// (b / 8 / workgroups per block) * 8 + b % 8), so an env's state, observation,
+// masks and actions stay in the L2 of one XCD from kernel to kernel.  44 rows:
+// 5632 envs are 16 blocks per XCD = 704 envs, exactly the tick kernel's one
+// round on an XCD's 32 CUs (22 envs each), and 256 act workgroups.
+constexpr int XCD_ROWS = 44;
+
 // Philox stream ids (third counter word); the host oracle uses the same ids.
 enum : uint32_t {
   STREAM_CRATE = 1, STREAM_RESET_CELL = 2, STREAM_RESET_MISC = 3,

@@ -244,16 +244,16 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
   __shared__ Lds<G, P> sh[WPB];
 
   // waves of one workgroup share nothing: each owns its envs and its LDS.
-  // Workgroups are dealt to the 8 XCDs round robin; block b takes 64-env row
-  // block (b / 8 / WGRB) * 8 + b % 8, so a row block's state, observation
+  // Workgroups are dealt to the 8 XCDs round robin; block b takes XCD_ROWS-env
+  // row block (b / 8 / WGRB) * 8 + b % 8, so a row block's state, observation
   // and masks stay in the L2 of the XCD whose policy workgroups read them
-  // (the act kernel deals 64-row blocks the same way).
-  constexpr int WGRB = 64 / (WPB * EPW);            // workgroups per 64-env row block
-  static_assert(WGRB * WPB * EPW == 64, "row blocks of 64 envs");
+  // (the act kernel deals its row blocks the same way).
+  constexpr int WGRB = XCD_ROWS / (WPB * EPW);      // workgroups per row block
+  static_assert(WGRB * WPB * EPW == XCD_ROWS, "whole workgroups per row block");
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int seq = blockIdx.x >> 3;
   const int rb = (seq / WGRB) * 8 + (blockIdx.x & 7);
-  const int g0 = rb * 64 + ((seq % WGRB) * WPB + wv) * EPW;
+  const int g0 = rb * XCD_ROWS + ((seq % WGRB) * WPB + wv) * EPW;
   if (g0 >= a.n_envs) return;
   Lds<G, P>& s = sh[wv];
   const int lane = threadIdx.x & 63;
@@ -1292,9 +1292,9 @@ int launch(const qqt_sim_config* cfg, const qqt_tick_args* a, hipStream_t st) {
   constexpr int LPE = QQT_LPE;
   constexpr int WPB = QQT_TICK_WPB;
   constexpr int EPW = 64 / LPE;
-  // 64-env row blocks, a multiple of 8 of them (one per XCD in turn)
-  const int nrb = (a->n_envs + 63) / 64;
-  const int blocks = ((nrb + 7) / 8) * 8 * (64 / (WPB * EPW));
+  // XCD_ROWS-env row blocks, a multiple of 8 of them (one per XCD in turn)
+  const int nrb = (a->n_envs + XCD_ROWS - 1) / XCD_ROWS;
+  const int blocks = ((nrb + 7) / 8) * 8 * (XCD_ROWS / (WPB * EPW));
   const bool ref = cfg->map_kind == QQT_MAP_REFERENCE;
   const dim3 grid(blocks), block(64 * WPB);
   if (a->mode == QQT_MODE_FLUSH)     // no reset in a flush
