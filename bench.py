@@ -57,6 +57,8 @@ MLP_BYTES_PER_ENV = 14 * 169 * 2 + 14 + 4 + 16
 MLP_FLOP_PER_ENV = 2 * 2 * (2366 * 128 + 128 * 128 + 3 * 128 * 64 + 64 * 8)
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_rollout_5632.json")
+STRESS_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_bomb_stress_16384.json")
+EVAL_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_eval_forward_4M.json")
 EVERY = 8   # kernel durations are sampled on every 8th timed step
 
 from qqtsim import _capi  # noqa: E402  (C ABI loader; loads the library lazily)
@@ -230,9 +232,11 @@ def cpu_baseline(cfg, spec, n, seed, budget_s, arch="mlp"):
                       f"{ticks1} ticks, {el1:.1f} s"}
 
 
-def read_traffic(kernel):
+def read_traffic(kernel, path=TRAFFIC_FILE):
+    """HBM bytes per dispatch of `kernel` (FETCH + WRITE, copy-calibrated) from
+    a committed rocprofv3 traffic summary, or None."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(path) as f:
             d = json.load(f)
         k = d["kernels"][kernel]
         return int(round(k["fetch_bytes"] + k["write_bytes"]))
@@ -446,7 +450,8 @@ def main_stress(args, torch, dev):
                    "envs": n, "parallelism": "single GPU"},
         "roofline": {"kernel": "tick_kernel", "bound": "hbm", "achieved": round(achieved, 3),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 5),
+                     "traffic": read_traffic("tick_kernel", STRESS_TRAFFIC_FILE)},
         "cpu_baseline": cpu,
         "kernels": {"tick_kernel": {"us": round(tick_ms * 1e3, 4),
                                     "bytes_per_env": TICK_BYTES_PER_ENV}},
@@ -643,6 +648,8 @@ def main_evalfwd(args, torch, dev):
     torch.cuda.synchronize()
     el_fwd = (time.perf_counter() - t1) / reps
     fwd_ms = kernel_ms()["mlp_act_kernel"]
+    if args.copy_calibrate:
+        _calibration_copy(torch, dev)
     gbs = EVAL_BYTES_PER_ROW * rows / (fwd_ms * 1e-3) / 1e9
     tflops = EVAL_FLOP_PER_ROW * rows / (fwd_ms * 1e-3) / 1e12
     cpu = cpu_baseline_forward(cfg, 32768, args.seed, args.cpu_seconds) \
@@ -660,7 +667,8 @@ def main_evalfwd(args, torch, dev):
                    "envs": n, "ticks": T, "rows": rows, "parallelism": "single GPU"},
         "roofline": {"kernel": "mlp_act_kernel (forward, 4.19M rows)", "bound": "hbm",
                      "achieved": round(gbs, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 5), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 5),
+                     "traffic": read_traffic("mlp_act_kernel", EVAL_TRAFFIC_FILE)},
         "mfma": {"achieved_tflops": round(tflops, 3), "peak_tflops": MFMA_F16_PEAK_TFLOPS,
                  "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 5),
                  "flop_per_row": EVAL_FLOP_PER_ROW},
