@@ -155,13 +155,31 @@ def cpu_baseline_stress(cfg, spec, n, seed, budget_s):
 
 
 def _cpu_model():
+    """lscpu's model name with its family / model / stepping ids and the
+    logical CPU count of the host (the name alone can be generic in a VM)."""
+    info = {}
     try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
-    except OSError:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if ":" in line:
+                k, v = line.split(":", 1)
+                info[k.strip()] = v.strip()
+    except (OSError, subprocess.SubprocessError):
         pass
-    return "unknown"
+    if not info.get("Model name"):
+        try:
+            for line in open("/proc/cpuinfo"):
+                if line.startswith("model name"):
+                    info["Model name"] = line.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            pass
+    name = info.get("Model name", "unknown")
+    ids = ", ".join(f"{k.lower()} {info[k]}" for k in ("CPU family", "Model", "Stepping")
+                    if info.get(k))
+    cpus = info.get("CPU(s)")
+    return f"{name} ({ids}; {cpus} logical CPUs on the host)" if ids or cpus else name
 
 
 def _cores(torch):
