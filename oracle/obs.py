@@ -138,3 +138,74 @@ def legal_mask(cfg, wall, fuse, owner, pos, alive, brick=None, bombs_p=None):
     bm = torch.ones((n, p, 2), dtype=torch.bool, device=pos.device)
     bm[..., 1] = place | ~alive
     return mm, bm
+
+
+# ---------------------------------------------------------------- lstm arch
+MAX_T = 10          # target slots of the relative-coordinate block
+GLOB_FEAT = 5       # global scalars
+LOCAL_K = 7         # side of the local window
+
+
+def local_view_features(cfg, obs, pos, alive, t, fuse, hp, only_p0: bool = False):
+    """Per-player features of the lstm arch (sim/obs.py:243-340):
+    local (N, P', C, 7, 7), rel (N, P', MAX_T, 6), glob (N, P', 5), in obs's
+    dtype, P' = 1 when only_p0 else P.
+
+    * local: the 7x7 window of every observation channel centred on the
+      player's centre cell (zero outside the grid).
+    * rel: slots 0..P-2 are the opponents (me + i + 1) % P: (pos diff axis 0,
+      pos diff axis 1, alive); the rest are the bombs (fuse > 0) nearest to
+      the centre cell in L1 distance: (column offset, row offset, 0, 1).
+      Slots past the last bomb carry the offsets of the remaining cells with
+      their third/fourth entries 0.  Bombs at equal distance, and the cells
+      of empty slots, are taken in ascending cell index (the reference takes
+      them in whatever order torch.topk returns among equal keys, which
+      differs between its CPU and GPU implementations).
+    * glob: t / max_steps, hp / max_hp, the danger channel at the centre
+      cell, bombs on the map / max_bombs, fuse total / (max_bombs * fuse).
+    """
+    n, p_full, _ = pos.shape
+    c, h, w = obs.shape[1], cfg.height, cfg.width
+    dt = obs.dtype
+    k, half = LOCAL_K, LOCAL_K // 2
+    p_out = 1 if only_p0 else p_full
+    cell = center_cell(pos)                                   # (N, P, 2)
+    pad = torch.nn.functional.pad(obs, (half, half, half, half))
+    local = torch.empty((n, p_out, c, k, k), dtype=dt)
+    rows = torch.arange(n)
+    for me in range(p_out):
+        for dy in range(k):
+            for dx in range(k):
+                local[:, me, :, dy, dx] = pad[rows, :, cell[:, me, 0] + dy, cell[:, me, 1] + dx]
+    rel = torch.zeros((n, p_out, MAX_T, 6), dtype=dt)
+    n_opp = p_full - 1
+    for me in range(p_out):
+        for i in range(n_opp):
+            opp = (me + i + 1) % p_full
+            rel[:, me, i, 0] = (pos[:, opp, 0] - pos[:, me, 0]).to(dt)
+            rel[:, me, i, 1] = (pos[:, opp, 1] - pos[:, me, 1]).to(dt)
+            rel[:, me, i, 2] = alive[:, opp].to(dt)
+    slots = min(MAX_T - n_opp, h * w)
+    gy = torch.arange(h).view(1, h, 1)
+    gx = torch.arange(w).view(1, 1, w)
+    has = (fuse > 0).reshape(n, -1)
+    idx = torch.arange(h * w)
+    for me in range(p_out):
+        cy, cx = cell[:, me, 0], cell[:, me, 1]
+        dist = ((gy - cy.view(n, 1, 1)).abs() + (gx - cx.view(n, 1, 1)).abs()).reshape(n, -1)
+        # (distance, cell) ascending; cells without a bomb after every bomb
+        key = torch.where(has, dist, torch.full_like(dist, 1 << 20)) * (h * w) + idx
+        order = key.argsort(dim=1)[:, :slots]
+        for j in range(slots):
+            gi = order[:, j]
+            rel[:, me, n_opp + j, 0] = ((gi % w).float() - cx.float()).to(dt)
+            rel[:, me, n_opp + j, 1] = ((gi // w).float() - cy.float()).to(dt)
+            rel[:, me, n_opp + j, 3] = has[rows, gi].to(dt)
+    glob = torch.zeros((n, p_out, GLOB_FEAT), dtype=dt)
+    glob[..., 0] = (t.to(dt) / cfg.max_steps).unsqueeze(-1)
+    glob[..., 1] = hp[:, :p_out].to(dt) / cfg.max_hp
+    dflat = obs[:, 2 * p_full + 1].reshape(n, -1)
+    glob[..., 2] = dflat.gather(1, (cell[:, :p_out, 0] * w + cell[:, :p_out, 1]).reshape(n, -1))
+    glob[..., 3] = (has.float().sum(1) / cfg.max_bombs).to(dt).unsqueeze(-1)
+    glob[..., 4] = (fuse.float().reshape(n, -1).sum(1) / (cfg.max_bombs * cfg.fuse)).to(dt).unsqueeze(-1)
+    return local, rel, glob

@@ -165,3 +165,54 @@ def cnn_forward(params: dict, obs: torch.Tensor, pid: int, n_players: int = 2,
         return F.linear(y, P[f"{name}.2.weight"], P[f"{name}.2.bias"])
 
     return head("move_head"), head("bomb_head"), head("critic").squeeze(-1)
+
+
+LSTM_HIDDEN = 128
+
+
+def lstm_cell(x, h, c, w_ih, w_hh, b_ih, b_hh):
+    """One step of a single-layer LSTM (gate order input, forget, cell,
+    output, as torch.nn.LSTM stores them): returns (h', c')."""
+    g = F.linear(x, w_ih, b_ih) + F.linear(h, w_hh, b_hh)
+    i, f, gg, o = g.chunk(4, dim=1)
+    c2 = torch.sigmoid(f) * c + torch.sigmoid(i) * torch.tanh(gg)
+    return torch.sigmoid(o) * torch.tanh(c2), c2
+
+
+def lstm_fused(params: dict, local, rel, glob, dtype=torch.float32):
+    """The lstm arch's per-frame features (train/model.py:198-214,
+    extract_fused): conv 3x3 C->32, ReLU, conv 3x3 32->64, ReLU, 2x2 max
+    pool (7 -> 3), Linear(576,128) ReLU; rel Linear(60,64) ReLU Linear(64,32)
+    ReLU; glob Linear(5,16) ReLU Linear(16,8) ReLU; Linear(168,256) ReLU."""
+    P = {k: v.to(dtype) for k, v in params.items()}
+    b = local.shape[0]
+    x = F.relu(F.conv2d(local.to(dtype), P["l_conv1.weight"], P["l_conv1.bias"], padding=1))
+    x = F.max_pool2d(F.relu(F.conv2d(x, P["l_conv2.weight"], P["l_conv2.bias"], padding=1)), 2)
+    x = F.relu(F.linear(x.reshape(b, -1), P["l_cnn_fc.weight"], P["l_cnn_fc.bias"]))
+    r = F.relu(F.linear(rel.to(dtype).reshape(b, -1), P["l_rel_fc1.weight"], P["l_rel_fc1.bias"]))
+    r = F.relu(F.linear(r, P["l_rel_fc2.weight"], P["l_rel_fc2.bias"]))
+    g = F.relu(F.linear(glob.to(dtype), P["l_glob_fc1.weight"], P["l_glob_fc1.bias"]))
+    g = F.relu(F.linear(g, P["l_glob_fc2.weight"], P["l_glob_fc2.bias"]))
+    return F.relu(F.linear(torch.cat([x, r, g], 1), P["l_fusion.weight"], P["l_fusion.bias"]))
+
+
+def lstm_forward(params: dict, local, rel, glob, hidden=None, dtype=torch.float32):
+    """(move_logits, bomb_logits, value, (h', c')) of the lstm ActorCritic
+    for one frame (train/model.py:176-185); hidden = (h, c), each (B, 128),
+    or None for the zero state."""
+    P = {k: v.to(dtype) for k, v in params.items()}
+    x = lstm_fused(params, local, rel, glob, dtype)
+    b = x.shape[0]
+    if hidden is None:
+        h = torch.zeros((b, LSTM_HIDDEN), dtype=dtype)
+        c = torch.zeros_like(h)
+    else:
+        h, c = (t.to(dtype) for t in hidden)
+    h, c = lstm_cell(x, h, c, P["lstm.weight_ih_l0"], P["lstm.weight_hh_l0"],
+                     P["lstm.bias_ih_l0"], P["lstm.bias_hh_l0"])
+
+    def head(name):
+        y = F.relu(F.linear(h, P[f"{name}.0.weight"], P[f"{name}.0.bias"]))
+        return F.linear(y, P[f"{name}.2.weight"], P[f"{name}.2.bias"])
+
+    return head("move_head"), head("bomb_head"), head("critic").squeeze(-1), (h, c)

@@ -26,6 +26,9 @@ permutation):
 * mlp.npz - MLP ActorCritic weights, inputs and forward/evaluate outputs.
 * cnn.npz - the same for ActorCritic(arch="cnn") (conv trunk with the view
   permutation on conv0's input channels, per-sample LayerNorms).
+* lstm.npz - the lstm arch's per-player features (sim/obs.py
+  local_view_features) on bomb-rich states, and ActorCritic(arch="lstm") run
+  over those frames as sequences (hidden state carried, zeroed on reset).
 * astar_<name>.npz - the reference astar bot (sim/bots.py astar_attack, no
   behaviour modes, no crate eating) as player 1 against random legal moves
   for player 0: per tick the bot's inputs (state, observation, masks, the
@@ -179,6 +182,80 @@ def rollout(name, spec, kind, n=64, ticks=128, seed=0, obs_envs=4, cfg_kw=None):
     placed = int((np.stack([st["fuse"] for st in states]) == 30).sum())
     print(f"{name}: ticks={ticks} placed~{placed} deaths={int(out['died'].sum())} "
           f"done_ticks={int(out['done'].sum())} resolve_hint={int(out['resolve_hint'])}")
+
+
+def lstm(n=64, ticks=48, seed=23, every=4):
+    """lstm.npz: the reference's per-player features for the lstm arch
+    (sim/obs.py local_view_features, full P and only_p0) on states of a
+    bomb-rich rollout, and the lstm ActorCritic (train/model.py, arch "lstm")
+    run over those frames as a sequence with its hidden state carried."""
+    from sim.obs import local_view_features
+
+    spec = MapSpec(kind="pillars", brick_p=0.4, bombs_cap=(2, 4), blast_cap=(2, 5))
+    s = ref_sim(n, spec, seed)
+    p = s.cfg.n_players
+    rec = {k: [] for k in ("obs", "pos", "alive", "t", "fuse", "hp", "local", "rel", "glob",
+                           "local0", "rel0", "glob0", "mm", "bm")}
+    mm, bm = (m.numpy().copy() for m in s.legal_mask())
+    for tick in range(ticks):
+        if tick % every == every - 1:
+            obs = s.observe()
+            args = (s.cfg, obs, s.pos, s.alive, s.t, s.fuse, s.hp)
+            lf = local_view_features(*args, only_p0=False)
+            l0 = local_view_features(*args, only_p0=True)
+            for k, v in (("obs", obs), ("pos", s.pos), ("alive", s.alive), ("t", s.t),
+                         ("fuse", s.fuse), ("hp", s.hp), ("local", lf[0]), ("rel", lf[1]),
+                         ("glob", lf[2]), ("local0", l0[0]), ("rel0", l0[1]), ("glob0", l0[2])):
+                rec[k].append(v.numpy().copy())
+            rec["mm"].append(mm)
+            rec["bm"].append(bm)
+        a = actions_for("inject", mm, bm, n, seed, tick)
+        cu = philox.uniforms(seed, np.arange(n), tick, philox.STREAM_CRATE, 2 * p)
+        cu = cu.reshape(n, p, 2).transpose(1, 2, 0).copy()
+        s._rand_buf = torch.from_numpy(np.concatenate(
+            [cu[:, 0, :].T.reshape(-1), cu[:, 1, :].T.reshape(-1)]))
+        s.step(torch.from_numpy(a), auto_reset=False)
+        mm, bm = (m.numpy().copy() for m in s.legal_mask())
+    out = {k: np.stack(v) for k, v in rec.items()}
+
+    torch.manual_seed(0)
+    net = ActorCritic((14, 13, 13), arch="lstm", n_players=2)
+    g = torch.Generator().manual_seed(2)
+    with torch.no_grad():
+        for name, prm in net.named_parameters():
+            if "bias" in name:
+                prm.add_(0.1 * torch.randn(prm.shape, generator=g))
+    out.update({"w_" + k.replace(".", "_"): v.numpy().copy() for k, v in net.state_dict().items()})
+    # player 0's frames as one sequence per env; hidden carried from zero,
+    # zeroed for envs flagged in `reset` after a frame (as collect does on done)
+    steps = out["local0"].shape[0]
+    reset = np.zeros((steps, n), dtype=bool)
+    reset[steps // 2, ::5] = True
+    hidden = None
+    acts = np.stack([actions_for("legal", out["mm"][i], out["bm"][i], n, seed, 1000 + i)[:, 0]
+                     for i in range(steps)])
+    res = {k: [] for k in ("move_logits", "bomb_logits", "value", "h", "c", "logp", "entropy")}
+    with torch.no_grad():
+        for i in range(steps):
+            f = (torch.from_numpy(out["local0"][i][:, 0]), torch.from_numpy(out["rel0"][i][:, 0]),
+                 torch.from_numpy(out["glob0"][i][:, 0]))
+            lp, ent, _ = net.evaluate(f, torch.from_numpy(out["mm"][i][:, 0]),
+                                      torch.from_numpy(out["bm"][i][:, 0]),
+                                      torch.from_numpy(acts[i]), 0, hidden)
+            ml, bl, v, hidden = net(f, 0, hidden)
+            for k, x in (("move_logits", ml), ("bomb_logits", bl), ("value", v),
+                         ("h", hidden[0][0]), ("c", hidden[1][0]), ("logp", lp), ("entropy", ent)):
+                res[k].append(x.numpy().copy())
+            if reset[i].any():
+                dk = torch.from_numpy(reset[i]).float().view(1, -1, 1)
+                hidden = (hidden[0] * (1 - dk), hidden[1] * (1 - dk))
+    out.update({k: np.stack(v) for k, v in res.items()})
+    out["actions"] = acts
+    out["reset"] = reset
+    out["param_count"] = np.int64(sum(q.numel() for q in net.parameters()))
+    np.savez_compressed(os.path.join(HERE, "lstm.npz"), **out)
+    print("lstm: frames", steps, "envs", n, "bombs/frame",
+          float((out["fuse"] > 0).sum(axis=(1, 2, 3)).mean()), "params", int(out["param_count"]))
 
 
 def deep_chain():
@@ -373,6 +450,8 @@ if __name__ == "__main__" and len(sys.argv) > 1:
             astar_chain()
         elif what == "cnn":
             mlp(arch="cnn")
+        elif what == "lstm":
+            lstm()
         else:
             raise SystemExit(f"unknown fixture group {what!r}")
 elif __name__ == "__main__":
@@ -391,3 +470,4 @@ elif __name__ == "__main__":
           seed=13)
     astar("open", MapSpec(kind="open", bombs_cap=(2, 3), blast_cap=(2, 4)), ticks=96, seed=17)
     astar_chain()
+    lstm()

@@ -87,3 +87,18 @@ def cnn_params(z):
         elif k.startswith("w_conv_"):
             out["conv." + k[len("w_conv_"):].replace("_", ".")] = torch.from_numpy(z[k])
     return out
+
+
+LSTM_KEYS = ("l_conv1.weight", "l_conv1.bias", "l_conv2.weight", "l_conv2.bias",
+             "l_cnn_fc.weight", "l_cnn_fc.bias", "l_rel_fc1.weight", "l_rel_fc1.bias",
+             "l_rel_fc2.weight", "l_rel_fc2.bias", "l_glob_fc1.weight", "l_glob_fc1.bias",
+             "l_glob_fc2.weight", "l_glob_fc2.bias", "l_fusion.weight", "l_fusion.bias",
+             "lstm.weight_ih_l0", "lstm.weight_hh_l0", "lstm.bias_ih_l0", "lstm.bias_hh_l0")
+
+
+def lstm_params(z):
+    """state_dict of the lstm ActorCritic from lstm.npz's w_* arrays."""
+    out = mlp_params(z)
+    for k in LSTM_KEYS:
+        out[k] = torch.from_numpy(z["w_" + k.replace(".", "_")])
+    return out
