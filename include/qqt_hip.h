@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 13
+#define QQT_ABI_VERSION 14
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -397,6 +397,71 @@ typedef struct qqt_cnn_args {
 } qqt_cnn_args;
 int qqt_cnn_act(const qqt_cnn_args* args, void* stream);
 
+/* Per-player features of the lstm arch (replaces sim/obs.py:243-340,
+ * local_view_features, which the reference's collect loop calls each tick
+ * for its lstm learner, train/ppo.py:227-231).  From the sim state and its
+ * float16 observation: local = the 7x7 window of every channel around the
+ * player's centre cell (zero outside the grid); rel = the P-1 opponents
+ * (pos difference on axis 0, on axis 1, alive) then the bombs nearest in L1
+ * distance (column offset, row offset, 0, 1; equal distances in ascending
+ * cell index; slots past the last bomb hold the offsets of the lowest-index
+ * remaining cells with flag 0); glob = t/max_steps, hp/max_hp, danger at the
+ * centre cell, bombs/max_bombs, fuse sum/(max_bombs*fuse).  Outputs are
+ * float16, rows of p_out players per env, `*_stride` elements apart (so a
+ * call can write straight into a rollout buffer's slot). */
+typedef struct qqt_lstm_feat_args {
+  int32_t n_envs;
+  int32_t p_out;              /* 1: player 0 only (only_p0=True), or n_players */
+  const int32_t* cells;       /* sim state, layout above */
+  const int32_t* players;
+  const int32_t* envs;
+  const uint16_t* obs;        /* [N][5P+4][H][W] float16 of the same state */
+  uint16_t* local;            /* per env [p_out][C][7][7] */
+  uint16_t* rel;              /* per env [p_out][10][6] */
+  uint16_t* glob;             /* per env [p_out][5] */
+  int64_t local_stride, rel_stride, glob_stride;   /* elements between envs */
+} qqt_lstm_feat_args;
+int qqt_lstm_features(const qqt_sim_config* cfg, const qqt_lstm_feat_args* args, void* stream);
+
+/* lstm actor/critic step (replaces ActorCritic.act / forward with arch
+ * "lstm", train/model.py:103-120, 176-185, 198-214, 230-245): per row the
+ * 7x7 conv trunk (C->32->64, 2x2 max pool, Linear 576->128), the rel and glob
+ * MLPs, the 256-wide fusion layer, one LSTM step (hidden 128) and the heads,
+ * then masked sampling (the same Philox draws and sampler as qqt_mlp_act).
+ * float32 arithmetic on the float32 MFMA.  Row r belongs to env
+ * r / rows_per_env and player (rows_per_env == 1 ? pid0 : r % rows_per_env).
+ * h and c are read (zero for rows of envs with reset[env] != 0) and
+ * overwritten with the new state. */
+typedef struct qqt_lstm_args {
+  int32_t batch;              /* rows B */
+  int32_t c_in;               /* observation channels C of the local windows (<= 14) */
+  int32_t rows_per_env;       /* 1 or P */
+  int32_t pid0;
+  int32_t sample;             /* 1: draw actions (needs masks) */
+  uint64_t seed;              /* Philox key of the policy uniforms */
+  uint32_t tick;              /* counter word of the policy uniforms */
+  const uint16_t* local;      /* [B] rows of [C][7][7] float16 */
+  const uint16_t* rel;        /* [B] rows of [10][6] */
+  const uint16_t* glob;       /* [B] rows of [5] */
+  int64_t local_stride, rel_stride, glob_stride;   /* elements between rows */
+  const float* params;        /* packed parameters (qqtsim/policy.py pack_lstm, QQT_LSTM_PARAMS floats) */
+  float* h;                   /* [B][128] hidden state in / out */
+  float* c;                   /* [B][128] cell state in / out */
+  const uint8_t* reset;       /* [envs] or NULL */
+  const uint8_t* move_mask;   /* row r at r * mm_row_stride, 5 bytes */
+  const uint8_t* bomb_mask;   /* row r at r * bm_row_stride, 2 bytes */
+  int32_t mm_row_stride, bm_row_stride;
+  const float* uniforms;      /* [B][2] (move, bomb) or NULL = Philox */
+  int32_t out_stride, out_slot;   /* outputs of row r at slot r * out_stride + out_slot */
+  int64_t* actions;           /* [slot][2] or NULL */
+  int8_t* actions_i8;         /* [slot][2] or NULL */
+  float* logp_out;            /* [slot] or NULL */
+  float* value_out;           /* [slot] or NULL */
+  float* logits_out;          /* [B][8]: 5 move, 2 bomb, value; or NULL */
+} qqt_lstm_args;
+#define QQT_LSTM_PARAMS 371584
+int qqt_lstm_act(const qqt_lstm_args* args, void* stream);
+
 /* Dispatch timing for benchmark harnesses (no counterpart in the reference:
  * its bench times whole steps with host clocks).  qqt_timing_arm(n) times
  * the next n kernel launches made through this library: each records a
@@ -408,7 +473,7 @@ int qqt_cnn_act(const qqt_cnn_args* args, void* stream);
  * memory (the event pool is created by the first arm). */
 enum { QQT_KERNEL_TICK = 0, QQT_KERNEL_MLP = 1, QQT_KERNEL_BOT = 2, QQT_KERNEL_REACH = 3,
        QQT_KERNEL_GAE = 4, QQT_KERNEL_L1GRAD = 5, QQT_KERNEL_PPO = 6, QQT_KERNEL_CNN = 7,
-       QQT_KERNEL_KINDS = 8 };
+       QQT_KERNEL_LSTM_FEAT = 8, QQT_KERNEL_LSTM = 9, QQT_KERNEL_KINDS = 10 };
 int qqt_timing_arm(int32_t launches);
 int qqt_timing_collect(double* ms, int32_t* count, int32_t n_kinds);
 

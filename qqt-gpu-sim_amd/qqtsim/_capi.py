@@ -14,7 +14,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 
 from ._build import LIB
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 MODE_STEP, MODE_OBSERVE, MODE_RESET, MODE_PROBE, MODE_FLUSH = 0, 1, 2, 3, 4
 MAP_PILLARS, MAP_OPEN, MAP_REFERENCE = 0, 1, 2
@@ -106,6 +106,23 @@ class CnnArgsC(ctypes.Structure):
                            "logp_out", "value_out", "logits_out")]
 
 
+class LstmFeatArgsC(ctypes.Structure):
+    _fields_ = [("n_envs", _i32), ("p_out", _i32)] + [
+        (n, _vp) for n in ("cells", "players", "envs", "obs", "local", "rel", "glob")] + [
+        (n, ctypes.c_int64) for n in ("local_stride", "rel_stride", "glob_stride")]
+
+
+class LstmArgsC(ctypes.Structure):
+    _fields_ = [(n, _i32) for n in ("batch", "c_in", "rows_per_env", "pid0", "sample")] + [
+        ("seed", _u64), ("tick", _u32)] + [
+        (n, _vp) for n in ("local", "rel", "glob")] + [
+        (n, ctypes.c_int64) for n in ("local_stride", "rel_stride", "glob_stride")] + [
+        (n, _vp) for n in ("params", "h", "c", "reset", "move_mask", "bomb_mask")] + [
+        ("mm_row_stride", _i32), ("bm_row_stride", _i32), ("uniforms", _vp),
+        ("out_stride", _i32), ("out_slot", _i32)] + [
+        (n, _vp) for n in ("actions", "actions_i8", "logp_out", "value_out", "logits_out")]
+
+
 class GaeArgsC(ctypes.Structure):
     _fields_ = [("steps", _i32), ("n_envs", _i32), ("gamma", _f32), ("gamma_lam", _f32),
                 ("step_stride", ctypes.c_int64), ("env_stride", ctypes.c_int64)] + [
@@ -143,6 +160,11 @@ def lib():
         L.qqt_ppo_grad.argtypes = [ctypes.POINTER(PpoArgsC), _vp]
         L.qqt_cnn_act.restype = ctypes.c_int
         L.qqt_cnn_act.argtypes = [ctypes.POINTER(CnnArgsC), _vp]
+        L.qqt_lstm_features.restype = ctypes.c_int
+        L.qqt_lstm_features.argtypes = [ctypes.POINTER(SimConfigC), ctypes.POINTER(LstmFeatArgsC),
+                                        _vp]
+        L.qqt_lstm_act.restype = ctypes.c_int
+        L.qqt_lstm_act.argtypes = [ctypes.POINTER(LstmArgsC), _vp]
         L.qqt_timing_arm.restype = ctypes.c_int
         L.qqt_timing_arm.argtypes = [_i32]
         L.qqt_timing_collect.restype = ctypes.c_int
@@ -154,7 +176,8 @@ def lib():
 
 
 KERNEL_KINDS = ("tick_kernel", "mlp_act_kernel", "bot_kernel", "reach_kernel",
-                "gae_kernel", "l1grad_kernels", "ppo_grad_kernel", "cnn_act_kernel")  # QQT_KERNEL_*
+                "gae_kernel", "l1grad_kernels", "ppo_grad_kernel", "cnn_act_kernel",
+                "lstm_feat_kernel", "lstm_act_kernel")  # QQT_KERNEL_*
 
 
 def timing_arm(launches: int) -> None:

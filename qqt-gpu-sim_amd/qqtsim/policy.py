@@ -31,6 +31,9 @@ from .config import n_obs_channels, view_perm
 KBLOCK = 64
 HID = 128
 HEAD = 64
+LSTM_HIDDEN = 128          # train/model.py LSTM_HIDDEN
+LSTM_MAX_T = 10            # rel target slots (sim/obs.py MAX_T)
+LSTM_GLOB = 5              # global scalars (sim/obs.py GLOB_FEAT)
 
 
 def column_permutation(pid: int, p: int, c: int, hw: int) -> torch.Tensor:
@@ -118,8 +121,10 @@ def pack_mlp(params: dict, n_players: int = 2, obs_shape=(14, 13, 13)) -> dict:
 def _layer_tree(arch: str, obs_shape, n_moves: int, n_bomb: int) -> torch.nn.Module:
     """The ActorCritic layers of `arch` as plain torch modules, created (and
     so drawing their PyTorch default init) in the reference's registration
-    order: the cnn trunk `conv0`, `conv` (train/model.py:76-93), then
-    `shared`, `move_head`, `bomb_head`, `critic` (:140-153)."""
+    order: the cnn trunk `conv0`, `conv` (train/model.py:76-93) or the lstm
+    arch's `l_conv1` .. `l_fusion`, `lstm` (:103-120; nn.LSTM draws its own
+    uniform init when built), then `shared` (not for lstm), `move_head`,
+    `bomb_head`, `critic` (:140-153)."""
     c, h, w = obs_shape
     nn = torch.nn
     tree = nn.Module()
@@ -131,12 +136,23 @@ def _layer_tree(arch: str, obs_shape, n_moves: int, n_bomb: int) -> torch.nn.Mod
             nn.LayerNorm([64, h, w]), nn.ReLU(), nn.Conv2d(64, 8, 1),
             nn.LayerNorm([8, h, w]), nn.ReLU())
         flat = 8 * h * w
+    elif arch == "lstm":
+        tree.l_conv1 = nn.Conv2d(c, 32, 3, padding=1)
+        tree.l_conv2 = nn.Conv2d(32, 64, 3, padding=1)
+        tree.l_cnn_fc = nn.Linear(64 * 3 * 3, HID)
+        tree.l_rel_fc1 = nn.Linear(LSTM_MAX_T * 6, 64)
+        tree.l_rel_fc2 = nn.Linear(64, 32)
+        tree.l_glob_fc1 = nn.Linear(LSTM_GLOB, 16)
+        tree.l_glob_fc2 = nn.Linear(16, 8)
+        tree.l_fusion = nn.Linear(HID + 32 + 8, 256)
+        tree.lstm = nn.LSTM(256, LSTM_HIDDEN, 1, batch_first=True)
     elif arch == "mlp":
         flat = c * h * w
     else:
         raise ValueError(f"no layer tree for arch {arch!r}")
-    tree.shared = nn.Sequential(nn.Linear(flat, HID), nn.LayerNorm(HID), nn.ReLU(),
-                                nn.Linear(HID, HID), nn.LayerNorm(HID), nn.ReLU())
+    if arch != "lstm":
+        tree.shared = nn.Sequential(nn.Linear(flat, HID), nn.LayerNorm(HID), nn.ReLU(),
+                                    nn.Linear(HID, HID), nn.LayerNorm(HID), nn.ReLU())
     tree.move_head = nn.Sequential(nn.Linear(HID, HEAD), nn.ReLU(), nn.Linear(HEAD, n_moves))
     tree.bomb_head = nn.Sequential(nn.Linear(HID, HEAD), nn.ReLU(), nn.Linear(HEAD, n_bomb))
     tree.critic = nn.Sequential(nn.Linear(HID, HEAD), nn.ReLU(), nn.Linear(HEAD, 1))
@@ -497,3 +513,234 @@ class HipCnnActorCritic(HipActorCritic):
 
     def _launch(self, a, stream) -> None:
         _capi.check(self._lib.qqt_cnn_act(a, stream))
+
+
+# ---------------------------------------------------------------- lstm arch
+LSTM_PARAMS = 371584       # QQT_LSTM_PARAMS
+# float offsets of the packed block: (key, rows, columns) per k-major matrix
+# [in][out] or vector, in block order (qqt-gpu-sim_amd/csrc/lstm.hip OFF_*)
+_LSTM_BLOCKS = (("c1w", 128, 32), ("c1b", 1, 64), ("c2w", 288, 64), ("c2b", 1, 64),
+                ("fcw", 576, 128), ("fcb", 1, 128), ("r1w", 64, 64), ("r1b", 1, 64),
+                ("r2w", 64, 32), ("r2b", 1, 64), ("g1w", 8, 16), ("g1b", 1, 64),
+                ("g2w", 16, 16), ("g2b", 1, 64), ("fuw", 168, 256), ("fub", 1, 256),
+                ("lw", 384, 512), ("lb", 1, 512), ("hw", 128, 192), ("hb", 1, 192),
+                ("ow", 192, 16), ("ob", 1, 64))
+
+
+def pack_lstm(params: dict, obs_channels: int = 14) -> torch.Tensor:
+    """One float32 block of QQT_LSTM_PARAMS values for qqt_lstm_act from an
+    lstm ActorCritic state_dict (train/model.py:103-120, 140-153): every
+    weight transposed to k-major [in][out] and zero-padded to the block's
+    shape.  Convolution rows are k = in_channel * 9 + ky * 3 + kx (conv1 padded
+    to 128 rows); the LSTM block stacks W_ih^T over W_hh^T with the bias
+    b_ih + b_hh, gate columns in torch's i, f, g, o order; the heads' hidden
+    layers sit side by side (move | bomb | critic, 192 columns) and their
+    output layers form one block-diagonal [192][16] matrix whose columns
+    0-4, 5-6, 7 are the move logits, bomb logits and value."""
+    c = obs_channels
+    f = lambda k: params[k].detach().float().cpu()  # noqa: E731
+    shapes = {"l_conv1.weight": (32, c, 3, 3), "l_conv2.weight": (64, 32, 3, 3),
+              "l_cnn_fc.weight": (HID, 576), "l_rel_fc1.weight": (64, LSTM_MAX_T * 6),
+              "l_rel_fc2.weight": (32, 64), "l_glob_fc1.weight": (16, LSTM_GLOB),
+              "l_glob_fc2.weight": (8, 16), "l_fusion.weight": (256, HID + 40),
+              "lstm.weight_ih_l0": (4 * LSTM_HIDDEN, 256),
+              "lstm.weight_hh_l0": (4 * LSTM_HIDDEN, LSTM_HIDDEN),
+              "move_head.0.weight": (HEAD, HID), "move_head.2.weight": (5, HEAD),
+              "bomb_head.0.weight": (HEAD, HID), "bomb_head.2.weight": (2, HEAD),
+              "critic.0.weight": (HEAD, HID), "critic.2.weight": (1, HEAD)}
+    if c > 14:
+        raise ValueError("the lstm kernel takes at most 14 observation channels")
+    for k, shp in shapes.items():
+        if tuple(params[k].shape) != shp:
+            raise ValueError(f"{k} must be {shp}, got {tuple(params[k].shape)}")
+    src = {
+        "c1w": f("l_conv1.weight").reshape(32, c * 9).t(), "c1b": f("l_conv1.bias"),
+        "c2w": f("l_conv2.weight").reshape(64, 288).t(), "c2b": f("l_conv2.bias"),
+        "fcw": f("l_cnn_fc.weight").t(), "fcb": f("l_cnn_fc.bias"),
+        "r1w": f("l_rel_fc1.weight").t(), "r1b": f("l_rel_fc1.bias"),
+        "r2w": f("l_rel_fc2.weight").t(), "r2b": f("l_rel_fc2.bias"),
+        "g1w": f("l_glob_fc1.weight").t(), "g1b": f("l_glob_fc1.bias"),
+        "g2w": f("l_glob_fc2.weight").t(), "g2b": f("l_glob_fc2.bias"),
+        "fuw": f("l_fusion.weight").t(), "fub": f("l_fusion.bias"),
+        "lw": torch.cat([f("lstm.weight_ih_l0").t(), f("lstm.weight_hh_l0").t()]),
+        "lb": f("lstm.bias_ih_l0") + f("lstm.bias_hh_l0"),
+        "hw": torch.cat([f(f"{n}.0.weight") for n in ("move_head", "bomb_head", "critic")]).t(),
+        "hb": torch.cat([f(f"{n}.0.bias") for n in ("move_head", "bomb_head", "critic")]),
+        "ob": torch.cat([f(f"{n}.2.bias") for n in ("move_head", "bomb_head", "critic")]),
+    }
+    ow = torch.zeros((3 * HEAD, 16))
+    ow[0:HEAD, 0:5] = f("move_head.2.weight").t()
+    ow[HEAD:2 * HEAD, 5:7] = f("bomb_head.2.weight").t()
+    ow[2 * HEAD:, 7:8] = f("critic.2.weight").t()
+    src["ow"] = ow
+    out = torch.zeros(LSTM_PARAMS, dtype=torch.float32)
+    off = 0
+    for key, rows, cols in _LSTM_BLOCKS:
+        blk = out[off:off + rows * cols].view(rows, cols)
+        v = src[key]
+        if v.dim() == 1:
+            blk[0, :v.numel()] = v
+        else:
+            blk[:v.shape[0], :v.shape[1]] = v
+        off += rows * cols
+    if off != LSTM_PARAMS:
+        raise AssertionError("packed block size")
+    return out
+
+
+def lstm_block_offsets() -> dict:
+    """Float offset of each block of the packed lstm parameters."""
+    offs, off = {}, 0
+    for key, rows, cols in _LSTM_BLOCKS:
+        offs[key] = off
+        off += rows * cols
+    return offs
+
+
+class HipLstmActorCritic:
+    """The reference's lstm `ActorCritic` (train/model.py:103-120, 176-185,
+    198-256) on qqt_lstm_act.  `obs` is the per-player feature triple
+    (local (B,C,7,7), rel (B,10,6), glob (B,5)) of
+    `HipBatchedSim.local_view_features` (float16), `hidden` the LSTM state
+    as torch.nn.LSTM holds it ((1,B,128), (1,B,128)) or None for zeros.
+
+    forward(obs, pid, hidden) -> (move logits, bomb logits, value, hidden')
+    act(obs, mm, bm, pid, hidden) -> (actions (B,2), logp, value, hidden')
+    evaluate(obs, mm, bm, actions, pid, hidden) -> (logp, entropy, value)
+
+    Every step runs the whole network in one kernel (float32 arithmetic);
+    hidden' is a new pair of tensors.  `step_` runs one frame of a rollout
+    with the state held in place and zeroed for the envs flagged in `reset`
+    (the reference's hidden * (1 - done) after each tick)."""
+
+    arch = "lstm"
+
+    def __init__(self, state_dict: dict | None = None, obs_shape=(14, 13, 13),
+                 n_players: int = 2, device="cuda", seed: int = 0):
+        self.obs_shape = tuple(obs_shape)
+        self.n_players = n_players
+        if n_obs_channels(n_players) != self.obs_shape[0]:
+            raise ValueError("observation channels do not match n_players")
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise ValueError("HipLstmActorCritic runs on a ROCm device")
+        self.seed = int(seed)
+        self.tick = 0
+        self._lib = _capi.lib()
+        self._w = None
+        self.load_state_dict(state_dict if state_dict is not None
+                             else reference_init(obs_shape, seed=0, arch="lstm"))
+
+    def load_state_dict(self, state_dict: dict) -> None:
+        """Repack and copy over the packed block in place (ordered on the
+        current stream), so argument blocks built before stay valid."""
+        params = {k: v.detach().float().cpu().clone() for k, v in state_dict.items()}
+        packed = pack_lstm(params, self.obs_shape[0]).to(self.device)
+        if self._w is None:
+            self._w = packed
+        else:
+            self._w.copy_(packed)
+        self.params = params
+
+    def state_dict(self) -> dict:
+        return {k: v.clone() for k, v in self.params.items()}
+
+    def n_params(self) -> int:
+        return sum(v.numel() for v in self.params.values())
+
+    # ------------------------------------------------------------ launch
+    def _feat(self, obs):
+        local, rel, glob = obs
+        b = local.shape[0]
+        c = self.obs_shape[0]
+        if tuple(local.shape[1:]) != (c, 7, 7) or tuple(rel.shape[1:]) != (LSTM_MAX_T, 6) \
+                or tuple(glob.shape[1:]) != (LSTM_GLOB,) or rel.shape[0] != b or glob.shape[0] != b:
+            raise ValueError("features must be local (B,C,7,7), rel (B,10,6), glob (B,5)")
+        out = []
+        for t in (local, rel, glob):
+            t = t if t.dtype == torch.float16 else t.half()
+            t = t.reshape(b, -1)
+            if t.stride(1) != 1:
+                t = t.contiguous()
+            out.append(t)
+        return out
+
+    def args(self, local, rel, glob, h, c, rows_per_env=1, pid0=0, reset=None):
+        """Argument block over row-strided float16 feature planes and
+        float32 [B][128] state (masks, uniforms and outputs left NULL)."""
+        a = _capi.LstmArgsC()
+        a.batch = local.shape[0]
+        a.c_in = self.obs_shape[0]
+        a.rows_per_env = rows_per_env
+        a.pid0 = pid0
+        a.seed = self.seed & 0xFFFFFFFFFFFFFFFF
+        a.local, a.rel, a.glob = local.data_ptr(), rel.data_ptr(), glob.data_ptr()
+        a.local_stride, a.rel_stride, a.glob_stride = local.stride(0), rel.stride(0), glob.stride(0)
+        a.params = self._w.data_ptr()
+        a.h, a.c = h.data_ptr(), c.data_ptr()
+        a.reset = _capi.ptr(reset)
+        a.out_stride, a.out_slot = 1, 0
+        return a
+
+    def launch(self, a) -> None:
+        _capi.check(self._lib.qqt_lstm_act(a, _capi.stream_handle(self.device)))
+
+    def _state(self, hidden, b):
+        if hidden is None:
+            z = torch.zeros((b, LSTM_HIDDEN), dtype=torch.float32, device=self.device)
+            return z, z.clone()
+        h, c = hidden
+        h = h.reshape(b, LSTM_HIDDEN).to(self.device, torch.float32).clone()
+        c = c.reshape(b, LSTM_HIDDEN).to(self.device, torch.float32).clone()
+        return h, c
+
+    def _run(self, obs, hidden, pid, mm=None, bm=None, uniforms=None, tick=None):
+        local, rel, glob = self._feat(obs)
+        b = local.shape[0]
+        h, c = self._state(hidden, b)
+        a = self.args(local, rel, glob, h, c, 1, pid)
+        lg = torch.empty((b, 8), dtype=torch.float32, device=self.device)
+        a.logits_out = lg.data_ptr()
+        res = {}
+        if mm is not None:
+            mm = (mm if mm.dtype == torch.uint8 else mm.to(torch.uint8)).contiguous()
+            bm = (bm if bm.dtype == torch.uint8 else bm.to(torch.uint8)).contiguous()
+            res["actions"] = torch.empty((b, 2), dtype=torch.int64, device=self.device)
+            res["logp"] = torch.empty((b,), dtype=torch.float32, device=self.device)
+            a.sample = 1
+            a.move_mask, a.bomb_mask = mm.data_ptr(), bm.data_ptr()
+            a.mm_row_stride, a.bm_row_stride = mm.stride(0), bm.stride(0)
+            a.tick = (self.tick if tick is None else tick) & 0xFFFFFFFF
+            if uniforms is not None:
+                uniforms = uniforms.to(self.device, torch.float32).reshape(b, 2).contiguous()
+                a.uniforms = uniforms.data_ptr()
+            a.actions, a.logp_out = res["actions"].data_ptr(), res["logp"].data_ptr()
+        self.launch(a)
+        hid = (h.view(1, b, LSTM_HIDDEN), c.view(1, b, LSTM_HIDDEN))
+        return lg, hid, res
+
+    # ------------------------------------------------------------ API
+    def forward(self, obs, pid: int = 0, hidden=None):
+        lg, hid, _ = self._run(obs, hidden, pid)
+        return lg[:, :5], lg[:, 5:7], lg[:, 7], hid
+
+    __call__ = forward
+
+    def act(self, obs, move_mask, bomb_mask, pid: int = 0, hidden=None, uniforms=None):
+        """Sample one step (train/model.py:230-245, lstm branch)."""
+        lg, hid, res = self._run(obs, hidden, pid, move_mask, bomb_mask, uniforms)
+        if uniforms is None:
+            self.tick += 1
+        return res["actions"], res["logp"], lg[:, 7], hid
+
+    def evaluate(self, obs, move_mask, bomb_mask, actions, pid: int = 0, hidden=None):
+        """(logp, entropy, value) of given actions (train/model.py:247-256)."""
+        ml, bl, v, _ = self.forward(obs, pid, hidden)
+        neg = torch.finfo(torch.float32).min
+        lp, ent = 0.0, 0.0
+        for logits, mask, act in ((ml, move_mask, actions[..., 0]), (bl, bomb_mask, actions[..., 1])):
+            d = torch.distributions.Categorical(
+                logits=torch.where(mask.bool(), logits, torch.full_like(logits, neg)))
+            lp = lp + d.log_prob(act)
+            ent = ent + d.entropy()
+        return lp, ent, v

@@ -1,8 +1,11 @@
 """The reference's rollout buffer and advantage estimation on the device.
 
-`HipRolloutBuffer` mirrors `RolloutBuffer` (train/ppo.py:54-99) for the mlp
-and cnn archs (both store the shared observation): the same attribute names, shapes and dtypes (`obs`, `mmask`, `bmask`,
-`act`, `logp`, `val`, `rew`, `done`, `dmg`, `steps`, `ptr`, `add`, `reset`).
+`HipRolloutBuffer` mirrors `RolloutBuffer` (train/ppo.py:54-99): the same
+attribute names, shapes and dtypes (`obs`, `mmask`, `bmask`, `act`, `logp`,
+`val`, `rew`, `done`, `dmg`, `steps`, `ptr`, `add`, `reset`; for the lstm
+arch also `local` (T,N,C,7,7), `rel` (T,N,10,6), `glob` (T,N,5), the
+learner's per-player features, with `obs` an all-zero view that the lstm
+path never fills, as in the reference).
 Underneath, every per-step field is a slab in the layout the kernels write
 (`[T][N][P]` for per-player values, int8 actions, uint8 flags), so
 `Rollout.collect` fills a whole buffer with no per-step copies: the MLP
@@ -27,9 +30,8 @@ class HipRolloutBuffer:
 
     def __init__(self, steps: int, num_envs: int, obs_shape, device,
                  obs_dtype=torch.float16, arch: str = "mlp", n_players: int = 2) -> None:
-        if arch not in ("mlp", "cnn"):
-            raise ValueError("HipRolloutBuffer serves the mlp and cnn archs (the shared full-map "
-                             "observation); the lstm arch keeps per-player local features")
+        if arch not in ("mlp", "cnn", "lstm"):
+            raise ValueError(f"unknown arch {arch!r}")
         if obs_dtype != torch.float16:
             raise ValueError("the device rollout keeps float16 observations")
         c, h, w = obs_shape
@@ -38,7 +40,13 @@ class HipRolloutBuffer:
             raise ValueError("steps and num_envs must be positive")
         dev = torch.device(device)
         self.arch, self.steps, self.num_envs, self.n_players, self.ptr = arch, t, n, p, 0
-        self.obs = torch.zeros((t, n, c, h, w), dtype=torch.float16, device=dev)
+        if arch == "lstm":
+            self.obs = torch.zeros((), dtype=torch.float16, device=dev).expand(t, n, c, h, w)
+            self.local = torch.zeros((t, n, c, 7, 7), dtype=torch.float16, device=dev)
+            self.rel = torch.zeros((t, n, 10, 6), dtype=torch.float16, device=dev)
+            self.glob = torch.zeros((t, n, 5), dtype=torch.float16, device=dev)
+        else:
+            self.obs = torch.zeros((t, n, c, h, w), dtype=torch.float16, device=dev)
         self._mm = torch.zeros((t, n, p, 5), dtype=torch.uint8, device=dev)
         self._bm = torch.zeros((t, n, p, 2), dtype=torch.uint8, device=dev)
         self._act = torch.zeros((t, n, p, 2), dtype=torch.int8, device=dev)
@@ -83,16 +91,21 @@ class HipRolloutBuffer:
 
     @property
     def device(self) -> torch.device:
-        return self.obs.device
+        return self._rew.device
 
     def add(self, obs, mmask, bmask, act, logp, val, rew, done, dmg) -> None:
         """RolloutBuffer.add (train/ppo.py:84-95): one step of player-0 data
-        from host or device tensors, copied into slot `ptr`."""
+        from host or device tensors, copied into slot `ptr`; for the lstm arch
+        `obs` is the feature triple (local, rel, glob)."""
         i = self.ptr
         if i >= self.steps:
             raise IndexError("rollout buffer is full")
         d = self.device
-        self.obs[i] = obs.to(d)
+        if self.arch == "lstm":
+            local, rel, glob = obs
+            self.local[i], self.rel[i], self.glob[i] = local.to(d), rel.to(d), glob.to(d)
+        else:
+            self.obs[i] = obs.to(d)
         self._mm[i, :, 0] = mmask.to(d).to(torch.uint8)
         self._bm[i, :, 0] = bmask.to(d).to(torch.uint8)
         self._act[i, :, 0] = act.to(d).to(torch.int8)

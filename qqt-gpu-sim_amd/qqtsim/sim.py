@@ -296,6 +296,35 @@ class HipBatchedSim:
         self._refresh()
         return self._mm.view(torch.bool), self._bm.view(torch.bool)
 
+    def local_view_features(self, only_p0: bool = False, out=None):
+        """The lstm arch's per-player features of the current state
+        (sim/obs.py:243-340 local_view_features(cfg, obs, pos, alive, t,
+        fuse, hp, only_p0)) in one launch: (local (N,P',C,7,7), rel
+        (N,P',10,6), glob (N,P',5)) float16, P' = 1 when only_p0.  Bombs at
+        equal L1 distance, and the cells of the slots past the last bomb, are
+        taken in ascending cell index (the reference leaves that order to
+        torch.topk).  `out` = three tensors of those shapes to write into
+        (rows may be strided, e.g. one tick of a rollout buffer)."""
+        self._refresh()
+        n, p, c = self.num_envs, self.cfg.n_players, self.cfg.n_channels
+        po = 1 if only_p0 else p
+        shapes = ((n, po, c, 7, 7), (n, po, 10, 6), (n, po, 5))
+        if out is None:
+            out = tuple(torch.empty(s, dtype=torch.float16, device=self.device) for s in shapes)
+        for t, s in zip(out, shapes):
+            if tuple(t.shape) != s or t.dtype != torch.float16 or t.device != self.device \
+                    or not t[0].is_contiguous():
+                raise ValueError(f"feature output must be float16 {s} with contiguous rows")
+        a = _capi.LstmFeatArgsC()
+        a.n_envs, a.p_out = n, po
+        a.cells, a.players, a.envs = (self._cells.data_ptr(), self._players.data_ptr(),
+                                      self._envs.data_ptr())
+        a.obs = self._obs.data_ptr()
+        a.local, a.rel, a.glob = (t.data_ptr() for t in out)
+        a.local_stride, a.rel_stride, a.glob_stride = (t.stride(0) for t in out)
+        _capi.check(self._lib.qqt_lstm_features(self._cfg_c, a, _capi.stream_handle(self.device)))
+        return out
+
     def danger(self) -> torch.Tensor:
         """(N, H, W) float32 danger map of the current state, as the
         reference's `_danger_c()` / `blast.danger_map` gives it

@@ -102,3 +102,33 @@ def lstm_params(z):
     for k in LSTM_KEYS:
         out[k] = torch.from_numpy(z["w_" + k.replace(".", "_")])
     return out
+
+
+def _bits(a):
+    return np.asarray(a).view(np.uint16)
+
+
+def check_features(ref, got):
+    """local and glob bit for bit; rel: opponent slots bit for bit, bomb
+    slots' flags and L1 distances exact and their offsets equal as a set
+    within each distance (the reference's order among equal distances is
+    torch.topk's), empty slots' type entries 0."""
+    (L, R, G), (l, r, g) = ref, got
+    assert np.array_equal(_bits(l), _bits(L)), "local window"
+    assert np.array_equal(_bits(g), _bits(G)), "global scalars"
+    n_opp = 1
+    assert np.array_equal(_bits(r[:, :, :n_opp]), _bits(R[:, :, :n_opp])), "opponent slots"
+    assert np.array_equal(r[..., 3], R[..., 3]), "bomb flags"
+    assert not np.any(r[..., n_opp:, 2]) and not np.any(r[..., n_opp:, 4:]), "bomb slot types"
+    f32 = lambda x: np.asarray(x, dtype=np.float32)  # noqa: E731
+    d_ref = np.abs(f32(R[..., 0])) + np.abs(f32(R[..., 1]))
+    d_got = np.abs(f32(r[..., 0])) + np.abs(f32(r[..., 1]))
+    ok = R[..., 3] > 0
+    assert np.array_equal(d_ref[ok], d_got[ok]), "bomb distances"
+    for e, me in zip(*np.nonzero(ok.any(-1))):
+        m = ok[e, me]
+        for d in np.unique(d_ref[e, me][m]):
+            sel = m & (d_ref[e, me] == d)
+            a = sorted(map(tuple, f32(R[e, me][sel][:, :2])))
+            b = sorted(map(tuple, f32(r[e, me][sel][:, :2])))
+            assert a == b, f"bomb offsets at distance {d}"

@@ -42,7 +42,8 @@ def test_header_declares_the_entry_points():
     assert _declared_functions() == ["qqt_abi_version", "qqt_bot_act", "qqt_cnn_act", "qqt_gae",
                                      "qqt_l1_grad", "qqt_l1_grad_noalloc",
                                      "qqt_l1_grad_workspace_floats",
-                                     "qqt_last_error", "qqt_mlp_act", "qqt_ppo_grad", "qqt_tick",
+                                     "qqt_last_error", "qqt_lstm_act", "qqt_lstm_features",
+                                     "qqt_mlp_act", "qqt_ppo_grad", "qqt_tick",
                                      "qqt_timing_arm", "qqt_timing_collect"]
 
 
@@ -93,7 +94,8 @@ def test_struct_layouts_match_the_header(tmp_path):
     structs = {"qqt_sim_config": _capi.SimConfigC, "qqt_tick_args": _capi.TickArgsC,
                "qqt_mlp_args": _capi.MlpArgsC, "qqt_bot_args": _capi.BotArgsC,
                "qqt_gae_args": _capi.GaeArgsC, "qqt_l1_grad_args": _capi.L1GradArgsC,
-               "qqt_ppo_args": _capi.PpoArgsC, "qqt_cnn_args": _capi.CnnArgsC}
+               "qqt_ppo_args": _capi.PpoArgsC, "qqt_cnn_args": _capi.CnnArgsC,
+               "qqt_lstm_feat_args": _capi.LstmFeatArgsC, "qqt_lstm_args": _capi.LstmArgsC}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "qqt_hip.h"',
              'int main(void) {']
     for cname, cls in structs.items():
@@ -243,6 +245,70 @@ def _cnn_args(**kw):
 def test_cnn_rejects_bad_arguments(lib, kw, msg):
     assert lib.qqt_cnn_act(_cnn_args(**kw), None) == -1
     assert msg in lib.qqt_last_error().decode()
+
+
+def _lstm_args(**kw):
+    from qqtsim import _capi
+
+    a = _capi.LstmArgsC()
+    a.batch, a.c_in, a.rows_per_env = 4, 14, 1
+    a.local_stride, a.rel_stride, a.glob_stride = 14 * 49, 60, 5
+    a.out_stride = 1
+    for i, name in enumerate(("local", "rel", "glob", "params", "h", "c")):
+        setattr(a, name, 0x10000 * (i + 1))
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(params=None), "null pointer"),
+    (dict(h=None), "null pointer"),
+    (dict(batch=0), "bad shape"),
+    (dict(c_in=15), "bad shape"),
+    (dict(local_stride=14 * 49 - 1), "bad shape"),
+    (dict(rel_stride=59), "bad shape"),
+    (dict(rows_per_env=0), "bad shape"),
+    (dict(out_slot=1), "bad shape"),
+    (dict(sample=1), "sampling needs masks"),
+])
+def test_lstm_rejects_bad_arguments(lib, kw, msg):
+    assert lib.qqt_lstm_act(_lstm_args(**kw), None) == -1
+    assert msg in lib.qqt_last_error().decode()
+
+
+def _lstm_feat_args(**kw):
+    from qqtsim import _capi
+
+    a = _capi.LstmFeatArgsC()
+    a.n_envs, a.p_out = 4, 2
+    a.local_stride, a.rel_stride, a.glob_stride = 2 * 14 * 49, 120, 10
+    for i, name in enumerate(("cells", "players", "envs", "obs", "local", "rel", "glob")):
+        setattr(a, name, 0x10000 * (i + 1))
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("cfg_kw,kw,msg", [
+    ({}, dict(obs=None), "null pointer"),
+    ({}, dict(n_envs=0), "bad sizes"),
+    ({}, dict(p_out=3), "bad sizes"),
+    (dict(max_hp=0), {}, "bad sizes"),
+    ({}, dict(rel_stride=119), "strides"),
+    ({}, dict(local_stride=2 * 14 * 49 - 1), "strides"),
+    (dict(height=11, width=11), {}, "not compiled"),
+])
+def test_lstm_features_reject_bad_arguments(lib, cfg_kw, kw, msg):
+    assert lib.qqt_lstm_features(_cfg(**cfg_kw), _lstm_feat_args(**kw), None) < 0
+    assert msg in lib.qqt_last_error().decode()
+
+
+def test_lstm_block_size_matches_the_header():
+    from qqtsim import policy
+
+    m = re.search(r"#define QQT_LSTM_PARAMS (\d+)", open(HEADER).read())
+    assert int(m.group(1)) == policy.LSTM_PARAMS == sum(r * c for _, r, c in policy._LSTM_BLOCKS)
 
 
 def _bot_args(**kw):

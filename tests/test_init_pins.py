@@ -1,11 +1,12 @@
 """`qqtsim.policy.reference_init` against the weights the reference's own
 `ActorCritic` holds after `torch.manual_seed(0)` (train/model.py:154-165),
-as `tests/golden/gen_reference_vectors.py` wrote them into `mlp.npz` and
-`cnn.npz`.
+as `tests/golden/gen_reference_vectors.py` wrote them into `mlp.npz`,
+`cnn.npz` and `lstm.npz`.
 
 The generator perturbed every bias, the LayerNorm affines and (cnn) every
 `conv.*` parameter by `0.1 * randn` from `Generator().manual_seed(1)`,
-drawn in `named_parameters()` order, before saving.  The unperturbed
+drawn in `named_parameters()` order, before saving (lstm: only the biases,
+from `Generator().manual_seed(2)`).  The unperturbed
 parameters (the Linear / conv0 weights: orthogonal draws) are compared bit
 for bit; the perturbed ones must equal the init plus the replayed
 perturbation, which pins zero biases and LayerNorm 1 / 0.  Planted
@@ -26,6 +27,8 @@ GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 
 
 def _perturbed(name: str, arch: str) -> bool:
+    if arch == "lstm":
+        return "bias" in name
     return (name.endswith("bias") or ".1." in name or ".4." in name
             or (arch == "cnn" and name.startswith("conv.")))
 
@@ -39,7 +42,7 @@ def _mismatches(sd: dict, arch: str) -> list[str]:
     """Names of parameters where `sd` (as the reference init) and the golden
     weights disagree once the generator's perturbation is replayed."""
     gold = _golden(arch)
-    g = torch.Generator().manual_seed(1)
+    g = torch.Generator().manual_seed(2 if arch == "lstm" else 1)
     bad = []
     names = [n for n, _ in _layer_tree(arch, (14, 13, 13), 5, 2).named_parameters()]
     for name in names:
@@ -53,14 +56,16 @@ def _mismatches(sd: dict, arch: str) -> list[str]:
     return bad
 
 
-@pytest.mark.parametrize("arch", ["mlp", "cnn"])
+@pytest.mark.parametrize("arch", ["mlp", "cnn", "lstm"])
 def test_reference_init_equals_reference_weights(arch):
+    """lstm: the torch.nn.LSTM's own uniform init, drawn when the layer is
+    built between l_fusion and the heads, is part of what is pinned."""
     sd = reference_init(seed=0, arch=arch)
     gold = _golden(arch)
     assert set(k.replace(".", "_") for k in sd) == set(gold), "state_dict keys differ"
     assert _mismatches(sd, arch) == []
     n = sum(v.numel() for v in sd.values())
-    assert n == (345_288 if arch == "mlp" else 281_744)
+    assert n == {"mlp": 345_288, "cnn": 281_744, "lstm": 368_816}[arch]
 
 
 def test_reference_init_structure():

@@ -1,0 +1,143 @@
+"""The packed parameter block of the lstm kernel (qqtsim.policy.pack_lstm),
+read the way qqt-gpu-sim_amd/csrc/lstm.hip reads it, on the CPU.
+
+`_emulate` restates the kernel's indexing in float64 numpy: the 7x7 windows
+in zero-bordered 9x9 grids with the tap map k -> (k / 9) * 81 + (k % 9 / 3) *
+9 + k % 3, conv1's output written back into a bordered grid, the 2x2 pool
+over 7x7 planes, the k-major blocks with their padding, the stacked LSTM
+block and the block-diagonal output layer.  Run over the reference's frames
+(tests/golden/lstm.npz, train/model.py:176-185 with the hidden state carried
+and reset) it must reproduce the reference's logits, values and (h, c);
+packings with a planted mistake (a transposed 3x3 kernel, the gates of W_hh
+in another order, the move and bomb output columns swapped) must not.
+"""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from golden_io import lstm_params
+from qqtsim.policy import LSTM_PARAMS, lstm_block_offsets, pack_lstm
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+_SHAPES = {"c1w": (128, 32), "c1b": (1, 64), "c2w": (288, 64), "c2b": (1, 64),
+           "fcw": (576, 128), "fcb": (1, 128), "r1w": (64, 64), "r1b": (1, 64),
+           "r2w": (64, 32), "r2b": (1, 64), "g1w": (8, 16), "g1b": (1, 64),
+           "g2w": (16, 16), "g2b": (1, 64), "fuw": (168, 256), "fub": (1, 256),
+           "lw": (384, 512), "lb": (1, 512), "hw": (128, 192), "hb": (1, 192),
+           "ow": (192, 16), "ob": (1, 64)}
+
+
+@pytest.fixture(scope="module")
+def z():
+    return np.load(os.path.join(HERE, "golden", "lstm.npz"))
+
+
+def _tap(k):
+    return (k // 9) * 81 + ((k % 9) // 3) * 9 + k % 3
+
+
+def _poff(p):
+    return (p // 7) * 9 + p % 7
+
+
+def _sig(x):
+    return 1.0 / (1.0 + np.exp(-x))
+
+
+def _emulate(block, local, rel, glob, h, c):
+    P = block.double().numpy()
+    off = lstm_block_offsets()
+
+    def W(k):
+        r, cc = _SHAPES[k]
+        m = P[off[k]:off[k] + r * cc].reshape(r, cc)
+        return m[0] if r == 1 else m
+
+    relu = lambda x: np.maximum(x, 0.0)  # noqa: E731
+    b, ch = local.shape[0], local.shape[1]
+    k1 = np.arange(128)
+    pos = np.arange(49)
+    grid = np.zeros((b, 14 * 81))
+    for ci in range(ch):
+        for p in pos:
+            grid[:, ci * 81 + (p // 7 + 1) * 9 + p % 7 + 1] = local[:, ci, p // 7, p % 7]
+    idx1 = _poff(pos)[:, None] + _tap(k1)[None, :]
+    a = np.where(k1[None, None, :] < 9 * ch, grid[:, np.minimum(idx1, 14 * 81 - 1)], 0.0)
+    a1 = relu(a @ W("c1w") + W("c1b")[:32])                       # (B, 49, 32)
+    grid2 = np.zeros((b, 32 * 81))
+    for co in range(32):
+        grid2[:, co * 81 + (pos // 7 + 1) * 9 + pos % 7 + 1] = a1[:, :, co]
+    idx2 = _poff(pos)[:, None] + _tap(np.arange(288))[None, :]
+    a2 = relu(grid2[:, idx2] @ W("c2w") + W("c2b")).transpose(0, 2, 1)   # (B, 64, 49)
+    pooled = np.zeros((b, 576))
+    for i in range(576):
+        cc, y, x = i // 9, (i % 9) // 3, i % 3
+        q = 2 * y * 7 + 2 * x
+        pooled[:, i] = np.max(a2[:, cc, [q, q + 1, q + 7, q + 8]], axis=1)
+    fc = relu(pooled @ W("fcw") + W("fcb"))
+    rin = np.zeros((b, 64))
+    rin[:, :60] = rel.reshape(b, 60)
+    r2 = relu(relu(rin @ W("r1w") + W("r1b")) @ W("r2w") + W("r2b")[:32])
+    gin = np.zeros((b, 8))
+    gin[:, :5] = glob
+    g2 = relu(relu(gin @ W("g1w") + W("g1b")[:16]) @ W("g2w") + W("g2b")[:16])[:, :8]
+    fu = relu(np.concatenate([fc, r2, g2], 1) @ W("fuw") + W("fub"))
+    g = np.concatenate([fu, h], 1) @ W("lw") + W("lb")
+    gi, gf, gg, go = (g[:, 128 * j:128 * (j + 1)] for j in range(4))
+    c2 = _sig(gf) * c + _sig(gi) * np.tanh(gg)
+    h2 = _sig(go) * np.tanh(c2)
+    lg = relu(h2 @ W("hw") + W("hb")) @ W("ow") + W("ob")[:16]
+    return lg, h2, c2
+
+
+def _worst(z, block):
+    n = z["local0"].shape[1]
+    h = np.zeros((n, 128))
+    c = np.zeros((n, 128))
+    worst = 0.0
+    for i in range(z["local0"].shape[0]):
+        f = [z[k][i][:, 0].astype(np.float64) for k in ("local0", "rel0", "glob0")]
+        lg, h, c = _emulate(block, *f, h, c)
+        assert np.all(lg[:, 8:] == 0.0)
+        for got, key in ((lg[:, :5], "move_logits"), (lg[:, 5:7], "bomb_logits"),
+                         (lg[:, 7], "value"), (h, "h"), (c, "c")):
+            worst = max(worst, float(np.abs(got - z[key][i]).max()))
+        keep = ~z["reset"][i]
+        h, c = h * keep[:, None], c * keep[:, None]
+    return worst
+
+
+def test_packed_block_reproduces_the_reference_sequence(z):
+    params = lstm_params(z)
+    block = pack_lstm(params)
+    assert block.shape == (LSTM_PARAMS,) and block.dtype == torch.float32
+    assert _worst(z, block) <= 1e-5
+
+
+@pytest.mark.parametrize("kind", ["conv_kernel_transposed", "hh_gates_rolled", "heads_swapped"])
+def test_planted_packing_mistakes_fail(z, kind):
+    params = {k: v.clone() for k, v in lstm_params(z).items()}
+    if kind == "conv_kernel_transposed":
+        params["l_conv2.weight"] = params["l_conv2.weight"].transpose(2, 3).contiguous()
+    elif kind == "hh_gates_rolled":
+        params["lstm.weight_hh_l0"] = params["lstm.weight_hh_l0"].roll(128, 0)
+    else:
+        m, bo = params["move_head.2.weight"], params["bomb_head.2.weight"]
+        params["move_head.2.weight"] = torch.cat([bo, m[2:]])
+        params["bomb_head.2.weight"] = m[:2].clone()
+    assert _worst(z, pack_lstm(params)) > 1e-3
+
+
+def test_pack_rejects_wrong_shapes(z):
+    params = lstm_params(z)
+    bad = dict(params)
+    bad["l_rel_fc1.weight"] = torch.zeros(64, 54)
+    with pytest.raises(ValueError, match="l_rel_fc1.weight"):
+        pack_lstm(bad)
+    with pytest.raises(ValueError, match="14"):
+        pack_lstm(params, obs_channels=15)
