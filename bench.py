@@ -80,7 +80,7 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="CPU work budget of the cpu_baseline sample (0 = skip)")
     ap.add_argument("--workload", choices=("rollout", "stress", "astar", "evalfwd", "collect",
-                                           "ppo", "train", "cnn"),
+                                           "ppo", "train", "cnn", "lstm"),
                     default="rollout",
                     help="rollout: the headline self-play rollout (default); stress: "
                          "16384-env bomb-stress ticks with injected actions; astar: "
@@ -92,7 +92,8 @@ def parse_args():
                          "(4 epochs x 4 minibatches) over a 5632 x 128 collected buffer; "
                          "train: whole training iterations (collect 128 steps + PPO update "
                          "+ weight sync to the acting network); cnn: the self-play rollout "
-                         "with the reference's cnn actor/critic, 5632 envs")
+                         "with the reference's cnn actor/critic, 5632 envs; lstm: the lstm "
+                         "learner (local features + LSTM) vs the astar bot, 5632 envs")
     ap.add_argument("--copy-calibrate", action="store_true",
                     help="after timing, run a 512 MiB device copy (HBM counter calibration)")
     return ap.parse_args()
@@ -287,6 +288,8 @@ def main():
         return main_ppo(args, torch, dev)
     if args.workload == "train":
         return main_train(args, torch, dev)
+    if args.workload == "lstm":
+        return main_lstm(args, torch, dev)
     if args.workload == "cnn":
         return main_cnn(args, torch, dev)
     n, K, W = args.envs, args.steps, args.warmup
@@ -1224,6 +1227,226 @@ def main_cnn(args, torch, dev):
     }
     print(json.dumps(out), flush=True)
 
+
+
+# Multiply-accumulates of one row (one player) of the lstm network
+# (train/model.py:103-120): conv 3x3 14->32 and 32->64 over 49 positions,
+# Linear 576->128, rel 60->64->32, glob 5->16->8, fusion 168->256, the LSTM
+# gates (256 + 128 inputs, 512 outputs), the heads 128->3x64 and 3x64->8.
+LSTM_MACS = (49 * 126 * 32 + 49 * 288 * 64 + 576 * 128 + 60 * 64 + 64 * 32 + 5 * 16 + 16 * 8
+             + 168 * 256 + 384 * 512 + 128 * 192 + 64 * 8)
+LSTM_FLOP_PER_ROW = 2 * LSTM_MACS
+MFMA_F32_PEAK = 157.3
+# Algorithmic bytes of the feature kernel per env (one player): the packed
+# cells (169 x 4 B), the player rows (2 x 48 B), t (4 B), the 14 x 7 x 7
+# float16 window read and written, rel (120 B) and glob (10 B) written.
+LSTM_FEAT_BYTES_PER_ENV = 169 * 4 + 2 * 48 + 4 + 2 * 14 * 49 * 2 + 120 + 10
+
+
+def _torch_lstm(torch, sd, dev):
+    """The reference's lstm ActorCritic (train/model.py:103-120, 176-185,
+    198-214, 230-245) as plain float32 eager torch modules: extract_fused,
+    nn.LSTM over one step, the heads and masked Categorical sampling."""
+    nn = torch.nn
+
+    class Lstm(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.l_conv1 = nn.Conv2d(14, 32, 3, padding=1)
+            self.l_conv2 = nn.Conv2d(32, 64, 3, padding=1)
+            self.l_pool = nn.MaxPool2d(2)
+            self.l_cnn_fc = nn.Linear(576, 128)
+            self.l_rel_fc1 = nn.Linear(60, 64)
+            self.l_rel_fc2 = nn.Linear(64, 32)
+            self.l_glob_fc1 = nn.Linear(5, 16)
+            self.l_glob_fc2 = nn.Linear(16, 8)
+            self.l_fusion = nn.Linear(168, 256)
+            self.lstm = nn.LSTM(256, 128, 1, batch_first=True)
+            self.move_head = nn.Sequential(nn.Linear(128, 64), nn.ReLU(), nn.Linear(64, 5))
+            self.bomb_head = nn.Sequential(nn.Linear(128, 64), nn.ReLU(), nn.Linear(64, 2))
+            self.critic = nn.Sequential(nn.Linear(128, 64), nn.ReLU(), nn.Linear(64, 1))
+
+        def forward(self, local, rel, glob, hidden):
+            r = torch.relu
+            x = r(self.l_conv1(local.float()))
+            x = self.l_pool(r(self.l_conv2(x)))
+            x = r(self.l_cnn_fc(x.view(x.size(0), -1)))
+            e = r(self.l_rel_fc2(r(self.l_rel_fc1(rel.float().view(rel.size(0), -1)))))
+            g = r(self.l_glob_fc2(r(self.l_glob_fc1(glob.float()))))
+            f = r(self.l_fusion(torch.cat([x, e, g], 1)))
+            lo, nh = self.lstm(f.unsqueeze(1), hidden)
+            lo = lo.squeeze(1)
+            return self.move_head(lo), self.bomb_head(lo), self.critic(lo).squeeze(-1), nh
+
+        @torch.no_grad()
+        def act(self, local, rel, glob, mm, bm, hidden):
+            ml, bl, v, nh = self(local, rel, glob, hidden)
+            neg = torch.finfo(ml.dtype).min
+            dm = torch.distributions.Categorical(logits=torch.where(mm, ml, torch.full_like(ml, neg)))
+            db = torch.distributions.Categorical(logits=torch.where(bm, bl, torch.full_like(bl, neg)))
+            a = torch.stack([dm.sample(), db.sample()], -1)
+            return a, dm.log_prob(a[:, 0]) + db.log_prob(a[:, 1]), v, nh
+
+    m = Lstm()
+    m.load_state_dict(sd)
+    return m.to(dev)
+
+
+def cpu_baseline_lstm(cfg, spec, n, seed, budget_s):
+    """The oracle's lstm learner-vs-astar env-step on the host cores:
+    local_view_features (only_p0), the lstm forward with the state carried
+    and zeroed on done, masked sampling, the astar bot, step."""
+    import numpy as np
+    import torch
+
+    from oracle import philox
+    from oracle.bots import astar_act
+    from oracle.obs import local_view_features
+    from oracle.policy import lstm_forward, sample_masked
+    from oracle.sim import OracleSim
+    from qqtsim.policy import reference_init
+
+    cores = _cores(torch)
+    params = reference_init(cfg.obs_shape, arch="lstm")
+    sim = OracleSim(cfg, n, spec, seed=seed)
+    envs = np.arange(n)
+    state = {"hidden": None}
+
+    def env_step(t):
+        obs = sim.observe()
+        mm, bm = sim.legal_mask()
+        s = sim.state_dict()
+        loc, rel, glb = local_view_features(cfg, obs, s["pos"], s["alive"], s["t"], s["fuse"],
+                                            s["hp"], only_p0=True)
+        ml, bl, _, hid = lstm_forward(params, loc[:, 0], rel[:, 0], glb[:, 0], state["hidden"])
+        u = philox.uniforms(seed, envs, t, philox.STREAM_POLICY, 2)
+        ub = torch.from_numpy(philox.uniforms(seed, envs, t, philox.STREAM_BOT, 5))
+        acts = torch.zeros((n, 2, 2), dtype=torch.int64)
+        acts[:, 0, 0] = torch.from_numpy(sample_masked(ml.numpy(), mm[:, 0].numpy(), u[:, 0])[0])
+        acts[:, 0, 1] = torch.from_numpy(sample_masked(bl.numpy(), bm[:, 0].numpy(), u[:, 1])[0])
+        acts[:, 1] = astar_act(cfg, s, obs, mm[:, 1], bm[:, 1], 1, ub)
+        _, done, _ = sim.step(acts, auto_reset=True)
+        keep = (~done.bool()).float().view(-1, 1)
+        state["hidden"] = (hid[0] * keep, hid[1] * keep)
+
+    env_step(0)
+    ticks, t0 = 0, time.perf_counter()
+    while True:
+        env_step(1 + ticks)
+        ticks += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or ticks >= 128:
+            break
+    return {"value": n * ticks / el, "unit": "env-steps/s", "cores": cores, "kind": "port",
+            "cpu_model": _cpu_model(),
+            "sample": f"oracle (torch CPU restatement) lstm-learner-vs-astar env-step, {n} envs x "
+                      f"{ticks} timed ticks after 1 warm-up tick, {el:.1f} s"}
+
+
+def main_lstm(args, torch, dev):
+    """The lstm arch's collect loop: player 0 = the lstm network (local
+    features, LSTM state carried and zeroed on done, masked sampling),
+    player 1 = the astar bot; tick with auto-reset.  Four launches per step
+    plus the bot's reach reduction.  `torch_gpu_baseline` times the
+    reference's act() for player 0 with the same network as float32 eager
+    torch modules (MIOpen convolutions, MIOpen LSTM) on the same GPU and
+    features."""
+    from qqtsim.bots import HipAstarBot
+    from qqtsim.config import corridor_training_config
+    from qqtsim.maps import MapSpec
+    from qqtsim.policy import HipLstmActorCritic, reference_init
+    from qqtsim.rollout import LstmRollout
+    from qqtsim.sim import HipBatchedSim
+
+    n, K, W = args.envs, args.steps, args.warmup
+    cfg = corridor_training_config()
+    spec = MapSpec(kind="pillars", brick_p=0.7, swap_spawns=True)
+    sim = HipBatchedSim(cfg, n, device=dev, seed=args.seed, map_spec=spec)
+    sd = reference_init(cfg.obs_shape, seed=args.seed, arch="lstm")
+    net = HipLstmActorCritic(sd, device=dev, seed=args.seed)
+    roll = LstmRollout(sim, net, HipAstarBot(sim, pid=1))
+    for _ in range(W):
+        roll.step()
+    torch.cuda.synchronize()
+    _capi.timing_arm(0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(K):
+        if k % EVERY == 0:
+            _capi.timing_arm(5)          # features, act, bot reach, bot, tick
+        roll.step()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    kms = kernel_ms()
+    us = {k: v * 1e3 for k, v in kms.items()}
+    bot_us = us["bot_kernel"] + us.get("reach_kernel", 0.0)
+    kernels = {
+        "lstm_act_kernel": {"us": us["lstm_act_kernel"], "bound": "mfma",
+                            "achieved": LSTM_FLOP_PER_ROW * n / (us["lstm_act_kernel"] * 1e-6)
+                            / 1e12,
+                            "peak": MFMA_F32_PEAK, "unit": "TFLOP/s",
+                            "flop_per_row": LSTM_FLOP_PER_ROW},
+        "lstm_feat_kernel": {"us": us["lstm_feat_kernel"], "bound": "hbm",
+                             "achieved": LSTM_FEAT_BYTES_PER_ENV * n
+                             / (us["lstm_feat_kernel"] * 1e-6) / 1e9,
+                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "bytes_per_env": LSTM_FEAT_BYTES_PER_ENV},
+        "bot_kernel": {"us": bot_us, "bound": "hbm",
+                       "achieved": BOT_BYTES_PER_ENV * n / (bot_us * 1e-6) / 1e9,
+                       "peak": HBM_PEAK_GBS, "unit": "GB/s", "bytes_per_env": BOT_BYTES_PER_ENV},
+        "tick_kernel": {"us": us["tick_kernel"], "bound": "hbm",
+                        "achieved": TICK_BYTES_PER_ENV * n / (us["tick_kernel"] * 1e-6) / 1e9,
+                        "peak": HBM_PEAK_GBS, "unit": "GB/s", "bytes_per_env": TICK_BYTES_PER_ENV},
+    }
+    for v in kernels.values():
+        v["frac"] = v["achieved"] / v["peak"]
+    d = kernels["lstm_act_kernel"]
+
+    # the reference's act() for player 0, eager float32 torch on this GPU
+    ref = _torch_lstm(torch, sd, dev)
+    loc, rel, glb = (x[:, 0].clone() for x in sim.local_view_features(only_p0=True))
+    mm, bm = (m[:, 0].bool().clone() for m in sim.legal_mask())
+    hid = (roll.h[None].clone(), roll.c[None].clone())
+    for _ in range(3):
+        ref.act(loc, rel, glb, mm, bm, hid)
+    torch.cuda.synchronize()
+    reps = 10
+    t1 = time.perf_counter()
+    for _ in range(reps):
+        ref.act(loc, rel, glb, mm, bm, hid)
+    torch.cuda.synchronize()
+    ref_ms = (time.perf_counter() - t1) / reps * 1e3
+    hip_ms = us["lstm_act_kernel"] * 1e-3
+
+    cpu = cpu_baseline_lstm(cfg, spec, 256, args.seed, args.cpu_seconds) \
+        if args.cpu_seconds > 0 else None
+    out = {
+        "metric": "env-steps/s at 5632 envs, lstm learner vs astar bot "
+                  "(step+obs+features+lstm act+bot), 1 MI355X",
+        "value": n * K / el, "unit": "env-steps/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": el / K * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32 sim, bot and network (f32 MFMA), f16 features",
+        "data": "synthetic: template maps from Philox draws, the reference's lstm init "
+                "(orthogonal, torch.nn.LSTM uniform)",
+        "config": {"workload": "lstm learner (player 0: 7x7 local features + LSTM, state "
+                               "carried) vs astar bot (player 1), 5632 envs, 13x13 pillars "
+                               "+ 70% bricks, auto-reset",
+                   "envs": n, "parallelism": "single GPU"},
+        "roofline": {"kernel": "lstm_act_kernel", "bound": d["bound"],
+                     "achieved": round(d["achieved"], 3), "peak": d["peak"], "unit": d["unit"],
+                     "frac": round(d["frac"], 5), "traffic": None,
+                     "note": "algorithmic FLOP over the dense float32 MFMA peak"},
+        "torch_gpu_baseline": {"act_ms_player0": round(ref_ms, 3),
+                               "hip_act_ms_player0": round(hip_ms, 4),
+                               "speedup": round(ref_ms / hip_ms, 2),
+                               "note": "the reference's act() (extract_fused, nn.LSTM step, "
+                                       "heads, masked Categorical sampling), float32 eager "
+                                       "torch, same features and state"},
+        "cpu_baseline": cpu,
+        "kernels": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
+                        for kk, vv in v.items()} for k, v in kernels.items()},
+    }
+    print(json.dumps(out), flush=True)
 
 if __name__ == "__main__":
     main()

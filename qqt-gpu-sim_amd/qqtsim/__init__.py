@@ -11,7 +11,7 @@ load the library; the first sim or policy does, and raises if it is missing.
 """
 
 from .bots import HipAstarBot
-from .learn import HipMlpActorCritic, PPOConfig, ppo_update
+from .learn import HipMlpActorCritic, LstmLearner, PPOConfig, ppo_update
 from .config import SimConfig, corridor_training_config
 from .factory import make_sim
 from .maps import BOMB_STRESS_40, CORRIDOR_70, OPEN_PILLARS, MapSpec
@@ -25,4 +25,4 @@ __all__ = ["HipAstarBot", "SimConfig", "corridor_training_config", "make_sim", "
            "OPEN_PILLARS", "CORRIDOR_70", "BOMB_STRESS_40", "HipActorCritic", "HipCnnActorCritic",
            "HipLstmActorCritic", "default_init", "default_init_cnn", "reference_init", "Rollout",
            "LstmRollout", "HipBatchedSim", "HipRolloutBuffer", "compute_gae",
-           "HipMlpActorCritic", "PPOConfig", "ppo_update"]
+           "HipMlpActorCritic", "LstmLearner", "PPOConfig", "ppo_update"]

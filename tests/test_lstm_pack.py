@@ -9,7 +9,9 @@ block and the block-diagonal output layer.  Run over the reference's frames
 (tests/golden/lstm.npz, train/model.py:176-185 with the hidden state carried
 and reset) it must reproduce the reference's logits, values and (h, c);
 packings with a planted mistake (a transposed 3x3 kernel, the gates of W_hh
-in another order, the move and bomb output columns swapped) must not.
+in another order, the move and bomb output columns swapped) must not.  The
+trainable `LstmLearner` (the lstm PPO update's module) is pinned to the same
+frames.
 """
 
 from __future__ import annotations
@@ -141,3 +143,28 @@ def test_pack_rejects_wrong_shapes(z):
         pack_lstm(bad)
     with pytest.raises(ValueError, match="14"):
         pack_lstm(params, obs_channels=15)
+
+
+def test_lstm_learner_matches_the_reference_sequence(z):
+    """The trainable LstmLearner (torch ops, CPU here) over the reference's
+    frames: logits, values and state, and evaluate()'s log-probabilities and
+    entropies of the recorded actions (the masked-logit distribution)."""
+    from qqtsim.learn import LstmLearner
+
+    net = LstmLearner(state_dict=lstm_params(z))
+    assert net.n_params() == int(z["param_count"])
+    hidden, worst = None, 0.0
+    with torch.no_grad():
+        for i in range(z["local0"].shape[0]):
+            f = tuple(torch.from_numpy(z[k][i][:, 0]) for k in ("local0", "rel0", "glob0"))
+            mm = torch.from_numpy(z["mm"][i][:, 0])
+            bm = torch.from_numpy(z["bm"][i][:, 0])
+            lp, ent, _ = net.evaluate(f, mm, bm, torch.from_numpy(z["actions"][i]), 0, hidden)
+            ml, bl, v, hidden = net(f, 0, hidden)
+            for got, key in ((ml, "move_logits"), (bl, "bomb_logits"), (v, "value"),
+                             (hidden[0][0], "h"), (hidden[1][0], "c"), (lp, "logp"),
+                             (ent, "entropy")):
+                worst = max(worst, float(np.abs(got.numpy() - z[key][i]).max()))
+            keep = (~torch.from_numpy(z["reset"][i])).float().view(1, -1, 1)
+            hidden = (hidden[0] * keep, hidden[1] * keep)
+    assert worst <= 1e-5
