@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 14
+#define QQT_ABI_VERSION 15
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -459,7 +459,7 @@ typedef struct qqt_lstm_args {
   float* value_out;           /* [slot] or NULL */
   float* logits_out;          /* [B][8]: 5 move, 2 bomb, value; or NULL */
 } qqt_lstm_args;
-#define QQT_LSTM_PARAMS 371584
+#define QQT_LSTM_PARAMS 374272
 int qqt_lstm_act(const qqt_lstm_args* args, void* stream);
 
 /* Dispatch timing for benchmark harnesses (no counterpart in the reference:

@@ -13,20 +13,24 @@
 // of four wavefronts per 16 rows, float32 arithmetic throughout on
 // v_mfma_f32_16x16x4_f32 (A: 16 rows x 4 K, B: 4 K x 16 columns; lane l
 // supplies A[l%16][l/16] and B[l/16][l%16] and holds D[4(l/16)+j][l%16]).
-// * Trunk, one row at a time: the 14 x 7 x 7 window sits in LDS as a zero-
-//   bordered 9 x 9 grid per channel; each 3x3 convolution is an implicit GEMM
-//   (M = the 49 positions in four tiles, one per wavefront; N = output
-//   channels; K = channel x tap) whose A operand is gathered from the grid and
-//   whose B operand (the weights, k-major) is staged in LDS for the whole
-//   launch.  conv1's output goes to a second zero-bordered grid, conv2's to a
-//   7 x 7 plane per channel, and the 2x2 max pool writes the row's 576
-//   features into a 16-row tile.
-// * Head, the 16 rows together (M = 16): Linear(576,128), the rel and glob
+// * Trunk, four rows at a time: the windows sit in LDS as zero-bordered 9 x 9
+//   grids per channel; each 3x3 convolution is an implicit GEMM with K
+//   ordered tap-major (k = tap * channels + channel), so a K step's A operand
+//   is one LDS read at a per-lane base plus an immediate offset.  Each
+//   wavefront holds its output-column tile of both weight matrices in
+//   registers for the whole launch.  conv1 runs over the 4 x 49 positions
+//   and writes a second bordered grid; conv2 runs only at the 36 positions
+//   per row that the 2x2 max pool reads (7 -> 3 drops row and column 6),
+//   ordered so that each output lane's four values are one pooling window:
+//   the pool is a max over the lane's accumulators.
+// * Head, 16 rows together (M = 16): Linear(576,128), the rel and glob
 //   MLPs, the fusion layer, the LSTM gates (K = 256 inputs + 128 hidden, N =
-//   512, gate order i, f, g, o as torch.nn.LSTM stores them), the cell update,
-//   the three heads and the block-diagonal output layer, all from k-major
-//   weight blocks read from L2 (each weight once per 16 rows), activations in
-//   LDS; then masked sampling, one thread per row.
+//   512, gate order i, f, g, o as torch.nn.LSTM stores them; each wavefront
+//   takes the same 32 hidden units of all four gates, so the cell update
+//   happens in registers), the three heads and the block-diagonal output
+//   layer, from k-major weight blocks read from L2 (each weight once per 16
+//   rows), activations in LDS with row strides of 4 mod 64 floats (bank
+//   conflict free A reads); then masked sampling, one thread per row.
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -45,23 +49,38 @@ namespace lstm {
 constexpr int MAX_T = 10, GLOB = 5, K7 = 7, HALF = 3;
 constexpr int HID = 128, HEAD = 64;
 constexpr int C_MAX = 14;                 // observation channels the packing allows
-constexpr int K1 = 128;                   // conv1 K (9 C_MAX = 126, padded)
-constexpr int K2 = 288;                   // conv2 K (9 x 32)
+constexpr int CS1 = 16;                   // channel slots per conv1 tap (C_MAX used)
+constexpr int K1 = 9 * CS1;               // conv1 K: tap-major, k = tap * 16 + channel
+constexpr int K2 = 9 * 32;                // conv2 K: tap-major, k = tap * 32 + channel
 constexpr int FEAT = 576;                 // 64 x 3 x 3 pooled features
 constexpr int XIN = 168;                  // 128 + 32 + 8 fusion inputs
-constexpr int XH = 384;                   // 256 fused + 128 hidden: LSTM inputs
+constexpr int XINP = 176;                 // padded to whole 16-k groups
 constexpr int G4 = 512;                   // 4 x 128 gates
-constexpr int ROWS = 16;                  // rows per workgroup
-constexpr int NTHR = 256;
+constexpr int NW = 8;                     // wavefronts per workgroup (two per SIMD)
+constexpr int NTHR = 64 * NW;
+constexpr int RG = 4;                     // rows per trunk group
+constexpr int M1T = (RG * 49 + 15) / 16;  // conv1 position tiles per group (13)
+constexpr int T1 = (M1T + 3) / 4;         // conv1 tiles per wavefront (four per column tile)
+constexpr int M2T = RG * 36 / 16;         // conv2 pooled-position tiles per group (9)
+constexpr int T2 = (M2T + 1) / 2;         // conv2 tiles per wavefront (two per column tile)
+static_assert(RG * 36 % 16 == 0, "whole conv2 tiles per group");
+// LDS row strides of the 16-row activation blocks: 4 mod 64 floats, so the
+// 16 rows x 4 k of one A-operand read land in 64 distinct banks
+constexpr int LD_POOL = 580, LD_XIN = 196, LD_XH = 388, LD_HN = 132, LD_HD = 196, LD_R = 68,
+              LD_G1 = 20, LD_GLB = 20, LD_LG = 16;
 
-// packed parameter block (floats; built by qqtsim/policy.py pack_lstm), all
-// weights k-major [in][out]
-constexpr int OFF_C1W = 0, OFF_C1B = 4096, OFF_C2W = 4160, OFF_C2B = 22592;
-constexpr int OFF_FCW = 22656, OFF_FCB = 96384, OFF_R1W = 96512, OFF_R1B = 100608;
-constexpr int OFF_R2W = 100672, OFF_R2B = 102720, OFF_G1W = 102784, OFF_G1B = 102912;
-constexpr int OFF_G2W = 102976, OFF_G2B = 103232, OFF_FUW = 103296, OFF_FUB = 146304;
-constexpr int OFF_LW = 146560, OFF_LB = 343168, OFF_HW = 343680, OFF_HB = 368256;
-constexpr int OFF_OW = 368448, OFF_OB = 371520, N_PARAMS = 371584;
+// packed parameter block (floats; built by qqtsim/policy.py pack_lstm): the
+// convolutions k-major [in][out], the head's layers as MFMA B fragments
+// [column tile][K / 16][64 lanes][4] (value i of lane 16 q + r in group g of
+// tile t = W[16 g + 4 q + i][16 t + r])
+constexpr int OFF_C1W = 0, OFF_C1B = OFF_C1W + K1 * 32, OFF_C2W = OFF_C1B + 64,
+              OFF_C2B = OFF_C2W + K2 * 64, OFF_FCW = OFF_C2B + 64, OFF_FCB = OFF_FCW + FEAT * 128,
+              OFF_R1W = OFF_FCB + 128, OFF_R1B = OFF_R1W + 64 * 64, OFF_R2W = OFF_R1B + 64,
+              OFF_R2B = OFF_R2W + 64 * 32, OFF_G1W = OFF_R2B + 64, OFF_G1B = OFF_G1W + 16 * 16,
+              OFF_G2W = OFF_G1B + 64, OFF_G2B = OFF_G2W + 16 * 16, OFF_FUW = OFF_G2B + 64,
+              OFF_FUB = OFF_FUW + XINP * 256, OFF_LW = OFF_FUB + 256, OFF_LB = OFF_LW + 384 * G4,
+              OFF_HW = OFF_LB + G4, OFF_HB = OFF_HW + 128 * 192, OFF_OW = OFF_HB + 192,
+              OFF_OB = OFF_OW + 192 * 16, N_PARAMS = OFF_OB + 64;
 static_assert(N_PARAMS == QQT_LSTM_PARAMS, "packed block size");
 
 __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
@@ -167,44 +186,60 @@ __global__ __launch_bounds__(64) void lstm_feat_kernel(const qqt_sim_config cf,
 }
 
 // ---------------------------------------------------------------- act
+template <int ROWS>
 struct __align__(16) ActLds {
+  static constexpr int HT = (ROWS + 15) / 16;   // 16-row head tiles
   union {
-    struct {                       // trunk: conv weights + one row's planes
-      float w1[K1 * 32];
-      float w2[K2 * 64];
-      float in[C_MAX * 81];        // zero-bordered 9 x 9 per input channel
-      float a1[32 * 81];           // conv1 output, zero-bordered
-      float a2[64 * 49];           // conv2 output
+    struct {                        // trunk: one group of RG rows
+      float in[RG][CS1 * 81];       // zero-bordered 9 x 9 per channel slot
+      float a1[RG][32 * 81];        // conv1 output, zero-bordered
     } t;
-    struct {                       // head: activations of the 16 rows
-      float xin[ROWS][XIN];        // fc | rel | glob outputs
-      float xh[ROWS][XH];          // fused | previous h
-      float g[ROWS][G4];           // LSTM gates
-      float hn[ROWS][HID];         // new h
-      float hd[ROWS][3 * HEAD];    // heads' hidden layers
-      float r1[ROWS][64], g1[ROWS][16];
-      float rel[ROWS][64];         // rel inputs (60 used)
-      float glb[ROWS][8];          // glob inputs (5 used)
-      float lg[ROWS][16];          // outputs
+    struct {                        // head: one 16-row tile
+      float xin[16 * LD_XIN];       // fc | rel | glob outputs
+      float xh[16 * LD_XH];         // fused | previous h
+      float hn[16 * LD_HN];         // new h
+      float hd[16 * LD_HD];         // heads' hidden layers
+      float r1[16 * LD_R], g1[16 * LD_G1];
+      float rel[16 * LD_R];         // rel inputs (60 used)
+      float glb[16 * LD_GLB];       // glob inputs (5 used)
+      float lg[16 * LD_LG];         // outputs
     } h;
   };
-  float pooled[ROWS][FEAT];
+  float pooled[HT * 16 * LD_POOL];  // 576 pooled features per row
 };
 
-// acc[t] += A (16 rows, LDS, row stride lda) x B (global k-major, row stride
-// ldb) over K (a multiple of 4), output column tiles n0 + 16 t.
-template <int NT>
-__device__ __forceinline__ void gemm16(floatx4 (&acc)[NT], const float* A, int lda, const float* B,
-                                       int ldb, int n0, int K, int lane) {
+// acc[t] += A (16 rows in LDS, row stride lda floats, 16-byte aligned) x B
+// over K (a multiple of 16), B's column tile tile(t) read from its MFMA
+// fragments F.  Per 16-k group: one 16-byte A read (row r, k = 16 g + 4 q ..
+// + 3) and one 16-byte fragment read per tile feed four K steps.
+template <int NT, class Tile>
+__device__ __forceinline__ void gemmf(floatx4 (&acc)[NT], const float* A, int lda, const float* F,
+                                      int K, Tile tile, int lane) {
   const int r = lane & 15, q = lane >> 4;
+  const int kg = K / 16;
+  const float4* Fv = reinterpret_cast<const float4*>(F);
+  const float* Ar = A + r * lda + 4 * q;
 #pragma unroll 4
-  for (int k0 = 0; k0 < K; k0 += 4) {
-    const float av = A[r * lda + k0 + q];
-    const float* b = B + (size_t)(k0 + q) * ldb + n0 + r;
+  for (int g = 0; g < kg; ++g) {
+    const float4 av = *reinterpret_cast<const float4*>(Ar + 16 * g);
+    float4 bv[NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = mfma4(av, b[16 * t], acc[t]);
+    for (int t = 0; t < NT; ++t) bv[t] = Fv[((size_t)tile(t) * kg + g) * 64 + lane];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      acc[t] = mfma4(av.x, bv[t].x, acc[t]);
+      acc[t] = mfma4(av.y, bv[t].y, acc[t]);
+      acc[t] = mfma4(av.z, bv[t].z, acc[t]);
+      acc[t] = mfma4(av.w, bv[t].w, acc[t]);
+    }
   }
 }
+
+// NT consecutive column tiles from t0
+struct Tiles {
+  int t0;
+  __device__ int operator()(int t) const { return t0 + t; }
+};
 
 // bias + optional ReLU of the output tiles into a row-major LDS block
 template <int NT>
@@ -225,223 +260,288 @@ __device__ __forceinline__ void store16(const floatx4 (&acc)[NT], float* D, int 
 }
 
 __device__ __forceinline__ float sigm(float x) { return 1.0f / (1.0f + expf(-x)); }
+__device__ __forceinline__ int tapoff(int tap) { return (tap / 3) * 9 + tap % 3; }
 
+// ROWS rows per workgroup: the trunk in groups of RG rows, the head in
+// 16-row tiles.
+template <int ROWS>
 __global__ __launch_bounds__(NTHR) void lstm_act_kernel(const qqt_lstm_args a) {
-  __shared__ ActLds s;
+  static_assert(ROWS % RG == 0, "whole trunk groups");
+  using L = ActLds<ROWS>;
+  constexpr int HT = L::HT;
+  __shared__ L s;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, q = lane >> 4;
   const int row0 = blockIdx.x * ROWS;
   const float* P = a.params;
-  const int cin = a.c_in, k1 = 9 * cin;
+  const int cin = a.c_in;
 
-  // conv weights to LDS; zero the bordered planes once
-  for (int i = tid; i < K1 * 32; i += NTHR) s.t.w1[i] = P[OFF_C1W + i];
-  for (int i = tid; i < K2 * 64; i += NTHR) s.t.w2[i] = P[OFF_C2W + i];
-  for (int i = tid; i < C_MAX * 81; i += NTHR) s.t.in[i] = 0.0f;
-  for (int i = tid; i < 32 * 81; i += NTHR) s.t.a1[i] = 0.0f;
+  // This wavefront's conv weights stay in registers for the whole trunk:
+  // conv1 column tile w & 1 (the four wavefronts w >> 1 take every fourth
+  // position tile), conv2 column tile w & 3 (wavefronts w >> 2 take every
+  // other position tile).  b1[ks] / b2[ks] is B[4 ks + q][column].
+  const int n1 = 16 * (w & 1) + r16, n2 = 16 * (w & 3) + r16;
+  float b1[K1 / 4], b2[K2 / 4];
+#pragma unroll
+  for (int ks = 0; ks < K1 / 4; ++ks) b1[ks] = P[OFF_C1W + (4 * ks + q) * 32 + n1];
+#pragma unroll
+  for (int ks = 0; ks < K2 / 4; ++ks) b2[ks] = P[OFF_C2W + (4 * ks + q) * 64 + n2];
+  const float bias1 = P[OFF_C1B + n1], bias2 = P[OFF_C2B + n2];
 
-  // per-lane gather geometry: wavefront w owns positions 16w .. 16w+15
-  const int pos = 16 * w + (lane & 15), q = lane >> 4;
-  const bool pv = pos < 49;
-  const int poff = pv ? (pos / 7) * 9 + pos % 7 : 0;   // top-left of the 3x3 window in a 9x9 grid
-  auto tap = [](int k) { return (k / 9) * 81 + ((k % 9) / 3) * 9 + (k % 3); };
+  // per-lane A-operand addresses (floats from the plane's start; the tap and
+  // channel step of each K step is an immediate offset).  conv1 positions
+  // run row-major over the group's 4 x 49 positions; conv2 positions are
+  // ordered (row, pooling window, position in the window), so each output
+  // lane's four values are one 2x2 window.
+  auto tile1 = [&](int i) { return 4 * i + (w >> 1); };   // conv1 tile of slot i
+  auto tile2 = [&](int i) { return 2 * i + (w >> 2); };   // conv2 tile of slot i
+  int base1[T1];
+  bool ok1[T1];
+#pragma unroll
+  for (int i = 0; i < T1; ++i) {
+    const int m = tile1(i) * 16 + r16;
+    ok1[i] = tile1(i) < M1T && m < RG * 49;
+    const int rr = ok1[i] ? m / 49 : 0, p = ok1[i] ? m % 49 : 0;
+    base1[i] = rr * (CS1 * 81) + q * 81 + (p / 7) * 9 + p % 7;
+  }
+  int base2[T2];
+  bool ok2[T2];
+#pragma unroll
+  for (int i = 0; i < T2; ++i) {
+    ok2[i] = tile2(i) < M2T;
+    const int m = (ok2[i] ? tile2(i) : 0) * 16 + r16;
+    const int rr = m / 36, wi = (m % 36) / 4, s4 = m % 4;
+    const int y = 2 * (wi / 3) + (s4 >> 1), x = 2 * (wi % 3) + (s4 & 1);
+    base2[i] = rr * (32 * 81) + q * 81 + y * 9 + x;
+  }
 
-  for (int rr = 0; rr < ROWS; ++rr) {
-    const int row = min(row0 + rr, a.batch - 1);        // rows past the batch: computed, dropped
-    __syncthreads();                                     // previous row's planes are consumed
-    const uint16_t* loc = a.local + (size_t)row * a.local_stride;
-    for (int i = tid; i < cin * 49; i += NTHR)
-      s.t.in[(i / 49) * 81 + ((i % 49) / 7 + 1) * 9 + (i % 7) + 1] = h2f(loc[i]);
-    __syncthreads();
-    // conv1: C -> 32; this wavefront's position tile, both channel tiles
+  // zero the bordered planes (borders and unused channel slots stay zero)
+  // and the pooled rows past ROWS (read by the last head tile, dropped)
+  for (int i = tid; i < RG * CS1 * 81; i += NTHR) (&s.t.in[0][0])[i] = 0.0f;
+  for (int i = tid; i < RG * 32 * 81; i += NTHR) (&s.t.a1[0][0])[i] = 0.0f;
+  for (int i = ROWS * LD_POOL + tid; i < HT * 16 * LD_POOL; i += NTHR) s.pooled[i] = 0.0f;
+  __syncthreads();
+
+  auto stage = [&](int g) {   // the group's windows, float16 -> float32 planes
+    const int n = cin * 49;
+    for (int i = tid; i < RG * n; i += NTHR) {
+      const int rr = i / n, rem = i % n, ci = rem / 49, p = rem % 49;
+      const int row = min(row0 + g * RG + rr, a.batch - 1);   // past the batch: computed, dropped
+      s.t.in[rr][ci * 81 + (p / 7 + 1) * 9 + p % 7 + 1] =
+          h2f(a.local[(size_t)row * a.local_stride + rem]);
+    }
+  };
+  stage(0);
+#pragma unroll 1
+  for (int g = 0; g < ROWS / RG; ++g) {
+    __syncthreads();   // in[] holds group g; a1 is free
+    // conv1 (C -> 32, 3x3, pad 1) + ReLU into a1's interior
     {
-      floatx4 acc[2] = {floatx4{0, 0, 0, 0}, floatx4{0, 0, 0, 0}};
-#pragma unroll 4
-      for (int k0 = 0; k0 < K1; k0 += 4) {
-        const int k = k0 + q;
-        const float av = (pv && k < k1) ? s.t.in[poff + tap(k)] : 0.0f;
-        acc[0] = mfma4(av, s.t.w1[k * 32 + (lane & 15)], acc[0]);
-        acc[1] = mfma4(av, s.t.w1[k * 32 + 16 + (lane & 15)], acc[1]);
+      floatx4 acc[T1];
+#pragma unroll
+      for (int i = 0; i < T1; ++i) acc[i] = floatx4{0, 0, 0, 0};
+      const float* ib = &s.t.in[0][0];
+#pragma unroll
+      for (int ks = 0; ks < K1 / 4; ++ks) {
+        const int off = 4 * (ks % 4) * 81 + tapoff(ks / 4);
+#pragma unroll
+        for (int i = 0; i < T1; ++i) {
+          const float av = ok1[i] ? ib[base1[i] + off] : 0.0f;
+          acc[i] = mfma4(av, b1[ks], acc[i]);
+        }
+        // keep the scheduler from hoisting every K step's loads (register
+        // pressure): loads run at most one K step ahead
+        if (ks % 2 == 1) __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int co = 16 * t + (lane & 15);
-        const float b = P[OFF_C1B + co];
+      for (int i = 0; i < T1; ++i) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int p = 16 * w + 4 * q + j;
-          if (p < 49) s.t.a1[co * 81 + (p / 7 + 1) * 9 + p % 7 + 1] = fmaxf(acc[t][j] + b, 0.0f);
+          const int m = tile1(i) * 16 + 4 * q + j;
+          if (tile1(i) < M1T && m < RG * 49) {
+            const int rr = m / 49, p = m % 49;
+            s.t.a1[rr][n1 * 81 + (p / 7 + 1) * 9 + p % 7 + 1] = fmaxf(acc[i][j] + bias1, 0.0f);
+          }
         }
       }
     }
+    __syncthreads();   // a1 complete; in[] free
+    if (g + 1 < ROWS / RG) stage(g + 1);
+    // conv2 (32 -> 64) at the 36 positions the 2x2 pool reads, ReLU, max pool
+    {
+      floatx4 acc[T2];
+#pragma unroll
+      for (int i = 0; i < T2; ++i) acc[i] = floatx4{0, 0, 0, 0};
+      const float* ab = &s.t.a1[0][0];
+#pragma unroll
+      for (int ks = 0; ks < K2 / 4; ++ks) {
+        const int off = 4 * (ks % 8) * 81 + tapoff(ks / 8);
+#pragma unroll
+        for (int i = 0; i < T2; ++i) acc[i] = mfma4(ab[base2[i] + off], b2[ks], acc[i]);
+        if (ks % 2 == 1) __builtin_amdgcn_sched_barrier(0);
+      }
+      // lane (q, j) of tile t holds window 4 t + q at its position j:
+      // max_j relu(v_j + b) = relu(max_j v_j + b)
+#pragma unroll
+      for (int i = 0; i < T2; ++i) {
+        if (!ok2[i]) continue;
+        const int wdx = 4 * tile2(i) + q, rr = wdx / 9, w9 = wdx % 9;
+        const float mx = fmaxf(fmaxf(acc[i][0], acc[i][1]), fmaxf(acc[i][2], acc[i][3]));
+        s.pooled[(g * RG + rr) * LD_POOL + n2 * 9 + w9] = fmaxf(mx + bias2, 0.0f);
+      }
+    }
+  }
+
+#pragma unroll 1
+  for (int ht = 0; ht < HT; ++ht) {
+    __syncthreads();   // trunk done / previous tile's buffers consumed
+    const int hr0 = row0 + 16 * ht;
+    // rel / glob inputs, previous hidden state (zero for reset envs)
+    for (int i = tid; i < 16 * 64; i += NTHR) {
+      const int r = i / 64, k = i % 64, row = min(hr0 + r, a.batch - 1);
+      s.h.rel[r * LD_R + k] = k < MAX_T * 6 ? h2f(a.rel[(size_t)row * a.rel_stride + k]) : 0.0f;
+    }
+    for (int i = tid; i < 16 * 16; i += NTHR) {
+      const int r = i / 16, k = i % 16, row = min(hr0 + r, a.batch - 1);
+      s.h.glb[r * LD_GLB + k] = k < GLOB ? h2f(a.glob[(size_t)row * a.glob_stride + k]) : 0.0f;
+      if (k < XINP - XIN) s.h.xin[r * LD_XIN + XIN + k] = 0.0f;   // fusion K padding
+    }
+    for (int i = tid; i < 16 * HID; i += NTHR) {
+      const int r = i / HID, k = i % HID, row = min(hr0 + r, a.batch - 1);
+      const bool zero = a.reset && a.reset[row / a.rows_per_env];
+      s.h.xh[r * LD_XH + 256 + k] = zero ? 0.0f : a.h[(size_t)row * HID + k];
+    }
+    // Linear(576, 128) + ReLU: 8 column tiles, one per wavefront
+    {
+      floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
+      gemmf<1>(acc, s.pooled + 16 * ht * LD_POOL, LD_POOL, P + OFF_FCW, FEAT, Tiles{w}, lane);
+      store16<1>(acc, s.h.xin, LD_XIN, 16 * w, P + OFF_FCB, true, lane, HID);
+    }
     __syncthreads();
-    // conv2: 32 -> 64
+    // rel 60 -> 64 (wavefronts 0-3), glob 5 -> 16 (wavefront 4)
+    if (w < 4) {
+      floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
+      gemmf<1>(acc, s.h.rel, LD_R, P + OFF_R1W, 64, Tiles{w}, lane);
+      store16<1>(acc, s.h.r1, LD_R, 16 * w, P + OFF_R1B, true, lane, 64);
+    } else {
+      if (w == 4) {
+        floatx4 ag[1] = {floatx4{0, 0, 0, 0}};
+        gemmf<1>(ag, s.h.glb, LD_GLB, P + OFF_G1W, 16, Tiles{0}, lane);
+        store16<1>(ag, s.h.g1, LD_G1, 0, P + OFF_G1B, true, lane, 16);
+      }
+    }
+    __syncthreads();
+    // rel 64 -> 32 (wavefronts 0, 1), glob 16 -> 8 (wavefront 2)
+    if (w < 2) {
+      floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
+      gemmf<1>(acc, s.h.r1, LD_R, P + OFF_R2W, 64, Tiles{w}, lane);
+      store16<1>(acc, s.h.xin + HID, LD_XIN, 16 * w, P + OFF_R2B, true, lane, 32);
+    } else if (w == 2) {
+      floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
+      gemmf<1>(acc, s.h.g1, LD_G1, P + OFF_G2W, 16, Tiles{0}, lane);
+      store16<1>(acc, s.h.xin + HID + 32, LD_XIN, 0, P + OFF_G2B, true, lane, 8);
+    }
+    __syncthreads();
+    // fusion Linear(168, 256) + ReLU: 16 tiles, two per wavefront
+    {
+      floatx4 acc[2] = {floatx4{0, 0, 0, 0}, floatx4{0, 0, 0, 0}};
+      gemmf<2>(acc, s.h.xin, LD_XIN, P + OFF_FUW, XINP, Tiles{2 * w}, lane);
+      store16<2>(acc, s.h.xh, LD_XH, 32 * w, P + OFF_FUB, true, lane, 256);
+    }
+    __syncthreads();
+    // LSTM gates [fused | h] (384) x W (384 x 512) + b.  Wavefront w takes
+    // hidden units 16 w .. 16 w + 15 of all four gates (tile t = gate), so
+    // each lane holds i, f, g, o of the same (row, unit) and updates the
+    // cell in registers.
     {
       floatx4 acc[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) acc[t] = floatx4{0, 0, 0, 0};
-#pragma unroll 4
-      for (int k0 = 0; k0 < K2; k0 += 4) {
-        const int k = k0 + q;
-        const float av = pv ? s.t.a1[poff + tap(k)] : 0.0f;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) acc[t] = mfma4(av, s.t.w2[k * 64 + 16 * t + (lane & 15)], acc[t]);
-      }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int co = 16 * t + (lane & 15);
-        const float b = P[OFF_C2B + co];
+      gemmf<4>(acc, s.h.xh, LD_XH, P + OFF_LW, 384, [&](int t) { return 8 * t + w; }, lane);
+      {
+        const int u = 16 * w + r16;
+        const float bi = P[OFF_LB + u], bf = P[OFF_LB + HID + u];
+        const float bg = P[OFF_LB + 2 * HID + u], bo = P[OFF_LB + 3 * HID + u];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int p = 16 * w + 4 * q + j;
-          if (p < 49) s.t.a2[co * 49 + p] = fmaxf(acc[t][j] + b, 0.0f);
+          const int r = 4 * q + j, row = hr0 + r;
+          const bool mine = 16 * ht + r < ROWS && row < a.batch;
+          const float ig = sigm(acc[0][j] + bi), fg = sigm(acc[1][j] + bf);
+          const float gg = tanhf(acc[2][j] + bg), og = sigm(acc[3][j] + bo);
+          float cp = 0.0f;
+          if (mine && !(a.reset && a.reset[row / a.rows_per_env])) cp = a.c[(size_t)row * HID + u];
+          const float c2 = fg * cp + ig * gg;
+          const float h2 = og * tanhf(c2);
+          s.h.hn[r * LD_HN + u] = h2;
+          if (mine) {
+            a.c[(size_t)row * HID + u] = c2;
+            a.h[(size_t)row * HID + u] = h2;
+          }
         }
       }
     }
     __syncthreads();
-    // 2x2 max pool (7 -> 3), flattened channel-major like x.view(B, -1)
-    for (int i = tid; i < FEAT; i += NTHR) {
-      const int c = i / 9, y = (i % 9) / 3, x = i % 3;
-      const float* p = s.t.a2 + c * 49 + (2 * y) * 7 + 2 * x;
-      s.pooled[rr][i] = fmaxf(fmaxf(p[0], p[1]), fmaxf(p[7], p[8]));
+    // heads' hidden layers 128 -> 192 + ReLU: 12 tiles, two per wavefront
+    // 0-3 and one per wavefront 4-7
+    if (w < 4) {
+      floatx4 acc[2] = {floatx4{0, 0, 0, 0}, floatx4{0, 0, 0, 0}};
+      gemmf<2>(acc, s.h.hn, LD_HN, P + OFF_HW, HID, Tiles{2 * w}, lane);
+      store16<2>(acc, s.h.hd, LD_HD, 32 * w, P + OFF_HB, true, lane, 3 * HEAD);
+    } else {
+      floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
+      gemmf<1>(acc, s.h.hn, LD_HN, P + OFF_HW, HID, Tiles{8 + (w - 4)}, lane);
+      store16<1>(acc, s.h.hd, LD_HD, 128 + 16 * (w - 4), P + OFF_HB, true, lane, 3 * HEAD);
     }
-  }
-  __syncthreads();   // trunk done: its LDS becomes the head's
-
-  // rel / glob inputs, previous hidden state
-  for (int i = tid; i < ROWS * 64; i += NTHR) {
-    const int r = i / 64, k = i % 64, row = min(row0 + r, a.batch - 1);
-    s.h.rel[r][k] = k < MAX_T * 6 ? h2f(a.rel[(size_t)row * a.rel_stride + k]) : 0.0f;
-  }
-  for (int i = tid; i < ROWS * 8; i += NTHR) {
-    const int r = i / 8, k = i % 8, row = min(row0 + r, a.batch - 1);
-    s.h.glb[r][k] = k < GLOB ? h2f(a.glob[(size_t)row * a.glob_stride + k]) : 0.0f;
-  }
-  for (int i = tid; i < ROWS * HID; i += NTHR) {
-    const int r = i / HID, k = i % HID, row = min(row0 + r, a.batch - 1);
-    const bool zero = a.reset && a.reset[row / a.rows_per_env];
-    s.h.xh[r][256 + k] = zero ? 0.0f : a.h[(size_t)row * HID + k];
-  }
-  // Linear(576, 128) + ReLU: 8 column tiles, two per wavefront
-  {
-    floatx4 acc[2] = {floatx4{0, 0, 0, 0}, floatx4{0, 0, 0, 0}};
-    gemm16<2>(acc, &s.pooled[0][0], FEAT, P + OFF_FCW, HID, 32 * w, FEAT, lane);
-    store16<2>(acc, &s.h.xin[0][0], XIN, 32 * w, P + OFF_FCB, true, lane, HID);
-  }
-  __syncthreads();
-  // rel 60 -> 64 (one tile per wavefront), glob 5 -> 16 (wavefront 0)
-  {
-    floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
-    gemm16<1>(acc, &s.h.rel[0][0], 64, P + OFF_R1W, 64, 16 * w, 64, lane);
-    store16<1>(acc, &s.h.r1[0][0], 64, 16 * w, P + OFF_R1B, true, lane, 64);
+    __syncthreads();
+    // output layer 192 -> 8 (block diagonal, 16 padded columns): wavefront 0
     if (w == 0) {
-      floatx4 ag[1] = {floatx4{0, 0, 0, 0}};
-      gemm16<1>(ag, &s.h.glb[0][0], 8, P + OFF_G1W, 16, 0, 8, lane);
-      store16<1>(ag, &s.h.g1[0][0], 16, 0, P + OFF_G1B, true, lane, 16);
+      floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
+      gemmf<1>(acc, s.h.hd, LD_HD, P + OFF_OW, 3 * HEAD, Tiles{0}, lane);
+      store16<1>(acc, s.h.lg, LD_LG, 0, P + OFF_OB, false, lane, 16);
     }
-  }
-  __syncthreads();
-  // rel 64 -> 32 (wavefronts 0, 1), glob 16 -> 8 (wavefront 2)
-  if (w < 2) {
-    floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
-    gemm16<1>(acc, &s.h.r1[0][0], 64, P + OFF_R2W, 32, 16 * w, 64, lane);
-    store16<1>(acc, &s.h.xin[0][HID], XIN, 16 * w, P + OFF_R2B, true, lane, 32);
-  } else if (w == 2) {
-    floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
-    gemm16<1>(acc, &s.h.g1[0][0], 16, P + OFF_G2W, 16, 0, 16, lane);
-    store16<1>(acc, &s.h.xin[0][HID + 32], XIN, 0, P + OFF_G2B, true, lane, 8);
-  }
-  __syncthreads();
-  // fusion Linear(168, 256) + ReLU: 16 tiles, four per wavefront
-  {
-    floatx4 acc[4];
+    __syncthreads();
+    // outputs and masked sampling: one thread per row
+    if (tid < 16 && 16 * ht + tid < ROWS && hr0 + tid < a.batch) {
+      const int row = hr0 + tid;
+      const float* lg = s.h.lg + tid * LD_LG;
+      const size_t o = (size_t)row * a.out_stride + a.out_slot;
+      if (a.logits_out) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[t] = floatx4{0, 0, 0, 0};
-    gemm16<4>(acc, &s.h.xin[0][0], XIN, P + OFF_FUW, 256, 64 * w, XIN, lane);
-    store16<4>(acc, &s.h.xh[0][0], XH, 64 * w, P + OFF_FUB, true, lane, 256);
-  }
-  __syncthreads();
-  // LSTM gates: [fused | h] (384) x W (384 x 512) + b: 32 tiles, eight per wavefront
-  {
-    floatx4 acc[8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) acc[t] = floatx4{0, 0, 0, 0};
-    gemm16<8>(acc, &s.h.xh[0][0], XH, P + OFF_LW, G4, 128 * w, XH, lane);
-    store16<8>(acc, &s.h.g[0][0], G4, 128 * w, P + OFF_LB, false, lane, G4);
-  }
-  __syncthreads();
-  // cell update
-  for (int i = tid; i < ROWS * HID; i += NTHR) {
-    const int r = i / HID, k = i % HID, row = row0 + r;
-    const float ig = sigm(s.h.g[r][k]), fg = sigm(s.h.g[r][HID + k]);
-    const float gg = tanhf(s.h.g[r][2 * HID + k]), og = sigm(s.h.g[r][3 * HID + k]);
-    float cp = 0.0f;
-    if (row < a.batch && !(a.reset && a.reset[row / a.rows_per_env])) cp = a.c[(size_t)row * HID + k];
-    const float c2 = fg * cp + ig * gg;
-    const float h2 = og * tanhf(c2);
-    s.h.hn[r][k] = h2;
-    if (row < a.batch) {
-      a.c[(size_t)row * HID + k] = c2;
-      a.h[(size_t)row * HID + k] = h2;
-    }
-  }
-  __syncthreads();
-  // heads' hidden layers 128 -> 192 + ReLU: 12 tiles, three per wavefront
-  {
-    floatx4 acc[3];
-#pragma unroll
-    for (int t = 0; t < 3; ++t) acc[t] = floatx4{0, 0, 0, 0};
-    gemm16<3>(acc, &s.h.hn[0][0], HID, P + OFF_HW, 3 * HEAD, 48 * w, HID, lane);
-    store16<3>(acc, &s.h.hd[0][0], 3 * HEAD, 48 * w, P + OFF_HB, true, lane, 3 * HEAD);
-  }
-  __syncthreads();
-  // output layer 192 -> 8 (block diagonal, 16 padded columns): wavefront 0
-  if (w == 0) {
-    floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
-    gemm16<1>(acc, &s.h.hd[0][0], 3 * HEAD, P + OFF_OW, 16, 0, 3 * HEAD, lane);
-    store16<1>(acc, &s.h.lg[0][0], 16, 0, P + OFF_OB, false, lane, 16);
-  }
-  __syncthreads();
-  // outputs and masked sampling: one thread per row
-  if (tid < ROWS && row0 + tid < a.batch) {
-    const int row = row0 + tid;
-    const float* lg = s.h.lg[tid];
-    const size_t o = (size_t)row * a.out_stride + a.out_slot;
-    if (a.logits_out) {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) a.logits_out[(size_t)row * 8 + k] = lg[k];
-    }
-    if (a.value_out) a.value_out[o] = lg[7];
-    if (a.sample) {
-      const int env = row / a.rows_per_env;
-      const int pid = a.rows_per_env == 1 ? a.pid0 : row % a.rows_per_env;
-      uint8_t mm[5], bm[2];
-#pragma unroll
-      for (int k = 0; k < 5; ++k) mm[k] = a.move_mask[(size_t)row * a.mm_row_stride + k];
-#pragma unroll
-      for (int k = 0; k < 2; ++k) bm[k] = a.bomb_mask[(size_t)row * a.bm_row_stride + k];
-      float um, ub;
-      if (a.uniforms) {
-        um = a.uniforms[(size_t)row * 2 + 0];
-        ub = a.uniforms[(size_t)row * 2 + 1];
-      } else {
-        float u4[4];
-        philox_block(a.seed, (uint32_t)env, a.tick, STREAM_POLICY, (uint32_t)((2 * pid) >> 2), u4);
-        um = u4[(2 * pid) & 3];
-        ub = u4[(2 * pid + 1) & 3];
+        for (int k = 0; k < 8; ++k) a.logits_out[(size_t)row * 8 + k] = lg[k];
       }
-      float lpm, lpb;
-      const int am = sample_masked<5>(lg, mm, um, &lpm);
-      const int ab = sample_masked<2>(lg + 5, bm, ub, &lpb);
-      if (a.actions) {
-        a.actions[o * 2 + 0] = am;
-        a.actions[o * 2 + 1] = ab;
+      if (a.value_out) a.value_out[o] = lg[7];
+      if (a.sample) {
+        const int env = row / a.rows_per_env;
+        const int pid = a.rows_per_env == 1 ? a.pid0 : row % a.rows_per_env;
+        uint8_t mm[5], bm[2];
+#pragma unroll
+        for (int k = 0; k < 5; ++k) mm[k] = a.move_mask[(size_t)row * a.mm_row_stride + k];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) bm[k] = a.bomb_mask[(size_t)row * a.bm_row_stride + k];
+        float um, ub;
+        if (a.uniforms) {
+          um = a.uniforms[(size_t)row * 2 + 0];
+          ub = a.uniforms[(size_t)row * 2 + 1];
+        } else {
+          float u4[4];
+          philox_block(a.seed, (uint32_t)env, a.tick, STREAM_POLICY, (uint32_t)((2 * pid) >> 2), u4);
+          um = u4[(2 * pid) & 3];
+          ub = u4[(2 * pid + 1) & 3];
+        }
+        float lpm, lpb;
+        const int am = sample_masked<5>(lg, mm, um, &lpm);
+        const int ab = sample_masked<2>(lg + 5, bm, ub, &lpb);
+        if (a.actions) {
+          a.actions[o * 2 + 0] = am;
+          a.actions[o * 2 + 1] = ab;
+        }
+        if (a.actions_i8) {
+          a.actions_i8[o * 2 + 0] = (int8_t)am;
+          a.actions_i8[o * 2 + 1] = (int8_t)ab;
+        }
+        if (a.logp_out) a.logp_out[o] = lpm + lpb;
       }
-      if (a.actions_i8) {
-        a.actions_i8[o * 2 + 0] = (int8_t)am;
-        a.actions_i8[o * 2 + 1] = (int8_t)ab;
-      }
-      if (a.logp_out) a.logp_out[o] = lpm + lpb;
     }
   }
 }
@@ -507,8 +607,8 @@ int qqt_lstm_act(const qqt_lstm_args* a, void* stream) {
     return QQT_E_ARG;
   }
   hipStream_t st = (hipStream_t)stream;
-  const int blocks = (a->batch + lstm::ROWS - 1) / lstm::ROWS;
-  QQT_LAUNCH(QQT_KERNEL_LSTM, lstm::lstm_act_kernel, dim3(blocks), dim3(lstm::NTHR), st, *a);
+  const int blocks = (a->batch + 15) / 16;
+  QQT_LAUNCH(QQT_KERNEL_LSTM, lstm::lstm_act_kernel<16>, dim3(blocks), dim3(lstm::NTHR), st, *a);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     snprintf(g_err, sizeof(g_err), "lstm act launch failed: %s", hipGetErrorString(err));

@@ -516,23 +516,39 @@ class HipCnnActorCritic(HipActorCritic):
 
 
 # ---------------------------------------------------------------- lstm arch
-LSTM_PARAMS = 371584       # QQT_LSTM_PARAMS
-# float offsets of the packed block: (key, rows, columns) per k-major matrix
-# [in][out] or vector, in block order (qqt-gpu-sim_amd/csrc/lstm.hip OFF_*)
-_LSTM_BLOCKS = (("c1w", 128, 32), ("c1b", 1, 64), ("c2w", 288, 64), ("c2b", 1, 64),
-                ("fcw", 576, 128), ("fcb", 1, 128), ("r1w", 64, 64), ("r1b", 1, 64),
-                ("r2w", 64, 32), ("r2b", 1, 64), ("g1w", 8, 16), ("g1b", 1, 64),
-                ("g2w", 16, 16), ("g2b", 1, 64), ("fuw", 168, 256), ("fub", 1, 256),
-                ("lw", 384, 512), ("lb", 1, 512), ("hw", 128, 192), ("hb", 1, 192),
-                ("ow", 192, 16), ("ob", 1, 64))
+LSTM_PARAMS = 374272       # QQT_LSTM_PARAMS
+# blocks of the packed parameters in order: (key, rows K, columns N, layout)
+# with layout "k" = k-major [K][N], "f" = MFMA B fragments (see _lstm_frag),
+# "v" = a vector in a block of N floats (qqt-gpu-sim_amd/csrc/lstm.hip OFF_*)
+_LSTM_BLOCKS = (("c1w", 144, 32, "k"), ("c1b", 1, 64, "v"), ("c2w", 288, 64, "k"),
+                ("c2b", 1, 64, "v"), ("fcw", 576, 128, "f"), ("fcb", 1, 128, "v"),
+                ("r1w", 64, 64, "f"), ("r1b", 1, 64, "v"), ("r2w", 64, 32, "f"),
+                ("r2b", 1, 64, "v"), ("g1w", 16, 16, "f"), ("g1b", 1, 64, "v"),
+                ("g2w", 16, 16, "f"), ("g2b", 1, 64, "v"), ("fuw", 176, 256, "f"),
+                ("fub", 1, 256, "v"), ("lw", 384, 512, "f"), ("lb", 1, 512, "v"),
+                ("hw", 128, 192, "f"), ("hb", 1, 192, "v"), ("ow", 192, 16, "f"),
+                ("ob", 1, 64, "v"))
+
+
+def _lstm_frag(w: torch.Tensor) -> torch.Tensor:
+    """k-major [K][N] (K, N multiples of 16) -> MFMA B fragments for
+    v_mfma_f32_16x16x4_f32 in groups of four K steps: value i of lane
+    16 q + r in group g of column tile t is W[16 g + 4 q + i][16 t + r], so a
+    lane's four B values of a group are one 16-byte load and pair with the
+    four consecutive A values (row r, k = 16 g + 4 q .. + 3) of one LDS read."""
+    k, n = w.shape
+    x = w.reshape(k // 16, 4, 4, n // 16, 16)            # [g][q][i][t][r]
+    return x.permute(3, 0, 1, 4, 2).reshape(-1)           # [t][g][q][r][i]
 
 
 def pack_lstm(params: dict, obs_channels: int = 14) -> torch.Tensor:
     """One float32 block of QQT_LSTM_PARAMS values for qqt_lstm_act from an
     lstm ActorCritic state_dict (train/model.py:103-120, 140-153): every
-    weight transposed to k-major [in][out] and zero-padded to the block's
-    shape.  Convolution rows are k = in_channel * 9 + ky * 3 + kx (conv1 padded
-    to 128 rows); the LSTM block stacks W_ih^T over W_hh^T with the bias
+    weight transposed to k-major [in][out], zero-padded to the block's shape
+    and, for the head's layers, stored as MFMA B fragments (`_lstm_frag`).
+    Convolution rows are tap-major: k = (ky * 3 + kx) * S + in_channel
+    with S = 16 channel slots for conv1 (14 used, 144 rows) and S = 32 for
+    conv2 (288 rows); the LSTM block stacks W_ih^T over W_hh^T with the bias
     b_ih + b_hh, gate columns in torch's i, f, g, o order; the heads' hidden
     layers sit side by side (move | bomb | critic, 192 columns) and their
     output layers form one block-diagonal [192][16] matrix whose columns
@@ -554,8 +570,8 @@ def pack_lstm(params: dict, obs_channels: int = 14) -> torch.Tensor:
         if tuple(params[k].shape) != shp:
             raise ValueError(f"{k} must be {shp}, got {tuple(params[k].shape)}")
     src = {
-        "c1w": f("l_conv1.weight").reshape(32, c * 9).t(), "c1b": f("l_conv1.bias"),
-        "c2w": f("l_conv2.weight").reshape(64, 288).t(), "c2b": f("l_conv2.bias"),
+        "c1b": f("l_conv1.bias"),
+        "c2w": f("l_conv2.weight").permute(2, 3, 1, 0).reshape(288, 64), "c2b": f("l_conv2.bias"),
         "fcw": f("l_cnn_fc.weight").t(), "fcb": f("l_cnn_fc.bias"),
         "r1w": f("l_rel_fc1.weight").t(), "r1b": f("l_rel_fc1.bias"),
         "r2w": f("l_rel_fc2.weight").t(), "r2b": f("l_rel_fc2.bias"),
@@ -568,6 +584,9 @@ def pack_lstm(params: dict, obs_channels: int = 14) -> torch.Tensor:
         "hb": torch.cat([f(f"{n}.0.bias") for n in ("move_head", "bomb_head", "critic")]),
         "ob": torch.cat([f(f"{n}.2.bias") for n in ("move_head", "bomb_head", "critic")]),
     }
+    c1w = torch.zeros((9, 16, 32))
+    c1w[:, :c] = f("l_conv1.weight").permute(2, 3, 1, 0).reshape(9, c, 32)
+    src["c1w"] = c1w.reshape(144, 32)
     ow = torch.zeros((3 * HEAD, 16))
     ow[0:HEAD, 0:5] = f("move_head.2.weight").t()
     ow[HEAD:2 * HEAD, 5:7] = f("bomb_head.2.weight").t()
@@ -575,13 +594,14 @@ def pack_lstm(params: dict, obs_channels: int = 14) -> torch.Tensor:
     src["ow"] = ow
     out = torch.zeros(LSTM_PARAMS, dtype=torch.float32)
     off = 0
-    for key, rows, cols in _LSTM_BLOCKS:
-        blk = out[off:off + rows * cols].view(rows, cols)
+    for key, rows, cols, layout in _LSTM_BLOCKS:
         v = src[key]
-        if v.dim() == 1:
-            blk[0, :v.numel()] = v
+        if layout == "v":
+            out[off:off + v.numel()] = v
         else:
+            blk = torch.zeros((rows, cols))
             blk[:v.shape[0], :v.shape[1]] = v
+            out[off:off + rows * cols] = blk.reshape(-1) if layout == "k" else _lstm_frag(blk)
         off += rows * cols
     if off != LSTM_PARAMS:
         raise AssertionError("packed block size")
@@ -591,7 +611,7 @@ def pack_lstm(params: dict, obs_channels: int = 14) -> torch.Tensor:
 def lstm_block_offsets() -> dict:
     """Float offset of each block of the packed lstm parameters."""
     offs, off = {}, 0
-    for key, rows, cols in _LSTM_BLOCKS:
+    for key, rows, cols, _ in _LSTM_BLOCKS:
         offs[key] = off
         off += rows * cols
     return offs

@@ -2,9 +2,12 @@
 read the way qqt-gpu-sim_amd/csrc/lstm.hip reads it, on the CPU.
 
 `_emulate` restates the kernel's indexing in float64 numpy: the 7x7 windows
-in zero-bordered 9x9 grids with the tap map k -> (k / 9) * 81 + (k % 9 / 3) *
-9 + k % 3, conv1's output written back into a bordered grid, the 2x2 pool
-over 7x7 planes, the k-major blocks with their padding, the stacked LSTM
+in zero-bordered 9x9 grids with 16 channel slots, tap-major K for both
+convolutions (k = tap * slots + channel, tap offset (tap / 3) * 9 + tap % 3),
+conv1's output written back into a bordered grid, conv2 evaluated only at
+the 36 positions the 2x2 pool reads, ordered by pooling window, and pooled
+as relu(max + bias), the k-major and MFMA-fragment blocks with their
+padding, the stacked LSTM
 block and the block-diagonal output layer.  Run over the reference's frames
 (tests/golden/lstm.npz, train/model.py:176-185 with the hidden state carried
 and reset) it must reproduce the reference's logits, values and (h, c);
@@ -23,15 +26,10 @@ import pytest
 import torch
 
 from golden_io import lstm_params
-from qqtsim.policy import LSTM_PARAMS, lstm_block_offsets, pack_lstm
+from qqtsim.policy import _LSTM_BLOCKS, LSTM_PARAMS, lstm_block_offsets, pack_lstm
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-_SHAPES = {"c1w": (128, 32), "c1b": (1, 64), "c2w": (288, 64), "c2b": (1, 64),
-           "fcw": (576, 128), "fcb": (1, 128), "r1w": (64, 64), "r1b": (1, 64),
-           "r2w": (64, 32), "r2b": (1, 64), "g1w": (8, 16), "g1b": (1, 64),
-           "g2w": (16, 16), "g2b": (1, 64), "fuw": (168, 256), "fub": (1, 256),
-           "lw": (384, 512), "lb": (1, 512), "hw": (128, 192), "hb": (1, 192),
-           "ow": (192, 16), "ob": (1, 64)}
+_LOGICAL_ROWS = {"g1w": 8, "fuw": 168}      # rows past these are K padding
 
 
 @pytest.fixture(scope="module")
@@ -39,8 +37,8 @@ def z():
     return np.load(os.path.join(HERE, "golden", "lstm.npz"))
 
 
-def _tap(k):
-    return (k // 9) * 81 + ((k % 9) // 3) * 9 + k % 3
+def _tapoff(t):
+    return (t // 3) * 9 + t % 3
 
 
 def _poff(p):
@@ -54,33 +52,39 @@ def _sig(x):
 def _emulate(block, local, rel, glob, h, c):
     P = block.double().numpy()
     off = lstm_block_offsets()
+    shapes = {k: (r, c, lay) for k, r, c, lay in _LSTM_BLOCKS}
 
     def W(k):
-        r, cc = _SHAPES[k]
-        m = P[off[k]:off[k] + r * cc].reshape(r, cc)
-        return m[0] if r == 1 else m
+        r, cc, lay = shapes[k]
+        flat = P[off[k]:off[k] + r * cc]
+        if lay == "v":
+            return flat
+        if lay == "k":
+            return flat.reshape(r, cc)
+        # MFMA fragments [t][g][q][r][i] -> W[16 g + 4 q + i][16 t + r]
+        m = flat.reshape(cc // 16, r // 16, 4, 16, 4).transpose(1, 2, 4, 0, 3).reshape(r, cc)
+        return m[:_LOGICAL_ROWS.get(k, r)]
 
     relu = lambda x: np.maximum(x, 0.0)  # noqa: E731
     b, ch = local.shape[0], local.shape[1]
-    k1 = np.arange(128)
     pos = np.arange(49)
-    grid = np.zeros((b, 14 * 81))
+    grid = np.zeros((b, 16 * 81))
     for ci in range(ch):
         for p in pos:
             grid[:, ci * 81 + (p // 7 + 1) * 9 + p % 7 + 1] = local[:, ci, p // 7, p % 7]
-    idx1 = _poff(pos)[:, None] + _tap(k1)[None, :]
-    a = np.where(k1[None, None, :] < 9 * ch, grid[:, np.minimum(idx1, 14 * 81 - 1)], 0.0)
-    a1 = relu(a @ W("c1w") + W("c1b")[:32])                       # (B, 49, 32)
+    k1 = np.arange(144)
+    idx1 = (k1 % 16)[None, :] * 81 + _poff(pos)[:, None] + _tapoff(k1 // 16)[None, :]
+    a1 = relu(grid[:, idx1] @ W("c1w") + W("c1b")[:32])            # (B, 49, 32)
     grid2 = np.zeros((b, 32 * 81))
     for co in range(32):
         grid2[:, co * 81 + (pos // 7 + 1) * 9 + pos % 7 + 1] = a1[:, :, co]
-    idx2 = _poff(pos)[:, None] + _tap(np.arange(288))[None, :]
-    a2 = relu(grid2[:, idx2] @ W("c2w") + W("c2b")).transpose(0, 2, 1)   # (B, 64, 49)
-    pooled = np.zeros((b, 576))
-    for i in range(576):
-        cc, y, x = i // 9, (i % 9) // 3, i % 3
-        q = 2 * y * 7 + 2 * x
-        pooled[:, i] = np.max(a2[:, cc, [q, q + 1, q + 7, q + 8]], axis=1)
+    m = np.arange(36)
+    wi, s4 = m // 4, m % 4
+    top = (2 * (wi // 3) + s4 // 2) * 9 + 2 * (wi % 3) + s4 % 2     # window position (y, x)
+    k2 = np.arange(288)
+    idx2 = (k2 % 32)[None, :] * 81 + top[:, None] + _tapoff(k2 // 32)[None, :]
+    v = (grid2[:, idx2] @ W("c2w")).reshape(b, 9, 4, 64).max(axis=2)      # (B, 9, 64)
+    pooled = relu(v + W("c2b")).transpose(0, 2, 1).reshape(b, 576)     # channel-major
     fc = relu(pooled @ W("fcw") + W("fcb"))
     rin = np.zeros((b, 64))
     rin[:, :60] = rel.reshape(b, 60)
