@@ -308,7 +308,7 @@ def test_lstm_block_size_matches_the_header():
     from qqtsim import policy
 
     m = re.search(r"#define QQT_LSTM_PARAMS (\d+)", open(HEADER).read())
-    assert int(m.group(1)) == policy.LSTM_PARAMS == sum(r * c for _, r, c in policy._LSTM_BLOCKS)
+    assert int(m.group(1)) == policy.LSTM_PARAMS == sum(r * c for _, r, c, _ in policy._LSTM_BLOCKS)
 
 
 def _bot_args(**kw):
