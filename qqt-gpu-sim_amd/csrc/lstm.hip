@@ -43,6 +43,7 @@
 namespace qqt {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 
 namespace lstm {
 
@@ -52,6 +53,11 @@ constexpr int C_MAX = 14;                 // observation channels the packing al
 constexpr int CS1 = 16;                   // channel slots per conv1 tap (C_MAX used)
 constexpr int K1 = 9 * CS1;               // conv1 K: tap-major, k = tap * 16 + channel
 constexpr int K2 = 9 * 32;                // conv2 K: tap-major, k = tap * 32 + channel
+constexpr int KS1 = (K1 + 31) / 32;       // conv1 K steps of 32 (the last half padding)
+constexpr int KS2 = K2 / 32;              // conv2 K steps of 32 (one tap each)
+// channel pitch (halves) of the position-major trunk planes: 16-byte
+// aligned, chosen for few LDS bank conflicts of the 16-byte A reads
+constexpr int CP1 = 24, CP2 = 40;
 constexpr int FEAT = 576;                 // 64 x 3 x 3 pooled features
 constexpr int XIN = 168;                  // 128 + 32 + 8 fusion inputs
 constexpr int XINP = 176;                 // padded to whole 16-k groups
@@ -85,6 +91,10 @@ static_assert(N_PARAMS == QQT_LSTM_PARAMS, "packed block size");
 
 __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ floatx4 mfma16(half8 a, half8 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 __device__ __forceinline__ float h2f(uint16_t b) { return __half2float(__ushort_as_half(b)); }
@@ -190,9 +200,10 @@ template <int ROWS>
 struct __align__(16) ActLds {
   static constexpr int HT = (ROWS + 15) / 16;   // 16-row head tiles
   union {
-    struct {                        // trunk: one group of RG rows
-      float in[RG][CS1 * 81];       // zero-bordered 9 x 9 per channel slot
-      float a1[RG][32 * 81];        // conv1 output, zero-bordered
+    struct {                        // trunk: one group of RG rows, zero-bordered 9 x 9 grids
+      uint16_t in[RG][81 * CP1];    // float16 windows [position][channel slot]
+      uint16_t a1h[RG][81 * CP2];   // conv1 output [position][channel], float16 hi part
+      uint16_t a1l[RG][81 * CP2];   // and lo part (v - hi)
     } t;
     struct {                        // head: one 16-row tile
       float xin[16 * LD_XIN];       // fc | rel | glob outputs
@@ -277,33 +288,53 @@ __global__ __launch_bounds__(NTHR) void lstm_act_kernel(const qqt_lstm_args a) {
   const float* P = a.params;
   const int cin = a.c_in;
 
-  // This wavefront's conv weights stay in registers for the whole trunk:
+  // The trunk multiplies on v_mfma_f32_16x16x32_f16 (A: lane l holds row
+  // l%16, k = 8(l/16) .. + 7; B: k = 8(l/16) .. + 7 of column l%16; D as for
+  // the float32 MFMA) with float32 accuracy: weights split into float16 hi
+  // + lo, conv1's output likewise, and each product taken as hi*hi + hi*lo +
+  // lo*hi (the windows are float16 already: two products).  This
+  // wavefront's weight fragments stay in registers for the whole trunk:
   // conv1 column tile w & 1 (the four wavefronts w >> 1 take every fourth
   // position tile), conv2 column tile w & 3 (wavefronts w >> 2 take every
-  // other position tile).  b1[ks] / b2[ks] is B[4 ks + q][column].
+  // other position tile).  K step s covers k = 32 s .. 32 s + 31 of the
+  // tap-major K (conv1: taps 2s, 2s+1 x 16 channel slots; conv2: tap s x 32
+  // channels).
   const int n1 = 16 * (w & 1) + r16, n2 = 16 * (w & 3) + r16;
-  float b1[K1 / 4], b2[K2 / 4];
+  half8 b1h[KS1], b1l[KS1], b2h[KS2], b2l[KS2];
 #pragma unroll
-  for (int ks = 0; ks < K1 / 4; ++ks) b1[ks] = P[OFF_C1W + (4 * ks + q) * 32 + n1];
+  for (int st = 0; st < KS1; ++st)
 #pragma unroll
-  for (int ks = 0; ks < K2 / 4; ++ks) b2[ks] = P[OFF_C2W + (4 * ks + q) * 64 + n2];
+    for (int i = 0; i < 8; ++i) {
+      const int k = 32 * st + 8 * q + i;
+      const float v = k < K1 ? P[OFF_C1W + k * 32 + n1] : 0.0f;
+      const _Float16 hi = (_Float16)v;
+      b1h[st][i] = hi;
+      b1l[st][i] = (_Float16)(v - (float)hi);
+    }
+#pragma unroll
+  for (int st = 0; st < KS2; ++st)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float v = P[OFF_C2W + (32 * st + 8 * q + i) * 64 + n2];
+      const _Float16 hi = (_Float16)v;
+      b2h[st][i] = hi;
+      b2l[st][i] = (_Float16)(v - (float)hi);
+    }
   const float bias1 = P[OFF_C1B + n1], bias2 = P[OFF_C2B + n2];
 
-  // per-lane A-operand addresses (floats from the plane's start; the tap and
-  // channel step of each K step is an immediate offset).  conv1 positions
-  // run row-major over the group's 4 x 49 positions; conv2 positions are
-  // ordered (row, pooling window, position in the window), so each output
-  // lane's four values are one 2x2 window.
+  // per-lane A-fragment addresses (halves; a K step adds its tap offset).
+  // conv1 positions run row-major over the group's 4 x 49 positions; conv2
+  // positions are ordered (row, pooling window, position in the window), so
+  // each output lane's four values are one 2x2 window.
   auto tile1 = [&](int i) { return 4 * i + (w >> 1); };   // conv1 tile of slot i
   auto tile2 = [&](int i) { return 2 * i + (w >> 2); };   // conv2 tile of slot i
   int base1[T1];
-  bool ok1[T1];
 #pragma unroll
   for (int i = 0; i < T1; ++i) {
     const int m = tile1(i) * 16 + r16;
-    ok1[i] = tile1(i) < M1T && m < RG * 49;
-    const int rr = ok1[i] ? m / 49 : 0, p = ok1[i] ? m % 49 : 0;
-    base1[i] = rr * (CS1 * 81) + q * 81 + (p / 7) * 9 + p % 7;
+    const bool ok = tile1(i) < M1T && m < RG * 49;     // else a valid dummy row, dropped
+    const int rr = ok ? m / 49 : 0, p = ok ? m % 49 : 0;
+    base1[i] = (rr * 81 + (p / 7) * 9 + p % 7) * CP1;
   }
   int base2[T2];
   bool ok2[T2];
@@ -313,46 +344,48 @@ __global__ __launch_bounds__(NTHR) void lstm_act_kernel(const qqt_lstm_args a) {
     const int m = (ok2[i] ? tile2(i) : 0) * 16 + r16;
     const int rr = m / 36, wi = (m % 36) / 4, s4 = m % 4;
     const int y = 2 * (wi / 3) + (s4 >> 1), x = 2 * (wi % 3) + (s4 & 1);
-    base2[i] = rr * (32 * 81) + q * 81 + y * 9 + x;
+    base2[i] = (rr * 81 + y * 9 + x) * CP2;
   }
 
-  // zero the bordered planes (borders and unused channel slots stay zero)
-  // and the pooled rows past ROWS (read by the last head tile, dropped)
-  for (int i = tid; i < RG * CS1 * 81; i += NTHR) (&s.t.in[0][0])[i] = 0.0f;
-  for (int i = tid; i < RG * 32 * 81; i += NTHR) (&s.t.a1[0][0])[i] = 0.0f;
+  // zero the planes (borders and unused channel slots stay zero) and the
+  // pooled rows past ROWS (read by the last head tile, dropped)
+  for (int i = tid; i < RG * 81 * CP1 / 2; i += NTHR) reinterpret_cast<uint32_t*>(&s.t.in[0][0])[i] = 0u;
+  for (int i = tid; i < RG * 81 * CP2 / 2; i += NTHR) {
+    reinterpret_cast<uint32_t*>(&s.t.a1h[0][0])[i] = 0u;
+    reinterpret_cast<uint32_t*>(&s.t.a1l[0][0])[i] = 0u;
+  }
   for (int i = ROWS * LD_POOL + tid; i < HT * 16 * LD_POOL; i += NTHR) s.pooled[i] = 0.0f;
   __syncthreads();
 
-  auto stage = [&](int g) {   // the group's windows, float16 -> float32 planes
+  auto stage = [&](int g) {   // the group's float16 windows into the position-major planes
     const int n = cin * 49;
     for (int i = tid; i < RG * n; i += NTHR) {
       const int rr = i / n, rem = i % n, ci = rem / 49, p = rem % 49;
       const int row = min(row0 + g * RG + rr, a.batch - 1);   // past the batch: computed, dropped
-      s.t.in[rr][ci * 81 + (p / 7 + 1) * 9 + p % 7 + 1] =
-          h2f(a.local[(size_t)row * a.local_stride + rem]);
+      s.t.in[rr][((p / 7 + 1) * 9 + p % 7 + 1) * CP1 + ci] =
+          a.local[(size_t)row * a.local_stride + rem];
     }
   };
   stage(0);
 #pragma unroll 1
   for (int g = 0; g < ROWS / RG; ++g) {
     __syncthreads();   // in[] holds group g; a1 is free
-    // conv1 (C -> 32, 3x3, pad 1) + ReLU into a1's interior
+    // conv1 (C -> 32, 3x3, pad 1) + ReLU into a1's interior, split hi / lo
     {
       floatx4 acc[T1];
 #pragma unroll
       for (int i = 0; i < T1; ++i) acc[i] = floatx4{0, 0, 0, 0};
-      const float* ib = &s.t.in[0][0];
+      const uint16_t* ib = &s.t.in[0][0];
 #pragma unroll
-      for (int ks = 0; ks < K1 / 4; ++ks) {
-        const int off = 4 * (ks % 4) * 81 + tapoff(ks / 4);
+      for (int st = 0; st < KS1; ++st) {
+        // taps 2st + q/2 (the padding tap 9 reads tap 8 against zero weights)
+        const int off = tapoff(min(2 * st + (q >> 1), 8)) * CP1 + 8 * (q & 1);
 #pragma unroll
         for (int i = 0; i < T1; ++i) {
-          const float av = ok1[i] ? ib[base1[i] + off] : 0.0f;
-          acc[i] = mfma4(av, b1[ks], acc[i]);
+          const half8 av = *reinterpret_cast<const half8*>(ib + base1[i] + off);
+          acc[i] = mfma16(av, b1h[st], acc[i]);
+          acc[i] = mfma16(av, b1l[st], acc[i]);
         }
-        // keep the scheduler from hoisting every K step's loads (register
-        // pressure): loads run at most one K step ahead
-        if (ks % 2 == 1) __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
       for (int i = 0; i < T1; ++i) {
@@ -361,7 +394,11 @@ __global__ __launch_bounds__(NTHR) void lstm_act_kernel(const qqt_lstm_args a) {
           const int m = tile1(i) * 16 + 4 * q + j;
           if (tile1(i) < M1T && m < RG * 49) {
             const int rr = m / 49, p = m % 49;
-            s.t.a1[rr][n1 * 81 + (p / 7 + 1) * 9 + p % 7 + 1] = fmaxf(acc[i][j] + bias1, 0.0f);
+            const float v = fmaxf(acc[i][j] + bias1, 0.0f);
+            const _Float16 hi = (_Float16)v;
+            const int at = ((p / 7 + 1) * 9 + p % 7 + 1) * CP2 + n1;
+            s.t.a1h[rr][at] = __half_as_ushort(hi);
+            s.t.a1l[rr][at] = __half_as_ushort((_Float16)(v - (float)hi));
           }
         }
       }
@@ -373,13 +410,19 @@ __global__ __launch_bounds__(NTHR) void lstm_act_kernel(const qqt_lstm_args a) {
       floatx4 acc[T2];
 #pragma unroll
       for (int i = 0; i < T2; ++i) acc[i] = floatx4{0, 0, 0, 0};
-      const float* ab = &s.t.a1[0][0];
+      const uint16_t* hb = &s.t.a1h[0][0];
+      const uint16_t* lb = &s.t.a1l[0][0];
 #pragma unroll
-      for (int ks = 0; ks < K2 / 4; ++ks) {
-        const int off = 4 * (ks % 8) * 81 + tapoff(ks / 8);
+      for (int st = 0; st < KS2; ++st) {
+        const int off = tapoff(st) * CP2 + 8 * q;
 #pragma unroll
-        for (int i = 0; i < T2; ++i) acc[i] = mfma4(ab[base2[i] + off], b2[ks], acc[i]);
-        if (ks % 2 == 1) __builtin_amdgcn_sched_barrier(0);
+        for (int i = 0; i < T2; ++i) {
+          const half8 ah = *reinterpret_cast<const half8*>(hb + base2[i] + off);
+          const half8 al = *reinterpret_cast<const half8*>(lb + base2[i] + off);
+          acc[i] = mfma16(ah, b2h[st], acc[i]);
+          acc[i] = mfma16(ah, b2l[st], acc[i]);
+          acc[i] = mfma16(al, b2h[st], acc[i]);
+        }
       }
       // lane (q, j) of tile t holds window 4 t + q at its position j:
       // max_j relu(v_j + b) = relu(max_j v_j + b)
