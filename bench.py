@@ -1236,6 +1236,12 @@ def main_cnn(args, torch, dev):
 LSTM_MACS = (49 * 126 * 32 + 49 * 288 * 64 + 576 * 128 + 60 * 64 + 64 * 32 + 5 * 16 + 16 * 8
              + 168 * 256 + 384 * 512 + 128 * 192 + 64 * 8)
 LSTM_FLOP_PER_ROW = 2 * LSTM_MACS
+# MACs the kernel issues per row on float16 MFMA: conv1 over 196 of 208
+# tile positions x 160 K (two products, the windows being float16), conv2 at
+# the 36 pooled positions x 288 K and the head (three products each).
+LSTM_ISSUED_MACS = (2 * (208 / 4) * 160 * 32 + 3 * 36 * 288 * 64
+                    + 3 * (576 * 128 + 64 * 64 + 64 * 32 + 2 * 32 * 16 + 192 * 256 + 384 * 512
+                           + 128 * 192 + 192 * 16))
 MFMA_F32_PEAK = 157.3
 # Algorithmic bytes of the feature kernel per env (one player): the packed
 # cells (169 x 4 B), the player rows (2 x 48 B), t (4 B), the 14 x 7 x 7
@@ -1384,8 +1390,12 @@ def main_lstm(args, torch, dev):
         "lstm_act_kernel": {"us": us["lstm_act_kernel"], "bound": "mfma",
                             "achieved": LSTM_FLOP_PER_ROW * n / (us["lstm_act_kernel"] * 1e-6)
                             / 1e12,
-                            "peak": MFMA_F32_PEAK, "unit": "TFLOP/s",
-                            "flop_per_row": LSTM_FLOP_PER_ROW},
+                            "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                            "flop_per_row": LSTM_FLOP_PER_ROW,
+                            "executed_tflops": 2 * LSTM_ISSUED_MACS * n
+                            / (us["lstm_act_kernel"] * 1e-6) / 1e12,
+                            "f32_equivalent_frac": LSTM_FLOP_PER_ROW * n
+                            / (us["lstm_act_kernel"] * 1e-6) / 1e12 / MFMA_F32_PEAK},
         "lstm_feat_kernel": {"us": us["lstm_feat_kernel"], "bound": "hbm",
                              "achieved": LSTM_FEAT_BYTES_PER_ENV * n
                              / (us["lstm_feat_kernel"] * 1e-6) / 1e9,
@@ -1425,7 +1435,9 @@ def main_lstm(args, torch, dev):
                   "(step+obs+features+lstm act+bot), 1 MI355X",
         "value": n * K / el, "unit": "env-steps/s", "n_gpus": 1, "steps": K, "warmup": W,
         "ms_per_step": el / K * 1e3, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f32 sim, bot and network (f32 MFMA), f16 features",
+        "vs_baseline": None,
+        "dtype": "f32 sim and bot; network as float16 MFMA products of hi/lo-split float32 "
+                 "operands (f32 accumulate, float32 accuracy); f16 features",
         "data": "synthetic: template maps from Philox draws, the reference's lstm init "
                 "(orthogonal, torch.nn.LSTM uniform)",
         "config": {"workload": "lstm learner (player 0: 7x7 local features + LSTM, state "
@@ -1435,7 +1447,9 @@ def main_lstm(args, torch, dev):
         "roofline": {"kernel": "lstm_act_kernel", "bound": d["bound"],
                      "achieved": round(d["achieved"], 3), "peak": d["peak"], "unit": d["unit"],
                      "frac": round(d["frac"], 5), "traffic": None,
-                     "note": "algorithmic FLOP over the dense float32 MFMA peak"},
+                     "note": "algorithmic FLOP of the reference network over the dense float16 "
+                             "MFMA peak (the products run there, three per float32-accurate "
+                             "product); executed_tflops and f32_equivalent_frac in kernels"},
         "torch_gpu_baseline": {"act_ms_player0": round(ref_ms, 3),
                                "hip_act_ms_player0": round(hip_ms, 4),
                                "speedup": round(ref_ms / hip_ms, 2),

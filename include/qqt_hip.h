@@ -459,7 +459,7 @@ typedef struct qqt_lstm_args {
   float* value_out;           /* [slot] or NULL */
   float* logits_out;          /* [B][8]: 5 move, 2 bomb, value; or NULL */
 } qqt_lstm_args;
-#define QQT_LSTM_PARAMS 374272
+#define QQT_LSTM_PARAMS 378880
 int qqt_lstm_act(const qqt_lstm_args* args, void* stream);
 
 /* Dispatch timing for benchmark harnesses (no counterpart in the reference:

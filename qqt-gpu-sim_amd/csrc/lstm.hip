@@ -60,7 +60,8 @@ constexpr int KS2 = K2 / 32;              // conv2 K steps of 32 (one tap each)
 constexpr int CP1 = 24, CP2 = 40;
 constexpr int FEAT = 576;                 // 64 x 3 x 3 pooled features
 constexpr int XIN = 168;                  // 128 + 32 + 8 fusion inputs
-constexpr int XINP = 176;                 // padded to whole 16-k groups
+constexpr int XINP = 192;                 // padded to whole 32-k MFMA steps
+constexpr int GK = 32;                    // glob layers' K, padded likewise
 constexpr int G4 = 512;                   // 4 x 128 gates
 constexpr int NW = 8;                     // wavefronts per workgroup (two per SIMD)
 constexpr int NTHR = 64 * NW;
@@ -70,20 +71,22 @@ constexpr int T1 = (M1T + 3) / 4;         // conv1 tiles per wavefront (four per
 constexpr int M2T = RG * 36 / 16;         // conv2 pooled-position tiles per group (9)
 constexpr int T2 = (M2T + 1) / 2;         // conv2 tiles per wavefront (two per column tile)
 static_assert(RG * 36 % 16 == 0, "whole conv2 tiles per group");
-// LDS row strides of the 16-row activation blocks: 4 mod 64 floats, so the
-// 16 rows x 4 k of one A-operand read land in 64 distinct banks
-constexpr int LD_POOL = 580, LD_XIN = 196, LD_XH = 388, LD_HN = 132, LD_HD = 196, LD_R = 68,
-              LD_G1 = 20, LD_GLB = 20, LD_LG = 16;
+// row pitches (halves) of the head's 16-row float16 planes: an odd number
+// of 16-byte chunks, so the 16 rows of one 16-byte A read land in distinct
+// bank groups
+constexpr int PP = 584, PX = 200, PXH = 392, PHN = 136, PHD = 200, PR = 72, PG = 40;
+constexpr int LD_LG = 16;                 // float32 outputs
 
 // packed parameter block (floats; built by qqtsim/policy.py pack_lstm): the
-// convolutions k-major [in][out], the head's layers as MFMA B fragments
-// [column tile][K / 16][64 lanes][4] (value i of lane 16 q + r in group g of
-// tile t = W[16 g + 4 q + i][16 t + r])
+// convolutions k-major [in][out]; each head layer W [K][N] as float16 hi
+// and lo planes of K N / 2 floats each, in MFMA B fragments
+// [column tile][K / 32][64 lanes][8 halves] (half i of lane 16 q + r in step
+// s of tile t = W[32 s + 8 q + i][16 t + r])
 constexpr int OFF_C1W = 0, OFF_C1B = OFF_C1W + K1 * 32, OFF_C2W = OFF_C1B + 64,
               OFF_C2B = OFF_C2W + K2 * 64, OFF_FCW = OFF_C2B + 64, OFF_FCB = OFF_FCW + FEAT * 128,
               OFF_R1W = OFF_FCB + 128, OFF_R1B = OFF_R1W + 64 * 64, OFF_R2W = OFF_R1B + 64,
-              OFF_R2B = OFF_R2W + 64 * 32, OFF_G1W = OFF_R2B + 64, OFF_G1B = OFF_G1W + 16 * 16,
-              OFF_G2W = OFF_G1B + 64, OFF_G2B = OFF_G2W + 16 * 16, OFF_FUW = OFF_G2B + 64,
+              OFF_R2B = OFF_R2W + 64 * 32, OFF_G1W = OFF_R2B + 64, OFF_G1B = OFF_G1W + GK * 16,
+              OFF_G2W = OFF_G1B + 64, OFF_G2B = OFF_G2W + GK * 16, OFF_FUW = OFF_G2B + 64,
               OFF_FUB = OFF_FUW + XINP * 256, OFF_LW = OFF_FUB + 256, OFF_LB = OFF_LW + 384 * G4,
               OFF_HW = OFF_LB + G4, OFF_HB = OFF_HW + 128 * 192, OFF_OW = OFF_HB + 192,
               OFF_OB = OFF_OW + 192 * 16, N_PARAMS = OFF_OB + 64;
@@ -205,43 +208,52 @@ struct __align__(16) ActLds {
       uint16_t a1h[RG][81 * CP2];   // conv1 output [position][channel], float16 hi part
       uint16_t a1l[RG][81 * CP2];   // and lo part (v - hi)
     } t;
-    struct {                        // head: one 16-row tile
-      float xin[16 * LD_XIN];       // fc | rel | glob outputs
-      float xh[16 * LD_XH];         // fused | previous h
-      float hn[16 * LD_HN];         // new h
-      float hd[16 * LD_HD];         // heads' hidden layers
-      float r1[16 * LD_R], g1[16 * LD_G1];
-      float rel[16 * LD_R];         // rel inputs (60 used)
-      float glb[16 * LD_GLB];       // glob inputs (5 used)
+    struct {                        // head: one 16-row tile; float16 [hi plane][lo plane]
+      uint16_t xin[2][16 * PX];     // fc | rel | glob outputs (192 K)
+      uint16_t xh[2][16 * PXH];     // fused | previous h (384 K)
+      uint16_t hn[2][16 * PHN];     // new h
+      uint16_t hd[2][16 * PHD];     // heads' hidden layers
+      uint16_t r1[2][16 * PR], g1[2][16 * PG];
+      uint16_t rel[16 * PR];        // rel inputs (float16 already; 60 used)
+      uint16_t glb[16 * PG];        // glob inputs (5 used)
       float lg[16 * LD_LG];         // outputs
     } h;
   };
-  float pooled[HT * 16 * LD_POOL];  // 576 pooled features per row
+  uint16_t pooled[2][HT * 16 * PP]; // 576 pooled features per row, hi and lo
 };
 
-// acc[t] += A (16 rows in LDS, row stride lda floats, 16-byte aligned) x B
-// over K (a multiple of 16), B's column tile tile(t) read from its MFMA
-// fragments F.  Per 16-k group: one 16-byte A read (row r, k = 16 g + 4 q ..
-// + 3) and one 16-byte fragment read per tile feed four K steps.
-template <int NT, class Tile>
-__device__ __forceinline__ void gemmf(floatx4 (&acc)[NT], const float* A, int lda, const float* F,
-                                      int K, Tile tile, int lane) {
+// acc[t] += A (16 rows of float16 hi / lo planes in LDS, row pitch lda
+// halves) x B over K (a multiple of 32), B's column tile tile(t) read from
+// its float16 hi / lo fragments F (N columns).  Per K step: one 16-byte A
+// read per plane (row r, k = 32 s + 8 q .. + 7) and one 16-byte fragment
+// read per plane and tile feed hi*hi + hi*lo + lo*hi (LO = false: the A
+// values are float16 exactly, hi*hi + hi*lo).
+template <int NT, bool LO, class Tile>
+__device__ __forceinline__ void gemmh(floatx4 (&acc)[NT], const uint16_t* Ah, const uint16_t* Al,
+                                      int lda, const float* F, int K, int N, Tile tile, int lane) {
   const int r = lane & 15, q = lane >> 4;
-  const int kg = K / 16;
-  const float4* Fv = reinterpret_cast<const float4*>(F);
-  const float* Ar = A + r * lda + 4 * q;
-#pragma unroll 4
-  for (int g = 0; g < kg; ++g) {
-    const float4 av = *reinterpret_cast<const float4*>(Ar + 16 * g);
-    float4 bv[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) bv[t] = Fv[((size_t)tile(t) * kg + g) * 64 + lane];
+  const int ks = K / 32;
+  const half8* Fh = reinterpret_cast<const half8*>(F);
+  const half8* Fl = reinterpret_cast<const half8*>(F + (size_t)K * N / 2);
+  const uint16_t* ah = Ah + r * lda + 8 * q;
+  const uint16_t* al = Al + r * lda + 8 * q;
+#pragma unroll 2
+  for (int st = 0; st < ks; ++st) {
+    const half8 xh = *reinterpret_cast<const half8*>(ah + 32 * st);
+    half8 xl;
+    if constexpr (LO) xl = *reinterpret_cast<const half8*>(al + 32 * st);
+    half8 bh[NT], bl[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      acc[t] = mfma4(av.x, bv[t].x, acc[t]);
-      acc[t] = mfma4(av.y, bv[t].y, acc[t]);
-      acc[t] = mfma4(av.z, bv[t].z, acc[t]);
-      acc[t] = mfma4(av.w, bv[t].w, acc[t]);
+      const size_t f = ((size_t)tile(t) * ks + st) * 64 + lane;
+      bh[t] = Fh[f];
+      bl[t] = Fl[f];
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      acc[t] = mfma16(xh, bh[t], acc[t]);
+      acc[t] = mfma16(xh, bl[t], acc[t]);
+      if constexpr (LO) acc[t] = mfma16(xl, bh[t], acc[t]);
     }
   }
 }
@@ -251,6 +263,28 @@ struct Tiles {
   int t0;
   __device__ int operator()(int t) const { return t0 + t; }
 };
+
+// float32 v as float16 hi + lo into a plane pair
+__device__ __forceinline__ void put_split(uint16_t* h, uint16_t* l, int at, float v) {
+  const _Float16 hi = (_Float16)v;
+  h[at] = __half_as_ushort(hi);
+  l[at] = __half_as_ushort((_Float16)(v - (float)hi));
+}
+
+// bias + optional ReLU of the output tiles, split into a float16 plane pair
+template <int NT>
+__device__ __forceinline__ void store16h(const floatx4 (&acc)[NT], uint16_t* Dh, uint16_t* Dl,
+                                         int ldd, int n0, const float* bias, int lane, int ncols) {
+  const int c = lane & 15, q = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int n = n0 + 16 * t + c;
+    if (n >= ncols) continue;
+    const float b = bias[n];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) put_split(Dh, Dl, (4 * q + j) * ldd + n, fmaxf(acc[t][j] + b, 0.0f));
+  }
+}
 
 // bias + optional ReLU of the output tiles into a row-major LDS block
 template <int NT>
@@ -354,7 +388,7 @@ __global__ __launch_bounds__(NTHR) void lstm_act_kernel(const qqt_lstm_args a) {
     reinterpret_cast<uint32_t*>(&s.t.a1h[0][0])[i] = 0u;
     reinterpret_cast<uint32_t*>(&s.t.a1l[0][0])[i] = 0u;
   }
-  for (int i = ROWS * LD_POOL + tid; i < HT * 16 * LD_POOL; i += NTHR) s.pooled[i] = 0.0f;
+  for (int i = ROWS * PP + tid; i < HT * 16 * PP; i += NTHR) s.pooled[0][i] = s.pooled[1][i] = 0;
   __syncthreads();
 
   auto stage = [&](int g) {   // the group's float16 windows into the position-major planes
@@ -431,7 +465,8 @@ __global__ __launch_bounds__(NTHR) void lstm_act_kernel(const qqt_lstm_args a) {
         if (!ok2[i]) continue;
         const int wdx = 4 * tile2(i) + q, rr = wdx / 9, w9 = wdx % 9;
         const float mx = fmaxf(fmaxf(acc[i][0], acc[i][1]), fmaxf(acc[i][2], acc[i][3]));
-        s.pooled[(g * RG + rr) * LD_POOL + n2 * 9 + w9] = fmaxf(mx + bias2, 0.0f);
+        put_split(s.pooled[0], s.pooled[1], (g * RG + rr) * PP + n2 * 9 + w9,
+                  fmaxf(mx + bias2, 0.0f));
       }
     }
   }
@@ -440,57 +475,60 @@ __global__ __launch_bounds__(NTHR) void lstm_act_kernel(const qqt_lstm_args a) {
   for (int ht = 0; ht < HT; ++ht) {
     __syncthreads();   // trunk done / previous tile's buffers consumed
     const int hr0 = row0 + 16 * ht;
-    // rel / glob inputs, previous hidden state (zero for reset envs)
+    // rel / glob inputs (float16 bits as they are), previous hidden state
+    // (zero for reset envs) split hi / lo, and the K padding of the layers
     for (int i = tid; i < 16 * 64; i += NTHR) {
       const int r = i / 64, k = i % 64, row = min(hr0 + r, a.batch - 1);
-      s.h.rel[r * LD_R + k] = k < MAX_T * 6 ? h2f(a.rel[(size_t)row * a.rel_stride + k]) : 0.0f;
+      s.h.rel[r * PR + k] = k < MAX_T * 6 ? a.rel[(size_t)row * a.rel_stride + k] : (uint16_t)0;
     }
-    for (int i = tid; i < 16 * 16; i += NTHR) {
-      const int r = i / 16, k = i % 16, row = min(hr0 + r, a.batch - 1);
-      s.h.glb[r * LD_GLB + k] = k < GLOB ? h2f(a.glob[(size_t)row * a.glob_stride + k]) : 0.0f;
-      if (k < XINP - XIN) s.h.xin[r * LD_XIN + XIN + k] = 0.0f;   // fusion K padding
+    for (int i = tid; i < 16 * GK; i += NTHR) {
+      const int r = i / GK, k = i % GK, row = min(hr0 + r, a.batch - 1);
+      s.h.glb[r * PG + k] = k < GLOB ? a.glob[(size_t)row * a.glob_stride + k] : (uint16_t)0;
+      if (k >= 16) s.h.g1[0][r * PG + k] = s.h.g1[1][r * PG + k] = 0;      // glob2 K padding
+      if (k < XINP - XIN) s.h.xin[0][r * PX + XIN + k] = s.h.xin[1][r * PX + XIN + k] = 0;
     }
     for (int i = tid; i < 16 * HID; i += NTHR) {
       const int r = i / HID, k = i % HID, row = min(hr0 + r, a.batch - 1);
       const bool zero = a.reset && a.reset[row / a.rows_per_env];
-      s.h.xh[r * LD_XH + 256 + k] = zero ? 0.0f : a.h[(size_t)row * HID + k];
+      put_split(s.h.xh[0], s.h.xh[1], r * PXH + 256 + k, zero ? 0.0f : a.h[(size_t)row * HID + k]);
     }
     // Linear(576, 128) + ReLU: 8 column tiles, one per wavefront
     {
       floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
-      gemmf<1>(acc, s.pooled + 16 * ht * LD_POOL, LD_POOL, P + OFF_FCW, FEAT, Tiles{w}, lane);
-      store16<1>(acc, s.h.xin, LD_XIN, 16 * w, P + OFF_FCB, true, lane, HID);
+      gemmh<1, true>(acc, s.pooled[0] + 16 * ht * PP, s.pooled[1] + 16 * ht * PP, PP, P + OFF_FCW,
+                     FEAT, HID, Tiles{w}, lane);
+      store16h<1>(acc, s.h.xin[0], s.h.xin[1], PX, 16 * w, P + OFF_FCB, lane, HID);
     }
     __syncthreads();
     // rel 60 -> 64 (wavefronts 0-3), glob 5 -> 16 (wavefront 4)
     if (w < 4) {
       floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
-      gemmf<1>(acc, s.h.rel, LD_R, P + OFF_R1W, 64, Tiles{w}, lane);
-      store16<1>(acc, s.h.r1, LD_R, 16 * w, P + OFF_R1B, true, lane, 64);
+      gemmh<1, false>(acc, s.h.rel, s.h.rel, PR, P + OFF_R1W, 64, 64, Tiles{w}, lane);
+      store16h<1>(acc, s.h.r1[0], s.h.r1[1], PR, 16 * w, P + OFF_R1B, lane, 64);
     } else {
       if (w == 4) {
         floatx4 ag[1] = {floatx4{0, 0, 0, 0}};
-        gemmf<1>(ag, s.h.glb, LD_GLB, P + OFF_G1W, 16, Tiles{0}, lane);
-        store16<1>(ag, s.h.g1, LD_G1, 0, P + OFF_G1B, true, lane, 16);
+        gemmh<1, false>(ag, s.h.glb, s.h.glb, PG, P + OFF_G1W, GK, 16, Tiles{0}, lane);
+        store16h<1>(ag, s.h.g1[0], s.h.g1[1], PG, 0, P + OFF_G1B, lane, 16);
       }
     }
     __syncthreads();
     // rel 64 -> 32 (wavefronts 0, 1), glob 16 -> 8 (wavefront 2)
     if (w < 2) {
       floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
-      gemmf<1>(acc, s.h.r1, LD_R, P + OFF_R2W, 64, Tiles{w}, lane);
-      store16<1>(acc, s.h.xin + HID, LD_XIN, 16 * w, P + OFF_R2B, true, lane, 32);
+      gemmh<1, true>(acc, s.h.r1[0], s.h.r1[1], PR, P + OFF_R2W, 64, 32, Tiles{w}, lane);
+      store16h<1>(acc, s.h.xin[0] + HID, s.h.xin[1] + HID, PX, 16 * w, P + OFF_R2B, lane, 32);
     } else if (w == 2) {
       floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
-      gemmf<1>(acc, s.h.g1, LD_G1, P + OFF_G2W, 16, Tiles{0}, lane);
-      store16<1>(acc, s.h.xin + HID + 32, LD_XIN, 0, P + OFF_G2B, true, lane, 8);
+      gemmh<1, true>(acc, s.h.g1[0], s.h.g1[1], PG, P + OFF_G2W, GK, 16, Tiles{0}, lane);
+      store16h<1>(acc, s.h.xin[0] + HID + 32, s.h.xin[1] + HID + 32, PX, 0, P + OFF_G2B, lane, 8);
     }
     __syncthreads();
     // fusion Linear(168, 256) + ReLU: 16 tiles, two per wavefront
     {
       floatx4 acc[2] = {floatx4{0, 0, 0, 0}, floatx4{0, 0, 0, 0}};
-      gemmf<2>(acc, s.h.xin, LD_XIN, P + OFF_FUW, XINP, Tiles{2 * w}, lane);
-      store16<2>(acc, s.h.xh, LD_XH, 32 * w, P + OFF_FUB, true, lane, 256);
+      gemmh<2, true>(acc, s.h.xin[0], s.h.xin[1], PX, P + OFF_FUW, XINP, 256, Tiles{2 * w}, lane);
+      store16h<2>(acc, s.h.xh[0], s.h.xh[1], PXH, 32 * w, P + OFF_FUB, lane, 256);
     }
     __syncthreads();
     // LSTM gates [fused | h] (384) x W (384 x 512) + b.  Wavefront w takes
@@ -501,7 +539,8 @@ __global__ __launch_bounds__(NTHR) void lstm_act_kernel(const qqt_lstm_args a) {
       floatx4 acc[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) acc[t] = floatx4{0, 0, 0, 0};
-      gemmf<4>(acc, s.h.xh, LD_XH, P + OFF_LW, 384, [&](int t) { return 8 * t + w; }, lane);
+      gemmh<4, true>(acc, s.h.xh[0], s.h.xh[1], PXH, P + OFF_LW, 384, G4,
+                     [&](int t) { return 8 * t + w; }, lane);
       {
         const int u = 16 * w + r16;
         const float bi = P[OFF_LB + u], bf = P[OFF_LB + HID + u];
@@ -516,7 +555,7 @@ __global__ __launch_bounds__(NTHR) void lstm_act_kernel(const qqt_lstm_args a) {
           if (mine && !(a.reset && a.reset[row / a.rows_per_env])) cp = a.c[(size_t)row * HID + u];
           const float c2 = fg * cp + ig * gg;
           const float h2 = og * tanhf(c2);
-          s.h.hn[r * LD_HN + u] = h2;
+          put_split(s.h.hn[0], s.h.hn[1], r * PHN + u, h2);
           if (mine) {
             a.c[(size_t)row * HID + u] = c2;
             a.h[(size_t)row * HID + u] = h2;
@@ -529,18 +568,19 @@ __global__ __launch_bounds__(NTHR) void lstm_act_kernel(const qqt_lstm_args a) {
     // 0-3 and one per wavefront 4-7
     if (w < 4) {
       floatx4 acc[2] = {floatx4{0, 0, 0, 0}, floatx4{0, 0, 0, 0}};
-      gemmf<2>(acc, s.h.hn, LD_HN, P + OFF_HW, HID, Tiles{2 * w}, lane);
-      store16<2>(acc, s.h.hd, LD_HD, 32 * w, P + OFF_HB, true, lane, 3 * HEAD);
+      gemmh<2, true>(acc, s.h.hn[0], s.h.hn[1], PHN, P + OFF_HW, HID, 3 * HEAD, Tiles{2 * w}, lane);
+      store16h<2>(acc, s.h.hd[0], s.h.hd[1], PHD, 32 * w, P + OFF_HB, lane, 3 * HEAD);
     } else {
       floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
-      gemmf<1>(acc, s.h.hn, LD_HN, P + OFF_HW, HID, Tiles{8 + (w - 4)}, lane);
-      store16<1>(acc, s.h.hd, LD_HD, 128 + 16 * (w - 4), P + OFF_HB, true, lane, 3 * HEAD);
+      gemmh<1, true>(acc, s.h.hn[0], s.h.hn[1], PHN, P + OFF_HW, HID, 3 * HEAD, Tiles{8 + (w - 4)},
+                     lane);
+      store16h<1>(acc, s.h.hd[0], s.h.hd[1], PHD, 128 + 16 * (w - 4), P + OFF_HB, lane, 3 * HEAD);
     }
     __syncthreads();
     // output layer 192 -> 8 (block diagonal, 16 padded columns): wavefront 0
     if (w == 0) {
       floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
-      gemmf<1>(acc, s.h.hd, LD_HD, P + OFF_OW, 3 * HEAD, Tiles{0}, lane);
+      gemmh<1, true>(acc, s.h.hd[0], s.h.hd[1], PHD, P + OFF_OW, 3 * HEAD, 16, Tiles{0}, lane);
       store16<1>(acc, s.h.lg, LD_LG, 0, P + OFF_OB, false, lane, 16);
     }
     __syncthreads();

@@ -516,36 +516,42 @@ class HipCnnActorCritic(HipActorCritic):
 
 
 # ---------------------------------------------------------------- lstm arch
-LSTM_PARAMS = 374272       # QQT_LSTM_PARAMS
+LSTM_PARAMS = 378880       # QQT_LSTM_PARAMS
 # blocks of the packed parameters in order: (key, rows K, columns N, layout)
-# with layout "k" = k-major [K][N], "f" = MFMA B fragments (see _lstm_frag),
-# "v" = a vector in a block of N floats (qqt-gpu-sim_amd/csrc/lstm.hip OFF_*)
+# with layout "k" = float32 k-major [K][N], "h" = float16 hi / lo MFMA
+# fragments (see _lstm_frag16), "v" = a float32 vector in a block of N
+# (qqt-gpu-sim_amd/csrc/lstm.hip OFF_*)
 _LSTM_BLOCKS = (("c1w", 144, 32, "k"), ("c1b", 1, 64, "v"), ("c2w", 288, 64, "k"),
-                ("c2b", 1, 64, "v"), ("fcw", 576, 128, "f"), ("fcb", 1, 128, "v"),
-                ("r1w", 64, 64, "f"), ("r1b", 1, 64, "v"), ("r2w", 64, 32, "f"),
-                ("r2b", 1, 64, "v"), ("g1w", 16, 16, "f"), ("g1b", 1, 64, "v"),
-                ("g2w", 16, 16, "f"), ("g2b", 1, 64, "v"), ("fuw", 176, 256, "f"),
-                ("fub", 1, 256, "v"), ("lw", 384, 512, "f"), ("lb", 1, 512, "v"),
-                ("hw", 128, 192, "f"), ("hb", 1, 192, "v"), ("ow", 192, 16, "f"),
+                ("c2b", 1, 64, "v"), ("fcw", 576, 128, "h"), ("fcb", 1, 128, "v"),
+                ("r1w", 64, 64, "h"), ("r1b", 1, 64, "v"), ("r2w", 64, 32, "h"),
+                ("r2b", 1, 64, "v"), ("g1w", 32, 16, "h"), ("g1b", 1, 64, "v"),
+                ("g2w", 32, 16, "h"), ("g2b", 1, 64, "v"), ("fuw", 192, 256, "h"),
+                ("fub", 1, 256, "v"), ("lw", 384, 512, "h"), ("lb", 1, 512, "v"),
+                ("hw", 128, 192, "h"), ("hb", 1, 192, "v"), ("ow", 192, 16, "h"),
                 ("ob", 1, 64, "v"))
 
 
-def _lstm_frag(w: torch.Tensor) -> torch.Tensor:
-    """k-major [K][N] (K, N multiples of 16) -> MFMA B fragments for
-    v_mfma_f32_16x16x4_f32 in groups of four K steps: value i of lane
-    16 q + r in group g of column tile t is W[16 g + 4 q + i][16 t + r], so a
-    lane's four B values of a group are one 16-byte load and pair with the
-    four consecutive A values (row r, k = 16 g + 4 q .. + 3) of one LDS read."""
+def _lstm_frag16(w: torch.Tensor) -> torch.Tensor:
+    """float32 k-major [K][N] (K a multiple of 32, N of 16) -> K N float32
+    words holding two float16 planes, hi = fp16(w) then lo = fp16(w - hi),
+    each in the B-fragment order of v_mfma_f32_16x16x32_f16: half i of lane
+    16 q + r in K step s of column tile t is W[32 s + 8 q + i][16 t + r]."""
     k, n = w.shape
-    x = w.reshape(k // 16, 4, 4, n // 16, 16)            # [g][q][i][t][r]
-    return x.permute(3, 0, 1, 4, 2).reshape(-1)           # [t][g][q][r][i]
+    hi = w.half()
+    lo = (w - hi.float()).half()
+
+    def frag(x):
+        return x.reshape(k // 32, 4, 8, n // 16, 16).permute(3, 0, 1, 4, 2).reshape(-1)
+
+    return torch.cat([frag(hi), frag(lo)]).contiguous().view(torch.float32)
 
 
 def pack_lstm(params: dict, obs_channels: int = 14) -> torch.Tensor:
     """One float32 block of QQT_LSTM_PARAMS values for qqt_lstm_act from an
     lstm ActorCritic state_dict (train/model.py:103-120, 140-153): every
     weight transposed to k-major [in][out], zero-padded to the block's shape
-    and, for the head's layers, stored as MFMA B fragments (`_lstm_frag`).
+    and, for the head's layers, stored as float16 hi / lo MFMA B fragments
+    (`_lstm_frag16`).
     Convolution rows are tap-major: k = (ky * 3 + kx) * S + in_channel
     with S = 16 channel slots for conv1 (14 used, 144 rows) and S = 32 for
     conv2 (288 rows); the LSTM block stacks W_ih^T over W_hh^T with the bias
@@ -601,7 +607,7 @@ def pack_lstm(params: dict, obs_channels: int = 14) -> torch.Tensor:
         else:
             blk = torch.zeros((rows, cols))
             blk[:v.shape[0], :v.shape[1]] = v
-            out[off:off + rows * cols] = blk.reshape(-1) if layout == "k" else _lstm_frag(blk)
+            out[off:off + rows * cols] = blk.reshape(-1) if layout == "k" else _lstm_frag16(blk)
         off += rows * cols
     if off != LSTM_PARAMS:
         raise AssertionError("packed block size")

@@ -6,8 +6,8 @@ in zero-bordered 9x9 grids with 16 channel slots, tap-major K for both
 convolutions (k = tap * slots + channel, tap offset (tap / 3) * 9 + tap % 3),
 conv1's output written back into a bordered grid, conv2 evaluated only at
 the 36 positions the 2x2 pool reads, ordered by pooling window, and pooled
-as relu(max + bias), the k-major and MFMA-fragment blocks with their
-padding, the stacked LSTM
+as relu(max + bias), the k-major blocks and the float16 hi / lo MFMA
+fragments (read back as hi + lo) with their padding, the stacked LSTM
 block and the block-diagonal output layer.  Run over the reference's frames
 (tests/golden/lstm.npz, train/model.py:176-185 with the hidden state carried
 and reset) it must reproduce the reference's logits, values and (h, c);
@@ -29,7 +29,7 @@ from golden_io import lstm_params
 from qqtsim.policy import _LSTM_BLOCKS, LSTM_PARAMS, lstm_block_offsets, pack_lstm
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-_LOGICAL_ROWS = {"g1w": 8, "fuw": 168}      # rows past these are K padding
+_LOGICAL_ROWS = {"g1w": 8, "g2w": 16, "fuw": 168}      # rows past these are K padding
 
 
 @pytest.fixture(scope="module")
@@ -61,8 +61,11 @@ def _emulate(block, local, rel, glob, h, c):
             return flat
         if lay == "k":
             return flat.reshape(r, cc)
-        # MFMA fragments [t][g][q][r][i] -> W[16 g + 4 q + i][16 t + r]
-        m = flat.reshape(cc // 16, r // 16, 4, 16, 4).transpose(1, 2, 4, 0, 3).reshape(r, cc)
+        # float16 hi / lo planes of MFMA fragments [t][s][q][r][i] ->
+        # W[32 s + 8 q + i][16 t + r] = hi + lo
+        halves = block[off[k]:off[k] + r * cc].contiguous().view(torch.float16).double().numpy()
+        planes = halves.reshape(2, cc // 16, r // 32, 4, 16, 8).transpose(0, 2, 3, 5, 1, 4)
+        m = planes.reshape(2, r, cc).sum(axis=0)
         return m[:_LOGICAL_ROWS.get(k, r)]
 
     relu = lambda x: np.maximum(x, 0.0)  # noqa: E731
