@@ -10,27 +10,31 @@
 // observation row (L2-hot: the tick kernel wrote it).
 //
 // lstm_act_kernel (train/model.py:103-120, 176-185, 198-214): one workgroup
-// of four wavefronts per 16 rows, float32 arithmetic throughout on
-// v_mfma_f32_16x16x4_f32 (A: 16 rows x 4 K, B: 4 K x 16 columns; lane l
-// supplies A[l%16][l/16] and B[l/16][l%16] and holds D[4(l/16)+j][l%16]).
+// of eight wavefronts (two per SIMD) per 16 or 24 rows.  Every product runs
+// on v_mfma_f32_16x16x32_f16 with float32 accuracy: float32 operands split
+// into float16 hi + lo, each product taken as hi*hi + hi*lo + lo*hi with
+// float32 accumulation (the float16 features need no lo part).  A: lane l
+// holds row l%16, k = 8(l/16) .. + 7; B: k = 8(l/16) .. + 7 of column l%16;
+// D: lane l holds D[4(l/16)+j][l%16].
 // * Trunk, four rows at a time: the windows sit in LDS as zero-bordered 9 x 9
-//   grids per channel; each 3x3 convolution is an implicit GEMM with K
-//   ordered tap-major (k = tap * channels + channel), so a K step's A operand
-//   is one LDS read at a per-lane base plus an immediate offset.  Each
-//   wavefront holds its output-column tile of both weight matrices in
+//   grids with a position's channels contiguous, so with K ordered tap-major
+//   (k = tap * channels + channel) one K step of 32 is one 16-byte read per
+//   lane at a per-lane base plus an immediate.  Each wavefront holds the hi
+//   / lo fragments of its output-column tile of both convolutions in
 //   registers for the whole launch.  conv1 runs over the 4 x 49 positions
-//   and writes a second bordered grid; conv2 runs only at the 36 positions
-//   per row that the 2x2 max pool reads (7 -> 3 drops row and column 6),
-//   ordered so that each output lane's four values are one pooling window:
-//   the pool is a max over the lane's accumulators.
-// * Head, 16 rows together (M = 16): Linear(576,128), the rel and glob
+//   and writes a second bordered grid (hi and lo planes); conv2 runs only at
+//   the 36 positions per row that the 2x2 max pool reads (7 -> 3 drops row
+//   and column 6), ordered so that each output lane's four values are one
+//   pooling window: the pool is a max over the lane's accumulators.
+// * Head, 16 rows at a time (M = 16): Linear(576,128), the rel and glob
 //   MLPs, the fusion layer, the LSTM gates (K = 256 inputs + 128 hidden, N =
 //   512, gate order i, f, g, o as torch.nn.LSTM stores them; each wavefront
-//   takes the same 32 hidden units of all four gates, so the cell update
+//   takes the same 16 hidden units of all four gates, so the cell update
 //   happens in registers), the three heads and the block-diagonal output
-//   layer, from k-major weight blocks read from L2 (each weight once per 16
-//   rows), activations in LDS with row strides of 4 mod 64 floats (bank
-//   conflict free A reads); then masked sampling, one thread per row.
+//   layer.  Weights come from L2 as hi / lo B fragments (16 bytes per lane
+//   per K step), activations from LDS hi / lo planes whose row pitch is an
+//   odd number of 16-byte chunks (the 16 rows of one read hit distinct bank
+//   groups); then masked sampling, one thread per row.
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -690,8 +694,15 @@ int qqt_lstm_act(const qqt_lstm_args* a, void* stream) {
     return QQT_E_ARG;
   }
   hipStream_t st = (hipStream_t)stream;
-  const int blocks = (a->batch + 15) / 16;
-  QQT_LAUNCH(QQT_KERNEL_LSTM, lstm::lstm_act_kernel<16>, dim3(blocks), dim3(lstm::NTHR), st, *a);
+  // 16 or 24 rows per workgroup (one workgroup per CU), whichever needs
+  // fewer rounds of the 256 CUs at its cost per workgroup: 24 rows take
+  // ~1.8x the time of 16 (1.5x the trunk, a second head tile)
+  const int blocks16 = (a->batch + 15) / 16, blocks24 = (a->batch + 23) / 24;
+  const int rounds16 = (blocks16 + 255) / 256, rounds24 = (blocks24 + 255) / 256;
+  if (rounds24 * 18 < rounds16 * 10)
+    QQT_LAUNCH(QQT_KERNEL_LSTM, lstm::lstm_act_kernel<24>, dim3(blocks24), dim3(lstm::NTHR), st, *a);
+  else
+    QQT_LAUNCH(QQT_KERNEL_LSTM, lstm::lstm_act_kernel<16>, dim3(blocks16), dim3(lstm::NTHR), st, *a);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     snprintf(g_err, sizeof(g_err), "lstm act launch failed: %s", hipGetErrorString(err));

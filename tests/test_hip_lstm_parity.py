@@ -325,3 +325,27 @@ def test_lstm_collect_fills_the_buffer(dev):
                               (troll.h[None] * keep, troll.c[None] * keep))
     assert torch.equal(lv, v)
     assert torch.equal(roll.h, troll.h)
+
+
+def test_lstm_large_batch_workgroup_shape(dev):
+    """5000 rows take the 24-row workgroups (one round of the CUs), 300 rows
+    the 16-row ones: both against the oracle in float64, and the rows they
+    share equal bit for bit (the per-row arithmetic does not depend on the
+    row's place in a workgroup)."""
+    from oracle.policy import lstm_forward
+    from qqtsim import HipLstmActorCritic
+
+    net = HipLstmActorCritic(device=dev, seed=4)
+    f, hid = _random_features(5000, 8, dev)
+    ml, bl, v, (h, c) = net.forward(f, 0, hid)
+    sub = slice(2000, 2300)
+    ml2, bl2, v2, (h2, c2) = net.forward(tuple(t[sub] for t in f), 0, tuple(t[:, sub] for t in hid))
+    for x, y in ((ml[sub], ml2), (bl[sub], bl2), (v[sub], v2), (h[:, sub], h2), (c[:, sub], c2)):
+        assert torch.equal(x, y)
+    rml, rbl, rv, (rh, rc) = lstm_forward(net.state_dict(), *(t.cpu() for t in f),
+                                          tuple(t[0].cpu() for t in hid), dtype=torch.float64)
+    worst = 0.0
+    for a, b in ((ml, rml), (bl, rbl), (v, rv), (h[0], rh), (c[0], rc)):
+        worst = max(worst, float((a.cpu().double() - b).abs().max()))
+    print(f"lstm 5000 rows: max |err| {worst:.2e}")
+    assert worst <= ATOL
