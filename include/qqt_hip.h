@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 15
+#define QQT_ABI_VERSION 16
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -332,8 +332,26 @@ typedef struct qqt_ppo_args {
   float* ln_part;             /* [ceil(B/16)][4][128]: dgamma1, dbeta1, dgamma2, dbeta2 */
   float* stats_part;          /* [ceil(B/16)][5]: sums of -min(surrogates), 0.5 max(value
                                  errors), entropy, old_logp - logp, clipped indicator */
+  float* bias_part;           /* [ceil(B/16)][456] or NULL: column sums of dz1 (128), dz2
+                                 (128), dhy (192), dl (8) over each 16-row block */
+  float* dz1_absmax_part;     /* [ceil(B/16)][128] or NULL: max |dz1| per column and block */
 } qqt_ppo_args;
 int qqt_ppo_grad(const qqt_ppo_args* args, void* stream);
+
+/* Row gather for the PPO update's minibatches (train/ppo.py:406-408,
+ * buf.obs[mb] with the flattened buffer): destination row r = source row
+ * index[r], row_words 4-byte words each.  Rows whose index lies outside
+ * [0, src_rows) are left untouched. */
+typedef struct qqt_gather_args {
+  int32_t n;                  /* destination rows */
+  int32_t row_words;          /* 4-byte words per row */
+  int64_t src_rows;           /* rows in src */
+  int64_t src_stride, dst_stride;   /* words between rows */
+  const uint32_t* src;
+  uint32_t* dst;
+  const int64_t* index;       /* [n] */
+} qqt_gather_args;
+int qqt_gather_rows(const qqt_gather_args* args, void* stream);
 
 /* Forward of the cnn actor/critic (train/model.py:79-96, 186-190) with
  * optional masked factored sampling.  Replaces ActorCritic.act / forward for

@@ -345,6 +345,49 @@ __global__ __launch_bounds__(T) void ppo_grad_kernel(const qqt_ppo_args a) {
       a.dhy[o] = s.dhy[r][c];
     }
   }
+  // ---- this block's column sums of dz1, dz2, dhy, dl (the bias gradients'
+  // partials) and max |dz1| per column (the weight-gradient kernel's scale)
+  constexpr int NB = 2 * H + HY + 8;
+  if (a.bias_part) {
+    for (int c = t; c < NB; c += T) {
+      float sum = 0.0f;
+      for (int r = 0; r < nrows; ++r)
+        sum += c < H ? s.z[r][c]
+                     : c < 2 * H ? s.g[r][c - H] : c < 2 * H + HY ? s.dhy[r][c - 2 * H]
+                                                                : s.dl[r][c - 2 * H - HY];
+      a.bias_part[(size_t)blockIdx.x * NB + c] = sum;
+    }
+  }
+  if (a.dz1_absmax_part && t < H) {
+    float m = 0.0f;
+    for (int r = 0; r < nrows; ++r) m = fmaxf(m, fabsf(s.z[r][t]));
+    a.dz1_absmax_part[(size_t)blockIdx.x * H + t] = m;
+  }
+}
+
+// One wavefront per destination row: all of the row's loads are issued
+// before its stores, 4-byte words coalesced across the lanes.
+__global__ __launch_bounds__(256) void gather_rows_kernel(const qqt_gather_args a) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= a.n) return;
+  const int64_t src = a.index[row];
+  if (src < 0 || src >= a.src_rows) return;
+  const uint32_t* s = a.src + src * a.src_stride;
+  uint32_t* d = a.dst + (int64_t)row * a.dst_stride;
+  constexpr int U = 8;
+  for (int w0 = 0; w0 < a.row_words; w0 += 64 * U) {
+    uint32_t v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int w = w0 + 64 * u + lane;
+      v[u] = w < a.row_words ? s[w] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int w = w0 + 64 * u + lane;
+      if (w < a.row_words) d[w] = v[u];
+    }
+  }
 }
 
 }  // namespace ppo
@@ -375,6 +418,29 @@ int qqt_ppo_grad(const qqt_ppo_args* a, void* stream) {
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     snprintf(g_err, sizeof(g_err), "ppo grad launch failed: %s", hipGetErrorString(err));
+    return QQT_E_LAUNCH;
+  }
+  return QQT_OK;
+}
+
+int qqt_gather_rows(const qqt_gather_args* a, void* stream) {
+  using namespace qqt;
+  g_err[0] = 0;
+  if (!a || !a->src || !a->dst || !a->index) {
+    snprintf(g_err, sizeof(g_err), "qqt_gather_rows: null pointer argument");
+    return QQT_E_ARG;
+  }
+  if (a->n < 0 || a->row_words <= 0 || a->src_rows < 0 || a->src_stride < a->row_words ||
+      a->dst_stride < a->row_words) {
+    snprintf(g_err, sizeof(g_err), "qqt_gather_rows: bad sizes or strides");
+    return QQT_E_ARG;
+  }
+  if (a->n == 0) return QQT_OK;
+  hipLaunchKernelGGL(ppo::gather_rows_kernel, dim3((a->n + 3) / 4), dim3(256), 0,
+                     (hipStream_t)stream, *a);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    snprintf(g_err, sizeof(g_err), "gather launch failed: %s", hipGetErrorString(err));
     return QQT_E_LAUNCH;
   }
   return QQT_OK;

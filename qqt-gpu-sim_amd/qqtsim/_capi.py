@@ -14,7 +14,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 
 from ._build import LIB
 
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 MODE_STEP, MODE_OBSERVE, MODE_RESET, MODE_PROBE, MODE_FLUSH = 0, 1, 2, 3, 4
 MAP_PILLARS, MAP_OPEN, MAP_REFERENCE = 0, 1, 2
@@ -90,7 +90,8 @@ class PpoArgsC(ctypes.Structure):
         (n, _vp) for n in ("z1", "ln1_w", "ln1_b", "w1", "w1t", "b1", "ln2_w", "ln2_b", "wh",
                            "wht", "bh", "wf", "bf", "actions", "move_mask", "bomb_mask",
                            "old_logp", "adv", "ret", "old_val", "dz1", "h1", "dz2", "h2", "hy",
-                           "dhy", "dl", "ln_part", "stats_part")]
+                           "dhy", "dl", "ln_part", "stats_part", "bias_part",
+                           "dz1_absmax_part")]
 
 
 class CnnArgsC(ctypes.Structure):
@@ -104,6 +105,12 @@ class CnnArgsC(ctypes.Structure):
                            "ln2b", "c3w", "c3w_lo", "c3b", "ln3w", "ln3b", "s0p", "s0b", "s1w", "s1b", "s3p", "s3b", "s4w", "s4b", "hp",
                            "hb", "fw", "fb", "move_mask", "bomb_mask", "uniforms", "actions", "actions_i8",
                            "logp_out", "value_out", "logits_out")]
+
+
+class GatherArgsC(ctypes.Structure):
+    _fields_ = [("n", _i32), ("row_words", _i32)] + [
+        (n, ctypes.c_int64) for n in ("src_rows", "src_stride", "dst_stride")] + [
+        (n, _vp) for n in ("src", "dst", "index")]
 
 
 class LstmFeatArgsC(ctypes.Structure):
@@ -163,6 +170,8 @@ def lib():
         L.qqt_lstm_features.restype = ctypes.c_int
         L.qqt_lstm_features.argtypes = [ctypes.POINTER(SimConfigC), ctypes.POINTER(LstmFeatArgsC),
                                         _vp]
+        L.qqt_gather_rows.restype = ctypes.c_int
+        L.qqt_gather_rows.argtypes = [ctypes.POINTER(GatherArgsC), _vp]
         L.qqt_lstm_act.restype = ctypes.c_int
         L.qqt_lstm_act.argtypes = [ctypes.POINTER(LstmArgsC), _vp]
         L.qqt_timing_arm.restype = ctypes.c_int

@@ -40,7 +40,7 @@ def _declared_functions():
 
 def test_header_declares_the_entry_points():
     assert _declared_functions() == ["qqt_abi_version", "qqt_bot_act", "qqt_cnn_act", "qqt_gae",
-                                     "qqt_l1_grad", "qqt_l1_grad_noalloc",
+                                     "qqt_gather_rows", "qqt_l1_grad", "qqt_l1_grad_noalloc",
                                      "qqt_l1_grad_workspace_floats",
                                      "qqt_last_error", "qqt_lstm_act", "qqt_lstm_features",
                                      "qqt_mlp_act", "qqt_ppo_grad", "qqt_tick",
@@ -95,7 +95,8 @@ def test_struct_layouts_match_the_header(tmp_path):
                "qqt_mlp_args": _capi.MlpArgsC, "qqt_bot_args": _capi.BotArgsC,
                "qqt_gae_args": _capi.GaeArgsC, "qqt_l1_grad_args": _capi.L1GradArgsC,
                "qqt_ppo_args": _capi.PpoArgsC, "qqt_cnn_args": _capi.CnnArgsC,
-               "qqt_lstm_feat_args": _capi.LstmFeatArgsC, "qqt_lstm_args": _capi.LstmArgsC}
+               "qqt_lstm_feat_args": _capi.LstmFeatArgsC, "qqt_lstm_args": _capi.LstmArgsC,
+               "qqt_gather_args": _capi.GatherArgsC}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "qqt_hip.h"',
              'int main(void) {']
     for cname, cls in structs.items():
@@ -422,3 +423,23 @@ def test_integration_doc_lists_every_source():
     doc = open(os.path.join(os.path.dirname(os.path.dirname(__file__)), "INTEGRATION.md")).read()
     missing = [s for s in _build.SOURCES if f"csrc/{s}" not in doc]
     assert missing == [], missing
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(src=None), "null pointer"),
+    (dict(index=None), "null pointer"),
+    (dict(n=-1), "bad sizes"),
+    (dict(row_words=0), "bad sizes"),
+    (dict(src_stride=1182), "bad sizes"),
+    (dict(dst_stride=1182), "bad sizes"),
+])
+def test_gather_rejects_bad_arguments(lib, kw, msg):
+    from qqtsim import _capi
+
+    a = _capi.GatherArgsC()
+    a.n, a.row_words, a.src_rows, a.src_stride, a.dst_stride = 4, 1183, 10, 1183, 1183
+    a.src, a.dst, a.index = 0x10000, 0x20000, 0x30000
+    for k, v in kw.items():
+        setattr(a, k, v)
+    assert lib.qqt_gather_rows(a, None) == -1
+    assert msg in lib.qqt_last_error().decode()

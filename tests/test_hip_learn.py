@@ -261,3 +261,26 @@ def test_fused_ppo_grads_match_autograd(dev):
         err = float((p.grad - want[k]).norm() / want[k].norm().clamp_min(1e-12))
         assert err <= 2e-4, (k, err)
     assert float((st - want_st).abs().max()) <= 1e-5 * max(1.0, float(want_st.abs().max()))
+
+
+def test_gather_rows_matches_torch_indexing(dev):
+    """qqt_gather_rows (the PPO minibatch's observation rows) equals torch's
+    row indexing bit for bit, repeated and out-of-order indices included;
+    rows with an index outside the source are left untouched."""
+    from qqtsim import _capi
+    from qqtsim.learn import _gather_rows
+
+    g = torch.Generator().manual_seed(4)
+    n, b = 3001, 2048
+    x = (torch.randn((n, 14, 13, 13), generator=g) * 3).half().to(dev)
+    idx = torch.randint(0, n, (b,), generator=g).to(dev)
+    idx[:30] = idx[30]
+    assert torch.equal(_gather_rows(x, idx), x[idx])
+    out = torch.full((3, 1183), 7, dtype=torch.int32, device=dev)
+    bad = torch.tensor([5, -1, n], dtype=torch.int64, device=dev)
+    a = _capi.GatherArgsC()
+    a.n, a.row_words, a.src_rows, a.src_stride, a.dst_stride = 3, 1183, n, 1183, 1183
+    a.src, a.dst, a.index = x.data_ptr(), out.data_ptr(), bad.data_ptr()
+    _capi.check(_capi.lib().qqt_gather_rows(a, _capi.stream_handle(dev)))
+    assert torch.equal(out[0], x[5].reshape(-1).view(torch.int32))
+    assert bool((out[1:] == 7).all())
