@@ -335,6 +335,13 @@ typedef struct qqt_ppo_args {
   float* bias_part;           /* [ceil(B/16)][456] or NULL: column sums of dz1 (128), dz2
                                  (128), dhy (192), dl (8) over each 16-row block */
   float* dz1_absmax_part;     /* [ceil(B/16)][128] or NULL: max |dz1| per column and block */
+  int32_t t_chunk;            /* 0: dz2, dhy, dl row-major.  A multiple of 16: written
+                                 chunk-transposed, element (row r, column c) of an
+                                 n-column output at ((r / t_chunk) n + c) t_chunk +
+                                 r % t_chunk (each chunk [n][t_chunk], ready for batched
+                                 products over the rows; the caller sizes the buffers to
+                                 whole chunks and zeroes the last chunk's tail) */
+  int32_t reserved;
 } qqt_ppo_args;
 int qqt_ppo_grad(const qqt_ppo_args* args, void* stream);
 

@@ -142,6 +142,13 @@ __device__ __forceinline__ void ln_backward(float (*G)[HP], const float (*xh)[HP
 
 // Per-workgroup sums over the rows of dgamma = dy xh and dbeta = dy, where
 // dy = G (before ln_backward overwrote it) masked by h > 0.
+// Index of (row r, column c) of an n-column output: row-major, or in
+// t_chunk-row chunks stored [chunk][n][t_chunk].
+__device__ __forceinline__ size_t out_at(int64_t r, int c, int n, int t_chunk) {
+  return t_chunk > 0 ? ((size_t)(r / t_chunk) * n + c) * t_chunk + (size_t)(r % t_chunk)
+                     : (size_t)r * n + c;
+}
+
 __device__ __forceinline__ void ln_param_sums(const float (*G)[HP], const float (*xh)[HP],
                                               const float (*h)[HP], float* out_g, float* out_b) {
   const int c = threadIdx.x;
@@ -279,7 +286,7 @@ __global__ __launch_bounds__(T) void ppo_grad_kernel(const qqt_ppo_args a) {
       st[3] = a.old_logp[g] - logp;
       st[4] = fabsf(ratio - 1.0f) > a.clip_eps ? 1.0f : 0.0f;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) a.dl[g * 8 + k] = dl[k];
+      for (int k = 0; k < 8; ++k) a.dl[out_at(g, k, 8, a.t_chunk)] = dl[k];
     }
 #pragma unroll
     for (int k = 0; k < 8; ++k) s.dl[r][k] = dl[k];
@@ -332,18 +339,23 @@ __global__ __launch_bounds__(T) void ppo_grad_kernel(const qqt_ppo_args a) {
     if (r < nrows) {
       const size_t o = (size_t)(row0 + r) * H + c;
       a.dz1[o] = s.z[r][c];
-      a.dz2[o] = s.g[r][c];
       a.h1[o] = s.h1[r][c];
       a.h2[o] = s.h2[r][c];
     }
   }
   for (int i = t; i < R * HY; i += T) {
     const int r = i / HY, c = i % HY;
-    if (r < nrows) {
-      const size_t o = (size_t)(row0 + r) * HY + c;
-      a.hy[o] = s.hy[r][c];
-      a.dhy[o] = s.dhy[r][c];
-    }
+    if (r < nrows) a.hy[(size_t)(row0 + r) * HY + c] = s.hy[r][c];
+  }
+  // dz2 and dhy in the caller's layout (rows fastest, so chunk-transposed
+  // stores are 16 consecutive floats)
+  for (int i = t; i < R * H; i += T) {
+    const int r = i % R, c = i / R;
+    if (r < nrows) a.dz2[out_at(row0 + r, c, H, a.t_chunk)] = s.g[r][c];
+  }
+  for (int i = t; i < R * HY; i += T) {
+    const int r = i % R, c = i / R;
+    if (r < nrows) a.dhy[out_at(row0 + r, c, HY, a.t_chunk)] = s.dhy[r][c];
   }
   // ---- this block's column sums of dz1, dz2, dhy, dl (the bias gradients'
   // partials) and max |dz1| per column (the weight-gradient kernel's scale)
@@ -409,7 +421,8 @@ int qqt_ppo_grad(const qqt_ppo_args* a, void* stream) {
   }
   const uintptr_t al = (uintptr_t)a->z1 | (uintptr_t)a->w1 | (uintptr_t)a->w1t | (uintptr_t)a->b1 |
                        (uintptr_t)a->wh | (uintptr_t)a->wht | (uintptr_t)a->bh;
-  if (a->batch <= 0 || (al & 15) || !(a->clip_eps >= 0.0f)) {
+  if (a->batch <= 0 || (al & 15) || !(a->clip_eps >= 0.0f) || a->t_chunk < 0 ||
+      a->t_chunk % R) {
     snprintf(g_err, sizeof(g_err), "qqt_ppo_grad: bad batch, clip or 16-byte alignment");
     return QQT_E_ARG;
   }

@@ -91,7 +91,7 @@ class PpoArgsC(ctypes.Structure):
                            "wht", "bh", "wf", "bf", "actions", "move_mask", "bomb_mask",
                            "old_logp", "adv", "ret", "old_val", "dz1", "h1", "dz2", "h2", "hy",
                            "dhy", "dl", "ln_part", "stats_part", "bias_part",
-                           "dz1_absmax_part")]
+                           "dz1_absmax_part")] + [("t_chunk", _i32), ("reserved", _i32)]
 
 
 class CnnArgsC(ctypes.Structure):
