@@ -313,10 +313,15 @@ typedef struct qqt_ppo_args {
   float value_coef, entropy_coef;
   const float* z1;            /* [B][128] */
   const float *ln1_w, *ln1_b; /* [128] */
-  const float *w1, *w1t;      /* shared.3.weight [128][128] and its transpose */
+  const float *w1, *w1t;      /* shared.3.weight W1 [128 out][128 in] as k-major matrices
+                                 [K][N] for the products dh1 = dz2 W1 (K = out) and
+                                 z2 = h1 W1^T (K = in), each in MFMA fragments: value i
+                                 of lane l in 16-k group g of column tile t is
+                                 M[16 g + 4 (l / 16) + i][16 t + l % 16] */
   const float* b1;
   const float *ln2_w, *ln2_b;
-  const float *wh, *wht;      /* the heads' hidden layers stacked [192][128] and transpose */
+  const float *wh, *wht;      /* the heads' hidden layers stacked, Wh [192][128], likewise:
+                                 wh for dh2 = dhy Wh (K = 192), wht for hy = h2 Wh^T */
   const float* bh;            /* [192] */
   const float* wf;            /* [8][64]: move rows 0-4, bomb 5-6, critic 7 (each head's
                                  output layer over its own 64 hidden units) */

@@ -55,23 +55,32 @@ struct __align__(16) Lds {
   float stat[R][5];
 };
 
-// Y[r][n] = sum_k X[r][k] W[k][n] (+ bias[n]) for the 16 rows; W row-major
-// [K][N] in global memory, X and Y in LDS.  MFMA 16x16x4 f32: lane l feeds
-// A[l%16][k0 + l/16] and B[k0 + l/16][n0 + l%16] and holds D[4(l/16)+q][l%16].
-// Wavefront w takes column tiles w, w+4, ...
+// Y[r][n] = sum_k X[r][k] W[k][n] (+ bias[n]) for the 16 rows, X and Y in
+// LDS.  W [K][N] comes from global memory as MFMA fragments: value i of lane
+// l in group g of column tile t is W[16 g + 4(l/16) + i][16 t + l%16], so a
+// lane's four B values of a 16-k group are one 16-byte load, paired with its
+// four A values X[l%16][16 g + 4(l/16) .. + 3] (one 16-byte LDS read).  MFMA
+// 16x16x4 f32 holds D[4(l/16)+q][l%16] in lane l.  Wavefront w takes column
+// tiles w, w+8, ...
 template <int K, int N, int LDX, int LDY>
 __device__ __forceinline__ void gemm(const float (*X)[LDX], const float* __restrict__ W,
                                      const float* __restrict__ bias, float (*Y)[LDY]) {
-  constexpr int CT = N / 16;
+  constexpr int CT = N / 16, KG = K / 16;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int i16 = lane & 15, kq = lane >> 4;
+  const float4* F = reinterpret_cast<const float4*>(W);
   for (int ct = w; ct < CT; ct += T / 64) {
     const int col = 16 * ct + i16;
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 16
-    for (int k0 = 0; k0 < K; k0 += 4)
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(X[i16][k0 + kq], W[(size_t)(k0 + kq) * N + col],
-                                                 acc, 0, 0, 0);
+#pragma unroll 8
+    for (int g = 0; g < KG; ++g) {
+      const float4 av = *reinterpret_cast<const float4*>(&X[i16][16 * g + 4 * kq]);
+      const float4 bv = F[((size_t)ct * KG + g) * 64 + lane];
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, bv.x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, bv.y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, bv.z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, bv.w, acc, 0, 0, 0);
+    }
     const float b = bias ? bias[col] : 0.0f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) Y[4 * kq + q][col] = acc[q] + b;
