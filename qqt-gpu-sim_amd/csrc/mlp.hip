@@ -56,6 +56,8 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <type_traits>
+
 #include "qqt_common.h"
 #include "qqt_hip.h"
 
@@ -72,9 +74,9 @@ constexpr int NOUT = 8;            // 5 move + 2 bomb + 1 value
 // tiles over an XCD row block of 44 rows: 5632 rows make 128 row blocks x 2
 // players = 256 workgroups, one per CU (64-row blocks left 80 of the 256 CUs
 // idle and put a third more MFMA work on each busy one).  Forward batches
-// from MLP_BIG_ROWS rows take RT = 8 (128 rows), which streams W0 once per
-// 128 rows.
-constexpr int RT_SMALL = (XCD_ROWS + 15) / 16, RT_BIG = 8;
+// (no sampling) from MLP_BIG_ROWS rows go to mlp_fwd_kernel (256-row
+// workgroups, W0 streamed once per 256 rows).
+constexpr int RT_SMALL = (XCD_ROWS + 15) / 16;
 constexpr int MLP_BIG_ROWS = 1 << 16;
 constexpr int NTHR = 512;          // 8 wavefronts
 #ifndef QQT_MLP_PD
@@ -98,6 +100,8 @@ __device__ __forceinline__ half8 as_h8(uint4 v) {
   c.u = v;
   return c.h;
 }
+
+__device__ __forceinline__ half8 as_h8(u32x4 v) { return __builtin_bit_cast(half8, v); }
 
 // 32 bytes of a first-layer weight fragment (32-byte aligned in w0).
 __device__ __forceinline__ Frag16 load_b(const uint16_t* p) {
@@ -605,6 +609,363 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Large forward batches (no sampling): mlp_fwd_kernel.
+//
+// Workgroup = 8 wavefronts = FWD_ROWS = 256 rows of one player; wavefront w
+// owns row tiles 2w, 2w+1 (rows 32w .. 32w+31) with all 128 features, so
+// layer 1 needs no partial-sum exchange and the tail starts from the
+// accumulators.  Layer 1: the observation B fragments go straight from HBM
+// into registers (a lane's 16 halves of one 64-K block are 32 contiguous
+// bytes of its row, read as two 16-byte loads at the row's 4-byte
+// alignment).  Layer 1 walks K in steps of FWD_KPS = 1 block (128 bytes of
+// each of the 256 rows), loaded one step ahead; two-block steps and loads
+// two steps ahead were measured slower (4.19 M rows: 5.65 ms at one block,
+// 6.18 at two, 6.25 at four).  W0's 16 KB per K block is loaded by the
+// wavefront of each feature tile and shared through a double-buffered LDS
+// stage (planes [block][tile][lo|hi][lane][8]: a wavefront's 16-byte reads
+// are 1 KB contiguous, conflict-free).  One barrier per step.  The tail runs both
+// row tiles of a wavefront together, so every later-layer weight fragment
+// read from LDS feeds two products.
+constexpr int FWD_RT = 16, FWD_ROWS = 16 * FWD_RT;
+#ifndef QQT_FWD_KPS
+#define QQT_FWD_KPS 1
+#endif
+constexpr int FWD_KPS = QQT_FWD_KPS;    // K blocks per step
+constexpr int W0_BLOCK = 8 * 2 * 64 * 8;          // halves of one K block of W0 (16 KB)
+constexpr int W0_STAGE = FWD_KPS * W0_BLOCK;      // halves of one step's stage
+
+// [W0 stage 0 | W0 stage 1] during layer 1, then W1 (hi | lo) for layer 2,
+// then the head weights (hi | lo)
+constexpr int FWD_BIG = 2 * W0_STAGE > 2 * WH_HALVES ? 2 * W0_STAGE : 2 * WH_HALVES;
+struct __align__(16) FwdLds {
+  uint16_t big[FWD_BIG];
+  uint16_t wf[2 * WF_HALVES];
+  float vec[V_N];
+};
+static_assert(FWD_BIG >= 2 * W1_HALVES, "W1 reuses the stages");
+
+// acc[r][t] += W(tile t) h_r over KS K steps for R row tiles that share every
+// weight fragment read (layout as tail_gemm).
+template <int NT, int KS, int R>
+__device__ __forceinline__ void tail_gemm_rows(floatx4 (&acc)[R][NT], const uint16_t* a_hi,
+                                               const uint16_t* a_lo, const half8 (&bh)[R][KS],
+                                               const half8 (&bl)[R][KS], int lane) {
+  constexpr int G = NT < 2 ? NT : 2;
+  static_assert(NT % G == 0, "whole chunks");
+  constexpr int NG = NT / G, NC = KS * NG;
+  half8 fa[2][2][G];
+  auto fetch = [&](int c, half8 (&f)[2][G]) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int off = (((G * (c % NG) + g) * KS + c / NG) * 64 + lane) * 8;
+      f[0][g] = *reinterpret_cast<const half8*>(a_hi + off);
+      f[1][g] = *reinterpret_cast<const half8*>(a_lo + off);
+    }
+  };
+  fetch(0, fa[0]);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    if (c + 1 < NC) fetch(c + 1, fa[(c + 1) & 1]);
+    const int s = c / NG, t0 = G * (c % NG);
+    const half8 (&f)[2][G] = fa[c & 1];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r][t0 + g] = mfma(f[0][g], bh[r][s], acc[r][t0 + g]);
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r][t0 + g] = mfma(f[0][g], bl[r][s], acc[r][t0 + g]);
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r][t0 + g] = mfma(f[1][g], bh[r][s], acc[r][t0 + g]);
+  }
+}
+
+template <bool Z1>
+__global__ __launch_bounds__(NTHR) void mlp_fwd_kernel(const qqt_mlp_args a) {
+  constexpr int W1_CH = 2 * W1_HALVES / 8 / NTHR;
+  constexpr int WH_CH = 2 * WH_HALVES / 8 / NTHR;
+  constexpr int WF_CH = 2 * WF_HALVES / 8;
+  __shared__ FwdLds s;
+  const int nrb = (a.batch + FWD_ROWS - 1) / FWD_ROWS;
+  const int xcd = blockIdx.x & 7, seq = blockIdx.x >> 3;
+  const int slot = seq % a.npid;
+  const int rb = (seq / a.npid) * 8 + xcd;
+  if (rb >= nrb) return;                   // padding workgroup (uniform, before any barrier)
+  const int pid = a.npid == 2 ? slot : a.pid0;
+  const int row0 = rb * FWD_ROWS;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int r16 = lane & 15, q = lane >> 4;
+  const int oslots = a.out_slots > 0 ? a.out_slots : a.npid;
+  const int oslot = a.npid == 2 ? slot : a.out_slot;
+  uint16_t* const w1s = s.big;
+
+  auto vec_src = [&](int i) -> const float* {
+    return i < V_G1 ? a.b0 + (i - V_B0) : i < V_BE1 ? a.ln1_w + (i - V_G1)
+         : i < V_B1 ? a.ln1_b + (i - V_BE1) : i < V_G2 ? a.b1 + (i - V_B1)
+         : i < V_BE2 ? a.ln2_w + (i - V_G2) : i < V_BH ? a.ln2_b + (i - V_BE2)
+         : i < V_BF ? a.bh + (i - V_BH) : a.bf + (i - V_BF);
+  };
+  const int vi0 = threadIdx.x, vi1 = threadIdx.x + NTHR;
+  const float vv0 = *vec_src(vi0);
+  const float vv1 = vi1 < V_N ? *vec_src(vi1) : 0.0f;
+  auto plane_src = [](const uint16_t* hi, const uint16_t* lo, int halves, int c) {
+    const int per = halves / 8;
+    return c < per ? reinterpret_cast<const u32x4*>(hi) + c
+                   : reinterpret_cast<const u32x4*>(lo) + (c - per);
+  };
+
+  // ---------------- layer 1
+  const int nkb = a.kblocks0;
+  const int k0 = a.k0;
+  constexpr int KPS = FWD_KPS;
+  const int nsteps = (nkb + KPS - 1) / KPS, last_s = nsteps - 1;
+  // W0: wavefront w loads feature tile w of each K block (32 bytes per lane);
+  // blocks past the last (a step's padding) reload the last block, which
+  // meets all-zero observation halves
+  const uint16_t* const wsrc = a.w0 + (size_t)((pid * 8 + w) * nkb) * 64 * 16 + lane * 16;
+  auto load_w = [&](int st, u32x4 (&wr)[KPS][2]) {
+#pragma unroll
+    for (int b = 0; b < KPS; ++b) {
+      const u32x4* p =
+          reinterpret_cast<const u32x4*>(wsrc + (size_t)min(KPS * st + b, nkb - 1) * 64 * 16);
+      wr[b][0] = p[0];
+      wr[b][1] = p[1];
+    }
+  };
+  auto store_w = [&](const u32x4 (&wr)[KPS][2], int buf) {
+    u32x4* stg = reinterpret_cast<u32x4*>(s.big + buf * W0_STAGE);
+#pragma unroll
+    for (int b = 0; b < KPS; ++b) {
+      stg[((b * 8 + w) * 2 + 0) * 64 + lane] = wr[b][0];
+      stg[((b * 8 + w) * 2 + 1) * 64 + lane] = wr[b][1];
+    }
+  };
+  // x: row tile rt of this wavefront, row clamped to the batch (a ragged last
+  // block computes copies of the last row and drops them)
+  const uint16_t* xrow[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int r = min(row0 + 32 * w + 16 * rt + r16, a.batch - 1);
+    xrow[rt] = a.obs + (size_t)r * a.obs_stride;
+  }
+  // Chunk h (8 halves from k = 64kb + 16q + 8h) of this lane's rows.  Every
+  // step but the last reads whole chunks below k0 (its blocks end at or
+  // before 64 KPS (nsteps - 1) <= 64 (nkb - 1) < k0), at a per-lane base and
+  // compile-time offsets.  The last step reads each chunk from
+  // off = min(k, k0 - 8), which always ends inside the row, and, when it is
+  // used, shifts it down by (k - off) / 2 words with zeros shifted in, so
+  // halves at or past k0 (k0 is even: a word never straddles it) become zero
+  // (a step's padding block entirely).  (The shift is applied at use so that
+  // no load is waited on before its step.)
+  const uint16_t* const xlane[2] = {xrow[0] + 16 * q, xrow[1] + 16 * q};
+  auto chunk_off = [&](int kb, int h) { return min(64 * kb + 16 * q + 8 * h, k0 - 8); };
+  auto load_x = [&](int st, u32x4 (&xr)[KPS][2][2]) {
+    if (st < last_s) {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int b = 0; b < KPS; ++b)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            __builtin_memcpy(&xr[b][rt][h], xlane[rt] + 64 * (KPS * st + b) + 8 * h, 16);
+    } else {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int b = 0; b < KPS; ++b)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            __builtin_memcpy(&xr[b][rt][h], xrow[rt] + chunk_off(KPS * st + b, h), 16);
+    }
+  };
+  auto shifted = [&](int kb, int h, const u32x4& v) {
+    const int sh = min((64 * kb + 16 * q + 8 * h - chunk_off(kb, h)) >> 1, 4);
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t e = 0u;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (i + j < 4) e = sh == j ? v[i + j] : e;
+      o[i] = e;
+    }
+    return o;
+  };
+
+  floatx4 acc[2][8];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[rt][t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // W0 of a step is loaded before its observation chunks, so the wait for
+  // the W0 registers (stored to LDS one step later) leaves the next step's
+  // observation loads in flight
+  u32x4 xr[KPS][2][2];
+  u32x4 wr[KPS][2];
+  load_w(0, wr);
+  load_x(0, xr);
+  u32x4 wfv[2];
+  const int wc1 = threadIdx.x + NTHR;
+  if constexpr (!Z1) {
+    wfv[0] = *plane_src(a.wf, a.wf_lo, WF_HALVES, threadIdx.x);
+    wfv[1] = wc1 < WF_CH ? *plane_src(a.wf, a.wf_lo, WF_HALVES, wc1) : u32x4{0u, 0u, 0u, 0u};
+  }
+  s.vec[vi0] = vv0;
+  if (vi1 < V_N) s.vec[vi1] = vv1;
+  store_w(wr, 0);
+  if (last_s > 0) load_w(1, wr);
+  if constexpr (!Z1) {
+    reinterpret_cast<u32x4*>(s.wf)[threadIdx.x] = wfv[0];
+    if (wc1 < WF_CH) reinterpret_cast<u32x4*>(s.wf)[wc1] = wfv[1];
+  }
+  __syncthreads();
+
+  auto compute = [&](int st, const u32x4 (&xraw)[KPS][2][2], auto last) {
+#pragma unroll
+    for (int b = 0; b < KPS; ++b) {
+      const int kb = KPS * st + b;
+      const half8* stg = reinterpret_cast<const half8*>(s.big + (st & 1) * W0_STAGE + b * W0_BLOCK);
+      u32x4 x[2][2];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) x[rt][h] = last ? shifted(kb, h, xraw[b][rt][h]) : xraw[b][rt][h];
+#pragma unroll
+      for (int tp = 0; tp < 4; ++tp) {       // feature tiles 2tp, 2tp+1
+        half8 f[2][2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          f[u][0] = stg[((2 * tp + u) * 2 + 0) * 64 + lane];
+          f[u][1] = stg[((2 * tp + u) * 2 + 1) * 64 + lane];
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+              acc[rt][2 * tp + u] = mfma(f[u][h], as_h8(x[rt][h]), acc[rt][2 * tp + u]);
+      }
+    }
+  };
+
+  // Step st: its W0 stage is LDS buffer st & 1.  It computes, loads the next
+  // step's observation chunks, stores the next step's W0 (loaded one step
+  // earlier) to the other buffer and loads the W0 of the step after that.
+  for (int st = 0; st < last_s; ++st) {
+    compute(st, xr, std::false_type{});
+    load_x(st + 1, xr);
+    store_w(wr, (st + 1) & 1);
+    if (st + 2 <= last_s) load_w(st + 2, wr);
+    __syncthreads();
+  }
+  compute(last_s, xr, std::true_type{});
+  __syncthreads();   // every wavefront is past its last read of the W0 stages
+
+  if constexpr (Z1) {   // first layer only (the training forward): z1 = f + b0
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int row = 32 * w + 16 * rt + r16, orow = row0 + row;
+      if (orow < a.batch) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const floatx4 b = vec4(s.vec + V_B0, t, q);
+          *reinterpret_cast<float4*>(a.z1_out + (size_t)orow * HID + 16 * t + 4 * q) =
+              make_float4(acc[rt][t][0] + b[0], acc[rt][t][1] + b[1], acc[rt][t][2] + b[2],
+                          acc[rt][t][3] + b[3]);
+        }
+      }
+    }
+    return;
+  }
+
+  // ---------------- LayerNorm 1, layer 2, LayerNorm 2 on both row tiles.
+  // W1 goes over the W0 stages (every wavefront is past its last read of
+  // them: the loop ends with a barrier); its loads overlap LayerNorm 1.
+  {
+    u32x4 w1v[W1_CH];
+#pragma unroll
+    for (int c = 0; c < W1_CH; ++c)
+      w1v[c] = *plane_src(a.w1, a.w1_lo, W1_HALVES, threadIdx.x + NTHR * c);
+#pragma unroll
+    for (int c = 0; c < W1_CH; ++c) reinterpret_cast<u32x4*>(w1s)[threadIdx.x + NTHR * c] = w1v[c];
+  }
+  half8 hh[2][4], hl[2][4];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    floatx4 v[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) v[t] = acc[rt][t] + vec4(s.vec + V_B0, t, q);
+    ln_relu_split(v, s.vec + V_G1, s.vec + V_BE1, q, hh[rt], hl[rt]);
+  }
+  __syncthreads();
+  {
+    floatx4 v2[2][8];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) v2[rt][t] = vec4(s.vec + V_B1, t, q);
+    tail_gemm_rows<8, 4, 2>(v2, w1s, w1s + W1_HALVES, hh, hl, lane);
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) ln_relu_split(v2[rt], s.vec + V_G2, s.vec + V_BE2, q, hh[rt], hl[rt]);
+  }
+  // head weights over W1 once every wavefront is past layer 2
+  {
+    u32x4 whv[WH_CH];
+#pragma unroll
+    for (int i = 0; i < WH_CH; ++i) whv[i] = *plane_src(a.wh, a.wh_lo, WH_HALVES, threadIdx.x + NTHR * i);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < WH_CH; ++i) reinterpret_cast<u32x4*>(s.big)[threadIdx.x + NTHR * i] = whv[i];
+  }
+  __syncthreads();
+
+  // ---------------- heads: 128 -> 192 (+ bias, ReLU), then 192 -> 8 (block diagonal)
+  half8 yh[2][6], yl[2][6];
+  floatx4 o[2][1];
+  {
+    floatx4 a3[2][12];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int t = 0; t < 12; ++t) a3[rt][t] = vec4(s.vec + V_BH, t, q);
+    tail_gemm_rows<12, 4, 2>(a3, s.big, s.big + WH_HALVES, hh, hl, lane);
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int t = 0; t < 12; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          split_into(fmaxf(a3[rt][t][j], 0.0f), yh[rt][t >> 1], yl[rt][t >> 1], 4 * (t & 1) + j);
+  }
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) o[rt][0] = vec4(s.vec + V_BF, 0, q & 1);
+  tail_gemm_rows<1, 6, 2>(o, s.wf, s.wf + WF_HALVES, yh, yl, lane);
+
+  // outputs: lanes r (outputs 0-3) and r + 16 (outputs 4-7) of each row tile
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int orow = row0 + 32 * w + 16 * rt + r16;
+    if (q < 2 && orow < a.batch) {
+      const size_t oo = (size_t)orow * oslots + oslot;
+      if (a.logits_out) {
+        float* lo = a.logits_out + oo * NOUT + 4 * q;
+        if ((reinterpret_cast<uintptr_t>(a.logits_out) & 15u) == 0u)   // one 16-byte store
+          *reinterpret_cast<float4*>(lo) = make_float4(o[rt][0][0], o[rt][0][1], o[rt][0][2], o[rt][0][3]);
+        else
+#pragma unroll
+          for (int j = 0; j < 4; ++j) lo[j] = o[rt][0][j];
+      }
+      if (q == 1 && a.value_out) a.value_out[oo] = o[rt][0][3];
+    }
+  }
+}
+
 extern thread_local char g_err[512];
 
 }  // namespace qqt
@@ -645,19 +1006,20 @@ int qqt_mlp_act(const qqt_mlp_args* a, void* stream) {
   }
   // one workgroup per (row block, player); row blocks are dealt to the 8
   // XCDs round robin with both players' workgroups adjacent on one XCD.
-  // Large forward batches take 128-row blocks (W0 streamed once per 128
-  // rows); everything else XCD row blocks.
-  const bool big = !a->sample && a->batch >= MLP_BIG_ROWS;
-  const int rows_wg = big ? 16 * RT_BIG : XCD_ROWS;
+  // Large forward batches take the streaming kernel's 256-row blocks (W0
+  // streamed once per 256 rows); everything else XCD row blocks.
+  const bool big = !a->sample && a->batch >= MLP_BIG_ROWS && a->k0 >= 64;   // (the streaming
+  // kernel's boundary loads read the 8 halves before k0)
+  const int rows_wg = big ? FWD_ROWS : XCD_ROWS;
   const int nrb = (a->batch + rows_wg - 1) / rows_wg;
   const int blocks = ((nrb + 7) / 8) * 8 * a->npid;
   hipStream_t st = (hipStream_t)stream;
   if (a->z1_out && big)
-    QQT_LAUNCH(QQT_KERNEL_MLP, (mlp_act_kernel<RT_BIG, true>), dim3(blocks), dim3(NTHR), st, *a);
+    QQT_LAUNCH(QQT_KERNEL_MLP, mlp_fwd_kernel<true>, dim3(blocks), dim3(NTHR), st, *a);
   else if (a->z1_out)
     QQT_LAUNCH(QQT_KERNEL_MLP, (mlp_act_kernel<RT_SMALL, true>), dim3(blocks), dim3(NTHR), st, *a);
   else if (big)
-    QQT_LAUNCH(QQT_KERNEL_MLP, (mlp_act_kernel<RT_BIG, false>), dim3(blocks), dim3(NTHR), st, *a);
+    QQT_LAUNCH(QQT_KERNEL_MLP, mlp_fwd_kernel<false>, dim3(blocks), dim3(NTHR), st, *a);
   else
     QQT_LAUNCH(QQT_KERNEL_MLP, (mlp_act_kernel<RT_SMALL, false>), dim3(blocks), dim3(NTHR), st,
                *a);
