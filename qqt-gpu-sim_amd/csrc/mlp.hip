@@ -57,6 +57,7 @@
 #include <stdio.h>
 
 #include <type_traits>
+#include <utility>
 
 #include "qqt_common.h"
 #include "qqt_hip.h"
@@ -619,19 +620,27 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
 // into registers (a lane's 16 halves of one 64-K block are 32 contiguous
 // bytes of its row, read as two 16-byte loads at the row's 4-byte
 // alignment).  Layer 1 walks K in steps of FWD_KPS = 1 block (128 bytes of
-// each of the 256 rows), loaded one step ahead; two-block steps and loads
-// two steps ahead were measured slower (4.19 M rows: 5.65 ms at one block,
-// 6.18 at two, 6.25 at four).  W0's 16 KB per K block is loaded by the
-// wavefront of each feature tile and shared through a double-buffered LDS
-// stage (planes [block][tile][lo|hi][lane][8]: a wavefront's 16-byte reads
-// are 1 KB contiguous, conflict-free).  One barrier per step.  The tail runs both
-// row tiles of a wavefront together, so every later-layer weight fragment
-// read from LDS feeds two products.
+// each of the 256 rows), loaded FWD_PD = 1 step ahead.  Wider steps, deeper
+// rings and non-temporal observation loads were all measured slower
+// (4.19 M rows: 5.52 ms as built; two-block steps 6.08, rings of 2/3/4
+// steps 6.07/5.95/6.03, non-temporal loads 9.07; likely causes, not
+// measured: more in-flight observation lines of an XCD's 32 workgroups
+// crowd W0 out of its L2, and non-temporal loads lose the L2's merging of a
+// row's 16-byte requests into 128-byte lines).  W0's 16 KB per K block is
+// loaded by the wavefront of each feature tile and shared through a
+// double-buffered LDS stage (planes [block][tile][lo|hi][lane][8]: a
+// wavefront's 16-byte reads are 1 KB contiguous, conflict-free).  One
+// barrier per step.  The tail runs both row tiles of a wavefront together,
+// so every later-layer weight fragment read from LDS feeds two products.
 constexpr int FWD_RT = 16, FWD_ROWS = 16 * FWD_RT;
 #ifndef QQT_FWD_KPS
 #define QQT_FWD_KPS 1
 #endif
+#ifndef QQT_FWD_PD
+#define QQT_FWD_PD 1
+#endif
 constexpr int FWD_KPS = QQT_FWD_KPS;    // K blocks per step
+constexpr int FWD_PD = QQT_FWD_PD;      // steps of loads in flight (register ring depth)
 constexpr int W0_BLOCK = 8 * 2 * 64 * 8;          // halves of one K block of W0 (16 KB)
 constexpr int W0_STAGE = FWD_KPS * W0_BLOCK;      // halves of one step's stage
 
@@ -682,6 +691,12 @@ __device__ __forceinline__ void tail_gemm_rows(floatx4 (&acc)[R][NT], const uint
 #pragma unroll
       for (int r = 0; r < R; ++r) acc[r][t0 + g] = mfma(f[1][g], bh[r][s], acc[r][t0 + g]);
   }
+}
+
+// f(std::integral_constant<int, J>) for each J of the sequence, in order.
+template <int... J, class F>
+__device__ __forceinline__ void for_each_index(std::integer_sequence<int, J...>, F&& f) {
+  (f(std::integral_constant<int, J>{}), ...);
 }
 
 template <bool Z1>
@@ -802,13 +817,22 @@ __global__ __launch_bounds__(NTHR) void mlp_fwd_kernel(const qqt_mlp_args a) {
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc[rt][t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // W0 of a step is loaded before its observation chunks, so the wait for
-  // the W0 registers (stored to LDS one step later) leaves the next step's
-  // observation loads in flight
-  u32x4 xr[KPS][2][2];
-  u32x4 wr[KPS][2];
-  load_w(0, wr);
-  load_x(0, xr);
+  // Register rings of PD steps for the observation chunks and the W0
+  // fragments: step st computes from ring slot st % PD, then refills that
+  // slot with step st + PD's chunks, stores step st + 1's W0 (in slot
+  // (st + 1) % PD) to the other LDS stage and refills its slot with step
+  // st + 1 + PD's.  Each W0 load is issued before the chunks of the step
+  // after it, so the in-order wait for a W0 slot never waits for chunks that
+  // are needed later.  Prefetch steps are clamped to the last step (those
+  // reloads are never used).
+  constexpr int PD = FWD_PD;
+  u32x4 xr[PD][KPS][2][2];
+  u32x4 wr[PD][KPS][2];
+#pragma unroll
+  for (int j = 0; j < PD; ++j) {
+    load_w(min(j, last_s), wr[j]);
+    load_x(min(j, last_s), xr[j]);
+  }
   u32x4 wfv[2];
   const int wc1 = threadIdx.x + NTHR;
   if constexpr (!Z1) {
@@ -817,8 +841,8 @@ __global__ __launch_bounds__(NTHR) void mlp_fwd_kernel(const qqt_mlp_args a) {
   }
   s.vec[vi0] = vv0;
   if (vi1 < V_N) s.vec[vi1] = vv1;
-  store_w(wr, 0);
-  if (last_s > 0) load_w(1, wr);
+  store_w(wr[0], 0);
+  load_w(min(PD, last_s), wr[0]);
   if constexpr (!Z1) {
     reinterpret_cast<u32x4*>(s.wf)[threadIdx.x] = wfv[0];
     if (wc1 < WF_CH) reinterpret_cast<u32x4*>(s.wf)[wc1] = wfv[1];
@@ -854,17 +878,25 @@ __global__ __launch_bounds__(NTHR) void mlp_fwd_kernel(const qqt_mlp_args a) {
     }
   };
 
-  // Step st: its W0 stage is LDS buffer st & 1.  It computes, loads the next
-  // step's observation chunks, stores the next step's W0 (loaded one step
-  // earlier) to the other buffer and loads the W0 of the step after that.
-  for (int st = 0; st < last_s; ++st) {
-    compute(st, xr, std::false_type{});
-    load_x(st + 1, xr);
-    store_w(wr, (st + 1) & 1);
-    if (st + 2 <= last_s) load_w(st + 2, wr);
+  // Step st (ring slot j = st % PD, W0 stage st & 1); every step but the
+  // last, which only computes.
+  auto step = [&](int st, auto jc) {
+    constexpr int j = decltype(jc)::value;
+    compute(st, xr[j], std::false_type{});
+    load_x(min(st + PD, last_s), xr[j]);
+    store_w(wr[(j + 1) % PD], (st + 1) & 1);
+    load_w(min(st + 1 + PD, last_s), wr[(j + 1) % PD]);
     __syncthreads();
-  }
-  compute(last_s, xr, std::true_type{});
+  };
+  auto unrolled = [&](auto f) { for_each_index(std::make_integer_sequence<int, PD>{}, f); };
+  int st0 = 0;
+  for (; st0 + PD <= last_s; st0 += PD) unrolled([&](auto jc) { step(st0 + jc, jc); });
+  unrolled([&](auto jc) {
+    if (st0 + jc < last_s) step(st0 + jc, jc);
+  });
+  unrolled([&](auto jc) {
+    if (st0 + jc == last_s) compute(last_s, xr[jc], std::true_type{});
+  });
   __syncthreads();   // every wavefront is past its last read of the W0 stages
 
   if constexpr (Z1) {   // first layer only (the training forward): z1 = f + b0
