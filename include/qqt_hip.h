@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 16
+#define QQT_ABI_VERSION 17
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -178,6 +178,12 @@ typedef struct qqt_mlp_args {
                                 z1 = obs W0[pid]^T + b0 in float32 (the training
                                 forward's input to LayerNorm 1), and writes
                                 nothing else */
+  const int64_t* row_index;  /* [B] or NULL: row b of the batch is observation row
+                                row_index[b] (a PPO minibatch read in place from the
+                                flattened rollout buffer, train/ppo.py:406-408,
+                                without a gather); entries are clamped into
+                                [0, obs_rows), so no index reads outside obs */
+  int64_t obs_rows;          /* rows of obs (> 0 when row_index is set) */
 } qqt_mlp_args;
 
 /* astar rule bot for one player (sim/bots.py:267-508, astar_attack with no
@@ -279,6 +285,9 @@ typedef struct qqt_l1_grad_args {
   const float* dz_scale;      /* [1] device float, or NULL */
   float* workspace;
   float* dw0;                 /* [128][k0] */
+  const int64_t* row_index;   /* [B] or NULL: row b is observation row row_index[b]
+                                 (as in qqt_mlp_args; clamped into [0, obs_rows)) */
+  int64_t obs_rows;           /* rows of obs (> 0 when row_index is set) */
 } qqt_l1_grad_args;
 int64_t qqt_l1_grad_workspace_floats(int32_t batch, int32_t k0);
 int qqt_l1_grad(const qqt_l1_grad_args* args, void* stream);

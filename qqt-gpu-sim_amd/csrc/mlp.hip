@@ -406,14 +406,14 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   // Loads run PD group steps ahead; the tail mask (elements >= k0) is applied
   // when the registers are written to LDS, so no load is waited on early.
   // Lanes past k0 read dword 0 of their row (in bounds).
+  const uint32_t* xrp[NX];
+#pragma unroll
+  for (int i = 0; i < NX; ++i) xrp[i] = xbase + obs_row(a, min(xrow0 + 2 * i, a.batch - 1)) * xstride;
   auto load_x = [&](int kb, uint32_t (&xr)[NX]) {
     const int k = 64 * kb + 2 * dw;              // first half of this lane's pair
     const int off = k < a.k0 ? (k >> 1) : 0;     // k0 is even: pairs never straddle
 #pragma unroll
-    for (int i = 0; i < NX; ++i) {
-      const int r = min(xrow0 + 2 * i, a.batch - 1);
-      xr[i] = xbase[(size_t)r * xstride + off];   // cached: two workgroups read each row
-    }
+    for (int i = 0; i < NX; ++i) xr[i] = xrp[i][off];   // cached: two workgroups read each row
   };
   auto load_w = [&](int kb, Frag16 (&br)[2]) {
 #pragma unroll
@@ -765,7 +765,7 @@ __global__ __launch_bounds__(NTHR) void mlp_fwd_kernel(const qqt_mlp_args a) {
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     const int r = min(row0 + 32 * w + 16 * rt + r16, a.batch - 1);
-    xrow[rt] = a.obs + (size_t)r * a.obs_stride;
+    xrow[rt] = a.obs + obs_row(a, r) * a.obs_stride;
   }
   // Chunk h (8 halves from k = 64kb + 16q + 8h) of this lane's rows.  Every
   // step but the last reads whole chunks below k0 (its blocks end at or
@@ -1030,6 +1030,10 @@ int qqt_mlp_act(const qqt_mlp_args* a, void* stream) {
   }
   if (a->sample && (!a->move_mask || !a->bomb_mask)) {
     snprintf(g_err, sizeof(g_err), "qqt_mlp_act: sampling needs masks");
+    return QQT_E_ARG;
+  }
+  if (a->row_index && (a->obs_rows <= 0 || (((uintptr_t)a->row_index) & 7))) {
+    snprintf(g_err, sizeof(g_err), "qqt_mlp_act: row_index needs obs_rows > 0 and 8-byte alignment");
     return QQT_E_ARG;
   }
   if (a->z1_out && (a->npid != 1 || a->sample || (((uintptr_t)a->z1_out) & 15))) {

@@ -79,7 +79,7 @@ __global__ __launch_bounds__(NT) void l1_grad_kernel(const qqt_l1_grad_args a, i
 
   // loader roles: observation dword column xd (columns 2xd, 2xd+1) of rows
   // 8xg..8xg+7; dz1 hidden pair hd (2hd, 2hd+1) of rows 4dg..4dg+3
-  const int xd = t & 127, xg = t >> 7;
+  const int xd = t & 127, xg = w >> 1;                    // xg = t >> 7, as a scalar
   const int hd = t & 63, dg = t >> 6;
   const bool xcol_ok = col0 + 2 * xd < a.k0;              // k0 is even
   const uint32_t* const xbase = reinterpret_cast<const uint32_t*>(a.obs);
@@ -92,7 +92,7 @@ __global__ __launch_bounds__(NT) void l1_grad_kernel(const qqt_l1_grad_args a, i
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int r = r0 + 8 * xg + i;
-      xr[i] = (r < r_end && xcol_ok) ? xbase[(size_t)r * xstride + (col0 >> 1) + xd] : 0u;
+      xr[i] = (r < r_end && xcol_ok) ? xbase[obs_row(a, r) * xstride + (col0 >> 1) + xd] : 0u;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -264,6 +264,10 @@ int l1_grad_check(const qqt_l1_grad_args* a, const char* who) {
   if (a->batch <= 0 || a->k0 <= 0 || (a->k0 & 1) || a->obs_stride < a->k0 ||
       (a->obs_stride & 1) || (((uintptr_t)a->obs) & 3) || (((uintptr_t)a->dz1) & 7)) {
     snprintf(g_err, sizeof(g_err), "%s: bad shape/stride/alignment", who);
+    return QQT_E_ARG;
+  }
+  if (a->row_index && (a->obs_rows <= 0 || (((uintptr_t)a->row_index) & 7))) {
+    snprintf(g_err, sizeof(g_err), "%s: row_index needs obs_rows > 0 and 8-byte alignment", who);
     return QQT_E_ARG;
   }
   return QQT_OK;

@@ -152,4 +152,12 @@ __device__ __forceinline__ int sample_masked(const float* logit, const uint8_t* 
   return a;
 }
 
+// Observation row of batch row r for an argument block with row_index /
+// obs_rows fields: row_index[r] clamped into [0, obs_rows) when the caller
+// maps the batch onto rows of a larger buffer, else r.
+template <class Args>
+__device__ __forceinline__ int64_t obs_row(const Args& a, int r) {
+  return a.row_index ? min(max(a.row_index[r], (int64_t)0), a.obs_rows - 1) : (int64_t)r;
+}
+
 }  // namespace qqt

@@ -14,7 +14,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 
 from ._build import LIB
 
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 MODE_STEP, MODE_OBSERVE, MODE_RESET, MODE_PROBE, MODE_FLUSH = 0, 1, 2, 3, 4
 MAP_PILLARS, MAP_OPEN, MAP_REFERENCE = 0, 1, 2
@@ -68,7 +68,8 @@ class MlpArgsC(ctypes.Structure):
         (n, _vp) for n in ("obs", "w0", "w1", "wh", "wf", "w1_lo", "wh_lo", "wf_lo", "b0", "ln1_w", "ln1_b", "b1",
                            "ln2_w", "ln2_b", "bh", "bf", "move_mask", "bomb_mask", "uniforms",
                            "actions", "actions_i8", "logp_out", "value_out", "logits_out")] + [
-        ("out_slots", _i32), ("out_slot", _i32), ("z1_out", _vp)]
+        ("out_slots", _i32), ("out_slot", _i32), ("z1_out", _vp), ("row_index", _vp),
+        ("obs_rows", ctypes.c_int64)]
 
 
 class BotArgsC(ctypes.Structure):
@@ -81,7 +82,8 @@ class BotArgsC(ctypes.Structure):
 class L1GradArgsC(ctypes.Structure):
     _fields_ = [("batch", _i32), ("k0", _i32), ("obs_stride", _i32), ("reserved", _i32),
                 ("workspace_floats", ctypes.c_int64)] + [
-        (n, _vp) for n in ("obs", "dz1", "dz_scale", "workspace", "dw0")]
+        (n, _vp) for n in ("obs", "dz1", "dz_scale", "workspace", "dw0", "row_index")] + [
+        ("obs_rows", ctypes.c_int64)]
 
 
 class PpoArgsC(ctypes.Structure):

@@ -284,3 +284,65 @@ def test_gather_rows_matches_torch_indexing(dev):
     _capi.check(_capi.lib().qqt_gather_rows(a, _capi.stream_handle(dev)))
     assert torch.equal(out[0], x[5].reshape(-1).view(torch.int32))
     assert bool((out[1:] == 7).all())
+
+
+@pytest.mark.parametrize("b", [3001, 70001])
+def test_row_index_reads_equal_gathered_rows(dev, b):
+    """Batch rows read in place through `row_index` (repeated and
+    out-of-order indices, and two outside the buffer, which are clamped)
+    give exactly what the gathered rows give: the policy forward of
+    `qqt_mlp_act` (the act kernel at 3001 rows, the streaming forward at
+    70001), the first layer's forward and weight gradient, and every
+    gradient and statistic of the fused PPO minibatch."""
+    from qqtsim import _capi
+    from qqtsim.learn import HipMlpActorCritic, PPOConfig
+    from qqtsim.policy import HipActorCritic
+
+    sd = _ortho_init(3)
+    g = torch.Generator().manual_seed(b)
+    n = b + 917
+    base = _obs(n, g).to(dev)
+    idx = torch.randint(0, n, (b,), generator=g)
+    idx[:40] = idx[40]
+    idx[7], idx[b - 1] = -5, n + 3
+    clamped = idx.clamp(0, n - 1)
+    idx, clamped = idx.to(dev), clamped.to(dev)
+    gathered = base[clamped].contiguous()
+
+    # policy forward (logits and values)
+    pol = HipActorCritic(sd, device=dev, seed=0)
+    want = torch.empty((b, 1, 8), dtype=torch.float32, device=dev)
+    pol._run(gathered, 1, 1, False, logits=want)
+    got = torch.full((b, 1, 8), float("nan"), dtype=torch.float32, device=dev)
+    a = pol._args(b, 1, 1, 0, base.data_ptr(), base.stride(0))
+    a.logits_out, a.row_index, a.obs_rows = got.data_ptr(), idx.data_ptr(), n
+    pol._launch(a, _capi.stream_handle(dev))
+    assert torch.equal(got, want)
+
+    # first layer forward and weight gradient
+    net = HipMlpActorCritic(device=dev, state_dict=sd)
+    w, bias = net.shared[0].weight, net.shared[0].bias
+    assert torch.equal(net._l1_forward(base, w, bias, 0, idx), net._l1_forward(gathered, w, bias, 0))
+    dz1 = torch.randn((b, 128), generator=g).to(dev)
+    assert torch.equal(net._l1_weight_grad(base, dz1, 0, rows=idx),
+                       net._l1_weight_grad(gathered, dz1, 0))
+
+    # the fused minibatch
+    mm = (torch.rand((b, 5), generator=g) < 0.6).to(dev)
+    mm[:, 4] = True
+    bm = torch.ones((b, 2), dtype=torch.bool, device=dev)
+    act = torch.stack([torch.multinomial(mm.float().cpu(), 1, generator=g)[:, 0],
+                       torch.zeros(b, dtype=torch.int64)], 1).to(dev)
+    old_logp = (torch.randn(b, generator=g) * 0.3 - 2.0).to(dev)
+    old_val, adv, ret = (torch.randn(b, generator=g).to(dev) for _ in range(3))
+    cfg = PPOConfig()
+    shape = (-1, 14, 13, 13)
+    st_want = net.ppo_grads(gathered.reshape(shape), mm, bm, act, old_logp, adv, ret, old_val,
+                            cfg, 0.05)
+    want_g = {k: p.grad.detach().clone() for k, p in net.named_parameters()}
+    net.zero_grad(set_to_none=True)
+    st_got = net.ppo_grads(base.reshape(shape), mm, bm, act, old_logp, adv, ret, old_val, cfg,
+                           0.05, rows=idx)
+    assert torch.equal(st_got, st_want)
+    for k, p in net.named_parameters():
+        assert torch.equal(p.grad, want_g[k]), k
