@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 17
+#define QQT_ABI_VERSION 18
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -356,6 +356,13 @@ typedef struct qqt_ppo_args {
                                  products over the rows; the caller sizes the buffers to
                                  whole chunks and zeroes the last chunk's tail) */
   int32_t reserved;
+  const int64_t* row_index;   /* [B] or NULL: the per-row inputs actions, move_mask,
+                                 bomb_mask, old_logp, adv, ret and old_val of minibatch
+                                 row b are their row row_index[b] (the flattened rollout
+                                 buffer's fields, read in place), clamped into
+                                 [0, src_rows); z1 and every output stay in minibatch
+                                 order */
+  int64_t src_rows;           /* rows of those inputs (> 0 when row_index is set) */
 } qqt_ppo_args;
 int qqt_ppo_grad(const qqt_ppo_args* args, void* stream);
 

@@ -243,13 +243,15 @@ __global__ __launch_bounds__(T) void ppo_grad_kernel(const qqt_ppo_args a) {
     float dl[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     float st[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
     if (r < nrows) {
-      const size_t g = (size_t)(row0 + r);
+      const size_t g = (size_t)(row0 + r);                       // minibatch row (outputs)
+      const size_t gi = a.row_index                              // its inputs' row
+          ? (size_t)min(max(a.row_index[g], (int64_t)0), a.src_rows - 1) : g;
       uint8_t mm[5], bm[2];
 #pragma unroll
-      for (int k = 0; k < 5; ++k) mm[k] = a.move_mask[g * 5 + k];
+      for (int k = 0; k < 5; ++k) mm[k] = a.move_mask[gi * 5 + k];
 #pragma unroll
-      for (int k = 0; k < 2; ++k) bm[k] = a.bomb_mask[g * 2 + k];
-      const int am = (int)a.actions[g * 2 + 0], ab = (int)a.actions[g * 2 + 1];
+      for (int k = 0; k < 2; ++k) bm[k] = a.bomb_mask[gi * 2 + k];
+      const int am = (int)a.actions[gi * 2 + 0], ab = (int)a.actions[gi * 2 + 1];
       float lpm[5], pm[5], lpb[2], pb[2], hm, hb;
       masked_cat<5>(&s.logit[r][0], mm, lpm, pm, &hm);
       masked_cat<2>(&s.logit[r][5], bm, lpb, pb, &hb);
@@ -262,8 +264,8 @@ __global__ __launch_bounds__(T) void ppo_grad_kernel(const qqt_ppo_args a) {
       const float v = s.logit[r][7];
       const float B = (float)a.batch;
       // policy term
-      const float ratio = expf(logp - a.old_logp[g]);
-      const float adv = a.adv[g];
+      const float ratio = expf(logp - a.old_logp[gi]);
+      const float adv = a.adv[gi];
       const float cr = fminf(fmaxf(ratio, a.ratio_lo), a.ratio_hi);
       const float s1 = ratio * adv, s2 = cr * adv;
       const float w1 = s1 < s2 ? 1.0f : s1 == s2 ? 0.5f : 0.0f;
@@ -272,7 +274,7 @@ __global__ __launch_bounds__(T) void ppo_grad_kernel(const qqt_ppo_args a) {
       const float gmin = -1.0f / B;                           // d loss / d min_i
       const float glogp = gmin * (w1 * adv + w2 * adv * pass) * ratio;
       // value term
-      const float ov = a.old_val[g], ret = a.ret[g];
+      const float ov = a.old_val[gi], ret = a.ret[gi];
       const float dvc = v - ov;
       const float vc = ov + fminf(fmaxf(dvc, -a.clip_eps), a.clip_eps);
       const float e1 = (v - ret) * (v - ret), e2 = (vc - ret) * (vc - ret);
@@ -292,7 +294,7 @@ __global__ __launch_bounds__(T) void ppo_grad_kernel(const qqt_ppo_args a) {
       st[0] = -fminf(s1, s2);
       st[1] = 0.5f * fmaxf(e1, e2);
       st[2] = hm + hb;
-      st[3] = a.old_logp[g] - logp;
+      st[3] = a.old_logp[gi] - logp;
       st[4] = fabsf(ratio - 1.0f) > a.clip_eps ? 1.0f : 0.0f;
 #pragma unroll
       for (int k = 0; k < 8; ++k) a.dl[out_at(g, k, 8, a.t_chunk)] = dl[k];
@@ -433,6 +435,10 @@ int qqt_ppo_grad(const qqt_ppo_args* a, void* stream) {
   if (a->batch <= 0 || (al & 15) || !(a->clip_eps >= 0.0f) || a->t_chunk < 0 ||
       a->t_chunk % R) {
     snprintf(g_err, sizeof(g_err), "qqt_ppo_grad: bad batch, clip or 16-byte alignment");
+    return QQT_E_ARG;
+  }
+  if (a->row_index && (a->src_rows <= 0 || (((uintptr_t)a->row_index) & 7))) {
+    snprintf(g_err, sizeof(g_err), "qqt_ppo_grad: row_index needs src_rows > 0 and 8-byte alignment");
     return QQT_E_ARG;
   }
   const int blocks = (a->batch + R - 1) / R;

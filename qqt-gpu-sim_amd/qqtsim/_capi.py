@@ -14,7 +14,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 
 from ._build import LIB
 
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 MODE_STEP, MODE_OBSERVE, MODE_RESET, MODE_PROBE, MODE_FLUSH = 0, 1, 2, 3, 4
 MAP_PILLARS, MAP_OPEN, MAP_REFERENCE = 0, 1, 2
@@ -93,7 +93,8 @@ class PpoArgsC(ctypes.Structure):
                            "wht", "bh", "wf", "bf", "actions", "move_mask", "bomb_mask",
                            "old_logp", "adv", "ret", "old_val", "dz1", "h1", "dz2", "h2", "hy",
                            "dhy", "dl", "ln_part", "stats_part", "bias_part",
-                           "dz1_absmax_part")] + [("t_chunk", _i32), ("reserved", _i32)]
+                           "dz1_absmax_part")] + [("t_chunk", _i32), ("reserved", _i32),
+                                                   ("row_index", _vp), ("src_rows", ctypes.c_int64)]
 
 
 class CnnArgsC(ctypes.Structure):

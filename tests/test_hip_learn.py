@@ -293,7 +293,8 @@ def test_row_index_reads_equal_gathered_rows(dev, b):
     give exactly what the gathered rows give: the policy forward of
     `qqt_mlp_act` (the act kernel at 3001 rows, the streaming forward at
     70001), the first layer's forward and weight gradient, and every
-    gradient and statistic of the fused PPO minibatch."""
+    gradient and statistic of the fused PPO minibatch (its masks, actions,
+    log-probs, advantages, returns and values read by index too)."""
     from qqtsim import _capi
     from qqtsim.learn import HipMlpActorCritic, PPOConfig
     from qqtsim.policy import HipActorCritic
@@ -327,22 +328,22 @@ def test_row_index_reads_equal_gathered_rows(dev, b):
     assert torch.equal(net._l1_weight_grad(base, dz1, 0, rows=idx),
                        net._l1_weight_grad(gathered, dz1, 0))
 
-    # the fused minibatch
-    mm = (torch.rand((b, 5), generator=g) < 0.6).to(dev)
+    # the fused minibatch: every per-row input of the whole buffer, read by index
+    mm = (torch.rand((n, 5), generator=g) < 0.6).to(dev)
     mm[:, 4] = True
-    bm = torch.ones((b, 2), dtype=torch.bool, device=dev)
+    bm = torch.ones((n, 2), dtype=torch.bool, device=dev)
+    bm[:, 1] = (torch.rand(n, generator=g) < 0.5).to(dev)
     act = torch.stack([torch.multinomial(mm.float().cpu(), 1, generator=g)[:, 0],
-                       torch.zeros(b, dtype=torch.int64)], 1).to(dev)
-    old_logp = (torch.randn(b, generator=g) * 0.3 - 2.0).to(dev)
-    old_val, adv, ret = (torch.randn(b, generator=g).to(dev) for _ in range(3))
+                       torch.multinomial(bm.float().cpu(), 1, generator=g)[:, 0]], 1).to(dev)
+    old_logp = (torch.randn(n, generator=g) * 0.3 - 2.0).to(dev)
+    old_val, adv, ret = (torch.randn(n, generator=g).to(dev) for _ in range(3))
+    per_row = (mm, bm, act, old_logp, adv, ret, old_val)
     cfg = PPOConfig()
     shape = (-1, 14, 13, 13)
-    st_want = net.ppo_grads(gathered.reshape(shape), mm, bm, act, old_logp, adv, ret, old_val,
-                            cfg, 0.05)
+    st_want = net.ppo_grads(gathered.reshape(shape), *(x[clamped] for x in per_row), cfg, 0.05)
     want_g = {k: p.grad.detach().clone() for k, p in net.named_parameters()}
     net.zero_grad(set_to_none=True)
-    st_got = net.ppo_grads(base.reshape(shape), mm, bm, act, old_logp, adv, ret, old_val, cfg,
-                           0.05, rows=idx)
+    st_got = net.ppo_grads(base.reshape(shape), *per_row, cfg, 0.05, rows=idx)
     assert torch.equal(st_got, st_want)
     for k, p in net.named_parameters():
         assert torch.equal(p.grad, want_g[k]), k
