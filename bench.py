@@ -96,6 +96,9 @@ def parse_args():
                          "learner (local features + LSTM) vs the astar bot, 5632 envs")
     ap.add_argument("--copy-calibrate", action="store_true",
                     help="after timing, run a 512 MiB device copy (HBM counter calibration)")
+    ap.add_argument("--no-torch-baseline", action="store_true",
+                    help="ppo: skip the eager-torch update on the GPU (kernel traces of the "
+                         "library's update alone)")
     return ap.parse_args()
 
 
@@ -944,8 +947,11 @@ def main_ppo(args, torch, dev):
     l1g_tf = L1G_FLOP_PER_ROW * mb_rows / (l1g_ms * 1e-3) / 1e12
     fwd_gbs = 2366 * 2 * mb_rows / (fwd_ms * 1e-3) / 1e9
     ppo_ms = tim["ppo_grad_kernel"][0] / tim["ppo_grad_kernel"][1]
-    ref = _torch_mlp(torch, sd, dev)
-    el_ref, ref_stats = run(ref)
+    if args.no_torch_baseline:
+        el_ref, ref_stats = None, None
+    else:
+        ref = _torch_mlp(torch, sd, dev)
+        el_ref, ref_stats = run(ref)
     samples = rows * pcfg.epochs
     cpu = None
     if args.cpu_seconds > 0:
@@ -993,12 +999,10 @@ def main_ppo(args, torch, dev):
                     "first-layer forward (per minibatch)": {
                         "us": round(fwd_ms * 1e3, 3), "obs_gbs": round(fwd_gbs, 3)},
                     "ppo_grad_kernel (per minibatch)": {"us": round(ppo_ms * 1e3, 3)}},
-        "torch_gpu_baseline": {"value": samples / el_ref, "unit": "samples/s",
-                               "ms_per_update": el_ref * 1e3,
-                               "speedup": round(el_ref / el, 3),
-                               "update_stats": ref_stats,
-                               "note": "same update, the reference's network as float32 "
-                                       "eager torch modules"},
+        "torch_gpu_baseline": None if el_ref is None else {
+            "value": samples / el_ref, "unit": "samples/s", "ms_per_update": el_ref * 1e3,
+            "speedup": round(el_ref / el, 3), "update_stats": ref_stats,
+            "note": "same update, the reference's network as float32 eager torch modules"},
         "update_stats": stats,
         "cpu_baseline": cpu,
     }
