@@ -40,6 +40,7 @@ namespace ppo {
 constexpr int R = 16;        // rows per workgroup
 constexpr int T = 512;       // threads: 8 wavefronts (one per column tile of a 128-wide product)
 constexpr int TR = 256;      // threads of the row-wise phases (16 per row)
+static_assert(R * 8 * 4 == T, "the output layer takes four threads per (row, output)");
 constexpr int H = 128;       // hidden width
 constexpr int HY = 192;      // three heads x 64
 constexpr int HP = H + 4, HYP = HY + 4;   // padded LDS row strides
@@ -62,7 +63,7 @@ struct __align__(16) Lds {
 // four A values X[l%16][16 g + 4(l/16) .. + 3] (one 16-byte LDS read).  MFMA
 // 16x16x4 f32 holds D[4(l/16)+q][l%16] in lane l.  Wavefront w takes column
 // tiles w, w+8, ...
-template <int K, int N, int LDX, int LDY>
+template <int K, int N, int LDX, int LDY, bool RELU = false>
 __device__ __forceinline__ void gemm(const float (*X)[LDX], const float* __restrict__ W,
                                      const float* __restrict__ bias, float (*Y)[LDY]) {
   constexpr int CT = N / 16, KG = K / 16;
@@ -83,7 +84,7 @@ __device__ __forceinline__ void gemm(const float (*X)[LDX], const float* __restr
     }
     const float b = bias ? bias[col] : 0.0f;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) Y[4 * kq + q][col] = acc[q] + b;
+    for (int q = 0; q < 4; ++q) Y[4 * kq + q][col] = RELU ? fmaxf(acc[q] + b, 0.0f) : acc[q] + b;
   }
 }
 
@@ -221,19 +222,20 @@ __global__ __launch_bounds__(T) void ppo_grad_kernel(const qqt_ppo_args a) {
   __syncthreads();
   if (t < TR) ln_forward(s.z, a.ln2_w, a.ln2_b, s.xh2, s.h2, s.rstd2);
   __syncthreads();
-  gemm<H, HY, HP, HYP>(s.h2, a.wht, a.bh, s.hy);            // heads' hidden layers
+  gemm<H, HY, HP, HYP, true>(s.h2, a.wht, a.bh, s.hy);      // heads' hidden layers + ReLU
   __syncthreads();
-  for (int i = t; i < R * HY; i += T) {
-    const int r = i / HY, c = i % HY;
-    s.hy[r][c] = fmaxf(s.hy[r][c], 0.0f);
-  }
-  __syncthreads();
-  if (t < R * 8) {                                            // outputs: 5 move, 2 bomb, value
-    const int r = t >> 3, j = t & 7;
-    const int base = j < 5 ? 0 : j < 7 ? 64 : 128;
-    float acc = a.bf[j];
-    for (int k = 0; k < 64; ++k) acc += s.hy[r][base + k] * a.wf[j * 64 + k];
-    s.logit[r][j] = acc;
+  {                                                           // outputs: 5 move, 2 bomb, value
+    // thread t: row t / 32, output (t / 4) % 8, quarter t % 4 of its 64 inputs;
+    // the quarters meet by two lane exchanges
+    const int r = t >> 5, j = (t >> 2) & 7, part = t & 3;
+    const int base = (j < 5 ? 0 : j < 7 ? 64 : 128) + 16 * part;
+    const float* wj = a.wf + j * 64 + 16 * part;
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) acc += s.hy[r][base + k] * wj[k];
+    acc += __shfl_xor(acc, 1, 64);
+    acc += __shfl_xor(acc, 2, 64);
+    if (part == 0) s.logit[r][j] = a.bf[j] + acc;
   }
   __syncthreads();
 
