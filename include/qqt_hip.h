@@ -295,8 +295,8 @@ int qqt_l1_grad(const qqt_l1_grad_args* args, void* stream);
 /* qqt_l1_grad without a caller workspace, for callers that cannot allocate
  * device memory (code under HIP graph capture, serving loops, harnesses that
  * forbid hipMalloc).  No counterpart in the reference.  The chunk partials
- * go to a file-scope device array of 32 x 128 x QQT_L1_GRAD_NOALLOC_MAX_K0
- * floats (40 MiB, one per GPU, held until the process ends); `workspace`
+ * go to a file-scope device array of 64 x 128 x QQT_L1_GRAD_NOALLOC_MAX_K0
+ * floats (80 MiB, one per GPU, held until the process ends); `workspace`
  * and `workspace_floats` are ignored.  Any batch size; k0 at most
  * QQT_L1_GRAD_NOALLOC_MAX_K0 (larger is QQT_E_ARG).  The result equals
  * qqt_l1_grad's bit for bit (same plan, same kernels).  The call allocates

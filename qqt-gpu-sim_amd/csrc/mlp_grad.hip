@@ -47,7 +47,8 @@ constexpr int NCOL = 256;         // observation columns per workgroup
 constexpr int KS = 32;            // batch rows per step (one MFMA K)
 constexpr int XS = KS + 8;        // LDS row stride (halves) of the transposed tiles
 constexpr int NT = 512;           // threads
-constexpr int MAX_CHUNKS = 32;
+constexpr int MAX_CHUNKS = 64;
+constexpr int TARGET_WGS = 512;  // two workgroups (80 KB of LDS each) on each of the 256 CUs
 constexpr int MIN_CHUNK_ROWS = 2048;
 
 struct __align__(16) Lds {
@@ -190,10 +191,17 @@ __global__ __launch_bounds__(256) void l1_grad_reduce(const qqt_l1_grad_args a, 
 }
 
 // Chunks of the batch: rows per chunk a multiple of KS, at least
-// MIN_CHUNK_ROWS, at most MAX_CHUNKS chunks.
-__host__ inline void plan(int batch, int& chunks, int& chunk_rows) {
+// MIN_CHUNK_ROWS, and chunks x column tiles at most TARGET_WGS (all
+// workgroups resident at once, evenly two per CU) and MAX_CHUNKS.  (A
+// 180,224-row minibatch of 2366 columns: 51 chunks x 10 tiles = 510
+// workgroups, 374 us; 32 chunks = 320 workgroups left 192 CUs with one
+// workgroup and took 526 us; 64 chunks need a second round, 478 us.)
+__host__ inline void plan(int batch, int k0, int& chunks, int& chunk_rows) {
+  const int tiles = (k0 + NCOL - 1) / NCOL;
   chunks = (batch + MIN_CHUNK_ROWS - 1) / MIN_CHUNK_ROWS;
+  if (chunks > TARGET_WGS / tiles) chunks = TARGET_WGS / tiles;
   if (chunks > MAX_CHUNKS) chunks = MAX_CHUNKS;
+  if (chunks < 1) chunks = 1;
   chunk_rows = (batch + chunks - 1) / chunks;
   chunk_rows = (chunk_rows + KS - 1) / KS * KS;
   chunks = (batch + chunk_rows - 1) / chunk_rows;
@@ -246,7 +254,7 @@ int64_t qqt_l1_grad_workspace_floats(int32_t batch, int32_t k0) {
   using namespace qqt::l1g;
   if (batch <= 0 || k0 <= 0) return -1;
   int chunks, rows;
-  plan(batch, chunks, rows);
+  plan(batch, k0, chunks, rows);
   const int tiles = (k0 + NCOL - 1) / NCOL;
   return (int64_t)chunks * HID * tiles * NCOL;
 }
@@ -279,7 +287,7 @@ int l1_grad_launch(const qqt_l1_grad_args& a, hipStream_t st) {
   using namespace qqt;
   using namespace qqt::l1g;
   int chunks, rows;
-  plan(a.batch, chunks, rows);
+  plan(a.batch, a.k0, chunks, rows);
   const int tiles = (a.k0 + NCOL - 1) / NCOL;
   const int ws_cols = tiles * NCOL;
   QQT_LAUNCH(QQT_KERNEL_L1GRAD, l1_grad_kernel, dim3(tiles, chunks), dim3(NT), st, a, rows,
