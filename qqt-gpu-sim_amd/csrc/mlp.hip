@@ -646,13 +646,17 @@ constexpr int W0_STAGE = FWD_KPS * W0_BLOCK;      // halves of one step's stage
 
 // [W0 stage 0 | W0 stage 1] during layer 1, then W1 (hi | lo) for layer 2,
 // then the head weights (hi | lo)
-constexpr int FWD_BIG = 2 * W0_STAGE > 2 * WH_HALVES ? 2 * W0_STAGE : 2 * WH_HALVES;
+// (the first-layer-only launch needs the W0 stages and the biases alone: 36
+// KB instead of 114, so more than one workgroup fits on a CU)
+template <bool Z1>
 struct __align__(16) FwdLds {
-  uint16_t big[FWD_BIG];
-  uint16_t wf[2 * WF_HALVES];
+  static constexpr int BIG = Z1 ? 2 * W0_STAGE
+                                : (2 * W0_STAGE > 2 * WH_HALVES ? 2 * W0_STAGE : 2 * WH_HALVES);
+  static_assert(Z1 || BIG >= 2 * W1_HALVES, "W1 reuses the stages");
+  uint16_t big[BIG];
+  uint16_t wf[Z1 ? 8 : 2 * WF_HALVES];
   float vec[V_N];
 };
-static_assert(FWD_BIG >= 2 * W1_HALVES, "W1 reuses the stages");
 
 // acc[r][t] += W(tile t) h_r over KS K steps for R row tiles that share every
 // weight fragment read (layout as tail_gemm).
@@ -704,7 +708,7 @@ __global__ __launch_bounds__(NTHR) void mlp_fwd_kernel(const qqt_mlp_args a) {
   constexpr int W1_CH = 2 * W1_HALVES / 8 / NTHR;
   constexpr int WH_CH = 2 * WH_HALVES / 8 / NTHR;
   constexpr int WF_CH = 2 * WF_HALVES / 8;
-  __shared__ FwdLds s;
+  __shared__ FwdLds<Z1> s;
   const int nrb = (a.batch + FWD_ROWS - 1) / FWD_ROWS;
   const int xcd = blockIdx.x & 7, seq = blockIdx.x >> 3;
   const int slot = seq % a.npid;
