@@ -6,9 +6,10 @@
 // A player's view permutation is folded into the first-layer weights, so a
 // player is just a column block of one shared weight buffer.
 //
-// Workgroup = 8 wavefronts (2 per SIMD) = one row block of one player: an
-// XCD row block of 44 rows (three 16-row tiles) for rollout-sized batches,
-// 128 rows (eight tiles) for large forward batches.  Both players'
+// mlp_act_kernel: workgroup = 8 wavefronts (2 per SIMD) = one row block of
+// one player, an XCD row block of 44 rows (three 16-row tiles).  Forward
+// batches without sampling from 65,536 rows take mlp_fwd_kernel instead
+// (256-row workgroups, described at that kernel).  Both players'
 // workgroups of a row block are dispatched back to back on the same XCD
 // (workgroups are dealt to the 8 XCDs round robin), so the second read of
 // the observation tile hits that XCD's L2, where the tick kernel wrote it.
