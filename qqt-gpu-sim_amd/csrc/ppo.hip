@@ -48,11 +48,18 @@ constexpr float LN_EPS = 1e-5f;
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
+// 48 KB, so three workgroups share a CU.  The LayerNorms keep their inputs
+// and per-row statistics, not the normalised values: the backward recomputes
+// xh = (z - mean) rstd and the ReLU mask xh gamma + beta > 0 with the
+// forward's operations (bit for bit).  Buffers are reused by liveness.
 struct __align__(16) Lds {
-  float xh1[R][HP], h1[R][HP], xh2[R][HP], h2[R][HP], g[R][HP], z[R][HP];
-  float hy[R][HYP], dhy[R][HYP];
+  float z1[R][HP];    // LayerNorm 1's input, for the whole kernel
+  float z2[R][HP];    // LayerNorm 2's input until its backward, then dh1 -> dz1
+  float hb[R][HP];    // h1 (stored out after its product), then h2
+  float g[R][HP];     // dh2 -> dz2
+  float y[R][HYP];    // hy (stored out when the backward starts), then dhy
   float logit[R][8], dl[R][8];
-  float rstd1[R], rstd2[R];
+  float mean1[R], rstd1[R], mean2[R], rstd2[R];
   float stat[R][5];
 };
 
@@ -95,11 +102,11 @@ __device__ __forceinline__ float sum16(float v) {
   return v;
 }
 
-// LayerNorm + ReLU of Z[r] (in place into xh = normalised, h = output);
-// 16 threads per row, feature c = lane + 16 i.
+// LayerNorm + ReLU of Z[r] into h, keeping the row's mean and rstd; 16
+// threads per row, feature c = lane + 16 i.
 __device__ __forceinline__ void ln_forward(const float (*Z)[HP], const float* __restrict__ gam,
-                                           const float* __restrict__ bet, float (*xh)[HP],
-                                           float (*h)[HP], float* rstd_out) {
+                                           const float* __restrict__ bet, float (*h)[HP],
+                                           float* mean_out, float* rstd_out) {
   const int r = threadIdx.x >> 4, j = threadIdx.x & 15;
   float v[8];
   float s = 0.0f;
@@ -120,26 +127,35 @@ __device__ __forceinline__ void ln_forward(const float (*Z)[HP], const float* __
   for (int i = 0; i < 8; ++i) {
     const int c = j + 16 * i;
     const float x = (v[i] - mean) * rstd;
-    xh[r][c] = x;
     h[r][c] = fmaxf(x * gam[c] + bet[c], 0.0f);
   }
-  if (j == 0) rstd_out[r] = rstd;
+  if (j == 0) {
+    mean_out[r] = mean;
+    rstd_out[r] = rstd;
+  }
+}
+
+// The forward's normalised value of (r, c) and whether its ReLU passed.
+__device__ __forceinline__ float ln_xh(const float (*Z)[HP], const float* mean, const float* rstd,
+                                       int r, int c) {
+  return (Z[r][c] - mean[r]) * rstd[r];
 }
 
 // LayerNorm backward with the ReLU after it: dy = G (gradient of the ReLU
 // output) where h > 0; dz = rstd (dx - mean(dx) - xh mean(dx xh)), dx =
 // dy gamma.  Writes dz over G.
-__device__ __forceinline__ void ln_backward(float (*G)[HP], const float (*xh)[HP],
-                                            const float (*h)[HP], const float* __restrict__ gam,
-                                            const float* rstd) {
+__device__ __forceinline__ void ln_backward(float (*G)[HP], const float (*Z)[HP],
+                                            const float* mean, const float* rstd,
+                                            const float* __restrict__ gam,
+                                            const float* __restrict__ bet) {
   const int r = threadIdx.x >> 4, j = threadIdx.x & 15;
   float dx[8], x[8];
   float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int c = j + 16 * i;
-    const float dy = h[r][c] > 0.0f ? G[r][c] : 0.0f;
-    x[i] = xh[r][c];
+    x[i] = ln_xh(Z, mean, rstd, r, c);
+    const float dy = x[i] * gam[c] + bet[c] > 0.0f ? G[r][c] : 0.0f;
     dx[i] = dy * gam[c];
     s1 += dx[i];
     s2 += dx[i] * x[i];
@@ -159,14 +175,18 @@ __device__ __forceinline__ size_t out_at(int64_t r, int c, int n, int t_chunk) {
                      : (size_t)r * n + c;
 }
 
-__device__ __forceinline__ void ln_param_sums(const float (*G)[HP], const float (*xh)[HP],
-                                              const float (*h)[HP], float* out_g, float* out_b) {
+__device__ __forceinline__ void ln_param_sums(const float (*G)[HP], const float (*Z)[HP],
+                                              const float* mean, const float* rstd,
+                                              const float* __restrict__ gam,
+                                              const float* __restrict__ bet, float* out_g,
+                                              float* out_b) {
   const int c = threadIdx.x;
   if (c < H) {
     float sg = 0.0f, sb = 0.0f;
     for (int r = 0; r < R; ++r) {
-      const float dy = h[r][c] > 0.0f ? G[r][c] : 0.0f;
-      sg += dy * xh[r][c];
+      const float x = ln_xh(Z, mean, rstd, r, c);
+      const float dy = x * gam[c] + bet[c] > 0.0f ? G[r][c] : 0.0f;
+      sg += dy * x;
       sb += dy;
     }
     out_g[c] = sg;
@@ -213,16 +233,21 @@ __global__ __launch_bounds__(T) void ppo_grad_kernel(const qqt_ppo_args a) {
     const int r = i / (H / 4), c4 = i % (H / 4);
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (r < nrows) v = reinterpret_cast<const float4*>(a.z1 + (size_t)(row0 + r) * H)[c4];
-    *reinterpret_cast<float4*>(&s.z[r][4 * c4]) = v;
+    *reinterpret_cast<float4*>(&s.z1[r][4 * c4]) = v;
   }
   __syncthreads();
-  if (t < TR) ln_forward(s.z, a.ln1_w, a.ln1_b, s.xh1, s.h1, s.rstd1);
+  if (t < TR) ln_forward(s.z1, a.ln1_w, a.ln1_b, s.hb, s.mean1, s.rstd1);
   __syncthreads();
-  gemm<H, H, HP, HP>(s.h1, a.w1t, a.b1, s.z);               // z2 = h1 W1^T + b1
+  gemm<H, H, HP, HP>(s.hb, a.w1t, a.b1, s.z2);              // z2 = h1 W1^T + b1
   __syncthreads();
-  if (t < TR) ln_forward(s.z, a.ln2_w, a.ln2_b, s.xh2, s.h2, s.rstd2);
+  for (int i = t; i < R * H; i += T) {                      // h1 out before h2 takes its place
+    const int r = i / H, c = i % H;
+    if (r < nrows) a.h1[(size_t)(row0 + r) * H + c] = s.hb[r][c];
+  }
   __syncthreads();
-  gemm<H, HY, HP, HYP, true>(s.h2, a.wht, a.bh, s.hy);      // heads' hidden layers + ReLU
+  if (t < TR) ln_forward(s.z2, a.ln2_w, a.ln2_b, s.hb, s.mean2, s.rstd2);
+  __syncthreads();
+  gemm<H, HY, HP, HYP, true>(s.hb, a.wht, a.bh, s.y);       // heads' hidden layers + ReLU
   __syncthreads();
   {                                                           // outputs: 5 move, 2 bomb, value
     // thread t: row t / 32, output (t / 4) % 8, quarter t % 4 of its 64 inputs;
@@ -232,7 +257,7 @@ __global__ __launch_bounds__(T) void ppo_grad_kernel(const qqt_ppo_args a) {
     const float* wj = a.wf + j * 64 + 16 * part;
     float acc = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) acc += s.hy[r][base + k] * wj[k];
+    for (int k = 0; k < 16; ++k) acc += s.y[r][base + k] * wj[k];
     acc += __shfl_xor(acc, 1, 64);
     acc += __shfl_xor(acc, 2, 64);
     if (part == 0) s.logit[r][j] = a.bf[j] + acc;
@@ -313,9 +338,11 @@ __global__ __launch_bounds__(T) void ppo_grad_kernel(const qqt_ppo_args a) {
     a.stats_part[(size_t)blockIdx.x * 5 + t] = sum;
   }
 
-  // ---- backward: output layer -> heads' hidden (ReLU)
+  // ---- backward: output layer -> heads' hidden (ReLU); hy goes out first
   for (int i = t; i < R * HY; i += T) {
     const int r = i / HY, c = i % HY;
+    const float hyv = s.y[r][c];
+    if (r < nrows) a.hy[(size_t)(row0 + r) * HY + c] = hyv;
     const int head = c >> 6, k = c & 63;
     float d = 0.0f;
     if (head == 0) {
@@ -326,24 +353,26 @@ __global__ __launch_bounds__(T) void ppo_grad_kernel(const qqt_ppo_args a) {
     } else {
       d = s.dl[r][7] * a.wf[7 * 64 + k];
     }
-    s.dhy[r][c] = s.hy[r][c] > 0.0f ? d : 0.0f;
+    s.y[r][c] = hyv > 0.0f ? d : 0.0f;                       // dhy over hy
   }
   __syncthreads();
-  gemm<HY, H, HYP, HP>(s.dhy, a.wh, nullptr, s.g);          // dh2 = dhy Wh
+  gemm<HY, H, HYP, HP>(s.y, a.wh, nullptr, s.g);            // dh2 = dhy Wh
   __syncthreads();
   if (t < H)
-    ln_param_sums(s.g, s.xh2, s.h2, a.ln_part + ((size_t)blockIdx.x * 4 + 2) * H,
+    ln_param_sums(s.g, s.z2, s.mean2, s.rstd2, a.ln2_w, a.ln2_b,
+                  a.ln_part + ((size_t)blockIdx.x * 4 + 2) * H,
                   a.ln_part + ((size_t)blockIdx.x * 4 + 3) * H);
   __syncthreads();
-  if (t < TR) ln_backward(s.g, s.xh2, s.h2, a.ln2_w, s.rstd2);   // s.g = dz2
+  if (t < TR) ln_backward(s.g, s.z2, s.mean2, s.rstd2, a.ln2_w, a.ln2_b);   // s.g = dz2
   __syncthreads();
-  gemm<H, H, HP, HP>(s.g, a.w1, nullptr, s.z);              // dh1 = dz2 W1
+  gemm<H, H, HP, HP>(s.g, a.w1, nullptr, s.z2);             // dh1 = dz2 W1 (z2 is dead)
   __syncthreads();
   if (t < H)
-    ln_param_sums(s.z, s.xh1, s.h1, a.ln_part + ((size_t)blockIdx.x * 4 + 0) * H,
+    ln_param_sums(s.z2, s.z1, s.mean1, s.rstd1, a.ln1_w, a.ln1_b,
+                  a.ln_part + ((size_t)blockIdx.x * 4 + 0) * H,
                   a.ln_part + ((size_t)blockIdx.x * 4 + 1) * H);
   __syncthreads();
-  if (t < TR) ln_backward(s.z, s.xh1, s.h1, a.ln1_w, s.rstd1);   // s.z = dz1
+  if (t < TR) ln_backward(s.z2, s.z1, s.mean1, s.rstd1, a.ln1_w, a.ln1_b);   // s.z2 = dz1
   __syncthreads();
 
   // ---- row outputs
@@ -351,14 +380,9 @@ __global__ __launch_bounds__(T) void ppo_grad_kernel(const qqt_ppo_args a) {
     const int r = i / H, c = i % H;
     if (r < nrows) {
       const size_t o = (size_t)(row0 + r) * H + c;
-      a.dz1[o] = s.z[r][c];
-      a.h1[o] = s.h1[r][c];
-      a.h2[o] = s.h2[r][c];
+      a.dz1[o] = s.z2[r][c];
+      a.h2[o] = s.hb[r][c];
     }
-  }
-  for (int i = t; i < R * HY; i += T) {
-    const int r = i / HY, c = i % HY;
-    if (r < nrows) a.hy[(size_t)(row0 + r) * HY + c] = s.hy[r][c];
   }
   // dz2 and dhy in the caller's layout (rows fastest, so chunk-transposed
   // stores are 16 consecutive floats)
@@ -368,7 +392,7 @@ __global__ __launch_bounds__(T) void ppo_grad_kernel(const qqt_ppo_args a) {
   }
   for (int i = t; i < R * HY; i += T) {
     const int r = i % R, c = i / R;
-    if (r < nrows) a.dhy[out_at(row0 + r, c, HY, a.t_chunk)] = s.dhy[r][c];
+    if (r < nrows) a.dhy[out_at(row0 + r, c, HY, a.t_chunk)] = s.y[r][c];
   }
   // ---- this block's column sums of dz1, dz2, dhy, dl (the bias gradients'
   // partials) and max |dz1| per column (the weight-gradient kernel's scale)
@@ -377,15 +401,15 @@ __global__ __launch_bounds__(T) void ppo_grad_kernel(const qqt_ppo_args a) {
     for (int c = t; c < NB; c += T) {
       float sum = 0.0f;
       for (int r = 0; r < nrows; ++r)
-        sum += c < H ? s.z[r][c]
-                     : c < 2 * H ? s.g[r][c - H] : c < 2 * H + HY ? s.dhy[r][c - 2 * H]
+        sum += c < H ? s.z2[r][c]
+                     : c < 2 * H ? s.g[r][c - H] : c < 2 * H + HY ? s.y[r][c - 2 * H]
                                                                 : s.dl[r][c - 2 * H - HY];
       a.bias_part[(size_t)blockIdx.x * NB + c] = sum;
     }
   }
   if (a.dz1_absmax_part && t < H) {
     float m = 0.0f;
-    for (int r = 0; r < nrows; ++r) m = fmaxf(m, fabsf(s.z[r][t]));
+    for (int r = 0; r < nrows; ++r) m = fmaxf(m, fabsf(s.z2[r][t]));
     a.dz1_absmax_part[(size_t)blockIdx.x * H + t] = m;
   }
 }
