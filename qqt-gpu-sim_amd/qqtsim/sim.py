@@ -145,6 +145,9 @@ class HipBatchedSim:
             raise ValueError("the HIP path writes the 5P+4-channel float16 observation")
         if cfg.fuse > 255:
             raise ValueError("fuse must be <= 255 for the packed cell word")
+        if cfg.chain_blast_bonus != 0:
+            raise ValueError("chain_blast_bonus (sim/torch_sim.py:981-1005) is not on the HIP "
+                             "rollout path; it must be 0")
         self.cfg = cfg
         self.spec = map_spec or MapSpec()
         self.num_envs = int(num_envs)
@@ -379,7 +382,26 @@ class HipBatchedSim:
         self.flushes += 1
         self._fresh = True
 
+    # Every launch and load_state_dict assigns `_fresh`, so an assignment
+    # marks the packed state as possibly changed and drops the converted
+    # attribute views.
+    @property
+    def _fresh(self) -> bool:
+        return self.__dict__["_fresh_flag"]
+
+    @_fresh.setter
+    def _fresh(self, v: bool) -> None:
+        self.__dict__["_fresh_flag"] = bool(v)
+        self.__dict__["_views"] = {}
+
     def __getattr__(self, name):
+        """Reference attribute reads (`sim.hp`, `sim.pos`, `sim.fuse`, ...): the
+        one tensor asked for, in the reference's layout, converted once per
+        state change and cached until the next launch (read-only copies)."""
         if name in st.ALL_KEYS:
-            return self.state_dict()[name]
+            views = self.__dict__.setdefault("_views", {})
+            if name not in views:
+                views[name] = st.unpack_key(self._cells, self._players, self._envs,
+                                            self.cfg.height, self.cfg.width, name)
+            return views[name]
         raise AttributeError(name)

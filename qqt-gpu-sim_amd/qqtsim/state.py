@@ -32,28 +32,38 @@ def _bits(x, shift):
     return (x >> shift) & 1
 
 
+def unpack_key(cells, players, envs, h, w, key):
+    """One state tensor in the reference's layout and dtype."""
+    n = cells.shape[0]
+    if key in GRID_KEYS:
+        cw = cells.view(n, h, w)
+        if key == "fuse":
+            return (cw & 0xFF).to(torch.int16)
+        if key == "owner":
+            return ((((cw >> 8) & 0xFF) ^ 0x80) - 0x80).to(torch.int8)
+        if key == "bomb_blast":
+            return ((cw >> 16) & 0xFF).to(torch.int16)
+        shift = {"wall": F_WALL, "brick": F_BRICK, "crate": F_CRATE, "recycle": F_REC}[key]
+        return _bits(cw, shift).bool()
+    if key == "pos":
+        return players[..., P_Y:P_X + 1].contiguous().view(torch.float32).clone()
+    if key in PLAYER_INT:
+        slot, dt = PLAYER_INT[key]
+        return players[..., slot].to(dt)
+    if key in PLAYER_FLOAT:
+        return players[..., PLAYER_FLOAT[key]].contiguous().view(torch.float32).clone()
+    if key == "t":
+        return envs[:, E_T].long()
+    if key == "crate_prob":
+        return envs[:, E_CRATE_PROB].contiguous().view(torch.float32).clone()
+    if key == "map_kind":
+        return envs[:, E_KIND].long()
+    raise KeyError(key)
+
+
 def unpack(cells, players, envs, h, w):
     """Reference-layout dict of every state tensor."""
-    n = cells.shape[0]
-    cw = cells.view(n, h, w)
-    out = {
-        "fuse": (cw & 0xFF).to(torch.int16),
-        "owner": ((((cw >> 8) & 0xFF) ^ 0x80) - 0x80).to(torch.int8),
-        "bomb_blast": ((cw >> 16) & 0xFF).to(torch.int16),
-        "wall": _bits(cw, F_WALL).bool(),
-        "brick": _bits(cw, F_BRICK).bool(),
-        "crate": _bits(cw, F_CRATE).bool(),
-        "recycle": _bits(cw, F_REC).bool(),
-        "pos": players[..., P_Y:P_X + 1].contiguous().view(torch.float32).clone(),
-    }
-    for k, (slot, dt) in PLAYER_INT.items():
-        out[k] = players[..., slot].to(dt)
-    for k, slot in PLAYER_FLOAT.items():
-        out[k] = players[..., slot].contiguous().view(torch.float32).clone()
-    out["t"] = envs[:, E_T].long()
-    out["crate_prob"] = envs[:, E_CRATE_PROB].contiguous().view(torch.float32).clone()
-    out["map_kind"] = envs[:, E_KIND].long()
-    return out
+    return {k: unpack_key(cells, players, envs, h, w, k) for k in ALL_KEYS}
 
 
 def _check_range(name, v, lo, hi):

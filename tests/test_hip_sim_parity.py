@@ -186,3 +186,34 @@ def test_hip_bomb_stress_injected_actions_match_oracle(dev):
     np.testing.assert_array_equal(hip.observe().cpu().numpy().view(np.uint16),
                                   ora.observe().numpy().view(np.uint16))
     assert resets > 0
+
+
+def test_hip_attribute_views_follow_the_state(dev):
+    """Reference-style attribute reads (`sim.hp`, `sim.pos`, `sim.fuse`, as
+    train/ppo.py:247-286 makes every tick) return the current state: cached
+    between launches, refreshed by each step, reset and load_state_dict."""
+    from qqtsim.config import corridor_training_config
+    from qqtsim.maps import MapSpec
+    from qqtsim.sim import HipBatchedSim
+
+    n = 64
+    sim = HipBatchedSim(corridor_training_config(), n, device=dev, seed=3,
+                        map_spec=MapSpec(kind="pillars", brick_p=0.4))
+    g = torch.Generator(device=dev).manual_seed(0)
+    keys = ("pos", "hp", "alive", "fuse", "owner", "t", "bombs_cap", "spd_g", "brick")
+    for t in range(40):
+        first = sim.pos
+        assert sim.pos is first, "reads between launches share one conversion"
+        sd = sim.state_dict()
+        for k in keys:
+            assert torch.equal(getattr(sim, k), sd[k]), f"{k} before tick {t}"
+        acts = torch.stack([torch.randint(0, 5, (n, 2), generator=g, device=dev),
+                            torch.randint(0, 2, (n, 2), generator=g, device=dev)], -1)
+        sim.step(acts)
+        assert sim.pos is not first
+    snap = sim.state_dict()
+    snap["hp"] = torch.full_like(snap["hp"], 1)
+    sim.load_state_dict({"hp": snap["hp"]})
+    assert torch.equal(sim.hp, snap["hp"])
+    sim.reset_all()
+    assert int(sim.t.max()) == 0

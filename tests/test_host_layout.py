@@ -320,3 +320,27 @@ def test_gather_rows_equals_advanced_indexing():
     assert torch.equal(_gather_rows(odd, s2), odd[s2])
     f32 = torch.rand((20, 6), generator=g)
     assert torch.equal(_gather_rows(f32, s2), f32[s2])
+
+
+def test_sim_rejects_chain_blast_bonus():
+    """A non-zero chain_blast_bonus (sim/torch_sim.py:981-1005) is refused
+    before any device work, instead of being dropped from the rewards."""
+    import dataclasses
+
+    from qqtsim.sim import HipBatchedSim
+
+    cfg = dataclasses.replace(corridor_training_config(), chain_blast_bonus=0.08)
+    with pytest.raises(ValueError, match="chain_blast_bonus"):
+        HipBatchedSim(cfg, 4, device="cpu")
+
+
+def test_unpack_key_matches_unpack():
+    snap = _random_state(seed=3)
+    cells, players, envs = _packed()
+    st.pack_into(cells, players, envs, snap, 13, 13)
+    full = st.unpack(cells, players, envs, 13, 13)
+    for k in st.ALL_KEYS:
+        one = st.unpack_key(cells, players, envs, 13, 13, k)
+        assert one.dtype == full[k].dtype and torch.equal(one, full[k]), k
+    with pytest.raises(KeyError):
+        st.unpack_key(cells, players, envs, 13, 13, "nope")
