@@ -25,9 +25,9 @@
 // stage by stage; the library is built with -ffp-contract=off.
 //
 // The explosion trigger stamp of a cell (0 = not triggered, else the round
-// that triggered it + 1) lives in bits 28-31 of the LDS copy of its word
-// while the explosion resolves; they are cleared before the words are
-// written back.
+// that triggered it + 1, saturating at 15) lives in bits 28-31 of the LDS
+// copy of its word while the explosion resolves; the words written back
+// carry no stamp.
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -44,14 +44,13 @@ int fail(int code, const char* msg);
 
 namespace grp {
 
-constexpr int L = 16;      // lanes per env: one DPP row
-constexpr int EPW = 4;     // envs per wavefront (= workgroup)
 constexpr int CPP = 7;     // observation channels per staging pass
 constexpr uint32_t STAMP_MASK = 0xF0000000u;
 constexpr int STAMP_SHIFT = 28;
 
-template <int H, int W, int P>
+template <int H, int W, int P, int L>
 struct Geo {
+  static_assert(L == 16 || L == 32, "an env takes one or two DPP rows");
   static constexpr int C = H * W;
   static constexpr int KC = (C + L - 1) / L;       // cells per lane
   static constexpr int NCH = 5 * P + 4;
@@ -87,17 +86,23 @@ __device__ __forceinline__ int row_sum(int v) {
   v += dpp<0x121>(v);   // row_ror:1
   return v;
 }
-__device__ __forceinline__ int row_max(int v) {
-  v = max(v, dpp<0x128>(v));
-  v = max(v, dpp<0x124>(v));
-  v = max(v, dpp<0x122>(v));
-  v = max(v, dpp<0x121>(v));
+// sum over the L lanes of the env, in every lane
+template <int L>
+__device__ __forceinline__ int env_sum(int v) {
+  v = row_sum(v);
+  if constexpr (L == 32) {
+    // v_permlane16_swap of v with itself: element 0 holds the even row's
+    // values in both rows of each pair, element 1 the odd row's
+    const auto pr = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+    v = (int)(pr[0] + pr[1]);
+  }
   return v;
 }
-// the 16 ballot bits of this lane's row
-__device__ __forceinline__ uint32_t row_bits(bool pred, int e) {
+// the L ballot bits of env e
+template <int L>
+__device__ __forceinline__ uint32_t env_bits(bool pred, int e) {
   const uint64_t b = __ballot(pred);
-  return (uint32_t)(b >> (16 * e)) & 0xFFFFu;
+  return (uint32_t)(b >> (L * e)) & (L == 32 ? 0xFFFFFFFFu : 0xFFFFu);
 }
 // partner lanes l ^ 1 and l ^ 2 of a quad
 __device__ __forceinline__ float qx1(float v) { return __int_as_float(dpp<0xB1>(__float_as_int(v))); }
@@ -136,6 +141,23 @@ __device__ __forceinline__ void bcast_allf(float v, float (&out)[P]) {
 
 __device__ __forceinline__ uint16_t h16(float v) { return __half_as_ushort(__float2half_rn(v)); }
 
+// f / F correctly rounded, for integers 0 <= f <= 255 and 1 <= F <= 255,
+// from rcp = f32(1 / F): the product's residual, one fused correction.
+// Equal to the IEEE quotient for every such pair (checked exhaustively in
+// exact rational arithmetic).
+__device__ __forceinline__ float qdiv(int f, float F, float rcp) {
+  const float ff = (float)f;
+  const float q0 = ff * rcp;
+  return fmaf(fmaf(-q0, F, ff), rcp, q0);
+}
+// Danger weight (1 - (f-1)/F)^2 clamped at 0 (sim/blast.py:218-220) for a
+// bomb's fuse f >= 1.
+__device__ __forceinline__ float fuse_weight(int f, float F, float rcp) {
+  const float raw = 1.0f - qdiv(f - 1, F, rcp);
+  const float v = raw > 0.0f ? raw : 0.0f;
+  return v * v;
+}
+
 // Player record (slots QQT_P_*) in the registers of the player's lane.
 struct Rec {
   float y, x;
@@ -159,10 +181,11 @@ __device__ __forceinline__ ArgP args_ptr() {
 }
 
 // ---------------------------------------------------------------- kernel
-template <int H, int W, int P, int MAPS>
+template <int H, int W, int P, int MAPS, int L>
 __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config cf,
                                                            const qqt_tick_args a) {
-  using G = Geo<H, W, P>;
+  using G = Geo<H, W, P, L>;
+  constexpr int EPW = 64 / L;   // envs per wavefront (= workgroup)
   constexpr int C = G::C, KC = G::KC, OBS = G::OBS;
   // The config and arguments are read through pointers into the kernel's own
   // argument segment, so each field is loaded (scalar loads) where it is used
@@ -174,7 +197,10 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
   __shared__ __align__(16) uint8_t lds[EPW * G::BLOCK];
 
   const int lane = threadIdx.x;
-  const int e = lane >> 4, l = lane & 15;
+  // env e of the wavefront; lane l of the env (its cells are l + L k); lane
+  // lr of the 16-lane row (a two-row env holds its player records in both
+  // rows, so that player values move with row broadcasts)
+  const int e = lane / L, l = lane % L, lr = lane & 15;
   // workgroups are dealt to the 8 XCDs round robin; block b takes the envs
   // of XCD_ROWS-env row block (b / 8 / WGRB) * 8 + b % 8, as the act kernel
   // deals its rows, so an env stays in one XCD's L2 from kernel to kernel
@@ -182,8 +208,9 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
   const int rb = (seq / WGRB) * 8 + (blockIdx.x & 7);
   const int g0 = rb * XCD_ROWS + (seq % WGRB) * EPW;
   if (g0 >= A->n_envs) return;
+  const int n_envs = A->n_envs;
   const int g = g0 + e;
-  const bool valid = g < A->n_envs;
+  const bool valid = g < n_envs;
   const size_t gs = valid ? (size_t)g : (size_t)g0;
 
   uint8_t* blk = lds + e * G::BLOCK;
@@ -194,15 +221,19 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
   uint8_t* list = blk + G::O_LIST;
   const float rad = CF->radius;
   const float fmax_f = (float)CF->fuse;
+  const float frcp = __fdiv_rn(1.0f, fmax_f);
+  const int cfg_blast = CF->blast;
+  const bool corridor = CF->corridor != 0;
 
   // ---- load: cells into registers, players into their lanes, env record
+  const int32_t* const cells_in = A->cells + gs * C;
   uint32_t cw[KC];
 #pragma unroll
   for (int k = 0; k < KC; ++k) {
     const int c = l + L * k;
-    cw[k] = (valid && c < C) ? (uint32_t)A->cells[gs * C + c] : (F_WALL | EMPTY_CELL);
+    cw[k] = (valid && c < C) ? (uint32_t)cells_in[c] : (F_WALL | EMPTY_CELL);
   }
-  const int pi = l < P ? l : 0;   // player of this lane (lanes >= P carry a copy of player 0)
+  const int pi = lr < P ? lr : 0;   // player of this lane (other lanes carry a copy of player 0)
   Rec r;
   {
     const int4* q = reinterpret_cast<const int4*>(A->players + (gs * P + pi) * QQT_P_SLOTS);
@@ -215,8 +246,8 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
   int4 ev = *reinterpret_cast<const int4*>(A->envs + gs * QQT_E_SLOTS);
   int in_mv = 4, in_bb = 0;
   float in_uh = 0.0f, in_ug = 0.0f;
-  if (l < P && valid) {
-    const size_t ai = (gs * P + l) * 2;
+  if (lr < P && valid) {
+    const size_t ai = (gs * P + lr) * 2;
     if (A->actions) {
       in_mv = (int)A->actions[ai];
       in_bb = (int)A->actions[ai + 1];
@@ -225,8 +256,8 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
       in_bb = A->actions_i8[ai + 1];
     }
     if (A->crate_u) {
-      in_uh = A->crate_u[((size_t)l * 2 + 0) * A->n_envs + g];
-      in_ug = A->crate_u[((size_t)l * 2 + 1) * A->n_envs + g];
+      in_uh = A->crate_u[((size_t)lr * 2 + 0) * n_envs + g];
+      in_ug = A->crate_u[((size_t)lr * 2 + 1) * n_envs + g];
     }
   }
 
@@ -241,7 +272,7 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
     const int o = cw_owner(cw[k]);
     if (cw_fuse(cw[k]) > 0 && o >= 0 && o < P) livepack += 1 << (8 * o);
   }
-  livepack = row_sum(livepack);
+  livepack = env_sum<L>(livepack);
   const int my_live = (livepack >> (8 * pi)) & 0xFF;
 #pragma unroll
   for (int k = 0; k < KC; ++k) {
@@ -253,7 +284,7 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
   // ---- 2. placement, players in id order (sim/torch_sim.py:1357-1402):
   // a player's bomb also blocks the cell for every later player
   const uint32_t wpre = cwl[fpre];
-  int placed = (l < P && alive0 && in_bb == 1 && cw_fuse(wpre) <= 0 && !(wpre & F_BRICK) &&
+  int placed = (lr < P && alive0 && in_bb == 1 && cw_fuse(wpre) <= 0 && !(wpre & F_BRICK) &&
                 my_live < r.bcap) ? 1 : 0;
   int fpre_b[P], alive_b[P], placed_b[P];
   bcast_all<P>(fpre, fpre_b);
@@ -263,11 +294,11 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
     const int pb = i == 0 ? rbc<0>(placed) : i == 1 ? rbc<1>(placed) : i == 2 ? rbc<2>(placed)
                                                                        : rbc<3>(placed);
     placed_b[i] = pb;
-    if (l > i && pb && fpre_b[i] == fpre) placed = 0;
+    if (lr > i && pb && fpre_b[i] == fpre) placed = 0;
   }
   const bool any_placed = __any(placed != 0);
   if (any_placed) {
-    if (placed) cwl[fpre] = cw_make(wpre, CF->fuse, l, r.zcap);
+    if (placed && l < P) cwl[fpre] = cw_make(wpre, CF->fuse, lr, r.zcap);
     int zcap_b[P];
     bcast_all<P>(r.zcap, zcap_b);
 #pragma unroll
@@ -282,7 +313,8 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
   // ---- 3. placement reward (sim/torch_sim.py:1263-1355): lane = me*4 + dir
   float pbonus = 0.0f;
   if (any_placed) {
-    const int me = l >> 2, d = l & 3;
+    const int me = lr >> 2, d = lr & 3;
+    const float ctf = CF->chain_time_factor, ctr = CF->chain_time_rest;
     float ypre_b[P], xpre_b[P];
     int since_b[P];
     bcast_allf<P>(r.y, ypre_b);
@@ -306,15 +338,15 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
             for (int i = 0; i < P; ++i)
               if (fpre_b[i] == x) pm = placed_b[i];
             if (!pm) {
-              float frac = __fdiv_rn((float)fx, fmax_f);
+              float frac = qdiv(fx, fmax_f, frcp);
               frac = fminf(fmaxf(frac, 0.0f), 1.0f);
-              const float wt = CF->chain_time_factor + CF->chain_time_rest * (1.0f - frac);
+              const float wt = ctf + ctr * (1.0f - frac);
               chain = chain + wt;
             }
           }
         };
         if (d == 0) visit(s0, w0);
-        walk_ray<H, W>(cwl, s0, d, blast_of(w0, CF->blast), 1, [&](int, int x, uint32_t wx) {
+        walk_ray<H, W>(cwl, s0, d, blast_of(w0, cfg_blast), 1, [&](int, int x, uint32_t wx) {
           if (wx & F_WALL) return false;
           visit(x, wx);
           return !cw_solid(wx);
@@ -361,7 +393,7 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
 
   // ---- 4. since_bomb; 5. movement (sim/move.py:234-279), both axes from
   // the pre-move box, in the player's lane
-  if (l < P) {
+  if (lr < P) {
     const int mc = min(max(in_mv, 0), 4);
     const float st = CF->step_len;
     const float tvy = mc == 0 ? -st : (mc == 1 ? st : 0.0f);
@@ -394,7 +426,7 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
     const int c = l + L * k;
     const uint32_t w = cw[k];
     const bool in = c < C && (cw_fuse(w) > 0 || cw_owner(w) >= 0);
-    const uint32_t bits = row_bits(in, e);
+    const uint32_t bits = env_bits<L>(in, e);
     if (in) list[nl + __popc(bits & ((1u << l) - 1u))] = (uint8_t)c;
     nl += __popc(bits);
     const bool due = c < C && cw_fuse(w) == 0 && cw_owner(w) >= 0;
@@ -404,41 +436,54 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
     }
     boom |= due;
   }
-  const bool env_boom = row_bits(boom, e) != 0;
+  const bool env_boom = env_bits<L>(boom, e) != 0;
   const bool wave_boom = __any(boom);
   if (wave_boom) {
     wave_sync();
     // rays of the list entries whose trigger stamp is `stamp`, one (entry,
     // direction) per lane: walls stop a ray before the cell, other solids after it
+    // a ray that covers a live bomb not yet triggered makes another round
+    // necessary; without one the remaining rounds trigger nothing
+    bool hit_live = false;
+    const int tiers = A->resolve_tiers;
     auto fire = [&](uint32_t stamp) {
+      hit_live = false;
       for (int it = l; it < 4 * nl; it += L) {
         const int src = list[it >> 2], d = it & 3;
         const uint32_t w = cwl[src];
-        const int b = blast_of(w, CF->blast);
-        if ((w >> STAMP_SHIFT) != stamp || (w & (F_WALL | F_BRICK)) || b > A->resolve_tiers) continue;
+        const int b = blast_of(w, cfg_blast);
+        if ((w >> STAMP_SHIFT) != stamp || (w & (F_WALL | F_BRICK)) || b > tiers) continue;
         walk_ray<H, W>(cwl, src, d, b, 1, [&](int, int x, uint32_t wx) {
           if (wx & F_WALL) return false;
           cov[x] = 1;
+          if (cw_fuse(wx) > 0 && (wx >> STAMP_SHIFT) == 0u) hit_live = true;
           return !cw_solid(wx);
         });
       }
     };
-    fire(1u);
+    // round 0 fires the due bombs; round r >= 1 first marks the live bombs
+    // the flames cover (stamp r + 1), then fires them
     const int rounds = min(CF->max_chain - 1, CF->chain_cap_rounds);
-    for (int rr = 0; rr < rounds; ++rr) {
-      wave_sync();
-      bool newly = false;
-      for (int j = l; j < nl; j += L) {
-        const int c = list[j];
-        const uint32_t w = cwl[c];
-        if (cw_fuse(w) > 0 && cov[c] && (w >> STAMP_SHIFT) == 0u) {
-          cwl[c] = w | ((uint32_t)(rr + 2) << STAMP_SHIFT);
-          newly = true;
+    for (int rr = 0; rr <= rounds; ++rr) {
+      // stamps saturate at 15: from round 14 on, the bombs stamped 15 fire
+      // again each round, which changes nothing (cover writes are idempotent)
+      const uint32_t stamp = (uint32_t)min(rr + 1, 15);
+      if (rr > 0) {
+        wave_sync();
+        bool newly = false;
+        for (int j = l; j < nl; j += L) {
+          const int c = list[j];
+          const uint32_t w = cwl[c];
+          if (cw_fuse(w) > 0 && cov[c] && (w >> STAMP_SHIFT) == 0u) {
+            cwl[c] = w | (stamp << STAMP_SHIFT);
+            newly = true;
+          }
         }
+        if (!__any(newly)) break;
+        wave_sync();
       }
-      if (!__any(newly)) break;
-      wave_sync();
-      fire((uint32_t)(rr + 2));
+      fire(stamp);
+      if (!__any(hit_live)) break;
     }
     wave_sync();
   }
@@ -471,17 +516,17 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
         trg = (cwl[c] >> STAMP_SHIFT) != 0u;
         uint32_t w = cw[k];
         if (env_boom && cvd && (w & F_BRICK)) {
-          if (CF->corridor) w |= F_CRATE;
+          if (corridor) w |= F_CRATE;
           w &= ~F_BRICK;
         }
         if (trg) w = cw_make(w, 0, -1, 0);
         cw[k] = w;
         cwl[c] = w;
       }
-      const uint32_t bc = row_bits(cvd, e), bt = row_bits(trg, e);
-      if ((k >> 1) == l) {
-        covw |= bc << (16 * (k & 1));
-        trgw |= bt << (16 * (k & 1));
+      const uint32_t bc = env_bits<L>(cvd, e), bt = env_bits<L>(trg, e);
+      if (((L * k) >> 5) == l) {   // cells L k .. L k + L - 1 sit at bit (L k) % 32 of word (L k) / 32
+        covw |= bc << ((L * k) & 31);
+        trgw |= bt << ((L * k) & 31);
       }
     }
   }
@@ -496,97 +541,102 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
   for (int k = 0; k < KC; ++k) {
     const int c = l + L * k;
     const bool in = c < C && cw_fuse(cw[k]) > 0;
-    const uint32_t bits = row_bits(in, e);
+    const uint32_t bits = env_bits<L>(in, e);
     if (in) list[nb + __popc(bits & ((1u << l) - 1u))] = (uint8_t)c;
     nb += __popc(bits);
   }
   bool has_danger = nb > 0;
   if (__any(has_danger)) {
     wave_sync();
+    // Stage A, synchronous relay rounds over (bomb, direction) items, one per
+    // lane: bomb j = item / 4 looks back along direction item % 4 for its
+    // in-neighbour, the first solid cell behind it, kept if it is a bomb
+    // whose range reaches j (bombs on walls have none; walls are senders
+    // like any bomb: the reference's stage-A origins are not masked by
+    // passability).  The quad's largest sender front is j's spread; a bomb
+    // whose spread beats its weight takes the spread as weight and as next
+    // round's front, every other bomb's next front is 0.  Weights by cell
+    // live in fw (read by stage B), fronts of rounds >= 1 in the danger
+    // map's space (zeroed before stage B), update flags by list index in
+    // the dead cover bytes.  Round 0's fronts are the fuse weights of the
+    // senders themselves, computed from the cell words the walk reads.
+    float* front = dng;
+    uint8_t* upd_f = cov;
+    const int rounds = CF->max_chain > 1 ? min(CF->max_chain, CF->chain_cap_rounds) : 0;
+    // the first L items (bombs 0 .. L/4 - 1 of the env) keep their cell, sender and
+    // weight in registers from round 0 on
+    int c0 = 0, snd0 = 255;
+    float w0r = 0.0f;
+    bool more = true;
+    for (int rr = 0; rr < rounds + (rounds == 0 ? 1 : 0) && more; ++rr) {
+      if (rr > 0) wave_sync();
+      bool upd = false, flag0 = false;
+      for (int it0 = 0; it0 < 4 * nb; it0 += L) {   // the env's items in passes of L
+        const int it = it0 + l;
+        const int j = it >> 2, d = it & 3;
+        const bool live = it < 4 * nb;
+        float spread = 0.0f;
+        if (it0 == 0 && rr > 0) {
+          if (live && snd0 != 255) spread = front[snd0];
+          spread = fmaxf(spread, qx1(spread));
+          spread = fmaxf(spread, qx2(spread));
+          if (live && d == 0) {
+            const bool f = spread > w0r;
+            if (f) {
+              w0r = spread;
+              fw[c0] = spread;
+            }
+            flag0 = f;
+            upd |= f;
+          }
+          continue;
+        }
+        const int c = live ? list[j] : 0;
+        const uint32_t wc = cwl[c];
+        int snd = 255;
+        if (live && rounds > 0 && !(wc & F_WALL)) {
+          walk_ray<H, W>(cwl, c, d, H + W, -1, [&](int k, int u, uint32_t wu) {
+            if (cw_fuse(wu) > 0) {
+              if (blast_of(wu, cfg_blast) >= k) {
+                snd = u;
+                spread = rr == 0 ? fuse_weight(cw_fuse(wu), fmax_f, frcp) : front[u];
+              }
+              return false;
+            }
+            return !(wu & (F_WALL | F_BRICK));
+          });
+        }
+        spread = fmaxf(spread, qx1(spread));
+        spread = fmaxf(spread, qx2(spread));
+        const float wj = (live && d == 0) ? (rr == 0 ? fuse_weight(cw_fuse(wc), fmax_f, frcp) : fw[c]) : 0.0f;
+        const bool f = spread > wj;
+        if (it0 == 0) {       // round 0 of the first pass
+          c0 = c;
+          snd0 = snd;
+          w0r = f ? spread : wj;
+        }
+        if (live && d == 0) {
+          fw[c] = f ? spread : wj;
+          if (rr == 0) front[c] = f ? spread : 0.0f;   // nobody reads fronts in round 0
+          else upd_f[j] = f ? 1 : 0;
+          upd |= f;
+        }
+      }
+      if (rr > 0) {
+        wave_sync();
+        if (l < 4 * nb && (l & 3) == 0) front[c0] = flag0 ? w0r : 0.0f;
+        for (int j = L / 4 + l; j < nb; j += L) {
+          const int c = list[j];
+          front[c] = upd_f[j] ? fw[c] : 0.0f;
+        }
+      }
+      more = __any(upd);
+    }
+    wave_sync();
     if (has_danger) {
 #pragma unroll
       for (int k = 0; k < KC; ++k)
         if (l + L * k < C) dng[l + L * k] = 0.0f;
-    }
-    // weights in the bomb lanes (bomb j = l + 16 i); the stage-A front by
-    // cell in LDS (walls included: the reference's stage-A origins are not
-    // masked by passability)
-    float wreg[KC];
-#pragma unroll
-    for (int i = 0; i < KC; ++i) {
-      const int j = l + L * i;
-      wreg[i] = 0.0f;
-      if (j < nb) {
-        const int c = list[j];
-        const float w0 = bomb_weight(cw_fuse(cwl[c]), fmax_f);
-        wreg[i] = w0;
-        fw[c] = w0;
-      }
-    }
-    if (CF->max_chain > 1) {
-      // in-edges: per direction, the first solid cell behind the bomb, kept if
-      // it is a bomb whose range reaches this one (sender cell, 255 = none)
-      uint32_t edge4[KC];
-#pragma unroll
-      for (int i = 0; i < KC; ++i) {
-        const int j = l + L * i;
-        uint32_t ed4 = 0xFFFFFFFFu;
-        if (j < nb) {
-          const int c = list[j];
-          if (!(cwl[c] & F_WALL)) {
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-              uint32_t ed = 0xFFu;
-              walk_ray<H, W>(cwl, c, d, H + W, -1, [&](int k, int u, uint32_t wu) {
-                if (cw_fuse(wu) > 0) {
-                  if (blast_of(wu, CF->blast) >= k) ed = (uint32_t)u;
-                  return false;
-                }
-                return !(wu & (F_WALL | F_BRICK));
-              });
-              ed4 = (ed4 & ~(0xFFu << (8 * d))) | (ed << (8 * d));
-            }
-          }
-        }
-        edge4[i] = ed4;
-      }
-      // stage A: synchronous relay rounds
-      const int rounds = min(CF->max_chain, CF->chain_cap_rounds);
-      for (int rr = 0; rr < rounds; ++rr) {
-        wave_sync();
-        float nf[KC];
-        bool upd = false;
-#pragma unroll
-        for (int i = 0; i < KC; ++i) {
-          nf[i] = 0.0f;
-          if (l + L * i >= nb) continue;
-          float spread = 0.0f;
-#pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            const uint32_t u = (edge4[i] >> (8 * d)) & 0xFFu;
-            if (u != 0xFFu) spread = fmaxf(spread, fw[u]);
-          }
-          const float nv = spread > wreg[i] ? spread : 0.0f;
-          nf[i] = nv;
-          upd |= nv > 0.0f;
-        }
-        wave_sync();
-#pragma unroll
-        for (int i = 0; i < KC; ++i) {
-          const int j = l + L * i;
-          if (j >= nb) continue;
-          if (nf[i] > 0.0f) wreg[i] = nf[i];
-          fw[list[j]] = nf[i];
-        }
-        if (!__any(upd)) break;
-      }
-      wave_sync();
-    }
-    // the final weights by cell for the rays
-#pragma unroll
-    for (int i = 0; i < KC; ++i) {
-      const int j = l + L * i;
-      if (j < nb) fw[list[j]] = wreg[i];
     }
     wave_sync();
     // stage B: every (bomb, direction) ray max-updates the danger map.
@@ -600,7 +650,7 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
       const int v = __float_as_int(fw[c]);
       if (wc & F_WALL) continue;
       if (d == 0) atomicMax(&dngi[c], v);   // the bomb's own cell (seed)
-      walk_ray<H, W>(cwl, c, d, blast_of(wc, CF->blast), 1, [&](int, int x, uint32_t wx) {
+      walk_ray<H, W>(cwl, c, d, blast_of(wc, cfg_blast), 1, [&](int, int x, uint32_t wx) {
         if (wx & F_WALL) return false;
         atomicMax(&dngi[x], v);
         return !cw_solid(wx);
@@ -615,9 +665,36 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
   int map_kind = ev.z;
   bool do_reset = false;
   {
+    const auto k_max_steps = CF->max_steps;
+    const auto k_explore_coef = A->explore_coef;
+    const auto k_crate_u = A->crate_u;
+    const auto k_seed = A->seed;
+    const auto k_tick = A->tick;
+    const auto k_step_penalty = CF->step_penalty;
+    const auto k_hit_reward = CF->hit_reward;
+    const auto k_hit_attr_penalty = CF->hit_attr_penalty;
+    const auto k_hit_speed_drop = CF->hit_speed_drop;
+    const auto k_growth_speed_step = CF->growth_speed_step;
+    const auto k_brick_reward = CF->brick_reward;
+    const auto k_recycle_crate_prob = CF->recycle_crate_prob;
+    const auto k_growth_bombs_max = CF->growth_bombs_max;
+    const auto k_growth_blast_max = CF->growth_blast_max;
+    const auto k_growth_speed_max = CF->growth_speed_max;
+    const auto k_danger_coef = A->danger_coef;
+    const auto k_combo_reward = CF->combo_reward;
+    const auto k_combo_gap_factor = CF->combo_gap_factor;
+    const auto k_timeout_draw = CF->timeout_draw;
+    const auto k_win_hp_scaled = CF->win_hp_scaled;
+    const auto k_win_per_hp = CF->win_per_hp;
+    const auto k_win_bonus = CF->win_bonus;
+    const auto k_reward = A->reward;
+    const auto k_winner = A->winner;
+    const auto k_done = A->done;
+    const auto k_n_alive = A->n_alive;
+    const auto k_auto_reset = A->auto_reset;
     int alv_b[P], hp_b[P], hp0_b[P], stood_b[P];
     const uint32_t wcell = cwl[fpost];
-    const int stood = CF->corridor && (wcell & F_CRATE) ? 1 : 0;
+    const int stood = corridor && (wcell & F_CRATE) ? 1 : 0;
     bcast_all<P>(r.alive, alv_b);
     bcast_all<P>(r.hp, hp_b);
     bcast_all<P>(hp0, hp0_b);
@@ -631,63 +708,63 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
       hsum_int += hp_b[o];
       any_stood |= stood_b[o] != 0;
     }
-    const bool done = (n_alive <= 1) || (t >= CF->max_steps);
-    const float alpha = A->explore_coef;
+    const bool done = (n_alive <= 1) || (t >= k_max_steps);
+    const float alpha = k_explore_coef;
     const float dmg = (float)max(hp0 - r.hp, 0);
     const float dng_here = has_danger ? dng[fpost] : 0.0f;
     // crate uniforms: injected, or Philox per tick (both players' pairs in one block)
     float uh = in_uh, ug = in_ug;
-    if (any_stood && !A->crate_u) {
+    if (any_stood && !k_crate_u) {
       float u4[4];
-      philox_block(A->seed, (uint32_t)gs, A->tick, STREAM_CRATE, (uint32_t)((2 * pi) >> 2), u4);
+      philox_block(k_seed, (uint32_t)gs, k_tick, STREAM_CRATE, (uint32_t)((2 * pi) >> 2), u4);
       const bool hi = ((2 * pi) & 3) != 0;   // player pairs sit at words 0-1 and 2-3
       uh = hi ? u4[2] : u4[0];
       ug = hi ? u4[3] : u4[1];
     }
-    if (l < P) {
+    if (lr < P) {
       const float a0 = (float)(alive0 != 0);
       const float dsum = (float)dsum_int;  // exact: a sum of small integers
       const float dealt = dsum - dmg;
-      float rw = (-CF->step_penalty) * a0;
-      rw = rw + CF->hit_reward * dealt;
-      rw = rw - CF->hit_reward * dmg;
+      float rw = (-k_step_penalty) * a0;
+      rw = rw + k_hit_reward * dealt;
+      rw = rw - k_hit_reward * dmg;
       rw = rw + (alpha * pbonus) * a0;
-      if (CF->hit_attr_penalty > 0 && dmg > 0.0f && alive0) {
-        const int pen = CF->hit_attr_penalty;
+      if (k_hit_attr_penalty > 0 && dmg > 0.0f && alive0) {
+        const int pen = k_hit_attr_penalty;
         const int bc = r.bcap, zc = r.zcap;
         const float sp = r.spd;
         const int nbc = max(bc - pen, r.lob);
         const int nzc = max(zc - pen, r.loz);
-        const float ns = fmaxf(sp - CF->hit_speed_drop, r.los);
+        const float ns = fmaxf(sp - k_hit_speed_drop, r.los);
         const float lost_f = (float)((bc - nbc) + (zc - nzc)) +
-                             rintf(__fdiv_rn(sp - ns, CF->growth_speed_step));
+                             rintf(__fdiv_rn(sp - ns, k_growth_speed_step));
         r.bcap = nbc;
         r.zcap = nzc;
         r.spd = ns;
         r.pend += (int)lost_f;
       }
       rw = rw + (alpha * 0.0f) * a0;  // chain_blast_bonus term (0: the host refuses other values)
-      if (CF->corridor) {
-        rw = rw + (CF->brick_reward * (float)stood) * a0;
+      if (corridor) {
+        rw = rw + (k_brick_reward * (float)stood) * a0;
         if (any_stood) {
-          const float prob = (wcell & F_REC) ? CF->recycle_crate_prob : crate_prob;
+          const float prob = (wcell & F_REC) ? k_recycle_crate_prob : crate_prob;
           const int h = stood && (uh < prob) && alive0;
           const int attr = (int)floorf(ug * 3.0f);
-          r.bcap = min(r.bcap + (attr == 0) * h, CF->growth_bombs_max);
-          r.zcap = min(r.zcap + (attr == 1) * h, CF->growth_blast_max);
-          const float sp = r.spd + (float)((attr == 2) * h) * CF->growth_speed_step;
-          r.spd = fminf(sp, CF->growth_speed_max);
+          r.bcap = min(r.bcap + (attr == 0) * h, k_growth_bombs_max);
+          r.zcap = min(r.zcap + (attr == 1) * h, k_growth_blast_max);
+          const float sp = r.spd + (float)((attr == 2) * h) * k_growth_speed_step;
+          r.spd = fminf(sp, k_growth_speed_max);
         }
         cwl[fpost] = wcell & ~(F_CRATE | F_REC);
       }
-      rw = rw - (A->danger_coef * dng_here) * a0;
-      if (CF->combo_reward > 0.0f) {
+      rw = rw - (k_danger_coef * dng_here) * a0;
+      if (k_combo_reward > 0.0f) {
         const int c0 = r.combo;
         if (dealt > 0.0f) {
           const int gap = t - r.last_hit;
-          const float factor = powf(CF->combo_gap_factor, (float)max(gap, 0));
+          const float factor = powf(k_combo_gap_factor, (float)max(gap, 0));
           const int combo_now = c0 + 1;
-          const float pts = (((float)combo_now * CF->combo_reward) * factor) * fminf(dealt, 1.0f);
+          const float pts = (((float)combo_now * k_combo_reward) * factor) * fminf(dealt, 1.0f);
           rw = rw + pts * a0;
           r.last_hit = t;
           r.combo = combo_now;
@@ -702,11 +779,11 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
       int win = death_done && al, lose = death_done && !al;
       const float hpf = (float)r.hp;
       float tscale = alpha;
-      if (!CF->timeout_draw) {
+      if (!k_timeout_draw) {
         bool gt = true, lt = false;
 #pragma unroll
         for (int o = 0; o < P; ++o) {
-          if (o == l) continue;
+          if (o == lr) continue;
           const float ho = (float)hp_b[o];
           gt = gt && (hpf > ho);
           lt = lt || (hpf < ho);
@@ -716,23 +793,23 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
         tscale = 1.0f;
       }
       const float diff = hpf - __fdiv_rn((float)hsum_int - hpf, (float)(P - 1));
-      if (CF->win_hp_scaled) {
-        const float base = CF->win_per_hp * diff;
+      if (k_win_hp_scaled) {
+        const float base = k_win_per_hp * diff;
         rw = rw + (base * (float)death_done + (base * (float)all_alive) * tscale);
       } else {
-        rw = rw + CF->win_bonus * ((float)win - (float)lose);
-        if (CF->timeout_draw) rw = rw + ((CF->win_per_hp * diff) * (float)all_alive) * tscale;
+        rw = rw + k_win_bonus * ((float)win - (float)lose);
+        if (k_timeout_draw) rw = rw + ((k_win_per_hp * diff) * (float)all_alive) * tscale;
       }
-      if (valid) {
-        if (A->reward) A->reward[gs * P + l] = rw;
-        if (A->winner) A->winner[gs * P + l] = win;
+      if (valid && l < P) {
+        if (k_reward) k_reward[gs * P + l] = rw;
+        if (k_winner) k_winner[gs * P + l] = win;
       }
     }
     if (valid && l == 0) {
-      if (A->done) A->done[gs] = done;
-      if (A->n_alive) A->n_alive[gs] = n_alive;
+      if (k_done) k_done[gs] = done;
+      if (k_n_alive) k_n_alive[gs] = n_alive;
     }
-    do_reset = done && A->auto_reset && valid;
+    do_reset = done && k_auto_reset && valid;
   }
 
   // ---- 11. auto-reset of finished envs (sim/torch_sim.py:178-420)
@@ -771,8 +848,8 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
         philox_block(A->seed, env_id, A->epoch, STREAM_RESET_MISC, (uint32_t)min(l, 2), ub);
         float u[12];
 #pragma unroll
-        for (int j = 0; j < 12; ++j) u[j] = __shfl(ub[j % 4], (lane & ~15) + j / 4);
-        if (l < P) {
+        for (int j = 0; j < 12; ++j) u[j] = __shfl(ub[j % 4], (lane & ~(L - 1)) + j / 4);
+        if (lr < P) {
           float py[P], px[P];
 #pragma unroll
           for (int i = 0; i < P; ++i) {
@@ -787,11 +864,11 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
           float ub1 = u[1], ub2 = u[2];
 #pragma unroll
           for (int i = 1; i < P; ++i)
-            if (l == i) { ub1 = u[1 + 2 * i]; ub2 = u[2 + 2 * i]; }
+            if (lr == i) { ub1 = u[1 + 2 * i]; ub2 = u[2 + 2 * i]; }
           const int bc = CF->bombs_lo + min((int)floorf(ub1 * (float)bspan), bspan - 1);
           const int zc = CF->blast_lo + min((int)floorf(ub2 * (float)zspan), zspan - 1);
-          r.y = self<P>(py, l);
-          r.x = self<P>(px, l);
+          r.y = self<P>(py, lr);
+          r.x = self<P>(px, lr);
           r.alive = 1;
           r.hp = CF->max_hp;
           r.since = CF->spawn_cooldown;
@@ -821,17 +898,17 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
         philox_block(A->seed, env_id, A->epoch, STREAM_RESET_MISC, (uint32_t)min(l, 4), ub);
         float u[19];
 #pragma unroll
-        for (int j = 0; j < 19; ++j) u[j] = __shfl(ub[j % 4], (lane & ~15) + j / 4);
+        for (int j = 0; j < 19; ++j) u[j] = __shfl(ub[j % 4], (lane & ~(L - 1)) + j / 4);
         int kind = 1;
         bool pure = false;
-        if (CF->corridor) {
+        if (corridor) {
           kind = u[0] < CF->thr_open ? 1 : u[0] < CF->thr_ring ? 2 : 0;
           pure = u[0] < CF->thr_pure;
         }
         const int T = CF->top_wall_rows;
         const int top = CF->random_wall_rows ? min((int)floorf(u[1] * (float)(T + 1)), T) : T;
         const int bot = CF->random_wall_rows ? T - top : 0;
-        const int sp_mode = CF->corridor ? 0 : 1;
+        const int sp_mode = corridor ? 0 : 1;
         const int sp_kind = kind == 0 ? 0 : kind == 2 ? 2 : 1;
         auto near_spawn = [&](int set, int rr, int col) {
           bool nbh = false;
@@ -920,15 +997,15 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
                       CF->ring_brick_density;
           } else {
             wall = ((obst >> k) & 1u) && !near_spawn(sp_mode, rr, col);
-            crate = CF->corridor && CF->open_crate_cross &&
+            crate = corridor && CF->open_crate_cross &&
                     (rr == cy - 1 || rr == cy || col == cx - 1 || col == cx) && !near_spawn(1, rr, col);
           }
           cwl[c] = (wall ? F_WALL : 0u) | (brick ? F_BRICK : 0u) | (crate ? F_CRATE : 0u) | EMPTY_CELL;
         }
         int b0, z0;
         float s0;
-        if (!CF->corridor) {
-          b0 = CF->max_bombs; z0 = CF->blast; s0 = 1.0f;
+        if (!corridor) {
+          b0 = CF->max_bombs; z0 = cfg_blast; s0 = 1.0f;
         } else if (kind == 1) {
           b0 = CF->open_growth_bombs; z0 = CF->open_growth_blast; s0 = CF->open_growth_speed;
         } else {
@@ -944,8 +1021,8 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
           s1 = fminf(s0 * CF->opp_hist_mult, CF->growth_speed_max);
         }
         const bool swap = u[2] < 0.5f;
-        if (l < P) {
-          const int i = l;
+        if (lr < P) {
+          const int i = lr;
           const int si = (swap && i < 2) ? 1 - i : i;
           float sy = CF->ref_spawn_y[sp_kind][0], sx = CF->ref_spawn_x[sp_kind][0];
 #pragma unroll
@@ -972,7 +1049,7 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
           }
         }
         t = 0;
-        if (CF->corridor)
+        if (corridor)
           crate_prob = kind == 1 ? 1.0f : kind == 2 ? CF->ring_crate_prob : CF->growth_crate_prob;
         map_kind = kind;
       }
@@ -985,6 +1062,9 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
 
   // ---- 12. the cells of the final state back into registers; legality
   // masks (sim/obs.py:139-229): lane = me*4 + probe (up, down, left, right)
+  const auto m_step_len = CF->step_len;
+  const auto m_move_mask = A->move_mask;
+  const auto m_bomb_mask = A->bomb_mask;
   livepack = 0;
 #pragma unroll
   for (int k = 0; k < KC; ++k) {
@@ -993,7 +1073,7 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
     const int o = cw_owner(cw[k]);
     if (cw_fuse(cw[k]) > 0 && o >= 0 && o < P) livepack += 1 << (8 * o);
   }
-  livepack = row_sum(livepack);
+  livepack = env_sum<L>(livepack);
   float y_b[P], x_b[P];
   int al_b[P], bcap_b[P];
   bcast_allf<P>(r.y, y_b);
@@ -1001,33 +1081,36 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
   bcast_all<P>(r.alive, al_b);
   bcast_all<P>(r.bcap, bcap_b);
   {
-    const int me = l >> 2, pr = l & 3;
-    if (me < P && valid) {
+    const int me = lr >> 2, pr = lr & 3;
+    if (me < P && l < 16 && valid) {
       const float y = self<P>(y_b, me), x = self<P>(x_b, me);
       const bool al = sel<P>(al_b, me) != 0;
-      const float st = CF->step_len;
+      const float st = m_step_len;
       const float d = (pr & 1) ? st : -st;
       const bool vert = pr < 2;
       const float own = vert ? y : x;
       const float nv = resolve_axis<H, W>(cwl, own + d, d, y, x, rad, vert);
       const bool moved = fabsf(nv - own) > 2e-4f;
-      if (A->move_mask) {
-        A->move_mask[(gs * P + me) * 5 + pr] = al ? moved : 1;
-        if (pr == 0) A->move_mask[(gs * P + me) * 5 + 4] = 1;
+      if (m_move_mask) {
+        m_move_mask[(gs * P + me) * 5 + pr] = al ? moved : 1;
+        if (pr == 0) m_move_mask[(gs * P + me) * 5 + 4] = 1;
       }
-      if (pr == 0 && A->bomb_mask) {
+      if (pr == 0 && m_bomb_mask) {
         const int flat = min(max((int)floorf(y) * W + (int)floorf(x), 0), C - 1);
         const uint32_t wc = cwl[flat];
         const bool under = cw_fuse(wc) > 0;
         const int live_me = (livepack >> (8 * me)) & 0xFF;
         const bool can = !under && !(wc & F_BRICK) && live_me < sel<P>(bcap_b, me);
-        A->bomb_mask[(gs * P + me) * 2 + 0] = 1;
-        A->bomb_mask[(gs * P + me) * 2 + 1] = (can && al) || !al;
+        m_bomb_mask[(gs * P + me) * 2 + 0] = 1;
+        m_bomb_mask[(gs * P + me) * 2 + 1] = (can && al) || !al;
       }
     }
   }
 
   // ---- 13. observation (sim/obs.py:25-136): the float32 danger of my
+  const auto o_growth_bombs_max = CF->growth_bombs_max;
+  const auto o_max_steps = CF->max_steps;
+  const auto o_obs = A->obs;
   // cells, the per-player values, then the channels in staging passes
   float dv[KC];
 #pragma unroll
@@ -1071,29 +1154,37 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
     const float invf = (r.inv > 0 && al) ? 1.0f : 0.0f;
     h_inv = h16(invf);
     h_avail = h16(__fdiv_rn(avail, cap) * gate);
-    h_cap = h16(__fdiv_rn(cap, (float)CF->growth_bombs_max) * gate);
+    h_cap = h16(__fdiv_rn(cap, (float)o_growth_bombs_max) * gate);
   }
   const uint16_t h_one = h16(1.0f);
-  const uint16_t h_t = h16(__fdiv_rn((float)t, (float)CF->max_steps));
+  const uint16_t h_t = h16(__fdiv_rn((float)t, (float)o_max_steps));
   wave_sync();
 
-  if (A->obs) {
+  if (o_obs) {
     const size_t obs_base = gs * OBS;
 #pragma unroll
     for (int pass = 0; pass < G::NPASS; ++pass) {
       const int ch0 = pass * CPP;
       const int nch = (G::NCH - ch0) < CPP ? (G::NCH - ch0) : CPP;
       const int nbytes = nch * C * 2;
-      uint16_t* dst = A->obs + obs_base + (size_t)ch0 * C;
+      uint16_t* dst = o_obs + obs_base + (size_t)ch0 * C;
       const int opad = (int)(((uintptr_t)dst) & 15u);
       uint16_t* sb = reinterpret_cast<uint16_t*>(blk + opad);
       if (pass > 0) wave_sync();   // the previous pass's copy-out has read the block
+      // Every cell of the cell-parallel channels is written below; only the
+      // players' sparse channels (splat [0, P) and the player-cell channels
+      // [2P + 4, 5P + 4), which never share a pass) start from zero.
       {
+        constexpr int SLO = 0, SHI = P, QLO = 2 * P + 4, QHI = 5 * P + 4;
+        const int zlo = max(SLO, ch0) < min(SHI, ch0 + nch) ? max(SLO, ch0)
+                      : max(QLO, ch0) < min(QHI, ch0 + nch) ? max(QLO, ch0) : ch0;
+        const int zhi = max(SLO, ch0) < min(SHI, ch0 + nch) ? min(SHI, ch0 + nch)
+                      : max(QLO, ch0) < min(QHI, ch0 + nch) ? min(QHI, ch0 + nch) : ch0;
+        const int b0 = (opad + (zlo - ch0) * C * 2) & ~15;
+        const int b1 = min((opad + (zhi - ch0) * C * 2 + 15) & ~15, G::BLOCK);
         uint4* z = reinterpret_cast<uint4*>(blk);
-        constexpr int N16 = G::BLOCK / 16;
-        for (int i = l; i < N16; i += L) z[i] = make_uint4(0u, 0u, 0u, 0u);
+        for (int i = b0 / 16 + l; i < b1 / 16; i += L) z[i] = make_uint4(0u, 0u, 0u, 0u);
       }
-      wave_sync();
       // cell-parallel channels (relative to ch0): walls+bricks, danger, time,
       // crates, and the own-bomb fuse channels
       constexpr int CW_CH = 2 * P, DG_CH = 2 * P + 1, T_CH = 2 * P + 2, CR_CH = 2 * P + 3;
@@ -1102,15 +1193,18 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
         const int c = l + L * k;
         if (c >= C) continue;
         const uint32_t w = cw[k];
-        if (CW_CH >= ch0 && CW_CH < ch0 + nch && (w & (F_WALL | F_BRICK)))
-          sb[(CW_CH - ch0) * C + c] = h_one;
-        if (DG_CH >= ch0 && DG_CH < ch0 + nch && dv[k] != 0.0f) sb[(DG_CH - ch0) * C + c] = h16(dv[k]);
+        if (CW_CH >= ch0 && CW_CH < ch0 + nch)
+          sb[(CW_CH - ch0) * C + c] = (w & (F_WALL | F_BRICK)) ? h_one : (uint16_t)0;
+        if (DG_CH >= ch0 && DG_CH < ch0 + nch) sb[(DG_CH - ch0) * C + c] = h16(dv[k]);
         if (T_CH >= ch0 && T_CH < ch0 + nch) sb[(T_CH - ch0) * C + c] = h_t;
-        if (CR_CH >= ch0 && CR_CH < ch0 + nch && (w & F_CRATE)) sb[(CR_CH - ch0) * C + c] = h_one;
+        if (CR_CH >= ch0 && CR_CH < ch0 + nch)
+          sb[(CR_CH - ch0) * C + c] = (w & F_CRATE) ? h_one : (uint16_t)0;
         if (P + P > ch0 && P < ch0 + nch) {
           const int f = cw_fuse(w), o = cw_owner(w);
-          if (f > 0 && o >= 0 && o < P && P + o >= ch0 && P + o < ch0 + nch)
-            sb[(P + o - ch0) * C + c] = h16(__fdiv_rn((float)f, fmax_f));
+          const uint16_t hq = f > 0 ? h16(qdiv(f, fmax_f, frcp)) : (uint16_t)0;
+#pragma unroll
+          for (int i = 0; i < P; ++i)
+            if (P + i >= ch0 && P + i < ch0 + nch) sb[(P + i - ch0) * C + c] = o == i ? hq : (uint16_t)0;
         }
       }
       // the players' channels, written after the cell-parallel ones
@@ -1134,8 +1228,16 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
         const int n16 = (nbytes - head) / 16;
         if (l * 2 < head)
           *reinterpret_cast<uint16_t*>(d8 + l * 2) = *reinterpret_cast<const uint16_t*>(src + l * 2);
-        for (int i = l; i < n16; i += L)
-          reinterpret_cast<uint4*>(d8 + head)[i] = reinterpret_cast<const uint4*>(src + head)[i];
+        // all of the lane's 16-byte units are read before the first store
+        constexpr int NU = (CPP * C * 2 / 16 + L - 1) / L;
+        const uint4* s16 = reinterpret_cast<const uint4*>(src + head);
+        uint4* d16 = reinterpret_cast<uint4*>(d8 + head);
+        uint4 u16[NU];
+#pragma clang loop unroll(full)
+        for (int m = 0; m < NU; ++m) u16[m] = s16[min(l + L * m, n16 - 1)];
+#pragma clang loop unroll(full)
+        for (int m = 0; m < NU; ++m)
+          if (l + L * m < n16) d16[l + L * m] = u16[m];
         const int tail0 = head + n16 * 16;
         if (tail0 + l * 2 < nbytes)
           *reinterpret_cast<uint16_t*>(d8 + tail0 + l * 2) =
@@ -1167,16 +1269,22 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
 }  // namespace grp
 
 // STEP launch of the group kernel: XCD_ROWS-env row blocks, a multiple of 8
-// of them (one per XCD in turn), XCD_ROWS / 4 one-wavefront workgroups each.
-template <int H, int W, int P>
-int launch_step_group(const qqt_sim_config* cfg, const qqt_tick_args* a, hipStream_t st) {
+// of them (one per XCD in turn), one-wavefront workgroups.  Up to
+// GROUP32_MAX_ENVS envs an env takes 32 lanes (two envs per wavefront: at
+// 5632 envs, 2816 wavefronts keep every SIMD at two or three of them and
+// halve the per-wavefront cell work); larger batches take 16 lanes per env
+// (four per wavefront), which keeps 16,384 envs resident in one round.
+constexpr int GROUP32_MAX_ENVS = 8192;
+
+template <int H, int W, int P, int L>
+int launch_group(const qqt_sim_config* cfg, const qqt_tick_args* a, hipStream_t st) {
   const int nrb = (a->n_envs + XCD_ROWS - 1) / XCD_ROWS;
-  const int blocks = ((nrb + 7) / 8) * 8 * (XCD_ROWS / grp::EPW);
+  const int blocks = ((nrb + 7) / 8) * 8 * (XCD_ROWS / (64 / L));
   const dim3 grid(blocks), block(64);
   if (cfg->map_kind == QQT_MAP_REFERENCE)
-    QQT_LAUNCH(QQT_KERNEL_TICK, (grp::tick_group_kernel<H, W, P, 1>), grid, block, st, *cfg, *a);
+    QQT_LAUNCH(QQT_KERNEL_TICK, (grp::tick_group_kernel<H, W, P, 1, L>), grid, block, st, *cfg, *a);
   else
-    QQT_LAUNCH(QQT_KERNEL_TICK, (grp::tick_group_kernel<H, W, P, 0>), grid, block, st, *cfg, *a);
+    QQT_LAUNCH(QQT_KERNEL_TICK, (grp::tick_group_kernel<H, W, P, 0, L>), grid, block, st, *cfg, *a);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     char msg[256];
@@ -1184,6 +1292,12 @@ int launch_step_group(const qqt_sim_config* cfg, const qqt_tick_args* a, hipStre
     return fail(QQT_E_LAUNCH, msg);
   }
   return QQT_OK;
+}
+
+template <int H, int W, int P>
+int launch_step_group(const qqt_sim_config* cfg, const qqt_tick_args* a, hipStream_t st) {
+  return a->n_envs <= GROUP32_MAX_ENVS ? launch_group<H, W, P, 32>(cfg, a, st)
+                                       : launch_group<H, W, P, 16>(cfg, a, st);
 }
 
 template int launch_step_group<13, 13, 2>(const qqt_sim_config*, const qqt_tick_args*, hipStream_t);
