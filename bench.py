@@ -306,8 +306,14 @@ def main():
         return main_cnn(args, torch, dev)
     n, K, W = args.envs, args.steps, args.warmup
     cfg, spec, roll = build_workload(n, args.seed, dev)
-    for _ in range(W):
+    # The timed window must see the whole tick: bombs placed from the first
+    # tick explode at tick cfg.fuse, so at least cfg.fuse + 2 untimed ticks
+    # run before the warm-up, whatever --warmup is.
+    preroll = cfg.fuse + 2
+    for _ in range(preroll + W):
         roll.step()
+    stats = torch.zeros(3, dtype=torch.int64, device=dev)
+    roll._tick.tick_stats = stats.data_ptr()   # the tick counts what the timed steps did
     torch.cuda.synchronize()
 
     # Both launches of every EVERY-th timed step (`sampled`) carry a HIP event pair on
@@ -323,9 +329,11 @@ def main():
         roll.launch_tick()
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
+    roll._tick.tick_stats = 0
     kms = kernel_ms()
     act_ms, tick_ms = kms["mlp_act_kernel"], kms["tick_kernel"]
     done_frac = float(roll.done.float().mean())
+    window = timed_window(stats, preroll + W, K, n)
 
     if args.copy_calibrate:
         _calibration_copy(torch, dev)
@@ -380,8 +388,18 @@ def main():
         "kernels": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                         for kk, vv in v.items()} for k, v in kernels.items()},
         "done_fraction_last_tick": done_frac,
+        "timed_window": window,
     }
     print(json.dumps(out), flush=True)
+
+
+def timed_window(stats, untimed, steps, n):
+    """What the timed ticks did, from the tick kernel's own launch totals:
+    bombs exploded, players died and envs auto-reset over the timed steps."""
+    ex, dead, resets = (int(v) for v in stats.tolist())
+    return {"ticks_before_timing": untimed, "timed_ticks": steps, "exploded_bombs": ex,
+            "deaths": dead, "auto_resets": resets,
+            "exploded_bombs_per_env_tick": round(ex / (n * steps), 5)}
 
 
 # Kernel launches of one eager BatchedSim.step of the reference on a GPU, as
@@ -452,10 +470,13 @@ def main_stress(args, torch, dev):
     K, W = args.steps, args.warmup
     cfg = corridor_training_config()
     sim = HipBatchedSim(cfg, n, device=dev, seed=args.seed, map_spec=BOMB_STRESS_40)
-    acts = stress_actions(n, K + W, args.seed, dev)
+    U = cfg.fuse + 2 + W      # untimed ticks: the timed window sees the whole tick
+    acts = stress_actions(n, K + U, args.seed, dev)
     loop = TickLoop(sim)
-    for k in range(W):
+    for k in range(U):
         loop.launch_tick(acts[k])
+    stats = torch.zeros(3, dtype=torch.int64, device=dev)
+    loop._tick.tick_stats = stats.data_ptr()
     torch.cuda.synchronize()
     _capi.timing_arm(0)          # creates the event pool outside the timed region
     torch.cuda.synchronize()
@@ -463,9 +484,10 @@ def main_stress(args, torch, dev):
     for k in range(K):
         if sampled(k, K):
             _capi.timing_arm(1)
-        loop.launch_tick(acts[W + k])
+        loop.launch_tick(acts[U + k])
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
+    loop._tick.tick_stats = 0
     tick_ms = kernel_ms()["tick_kernel"]
     if args.copy_calibrate:
         _calibration_copy(torch, dev)
@@ -488,6 +510,7 @@ def main_stress(args, torch, dev):
         "cpu_baseline": cpu,
         "kernels": {"tick_kernel": {"us": round(tick_ms * 1e3, 4),
                                     "bytes_per_env": TICK_BYTES_PER_ENV}},
+        "timed_window": timed_window(stats, U, K, n),
     }
     print(json.dumps(out), flush=True)
 

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 18
+#define QQT_ABI_VERSION 19
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -135,6 +135,11 @@ typedef struct qqt_tick_args {
   float* danger_out;          /* OBSERVE: [N][H][W] float32 danger map of the current
                                  state (blast.danger_map as BatchedSim._danger_c
                                  computes it, sim/torch_sim.py:732-762), or NULL */
+  int64_t* tick_stats;        /* STEP: [3] incremented by this launch's exploded bombs
+                                 (info["trig"] cells), deaths (info["died"]) and
+                                 auto-resets (done envs reset), summed over envs; or
+                                 NULL.  For benchmark harnesses that report what their
+                                 timed ticks did; no reference counterpart. */
 } qqt_tick_args;
 
 /* MLP actor/critic forward (+ masked sampling).  Weights are the packed

@@ -68,17 +68,11 @@ struct __align__(16) Lds {
   };
   uint32_t cw[G::EPW][G::C];
   float dng[G::EPW][G::C];   // danger map
-  uint32_t cov[G::EPW][G::CW4];  // byte maps viewed as dwords for clearing
-  uint32_t trg[G::EPW][G::CW4];
   uint8_t list[G::EPW][G::C];
-  int32_t nlist[G::EPW];
   int32_t pl[G::EPW][P][QQT_P_SLOTS];
   int32_t ev[G::EPW][QQT_E_SLOTS];
-  int32_t alive0[G::EPW][P], hp0[G::EPW][P], placed[G::EPW][P], live[G::EPW][P];
-  int32_t fpre[G::EPW][P], fpost[G::EPW][P], act_m[G::EPW][P], act_b[G::EPW][P];
-  float pbonus[G::EPW][P];
+  int32_t alive0[G::EPW][P], live[G::EPW][P], fpre[G::EPW][P], act_b[G::EPW][P];
   int32_t done[G::EPW];
-  int32_t boom[G::EPW];
 };
 
 // ---------------------------------------------------------------- lane helpers
@@ -129,12 +123,10 @@ __device__ __forceinline__ int build_list(uint8_t* list, int e, int l, Pred pred
 }
 
 // ---------------------------------------------------------------- kernel
-// KMODE fixes the mode at compile time for the two modes with an
-// instantiation of their own: QQT_MODE_STEP (the hot one, which then carries
-// no code of the other modes) and QQT_MODE_FLUSH (whose code lives only
-// there).  KMODE = -1 serves the other modes from a.mode.  MAPS selects the
-// reset's map source: 0 the templates, 1 the reference's map modes (each
-// kernel carries one of the two).
+// KMODE = QQT_MODE_FLUSH fixes the flush at compile time (its code lives
+// only in that instantiation); KMODE = -1 serves RESET, OBSERVE and PROBE
+// from a.mode.  MAPS selects the reset's map source: 0 the templates, 1 the
+// reference's map modes (each kernel carries one of the two).
 template <int H, int W, int P, int LPE, int WPB, int KMODE, int MAPS>
 __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf, const qqt_tick_args a) {
   using G = Geo<H, W, P, LPE>;
@@ -168,8 +160,6 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
 
   uint32_t* cw = s.cw[e];
   int32_t(*pl)[QQT_P_SLOTS] = s.pl[e];
-  uint8_t* cov = reinterpret_cast<uint8_t*>(s.cov[e]);
-  uint8_t* trg = reinterpret_cast<uint8_t*>(s.trg[e]);
   uint8_t* list = s.list[e];
 
   // ---- load
@@ -182,32 +172,18 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
     pl[i / QQT_P_SLOTS][i % QQT_P_SLOTS] = valid ? a.players[(size_t)g * P * QQT_P_SLOTS + i] : 0;
   if (l < QQT_E_SLOTS) s.ev[e][l] = valid ? a.envs[(size_t)g * QQT_E_SLOTS + l] : 0;
   if (l == 0) s.done[e] = 0;
-  // per-player inputs, issued together with the state loads
-  int in_mv = 4, in_bb = 0;
-  float in_uh = 0.0f, in_ug = 0.0f;
-  if (mode == QQT_MODE_STEP || mode == QQT_MODE_PROBE) {
-    if (l < P && valid) {
-      if (a.actions) {
-        in_mv = (int)a.actions[((size_t)g * P + l) * 2 + 0];
-        in_bb = (int)a.actions[((size_t)g * P + l) * 2 + 1];
-      } else if (a.actions_i8) {
-        in_mv = a.actions_i8[((size_t)g * P + l) * 2 + 0];
-        in_bb = a.actions_i8[((size_t)g * P + l) * 2 + 1];
-      }
-      if (a.crate_u) {
-        in_uh = a.crate_u[((size_t)l * 2 + 0) * a.n_envs + g];
-        in_ug = a.crate_u[((size_t)l * 2 + 1) * a.n_envs + g];
-      }
-    }
-  }
+  // PROBE's bomb actions, issued together with the state loads
+  int in_bb = 0;
+  if (mode == QQT_MODE_PROBE && l < P && valid)
+    in_bb = a.actions ? (int)a.actions[((size_t)g * P + l) * 2 + 1]
+                      : a.actions_i8[((size_t)g * P + l) * 2 + 1];
   wave_sync();
 
-  if (mode == QQT_MODE_STEP || mode == QQT_MODE_PROBE) {
-    // ---- 1. snapshots, actions, fuse countdown, live counts
+  if (mode == QQT_MODE_PROBE) {
+    // fuse countdown, live counts, placement as the tick makes them
+    // (sim/torch_sim.py:1357-1402), then the largest bomb_blast
     if (l < P) {
       s.alive0[e][l] = pl[l][QQT_P_ALIVE];
-      s.hp0[e][l] = pl[l][QQT_P_HP];
-      s.act_m[e][l] = in_mv;
       s.act_b[e][l] = in_bb;
       const float y = __int_as_float(pl[l][QQT_P_Y]), x = __int_as_float(pl[l][QQT_P_X]);
       s.fpre[e][l] = min(max((int)floorf(y) * W + (int)floorf(x), 0), C - 1);
@@ -238,13 +214,12 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
         const uint32_t w = cw[idx];
         const bool ok = s.alive0[e][me] && s.act_b[e][me] == 1 && cw_fuse(w) <= 0 &&
                         !(w & F_BRICK) && s.live[e][me] < pl[me][QQT_P_BOMBS_CAP];
-        s.placed[e][me] = ok;
         if (ok) cw[idx] = cw_make(w, cf.fuse, me, pl[me][QQT_P_BLAST_CAP]);
       }
     }
     wave_sync();
 
-    if (mode == QQT_MODE_PROBE) {
+    {   // PROBE: the largest bomb_blast after placement
       int mb = 0;
 #pragma unroll
       for (int k = 0; k < KMAX; ++k) {
@@ -255,230 +230,6 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
       if (valid && l == 0) a.probe_out[g] = mb;
       return;
     }
-
-    // ---- 3. placement reward (sim/torch_sim.py:1263-1355): lane = me*4 + dir
-    {
-      const int me = l >> 2, d = l & 3;
-      float chain = 0.0f;
-      int cover_bits = 0;
-      if (me < P && s.placed[e][me]) {
-        const int s0 = s.fpre[e][me];
-        const uint32_t w0 = cw[s0];
-        if (!(w0 & (F_WALL | F_BRICK))) {
-          const int r0 = s0 / W, c0 = s0 % W;
-          const int dr = dir_dr(d), dc = dir_dc(d);
-          auto visit = [&](int x) {
-#pragma unroll
-            for (int o = 0; o < P; ++o)
-              if (o != me && s.fpre[e][o] == x && s.alive0[e][o]) cover_bits |= 1 << o;
-            const uint32_t wx = cw[x];
-            const int fx = cw_fuse(wx);
-            if (fx > 0 && cw_owner(wx) >= 0) {
-              int pm = 0;
-#pragma unroll
-              for (int i = 0; i < P; ++i)
-                if (s.fpre[e][i] == x) pm = s.placed[e][i];
-              if (!pm) {
-                float frac = __fdiv_rn((float)fx, fmax_f);
-                frac = fminf(fmaxf(frac, 0.0f), 1.0f);
-                const float wt = cf.chain_time_factor + cf.chain_time_rest * (1.0f - frac);
-                chain = chain + wt;
-              }
-            }
-          };
-          if (d == 0) visit(s0);
-          const int b = blast_of(w0, cf.blast);
-          for (int k = 1; k <= b; ++k) {
-            const int rr = r0 + k * dr, cc = c0 + k * dc;
-            if (rr < 0 || rr >= H || cc < 0 || cc >= W) break;
-            const int x = rr * W + cc;
-            const uint32_t wx = cw[x];
-            if (wx & F_WALL) break;
-            visit(x);
-            if (cw_solid(wx)) break;
-          }
-        }
-      }
-      chain += __shfl_xor(chain, 1, LPE);
-      chain += __shfl_xor(chain, 2, LPE);
-      cover_bits |= __shfl_xor(cover_bits, 1, LPE);
-      cover_bits |= __shfl_xor(cover_bits, 2, LPE);
-      if (me < P && d == 0) {
-        float bonus = 0.0f;
-        if (s.placed[e][me]) {
-          float cover = 0.0f, dist = 0.0f;
-#pragma unroll
-          for (int o = 0; o < P; ++o) cover += (float)((cover_bits >> o) & 1);
-          if (cf.place_dist_reward > 0.0f) {
-            const float ym = floorf(__int_as_float(pl[me][QQT_P_Y]));
-            const float xm = floorf(__int_as_float(pl[me][QQT_P_X]));
-            const bool cool = pl[me][QQT_P_SINCE_BOMB] >= cf.place_dist_cooldown;
-            for (int o = 0; o < P; ++o) {
-              if (o == me) continue;
-              const float dy = ym - floorf(__int_as_float(pl[o][QQT_P_Y]));
-              const float dx = xm - floorf(__int_as_float(pl[o][QQT_P_X]));
-              const float dd = sqrtf(dy * dy + dx * dx);
-              const bool under = (cover_bits >> o) & 1;
-              const bool ok = !under && dd < cf.place_dist_radius && cool && s.alive0[e][o];
-              const float gain = 1.0f - __fdiv_rn(dd, cf.place_dist_radius);
-              dist = dist + (ok ? fmaxf(gain, 0.0f) : 0.0f);
-            }
-          }
-          bonus = (cf.place_cover_reward * cover + cf.place_dist_reward * dist) +
-                  cf.place_chain_reward * chain;
-        }
-        s.pbonus[e][me] = bonus * (float)s.alive0[e][me];
-      }
-    }
-    wave_sync();
-
-    // ---- 4. since_bomb; 5. movement (sim/move.py:234-279); explosion list
-    if (l < 2 * P) {  // lane = player * 2 + axis; both axes start from the pre-move box
-      const int me = l >> 1;
-      const bool vert = (l & 1) == 0;
-      const float y = __int_as_float(pl[me][QQT_P_Y]), x = __int_as_float(pl[me][QQT_P_X]);
-      const int mv = s.act_m[e][me];
-      const int mc = min(max(mv, 0), 4);
-      const float spd = __int_as_float(pl[me][QQT_P_SPD]);
-      const float st = cf.step_len;
-      float tv = 0.0f;
-      if (vert) { if (mc == 0) tv = -st; else if (mc == 1) tv = st; }
-      else { if (mc == 2) tv = -st; else if (mc == 3) tv = st; }
-      float dv = tv * spd;
-      if (!(s.alive0[e][me] && mv != 4)) dv = 0.0f;
-      const float own = vert ? y : x;
-      const float nv = resolve_axis<H, W>(cw, own + dv, dv, y, x, rad, vert);
-      float ov = dv != 0.0f ? nv : own;
-      ov = fminf(fmaxf(ov, rad), vert ? cf.pos_hi_y : cf.pos_hi_x);
-      if (vert) {
-        int sb = pl[me][QQT_P_SINCE_BOMB] + 1;
-        if (s.placed[e][me]) sb = 0;
-        pl[me][QQT_P_SINCE_BOMB] = sb;
-        pl[me][QQT_P_Y] = __float_as_int(ov);
-      } else {
-        pl[me][QQT_P_X] = __float_as_int(ov);
-      }
-    }
-    for (int i = l; i < G::CW4; i += LPE) { s.cov[e][i] = 0u; s.trg[e][i] = 0u; }
-    // bomb cells: live (fuse > 0) or due (fuse == 0 with an owner)
-    const int nl = build_list<G>(list, e, l, [&](int c) {
-      const uint32_t w = cw[c];
-      return cw_fuse(w) > 0 || cw_owner(w) >= 0;
-    });
-    wave_sync();
-
-    // ---- 6. explosions (sim/blast.py:101-155), fixed synchronous rounds
-    // rays of the list entries whose trigger stamp is `stamp`, one
-    // (entry, direction) per lane: walls stop a ray before the cell, other
-    // solids after it
-    auto fire = [&](uint8_t stamp) {
-      for (int it = l; it < 4 * nl; it += LPE) {
-        const int src = list[it >> 2], d = it & 3;
-        const uint32_t w = cw[src];
-        const int b = blast_of(w, cf.blast);
-        if (trg[src] != stamp || (w & (F_WALL | F_BRICK)) || b > a.resolve_tiers) continue;
-        walk_ray<H, W>(cw, src, d, b, 1, [&](int, int x, uint32_t wx) {
-          if (wx & F_WALL) return false;
-          cov[x] = 1;
-          return !cw_solid(wx);
-        });
-      }
-    };
-    bool boom = false;
-    for (int j = l; j < nl; j += LPE) {
-      const int c = list[j];
-      const uint32_t w = cw[c];
-      if (cw_fuse(w) == 0 && cw_owner(w) >= 0) {
-        trg[c] = 1;
-        if (!(w & (F_WALL | F_BRICK))) cov[c] = 1;
-        boom = true;
-      }
-    }
-    const bool env_boom = env_bits<LPE>(boom, e) != 0;
-    wave_sync();
-    if (__any(env_boom)) {
-      fire(1);
-      // chain rounds: entries triggered in round r carry stamp r + 2 (any
-      // nonzero stamp means triggered), so the rays of one round are spread
-      // over all lanes
-      const int rounds = min(cf.max_chain - 1, cf.chain_cap_rounds);
-      for (int r = 0; r < rounds; ++r) {
-        wave_sync();
-        bool newly = false;
-        for (int j = l; j < nl; j += LPE) {
-          const int c = list[j];
-          if (cw_fuse(cw[c]) > 0 && cov[c] && !trg[c]) {
-            trg[c] = (uint8_t)(r + 2);
-            newly = true;
-          }
-        }
-        if (!__any(newly)) break;
-        wave_sync();
-        fire((uint8_t)(r + 2));
-      }
-      wave_sync();
-      // ---- 7. burnt bricks (corridor: into crates)
-      if (env_boom) {
-#pragma unroll
-        for (int k = 0; k < KMAX; ++k) {
-          const int c = l + LPE * k;
-          if (c < C && cov[c]) {
-            uint32_t w = cw[c];
-            if (w & F_BRICK) {
-              if (cf.corridor) w |= F_CRATE;
-              w &= ~F_BRICK;
-              cw[c] = w;
-            }
-          }
-        }
-      }
-    }
-    // ---- 8. damage at the post-move centre cell (sim/torch_sim.py:1007-1034)
-    if (l < P) {
-      const int me = l;
-      const float y = __int_as_float(pl[me][QQT_P_Y]), x = __int_as_float(pl[me][QQT_P_X]);
-      const int flat = min(max((int)floorf(y) * W + (int)floorf(x), 0), C - 1);
-      s.fpost[e][me] = flat;
-      const bool hit = s.alive0[e][me] && cov[flat];
-      const bool hit_eff = hit && pl[me][QQT_P_INVULN] <= 0;
-      const int hp_new = max(pl[me][QQT_P_HP] - (int)hit_eff, 0);
-      const bool died = hit_eff && hp_new == 0;
-      pl[me][QQT_P_HP] = hp_new;
-      pl[me][QQT_P_ALIVE] = s.alive0[e][me] && !died;
-      int inv = max(pl[me][QQT_P_INVULN] - 1, 0);
-      if (hit_eff) inv = cf.invuln_ticks;
-      pl[me][QQT_P_INVULN] = inv;
-      if (valid && a.died) a.died[(size_t)g * P + me] = died;
-    }
-    // ---- 9. info bitsets (bit c of 8 words per env), then clear exploded cells
-    if (a.covered || a.triggered) {
-      uint32_t myc = 0, myt = 0;
-#pragma unroll
-      for (int k = 0; k < KMAX; ++k) {
-        const int c = l + LPE * k;
-        const uint64_t bc = env_bits<LPE>(c < C && cov[c], e);
-        const uint64_t bt = env_bits<LPE>(c < C && trg[c], e);
-        // chunk k covers cells [LPE*k, LPE*k + LPE): word (LPE*k)/32 + q
-#pragma unroll
-        for (int q = 0; q < (LPE + 31) / 32; ++q) {
-          const int word = (LPE * k) / 32 + q;
-          const int shift = (LPE >= 32) ? 0 : (16 * (k & 1));
-          const uint32_t vc = (uint32_t)(bc >> (32 * q)) << shift;
-          const uint32_t vt = (uint32_t)(bt >> (32 * q)) << shift;
-          myc = (word == l) ? (myc | vc) : myc;
-          myt = (word == l) ? (myt | vt) : myt;
-        }
-      }
-      if (valid && l < 8) {
-        if (a.covered) a.covered[(size_t)g * 8 + l] = myc;
-        if (a.triggered) a.triggered[(size_t)g * 8 + l] = myt;
-      }
-    }
-    for (int j = l; j < nl; j += LPE) {
-      const int c = list[j];
-      if (trg[c]) cw[c] = cw_make(cw[c], 0, -1, 0);
-    }
-    wave_sync();
   }
 
   auto template_reset = [&]() {  // qqtsim/maps.py; re-init of sim/torch_sim.py:178-420
@@ -892,143 +643,13 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
     }
   }
 
-  if (mode == QQT_MODE_STEP) {
-    // ---- 10. time, rewards, growth, combo, terminal terms; lane i < P is player i
-    {
-      const int i = l;
-      const bool me_ok = i < P;
-      const float alpha = a.explore_coef;
-      const int t = s.ev[e][QQT_E_T] + 1;
-      // env-wide sums over the players, read by every lane (LDS broadcasts)
-      int n_alive = 0, dsum_int = 0, hsum_int = 0;
-      bool any_stood = false;
-#pragma unroll
-      for (int o = 0; o < P; ++o) {
-        const int hpo = pl[o][QQT_P_HP];
-        n_alive += pl[o][QQT_P_ALIVE] != 0;
-        dsum_int += max(s.hp0[e][o] - hpo, 0);
-        hsum_int += hpo;
-        any_stood |= cf.corridor && (cw[s.fpost[e][o]] & F_CRATE);
-      }
-      const bool done = (n_alive <= 1) || (t >= cf.max_steps);
-      const int ip = me_ok ? i : 0;
-      const int hp_i = pl[ip][QQT_P_HP];
-      const float dmg = (float)max(s.hp0[e][ip] - hp_i, 0);
-      const int fp = s.fpost[e][ip];
-      const uint32_t wcell = cw[fp];
-      const int stood = (cf.corridor && me_ok) ? ((wcell & F_CRATE) != 0) : 0;
-      if (me_ok) {
-        const float a0 = (float)(s.alive0[e][i] != 0);
-        const float dsum = (float)dsum_int;  // exact: a sum of small integers
-        const float dealt = dsum - dmg;
-        float r = (-cf.step_penalty) * a0;
-        r = r + cf.hit_reward * dealt;
-        r = r - cf.hit_reward * dmg;
-        r = r + (alpha * s.pbonus[e][i]) * a0;
-        if (cf.hit_attr_penalty > 0 && dmg > 0.0f && s.alive0[e][i]) {
-          const int pen = cf.hit_attr_penalty;
-          const int bc = pl[i][QQT_P_BOMBS_CAP], zc = pl[i][QQT_P_BLAST_CAP];
-          const float sp = __int_as_float(pl[i][QQT_P_SPD]);
-          const int nbc = max(bc - pen, pl[i][QQT_P_LO_BOMBS]);
-          const int nzc = max(zc - pen, pl[i][QQT_P_LO_BLAST]);
-          const float ns = fmaxf(sp - cf.hit_speed_drop, __int_as_float(pl[i][QQT_P_LO_SPD]));
-          const float lost_f = (float)((bc - nbc) + (zc - nzc)) +
-                               rintf(__fdiv_rn(sp - ns, cf.growth_speed_step));
-          pl[i][QQT_P_BOMBS_CAP] = nbc;
-          pl[i][QQT_P_BLAST_CAP] = nzc;
-          pl[i][QQT_P_SPD] = __float_as_int(ns);
-          pl[i][QQT_P_PENDING_LOST] += (int)lost_f;
-        }
-        r = r + (alpha * 0.0f) * a0;  // chain_blast_bonus term (0 in every supported config)
-        if (cf.corridor) {
-          r = r + (cf.brick_reward * (float)stood) * a0;
-          if (any_stood) {
-            float uh = in_uh, ug = in_ug;
-            if (!a.crate_u) {
-              float u4[4];
-              philox_block(a.seed, (uint32_t)g, a.tick, STREAM_CRATE, (uint32_t)((2 * i) >> 2), u4);
-              uh = u4[(2 * i) & 3];
-              ug = u4[(2 * i + 1) & 3];
-            }
-            const float prob = (wcell & F_REC) ? cf.recycle_crate_prob
-                                               : __int_as_float(s.ev[e][QQT_E_CRATE_PROB]);
-            const int h = stood && (uh < prob) && s.alive0[e][i];
-            const int attr = (int)floorf(ug * 3.0f);
-            pl[i][QQT_P_BOMBS_CAP] = min(pl[i][QQT_P_BOMBS_CAP] + (attr == 0) * h, cf.growth_bombs_max);
-            pl[i][QQT_P_BLAST_CAP] = min(pl[i][QQT_P_BLAST_CAP] + (attr == 1) * h, cf.growth_blast_max);
-            const float sp = __int_as_float(pl[i][QQT_P_SPD]) + (float)((attr == 2) * h) * cf.growth_speed_step;
-            pl[i][QQT_P_SPD] = __float_as_int(fminf(sp, cf.growth_speed_max));
-          }
-          cw[fp] = wcell & ~(F_CRATE | F_REC);
-        }
-        r = r - (a.danger_coef * s.dng[e][fp]) * a0;
-        if (cf.combo_reward > 0.0f) {
-          const int c = pl[i][QQT_P_COMBO];
-          if (dealt > 0.0f) {
-            const int gap = t - pl[i][QQT_P_LAST_HIT];
-            const float factor = powf(cf.combo_gap_factor, (float)max(gap, 0));
-            const int combo_now = c + 1;
-            const float pts = (((float)combo_now * cf.combo_reward) * factor) * fminf(dealt, 1.0f);
-            r = r + pts * a0;
-            pl[i][QQT_P_LAST_HIT] = t;
-            pl[i][QQT_P_COMBO] = combo_now;
-          } else {
-            r = r + 0.0f * a0;
-          }
-          if (dmg > 0.0f) pl[i][QQT_P_COMBO] = 0;
-        }
-        const bool death_done = done && n_alive == 1;
-        const bool all_alive = done && n_alive == P;
-        const bool al = pl[i][QQT_P_ALIVE] != 0;
-        int win = death_done && al, lose = death_done && !al;
-        const float hpf = (float)hp_i;
-        float tscale = alpha;
-        if (!cf.timeout_draw) {
-          bool gt = true, lt = false;
-          for (int o = 0; o < P; ++o) {
-            if (o == i) continue;
-            const float ho = (float)pl[o][QQT_P_HP];
-            gt = gt && (hpf > ho);
-            lt = lt || (hpf < ho);
-          }
-          win |= all_alive && gt;
-          lose |= all_alive && lt;
-          tscale = 1.0f;
-        }
-        const float diff = hpf - __fdiv_rn((float)hsum_int - hpf, (float)(P - 1));
-        if (cf.win_hp_scaled) {
-          const float base = cf.win_per_hp * diff;
-          r = r + (base * (float)death_done + (base * (float)all_alive) * tscale);
-        } else {
-          r = r + cf.win_bonus * ((float)win - (float)lose);
-          if (cf.timeout_draw) r = r + ((cf.win_per_hp * diff) * (float)all_alive) * tscale;
-        }
-        if (valid) {
-          if (a.reward) a.reward[(size_t)g * P + i] = r;
-          if (a.winner) a.winner[(size_t)g * P + i] = win;
-        }
-      }
-      if (l == 0) {
-        s.ev[e][QQT_E_T] = t;
-        if (valid) {
-          if (a.done) a.done[g] = done;
-          if (a.n_alive) a.n_alive[g] = n_alive;
-        }
-        s.done[e] = done && a.auto_reset && valid;
-      }
-    }
-  }
-  if (mode == QQT_MODE_STEP || mode == QQT_MODE_RESET) {
+  if (mode == QQT_MODE_RESET) {
     wave_sync();
     if (s.done[e]) {
       if constexpr (MAPS == 1) reference_reset();
       else template_reset();
     }
     wave_sync();
-    // hp fell this tick, judged on the post-reset record (the collect loop
-    // compares after step() returns)
-    if (mode == QQT_MODE_STEP && a.damaged && valid && l < P)
-      a.damaged[(size_t)g * P + l] = s.hp0[e][l] - pl[l][QQT_P_HP] > 0 ? 1 : 0;
   }
 
   // ---- observation + legality masks of the current state (sim/obs.py:25-229)
@@ -1141,7 +762,7 @@ __global__ __launch_bounds__(64 * WPB) void tick_kernel(const qqt_sim_config cf,
   wave_sync();
 
   // ---- store state and the staged observation
-  if (mode == QQT_MODE_STEP || mode == QQT_MODE_RESET || mode == QQT_MODE_FLUSH) {
+  if (mode == QQT_MODE_RESET || mode == QQT_MODE_FLUSH) {
     if (valid) {
 #pragma unroll
       for (int k = 0; k < KMAX; ++k) {
@@ -1205,12 +826,6 @@ int launch(const qqt_sim_config* cfg, const qqt_tick_args* a, hipStream_t st) {
   const dim3 grid(blocks), block(64 * WPB);
   if (a->mode == QQT_MODE_FLUSH)     // no reset in a flush
     QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB, QQT_MODE_FLUSH, 0>), grid, block, st,
-               *cfg, *a);
-  else if (a->mode == QQT_MODE_STEP && !ref)
-    QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB, QQT_MODE_STEP, 0>), grid, block, st,
-               *cfg, *a);
-  else if (a->mode == QQT_MODE_STEP)
-    QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB, QQT_MODE_STEP, 1>), grid, block, st,
                *cfg, *a);
   else if (!ref)
     QQT_LAUNCH(QQT_KERNEL_TICK, (tick_kernel<H, W, P, LPE, WPB, -1, 0>), grid, block, st, *cfg, *a);

@@ -489,6 +489,7 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
   }
 
   // ---- 7. damage at the post-move centre cell (sim/torch_sim.py:1007-1034)
+  int n_died = 0;                 // deaths among the players of row 0 (tick_stats)
   const int fpost = min(max((int)floorf(r.y) * W + (int)floorf(r.x), 0), C - 1);
   {
     const bool hit = alive0 && cov[fpost];
@@ -501,11 +502,13 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
     if (hit_eff) inv = CF->invuln_ticks;
     r.inv = inv;
     if (valid && l < P && A->died) A->died[gs * P + l] = died;
+    n_died = (valid && l < P && died) ? 1 : 0;
   }
 
   // ---- 8. burnt bricks (corridor: into crates), info bitsets, clear the
   // exploded cells, then the LDS copy takes the cleared words
   uint32_t covw = 0, trgw = 0;   // lane w < 8: word w of the env's bitsets
+  int n_trg = 0;                  // exploded bombs among this lane's cells (tick_stats)
   if (wave_boom) {
 #pragma unroll
     for (int k = 0; k < KC; ++k) {
@@ -520,6 +523,7 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
           w &= ~F_BRICK;
         }
         if (trg) w = cw_make(w, 0, -1, 0);
+        n_trg += trg && valid;
         cw[k] = w;
         cwl[c] = w;
       }
@@ -1263,6 +1267,24 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
     if (l == 0)
       *reinterpret_cast<int4*>(A->envs + gs * QQT_E_SLOTS) =
           make_int4(t, __float_as_int(crate_prob), map_kind, ev.w);
+  }
+
+  // ---- 15. optional launch totals: exploded bombs, deaths, auto-resets
+  int64_t* const stats = A->tick_stats;
+  if (stats) {
+    const int v0 = row_sum(n_trg), v1 = row_sum(n_died), v2 = row_sum(do_reset && l == 0 ? 1 : 0);
+    int s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+    for (int rw = 0; rw < 4; ++rw) {
+      s0 += __builtin_amdgcn_readlane(v0, 16 * rw);
+      s1 += __builtin_amdgcn_readlane(v1, 16 * rw);
+      s2 += __builtin_amdgcn_readlane(v2, 16 * rw);
+    }
+    if (lane == 0) {
+      if (s0) atomicAdd(reinterpret_cast<unsigned long long*>(stats), (unsigned long long)s0);
+      if (s1) atomicAdd(reinterpret_cast<unsigned long long*>(stats + 1), (unsigned long long)s1);
+      if (s2) atomicAdd(reinterpret_cast<unsigned long long*>(stats + 2), (unsigned long long)s2);
+    }
   }
 }
 

@@ -67,7 +67,10 @@ int qqt_timing_arm(int32_t launches) {
   std::lock_guard<std::mutex> g(t.mu);
   if (!t.created) {
     for (int i = 0; i < POOL; ++i) {
-      if (hipEventCreate(&t.start[i]) != hipSuccess || hipEventCreate(&t.stop[i]) != hipSuccess) {
+      // no system-scope fence at the events (an L2 writeback that would slow
+      // the timed dispatch and the kernel after it): the timestamps alone
+      if (hipEventCreateWithFlags(&t.start[i], hipEventDisableSystemFence) != hipSuccess ||
+          hipEventCreateWithFlags(&t.stop[i], hipEventDisableSystemFence) != hipSuccess) {
         snprintf(g_err, sizeof(g_err), "qqt_timing_arm: hipEventCreate failed");
         return QQT_E_LAUNCH;
       }

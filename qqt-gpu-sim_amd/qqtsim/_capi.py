@@ -14,7 +14,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 
 from ._build import LIB
 
-ABI_VERSION = 18
+ABI_VERSION = 19
 
 MODE_STEP, MODE_OBSERVE, MODE_RESET, MODE_PROBE, MODE_FLUSH = 0, 1, 2, 3, 4
 MAP_PILLARS, MAP_OPEN, MAP_REFERENCE = 0, 1, 2
@@ -57,7 +57,8 @@ class TickArgsC(ctypes.Structure):
                            "reset_mask", "reward", "done", "n_alive", "died", "winner",
                            "covered", "triggered", "obs", "move_mask", "bomb_mask",
                            "probe_out", "damaged", "recycle_excl")] + [("opp_boost", _i32),
-                                                                        ("danger_out", _vp)]
+                                                                        ("danger_out", _vp),
+                                                                        ("tick_stats", _vp)]
 
 
 class MlpArgsC(ctypes.Structure):

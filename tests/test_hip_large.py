@@ -11,6 +11,9 @@ first term is non-zero, so these tests run the benchmark sizes themselves:
   chain and damage within the run: observation, masks, sampled actions
   (the host sampler on the kernel's logits with the same Philox uniforms),
   logits against the oracle's forward, every state field, done and reward;
+* the learner (MLP, player 0) vs astar bot (player 1) rollout at 5632 envs:
+  the bot kernel over every row block, the batch-max reach and the
+  single-player act kernel at their measured launch shapes;
 * the bomb-stress tick at 16384 envs (injected unmasked actions, 40%
   bricks, caps 1-4 / 2-5, 5-tick fuse), bit-exact state tick after tick;
 * the reference-written deep-chain fixture (`tests/golden/deep_chain.npz`:
@@ -115,6 +118,77 @@ def test_mlp_rollout_5632_matches_oracle(dev, rules):
         assert exploded > 0
     print(f"rollout {rules}: {ticks} ticks x {n} envs exact, {resets} resets, "
           f"{exploded} bombs exploded")
+
+
+def test_learner_vs_astar_5632_matches_oracle(dev):
+    """The learner-vs-astar rollout at its measured size (5632 envs, 70%
+    bricks, spawn swap): the MLP plays player 0 and the astar bot player 1
+    (`HipAstarBot`: bot_kernel over every 44-env row block, the batch-max
+    reach of reach_kernel, and the single-player act kernel at 5632 rows).
+    A 5-tick fuse and 10-tick episodes make bombs explode and every env
+    auto-reset within the run.  Every tick: the learner's logits (every
+    fourth tick) against the oracle forward, its sampled actions against the
+    host sampler on the kernel's logits, the bot's actions against the
+    oracle bot with the same Philox noise, then every state field, done and
+    reward after the tick."""
+    from oracle import philox
+    from oracle.bots import astar_act
+    from oracle.policy import mlp_forward, sample_masked
+    from oracle.sim import OracleSim
+    from qqtsim import (HipActorCritic, HipAstarBot, HipBatchedSim, MapSpec, Rollout,
+                        corridor_training_config)
+    from qqtsim.policy import default_init
+
+    n, seed, ticks = 5632, 31, 12
+    cfg = corridor_training_config(fuse=5, max_hp=2, invuln_ticks=3, max_steps=10)
+    spec = MapSpec(kind="pillars", brick_p=0.7, swap_spawns=True)
+    params = default_init(cfg.obs_shape)
+    sim = HipBatchedSim(cfg, n, device=dev, seed=seed, map_spec=spec)
+    net = HipActorCritic(params, device=dev, seed=seed)
+    bot = HipAstarBot(sim, pid=1)
+    roll = Rollout(sim, net, opponent=bot)
+    ora = OracleSim(cfg, n, spec, seed=seed)
+    rows = np.arange(n)
+    resets = exploded = bot_moves = bot_bombs = 0
+    for t in range(ticks):
+        print(f"[large] learner vs astar n={n} tick {t}", flush=True)
+        o_obs = ora.observe()
+        mm, bm = ora.legal_mask()
+        u_pol = philox.uniforms(seed, rows, net.tick, philox.STREAM_POLICY, 4)
+        u_bot = torch.from_numpy(philox.uniforms(seed, rows, bot.tick, philox.STREAM_BOT, 5))
+        ml, bl, v = net.forward(sim.observe(), 0)
+        lg = torch.cat([ml, bl, v[:, None]], 1).cpu()
+        if t % 4 == 0:
+            rml, rbl, rv = mlp_forward(params, o_obs, 0)
+            err = float((lg - torch.cat([rml, rbl, rv[:, None]], 1)).abs().max())
+            assert err <= LOGIT_ATOL, f"tick {t}: logit error {err:.2e}"
+        roll.launch_act()
+        acts = roll.actions.long().cpu()
+        want = torch.zeros((n, 2, 2), dtype=torch.int64)
+        want[:, 0, 0] = torch.from_numpy(sample_masked(lg[:, :5].numpy(), mm[:, 0].numpy(),
+                                                       u_pol[:, 0])[0])
+        want[:, 0, 1] = torch.from_numpy(sample_masked(lg[:, 5:7].numpy(), bm[:, 0].numpy(),
+                                                       u_pol[:, 1])[0])
+        want[:, 1] = astar_act(cfg, ora.state_dict(), o_obs, mm[:, 1], bm[:, 1], 1, u_bot)
+        np.testing.assert_array_equal(acts[:, 0].numpy(), want[:, 0].numpy(),
+                                      err_msg=f"learner actions tick {t}")
+        np.testing.assert_array_equal(acts[:, 1].numpy(), want[:, 1].numpy(),
+                                      err_msg=f"bot actions tick {t}")
+        bot_moves += int((want[:, 1, 0] != 4).sum())
+        bot_bombs += int(want[:, 1, 1].sum())
+        roll.launch_tick()
+        o_rew, o_done, o_info = ora.step(acts, auto_reset=True)
+        resets += int(o_done.sum())
+        exploded += int(o_info["trig"].sum())
+        _same_state(sim, ora, t)
+        np.testing.assert_array_equal(roll.done.cpu().numpy(), o_done.numpy(), err_msg=f"done {t}")
+        r_err = float((roll.reward.cpu() - o_rew).abs().max())
+        assert r_err <= REWARD_ATOL, f"tick {t}: reward error {r_err:.2e}"
+    # (the bot's placements are pinned by the reference's astar fixtures;
+    # in these short episodes it may place none)
+    assert resets > 0 and exploded > 0 and bot_moves > 0
+    print(f"learner vs astar: {ticks} ticks x {n} envs exact, {resets} resets, {exploded} "
+          f"bombs exploded, bot moves {bot_moves}, bot bombs {bot_bombs}")
 
 
 def test_bomb_stress_16384_matches_oracle(dev):

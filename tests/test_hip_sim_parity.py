@@ -188,6 +188,39 @@ def test_hip_bomb_stress_injected_actions_match_oracle(dev):
     assert resets > 0
 
 
+@pytest.mark.parametrize("n", [300, 9000])
+def test_hip_tick_stats_count_what_the_ticks_did(dev, n):
+    """The optional launch totals (`tick_stats`: exploded bombs, deaths,
+    auto-resets) equal the oracle's info["trig"], info["died"] and done
+    summed over the same ticks, for both lane layouts of the STEP kernel
+    (two envs per wavefront up to 8192 envs, four above)."""
+    from oracle.sim import OracleSim
+    from qqtsim.config import corridor_training_config
+    from qqtsim.maps import BOMB_STRESS_40
+    from qqtsim.rollout import TickLoop
+    from qqtsim.sim import HipBatchedSim
+
+    cfg = corridor_training_config(fuse=5, max_hp=2, invuln_ticks=3, max_steps=14)
+    ticks, seed = 24, 13
+    hip = HipBatchedSim(cfg, n, device=dev, seed=seed, map_spec=BOMB_STRESS_40)
+    ora = OracleSim(cfg, n, BOMB_STRESS_40, seed=seed)
+    loop = TickLoop(hip)
+    stats = torch.zeros(3, dtype=torch.int64, device=dev)
+    loop._tick.tick_stats = stats.data_ptr()
+    g = torch.Generator().manual_seed(seed)
+    want = np.zeros(3, dtype=np.int64)
+    for t in range(ticks):
+        mv = torch.randint(0, 5, (n, 2), generator=g)
+        bb = (torch.rand((n, 2), generator=g) < 0.5).long()
+        act = torch.stack([mv, bb], -1)
+        _, d1, info = ora.step(act, auto_reset=True)
+        loop.launch_tick(act.to(torch.int8).to(dev).contiguous())
+        want += [int(info["trig"].sum()), int(info["died"].sum()), int(d1.sum())]
+    np.testing.assert_array_equal(stats.cpu().numpy(), want)
+    assert (want > 0).all(), want
+    _compare_state(hip.state_dict(), ora.state_dict(), ticks)
+
+
 def test_hip_attribute_views_follow_the_state(dev):
     """Reference-style attribute reads (`sim.hp`, `sim.pos`, `sim.fuse`, as
     train/ppo.py:247-286 makes every tick) return the current state: cached
