@@ -2,12 +2,12 @@
 lstm rollout buffer, the truncated-BPTT PPO update (qqtsim.ppo_update with
 an LstmLearner) and the weight sync back to the acting kernel.
 
-The update is checked against a restatement of the reference's
-_ppo_update_lstm (train/ppo.py:440-537) written here step by step: the
-per-frame heads and torch.distributions.Categorical, the host-side
-`if done.any()` reset, the oracle's GAE.  With plain SGD the weights after
-a whole update (2 epochs x 3 minibatches, with a bptt window) must agree
-within 2e-6 absolute; the statistics within 1e-5 relative.
+The update is checked against the oracle's restatement of the reference's
+_ppo_update_lstm (train/ppo.py:440-537, `oracle.ppo_lstm.lstm_update`): the
+same randperm consumption, per-frame torch.distributions.Categorical, the
+host-side `if done.any()` reset and the oracle's GAE.  With plain SGD the
+weights after a whole update (2 epochs x 3 minibatches, with a bptt window)
+must agree within 2e-6 absolute; the statistics within 1e-5 relative.
 """
 
 from __future__ import annotations
@@ -42,73 +42,8 @@ def _collect(dev, n, T, seed):
     return sim, net, roll, buf
 
 
-def _reference_update(learner, opt, buf, last_val, cfg, entropy_coef):
-    """train/ppo.py:440-537 restated for the check."""
-    from oracle.ppo import gae
-
-    T, N = buf.rew.shape
-    dev = buf.rew.device
-    a, r = gae(buf.rew.cpu(), buf.val.cpu(), buf.done.cpu(), last_val.cpu(), cfg.gamma,
-               cfg.gae_lambda)
-    adv, ret = torch.from_numpy(a).to(dev), torch.from_numpy(r).to(dev)
-    adv = (adv - adv.mean()) / (adv.std() + 1e-8)
-    old_logp, old_val = buf.logp, buf.val
-    stats = {"pg": 0.0, "vf": 0.0, "ent": 0.0, "kl": 0.0, "clipfrac": 0.0}
-    n_updates = 0
-    mb_n = max(1, N // cfg.minibatches)
-    for _ in range(cfg.epochs):
-        env_perm = torch.randperm(N, device=dev)
-        for start in range(0, N, mb_n):
-            sel = env_perm[start:start + mb_n]
-            ns = sel.numel()
-            logp = torch.empty((T, ns), device=dev)
-            ent = torch.empty((T, ns), device=dev)
-            value = torch.empty((T, ns), device=dev)
-            fused_all = learner.extract_fused(buf.local[:, sel].reshape(T * ns, -1, 7, 7),
-                                              buf.rel[:, sel].reshape(T * ns, -1, 6),
-                                              buf.glob[:, sel].reshape(T * ns, -1)).view(T, ns, -1)
-            hidden = None
-            for t in range(T):
-                if cfg.bptt_window > 0 and t % cfg.bptt_window == 0 and hidden is not None:
-                    hidden = (hidden[0].detach(), hidden[1].detach())
-                lo, hidden = learner.lstm(fused_all[t].unsqueeze(1), hidden)
-                lo = lo.squeeze(1)
-                ml, bl = learner.move_head(lo), learner.bomb_head(lo)
-                v = learner.critic(lo).squeeze(-1)
-                neg = torch.finfo(ml.dtype).min
-                dm = torch.distributions.Categorical(
-                    logits=torch.where(buf.mmask[t][sel], ml, torch.full_like(ml, neg)))
-                db = torch.distributions.Categorical(
-                    logits=torch.where(buf.bmask[t][sel], bl, torch.full_like(bl, neg)))
-                am, ab = buf.act[t][sel, 0], buf.act[t][sel, 1]
-                logp[t] = dm.log_prob(am) + db.log_prob(ab)
-                ent[t] = dm.entropy() + db.entropy()
-                value[t] = v
-                if bool(buf.done[t][sel].any()):
-                    dk = buf.done[t][sel].to(hidden[0].dtype).view(1, -1, 1)
-                    hidden = (hidden[0] * (1 - dk), hidden[1] * (1 - dk))
-            ratio = (logp - old_logp[:, sel]).exp()
-            pg = -torch.min(ratio * adv[:, sel],
-                            ratio.clamp(1 - cfg.clip_eps, 1 + cfg.clip_eps) * adv[:, sel]).mean()
-            v_clipped = old_val[:, sel] + (value - old_val[:, sel]).clamp(-cfg.clip_eps,
-                                                                           cfg.clip_eps)
-            vf = 0.5 * torch.max((value - ret[:, sel]) ** 2, (v_clipped - ret[:, sel]) ** 2).mean()
-            loss = pg + cfg.value_coef * vf - entropy_coef * ent.mean()
-            opt.zero_grad(set_to_none=True)
-            loss.backward()
-            torch.nn.utils.clip_grad_norm_(learner.parameters(), cfg.max_grad_norm)
-            opt.step()
-            with torch.no_grad():
-                stats["pg"] += float(pg)
-                stats["vf"] += float(vf)
-                stats["ent"] += float(ent.mean())
-                stats["kl"] += float((old_logp[:, sel] - logp).mean())
-                stats["clipfrac"] += float(((ratio - 1).abs() > cfg.clip_eps).float().mean())
-            n_updates += 1
-    return {k: v / max(1, n_updates) for k, v in stats.items()}
-
-
 def test_lstm_update_matches_the_reference_restatement(dev):
+    from oracle.ppo_lstm import lstm_update
     from qqtsim import LstmLearner, PPOConfig, ppo_update
 
     n, T, seed = 48, 14, 6
@@ -123,7 +58,7 @@ def test_lstm_update_matches_the_reference_restatement(dev):
     torch.manual_seed(3)
     got = ppo_update(a, oa, buf, last_val, cfg, 0.05)
     torch.manual_seed(3)
-    want = _reference_update(b, ob, buf, last_val, cfg, 0.05)
+    want = lstm_update(b, ob, buf, last_val, cfg, 0.05)
     print("stats", got, want)
     for k in want:
         assert np.isfinite(got[k])

@@ -110,3 +110,84 @@ def test_planted_mistakes_fail():
         run = ((rew[t] + np.float32(gamma) * nv) - val[t]) + (np.float32(gamma * lam) * nt) * run
         adv2[t] = run
     assert not np.array_equal(adv2, ta)
+
+
+def _lstm_buffer(steps=5, n=6, seed=0):
+    """A synthetic lstm rollout buffer on the CPU with the reference
+    RolloutBuffer's (T, N, ...) fields."""
+    from types import SimpleNamespace
+
+    g = torch.Generator().manual_seed(seed)
+    done = torch.zeros((steps, n), dtype=torch.bool)
+    done[2, 1] = done[3, 4] = True
+    return SimpleNamespace(
+        local=torch.rand((steps, n, 14, 7, 7), generator=g).half(),
+        rel=torch.rand((steps, n, 10, 6), generator=g).half(),
+        glob=torch.rand((steps, n, 5), generator=g).half(),
+        act=torch.stack([torch.randint(0, 5, (steps, n), generator=g),
+                         torch.randint(0, 2, (steps, n), generator=g)], -1),
+        mmask=torch.ones((steps, n, 5), dtype=torch.bool),
+        bmask=torch.ones((steps, n, 2), dtype=torch.bool),
+        rew=torch.randn((steps, n), generator=g), val=torch.randn((steps, n), generator=g),
+        logp=-torch.rand((steps, n), generator=g) * 2, done=done)
+
+
+def test_lstm_update_minibatches_consume_the_random_stream_like_the_reference():
+    """One randperm of the envs per epoch, cut into slices of N // minibatches
+    (train/ppo.py:460-465): replaying the same seed by hand gives the same
+    slices in the same order."""
+    from oracle.ppo_lstm import env_minibatches
+    from qqtsim.learn import PPOConfig
+
+    cfg = PPOConfig(epochs=3, minibatches=4)
+    torch.manual_seed(11)
+    got = [s.tolist() for s in env_minibatches(10, cfg, torch.device("cpu"))]
+    torch.manual_seed(11)
+    want = []
+    for _ in range(3):
+        perm = torch.randperm(10).tolist()
+        want += [perm[i:i + 2] for i in range(0, 10, 2)]
+    assert got == want
+
+
+def test_lstm_update_losses_reduce_to_closed_forms():
+    """At ratio 1 (new log-probs equal the old) the clipped surrogate is
+    -mean(adv) and the value loss is 0.5 mean((v - ret)^2) when v equals
+    the old value (no clipping in play); the entropy bonus enters with its
+    coefficient."""
+    from oracle.ppo_lstm import clipped_losses
+    from qqtsim.learn import PPOConfig
+
+    cfg = PPOConfig()
+    g = torch.Generator().manual_seed(2)
+    logp = -torch.rand((4, 3), generator=g)
+    ent = torch.rand((4, 3), generator=g)
+    val = torch.randn((4, 3), generator=g)
+    adv, ret = torch.randn((4, 3), generator=g), torch.randn((4, 3), generator=g)
+    loss, st = clipped_losses(logp, ent, val, logp.clone(), val.clone(), adv, ret, cfg, 0.07)
+    pg = -float(adv.mean())
+    vf = 0.5 * float(((val - ret) ** 2).mean())
+    assert abs(st["pg"] - pg) <= 1e-6 and abs(st["vf"] - vf) <= 1e-6
+    assert st["kl"] == 0.0 and st["clipfrac"] == 0.0
+    assert abs(float(loss) - (pg + cfg.value_coef * vf - 0.07 * float(ent.mean()))) <= 1e-6
+
+
+def test_lstm_replay_resets_the_state_where_an_episode_ended():
+    """The frame after a done frame starts from a zero LSTM state: replaying
+    env 1 of the buffer from frame 3 alone (a fresh zero state) gives the same
+    log-probs, entropies and values as frames 3.. of the full replay."""
+    from oracle.ppo_lstm import replay_sequence
+    from qqtsim.learn import LstmLearner
+
+    torch.manual_seed(0)
+    learner = LstmLearner()
+    buf = _lstm_buffer()
+    full = replay_sequence(learner, buf, torch.tensor([1]), window=0)
+    tail = type(buf)(**{k: v[3:] for k, v in vars(buf).items()})
+    part = replay_sequence(learner, tail, torch.tensor([1]), window=0)
+    for a, b in zip(full, part):
+        assert torch.allclose(a[3:], b, atol=1e-6), (a[3:], b)
+    # without the reset (an env that never ended) the replays differ
+    ref = replay_sequence(learner, buf, torch.tensor([0]), window=0)
+    tail0 = replay_sequence(learner, tail, torch.tensor([0]), window=0)
+    assert not torch.allclose(ref[2][3:], tail0[2], atol=1e-6)
