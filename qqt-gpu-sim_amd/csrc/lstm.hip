@@ -11,9 +11,11 @@
 //
 // lstm_act_kernel (train/model.py:103-120, 176-185, 198-214): one workgroup
 // of eight wavefronts (two per SIMD) per 16 or 24 rows.  Every product runs
-// on v_mfma_f32_16x16x32_f16 with float32 accuracy: float32 operands split
-// into float16 hi + lo, each product taken as hi*hi + hi*lo + lo*hi with
-// float32 accumulation (the float16 features need no lo part).  A: lane l
+// on v_mfma_f32_16x16x32_f16 with float32-level accuracy (within 5e-6 of the
+// float32 module): float32 operands split into float16 hi + lo, each
+// product taken as hi*hi + hi*lo + lo*hi with float32 accumulation (the
+// float16 features need no lo part).  The split saturates at 65504, so
+// larger activations stay finite, their remainder at float16 precision.  A: lane l
 // holds row l%16, k = 8(l/16) .. + 7; B: k = 8(l/16) .. + 7 of column l%16;
 // D: lane l holds D[4(l/16)+j][l%16].
 // * Trunk, four rows at a time: the windows sit in LDS as zero-bordered 9 x 9
@@ -268,11 +270,23 @@ struct Tiles {
   __device__ int operator()(int t) const { return t0 + t; }
 };
 
+// float32 v as float16 hi + lo (hi*w + lo*w carries v's product to float32
+// accuracy for |v| <= 65504).  Saturating: past float16's range hi stays at
+// +-65504 and lo takes the (clamped) remainder, so a large activation gives
+// a large finite product instead of inf - inf = NaN; exact in hi + lo up to
+// |v| = 131008, clamped beyond.
+__device__ __forceinline__ void split16(float v, _Float16& hi, _Float16& lo) {
+  constexpr float HMAX = 65504.0f;
+  hi = (_Float16)fminf(fmaxf(v, -HMAX), HMAX);
+  lo = (_Float16)fminf(fmaxf(v - (float)hi, -HMAX), HMAX);
+}
+
 // float32 v as float16 hi + lo into a plane pair
 __device__ __forceinline__ void put_split(uint16_t* h, uint16_t* l, int at, float v) {
-  const _Float16 hi = (_Float16)v;
+  _Float16 hi, lo;
+  split16(v, hi, lo);
   h[at] = __half_as_ushort(hi);
-  l[at] = __half_as_ushort((_Float16)(v - (float)hi));
+  l[at] = __half_as_ushort(lo);
 }
 
 // bias + optional ReLU of the output tiles, split into a float16 plane pair
@@ -345,18 +359,14 @@ __global__ __launch_bounds__(NTHR) void lstm_act_kernel(const qqt_lstm_args a) {
     for (int i = 0; i < 8; ++i) {
       const int k = 32 * st + 8 * q + i;
       const float v = k < K1 ? P[OFF_C1W + k * 32 + n1] : 0.0f;
-      const _Float16 hi = (_Float16)v;
-      b1h[st][i] = hi;
-      b1l[st][i] = (_Float16)(v - (float)hi);
+      split16(v, b1h[st][i], b1l[st][i]);
     }
 #pragma unroll
   for (int st = 0; st < KS2; ++st)
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float v = P[OFF_C2W + (32 * st + 8 * q + i) * 64 + n2];
-      const _Float16 hi = (_Float16)v;
-      b2h[st][i] = hi;
-      b2l[st][i] = (_Float16)(v - (float)hi);
+      split16(v, b2h[st][i], b2l[st][i]);
     }
   const float bias1 = P[OFF_C1B + n1], bias2 = P[OFF_C2B + n2];
 
@@ -433,10 +443,8 @@ __global__ __launch_bounds__(NTHR) void lstm_act_kernel(const qqt_lstm_args a) {
           if (tile1(i) < M1T && m < RG * 49) {
             const int rr = m / 49, p = m % 49;
             const float v = fmaxf(acc[i][j] + bias1, 0.0f);
-            const _Float16 hi = (_Float16)v;
             const int at = ((p / 7 + 1) * 9 + p % 7 + 1) * CP2 + n1;
-            s.t.a1h[rr][at] = __half_as_ushort(hi);
-            s.t.a1l[rr][at] = __half_as_ushort((_Float16)(v - (float)hi));
+            put_split(s.t.a1h[rr], s.t.a1l[rr], at, v);
           }
         }
       }

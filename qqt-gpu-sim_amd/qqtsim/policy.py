@@ -398,10 +398,16 @@ def _conv_operand(w: torch.Tensor, n_tiles: int) -> torch.Tensor:
     return out.permute(0, 2, 3, 1, 4).reshape(-1).contiguous()          # [tile][step][g*16+i16][j]
 
 
+HALF_MAX = 65504.0
+
+
 def _split16(x: torch.Tensor):
-    """float32 -> float16 hi and lo (x = hi + lo to ~2^-22 relative)."""
-    hi = x.half()
-    return hi, (x - hi.float()).half()
+    """float32 -> float16 hi and lo (x = hi + lo to ~2^-22 relative for
+    |x| <= 65504).  Saturating like the kernels' split: past float16's range
+    hi stays at +-65504 and lo takes the clamped remainder (finite, never
+    inf - inf)."""
+    hi = x.clamp(-HALF_MAX, HALF_MAX).half()
+    return hi, (x - hi.float()).clamp(-HALF_MAX, HALF_MAX).half()
 
 
 def _pack_linear(w: torch.Tensor) -> torch.Tensor:
@@ -537,8 +543,7 @@ def _lstm_frag16(w: torch.Tensor) -> torch.Tensor:
     each in the B-fragment order of v_mfma_f32_16x16x32_f16: half i of lane
     16 q + r in K step s of column tile t is W[32 s + 8 q + i][16 t + r]."""
     k, n = w.shape
-    hi = w.half()
-    lo = (w - hi.float()).half()
+    hi, lo = _split16(w)
 
     def frag(x):
         return x.reshape(k // 32, 4, 8, n // 16, 16).permute(3, 0, 1, 4, 2).reshape(-1)
