@@ -359,14 +359,20 @@ __global__ __launch_bounds__(NTHR) void lstm_act_kernel(const qqt_lstm_args a) {
     for (int i = 0; i < 8; ++i) {
       const int k = 32 * st + 8 * q + i;
       const float v = k < K1 ? P[OFF_C1W + k * 32 + n1] : 0.0f;
-      split16(v, b1h[st][i], b1l[st][i]);
+      _Float16 hi, lo;
+      split16(v, hi, lo);
+      b1h[st][i] = hi;
+      b1l[st][i] = lo;
     }
 #pragma unroll
   for (int st = 0; st < KS2; ++st)
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float v = P[OFF_C2W + (32 * st + 8 * q + i) * 64 + n2];
-      split16(v, b2h[st][i], b2l[st][i]);
+      _Float16 hi, lo;
+      split16(v, hi, lo);
+      b2h[st][i] = hi;
+      b2l[st][i] = lo;
     }
   const float bias1 = P[OFF_C1B + n1], bias2 = P[OFF_C2B + n2];
 
