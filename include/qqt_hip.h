@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 19
+#define QQT_ABI_VERSION 20
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -189,6 +189,32 @@ typedef struct qqt_mlp_args {
                                 without a gather); entries are clamped into
                                 [0, obs_rows), so no index reads outside obs */
   int64_t obs_rows;          /* rows of obs (> 0 when row_index is set) */
+  /* Sparse first layer.  When `sparse` is 1 and the shapes qualify (no
+     z1_out; sampling, or fewer than 65,536 rows; npid 1 or 2; 128 <= cells
+     <= 192; channels <= 16 with k0 = channels * cells; at most two dense
+     channels), the launch computes z1 = W0 x + b0 per workgroup of 22 rows
+     and both players as
+       the sum over the dense channels c of W0[:, c] x[c] on MFMA (the
+       float16 hi and lo parts of the weights times the exact float16
+       observation), plus
+       the sum over the nonzero cells k of every other channel of
+       x[k] * W0[:, column of k in the player's view] (float16 columns,
+       float32 sums).
+     Otherwise (or when a workgroup's rows hold more nonzero cells than its
+     lists take) the first layer is the dense product.  Both give the same
+     function up to float rounding. */
+  int32_t sparse;
+  int32_t channels, cells;   /* C and H*W (k0 = channels * cells) */
+  uint32_t dense_mask;       /* storage channels multiplied on MFMA (<= 2 bits) */
+  const uint16_t* w0g;       /* [k0][128] float16: row k = W0[:, k] in the network's
+                                own (view) input order */
+  const uint16_t* w0d;       /* [C][8 tiles][ceil(cells/32)][2 planes][64 lanes][8]
+                                float16 MFMA A fragments of view channel j: lane
+                                (r = lane%16, g = lane/16) holds W0[16 tile + r]
+                                [j*cells + 32 s + 8 g + i] (0 past the channel),
+                                plane 0 float16(w), plane 1 float16(w - plane 0) */
+  int8_t vmap[4][16];        /* view channel of storage channel c for player p
+                                (the inverse of the view permutation) */
 } qqt_mlp_args;
 
 /* astar rule bot for one player (sim/bots.py:267-508, astar_attack with no

@@ -25,7 +25,7 @@ CSRC = os.path.join(ROOT, "csrc")
 INCLUDE = os.path.join(REPO, "include")
 LIBDIR = os.path.join(PKG, "_lib")
 LIB = os.path.join(LIBDIR, "libqqt_hip.so")
-SOURCES = ["tick.hip", "tick_group.hip", "mlp.hip", "mlp_grad.hip", "ppo.hip", "cnn.hip", "lstm.hip", "bot.hip", "gae.hip",
+SOURCES = ["tick.hip", "tick_group.hip", "mlp.hip", "mlp_sparse.hip", "mlp_grad.hip", "ppo.hip", "cnn.hip", "lstm.hip", "bot.hip", "gae.hip",
            "timing.hip"]
 ARCH = os.environ.get("QQT_OFFLOAD_ARCH", "gfx950")
 

@@ -14,7 +14,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 
 from ._build import LIB
 
-ABI_VERSION = 19
+ABI_VERSION = 20
 
 MODE_STEP, MODE_OBSERVE, MODE_RESET, MODE_PROBE, MODE_FLUSH = 0, 1, 2, 3, 4
 MAP_PILLARS, MAP_OPEN, MAP_REFERENCE = 0, 1, 2
@@ -70,7 +70,10 @@ class MlpArgsC(ctypes.Structure):
                            "ln2_w", "ln2_b", "bh", "bf", "move_mask", "bomb_mask", "uniforms",
                            "actions", "actions_i8", "logp_out", "value_out", "logits_out")] + [
         ("out_slots", _i32), ("out_slot", _i32), ("z1_out", _vp), ("row_index", _vp),
-        ("obs_rows", ctypes.c_int64)]
+        ("obs_rows", ctypes.c_int64)] + [
+        (n, _i32) for n in ("sparse", "channels", "cells")] + [
+        ("dense_mask", _u32), ("w0g", _vp), ("w0d", _vp),
+        ("vmap", (ctypes.c_int8 * 16) * 4)]
 
 
 class BotArgsC(ctypes.Structure):

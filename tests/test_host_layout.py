@@ -344,3 +344,72 @@ def test_unpack_key_matches_unpack():
         assert one.dtype == full[k].dtype and torch.equal(one, full[k]), k
     with pytest.raises(KeyError):
         st.unpack_key(cells, players, envs, 13, 13, "nope")
+
+
+def _sparse_first_layer(packed, obs16, pid):
+    """CPU emulation, in float64, of the sparse act kernel's first layer
+    (csrc/mlp_sparse.hip) from the packed operands: the dense channels from
+    the hi + lo MFMA A fragments read in the kernel's lane layout, every
+    other channel c as its nonzero cells times the gather table's rows of
+    view channel vmap[pid][c]."""
+    si = packed["sparse_info"]
+    c_n, hw = si["channels"], si["cells"]
+    k0 = c_n * hw
+    ksc = -(-hw // 32)
+    tab = packed["w0g"].double().view(k0, 128)
+    w0d = packed["w0d"].double().view(c_n, 8, ksc, 2, 64, 8)
+    x = obs16.double().reshape(obs16.shape[0], c_n, hw)
+    z = torch.zeros((x.shape[0], 128), dtype=torch.float64)
+    for c in range(c_n):
+        j = si["vmap"][pid][c]
+        if (si["dense_mask"] >> c) & 1:
+            # lane 16 g + r of (tile, step) holds W[16 tile + r][j hw + 32 step + 8 g + i]
+            wd = (w0d[j, :, :, 0] + w0d[j, :, :, 1]).view(8, ksc, 4, 16, 8)
+            wd = wd.permute(0, 3, 1, 2, 4).reshape(128, ksc * 32)
+            assert float(wd[:, hw:].abs().max()) == 0.0
+            z += x[:, c] @ wd[:, :hw].t()
+        else:
+            xc = x[:, c]
+            nz = xc != 0
+            z += torch.where(nz, xc, torch.zeros_like(xc)) @ tab[j * hw:(j + 1) * hw]
+    return z
+
+
+def test_sparse_first_layer_operands_reproduce_the_view_folded_product():
+    """The sparse kernel's first-layer operands (gather table, dense-channel
+    fragments, view map, dense-channel mask) put together as the kernel does
+    give the reference's x @ W0[:, inv_cols[pid]]^T (train/model.py:192-196)
+    for both players, on observations from a reference trajectory and on
+    the same rows with every cell perturbed."""
+    from oracle.policy import column_permutation
+
+    from golden_io import traj
+
+    params = default_init()
+    packed = pack_mlp(params)
+    si = packed["sparse_info"]
+    # wall | brick (channel 2P) and progress (2P + 2) are the dense channels (sim/obs.py:88-101)
+    assert si["dense_mask"] == (1 << 4) | (1 << 6)
+    W0 = params["shared.0.weight"].double()
+    obs = torch.from_numpy(traj("pillars70")["obs"].reshape(-1, 14, 13, 13)[:64].copy())
+    g = torch.Generator().manual_seed(1)
+    noisy = (obs.float() + 0.01 * torch.randn(obs.shape, generator=g)).half()
+    dense = torch.zeros(2366, dtype=torch.bool)
+    dense[4 * 169:5 * 169] = True
+    dense[6 * 169:7 * 169] = True
+    for x16 in (obs, noisy):
+        xf = x16.double().reshape(x16.shape[0], -1)
+        for pid in range(2):
+            cols = column_permutation(pid, 2, 14, 169)
+            ref = xf @ W0[:, cols].t()
+            got = _sparse_first_layer(packed, x16, pid)
+            # the gathered columns are float16: |error| <= sum over them of |x| |w| 2^-11;
+            # the dense channels' hi + lo weights are float32-accurate
+            wabs = W0[:, cols].abs()
+            bound = (xf * ~dense) @ wabs.t() * 2.0 ** -11 + (xf * dense) @ wabs.t() * 2.0 ** -20 + 1e-9
+            assert bool(torch.all((got - ref).abs() <= bound)), pid
+    # a planted slip: the other player's view map misplaces the player channels
+    bad = dict(packed, sparse_info=dict(si, vmap=[si["vmap"][1], si["vmap"][0]]))
+    xf = obs.double().reshape(obs.shape[0], -1)
+    ref = xf @ W0[:, column_permutation(0, 2, 14, 169)].t()
+    assert float((_sparse_first_layer(bad, obs, 0) - ref).abs().max()) > 1e-3
