@@ -312,7 +312,7 @@ def main():
     preroll = cfg.fuse + 2
     for _ in range(preroll + W):
         roll.step()
-    stats = torch.zeros(3, dtype=torch.int64, device=dev)
+    stats = torch.zeros((n, 4), dtype=torch.int32, device=dev)
     roll._tick.tick_stats = stats.data_ptr()   # the tick counts what the timed steps did
     torch.cuda.synchronize()
 
@@ -394,9 +394,10 @@ def main():
 
 
 def timed_window(stats, untimed, steps, n):
-    """What the timed ticks did, from the tick kernel's own launch totals:
-    bombs exploded, players died and envs auto-reset over the timed steps."""
-    ex, dead, resets = (int(v) for v in stats.tolist())
+    """What the timed ticks did, from the tick kernel's own per-env counters
+    (summed over envs after timing): bombs exploded, players died and envs
+    auto-reset over the timed steps."""
+    ex, dead, resets = (int(v) for v in stats[:, :3].long().sum(0).tolist())
     return {"ticks_before_timing": untimed, "timed_ticks": steps, "exploded_bombs": ex,
             "deaths": dead, "auto_resets": resets,
             "exploded_bombs_per_env_tick": round(ex / (n * steps), 5)}
@@ -475,7 +476,7 @@ def main_stress(args, torch, dev):
     loop = TickLoop(sim)
     for k in range(U):
         loop.launch_tick(acts[k])
-    stats = torch.zeros(3, dtype=torch.int64, device=dev)
+    stats = torch.zeros((n, 4), dtype=torch.int32, device=dev)
     loop._tick.tick_stats = stats.data_ptr()
     torch.cuda.synchronize()
     _capi.timing_arm(0)          # creates the event pool outside the timed region

@@ -135,11 +135,20 @@ typedef struct qqt_tick_args {
   float* danger_out;          /* OBSERVE: [N][H][W] float32 danger map of the current
                                  state (blast.danger_map as BatchedSim._danger_c
                                  computes it, sim/torch_sim.py:732-762), or NULL */
-  int64_t* tick_stats;        /* STEP: [3] incremented by this launch's exploded bombs
+  int32_t* tick_stats;        /* STEP: [N][4], 16-byte aligned, or NULL: slots 0-2 of env
+                                 n are incremented by this launch's exploded bombs
                                  (info["trig"] cells), deaths (info["died"]) and
-                                 auto-resets (done envs reset), summed over envs; or
-                                 NULL.  For benchmark harnesses that report what their
-                                 timed ticks did; no reference counterpart. */
+                                 auto-reset (1 if the env was done and reset) of env n;
+                                 slot 3 is left as it is.  For benchmark harnesses that
+                                 report what their timed ticks did (sum over envs after
+                                 the launches); no reference counterpart. */
+  int8_t* reach_caps;         /* STEP: int8 [N rounded up to a multiple of 16] or NULL:
+                                 entry n = the blast cap of player reach_pid of env n
+                                 after the tick and its auto-reset (the padding is left
+                                 as it is).  The astar bot's next call reduces it to the
+                                 batch max (qqt_bot_args reach_mode 3) instead of a
+                                 reduction launch of its own. */
+  int32_t reach_pid;
 } qqt_tick_args;
 
 /* MLP actor/critic forward (+ masked sampling).  Weights are the packed
@@ -230,7 +239,10 @@ typedef struct qqt_bot_args {
                                  1 = the batch max of the bot's blast cap (the
                                  reference's rule), computed by this call into
                                  reach[reach_slot & 1]; 2 = the value already in
-                                 reach[0] */
+                                 reach[0]; 3 = that batch max from the caps a STEP
+                                 tick wrote to reach_caps (its reach_pid = pid, the
+                                 padding 0), when nothing changed the state since
+                                 that tick */
   int32_t reach_slot;         /* mode 1: reach is int32[2], both INT32_MIN before
                                  the first call; call k passes slot k (any
                                  counter that alternates): the call max-reduces
@@ -243,6 +255,8 @@ typedef struct qqt_bot_args {
   const uint8_t* bomb_mask;   /* [N][P][2] */
   const float* uniforms;      /* [N][5] noise uniforms, or NULL = Philox stream 7 */
   int32_t* reach;             /* device int32[2] (mode 1) or scalar (mode 2) */
+  const int8_t* reach_caps;   /* mode 3: the tick's caps, int8 [N rounded up to 16],
+                                 16-byte aligned */
   int64_t* actions;           /* [N][P][2], slot pid written; or NULL */
   int8_t* actions_i8;         /* same as int8; or NULL */
 } qqt_bot_args;

@@ -92,8 +92,32 @@ __global__ __launch_bounds__(64 * WPB) void bot_kernel(const qqt_sim_config cf, 
   const int mv = lane < 5 ? a.move_mask[((size_t)g * P + pid) * 5 + lane] : 0;
   const int bv = lane < 2 ? a.bomb_mask[((size_t)g * P + pid) * 2 + lane] : 0;
   const float uv = (a.uniforms && lane < 5) ? a.uniforms[(size_t)g * 5 + lane] : 0.0f;
-  const int reach_in = a.reach_mode == 1 ? a.reach[a.reach_slot & 1]
-                       : a.reach_mode == 2 ? a.reach[0] : 0;
+  int reach_in = a.reach_mode == 1 ? a.reach[a.reach_slot & 1]
+                 : a.reach_mode == 2 ? a.reach[0] : 0;
+  if (a.reach_mode == 3) {   // the batch max of the caps the last STEP tick wrote
+    // 16 caps per lane load, eight loads in flight per lane (8192 envs per pass)
+    const uint4* c16 = reinterpret_cast<const uint4*>(a.reach_caps);
+    const int n16 = (a.n_envs + 15) >> 4;
+    uint32_t m = 0u;
+    for (int base = 0; base < n16; base += 512) {
+      uint4 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = base + lane + 64 * j;
+        v[j] = i < n16 ? c16[i] : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q)   // four caps in 0..127 per word
+          m = max(m, max(max(w[q] & 0xffu, (w[q] >> 8) & 0xffu), max((w[q] >> 16) & 0xffu, w[q] >> 24)));
+      }
+    }
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, sh, 64));
+    reach_in = (int)m;
+  }
   if (!a.uniforms && lane < 2) {
     float ub[4];
     philox_block(a.seed, (uint32_t)g, a.tick, STREAM_BOT, (uint32_t)lane, ub);
@@ -380,8 +404,9 @@ int qqt_bot_act(const qqt_sim_config* cfg, const qqt_bot_args* a, void* stream) 
     snprintf(g_err, sizeof(g_err), "qqt_bot_act: null pointer or empty batch");
     return QQT_E_ARG;
   }
-  if (a->reach_mode < 0 || a->reach_mode > 2 || (a->reach_mode != 0 && !a->reach)) {
-    snprintf(g_err, sizeof(g_err), "qqt_bot_act: reach_mode 1/2 needs a reach buffer");
+  if (a->reach_mode < 0 || a->reach_mode > 3 || ((a->reach_mode == 1 || a->reach_mode == 2) && !a->reach) ||
+      (a->reach_mode == 3 && (!a->reach_caps || (((uintptr_t)a->reach_caps) & 15)))) {
+    snprintf(g_err, sizeof(g_err), "qqt_bot_act: reach_mode 1/2 needs a reach buffer, 3 aligned reach_caps");
     return QQT_E_ARG;
   }
   if (a->pid < 0 || a->pid >= cfg->n_players || cfg->growth_blast_max < 0 ||

@@ -73,6 +73,7 @@ namespace qqt {
 // (no sampling) from MLP_BIG_ROWS rows go to mlp_fwd_kernel (256-row
 // workgroups, W0 streamed once per 256 rows).
 constexpr int RT_SMALL = (XCD_ROWS + 15) / 16;
+constexpr int RT_HALF = (XCD_ROWS / 2 + 15) / 16;   // half an XCD row block
 constexpr int MLP_BIG_ROWS = 1 << 16;
 #ifndef QQT_MLP_PD
 #define QQT_MLP_PD 2
@@ -117,13 +118,16 @@ __device__ __forceinline__ Frag16 read_x(const uint16_t* tile, int row, int q) {
 
 // RT row tiles (16RT rows) per workgroup.
 // Z1: the first-layer-only instantiation of the training forward (z1_out).
-template <int RT, bool Z1>
+// HALF: the workgroup owns half an XCD row block (one-player launches: 5632
+// rows then make 256 workgroups instead of 128).
+template <int RT, bool Z1, bool HALF = false>
 __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   static_assert(RT >= 1 && RT <= 8, "tail wavefronts take one row tile each");
   constexpr int ROWS = 16 * RT;            // rows of the workgroup's tiles
-  // rows the workgroup owns: an XCD row block for rollout-sized batches (the
-  // last tile's rows past it are computed on the next block's rows and dropped)
-  constexpr int BROWS = RT == RT_SMALL ? XCD_ROWS : ROWS;
+  // rows the workgroup owns: an XCD row block (or half of one) for
+  // rollout-sized batches (the last tile's rows past it are computed on the
+  // next block's rows and dropped)
+  constexpr int BROWS = HALF ? XCD_ROWS / 2 : RT == RT_SMALL ? XCD_ROWS : ROWS;
   static_assert(BROWS <= ROWS && BROWS > ROWS - 16, "the tiles cover the block");
   constexpr int NX = 2 * RT;               // x load instructions per wavefront and K block
   constexpr int XT = MlpLds<RT>::XT;       // one x tile of the workgroup
@@ -137,7 +141,9 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   const int nrb = (a.batch + BROWS - 1) / BROWS;
   const int xcd = blockIdx.x & 7, seq = blockIdx.x >> 3;
   const int slot = seq % a.npid;
-  const int rb = (seq / a.npid) * 8 + xcd;
+  // (half blocks 2k, 2k + 1 of XCD row block k, on that block's XCD)
+  const int rb = HALF ? (((seq / a.npid) >> 1) * 8 + xcd) * 2 + ((seq / a.npid) & 1)
+                      : (seq / a.npid) * 8 + xcd;
   if (rb >= nrb) return;                   // padding workgroup (uniform, before any barrier)
   const int pid = a.npid == 2 ? slot : a.pid0;
   const int row0 = rb * BROWS;
@@ -862,13 +868,18 @@ int qqt_mlp_act(const qqt_mlp_args* a, void* stream) {
   }
   const int rows_wg = big ? FWD_ROWS : XCD_ROWS;
   const int nrb = (a->batch + rows_wg - 1) / rows_wg;
-  const int blocks = ((nrb + 7) / 8) * 8 * a->npid;
+  // one-player rollout launches: two workgroups (half blocks) per XCD row block
+  const bool half = !big && !a->z1_out && a->npid == 1;
+  const int blocks = ((nrb + 7) / 8) * 8 * a->npid * (half ? 2 : 1);
   if (a->z1_out && big)
     QQT_LAUNCH(QQT_KERNEL_MLP, mlp_fwd_kernel<true>, dim3(blocks), dim3(NTHR), st, *a);
   else if (a->z1_out)
     QQT_LAUNCH(QQT_KERNEL_MLP, (mlp_act_kernel<RT_SMALL, true>), dim3(blocks), dim3(NTHR), st, *a);
   else if (big)
     QQT_LAUNCH(QQT_KERNEL_MLP, mlp_fwd_kernel<false>, dim3(blocks), dim3(NTHR), st, *a);
+  else if (half)
+    QQT_LAUNCH(QQT_KERNEL_MLP, (mlp_act_kernel<RT_HALF, false, true>), dim3(blocks), dim3(NTHR),
+               st, *a);
   else
     QQT_LAUNCH(QQT_KERNEL_MLP, (mlp_act_kernel<RT_SMALL, false>), dim3(blocks), dim3(NTHR), st,
                *a);

@@ -863,6 +863,10 @@ int qqt_tick(const qqt_sim_config* cfg, const qqt_tick_args* a, void* stream) {
   if (a->mode == QQT_MODE_RESET && !a->reset_mask) return fail(QQT_E_ARG, "RESET needs reset_mask");
   if (a->mode == QQT_MODE_PROBE && !a->probe_out) return fail(QQT_E_ARG, "PROBE needs probe_out");
   if (a->obs && (((uintptr_t)a->obs) & 15)) return fail(QQT_E_ARG, "obs must be 16-byte aligned");
+  if (a->tick_stats && (((uintptr_t)a->tick_stats) & 15))
+    return fail(QQT_E_ARG, "tick_stats must be 16-byte aligned");
+  if (a->reach_caps && (a->reach_pid < 0 || a->reach_pid >= cfg->n_players))
+    return fail(QQT_E_ARG, "reach_pid out of range");
   if (cfg->fuse < 1 || cfg->fuse > 255) return fail(QQT_E_ARG, "fuse must be in 1..255");
   if (cfg->chain_cap_rounds < 0 || cfg->chain_cap_rounds > 64)
     return fail(QQT_E_ARG, "chain_cap_rounds must be in 0..64");

@@ -1269,23 +1269,23 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
           make_int4(t, __float_as_int(crate_prob), map_kind, ev.w);
   }
 
-  // ---- 15. optional launch totals: exploded bombs, deaths, auto-resets
-  int64_t* const stats = A->tick_stats;
+  // ---- 15. optional per-env counters: exploded bombs, deaths, auto-resets
+  // (each env's own int4, added to by lane 0 of the env: no atomics and no
+  // contention between envs)
+  int32_t* const stats = A->tick_stats;
   if (stats) {
-    const int v0 = row_sum(n_trg), v1 = row_sum(n_died), v2 = row_sum(do_reset && l == 0 ? 1 : 0);
-    int s0 = 0, s1 = 0, s2 = 0;
-#pragma unroll
-    for (int rw = 0; rw < 4; ++rw) {
-      s0 += __builtin_amdgcn_readlane(v0, 16 * rw);
-      s1 += __builtin_amdgcn_readlane(v1, 16 * rw);
-      s2 += __builtin_amdgcn_readlane(v2, 16 * rw);
-    }
-    if (lane == 0) {
-      if (s0) atomicAdd(reinterpret_cast<unsigned long long*>(stats), (unsigned long long)s0);
-      if (s1) atomicAdd(reinterpret_cast<unsigned long long*>(stats + 1), (unsigned long long)s1);
-      if (s2) atomicAdd(reinterpret_cast<unsigned long long*>(stats + 2), (unsigned long long)s2);
+    const int v0 = env_sum<L>(n_trg), v1 = env_sum<L>(n_died);
+    if (valid && l == 0) {
+      int4* sp = reinterpret_cast<int4*>(stats) + gs;
+      const int4 o = *sp;
+      *sp = make_int4(o.x + v0, o.y + v1, o.z + (do_reset ? 1 : 0), o.w);
     }
   }
+
+  // ---- 16. optional per-env blast cap of one player (int8), the astar
+  // bot's chain-check reach source for its next call
+  int8_t* const rcaps = A->reach_caps;
+  if (rcaps && valid && l == A->reach_pid) rcaps[gs] = (int8_t)min(r.zcap, 127);
 }
 
 }  // namespace grp

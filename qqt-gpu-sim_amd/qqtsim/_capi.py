@@ -58,7 +58,9 @@ class TickArgsC(ctypes.Structure):
                            "covered", "triggered", "obs", "move_mask", "bomb_mask",
                            "probe_out", "damaged", "recycle_excl")] + [("opp_boost", _i32),
                                                                         ("danger_out", _vp),
-                                                                        ("tick_stats", _vp)]
+                                                                        ("tick_stats", _vp),
+                                                                        ("reach_caps", _vp),
+                                                                        ("reach_pid", _i32)]
 
 
 class MlpArgsC(ctypes.Structure):
@@ -80,7 +82,7 @@ class BotArgsC(ctypes.Structure):
     _fields_ = [("n_envs", _i32), ("pid", _i32), ("seed", _u64), ("tick", _u32),
                 ("reach_mode", _i32), ("reach_slot", _i32)] + [
         (n, _vp) for n in ("cells", "players", "obs", "move_mask", "bomb_mask", "uniforms",
-                           "reach", "actions", "actions_i8")]
+                           "reach", "reach_caps", "actions", "actions_i8")]
 
 
 class L1GradArgsC(ctypes.Structure):

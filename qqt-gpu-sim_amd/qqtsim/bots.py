@@ -12,8 +12,10 @@ The noise uniforms come from Philox (stream 7, keyed by env and this bot's
 call counter) unless `uniforms=(N, 5)` is passed.  The chain check reaches
 out to the batch maximum of the bot's blast cap, as in the reference
 (`int(cap.max().item())`, sim/bots.py:477), computed on the device without a
-host round trip (a one-workgroup reduction launched by `qqt_bot_act`);
-`own_cap_reach=True` uses each bot's own cap instead.
+host round trip: from the per-row-block maxima the last STEP tick wrote
+when a `Rollout` drives this bot and nothing changed the state since that
+tick, else by a reduction launched by `qqt_bot_act`; `own_cap_reach=True`
+uses each bot's own cap instead.
 """
 
 from __future__ import annotations
@@ -39,6 +41,10 @@ class HipAstarBot:
         self._stream = _capi.stream_handle(sim.device)
         # two reach slots (the batch-max reduction alternates between them)
         self._reach = torch.full((2,), -2 ** 31, dtype=torch.int32, device=sim.device)
+        # the per-env caps a Rollout's STEP ticks write (padding 0) and the
+        # state version right after the last such tick
+        self._caps = torch.zeros((-(-sim.num_envs // 16) * 16,), dtype=torch.int8, device=sim.device)
+        self._tick_version = None
         self._calls = 0
         self._out = torch.zeros((sim.num_envs, sim.cfg.n_players, 2), dtype=torch.int64,
                                 device=sim.device)
@@ -52,6 +58,30 @@ class HipAstarBot:
         b.reach = self._reach.data_ptr()
         self._args = b
 
+    def _set_reach(self, b) -> None:
+        """The chain check's reach source for this call: the caps the last STEP
+        tick wrote when the sim's state is still that tick's (mode 3), else a
+        reduction of the batch (mode 1), or the own cap (mode 0)."""
+        if self.own_cap_reach:
+            b.reach_mode = 0
+        elif self._tick_version is not None and self._tick_version == self.sim._state_version:
+            b.reach_mode, b.reach_caps = 3, self._caps.data_ptr()
+        else:
+            b.reach_mode, b.reach, b.reach_slot = 1, self._reach.data_ptr(), self._calls & 1
+            self._calls += 1
+
+    def tick_writes_reach(self, tick_args) -> None:
+        """Point a STEP tick's argument block at this bot's cap array, before
+        the launch."""
+        tick_args.reach_caps = 0 if self.own_cap_reach else self._caps.data_ptr()
+        tick_args.reach_pid = self.pid
+
+    def tick_wrote_reach(self) -> None:
+        """Record that the STEP tick just launched wrote the caps (after the
+        sim marked its state changed by that tick)."""
+        if not self.own_cap_reach:
+            self._tick_version = self.sim._state_version
+
     def launch(self, actions: torch.Tensor) -> None:
         """Write this bot's [move, place] into slot `pid` of an (N, P, 2)
         int8 or int64 device action buffer (observation and masks are the
@@ -62,8 +92,7 @@ class HipAstarBot:
         self.sim._refresh()
         b = self._args
         b.tick = self.tick & 0xFFFFFFFF
-        b.reach_slot = self._calls & 1
-        self._calls += 1
+        self._set_reach(b)
         b.uniforms = None
         b.actions = actions.data_ptr() if actions.dtype == torch.int64 else None
         b.actions_i8 = actions.data_ptr() if actions.dtype == torch.int8 else None
@@ -91,8 +120,7 @@ class HipAstarBot:
         u = None if uniforms is None else uniforms.to(sim.device, torch.float32).contiguous()
         b.obs, b.move_mask, b.bomb_mask = obs_t.data_ptr(), mm.data_ptr(), bm.data_ptr()
         b.tick = self.tick & 0xFFFFFFFF
-        b.reach_slot = self._calls & 1
-        self._calls += 1
+        self._set_reach(b)
         b.uniforms = _capi.ptr(u)
         b.actions, b.actions_i8 = self._out.data_ptr(), None
         try:

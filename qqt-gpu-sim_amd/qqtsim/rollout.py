@@ -126,10 +126,15 @@ class Rollout:
         t.danger_coef = float(sim.explore_coef * sim.cfg.danger_penalty)
         t.tick = sim.tick & 0xFFFFFFFF
         t.epoch = sim.epoch & 0xFFFFFFFF
+        bot = self.opponent if hasattr(self.opponent, "tick_writes_reach") else None
+        if bot is not None:          # the tick leaves the bot's reach for its next call
+            bot.tick_writes_reach(t)
         _capi.check(self._lib.qqt_tick(sim._cfg_c, t, self._stream))
         sim.tick += 1
         sim.epoch += 1
         sim._fresh = True
+        if bot is not None:
+            bot.tick_wrote_reach()
 
     def step(self) -> None:
         """One env-step for every env."""
@@ -416,10 +421,15 @@ class LstmRollout:
         t.danger_coef = float(sim.explore_coef * sim.cfg.danger_penalty)
         t.tick = sim.tick & 0xFFFFFFFF
         t.epoch = sim.epoch & 0xFFFFFFFF
+        bot = self.opponent if hasattr(self.opponent, "tick_writes_reach") else None
+        if bot is not None:          # the tick leaves the bot's reach for its next call
+            bot.tick_writes_reach(t)
         _capi.check(self._lib.qqt_tick(sim._cfg_c, t, self._stream))
         sim.tick += 1
         sim.epoch += 1
         sim._fresh = True
+        if bot is not None:
+            bot.tick_wrote_reach()
 
     def step(self) -> None:
         """One env-step for every env."""

@@ -383,8 +383,9 @@ class HipBatchedSim:
         self._fresh = True
 
     # Every launch and load_state_dict assigns `_fresh`, so an assignment
-    # marks the packed state as possibly changed and drops the converted
-    # attribute views.
+    # marks the packed state as possibly changed: it drops the converted
+    # attribute views and counts a state version (a bot reading a batch
+    # statistic that a tick wrote checks that nothing changed since).
     @property
     def _fresh(self) -> bool:
         return self.__dict__["_fresh_flag"]
@@ -393,6 +394,7 @@ class HipBatchedSim:
     def _fresh(self, v: bool) -> None:
         self.__dict__["_fresh_flag"] = bool(v)
         self.__dict__["_views"] = {}
+        self.__dict__["_state_version"] = self.__dict__.get("_state_version", 0) + 1
 
     def __getattr__(self, name):
         """Reference attribute reads (`sim.hp`, `sim.pos`, `sim.fuse`, ...): the

@@ -331,7 +331,7 @@ def _bot_args(**kw):
     (dict(pid=2), "bad player id"),
     (dict(pid=-1), "bad player id"),
     (dict(reach_mode=1), "reach buffer"),
-    (dict(reach_mode=3, reach=0x9000), "reach buffer"),
+    (dict(reach_mode=4, reach=0x9000), "reach buffer"),
 ])
 def test_bot_rejects_bad_arguments(lib, kw, msg):
     assert lib.qqt_bot_act(_cfg(), _bot_args(**kw), None) == -1

@@ -123,3 +123,42 @@ def test_hip_bot_reach_follows_the_batch_from_call_to_call(dev):
             sim.load_state_dict(state)
             got = bot.act(*inputs, 1, uniforms=u)
             np.testing.assert_array_equal(got.cpu().numpy(), want, err_msg=f"rep {rep}")
+
+
+def test_tick_written_reach_equals_the_batch_max(dev):
+    """A Rollout's STEP ticks leave the bot's chain-check reach source (its
+    blast cap per env, whose batch max is the reach of sim/bots.py:477): the
+    caps equal the state's, the bot's next call reads them (reach mode 3) and
+    draws the same actions as a twin bot reducing the batch itself (mode 1),
+    and a state change after the tick sends the bot back to the reduction."""
+    from qqtsim.bots import HipAstarBot
+    from qqtsim.config import corridor_training_config
+    from qqtsim.maps import BOMB_STRESS_40
+    from qqtsim.policy import HipActorCritic, default_init
+    from qqtsim.rollout import Rollout
+    from qqtsim.sim import HipBatchedSim
+
+    n = 301                                   # caps padded to 304 with zeros
+    cfg = corridor_training_config()
+    sim = HipBatchedSim(cfg, n, device=dev, seed=3, map_spec=BOMB_STRESS_40)
+    net = HipActorCritic(default_init(cfg.obs_shape), device=dev, seed=3)
+    bot = HipAstarBot(sim, pid=1)
+    roll = Rollout(sim, net, opponent=bot)
+    for _ in range(6):
+        roll.step()
+        torch.cuda.synchronize()
+        cap = sim.state_dict()["blast_cap"][:, 1]
+        np.testing.assert_array_equal(bot._caps[:n].cpu().numpy(), cap.cpu().numpy())
+        assert int(bot._caps[n:].abs().sum()) == 0
+    assert len(set(sim.state_dict()["blast_cap"][:, 1].tolist())) > 1
+    twin = HipAstarBot(sim, pid=1)
+    twin.tick = bot.tick
+    a3 = torch.zeros_like(roll.actions)
+    a1 = torch.zeros_like(roll.actions)
+    bot.launch(a3)
+    twin.launch(a1)
+    assert bot._args.reach_mode == 3 and twin._args.reach_mode == 1
+    assert torch.equal(a3[:, 1], a1[:, 1])
+    sim.load_state_dict(sim.state_dict())
+    bot.launch(a3)
+    assert bot._args.reach_mode == 1

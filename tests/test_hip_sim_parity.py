@@ -190,10 +190,11 @@ def test_hip_bomb_stress_injected_actions_match_oracle(dev):
 
 @pytest.mark.parametrize("n", [300, 9000])
 def test_hip_tick_stats_count_what_the_ticks_did(dev, n):
-    """The optional launch totals (`tick_stats`: exploded bombs, deaths,
-    auto-resets) equal the oracle's info["trig"], info["died"] and done
-    summed over the same ticks, for both lane layouts of the STEP kernel
-    (two envs per wavefront up to 8192 envs, four above)."""
+    """The optional per-env counters (`tick_stats`: exploded bombs, deaths,
+    auto-resets) equal the oracle's info["trig"], info["died"] and done of
+    each env summed over the same ticks, for both lane layouts of the STEP
+    kernel (two envs per wavefront up to 8192 envs, four above); slot 3 is
+    left as it was."""
     from oracle.sim import OracleSim
     from qqtsim.config import corridor_training_config
     from qqtsim.maps import BOMB_STRESS_40
@@ -205,19 +206,23 @@ def test_hip_tick_stats_count_what_the_ticks_did(dev, n):
     hip = HipBatchedSim(cfg, n, device=dev, seed=seed, map_spec=BOMB_STRESS_40)
     ora = OracleSim(cfg, n, BOMB_STRESS_40, seed=seed)
     loop = TickLoop(hip)
-    stats = torch.zeros(3, dtype=torch.int64, device=dev)
+    stats = torch.zeros((n, 4), dtype=torch.int32, device=dev)
+    stats[:, 3] = 7
     loop._tick.tick_stats = stats.data_ptr()
     g = torch.Generator().manual_seed(seed)
-    want = np.zeros(3, dtype=np.int64)
+    want = np.zeros((n, 4), dtype=np.int64)
+    want[:, 3] = 7
     for t in range(ticks):
         mv = torch.randint(0, 5, (n, 2), generator=g)
         bb = (torch.rand((n, 2), generator=g) < 0.5).long()
         act = torch.stack([mv, bb], -1)
         _, d1, info = ora.step(act, auto_reset=True)
         loop.launch_tick(act.to(torch.int8).to(dev).contiguous())
-        want += [int(info["trig"].sum()), int(info["died"].sum()), int(d1.sum())]
+        want[:, 0] += info["trig"].reshape(n, -1).sum(1).numpy()
+        want[:, 1] += info["died"].sum(1).numpy()
+        want[:, 2] += d1.numpy()
     np.testing.assert_array_equal(stats.cpu().numpy(), want)
-    assert (want > 0).all(), want
+    assert (want[:, :3].sum(0) > 0).all(), want.sum(0)
     _compare_state(hip.state_dict(), ora.state_dict(), ticks)
 
 
