@@ -157,8 +157,9 @@ typedef struct qqt_tick_args {
  * w0 (both players' view-permuted first layers), w1, wh (the three head
  * hidden layers stacked), wf (the three output layers, block diagonal, 16
  * padded rows), the float16 residuals of w1/wh/wf (the later layers run as
- * hi/lo pairs), and float32 vectors.  w0 is [tile][64-deep K block][lane][16];
- * w1/wh/wf are [tile][32-deep K step][lane][8] in the K order in which one
+ * hi/lo pairs), and float32 vectors.  w0 is [tile][64-deep K block][lane][16],
+ * zero at K >= k0 (the act kernel's K blocks read past k0 from inside the
+ * row and rely on those zero weights); w1/wh/wf are [tile][32-deep K step][lane][8] in the K order in which one
  * layer's MFMA output tiles feed the next (csrc/mlp.hip documents both).
  * Outputs are indexed [row][player slot]. */
 typedef struct qqt_mlp_args {

@@ -209,9 +209,10 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   const size_t wtile = (size_t)nkb * 64 * 16;   // halves between weight tiles
   uint16_t* const xt = s.xw + kg * 2 * XT;      // this group's two x tiles
 
-  // Loads run PD group steps ahead; the tail mask (elements >= k0) is applied
-  // when the registers are written to LDS, so no load is waited on early.
-  // Lanes past k0 read dword 0 of their row (in bounds).
+  // Loads run PD group steps ahead and go to LDS unchanged (a select on them
+  // is scheduled early and shortens the prefetch).  Lanes past k0 read dword 0
+  // of their row (in bounds, finite): w0 is zero at K >= k0, so those
+  // products add zero.
   const uint32_t* xrp[NX];
 #pragma unroll
   for (int i = 0; i < NX; ++i) xrp[i] = xbase + obs_row(a, min(xrow0 + 2 * i, a.batch - 1)) * xstride;
@@ -225,13 +226,12 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) br[ct] = load_b(wb + ct * wtile + (size_t)kb * 64 * 16);
   };
-  auto store_x = [&](const uint32_t (&xr)[NX], int buf, int kb) {
-    const bool ok = 64 * kb + 2 * dw < a.k0;
+  auto store_x = [&](const uint32_t (&xr)[NX], int buf, int) {
     uint32_t* t = reinterpret_cast<uint32_t*>(xt + buf * XT);
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
       const int r = 4 * RT * cg + 2 * i + (lane >> 5);
-      t[r * 32 + (swz(r, dw >> 2) << 2) + (dw & 3)] = ok ? xr[i] : 0u;
+      t[r * 32 + (swz(r, dw >> 2) << 2) + (dw & 3)] = xr[i];
     }
   };
   auto compute = [&](int buf, const Frag16 (&br)[2]) {
@@ -251,10 +251,11 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   };
 
   // Group step i handles K block 2i + kg.  Register ring of PD steps in
-  // flight, LDS double buffer per group, one barrier per step, no branches:
-  // prefetch indices are clamped to the last block, and the step count is
-  // padded to a multiple of PD with all-zero x tiles (store_x masks every
-  // element >= k0), which add exactly zero.
+  // flight, LDS double buffer per group, one barrier per step: prefetch
+  // indices are clamped to the last block, and the step count is padded to a
+  // multiple of PD.  A group has at most PD padded steps (nsteps - floor(nkb/2)
+  // <= PD), so they all fall in the last PD steps, whose products are skipped
+  // by a uniform branch (their tiles hold the clamped last block).
   uint32_t xr[PD][NX];
   Frag16 br[PD][2];
   const int last = nkb - 1;
@@ -296,7 +297,7 @@ __global__ __launch_bounds__(NTHR) void mlp_act_kernel(const qqt_mlp_args a) {
   // last PD steps: everything they need is already in flight
 #pragma unroll
   for (int j = 0; j < PD; ++j) {
-    compute(j & 1, br[j]);
+    if (kblk(nsteps - PD + j) <= last) compute(j & 1, br[j]);
     if (j + 1 < PD) store_x(xr[(j + 1) % PD], (j + 1) & 1, kblk(nsteps - PD + j + 1));
     __syncthreads();
   }

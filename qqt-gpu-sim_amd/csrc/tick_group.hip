@@ -16,9 +16,10 @@
 //   scattered into (the flame cover bytes, the danger map, the danger
 //   front): a workgroup is one wavefront, so all 16,384 envs of a large
 //   batch are resident at once (16 wavefronts per CU);
-// * the observation leaves in two passes of seven channels, each staged in
-//   the env's (then dead) LDS block in output layout and copied out with
-//   16-byte stores.
+// * the observation is staged in the env's (then dead) LDS block in output
+//   layout and copied out with 16-byte stores: all channels in one pass for
+//   two-player envs at 32 lanes (a 4.75 KB block: 16 wavefronts per CU at
+//   8192 envs still fit), else in passes of seven channels.
 //
 // Semantics and float32 operation order follow the per-env kernel in
 // tick.hip, which follows the reference tick (sim/torch_sim.py:895-1261)
@@ -44,7 +45,6 @@ int fail(int code, const char* msg);
 
 namespace grp {
 
-constexpr int CPP = 7;     // observation channels per staging pass
 constexpr uint32_t STAMP_MASK = 0xF0000000u;
 constexpr int STAMP_SHIFT = 28;
 
@@ -55,6 +55,8 @@ struct Geo {
   static constexpr int KC = (C + L - 1) / L;       // cells per lane
   static constexpr int NCH = 5 * P + 4;
   static constexpr int OBS = NCH * C;
+  // observation channels per staging pass
+  static constexpr int CPP = (L == 32 && NCH * C * 2 <= 5120) ? NCH : 7;
   static constexpr int NPASS = (NCH + CPP - 1) / CPP;
   static constexpr int C4 = (C + 3) / 4 * 4;
   // block: cell words | danger front / weight by cell | danger map | cover bytes | bomb list
@@ -1168,6 +1170,7 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
     const size_t obs_base = gs * OBS;
 #pragma unroll
     for (int pass = 0; pass < G::NPASS; ++pass) {
+      constexpr int CPP = G::CPP;
       const int ch0 = pass * CPP;
       const int nch = (G::NCH - ch0) < CPP ? (G::NCH - ch0) : CPP;
       const int nbytes = nch * C * 2;
@@ -1177,17 +1180,21 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
       if (pass > 0) wave_sync();   // the previous pass's copy-out has read the block
       // Every cell of the cell-parallel channels is written below; only the
       // players' sparse channels (splat [0, P) and the player-cell channels
-      // [2P + 4, 5P + 4), which never share a pass) start from zero.
+      // [2P + 4, 5P + 4)) start from zero.  The 16-byte units that hold them
+      // are cleared first (a unit shared with a cell-parallel channel gets
+      // that channel's values afterwards: one wavefront's LDS accesses
+      // complete in order).
       {
-        constexpr int SLO = 0, SHI = P, QLO = 2 * P + 4, QHI = 5 * P + 4;
-        const int zlo = max(SLO, ch0) < min(SHI, ch0 + nch) ? max(SLO, ch0)
-                      : max(QLO, ch0) < min(QHI, ch0 + nch) ? max(QLO, ch0) : ch0;
-        const int zhi = max(SLO, ch0) < min(SHI, ch0 + nch) ? min(SHI, ch0 + nch)
-                      : max(QLO, ch0) < min(QHI, ch0 + nch) ? min(QHI, ch0 + nch) : ch0;
-        const int b0 = (opad + (zlo - ch0) * C * 2) & ~15;
-        const int b1 = min((opad + (zhi - ch0) * C * 2 + 15) & ~15, G::BLOCK);
         uint4* z = reinterpret_cast<uint4*>(blk);
-        for (int i = b0 / 16 + l; i < b1 / 16; i += L) z[i] = make_uint4(0u, 0u, 0u, 0u);
+        auto clear = [&](int lo, int hi) {   // channels [lo, hi) of the pass, when not empty
+          const int zlo = max(lo, ch0), zhi = min(hi, ch0 + nch);
+          if (zlo >= zhi) return;
+          const int b0 = (opad + (zlo - ch0) * C * 2) & ~15;
+          const int b1 = min((opad + (zhi - ch0) * C * 2 + 15) & ~15, G::BLOCK);
+          for (int i = b0 / 16 + l; i < b1 / 16; i += L) z[i] = make_uint4(0u, 0u, 0u, 0u);
+        };
+        clear(0, P);
+        clear(2 * P + 4, 5 * P + 4);
       }
       // cell-parallel channels (relative to ch0): walls+bricks, danger, time,
       // crates, and the own-bomb fuse channels
@@ -1230,22 +1237,27 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
         const uint8_t* src = blk + opad;
         const int head = min((16 - opad) & 15, nbytes);
         const int n16 = (nbytes - head) / 16;
-        if (l * 2 < head)
-          *reinterpret_cast<uint16_t*>(d8 + l * 2) = *reinterpret_cast<const uint16_t*>(src + l * 2);
-        // all of the lane's 16-byte units are read before the first store
+        const int tail0 = head + n16 * 16;
+        // every LDS read of the lane (head and tail halfwords, 16-byte units,
+        // all at clamped in-block addresses) is issued before the first store,
+        // so the copy waits on LDS once
         constexpr int NU = (CPP * C * 2 / 16 + L - 1) / L;
         const uint4* s16 = reinterpret_cast<const uint4*>(src + head);
         uint4* d16 = reinterpret_cast<uint4*>(d8 + head);
+        uint32_t hv = *reinterpret_cast<const uint16_t*>(src + min(l * 2, max(head - 2, 0)));
+        uint32_t tv = *reinterpret_cast<const uint16_t*>(src + min(tail0 + l * 2, nbytes - 2));
         uint4 u16[NU];
 #pragma clang loop unroll(full)
         for (int m = 0; m < NU; ++m) u16[m] = s16[min(l + L * m, n16 - 1)];
+        // the values are materialised here: no read sinks below a store
+        asm volatile("" : "+v"(hv), "+v"(tv));
+#pragma clang loop unroll(full)
+        for (int m = 0; m < NU; ++m) asm volatile("" : "+v"(u16[m].x), "+v"(u16[m].y), "+v"(u16[m].z), "+v"(u16[m].w));
+        if (l * 2 < head) *reinterpret_cast<uint16_t*>(d8 + l * 2) = (uint16_t)hv;
 #pragma clang loop unroll(full)
         for (int m = 0; m < NU; ++m)
           if (l + L * m < n16) d16[l + L * m] = u16[m];
-        const int tail0 = head + n16 * 16;
-        if (tail0 + l * 2 < nbytes)
-          *reinterpret_cast<uint16_t*>(d8 + tail0 + l * 2) =
-              *reinterpret_cast<const uint16_t*>(src + tail0 + l * 2);
+        if (tail0 + l * 2 < nbytes) *reinterpret_cast<uint16_t*>(d8 + tail0 + l * 2) = (uint16_t)tv;
       }
     }
   }
