@@ -809,7 +809,8 @@ int fail(int code, const char* msg) {
 #define QQT_TICK_WPB 2
 #endif
 
-// The STEP tick (tick_group.hip): four envs per wavefront.
+// The STEP tick (tick_group.hip): two envs per wavefront up to 8192 envs,
+// four above.
 template <int H, int W, int P>
 int launch_step_group(const qqt_sim_config* cfg, const qqt_tick_args* a, hipStream_t st);
 
