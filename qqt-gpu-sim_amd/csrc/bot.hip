@@ -80,44 +80,37 @@ __global__ __launch_bounds__(64 * WPB) void bot_kernel(const qqt_sim_config cf, 
 
   // ---- every global load is issued first; the Philox noise is computed
   // (lane 0: words 0-3, lane 1: words 4-7) while they are in flight
+  // Every lane loads from a clamped in-bounds index and every use is guarded
+  // by the lane's range: a select on a loaded value would make the kernel
+  // wait for that load before issuing the rest.
   uint32_t wreg[KMAX];
   uint16_t dreg[KMAX];
 #pragma unroll
   for (int k = 0; k < KMAX; ++k) {
-    const int c = lane + 64 * k;
-    wreg[k] = c < C ? (uint32_t)a.cells[(size_t)g * C + c] : 0u;
-    dreg[k] = c < C ? obs[c] : (uint16_t)0;
+    const int c = min(lane + 64 * k, C - 1);
+    wreg[k] = (uint32_t)a.cells[(size_t)g * C + c];
+    dreg[k] = obs[c];
   }
-  const int plv = lane < NPL ? a.players[(size_t)g * NPL + lane] : 0;
-  const int mv = lane < 5 ? a.move_mask[((size_t)g * P + pid) * 5 + lane] : 0;
-  const int bv = lane < 2 ? a.bomb_mask[((size_t)g * P + pid) * 2 + lane] : 0;
-  const float uv = (a.uniforms && lane < 5) ? a.uniforms[(size_t)g * 5 + lane] : 0.0f;
+  const int plv = a.players[(size_t)g * NPL + min(lane, NPL - 1)];
+  const int mv = a.move_mask[((size_t)g * P + pid) * 5 + min(lane, 4)];
+  const int bv = a.bomb_mask[((size_t)g * P + pid) * 2 + min(lane, 1)];
+  // (loads are unconditional, so that the compiler counts them exactly: a
+  // source that is not in use is read from a buffer that is, and ignored)
+  const float* const usrc = a.uniforms ? a.uniforms + (size_t)g * 5
+                                       : reinterpret_cast<const float*>(a.players);
+  const float uv = usrc[min(lane, 4)];
   int reach_in = a.reach_mode == 1 ? a.reach[a.reach_slot & 1]
                  : a.reach_mode == 2 ? a.reach[0] : 0;
-  if (a.reach_mode == 3) {   // the batch max of the caps the last STEP tick wrote
-    // 16 caps per lane load, eight loads in flight per lane (8192 envs per pass)
-    const uint4* c16 = reinterpret_cast<const uint4*>(a.reach_caps);
-    const int n16 = (a.n_envs + 15) >> 4;
-    uint32_t m = 0u;
-    for (int base = 0; base < n16; base += 512) {
-      uint4 v[8];
+  // reach mode 3: the caps the last STEP tick wrote, 16 per lane load; the
+  // first 8192 are loaded here with everything else and reduced where the
+  // chain check needs them, so their latency overlaps the cost fields
+  const bool caps = a.reach_mode == 3;
+  const uint4* const c16 = reinterpret_cast<const uint4*>(caps ? (const void*)a.reach_caps
+                                                               : (const void*)a.cells);
+  const int n16 = caps ? (a.n_envs + 15) >> 4 : 1;
+  uint4 capv[8];   // lanes past the caps re-read the last unit (the max is unchanged)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int i = base + lane + 64 * j;
-        v[j] = i < n16 ? c16[i] : make_uint4(0u, 0u, 0u, 0u);
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q)   // four caps in 0..127 per word
-          m = max(m, max(max(w[q] & 0xffu, (w[q] >> 8) & 0xffu), max((w[q] >> 16) & 0xffu, w[q] >> 24)));
-      }
-    }
-#pragma unroll
-    for (int sh = 32; sh >= 1; sh >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, sh, 64));
-    reach_in = (int)m;
-  }
+  for (int j = 0; j < 8; ++j) capv[j] = c16[min(lane + 64 * j, n16 - 1)];
   if (!a.uniforms && lane < 2) {
     float ub[4];
     philox_block(a.seed, (uint32_t)g, a.tick, STREAM_BOT, (uint32_t)lane, ub);
@@ -235,6 +228,22 @@ __global__ __launch_bounds__(64 * WPB) void bot_kernel(const qqt_sim_config cf, 
   const int c = min(max((int)floorf(bx), 0), W - 1);
   const bool alive = pl[pid * QQT_P_SLOTS + QQT_P_ALIVE] != 0;
   const int cap = pl[pid * QQT_P_SLOTS + QQT_P_BLAST_CAP];
+  if (a.reach_mode == 3) {   // the batch max of the caps (each in 0..127)
+    auto bmax = [](uint32_t m, const uint4& v) {
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        m = max(m, max(max(w[q] & 0xffu, (w[q] >> 8) & 0xffu), max((w[q] >> 16) & 0xffu, w[q] >> 24)));
+      return m;
+    };
+    uint32_t m = 0u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = bmax(m, capv[j]);
+    for (int i = 512 + lane; i < n16; i += 64) m = bmax(m, c16[i]);   // batches past 8192 envs
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, sh, 64));
+    reach_in = (int)m;
+  }
   const int reach = a.reach_mode != 0 ? reach_in : cap;
 
   // chain: a bomb with fuse 1..10 within `reach` cells in line (lane = step, direction)
