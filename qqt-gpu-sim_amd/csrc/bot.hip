@@ -197,13 +197,32 @@ __global__ __launch_bounds__(64 * WPB) void bot_kernel(const qqt_sim_config cf, 
     vsr[k] = c < C ? s.vs[c] : INF;
     vor[k] = c < C ? s.vo[c] : INF;
   }
+  // A cell can only improve when a neighbour changed since it was last
+  // relaxed, so a pass relaxes the cells next to a change of the previous
+  // pass or of an earlier slice of this one (every cell in the first pass).
+  // Change sets are one 64-cell ballot per slice, shifted by 1 and W to find
+  // the neighbours; a superset (row wrap-around) only costs work.
+  uint64_t prev[KMAX];
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) prev[k] = ~0ull;
+  // bit i: a neighbour (c - 1, c + 1, c - W, c + W) of cell c = 64k + i is in x
+  auto near = [](const uint64_t (&x)[KMAX], int k) -> uint64_t {
+    const uint64_t w = x[k], lo = k > 0 ? x[k - 1] : 0ull, hi = k + 1 < KMAX ? x[k + 1] : 0ull;
+    return ((w << 1) | (lo >> 63)) | ((w >> 1) | (hi << 63)) |
+           ((w << W) | (lo >> (64 - W))) | ((w >> W) | (hi << (64 - W)));
+  };
   for (int pass = 0; pass < 4 * C; ++pass) {
-    bool changed = false;
+    uint64_t seen[KMAX];   // the previous pass's changes, then this pass's of earlier slices
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) seen[k] = prev[k];
+    bool any = false;
 #pragma unroll
     for (int k = 0; k < KMAX; ++k) {
+      const uint64_t act = near(seen, k);
       const int c = lane + 64 * k;
       const float cc = cst[k];
-      if (c < C && cc != INF) {
+      bool changed = false;
+      if (((act >> lane) & 1ull) && c < C && cc != INF) {
         const int r = c / W, col = c % W;
         float ns = INF, no = INF;
         if (r > 0) { ns = fminf(ns, s.vs[c - W]); no = fminf(no, s.vo[c - W]); }
@@ -214,8 +233,12 @@ __global__ __launch_bounds__(64 * WPB) void bot_kernel(const qqt_sim_config cf, 
         if (cs < vsr[k]) { vsr[k] = cs; s.vs[c] = cs; changed = true; }
         if (co < vor[k]) { vor[k] = co; s.vo[c] = co; changed = true; }
       }
+      const uint64_t ch = __ballot(changed);
+      prev[k] = ch;
+      seen[k] |= ch;
+      any |= ch != 0ull;
     }
-    if (__ballot(changed) == 0ull) break;
+    if (!any) break;
     wave_sync();
   }
   wave_sync();
