@@ -282,34 +282,39 @@ __global__ __launch_bounds__(64 * WPB) void bot_kernel(const qqt_sim_config cf, 
   }
   const bool chain = __ballot(chain_l) != 0ull;
 
+  // the five candidate moves (up, down, left, right, stay), one per lane
+  // 0-4, then read by lane 0 (the scoring below is one lane's work)
+  const int kk = min(lane, 4);
+  const int ck = kk == 0 ? max(r - 1, 0) * W + c : kk == 1 ? min(r + 1, H - 1) * W + c
+               : kk == 2 ? r * W + max(c - 1, 0) : kk == 3 ? r * W + min(c + 1, W - 1) : r * W + c;
+  const uint32_t wk = s.cw[ck];
+  const bool legal_k = s.mm[kk] != 0 && !(wk & (bot::F_WALL | bot::F_BRICK));
+  const bool thr_k = s.thr[ck] != 0;
+  const float thf_k = thr_k ? 1.0f : 0.0f;
+  const float noise_k = 0.05f * s.u[kk];
+  const float dng_k = s.dng[ck];
+  float ap_k = ((s.vo[ck] + 2.0f * dng_k) + 2.0f * thf_k) + noise_k;
+  if (dng_k >= 0.5f || !legal_k) ap_k = INF;
+  const float esc_k = ((s.vs[ck] * 100.0f) + 2.0f * thf_k) + noise_k;
+  const int flags_k = (legal_k ? 1 : 0) | (thr_k ? 2 : 0);
+  float app[5], esc[5], dngc[5];
+  bool legal[5], thr[5];
+#pragma unroll
+  for (int k = 0; k < 5; ++k) {
+    app[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ap_k), k));
+    esc[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(esc_k), k));
+    dngc[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dng_k), k));
+    const int f = __builtin_amdgcn_readlane(flags_k, k);
+    legal[k] = (f & 1) != 0;
+    thr[k] = (f & 2) != 0;
+  }
+
   if (lane == 0) {
-    const float* u = s.u;
-    const uint8_t* mm = s.mm;
     const uint8_t* bm = s.bm;
     const float own_dng = s.dng[r * W + c];
-    int cell[5];
-    cell[0] = max(r - 1, 0) * W + c;
-    cell[1] = min(r + 1, H - 1) * W + c;
-    cell[2] = r * W + max(c - 1, 0);
-    cell[3] = r * W + min(c + 1, W - 1);
-    cell[4] = r * W + c;
-    float app[5], esc[5], dngc[5];
-    bool legal[5], thr[5];
     bool app_ok = false;
 #pragma unroll
-    for (int k = 0; k < 5; ++k) {
-      const uint32_t w = s.cw[cell[k]];
-      legal[k] = mm[k] != 0 && !(w & (bot::F_WALL | bot::F_BRICK));
-      thr[k] = s.thr[cell[k]] != 0;
-      const float thf = thr[k] ? 1.0f : 0.0f;
-      const float noise = 0.05f * u[k];
-      dngc[k] = s.dng[cell[k]];
-      float ap = ((s.vo[cell[k]] + 2.0f * dngc[k]) + 2.0f * thf) + noise;
-      if (dngc[k] >= 0.5f || !legal[k]) ap = INF;
-      app[k] = ap;
-      app_ok |= ap != INF;
-      esc[k] = ((s.vs[cell[k]] * 100.0f) + 2.0f * thf) + noise;
-    }
+    for (int k = 0; k < 5; ++k) app_ok |= app[k] != INF;
     const bool use_esc = own_dng >= 0.35f || !app_ok;
     float score[5];
 #pragma unroll
