@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 20
+#define QQT_ABI_VERSION 21
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -142,12 +142,14 @@ typedef struct qqt_tick_args {
                                  slot 3 is left as it is.  For benchmark harnesses that
                                  report what their timed ticks did (sum over envs after
                                  the launches); no reference counterpart. */
-  int8_t* reach_caps;         /* STEP: int8 [N rounded up to a multiple of 16] or NULL:
-                                 entry n = the blast cap of player reach_pid of env n
-                                 after the tick and its auto-reset (the padding is left
-                                 as it is).  The astar bot's next call reduces it to the
-                                 batch max (qqt_bot_args reach_mode 3) instead of a
-                                 reduction launch of its own. */
+  int8_t* reach_caps;         /* STEP: int8 [N rounded up to a multiple of 16], zeroed
+                                 once by the caller, or NULL: maxima of the blast cap
+                                 of player reach_pid after the tick and its auto-reset,
+                                 one per group of E consecutive envs (E = 2 up to 8192
+                                 envs, else 4), in the first ceil(N / E) entries (the
+                                 rest is left as it is).  The astar bot's next call
+                                 reduces them to the batch max (qqt_bot_args
+                                 reach_mode 3) instead of a reduction launch of its own. */
   int32_t reach_pid;
 } qqt_tick_args;
 
@@ -256,8 +258,8 @@ typedef struct qqt_bot_args {
   const uint8_t* bomb_mask;   /* [N][P][2] */
   const float* uniforms;      /* [N][5] noise uniforms, or NULL = Philox stream 7 */
   int32_t* reach;             /* device int32[2] (mode 1) or scalar (mode 2) */
-  const int8_t* reach_caps;   /* mode 3: the tick's caps, int8 [N rounded up to 16],
-                                 16-byte aligned */
+  const int8_t* reach_caps;   /* mode 3: the tick's cap maxima, int8 [N rounded up to
+                                 16], 16-byte aligned, zero past the tick's entries */
   int64_t* actions;           /* [N][P][2], slot pid written; or NULL */
   int8_t* actions_i8;         /* same as int8; or NULL */
 } qqt_bot_args;

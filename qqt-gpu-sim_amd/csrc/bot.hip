@@ -101,16 +101,19 @@ __global__ __launch_bounds__(64 * WPB) void bot_kernel(const qqt_sim_config cf, 
   const float uv = usrc[min(lane, 4)];
   int reach_in = a.reach_mode == 1 ? a.reach[a.reach_slot & 1]
                  : a.reach_mode == 2 ? a.reach[0] : 0;
-  // reach mode 3: the caps the last STEP tick wrote, 16 per lane load; the
-  // first 8192 are loaded here with everything else and reduced where the
-  // chain check needs them, so their latency overlaps the cost fields
+  // reach mode 3: the cap maxima the last STEP tick wrote (one per tick
+  // wavefront), 16 per lane load; the first 4096 are loaded here with
+  // everything else and reduced where the chain check needs them, so their
+  // latency overlaps the cost fields
   const bool caps = a.reach_mode == 3;
   const uint4* const c16 = reinterpret_cast<const uint4*>(caps ? (const void*)a.reach_caps
                                                                : (const void*)a.cells);
-  const int n16 = caps ? (a.n_envs + 15) >> 4 : 1;
-  uint4 capv[8];   // lanes past the caps re-read the last unit (the max is unchanged)
+  const int epw = tick_envs_per_wave(a.n_envs);
+  const int n16 = caps ? ((a.n_envs + epw - 1) / epw + 15) >> 4 : 1;
+  constexpr int CAPL = 4;   // loads per lane up front
+  uint4 capv[CAPL];   // lanes past the maxima re-read the last unit (the max is unchanged)
 #pragma unroll
-  for (int j = 0; j < 8; ++j) capv[j] = c16[min(lane + 64 * j, n16 - 1)];
+  for (int j = 0; j < CAPL; ++j) capv[j] = c16[min(lane + 64 * j, n16 - 1)];
   if (!a.uniforms && lane < 2) {
     float ub[4];
     philox_block(a.seed, (uint32_t)g, a.tick, STREAM_BOT, (uint32_t)lane, ub);
@@ -261,8 +264,8 @@ __global__ __launch_bounds__(64 * WPB) void bot_kernel(const qqt_sim_config cf, 
     };
     uint32_t m = 0u;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) m = bmax(m, capv[j]);
-    for (int i = 512 + lane; i < n16; i += 64) m = bmax(m, c16[i]);   // batches past 8192 envs
+    for (int j = 0; j < CAPL; ++j) m = bmax(m, capv[j]);
+    for (int i = 64 * CAPL + lane; i < n16; i += 64) m = bmax(m, c16[i]);   // larger batches
 #pragma unroll
     for (int sh = 32; sh >= 1; sh >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, sh, 64));
     reach_in = (int)m;

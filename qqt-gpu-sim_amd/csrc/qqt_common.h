@@ -16,6 +16,15 @@ namespace qqt {
 // round on an XCD's 32 CUs (22 envs each), and 256 act workgroups.
 constexpr int XCD_ROWS = 44;
 
+// Envs per wavefront of the STEP tick: two (32 lanes each) up to
+// GROUP32_MAX_ENVS envs, four above.  The tick writes the astar bot's reach
+// source one blast-cap maximum per wavefront, i.e. per group of that many
+// envs.
+constexpr int GROUP32_MAX_ENVS = 8192;
+__host__ __device__ inline int tick_envs_per_wave(int n_envs) {
+  return n_envs <= GROUP32_MAX_ENVS ? 2 : 4;
+}
+
 // Philox stream ids (third counter word); the host oracle uses the same ids.
 enum : uint32_t {
   STREAM_CRATE = 1, STREAM_RESET_CELL = 2, STREAM_RESET_MISC = 3,

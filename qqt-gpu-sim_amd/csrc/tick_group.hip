@@ -1294,10 +1294,17 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
     }
   }
 
-  // ---- 16. optional per-env blast cap of one player (int8), the astar
-  // bot's chain-check reach source for its next call
+  // ---- 16. optional blast-cap maximum of one player over the wavefront's
+  // envs (int8, one per wavefront), the astar bot's chain-check reach source
+  // for its next call
   int8_t* const rcaps = A->reach_caps;
-  if (rcaps && valid && l == A->reach_pid) rcaps[gs] = (int8_t)min(r.zcap, 127);
+  if (rcaps) {
+    const int cap = (valid && l == A->reach_pid) ? min(r.zcap, 127) : 0;
+    int m = 0;
+#pragma unroll
+    for (int ee = 0; ee < EPW; ++ee) m = max(m, __builtin_amdgcn_readlane(cap, L * ee + A->reach_pid));
+    if (lane == 0) rcaps[g0 / EPW] = (int8_t)m;
+  }
 }
 
 }  // namespace grp
@@ -1307,8 +1314,8 @@ __global__ __launch_bounds__(64, 4) void tick_group_kernel(const qqt_sim_config 
 // GROUP32_MAX_ENVS envs an env takes 32 lanes (two envs per wavefront: at
 // 5632 envs, 2816 wavefronts keep every SIMD at two or three of them and
 // halve the per-wavefront cell work); larger batches take 16 lanes per env
-// (four per wavefront), which keeps 16,384 envs resident in one round.
-constexpr int GROUP32_MAX_ENVS = 8192;
+// (four per wavefront), which keeps 16,384 envs resident in one round
+// (GROUP32_MAX_ENVS, tick_envs_per_wave in qqt_common.h).
 
 template <int H, int W, int P, int L>
 int launch_group(const qqt_sim_config* cfg, const qqt_tick_args* a, hipStream_t st) {

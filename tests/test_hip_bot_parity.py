@@ -125,12 +125,15 @@ def test_hip_bot_reach_follows_the_batch_from_call_to_call(dev):
             np.testing.assert_array_equal(got.cpu().numpy(), want, err_msg=f"rep {rep}")
 
 
-def test_tick_written_reach_equals_the_batch_max(dev):
-    """A Rollout's STEP ticks leave the bot's chain-check reach source (its
-    blast cap per env, whose batch max is the reach of sim/bots.py:477): the
-    caps equal the state's, the bot's next call reads them (reach mode 3) and
-    draws the same actions as a twin bot reducing the batch itself (mode 1),
-    and a state change after the tick sends the bot back to the reduction."""
+@pytest.mark.parametrize("n", [301, 8200])
+def test_tick_written_reach_equals_the_batch_max(dev, n):
+    """A Rollout's STEP ticks leave the bot's chain-check reach source (the
+    batch max of its blast cap, sim/bots.py:477): the largest cap among each
+    tick wavefront's envs (groups of 2 up to 8192 envs, 301 -> 151 entries;
+    groups of 4 above, 8200 -> 2050), padding zero; the bot's next call reads
+    them (reach mode 3) and draws the same actions as a twin bot reducing
+    the batch itself (mode 1), and a state change after the tick sends the
+    bot back to the reduction."""
     from qqtsim.bots import HipAstarBot
     from qqtsim.config import corridor_training_config
     from qqtsim.maps import BOMB_STRESS_40
@@ -138,18 +141,24 @@ def test_tick_written_reach_equals_the_batch_max(dev):
     from qqtsim.rollout import Rollout
     from qqtsim.sim import HipBatchedSim
 
-    n = 301                                   # caps padded to 304 with zeros
     cfg = corridor_training_config()
     sim = HipBatchedSim(cfg, n, device=dev, seed=3, map_spec=BOMB_STRESS_40)
     net = HipActorCritic(default_init(cfg.obs_shape), device=dev, seed=3)
     bot = HipAstarBot(sim, pid=1)
     roll = Rollout(sim, net, opponent=bot)
+    group = 2 if n <= 8192 else 4
+    ng = -(-n // group)
     for _ in range(6):
         roll.step()
         torch.cuda.synchronize()
-        cap = sim.state_dict()["blast_cap"][:, 1]
-        np.testing.assert_array_equal(bot._caps[:n].cpu().numpy(), cap.cpu().numpy())
-        assert int(bot._caps[n:].abs().sum()) == 0
+        cap = sim.state_dict()["blast_cap"][:, 1].cpu().numpy()
+        pad = np.zeros(ng * group, dtype=cap.dtype)
+        pad[:n] = cap
+        want = pad.reshape(ng, group).max(axis=1)
+        caps = bot._caps.cpu().numpy()
+        np.testing.assert_array_equal(caps[:ng], want)
+        assert int(np.abs(caps[ng:]).sum()) == 0
+        assert int(caps.max()) == int(cap.max())
     assert len(set(sim.state_dict()["blast_cap"][:, 1].tolist())) > 1
     twin = HipAstarBot(sim, pid=1)
     twin.tick = bot.tick
