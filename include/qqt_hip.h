@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 21
+#define QQT_ABI_VERSION 22
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -441,11 +441,18 @@ int qqt_gather_rows(const qqt_gather_args* args, void* stream);
  * 14 with zero weights, and conv 16->32) combination c = 4 step + g, tap
  * c / 2 (taps 3 dy + dx; combinations 18, 19 are zero), channels 8 (c % 2)..;
  * for 32 input channels tap = step, channels 8 g..; for the 1x1 conv
- * channels 8 (4 step + g)...  Linear weights are float32 [tile][step][lane],
- * lane l holding output 16 tile + l % 16, input 4 step + l / 16.
- * LayerNorm tables are packed [tile][11 position tiles][lane][4] (value q of
- * lane l: channel 16 tile + l % 16, position 16 ptile + 4 (l / 16) + q;
- * zero past 169 positions or the channel count), 16-byte aligned. */
+ * channels 8 (4 step + g)...  Linear(1352,128) comes as float16 hi / lo
+ * planes [tile][43 steps][lane][8]: lane l holds output 16 tile + l % 16 and
+ * inputs 32 step + 8 (l / 16) .. + 7 of the flattened [8][13][13] (inputs
+ * 1352..1375 zero).  The other Linear weights are float32
+ * [tile][step][lane], lane l holding output 16 tile + l % 16, input
+ * 4 step + l / 16.  LayerNorm tables are packed [tile][11 position
+ * tiles][lane][4] (value q of lane l: channel 16 tile + l % 16, position
+ * 16 ptile + 4 (l / 16) + q; zero past 169 positions or the channel count),
+ * 16-byte aligned.  Two launches on `stream`: the trunk writes each item's
+ * flattened features as float16 hi / lo rows into the workspace, the head
+ * reads them; calls that overlap on one workspace race. */
+#define QQT_CNN_WS_BYTES_PER_ITEM 5504   /* workspace bytes per (row, player) item */
 typedef struct qqt_cnn_args {
   int32_t batch;              /* rows B */
   int32_t npid;               /* 1: player pid0 only; 2: both players */
@@ -472,8 +479,9 @@ typedef struct qqt_cnn_args {
   const float *c2b, *ln2w, *ln2b;         /* [64]; LN [4][11][64][4] */
   const uint16_t *c3w, *c3w_lo;           /* 1x1 64->8 [1][2][64][8] (outputs 8..15 zero) */
   const float *c3b, *ln3w, *ln3b;         /* [16] (8..15 zero); LN [1][11][64][4] */
-  const float *s0p, *s0b;     /* Linear(1352,128) packed [8][338][64] (input index
-                                 c * 169 + p of the flattened [8][13][13]); [128] */
+  const uint16_t *s0h, *s0l;  /* Linear(1352,128) float16 hi / lo [8][43][64][8] (input
+                                 index c * 169 + p of the flattened [8][13][13]) */
+  const float* s0b;           /* [128] */
   const float *s1w, *s1b;     /* LayerNorm(128) */
   const float *s3p, *s3b;     /* Linear(128,128) packed [8][32][64]; [128] */
   const float *s4w, *s4b;     /* LayerNorm(128) */
@@ -488,6 +496,9 @@ typedef struct qqt_cnn_args {
   float* logp_out;            /* [B][out_slots] or NULL */
   float* value_out;           /* [B][out_slots] or NULL */
   float* logits_out;          /* [B][out_slots][8]: 5 move, 2 bomb, value; or NULL */
+  uint16_t* workspace;        /* >= B * npid * QQT_CNN_WS_BYTES_PER_ITEM bytes, 16-byte
+                                 aligned: the trunk's float16 hi / lo feature rows */
+  int64_t workspace_bytes;
 } qqt_cnn_args;
 int qqt_cnn_act(const qqt_cnn_args* args, void* stream);
 
@@ -571,8 +582,9 @@ int qqt_lstm_act(const qqt_lstm_args* args, void* stream);
  * most 4096 launches are timed between collects.  Allocates no device
  * memory (the event pool is created by the first arm). */
 enum { QQT_KERNEL_TICK = 0, QQT_KERNEL_MLP = 1, QQT_KERNEL_BOT = 2, QQT_KERNEL_REACH = 3,
-       QQT_KERNEL_GAE = 4, QQT_KERNEL_L1GRAD = 5, QQT_KERNEL_PPO = 6, QQT_KERNEL_CNN = 7,
-       QQT_KERNEL_LSTM_FEAT = 8, QQT_KERNEL_LSTM = 9, QQT_KERNEL_KINDS = 10 };
+       QQT_KERNEL_GAE = 4, QQT_KERNEL_L1GRAD = 5, QQT_KERNEL_PPO = 6, QQT_KERNEL_CNN = 7 /* trunk */,
+       QQT_KERNEL_LSTM_FEAT = 8, QQT_KERNEL_LSTM = 9, QQT_KERNEL_CNN_HEAD = 10,
+       QQT_KERNEL_KINDS = 11 };
 int qqt_timing_arm(int32_t launches);
 int qqt_timing_collect(double* ms, int32_t* count, int32_t n_kinds);
 

@@ -9,17 +9,20 @@
 // heads 128 -> 64 -> ReLU -> 5 | 2 | 1.  Every LayerNorm normalises one
 // sample over all of its values (eps 1e-5) with an elementwise affine.
 //
-// Persistent kernel: one workgroup (4 wavefronts, one per SIMD, so each
-// wavefront may hold 512 registers) per CU walks a contiguous range of items
-// (row, player).
+// Two kernels.  cnn_trunk_kernel: persistent, two workgroups of 4
+// wavefronts per CU (one wavefront per SIMD each, 256 registers), each
+// walking a contiguous range of items (row, player) one item at a time, so
+// one workgroup's barriers and LayerNorm reductions overlap the other's
+// convolutions.  cnn_head_kernel: 16 items per workgroup, from the trunk's
+// flattened features in the workspace.
 //
-// Trunk, one item at a time.  Feature maps live in LDS as zero-bordered
-// 15 x 15 grids of positions with the channels of a position contiguous
-// (72 halves per position), as float16 hi and lo planes (x = hi + lo).
-// Convolutions are implicit GEMMs on v_mfma_f32_16x16x32_f16 with float32
-// accumulation: M = positions (11 tiles of 16), N = output channels, K in
-// steps of 32 = four 8-channel blocks, so lane l's A operand (8 halves) is
-// one 16-byte LDS read of 8 channels at one position and tap:
+// Trunk.  Feature maps live in LDS as zero-bordered 15 x 15 grids of
+// positions with the channels of a position contiguous (72 halves per
+// position), as float16 hi and lo planes (x = hi + lo).  Convolutions are
+// implicit GEMMs on v_mfma_f32_16x16x32_f16 with float32 accumulation: M =
+// positions (11 tiles of 16), N = output channels, K in steps of 32 = four
+// 8-channel blocks, so lane l's A operand (8 halves) is one 16-byte LDS read
+// of 8 channels at one position and tap:
 //   16 input channels (conv0, conv 16->32): step s, lane group g = l / 16
 //     takes combination c = 4 s + g: tap min(c / 2, 8), channels 8 (c % 2)..;
 //     combinations 18, 19 carry zero weights;
@@ -35,11 +38,13 @@
 // are the layer's output: the per-sample LayerNorm reduces them across the
 // workgroup (mean, then squared deviations) and the rectified, normalised
 // values are written over the input planes as hi/lo halves (after the last
-// conv, into this item's row of the float32 flat buffer).
-// Head, per batch of up to 15 items: Linear(1352,128), Linear(128,128) and
-// the heads' hidden layer are v_mfma_f32_16x16x4_f32 GEMMs with M = the items
-// (B streamed from L2 once per batch), LayerNorm(128) by 16 threads per item,
-// then the output layer and the masked sampling per item.
+// conv, into this item's workspace row: 1376 hi halves, then 1376 lo, the
+// flattened index c * 169 + p, zero from 1352).
+// Head: Linear(1352,128) on the same float16 MFMA with the three hi/lo
+// products (K = 43 steps of 32), then Linear(128,128) and the heads' hidden
+// layer as v_mfma_f32_16x16x4_f32 GEMMs with M = the 16 items,
+// LayerNorm(128) by 16 threads per item, the output layer and the masked
+// sampling per item.
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -64,24 +69,28 @@ constexpr int HW = 13, NP = 169, MT = 11;
 constexpr int PP = 225;                     // padded positions (15 x 15)
 constexpr int CS = 72;                      // halves per position (64 channels + 8: bank spread)
 constexpr int C0 = 14;
-constexpr int SB = 15;                      // items per head batch (<= the 16 MFMA rows)
+constexpr int HB = 16;                      // items per head workgroup (the 16 MFMA rows)
 constexpr int FLAT = 8 * NP;                // 1352
-constexpr int FS = 1378;                    // flat row stride (2 mod 32 banks)
+constexpr int KF = 1376;                    // flattened features padded to 43 K steps of 32
+constexpr int S0H = KF / 32;                // 43
+constexpr int WS_ROW = 2 * KF;              // workspace halves per item (hi row, lo row)
 constexpr int HID = 128, HS = 130, HYS = 194;
 constexpr int S0 = 5, S1 = 5, S2 = 9, S3 = 2;       // 32-deep K steps of the four convolutions
-constexpr int L0 = FLAT / 4, L1 = HID / 4;          // K steps of the head GEMMs
+constexpr int L1 = HID / 4;                         // K steps of the float32 head GEMMs
 constexpr int BFRAG = 64 * 8;                       // halves of one step's B fragments
+static_assert(WS_ROW * 2 == QQT_CNN_WS_BYTES_PER_ITEM, "workspace row size");
 
 struct __align__(16) Lds {                 // every member a multiple of 16 bytes long
   uint16_t act[2][PP * CS];                 // hi, lo planes [position][channel]
   uint16_t wc0[2][S0 * BFRAG], wc3[2][S3 * BFRAG];   // conv0 / 1x1 B (hi, lo), all waves
-  float flat[SB * FS];                      // trunk outputs; head scratch after GEMM 1
   float red[2][NW];
 };
 static_assert(sizeof(uint16_t) * 2 * PP * CS % 16 == 0, "16-byte fragment reads stay aligned");
-// head scratch inside flat (free once Linear(1352,128) has read it)
-constexpr int H_OFF = 0, H2_OFF = SB * HS, HY_OFF = 2 * SB * HS, LG_OFF = 2 * SB * HS + SB * HYS;
-static_assert(LG_OFF + 16 * 8 <= SB * FS, "head scratch (16 rows) fits in the flat buffer");
+static_assert(2 * sizeof(Lds) <= 160 * 1024, "two trunk workgroups fit in one CU's LDS");
+
+struct __align__(16) HeadLds {
+  float h[HB * HS], h2[HB * HS], hy[HB * HYS], lg[HB * 8];
+};
 
 __device__ __forceinline__ floatx4 mfma(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -112,13 +121,24 @@ __device__ __forceinline__ floatx4 mfma16(half8 a, half8 b, floatx4 c) {
 }
 struct BFrag { half8 hi, lo; };
 
+// float32 -> float16 hi + lo (x = hi + lo to ~2^-22 relative), saturating
+// at float16's range so that both halves stay finite.
+__device__ __forceinline__ void split16(float x, uint16_t& hi, uint16_t& lo) {
+  const __half h = __float2half_rn(fminf(fmaxf(x, -65504.0f), 65504.0f));
+  hi = __half_as_ushort(h);
+  lo = __half_as_ushort(__float2half_rn(fminf(fmaxf(x - __half2float(h), -65504.0f), 65504.0f)));
+}
+
 __device__ __forceinline__ constexpr int tap_off(int tap) { return (tap / 3) * 15 + tap % 3; }
 
 // One conv layer for this wavefront (KIND 0: 3x3 over 16 channels, 1: 3x3
 // over 32, 2: 1x1 over 64): position tiles min(mt0 + t ms, 10), t < NTL
 // (duplicates of tile 10 are computed and later ignored); acc[t] = bias +
 // sum over steps of A B, three float16 products per step (two without the
-// activations' lo plane).  bfrag(s) returns step s's B fragments.
+// activations' lo plane).  bfrag(s) returns step s's B fragments; the step
+// loop stays rolled, with the next step's B fragments loaded one step
+// ahead, and each product kind runs over all tiles before the next, so no
+// two consecutive MFMAs share an accumulator.
 template <int KIND, int STEPS, int NTL, bool ALO, class BF>
 __device__ __forceinline__ void conv(const uint16_t* act_hi, const uint16_t* act_lo, BF bfrag,
                                      float bias, int mt0, int ms, floatx4 (&acc)[NTL]) {
@@ -132,23 +152,32 @@ __device__ __forceinline__ void conv(const uint16_t* act_hi, const uint16_t* act
                         : (pb + 16) * CS + 8 * kq;
     acc[t] = floatx4{bias, bias, bias, bias};
   }
-#pragma unroll
+  BFrag b = bfrag(0);
+#pragma unroll 1
   for (int st = 0; st < STEPS; ++st) {
+    const BFrag bn = bfrag(min(st + 1, STEPS - 1));
     int off;
     if constexpr (KIND == 0)
-      off = ((kq >> 1) ? tap_off(min(2 * st + 1, 8)) : tap_off(min(2 * st, 8))) * CS;
+      off = tap_off(min(2 * st + (kq >> 1), 8)) * CS;
     else if constexpr (KIND == 1)
       off = tap_off(st) * CS;
     else
       off = 32 * st;
-    const BFrag b = bfrag(st);
+    half8 ah[NTL], al[NTL];
 #pragma unroll
     for (int t = 0; t < NTL; ++t) {
-      const half8 ah = ld8(act_hi + base[t] + off);
-      acc[t] = mfma16(ah, b.hi, acc[t]);
-      acc[t] = mfma16(ah, b.lo, acc[t]);
-      if constexpr (ALO) acc[t] = mfma16(ld8(act_lo + base[t] + off), b.hi, acc[t]);
+      ah[t] = ld8(act_hi + base[t] + off);
+      if constexpr (ALO) al[t] = ld8(act_lo + base[t] + off);
     }
+#pragma unroll
+    for (int t = 0; t < NTL; ++t) acc[t] = mfma16(ah[t], b.hi, acc[t]);
+#pragma unroll
+    for (int t = 0; t < NTL; ++t) acc[t] = mfma16(ah[t], b.lo, acc[t]);
+    if constexpr (ALO) {
+#pragma unroll
+      for (int t = 0; t < NTL; ++t) acc[t] = mfma16(al[t], b.hi, acc[t]);
+    }
+    b = bn;
   }
 }
 
@@ -182,20 +211,24 @@ __device__ __forceinline__ void ln_stats(const floatx4 (&acc)[NTL], int mt0, int
 }
 
 // relu(LN affine) of this wavefront's outputs: into the hi/lo activation
-// planes, or (flat != nullptr) into flat[n * 169 + p].  g / bt: [NT][11][64][4]
-// packed.
+// planes, or (fl != nullptr) into the workspace row fl (hi at n * 169 + p,
+// lo KF halves on).  g / bt: [NT][11][64][4] packed.
 template <int NTL>
 __device__ __forceinline__ void ln_write(const floatx4 (&acc)[NTL], int mt0, int ms, int ntile,
                                          bool nvalid, float mean, float rstd,
                                          const float* __restrict__ g, const float* __restrict__ bt,
-                                         uint16_t* act_hi, uint16_t* act_lo, float* flat) {
+                                         uint16_t* act_hi, uint16_t* act_lo, uint16_t* fl) {
   const int lane = threadIdx.x & 63, i16 = lane & 15, kq = lane >> 4;
   const int n = 16 * ntile + i16;
+  // the table addresses are loop-invariant in the caller's item loop: an
+  // opaque lane offset keeps the compiler from hoisting (and spilling) them
+  int tl = lane * 4;
+  asm volatile("" : "+v"(tl));
 #pragma unroll
   for (int t = 0; t < NTL; ++t)
     if (mt0 + t * ms < MT && nvalid) {
       const int mt = mt0 + t * ms;
-      const size_t gi = ((size_t)(ntile * MT + mt) * 64 + lane) * 4;
+      const int gi = (ntile * MT + mt) * 256 + tl;
       const float4 gg = *reinterpret_cast<const float4*>(g + gi);
       const float4 bb = *reinterpret_cast<const float4*>(bt + gi);
       const float gv[4] = {gg.x, gg.y, gg.z, gg.w}, bv[4] = {bb.x, bb.y, bb.z, bb.w};
@@ -204,13 +237,15 @@ __device__ __forceinline__ void ln_write(const floatx4 (&acc)[NTL], int mt0, int
         const int p = 16 * mt + 4 * kq + q;
         if (p < NP) {
           const float y = fmaxf((acc[t][q] - mean) * rstd * gv[q] + bv[q], 0.0f);
-          if (flat) {
-            flat[n * NP + p] = y;
+          uint16_t hi, lo;
+          split16(y, hi, lo);
+          if (fl) {
+            fl[n * NP + p] = hi;
+            fl[KF + n * NP + p] = lo;
           } else {
             const int i = ((p / HW + 1) * 15 + (p % HW) + 1) * CS + n;
-            const __half h = __float2half_rn(y);
-            act_hi[i] = __half_as_ushort(h);
-            act_lo[i] = __half_as_ushort(__float2half_rn(y - __half2float(h)));
+            act_hi[i] = hi;
+            act_lo[i] = lo;
           }
         }
       }
@@ -223,7 +258,7 @@ template <int STEPS, int NTW>
 __device__ __forceinline__ void head_gemm(const float* A, int as, const float* __restrict__ w,
                                           int nt0, floatx4 (&c)[NTW]) {
   const int lane = threadIdx.x & 63, i16 = lane & 15, kq = lane >> 4;
-  const float* a = A + min(i16, SB - 1) * as + kq;   // rows past the batch repeat its last
+  const float* a = A + i16 * as + kq;
   const float* b = w + (size_t)nt0 * STEPS * 64 + lane;
 #pragma unroll
   for (int i = 0; i < NTW; ++i) c[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -277,27 +312,17 @@ __device__ __forceinline__ void head_ln(float* h, int nb, const float* __restric
   }
 }
 
-__global__ __launch_bounds__(T, 1) void cnn_act_kernel(const qqt_cnn_args a, int items, int per) {
+__global__ __launch_bounds__(T, 2) void cnn_trunk_kernel(const qqt_cnn_args a, int items,
+                                                          int per) {
   __shared__ Lds s;
   const int t = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int lane = t & 63, i16 = lane & 15;
 
-  // B operands of the 16->32 and 32->64 convs, resident for the whole kernel
-  half8 b1h[S1], b1l[S1], b2h[S2], b2l[S2];
+  // B operands: the 16->32 and 32->64 convs' from global memory one step at
+  // a time (L2 hits: 20 and 72 KB shared by every workgroup), conv0's and
+  // the 1x1 conv's from LDS
   const int n1 = w & 1, n2 = w;
-#pragma unroll
-  for (int j = 0; j < S1; ++j) {
-    const size_t o = ((size_t)(n1 * S1 + j) * 64 + lane) * 8;
-    b1h[j] = ld8(a.c1w + o);
-    b1l[j] = ld8(a.c1w_lo + o);
-  }
-#pragma unroll
-  for (int j = 0; j < S2; ++j) {
-    const size_t o = ((size_t)(n2 * S2 + j) * 64 + lane) * 8;
-    b2h[j] = ld8(a.c2w + o);
-    b2l[j] = ld8(a.c2w_lo + o);
-  }
   const float bias0 = a.c0b[i16], bias1 = a.c1b[16 * n1 + i16], bias2 = a.c2b[16 * n2 + i16];
   const float bias3 = a.c3b[i16];
 
@@ -314,8 +339,12 @@ __global__ __launch_bounds__(T, 1) void cnn_act_kernel(const qqt_cnn_args a, int
     s.wc3[0][i] = a.c3w[i];
     s.wc3[1][i] = a.c3w_lo[i];
   }
-  auto breg1 = [&](int j) { return BFrag{b1h[j], b1l[j]}; };
-  auto breg2 = [&](int j) { return BFrag{b2h[j], b2l[j]}; };
+  const uint16_t* const c1h = a.c1w + ((size_t)n1 * S1 * 64 + lane) * 8;
+  const uint16_t* const c1l = a.c1w_lo + ((size_t)n1 * S1 * 64 + lane) * 8;
+  auto breg1 = [&](int j) { return BFrag{ld8(c1h + j * BFRAG), ld8(c1l + j * BFRAG)}; };
+  const uint16_t* const c2h = a.c2w + ((size_t)n2 * S2 * 64 + lane) * 8;
+  const uint16_t* const c2l = a.c2w_lo + ((size_t)n2 * S2 * 64 + lane) * 8;
+  auto breg2 = [&](int j) { return BFrag{ld8(c2h + j * BFRAG), ld8(c2l + j * BFRAG)}; };
   auto blds0 = [&](int j) {
     return BFrag{ld8(s.wc0[0] + (j * 64 + lane) * 8), ld8(s.wc0[1] + (j * 64 + lane) * 8)};
   };
@@ -325,146 +354,161 @@ __global__ __launch_bounds__(T, 1) void cnn_act_kernel(const qqt_cnn_args a, int
 
   int rslot = 0;                                   // reduction slot
   const int start = blockIdx.x * per, end = min(items, start + per);
-  for (int ib = start; ib < end; ib += SB) {
-    const int nb = min(SB, end - ib);
-    for (int ii = 0; ii < nb; ++ii) {
-      const int item = ib + ii;
-      const int row = item / a.npid, slot = item % a.npid;
-      const int pid = a.npid == 2 ? slot : a.pid0;
-      __syncthreads();                                  // channels 0..13 free
-      const uint16_t* ob = a.obs + (size_t)row * a.obs_stride;
-      const int32_t* perm = a.view_perm + pid * C0;
-      for (int i = t; i < C0 * NP; i += T) {          // exact in float16: hi plane only
-        const int c = i / NP, p = i - c * NP;
-        s.act[0][((p / HW + 1) * 15 + (p % HW) + 1) * CS + c] = ob[perm[c] * NP + p];
-      }
-      __syncthreads();
-
-      float mean, rstd;
-      {
-        floatx4 acc[3];
-        conv<0, S0, 3, false>(s.act[0], s.act[1], blds0, bias0, w, 4, acc);
-        ln_stats<3>(acc, w, 4, true, s.red, rslot, 1.0f / (16 * NP), mean, rstd);
-        ln_write<3>(acc, w, 4, 0, true, mean, rstd, a.ln0w, a.ln0b, s.act[0], s.act[1], nullptr);
-      }
-      __syncthreads();
-      {
-        floatx4 acc[6];
-        conv<0, S1, 6, true>(s.act[0], s.act[1], breg1, bias1, mt1, 2, acc);
-        ln_stats<6>(acc, mt1, 2, true, s.red, rslot, 1.0f / (32 * NP), mean, rstd);
-        ln_write<6>(acc, mt1, 2, n1, true, mean, rstd, a.ln1w, a.ln1b, s.act[0], s.act[1],
-                    nullptr);
-      }
-      __syncthreads();
-      {
-        floatx4 acc[MT];
-        conv<1, S2, MT, true>(s.act[0], s.act[1], breg2, bias2, 0, 1, acc);
-        ln_stats<MT>(acc, 0, 1, true, s.red, rslot, 1.0f / (64 * NP), mean, rstd);
-        ln_write<MT>(acc, 0, 1, n2, true, mean, rstd, a.ln2w, a.ln2b, s.act[0], s.act[1],
-                     nullptr);
-      }
-      __syncthreads();
-      {
-        floatx4 acc[3];
-        conv<2, S3, 3, true>(s.act[0], s.act[1], blds3, bias3, w, 4, acc);
-        const bool nv = i16 < 8;
-        ln_stats<3>(acc, w, 4, nv, s.red, rslot, 1.0f / (8 * NP), mean, rstd);
-        ln_write<3>(acc, w, 4, 0, nv, mean, rstd, a.ln3w, a.ln3b, s.act[0], s.act[1],
-                    s.flat + ii * FS);
-      }
+  for (int item = start; item < end; ++item) {
+    const int row = item / a.npid, slot = item % a.npid;
+    const int pid = a.npid == 2 ? slot : a.pid0;
+    __syncthreads();                                  // channels 0..13 free
+    const uint16_t* ob = a.obs + (size_t)row * a.obs_stride;
+    const int32_t* perm = a.view_perm + pid * C0;
+    for (int i = t; i < C0 * NP; i += T) {          // exact in float16: hi plane only
+      const int c = i / NP, p = i - c * NP;
+      s.act[0][((p / HW + 1) * 15 + (p % HW) + 1) * CS + c] = ob[perm[c] * NP + p];
     }
     __syncthreads();
 
-    // ---------------- head over the batch's nb items (rows m of the GEMMs;
-    // rows >= nb carry stale values that only reach their own rows)
-    float* const h = s.flat + H_OFF;
-    float* const h2 = s.flat + H2_OFF;
-    float* const hy = s.flat + HY_OFF;
-    float* const lg = s.flat + LG_OFF;
+    float mean, rstd;
     {
-      floatx4 c[2];
-      head_gemm<L0, 2>(s.flat, FS, a.s0p, 2 * w, c);
-      __syncthreads();                                  // flat fully read
-      head_store(c[0], h, HS, 2 * w, a.s0b, false);
-      head_store(c[1], h, HS, 2 * w + 1, a.s0b, false);
+      floatx4 acc[3];
+      conv<0, S0, 3, false>(s.act[0], s.act[1], blds0, bias0, w, 4, acc);
+      ln_stats<3>(acc, w, 4, true, s.red, rslot, 1.0f / (16 * NP), mean, rstd);
+      ln_write<3>(acc, w, 4, 0, true, mean, rstd, a.ln0w, a.ln0b, s.act[0], s.act[1], nullptr);
     }
     __syncthreads();
-    head_ln(h, nb, a.s1w, a.s1b);
-    __syncthreads();
     {
-      floatx4 c[2];
-      head_gemm<L1, 2>(h, HS, a.s3p, 2 * w, c);
-      head_store(c[0], h2, HS, 2 * w, a.s3b, false);
-      head_store(c[1], h2, HS, 2 * w + 1, a.s3b, false);
+      floatx4 acc[6];
+      conv<0, S1, 6, true>(s.act[0], s.act[1], breg1, bias1, mt1, 2, acc);
+      ln_stats<6>(acc, mt1, 2, true, s.red, rslot, 1.0f / (32 * NP), mean, rstd);
+      ln_write<6>(acc, mt1, 2, n1, true, mean, rstd, a.ln1w, a.ln1b, s.act[0], s.act[1],
+                  nullptr);
     }
     __syncthreads();
-    head_ln(h2, nb, a.s4w, a.s4b);
+    {
+      floatx4 acc[MT];
+      conv<1, S2, MT, true>(s.act[0], s.act[1], breg2, bias2, 0, 1, acc);
+      ln_stats<MT>(acc, 0, 1, true, s.red, rslot, 1.0f / (64 * NP), mean, rstd);
+      ln_write<MT>(acc, 0, 1, n2, true, mean, rstd, a.ln2w, a.ln2b, s.act[0], s.act[1],
+                   nullptr);
+    }
     __syncthreads();
     {
-      floatx4 c[3];
-      head_gemm<L1, 3>(h2, HS, a.hp, 3 * w, c);
+      floatx4 acc[3];
+      conv<2, S3, 3, true>(s.act[0], s.act[1], blds3, bias3, w, 4, acc);
+      const bool nv = i16 < 8;
+      uint16_t* const fl = a.workspace + (size_t)item * WS_ROW;
+      ln_stats<3>(acc, w, 4, nv, s.red, rslot, 1.0f / (8 * NP), mean, rstd);
+      ln_write<3>(acc, w, 4, 0, nv, mean, rstd, a.ln3w, a.ln3b, s.act[0], s.act[1], fl);
+      if (t < KF - FLAT) fl[FLAT + t] = fl[KF + FLAT + t] = 0;
+    }
+  }
+}
+
+// Head over items ib .. ib + 15 (rows m of the GEMMs; rows past the batch
+// repeat its last item and are not written out).
+__global__ __launch_bounds__(T) void cnn_head_kernel(const qqt_cnn_args a, int items) {
+  __shared__ HeadLds s;
+  const int t = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int lane = t & 63, i16 = lane & 15, kq = lane >> 4;
+  const int ib = blockIdx.x * HB, nb = min(HB, items - ib);
+
+  // Linear(1352,128): wavefront w computes output tiles 2w, 2w + 1
+  {
+    const uint16_t* const ar = a.workspace + (size_t)min(ib + i16, items - 1) * WS_ROW + 8 * kq;
+    const size_t tile = (size_t)S0H * BFRAG;
+    const uint16_t* const bh = a.s0h + 2 * w * tile + lane * 8;
+    const uint16_t* const bl = a.s0l + 2 * w * tile + lane * 8;
+    floatx4 c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0;
+#pragma unroll 4
+    for (int st = 0; st < S0H; ++st) {
+      const half8 ah = ld8(ar + 32 * st), al = ld8(ar + KF + 32 * st);
+      const half8 h0 = ld8(bh + st * BFRAG), l0 = ld8(bl + st * BFRAG);
+      const half8 h1 = ld8(bh + tile + st * BFRAG), l1 = ld8(bl + tile + st * BFRAG);
+      c0 = mfma16(ah, h0, c0);
+      c1 = mfma16(ah, h1, c1);
+      c0 = mfma16(ah, l0, c0);
+      c1 = mfma16(ah, l1, c1);
+      c0 = mfma16(al, h0, c0);
+      c1 = mfma16(al, h1, c1);
+    }
+    head_store(c0, s.h, HS, 2 * w, a.s0b, false);
+    head_store(c1, s.h, HS, 2 * w + 1, a.s0b, false);
+  }
+  __syncthreads();
+  head_ln(s.h, nb, a.s1w, a.s1b);
+  __syncthreads();
+  {
+    floatx4 c[2];
+    head_gemm<L1, 2>(s.h, HS, a.s3p, 2 * w, c);
+    head_store(c[0], s.h2, HS, 2 * w, a.s3b, false);
+    head_store(c[1], s.h2, HS, 2 * w + 1, a.s3b, false);
+  }
+  __syncthreads();
+  head_ln(s.h2, nb, a.s4w, a.s4b);
+  __syncthreads();
+  {
+    floatx4 c[3];
+    head_gemm<L1, 3>(s.h2, HS, a.hp, 3 * w, c);
 #pragma unroll
-      for (int i = 0; i < 3; ++i) head_store(c[i], hy, HYS, 3 * w + i, a.hb, true);
-    }
-    __syncthreads();
-    if (t < SB * 8) {                                   // output layer: item m, output o
-      const int m = t >> 3, o = t & 7;
-      const int base = o < 5 ? 0 : o < 7 ? 64 : 128;
-      const float* x = hy + m * HYS + base;
-      const float* wf = a.fw + o * 64;
-      float acc = 0.0f;
+    for (int i = 0; i < 3; ++i) head_store(c[i], s.hy, HYS, 3 * w + i, a.hb, true);
+  }
+  __syncthreads();
+  if (t < HB * 8) {                                   // output layer: item m, output o
+    const int m = t >> 3, o = t & 7;
+    const int base = o < 5 ? 0 : o < 7 ? 64 : 128;
+    const float* x = s.hy + m * HYS + base;
+    const float* wf = a.fw + o * 64;
+    float acc = 0.0f;
 #pragma unroll 8
-      for (int k = 0; k < 64; ++k) acc += x[k] * wf[k];
-      lg[m * 8 + o] = acc + a.fb[o];
+    for (int k = 0; k < 64; ++k) acc += x[k] * wf[k];
+    s.lg[m * 8 + o] = acc + a.fb[o];
+  }
+  __syncthreads();
+  if (t < nb) {
+    const int item = ib + t;
+    const int row = item / a.npid, slot = item % a.npid;
+    const int pid = a.npid == 2 ? slot : a.pid0;
+    float l8[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) l8[k] = s.lg[t * 8 + k];
+    const int oslots = a.out_slots > 0 ? a.out_slots : a.npid;
+    const int oslot = a.npid == 2 ? slot : a.out_slot;
+    const size_t o = (size_t)row * oslots + oslot;
+    if (a.logits_out) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) a.logits_out[o * 8 + k] = l8[k];
     }
-    __syncthreads();
-    if (t < nb) {
-      const int item = ib + t;
-      const int row = item / a.npid, slot = item % a.npid;
-      const int pid = a.npid == 2 ? slot : a.pid0;
-      float l8[8];
+    if (a.value_out) a.value_out[o] = l8[7];
+    if (a.sample) {
+      uint8_t mm[5], bm[2];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) l8[k] = lg[t * 8 + k];
-      const int oslots = a.out_slots > 0 ? a.out_slots : a.npid;
-      const int oslot = a.npid == 2 ? slot : a.out_slot;
-      const size_t o = (size_t)row * oslots + oslot;
-      if (a.logits_out) {
+      for (int k = 0; k < 5; ++k)
+        mm[k] = a.move_mask[(size_t)row * a.mm_row_stride + (size_t)pid * a.mm_pid_stride + k];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) a.logits_out[o * 8 + k] = l8[k];
+      for (int k = 0; k < 2; ++k)
+        bm[k] = a.bomb_mask[(size_t)row * a.bm_row_stride + (size_t)pid * a.bm_pid_stride + k];
+      float um, ub;
+      if (a.uniforms) {
+        um = a.uniforms[o * 2 + 0];
+        ub = a.uniforms[o * 2 + 1];
+      } else {
+        float u4[4];
+        philox_block(a.seed, (uint32_t)row, a.tick, STREAM_POLICY, (uint32_t)((2 * pid) >> 2),
+                     u4);
+        um = u4[(2 * pid) & 3];
+        ub = u4[(2 * pid + 1) & 3];
       }
-      if (a.value_out) a.value_out[o] = l8[7];
-      if (a.sample) {
-        uint8_t mm[5], bm[2];
-#pragma unroll
-        for (int k = 0; k < 5; ++k)
-          mm[k] = a.move_mask[(size_t)row * a.mm_row_stride + (size_t)pid * a.mm_pid_stride + k];
-#pragma unroll
-        for (int k = 0; k < 2; ++k)
-          bm[k] = a.bomb_mask[(size_t)row * a.bm_row_stride + (size_t)pid * a.bm_pid_stride + k];
-        float um, ub;
-        if (a.uniforms) {
-          um = a.uniforms[o * 2 + 0];
-          ub = a.uniforms[o * 2 + 1];
-        } else {
-          float u4[4];
-          philox_block(a.seed, (uint32_t)row, a.tick, STREAM_POLICY, (uint32_t)((2 * pid) >> 2),
-                       u4);
-          um = u4[(2 * pid) & 3];
-          ub = u4[(2 * pid + 1) & 3];
-        }
-        float lpm, lpb;
-        const int am = sample_masked<5>(l8, mm, um, &lpm);
-        const int ab = sample_masked<2>(l8 + 5, bm, ub, &lpb);
-        if (a.actions) {
-          a.actions[o * 2 + 0] = am;
-          a.actions[o * 2 + 1] = ab;
-        }
-        if (a.actions_i8) {
-          a.actions_i8[o * 2 + 0] = (int8_t)am;
-          a.actions_i8[o * 2 + 1] = (int8_t)ab;
-        }
-        if (a.logp_out) a.logp_out[o] = lpm + lpb;
+      float lpm, lpb;
+      const int am = sample_masked<5>(l8, mm, um, &lpm);
+      const int ab = sample_masked<2>(l8 + 5, bm, ub, &lpb);
+      if (a.actions) {
+        a.actions[o * 2 + 0] = am;
+        a.actions[o * 2 + 1] = ab;
       }
+      if (a.actions_i8) {
+        a.actions_i8[o * 2 + 0] = (int8_t)am;
+        a.actions_i8[o * 2 + 1] = (int8_t)ab;
+      }
+      if (a.logp_out) a.logp_out[o] = lpm + lpb;
     }
   }
 }
@@ -495,7 +539,7 @@ int qqt_cnn_act(const qqt_cnn_args* a, void* stream) {
   if (!a || !a->obs || !a->view_perm || !a->c0w || !a->c0w_lo || !a->c0b || !a->ln0w ||
       !a->ln0b || !a->c1w || !a->c1w_lo || !a->c1b || !a->ln1w || !a->ln1b || !a->c2w ||
       !a->c2w_lo || !a->c2b || !a->ln2w || !a->ln2b || !a->c3w || !a->c3w_lo || !a->c3b ||
-      !a->ln3w || !a->ln3b || !a->s0p || !a->s0b ||
+      !a->ln3w || !a->ln3b || !a->s0h || !a->s0l || !a->s0b ||
       !a->s1w || !a->s1b || !a->s3p || !a->s3b || !a->s4w || !a->s4b || !a->hp || !a->hb ||
       !a->fw || !a->fb) {
     snprintf(g_err, sizeof(g_err), "qqt_cnn_act: null pointer argument");
@@ -503,9 +547,10 @@ int qqt_cnn_act(const qqt_cnn_args* a, void* stream) {
   }
   if (((uintptr_t)a->ln0w | (uintptr_t)a->ln0b | (uintptr_t)a->ln1w | (uintptr_t)a->ln1b |
        (uintptr_t)a->ln2w | (uintptr_t)a->ln2b | (uintptr_t)a->ln3w | (uintptr_t)a->ln3b |
-       (uintptr_t)a->c1w | (uintptr_t)a->c1w_lo | (uintptr_t)a->c2w | (uintptr_t)a->c2w_lo) & 15) {
+       (uintptr_t)a->c1w | (uintptr_t)a->c1w_lo | (uintptr_t)a->c2w | (uintptr_t)a->c2w_lo |
+       (uintptr_t)a->s0h | (uintptr_t)a->s0l) & 15) {
     snprintf(g_err, sizeof(g_err),
-             "qqt_cnn_act: LayerNorm tables and conv weights must be 16-byte aligned");
+             "qqt_cnn_act: LayerNorm tables, conv and first head weights must be 16-byte aligned");
     return QQT_E_ARG;
   }
   if (a->batch <= 0 || (a->npid != 1 && a->npid != 2) || a->w_players < a->npid ||
@@ -525,11 +570,23 @@ int qqt_cnn_act(const qqt_cnn_args* a, void* stream) {
     return QQT_E_ARG;
   }
   const int items = a->batch * a->npid;
-  const int grid = min(cu_count(), (items + SB - 1) / SB);
+  if (!a->workspace || ((uintptr_t)a->workspace & 15) ||
+      a->workspace_bytes < (int64_t)items * QQT_CNN_WS_BYTES_PER_ITEM) {
+    snprintf(g_err, sizeof(g_err),
+             "qqt_cnn_act: workspace must be 16-byte aligned and hold %d bytes per item",
+             QQT_CNN_WS_BYTES_PER_ITEM);
+    return QQT_E_ARG;
+  }
+  const int grid = min(2 * cu_count(), items);
   const int per = (items + grid - 1) / grid;
-  QQT_LAUNCH(QQT_KERNEL_CNN, cnn_act_kernel, dim3(grid), dim3(T), (hipStream_t)stream, *a,
-             items, per);
-  const hipError_t err = hipGetLastError();
+  hipStream_t st = (hipStream_t)stream;
+  QQT_LAUNCH(QQT_KERNEL_CNN, cnn_trunk_kernel, dim3(grid), dim3(T), st, *a, items, per);
+  hipError_t err = hipGetLastError();
+  if (err == hipSuccess) {
+    QQT_LAUNCH(QQT_KERNEL_CNN_HEAD, cnn_head_kernel, dim3((items + HB - 1) / HB), dim3(T), st,
+               *a, items);
+    err = hipGetLastError();
+  }
   if (err != hipSuccess) {
     snprintf(g_err, sizeof(g_err), "cnn launch failed: %s", hipGetErrorString(err));
     return QQT_E_LAUNCH;

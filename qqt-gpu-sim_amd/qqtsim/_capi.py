@@ -14,7 +14,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 
 from ._build import LIB
 
-ABI_VERSION = 21
+ABI_VERSION = 22
 
 MODE_STEP, MODE_OBSERVE, MODE_RESET, MODE_PROBE, MODE_FLUSH = 0, 1, 2, 3, 4
 MAP_PILLARS, MAP_OPEN, MAP_REFERENCE = 0, 1, 2
@@ -111,9 +111,11 @@ class CnnArgsC(ctypes.Structure):
         ("reserved", _i32)] + [
         (n, _vp) for n in ("obs", "view_perm", "c0w", "c0w_lo", "c0b", "ln0w", "ln0b", "c1w",
                            "c1w_lo", "c1b", "ln1w", "ln1b", "c2w", "c2w_lo", "c2b", "ln2w",
-                           "ln2b", "c3w", "c3w_lo", "c3b", "ln3w", "ln3b", "s0p", "s0b", "s1w", "s1b", "s3p", "s3b", "s4w", "s4b", "hp",
-                           "hb", "fw", "fb", "move_mask", "bomb_mask", "uniforms", "actions", "actions_i8",
-                           "logp_out", "value_out", "logits_out")]
+                           "ln2b", "c3w", "c3w_lo", "c3b", "ln3w", "ln3b", "s0h", "s0l", "s0b", "s1w", "s1b",
+                           "s3p", "s3b", "s4w", "s4b", "hp", "hb", "fw", "fb", "move_mask",
+                           "bomb_mask", "uniforms", "actions", "actions_i8", "logp_out",
+                           "value_out", "logits_out", "workspace")] + [
+        ("workspace_bytes", ctypes.c_int64)]
 
 
 class GatherArgsC(ctypes.Structure):
@@ -194,8 +196,8 @@ def lib():
 
 
 KERNEL_KINDS = ("tick_kernel", "mlp_act_kernel", "bot_kernel", "reach_kernel",
-                "gae_kernel", "l1grad_kernels", "ppo_grad_kernel", "cnn_act_kernel",
-                "lstm_feat_kernel", "lstm_act_kernel")  # QQT_KERNEL_*
+                "gae_kernel", "l1grad_kernels", "ppo_grad_kernel", "cnn_trunk_kernel",
+                "lstm_feat_kernel", "lstm_act_kernel", "cnn_head_kernel")  # QQT_KERNEL_*
 
 
 def timing_arm(launches: int) -> None:

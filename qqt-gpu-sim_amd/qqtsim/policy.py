@@ -460,6 +460,22 @@ def _pack_linear(w: torch.Tensor) -> torch.Tensor:
     return x.permute(0, 2, 3, 1).reshape(-1).contiguous()
 
 
+def _frag16_planes(w: torch.Tensor, kpad: int):
+    """[out][in] Linear weight -> float16 hi and lo planes of the k-major
+    [kpad][out] matrix (rows past `in` zero) in the B-fragment order of
+    v_mfma_f32_16x16x32_f16: half i of lane 16 q + r in K step s of column
+    tile t is W[32 s + 8 q + i][16 t + r]."""
+    n, k = w.shape
+    wk = torch.zeros((kpad, n), dtype=torch.float32)
+    wk[:k] = w.float().t()
+    hi, lo = _split16(wk)
+
+    def frag(x):
+        return x.reshape(kpad // 32, 4, 8, n // 16, 16).permute(3, 0, 1, 4, 2).reshape(-1)
+
+    return frag(hi).contiguous(), frag(lo).contiguous()
+
+
 def _pack_ln(g: torch.Tensor, n_tiles: int) -> torch.Tensor:
     """[C][13][13] LayerNorm affine -> [tile][11][lane][4]: value q of lane l
     in position tile mt is channel 16 tile + l % 16, position 16 mt +
@@ -469,6 +485,10 @@ def _pack_ln(g: torch.Tensor, n_tiles: int) -> torch.Tensor:
     gp[:c, :169] = g.float().reshape(c, 169)
     x = gp.view(n_tiles, 16, 11, 4, 4)                        # [tile][i16][mt][kq][q]
     return x.permute(0, 2, 3, 1, 4).reshape(-1).contiguous()
+
+
+CNN_FLAT_PAD = 1376            # flattened trunk features padded to 43 K steps of 32
+CNN_WS_BYTES_PER_ITEM = 5504   # QQT_CNN_WS_BYTES_PER_ITEM
 
 
 def pack_cnn(params: dict, n_players: int = 2, obs_shape=(14, 13, 13)) -> dict:
@@ -505,7 +525,7 @@ def pack_cnn(params: dict, n_players: int = 2, obs_shape=(14, 13, 13)) -> dict:
         ln2w=_pack_ln(f("conv.6.weight"), 4), ln2b=_pack_ln(f("conv.6.bias"), 4),
         c3b=c3b,
         ln3w=_pack_ln(f("conv.9.weight"), 1), ln3b=_pack_ln(f("conv.9.bias"), 1),
-        s0p=_pack_linear(f("shared.0.weight")), s0b=f("shared.0.bias"),
+        s0b=f("shared.0.bias"),
         s1w=f("shared.1.weight"), s1b=f("shared.1.bias"),
         s3p=_pack_linear(f("shared.3.weight")), s3b=f("shared.3.bias"),
         s4w=f("shared.4.weight"), s4b=f("shared.4.bias"),
@@ -515,8 +535,9 @@ def pack_cnn(params: dict, n_players: int = 2, obs_shape=(14, 13, 13)) -> dict:
     for key, src, nt in (("c0w", "conv0.weight", 1), ("c1w", "conv.2.weight", 2),
                          ("c2w", "conv.5.weight", 4), ("c3w", "conv.8.weight", 1)):
         out[key], out[key + "_lo"] = _split16(_conv_operand(f(src), nt))
+    out["s0h"], out["s0l"] = _frag16_planes(f("shared.0.weight"), CNN_FLAT_PAD)
     expect = dict(c0w=5 * 64 * 8, c1w=2 * 5 * 64 * 8, c2w=4 * 9 * 64 * 8, c3w=2 * 64 * 8,
-                  s0p=8 * 338 * 64, s3p=8 * 32 * 64, hp=12 * 32 * 64, ln2w=4 * 11 * 64 * 4)
+                  s0h=8 * 43 * 64 * 8, s3p=8 * 32 * 64, hp=12 * 32 * 64, ln2w=4 * 11 * 64 * 4)
     for k, numel in expect.items():
         if out[k].numel() != numel:
             raise ValueError(f"{k} packs to {out[k].numel()} values, expected {numel}")
@@ -548,6 +569,19 @@ class HipCnnActorCritic(HipActorCritic):
         self.k0 = self.obs_shape[0] * self.obs_shape[1] * self.obs_shape[2]
         return packed
 
+    def _workspace(self, items: int) -> torch.Tensor:
+        """The trunk's feature rows for launches of `items` (row, player)
+        items: one buffer per item count, kept for the policy's lifetime so
+        that argument blocks built earlier (a `Rollout`'s) stay valid.
+        Launches share it in stream order."""
+        ws = getattr(self, "_ws", None)
+        if ws is None:
+            ws = self._ws = {}
+        if items not in ws:
+            ws[items] = torch.empty(items * CNN_WS_BYTES_PER_ITEM, dtype=torch.uint8,
+                                    device=self.device)
+        return ws[items]
+
     def _args(self, b, npid, pid0, sample, obs_ptr, obs_stride):
         a = _capi.CnnArgsC()
         a.batch, a.npid, a.pid0, a.sample = b, npid, pid0, int(sample)
@@ -557,6 +591,8 @@ class HipCnnActorCritic(HipActorCritic):
         a.obs = obs_ptr
         for k, v in self._w.items():
             setattr(a, k, v.data_ptr())
+        ws = self._workspace(b * npid)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
         return a
 
     def _launch(self, a, stream) -> None:

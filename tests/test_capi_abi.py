@@ -211,8 +211,8 @@ def test_mlp_rejects_bad_output_slots(lib, kw, msg):
 
 _CNN_PTRS = ("obs", "view_perm", "c0w", "c0w_lo", "c0b", "ln0w", "ln0b", "c1w", "c1w_lo", "c1b",
              "ln1w", "ln1b", "c2w", "c2w_lo", "c2b", "ln2w", "ln2b", "c3w", "c3w_lo", "c3b",
-             "ln3w", "ln3b", "s0p", "s0b", "s1w", "s1b", "s3p", "s3b", "s4w", "s4b", "hp", "hb",
-             "fw", "fb")
+             "ln3w", "ln3b", "s0h", "s0l", "s0b", "s1w", "s1b", "s3p", "s3b", "s4w", "s4b", "hp",
+             "hb", "fw", "fb", "workspace")
 
 
 def _cnn_args(**kw):
@@ -222,6 +222,7 @@ def _cnn_args(**kw):
     a.batch, a.npid, a.obs_stride, a.w_players = 4, 2, 14 * 169, 2
     for i, name in enumerate(_CNN_PTRS):
         setattr(a, name, 0x10000 * (i + 1))
+    a.workspace_bytes = 4 * 2 * 5504
     for k, v in kw.items():
         setattr(a, k, v)
     return a
@@ -242,6 +243,11 @@ def _cnn_args(**kw):
     (dict(out_slots=1), "output slots"),
     (dict(npid=1, out_slots=2, out_slot=2), "output slots"),
     (dict(sample=1), "sampling needs masks"),
+    (dict(s0l=None), "null pointer"),
+    (dict(s0h=0x10002), "16-byte aligned"),
+    (dict(workspace=None), "workspace"),
+    (dict(workspace=0x10008), "workspace"),
+    (dict(workspace_bytes=4 * 2 * 5504 - 1), "workspace"),
 ])
 def test_cnn_rejects_bad_arguments(lib, kw, msg):
     assert lib.qqt_cnn_act(_cnn_args(**kw), None) == -1

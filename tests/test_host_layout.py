@@ -293,11 +293,18 @@ def test_pack_cnn_operands_reproduce_the_reference_layers():
         want = F.conv2d(x[None], wd, params[bk].double(), padding=wd.shape[-1] // 2)[0]
         got = kernel_conv(x, key, nt, steps, kind, wd.shape[0]) + params[bk].double()[:, None, None]
         torch.testing.assert_close(got, want, rtol=1e-12, atol=1e-12)
-    for key, pkey, n, k in (("shared.0.weight", "s0p", 128, 1352),
-                            ("shared.3.weight", "s3p", 128, 128)):
-        p = pk[pkey].view(n // 16, k // 4, 4, 16)                 # [tile][j][kq][i16]
-        dense = p.permute(0, 3, 1, 2).reshape(n, k)
-        assert torch.equal(dense, params[key])
+    p = pk["s3p"].view(8, 32, 4, 16)                             # [tile][j][kq][i16]
+    assert torch.equal(p.permute(0, 3, 1, 2).reshape(128, 128), params["shared.3.weight"])
+    # Linear(1352,128) as float16 hi / lo B fragments [tile][step][q * 16 + r][i]:
+    # W^T[32 step + 8 q + i][16 tile + r], inputs 1352..1375 zero
+    w0 = params["shared.0.weight"]
+    planes = [pk[k].float().view(8, 43, 4, 16, 8) for k in ("s0h", "s0l")]
+    kn = [x.permute(1, 2, 4, 0, 3).reshape(1376, 128) for x in planes]
+    assert torch.count_nonzero(kn[0][1352:]) == 0 and torch.count_nonzero(kn[1][1352:]) == 0
+    assert float(planes[0][3, 7, 2, 5, 1]) == float(w0[16 * 3 + 5, 32 * 7 + 8 * 2 + 1].half())
+    wt = w0.t().double()
+    err = (kn[0][:1352].double() + kn[1][:1352].double() - wt).abs()
+    assert bool((err <= 2.0 ** -22 * wt.abs() + 2.0 ** -24).all())
     ln = pk["ln2w"].view(4, 11, 4, 16, 4)                        # [tile][mt][kq][i16][q]
     gam = params["conv.6.weight"].reshape(64, 169)
     assert float(ln[1, 3, 2, 5, 1]) == float(gam[16 + 5, 16 * 3 + 4 * 2 + 1])
