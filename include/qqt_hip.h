@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 22
+#define QQT_ABI_VERSION 23
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -446,10 +446,10 @@ int qqt_gather_rows(const qqt_gather_args* args, void* stream);
  * inputs 32 step + 8 (l / 16) .. + 7 of the flattened [8][13][13] (inputs
  * 1352..1375 zero).  The other Linear weights are float32
  * [tile][step][lane], lane l holding output 16 tile + l % 16, input
- * 4 step + l / 16.  LayerNorm tables are packed [tile][11 position
- * tiles][lane][4] (value q of lane l: channel 16 tile + l % 16, position
- * 16 ptile + 4 (l / 16) + q; zero past 169 positions or the channel count),
- * 16-byte aligned.  Two launches on `stream`: the trunk writes each item's
+ * 4 step + l / 16.  LayerNorm tables are packed [tile][13 rows][lane][4]
+ * (value q of lane l in row y: channel 16 tile + l % 16 at position (y, x =
+ * 4 (l / 16) + q); zero for x >= 13 or past the channel count), 16-byte
+ * aligned.  Two launches on `stream`: the trunk writes each item's
  * flattened features as float16 hi / lo rows into the workspace, the head
  * reads them; calls that overlap on one workspace race. */
 #define QQT_CNN_WS_BYTES_PER_ITEM 5504   /* workspace bytes per (row, player) item */
@@ -472,13 +472,13 @@ typedef struct qqt_cnn_args {
                                  observation channel view_perm[p][j] (the reference's
                                  conv0.weight[:, argsort(view_perm)] on the stored obs) */
   const uint16_t *c0w, *c0w_lo;           /* conv0 [1][5][64][8] */
-  const float *c0b, *ln0w, *ln0b;         /* [16]; LN [1][11][64][4] */
+  const float *c0b, *ln0w, *ln0b;         /* [16]; LN [1][13][64][4] */
   const uint16_t *c1w, *c1w_lo;           /* conv 16->32 [2][5][64][8] */
-  const float *c1b, *ln1w, *ln1b;         /* [32]; LN [2][11][64][4] */
+  const float *c1b, *ln1w, *ln1b;         /* [32]; LN [2][13][64][4] */
   const uint16_t *c2w, *c2w_lo;           /* conv 32->64 [4][9][64][8] */
-  const float *c2b, *ln2w, *ln2b;         /* [64]; LN [4][11][64][4] */
+  const float *c2b, *ln2w, *ln2b;         /* [64]; LN [4][13][64][4] */
   const uint16_t *c3w, *c3w_lo;           /* 1x1 64->8 [1][2][64][8] (outputs 8..15 zero) */
-  const float *c3b, *ln3w, *ln3b;         /* [16] (8..15 zero); LN [1][11][64][4] */
+  const float *c3b, *ln3w, *ln3b;         /* [16] (8..15 zero); LN [1][13][64][4] */
   const uint16_t *s0h, *s0l;  /* Linear(1352,128) float16 hi / lo [8][43][64][8] (input
                                  index c * 169 + p of the flattened [8][13][13]) */
   const float* s0b;           /* [128] */

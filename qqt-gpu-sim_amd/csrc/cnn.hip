@@ -65,8 +65,9 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 
 constexpr int T = 256, NW = 4;
-constexpr int HW = 13, NP = 169, MT = 11;
-constexpr int PP = 225;                     // padded positions (15 x 15)
+constexpr int HW = 13, NP = 169, MT = 13;    // position tiles = the 13 output rows
+constexpr int PW = 16;                      // padded row: x = -1 .. 14 (lane x of a row tile)
+constexpr int PP = 15 * PW + 2;             // padded positions (row tile 12's lane 15 reads 2 past)
 constexpr int CS = 72;                      // halves per position (64 channels + 8: bank spread)
 constexpr int C0 = 14;
 constexpr int HB = 16;                      // items per head workgroup (the 16 MFMA rows)
@@ -82,8 +83,8 @@ static_assert(WS_ROW * 2 == QQT_CNN_WS_BYTES_PER_ITEM, "workspace row size");
 
 struct __align__(16) Lds {                 // every member a multiple of 16 bytes long
   uint16_t act[2][PP * CS];                 // hi, lo planes [position][channel]
-  uint16_t wc0[2][S0 * BFRAG], wc3[2][S3 * BFRAG];   // conv0 / 1x1 B (hi, lo), all waves
   float red[2][NW];
+  int perm[2][16];                          // view permutations of the two item kinds
 };
 static_assert(sizeof(uint16_t) * 2 * PP * CS % 16 == 0, "16-byte fragment reads stay aligned");
 static_assert(2 * sizeof(Lds) <= 160 * 1024, "two trunk workgroups fit in one CU's LDS");
@@ -121,6 +122,20 @@ __device__ __forceinline__ floatx4 mfma16(half8 a, half8 b, floatx4 c) {
 }
 struct BFrag { half8 hi, lo; };
 
+// Lane (thread) index the compiler cannot see through: values derived from
+// it inside the persistent item loop are recomputed per item instead of
+// hoisted out of the loop and held (or spilled) for the whole kernel.
+__device__ __forceinline__ int opaque_lane() {
+  int l = threadIdx.x & 63;
+  asm volatile("" : "+v"(l));
+  return l;
+}
+__device__ __forceinline__ int opaque_tid() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 // float32 -> float16 hi + lo (x = hi + lo to ~2^-22 relative), saturating
 // at float16's range so that both halves stay finite.
 __device__ __forceinline__ void split16(float x, uint16_t& hi, uint16_t& lo) {
@@ -129,33 +144,36 @@ __device__ __forceinline__ void split16(float x, uint16_t& hi, uint16_t& lo) {
   lo = __half_as_ushort(__float2half_rn(fminf(fmaxf(x - __half2float(h), -65504.0f), 65504.0f)));
 }
 
-__device__ __forceinline__ constexpr int tap_off(int tap) { return (tap / 3) * 15 + tap % 3; }
+__device__ __forceinline__ constexpr int tap_off(int tap) { return (tap / 3) * PW + tap % 3; }
 
 // One conv layer for this wavefront (KIND 0: 3x3 over 16 channels, 1: 3x3
-// over 32, 2: 1x1 over 64): position tiles min(mt0 + t ms, 10), t < NTL
-// (duplicates of tile 10 are computed and later ignored); acc[t] = bias +
+// over 32, 2: 1x1 over 64): row tiles min(mt0 + t ms, 12), t < NTL
+// (duplicates of row 12 are computed and later ignored), lane x of a tile
+// at output position (row, x), x >= 13 computed from the padding and
+// ignored; the 16 lanes of a tile read consecutive padded positions, so the
+// 16-byte reads are free of bank conflicts; acc[t] = bias +
 // sum over steps of A B, three float16 products per step (two without the
 // activations' lo plane).  bfrag(s) returns step s's B fragments; the step
-// loop stays rolled, with the next step's B fragments loaded one step
-// ahead, and each product kind runs over all tiles before the next, so no
-// two consecutive MFMAs share an accumulator.
+// loop stays rolled, with B fragments loaded two steps ahead, and each
+// product kind runs over all tiles before the next, so no two consecutive
+// MFMAs share an accumulator.
 template <int KIND, int STEPS, int NTL, bool ALO, class BF>
 __device__ __forceinline__ void conv(const uint16_t* act_hi, const uint16_t* act_lo, BF bfrag,
                                      float bias, int mt0, int ms, floatx4 (&acc)[NTL]) {
-  const int lane = threadIdx.x & 63, i16 = lane & 15, kq = lane >> 4;
+  constexpr int CG = NTL > 8 ? (NTL + 1) / 2 : NTL;
+  const int lane = opaque_lane(), i16 = lane & 15, kq = lane >> 4;
   int base[NTL];
 #pragma unroll
   for (int t = 0; t < NTL; ++t) {
-    const int p = min(16 * min(mt0 + t * ms, MT - 1) + i16, NP - 1);
-    const int pb = (p / HW) * 15 + (p % HW);          // padded position of tap (0, 0)
+    const int pb = min(mt0 + t * ms, MT - 1) * PW + i16;   // padded position of tap (0, 0)
     base[t] = KIND == 0 ? pb * CS + 8 * (kq & 1) : KIND == 1 ? pb * CS + 8 * kq
-                        : (pb + 16) * CS + 8 * kq;
+                        : (pb + PW + 1) * CS + 8 * kq;
     acc[t] = floatx4{bias, bias, bias, bias};
   }
-  BFrag b = bfrag(0);
+  BFrag b = bfrag(0), b1 = bfrag(min(1, STEPS - 1));
 #pragma unroll 1
   for (int st = 0; st < STEPS; ++st) {
-    const BFrag bn = bfrag(min(st + 1, STEPS - 1));
+    const BFrag bn = bfrag(min(st + 2, STEPS - 1));
     int off;
     if constexpr (KIND == 0)
       off = tap_off(min(2 * st + (kq >> 1), 8)) * CS;
@@ -163,89 +181,109 @@ __device__ __forceinline__ void conv(const uint16_t* act_hi, const uint16_t* act
       off = tap_off(st) * CS;
     else
       off = 32 * st;
-    half8 ah[NTL], al[NTL];
+    // tiles in groups of at most 8, so that one group's A fragments are live
 #pragma unroll
-    for (int t = 0; t < NTL; ++t) {
-      ah[t] = ld8(act_hi + base[t] + off);
-      if constexpr (ALO) al[t] = ld8(act_lo + base[t] + off);
+    for (int t0 = 0; t0 < NTL; t0 += CG) {
+      half8 ah[CG], al[CG];
+#pragma unroll
+      for (int u = 0; u < CG; ++u)
+        if (t0 + u < NTL) {
+          ah[u] = ld8(act_hi + base[t0 + u] + off);
+          if constexpr (ALO) al[u] = ld8(act_lo + base[t0 + u] + off);
+        }
+#pragma unroll
+      for (int u = 0; u < CG; ++u)
+        if (t0 + u < NTL) acc[t0 + u] = mfma16(ah[u], b.hi, acc[t0 + u]);
+#pragma unroll
+      for (int u = 0; u < CG; ++u)
+        if (t0 + u < NTL) acc[t0 + u] = mfma16(ah[u], b.lo, acc[t0 + u]);
+      if constexpr (ALO) {
+#pragma unroll
+        for (int u = 0; u < CG; ++u)
+          if (t0 + u < NTL) acc[t0 + u] = mfma16(al[u], b.hi, acc[t0 + u]);
+      }
     }
-#pragma unroll
-    for (int t = 0; t < NTL; ++t) acc[t] = mfma16(ah[t], b.hi, acc[t]);
-#pragma unroll
-    for (int t = 0; t < NTL; ++t) acc[t] = mfma16(ah[t], b.lo, acc[t]);
-    if constexpr (ALO) {
-#pragma unroll
-      for (int t = 0; t < NTL; ++t) acc[t] = mfma16(al[t], b.hi, acc[t]);
-    }
-    b = bn;
+    b = b1;
+    b1 = bn;
   }
 }
 
-// LayerNorm statistics over the valid outputs of a layer (n < cout, p < 169).
+// LayerNorm statistics over the valid outputs of a layer (channel valid,
+// row tile < 13, x = 4 (lane / 16) + q < 13).
 template <int NTL>
 __device__ __forceinline__ void ln_stats(const floatx4 (&acc)[NTL], int mt0, int ms,
                                          bool nvalid, float (*red)[NW], int& slot,
                                          float inv_count, float& mean, float& rstd) {
-  const int kq = (threadIdx.x & 63) >> 4;
+  const int kq = opaque_lane() >> 4;
   float s = 0.0f;
 #pragma unroll
   for (int t = 0; t < NTL; ++t)
-    if (mt0 + t * ms < MT && nvalid) {
+    if (mt0 + t * ms < MT) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (16 * (mt0 + t * ms) + 4 * kq + q < NP) s += acc[t][q];
+      for (int q = 0; q < 4; ++q) s += (nvalid && 4 * kq + q < HW) ? acc[t][q] : 0.0f;
     }
   mean = block_sum(s, red, slot) * inv_count;
   float v = 0.0f;
 #pragma unroll
   for (int t = 0; t < NTL; ++t)
-    if (mt0 + t * ms < MT && nvalid) {
+    if (mt0 + t * ms < MT) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (16 * (mt0 + t * ms) + 4 * kq + q < NP) {
-          const float d = acc[t][q] - mean;
-          v += d * d;
-        }
+      for (int q = 0; q < 4; ++q) {
+        const float d = acc[t][q] - mean;
+        v += (nvalid && 4 * kq + q < HW) ? d * d : 0.0f;
+      }
     }
   rstd = 1.0f / sqrtf(block_sum(v, red, slot) * inv_count + 1e-5f);
 }
 
+// LayerNorm affine tables of this wavefront's row tiles (min(mt0 + t ms,
+// 12)), loaded before the statistics so that their latency overlaps the
+// reductions.  g / bt: [NT][13][64][4] packed.
+template <int NTL>
+__device__ __forceinline__ void ln_tables(int mt0, int ms, int ntile,
+                                          const float* __restrict__ g,
+                                          const float* __restrict__ bt, float4 (&gg)[NTL],
+                                          float4 (&bb)[NTL]) {
+  const int tl = opaque_lane() * 4;
+#pragma unroll
+  for (int t = 0; t < NTL; ++t) {
+    const int gi = (ntile * MT + min(mt0 + t * ms, MT - 1)) * 256 + tl;
+    gg[t] = *reinterpret_cast<const float4*>(g + gi);
+    bb[t] = *reinterpret_cast<const float4*>(bt + gi);
+  }
+}
+
 // relu(LN affine) of this wavefront's outputs: into the hi/lo activation
 // planes, or (fl != nullptr) into the workspace row fl (hi at n * 169 + p,
-// lo KF halves on).  g / bt: [NT][11][64][4] packed.
+// lo KF halves on).  A lane's four values are consecutive positions of one
+// row, so one address serves all four.
 template <int NTL>
 __device__ __forceinline__ void ln_write(const floatx4 (&acc)[NTL], int mt0, int ms, int ntile,
                                          bool nvalid, float mean, float rstd,
-                                         const float* __restrict__ g, const float* __restrict__ bt,
+                                         const float4 (&gg)[NTL], const float4 (&bb)[NTL],
                                          uint16_t* act_hi, uint16_t* act_lo, uint16_t* fl) {
-  const int lane = threadIdx.x & 63, i16 = lane & 15, kq = lane >> 4;
+  const int lane = opaque_lane(), i16 = lane & 15, kq = lane >> 4;
   const int n = 16 * ntile + i16;
-  // the table addresses are loop-invariant in the caller's item loop: an
-  // opaque lane offset keeps the compiler from hoisting (and spilling) them
-  int tl = lane * 4;
-  asm volatile("" : "+v"(tl));
 #pragma unroll
   for (int t = 0; t < NTL; ++t)
     if (mt0 + t * ms < MT && nvalid) {
-      const int mt = mt0 + t * ms;
-      const int gi = (ntile * MT + mt) * 256 + tl;
-      const float4 gg = *reinterpret_cast<const float4*>(g + gi);
-      const float4 bb = *reinterpret_cast<const float4*>(bt + gi);
-      const float gv[4] = {gg.x, gg.y, gg.z, gg.w}, bv[4] = {bb.x, bb.y, bb.z, bb.w};
+      const int y = mt0 + t * ms;
+      const float gv[4] = {gg[t].x, gg[t].y, gg[t].z, gg[t].w};
+      const float bv[4] = {bb[t].x, bb[t].y, bb[t].z, bb[t].w};
+      const int i0 = ((y + 1) * PW + 1 + 4 * kq) * CS + n;
+      const int f0 = n * NP + y * HW + 4 * kq;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int p = 16 * mt + 4 * kq + q;
-        if (p < NP) {
-          const float y = fmaxf((acc[t][q] - mean) * rstd * gv[q] + bv[q], 0.0f);
+        if (4 * kq + q < HW) {
+          const float y4 = fmaxf((acc[t][q] - mean) * rstd * gv[q] + bv[q], 0.0f);
           uint16_t hi, lo;
-          split16(y, hi, lo);
+          split16(y4, hi, lo);
           if (fl) {
-            fl[n * NP + p] = hi;
-            fl[KF + n * NP + p] = lo;
+            fl[f0 + q] = hi;
+            fl[KF + f0 + q] = lo;
           } else {
-            const int i = ((p / HW + 1) * 15 + (p % HW) + 1) * CS + n;
-            act_hi[i] = hi;
-            act_lo[i] = lo;
+            act_hi[i0 + q * CS] = hi;
+            act_lo[i0 + q * CS] = lo;
           }
         }
       }
@@ -319,84 +357,108 @@ __global__ __launch_bounds__(T, 2) void cnn_trunk_kernel(const qqt_cnn_args a, i
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int lane = t & 63, i16 = lane & 15;
 
-  // B operands: the 16->32 and 32->64 convs' from global memory one step at
-  // a time (L2 hits: 20 and 72 KB shared by every workgroup), conv0's and
-  // the 1x1 conv's from LDS
+  // B operands of every conv from global memory step by step (L2 hits:
+  // 10, 20, 72 and 4 KB shared by every workgroup)
   const int n1 = w & 1, n2 = w;
   const float bias0 = a.c0b[i16], bias1 = a.c1b[16 * n1 + i16], bias2 = a.c2b[16 * n2 + i16];
   const float bias3 = a.c3b[i16];
 
-  // position tiles per wavefront: conv0 / conv3 {w + 4i}, i < 3; conv1
-  // {w/2 + 2i}, i < 6; conv2 all 11
+  // row tiles per wavefront: conv0 / conv3 {w + 4i}, i < 4; conv1
+  // {w/2 + 2i}, i < 7; conv2 all 13
   const int mt1 = w >> 1;
 
   for (int i = t; i < PP * CS; i += T) s.act[0][i] = s.act[1][i] = 0;
-  for (int i = t; i < S0 * BFRAG; i += T) {
-    s.wc0[0][i] = a.c0w[i];
-    s.wc0[1][i] = a.c0w_lo[i];
-  }
-  for (int i = t; i < S3 * BFRAG; i += T) {
-    s.wc3[0][i] = a.c3w[i];
-    s.wc3[1][i] = a.c3w_lo[i];
-  }
   const uint16_t* const c1h = a.c1w + ((size_t)n1 * S1 * 64 + lane) * 8;
   const uint16_t* const c1l = a.c1w_lo + ((size_t)n1 * S1 * 64 + lane) * 8;
   auto breg1 = [&](int j) { return BFrag{ld8(c1h + j * BFRAG), ld8(c1l + j * BFRAG)}; };
   const uint16_t* const c2h = a.c2w + ((size_t)n2 * S2 * 64 + lane) * 8;
   const uint16_t* const c2l = a.c2w_lo + ((size_t)n2 * S2 * 64 + lane) * 8;
   auto breg2 = [&](int j) { return BFrag{ld8(c2h + j * BFRAG), ld8(c2l + j * BFRAG)}; };
-  auto blds0 = [&](int j) {
-    return BFrag{ld8(s.wc0[0] + (j * 64 + lane) * 8), ld8(s.wc0[1] + (j * 64 + lane) * 8)};
+  auto bglob0 = [&](int j) {
+    return BFrag{ld8(a.c0w + (j * 64 + lane) * 8), ld8(a.c0w_lo + (j * 64 + lane) * 8)};
   };
-  auto blds3 = [&](int j) {
-    return BFrag{ld8(s.wc3[0] + (j * 64 + lane) * 8), ld8(s.wc3[1] + (j * 64 + lane) * 8)};
+  auto bglob3 = [&](int j) {
+    return BFrag{ld8(a.c3w + (j * 64 + lane) * 8), ld8(a.c3w_lo + (j * 64 + lane) * 8)};
+  };
+
+  // Observation staging: thread t moves values i = t + 256 k (k < OBS_K) of
+  // the item's 14 x 169 input planes (plane c = i / 169 is observation
+  // channel view_perm[pid][c]); the next item's values are loaded into
+  // registers while this item computes.  Threads past the 2366 values load
+  // a valid value and write nothing.
+  constexpr int OBS_K = (C0 * NP + T - 1) / T;
+  if (t < 2 * C0) {
+    const int kind = t / C0;
+    const int pid = a.npid == 2 ? kind : a.pid0;
+    s.perm[kind][t % C0] = a.view_perm[pid * C0 + t % C0];
+  }
+  __syncthreads();
+  uint16_t ov[OBS_K];
+  auto fetch = [&](int item) {
+    const int row = item / a.npid, kind = a.npid == 2 ? (item & 1) : 0;
+    const uint16_t* const ob = a.obs + (size_t)row * a.obs_stride;
+    const int tt = opaque_tid();
+#pragma unroll
+    for (int k = 0; k < OBS_K; ++k) {
+      const int i = min(tt + T * k, C0 * NP - 1), c = i / NP;
+      ov[k] = ob[s.perm[kind][c] * NP + (i - c * NP)];
+    }
+  };
+  auto stage = [&]() {
+    const int tt = opaque_tid();
+#pragma unroll
+    for (int k = 0; k < OBS_K; ++k) {
+      const int i = tt + T * k, c = i / NP, p = i - c * NP, y = p / HW;
+      if (i < C0 * NP) s.act[0][((y + 1) * PW + (p - y * HW) + 1) * CS + c] = ov[k];
+    }
   };
 
   int rslot = 0;                                   // reduction slot
   const int start = blockIdx.x * per, end = min(items, start + per);
+  if (start < end) fetch(start);
   for (int item = start; item < end; ++item) {
-    const int row = item / a.npid, slot = item % a.npid;
-    const int pid = a.npid == 2 ? slot : a.pid0;
     __syncthreads();                                  // channels 0..13 free
-    const uint16_t* ob = a.obs + (size_t)row * a.obs_stride;
-    const int32_t* perm = a.view_perm + pid * C0;
-    for (int i = t; i < C0 * NP; i += T) {          // exact in float16: hi plane only
-      const int c = i / NP, p = i - c * NP;
-      s.act[0][((p / HW + 1) * 15 + (p % HW) + 1) * CS + c] = ob[perm[c] * NP + p];
-    }
+    stage();                                          // exact in float16: hi plane only
+    fetch(min(item + 1, end - 1));
     __syncthreads();
 
     float mean, rstd;
     {
-      floatx4 acc[3];
-      conv<0, S0, 3, false>(s.act[0], s.act[1], blds0, bias0, w, 4, acc);
-      ln_stats<3>(acc, w, 4, true, s.red, rslot, 1.0f / (16 * NP), mean, rstd);
-      ln_write<3>(acc, w, 4, 0, true, mean, rstd, a.ln0w, a.ln0b, s.act[0], s.act[1], nullptr);
+      floatx4 acc[4];
+      float4 gg[4], bb[4];
+      conv<0, S0, 4, false>(s.act[0], s.act[1], bglob0, bias0, w, 4, acc);
+      ln_tables<4>(w, 4, 0, a.ln0w, a.ln0b, gg, bb);
+      ln_stats<4>(acc, w, 4, true, s.red, rslot, 1.0f / (16 * NP), mean, rstd);
+      ln_write<4>(acc, w, 4, 0, true, mean, rstd, gg, bb, s.act[0], s.act[1], nullptr);
     }
     __syncthreads();
     {
-      floatx4 acc[6];
-      conv<0, S1, 6, true>(s.act[0], s.act[1], breg1, bias1, mt1, 2, acc);
-      ln_stats<6>(acc, mt1, 2, true, s.red, rslot, 1.0f / (32 * NP), mean, rstd);
-      ln_write<6>(acc, mt1, 2, n1, true, mean, rstd, a.ln1w, a.ln1b, s.act[0], s.act[1],
-                  nullptr);
+      floatx4 acc[7];
+      float4 gg[7], bb[7];
+      conv<0, S1, 7, true>(s.act[0], s.act[1], breg1, bias1, mt1, 2, acc);
+      ln_tables<7>(mt1, 2, n1, a.ln1w, a.ln1b, gg, bb);
+      ln_stats<7>(acc, mt1, 2, true, s.red, rslot, 1.0f / (32 * NP), mean, rstd);
+      ln_write<7>(acc, mt1, 2, n1, true, mean, rstd, gg, bb, s.act[0], s.act[1], nullptr);
     }
     __syncthreads();
     {
       floatx4 acc[MT];
+      float4 gg[MT], bb[MT];
       conv<1, S2, MT, true>(s.act[0], s.act[1], breg2, bias2, 0, 1, acc);
+      ln_tables<MT>(0, 1, n2, a.ln2w, a.ln2b, gg, bb);
       ln_stats<MT>(acc, 0, 1, true, s.red, rslot, 1.0f / (64 * NP), mean, rstd);
-      ln_write<MT>(acc, 0, 1, n2, true, mean, rstd, a.ln2w, a.ln2b, s.act[0], s.act[1],
-                   nullptr);
+      ln_write<MT>(acc, 0, 1, n2, true, mean, rstd, gg, bb, s.act[0], s.act[1], nullptr);
     }
     __syncthreads();
     {
-      floatx4 acc[3];
-      conv<2, S3, 3, true>(s.act[0], s.act[1], blds3, bias3, w, 4, acc);
+      floatx4 acc[4];
+      float4 gg[4], bb[4];
+      conv<2, S3, 4, true>(s.act[0], s.act[1], bglob3, bias3, w, 4, acc);
       const bool nv = i16 < 8;
       uint16_t* const fl = a.workspace + (size_t)item * WS_ROW;
-      ln_stats<3>(acc, w, 4, nv, s.red, rslot, 1.0f / (8 * NP), mean, rstd);
-      ln_write<3>(acc, w, 4, 0, nv, mean, rstd, a.ln3w, a.ln3b, s.act[0], s.act[1], fl);
+      ln_tables<4>(w, 4, 0, a.ln3w, a.ln3b, gg, bb);
+      ln_stats<4>(acc, w, 4, nv, s.red, rslot, 1.0f / (8 * NP), mean, rstd);
+      ln_write<4>(acc, w, 4, 0, nv, mean, rstd, gg, bb, s.act[0], s.act[1], fl);
       if (t < KF - FLAT) fl[FLAT + t] = fl[KF + FLAT + t] = 0;
     }
   }

@@ -477,13 +477,13 @@ def _frag16_planes(w: torch.Tensor, kpad: int):
 
 
 def _pack_ln(g: torch.Tensor, n_tiles: int) -> torch.Tensor:
-    """[C][13][13] LayerNorm affine -> [tile][11][lane][4]: value q of lane l
-    in position tile mt is channel 16 tile + l % 16, position 16 mt +
-    4 (l // 16) + q (zero past 169 positions or C channels)."""
+    """[C][13][13] LayerNorm affine -> [tile][13][lane][4]: value q of lane l
+    in row tile y is channel 16 tile + l % 16 at position (y, x = 4 (l // 16)
+    + q) (zero for x >= 13 or past C channels)."""
     c = g.shape[0]
-    gp = torch.zeros((n_tiles * 16, 176), dtype=torch.float32)
-    gp[:c, :169] = g.float().reshape(c, 169)
-    x = gp.view(n_tiles, 16, 11, 4, 4)                        # [tile][i16][mt][kq][q]
+    gp = torch.zeros((n_tiles * 16, 13, 16), dtype=torch.float32)
+    gp[:c, :, :13] = g.float().reshape(c, 13, 13)
+    x = gp.view(n_tiles, 16, 13, 4, 4)                        # [tile][i16][y][kq][q]
     return x.permute(0, 2, 3, 1, 4).reshape(-1).contiguous()
 
 
@@ -537,7 +537,7 @@ def pack_cnn(params: dict, n_players: int = 2, obs_shape=(14, 13, 13)) -> dict:
         out[key], out[key + "_lo"] = _split16(_conv_operand(f(src), nt))
     out["s0h"], out["s0l"] = _frag16_planes(f("shared.0.weight"), CNN_FLAT_PAD)
     expect = dict(c0w=5 * 64 * 8, c1w=2 * 5 * 64 * 8, c2w=4 * 9 * 64 * 8, c3w=2 * 64 * 8,
-                  s0h=8 * 43 * 64 * 8, s3p=8 * 32 * 64, hp=12 * 32 * 64, ln2w=4 * 11 * 64 * 4)
+                  s0h=8 * 43 * 64 * 8, s3p=8 * 32 * 64, hp=12 * 32 * 64, ln2w=4 * 13 * 64 * 4)
     for k, numel in expect.items():
         if out[k].numel() != numel:
             raise ValueError(f"{k} packs to {out[k].numel()} values, expected {numel}")

@@ -305,10 +305,12 @@ def test_pack_cnn_operands_reproduce_the_reference_layers():
     wt = w0.t().double()
     err = (kn[0][:1352].double() + kn[1][:1352].double() - wt).abs()
     assert bool((err <= 2.0 ** -22 * wt.abs() + 2.0 ** -24).all())
-    ln = pk["ln2w"].view(4, 11, 4, 16, 4)                        # [tile][mt][kq][i16][q]
-    gam = params["conv.6.weight"].reshape(64, 169)
-    assert float(ln[1, 3, 2, 5, 1]) == float(gam[16 + 5, 16 * 3 + 4 * 2 + 1])
-    assert float(ln[0, 10, 3, 0, 3]) == 0.0                      # position 175 >= 169
+    ln = pk["ln2w"].view(4, 13, 4, 16, 4)                        # [tile][row][kq][i16][q]
+    gam = params["conv.6.weight"].reshape(64, 13, 13)
+    assert float(ln[1, 3, 2, 5, 1]) == float(gam[16 + 5, 3, 4 * 2 + 1])
+    assert float(ln[2, 12, 3, 7, 0]) == float(gam[32 + 7, 12, 12])
+    assert float(ln[0, 10, 3, 0, 1]) == 0.0                      # x = 13 is past the row
+    assert torch.equal(ln.permute(0, 3, 1, 2, 4).reshape(64, 13, 16)[:, :, :13], gam)
     assert torch.equal(pk["fw"][5:7], params["bomb_head.2.weight"])
     assert sum(v.numel() for v in params.values()) == 281744
 
