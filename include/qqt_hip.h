@@ -447,8 +447,8 @@ int qqt_gather_rows(const qqt_gather_args* args, void* stream);
  * 1352..1375 zero).  The other Linear weights are float32
  * [tile][step][lane], lane l holding output 16 tile + l % 16, input
  * 4 step + l / 16.  LayerNorm tables are packed [tile][13 rows][lane][4]
- * (value q of lane l in row y: channel 16 tile + l % 16 at position (y, x =
- * 4 (l / 16) + q); zero for x >= 13 or past the channel count), 16-byte
+ * (value q of lane l in row y: channel 16 tile + 4 (l / 16) + q at position
+ * (y, x = l % 16); zero for x >= 13 or past the channel count), 16-byte
  * aligned.  Two launches on `stream`: the trunk writes each item's
  * flattened features as float16 hi / lo rows into the workspace, the head
  * reads them; calls that overlap on one workspace race. */

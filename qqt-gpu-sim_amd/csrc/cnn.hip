@@ -151,7 +151,10 @@ __device__ __forceinline__ constexpr int tap_off(int tap) { return (tap / 3) * P
 // (duplicates of row 12 are computed and later ignored), lane x of a tile
 // at output position (row, x), x >= 13 computed from the padding and
 // ignored; the 16 lanes of a tile read consecutive padded positions, so the
-// 16-byte reads are free of bank conflicts; acc[t] = bias +
+// 16-byte reads are free of bank conflicts.  The products are taken as
+// weights x activations, so the accumulators hold the transposed tile:
+// value q of lane l is output channel 16 ntile + 4 (l / 16) + q at
+// position x = l % 16 of the row; acc[t] = bias +
 // sum over steps of A B, three float16 products per step (two without the
 // activations' lo plane).  bfrag(s) returns step s's B fragments; the step
 // loop stays rolled, with B fragments loaded two steps ahead, and each
@@ -159,7 +162,7 @@ __device__ __forceinline__ constexpr int tap_off(int tap) { return (tap / 3) * P
 // MFMAs share an accumulator.
 template <int KIND, int STEPS, int NTL, bool ALO, class BF>
 __device__ __forceinline__ void conv(const uint16_t* act_hi, const uint16_t* act_lo, BF bfrag,
-                                     float bias, int mt0, int ms, floatx4 (&acc)[NTL]) {
+                                     floatx4 bias, int mt0, int ms, floatx4 (&acc)[NTL]) {
   constexpr int CG = NTL > 8 ? (NTL + 1) / 2 : NTL;
   const int lane = opaque_lane(), i16 = lane & 15, kq = lane >> 4;
   int base[NTL];
@@ -168,7 +171,7 @@ __device__ __forceinline__ void conv(const uint16_t* act_hi, const uint16_t* act
     const int pb = min(mt0 + t * ms, MT - 1) * PW + i16;   // padded position of tap (0, 0)
     base[t] = KIND == 0 ? pb * CS + 8 * (kq & 1) : KIND == 1 ? pb * CS + 8 * kq
                         : (pb + PW + 1) * CS + 8 * kq;
-    acc[t] = floatx4{bias, bias, bias, bias};
+    acc[t] = bias;
   }
   BFrag b = bfrag(0), b1 = bfrag(min(1, STEPS - 1));
 #pragma unroll 1
@@ -193,14 +196,14 @@ __device__ __forceinline__ void conv(const uint16_t* act_hi, const uint16_t* act
         }
 #pragma unroll
       for (int u = 0; u < CG; ++u)
-        if (t0 + u < NTL) acc[t0 + u] = mfma16(ah[u], b.hi, acc[t0 + u]);
+        if (t0 + u < NTL) acc[t0 + u] = mfma16(b.hi, ah[u], acc[t0 + u]);
 #pragma unroll
       for (int u = 0; u < CG; ++u)
-        if (t0 + u < NTL) acc[t0 + u] = mfma16(ah[u], b.lo, acc[t0 + u]);
+        if (t0 + u < NTL) acc[t0 + u] = mfma16(b.lo, ah[u], acc[t0 + u]);
       if constexpr (ALO) {
 #pragma unroll
         for (int u = 0; u < CG; ++u)
-          if (t0 + u < NTL) acc[t0 + u] = mfma16(al[u], b.hi, acc[t0 + u]);
+          if (t0 + u < NTL) acc[t0 + u] = mfma16(b.hi, al[u], acc[t0 + u]);
       }
     }
     b = b1;
@@ -208,21 +211,22 @@ __device__ __forceinline__ void conv(const uint16_t* act_hi, const uint16_t* act
   }
 }
 
-// LayerNorm statistics over the valid outputs of a layer (channel valid,
-// row tile < 13, x = 4 (lane / 16) + q < 13).
+// LayerNorm statistics over the valid outputs of a layer (lane x < 13,
+// channel group kq < cq, row tile < 13).
 template <int NTL>
-__device__ __forceinline__ void ln_stats(const floatx4 (&acc)[NTL], int mt0, int ms,
-                                         bool nvalid, float (*red)[NW], int& slot,
-                                         float inv_count, float& mean, float& rstd) {
-  const int kq = opaque_lane() >> 4;
+__device__ __forceinline__ void ln_stats(const floatx4 (&acc)[NTL], int mt0, int ms, int cq,
+                                         float (*red)[NW], int& slot, float inv_count,
+                                         float& mean, float& rstd) {
+  const int lane = opaque_lane();
+  const bool on = (lane & 15) < HW && (lane >> 4) < cq;
   float s = 0.0f;
 #pragma unroll
   for (int t = 0; t < NTL; ++t)
     if (mt0 + t * ms < MT) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) s += (nvalid && 4 * kq + q < HW) ? acc[t][q] : 0.0f;
+      for (int q = 0; q < 4; ++q) s += acc[t][q];
     }
-  mean = block_sum(s, red, slot) * inv_count;
+  mean = block_sum(on ? s : 0.0f, red, slot) * inv_count;
   float v = 0.0f;
 #pragma unroll
   for (int t = 0; t < NTL; ++t)
@@ -230,15 +234,15 @@ __device__ __forceinline__ void ln_stats(const floatx4 (&acc)[NTL], int mt0, int
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const float d = acc[t][q] - mean;
-        v += (nvalid && 4 * kq + q < HW) ? d * d : 0.0f;
+        v += d * d;
       }
     }
-  rstd = 1.0f / sqrtf(block_sum(v, red, slot) * inv_count + 1e-5f);
+  rstd = 1.0f / sqrtf(block_sum(on ? v : 0.0f, red, slot) * inv_count + 1e-5f);
 }
 
 // LayerNorm affine tables of this wavefront's row tiles (min(mt0 + t ms,
 // 12)), loaded before the statistics so that their latency overlaps the
-// reductions.  g / bt: [NT][13][64][4] packed.
+// reductions.  g / bt: [NT][13][64][4] packed in the accumulator layout.
 template <int NTL>
 __device__ __forceinline__ void ln_tables(int mt0, int ms, int ntile,
                                           const float* __restrict__ g,
@@ -253,39 +257,42 @@ __device__ __forceinline__ void ln_tables(int mt0, int ms, int ntile,
   }
 }
 
-// relu(LN affine) of this wavefront's outputs: into the hi/lo activation
-// planes, or (fl != nullptr) into the workspace row fl (hi at n * 169 + p,
-// lo KF halves on).  A lane's four values are consecutive positions of one
-// row, so one address serves all four.
+// relu(LN affine) of this wavefront's outputs (lanes x < 13, channel groups
+// kq < cq): a lane's four values are four consecutive channels of one
+// position, one 8-byte store per plane into the activation planes, or
+// (fl != nullptr) into the workspace row fl (hi at n * 169 + p, lo KF
+// halves on).
 template <int NTL>
 __device__ __forceinline__ void ln_write(const floatx4 (&acc)[NTL], int mt0, int ms, int ntile,
-                                         bool nvalid, float mean, float rstd,
+                                         int cq, float mean, float rstd,
                                          const float4 (&gg)[NTL], const float4 (&bb)[NTL],
                                          uint16_t* act_hi, uint16_t* act_lo, uint16_t* fl) {
-  const int lane = opaque_lane(), i16 = lane & 15, kq = lane >> 4;
-  const int n = 16 * ntile + i16;
+  const int lane = opaque_lane(), x = lane & 15, kq = lane >> 4;
+  if (x >= HW || kq >= cq) return;
+  const int n0 = 16 * ntile + 4 * kq;
 #pragma unroll
   for (int t = 0; t < NTL; ++t)
-    if (mt0 + t * ms < MT && nvalid) {
+    if (mt0 + t * ms < MT) {
       const int y = mt0 + t * ms;
       const float gv[4] = {gg[t].x, gg[t].y, gg[t].z, gg[t].w};
       const float bv[4] = {bb[t].x, bb[t].y, bb[t].z, bb[t].w};
-      const int i0 = ((y + 1) * PW + 1 + 4 * kq) * CS + n;
-      const int f0 = n * NP + y * HW + 4 * kq;
+      uint16_t hi[4], lo[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (4 * kq + q < HW) {
-          const float y4 = fmaxf((acc[t][q] - mean) * rstd * gv[q] + bv[q], 0.0f);
-          uint16_t hi, lo;
-          split16(y4, hi, lo);
-          if (fl) {
-            fl[f0 + q] = hi;
-            fl[KF + f0 + q] = lo;
-          } else {
-            act_hi[i0 + q * CS] = hi;
-            act_lo[i0 + q * CS] = lo;
-          }
+      for (int q = 0; q < 4; ++q)
+        split16(fmaxf((acc[t][q] - mean) * rstd * gv[q] + bv[q], 0.0f), hi[q], lo[q]);
+      if (fl) {
+        const int f0 = n0 * NP + y * HW + x;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          fl[f0 + q * NP] = hi[q];
+          fl[KF + f0 + q * NP] = lo[q];
         }
+      } else {
+        const int i0 = ((y + 1) * PW + x + 1) * CS + n0;
+        *reinterpret_cast<uint2*>(act_hi + i0) =
+            uint2{hi[0] | (uint32_t)hi[1] << 16, hi[2] | (uint32_t)hi[3] << 16};
+        *reinterpret_cast<uint2*>(act_lo + i0) =
+            uint2{lo[0] | (uint32_t)lo[1] << 16, lo[2] | (uint32_t)lo[3] << 16};
       }
     }
 }
@@ -360,8 +367,14 @@ __global__ __launch_bounds__(T, 2) void cnn_trunk_kernel(const qqt_cnn_args a, i
   // B operands of every conv from global memory step by step (L2 hits:
   // 10, 20, 72 and 4 KB shared by every workgroup)
   const int n1 = w & 1, n2 = w;
-  const float bias0 = a.c0b[i16], bias1 = a.c1b[16 * n1 + i16], bias2 = a.c2b[16 * n2 + i16];
-  const float bias3 = a.c3b[i16];
+  // biases of the four output channels 16 tile + 4 (lane / 16) .. + 3
+  const int kq4 = 4 * (lane >> 4);
+  auto bias4 = [&](const float* b, int tile) {
+    const float* const p = b + 16 * tile + kq4;
+    return floatx4{p[0], p[1], p[2], p[3]};
+  };
+  const floatx4 bias0 = bias4(a.c0b, 0), bias1 = bias4(a.c1b, n1), bias2 = bias4(a.c2b, n2);
+  const floatx4 bias3 = bias4(a.c3b, 0);
 
   // row tiles per wavefront: conv0 / conv3 {w + 4i}, i < 4; conv1
   // {w/2 + 2i}, i < 7; conv2 all 13
@@ -428,8 +441,8 @@ __global__ __launch_bounds__(T, 2) void cnn_trunk_kernel(const qqt_cnn_args a, i
       float4 gg[4], bb[4];
       conv<0, S0, 4, false>(s.act[0], s.act[1], bglob0, bias0, w, 4, acc);
       ln_tables<4>(w, 4, 0, a.ln0w, a.ln0b, gg, bb);
-      ln_stats<4>(acc, w, 4, true, s.red, rslot, 1.0f / (16 * NP), mean, rstd);
-      ln_write<4>(acc, w, 4, 0, true, mean, rstd, gg, bb, s.act[0], s.act[1], nullptr);
+      ln_stats<4>(acc, w, 4, 4, s.red, rslot, 1.0f / (16 * NP), mean, rstd);
+      ln_write<4>(acc, w, 4, 0, 4, mean, rstd, gg, bb, s.act[0], s.act[1], nullptr);
     }
     __syncthreads();
     {
@@ -437,8 +450,8 @@ __global__ __launch_bounds__(T, 2) void cnn_trunk_kernel(const qqt_cnn_args a, i
       float4 gg[7], bb[7];
       conv<0, S1, 7, true>(s.act[0], s.act[1], breg1, bias1, mt1, 2, acc);
       ln_tables<7>(mt1, 2, n1, a.ln1w, a.ln1b, gg, bb);
-      ln_stats<7>(acc, mt1, 2, true, s.red, rslot, 1.0f / (32 * NP), mean, rstd);
-      ln_write<7>(acc, mt1, 2, n1, true, mean, rstd, gg, bb, s.act[0], s.act[1], nullptr);
+      ln_stats<7>(acc, mt1, 2, 4, s.red, rslot, 1.0f / (32 * NP), mean, rstd);
+      ln_write<7>(acc, mt1, 2, n1, 4, mean, rstd, gg, bb, s.act[0], s.act[1], nullptr);
     }
     __syncthreads();
     {
@@ -446,19 +459,18 @@ __global__ __launch_bounds__(T, 2) void cnn_trunk_kernel(const qqt_cnn_args a, i
       float4 gg[MT], bb[MT];
       conv<1, S2, MT, true>(s.act[0], s.act[1], breg2, bias2, 0, 1, acc);
       ln_tables<MT>(0, 1, n2, a.ln2w, a.ln2b, gg, bb);
-      ln_stats<MT>(acc, 0, 1, true, s.red, rslot, 1.0f / (64 * NP), mean, rstd);
-      ln_write<MT>(acc, 0, 1, n2, true, mean, rstd, gg, bb, s.act[0], s.act[1], nullptr);
+      ln_stats<MT>(acc, 0, 1, 4, s.red, rslot, 1.0f / (64 * NP), mean, rstd);
+      ln_write<MT>(acc, 0, 1, n2, 4, mean, rstd, gg, bb, s.act[0], s.act[1], nullptr);
     }
     __syncthreads();
     {
       floatx4 acc[4];
       float4 gg[4], bb[4];
       conv<2, S3, 4, true>(s.act[0], s.act[1], bglob3, bias3, w, 4, acc);
-      const bool nv = i16 < 8;
       uint16_t* const fl = a.workspace + (size_t)item * WS_ROW;
       ln_tables<4>(w, 4, 0, a.ln3w, a.ln3b, gg, bb);
-      ln_stats<4>(acc, w, 4, nv, s.red, rslot, 1.0f / (8 * NP), mean, rstd);
-      ln_write<4>(acc, w, 4, 0, nv, mean, rstd, gg, bb, s.act[0], s.act[1], fl);
+      ln_stats<4>(acc, w, 4, 2, s.red, rslot, 1.0f / (8 * NP), mean, rstd);
+      ln_write<4>(acc, w, 4, 0, 2, mean, rstd, gg, bb, s.act[0], s.act[1], fl);
       if (t < KF - FLAT) fl[FLAT + t] = fl[KF + FLAT + t] = 0;
     }
   }

@@ -478,13 +478,14 @@ def _frag16_planes(w: torch.Tensor, kpad: int):
 
 def _pack_ln(g: torch.Tensor, n_tiles: int) -> torch.Tensor:
     """[C][13][13] LayerNorm affine -> [tile][13][lane][4]: value q of lane l
-    in row tile y is channel 16 tile + l % 16 at position (y, x = 4 (l // 16)
-    + q) (zero for x >= 13 or past C channels)."""
+    in row tile y is channel 16 tile + 4 (l // 16) + q at position (y, x =
+    l % 16) (zero for x >= 13 or past C channels), the layout of the
+    kernel's transposed convolution accumulators."""
     c = g.shape[0]
     gp = torch.zeros((n_tiles * 16, 13, 16), dtype=torch.float32)
     gp[:c, :, :13] = g.float().reshape(c, 13, 13)
-    x = gp.view(n_tiles, 16, 13, 4, 4)                        # [tile][i16][y][kq][q]
-    return x.permute(0, 2, 3, 1, 4).reshape(-1).contiguous()
+    x = gp.view(n_tiles, 4, 4, 13, 16)                        # [tile][kq][q][y][x]
+    return x.permute(0, 3, 1, 4, 2).reshape(-1).contiguous()
 
 
 CNN_FLAT_PAD = 1376            # flattened trunk features padded to 43 K steps of 32

@@ -305,12 +305,14 @@ def test_pack_cnn_operands_reproduce_the_reference_layers():
     wt = w0.t().double()
     err = (kn[0][:1352].double() + kn[1][:1352].double() - wt).abs()
     assert bool((err <= 2.0 ** -22 * wt.abs() + 2.0 ** -24).all())
-    ln = pk["ln2w"].view(4, 13, 4, 16, 4)                        # [tile][row][kq][i16][q]
+    ln = pk["ln2w"].view(4, 13, 4, 16, 4)                        # [tile][row][kq][x][q]
     gam = params["conv.6.weight"].reshape(64, 13, 13)
-    assert float(ln[1, 3, 2, 5, 1]) == float(gam[16 + 5, 3, 4 * 2 + 1])
-    assert float(ln[2, 12, 3, 7, 0]) == float(gam[32 + 7, 12, 12])
-    assert float(ln[0, 10, 3, 0, 1]) == 0.0                      # x = 13 is past the row
-    assert torch.equal(ln.permute(0, 3, 1, 2, 4).reshape(64, 13, 16)[:, :, :13], gam)
+    assert float(ln[1, 3, 2, 5, 1]) == float(gam[16 + 4 * 2 + 1, 3, 5])
+    assert float(ln[2, 12, 3, 12, 0]) == float(gam[32 + 12, 12, 12])
+    assert float(ln[0, 10, 3, 13, 1]) == 0.0                     # x = 13 is past the row
+    assert torch.equal(ln.permute(0, 2, 4, 1, 3).reshape(64, 13, 16)[:, :, :13], gam)
+    ln3 = pk["ln3w"].view(1, 13, 4, 16, 4)
+    assert float(ln3[0, 0, 2:].abs().max()) == 0.0               # channels 8..15 are zero
     assert torch.equal(pk["fw"][5:7], params["bomb_head.2.weight"])
     assert sum(v.numel() for v in params.values()) == 281744
 
