@@ -496,8 +496,9 @@ typedef struct qqt_cnn_args {
   float* logp_out;            /* [B][out_slots] or NULL */
   float* value_out;           /* [B][out_slots] or NULL */
   float* logits_out;          /* [B][out_slots][8]: 5 move, 2 bomb, value; or NULL */
-  uint16_t* workspace;        /* >= B * npid * QQT_CNN_WS_BYTES_PER_ITEM bytes, 16-byte
-                                 aligned: the trunk's float16 hi / lo feature rows */
+  uint16_t* workspace;        /* >= ceil(B * npid / 32) * 32 * QQT_CNN_WS_BYTES_PER_ITEM
+                                 bytes, 16-byte aligned: the trunk's float16 hi / lo
+                                 features, in blocks of 32 items */
   int64_t workspace_bytes;
 } qqt_cnn_args;
 int qqt_cnn_act(const qqt_cnn_args* args, void* stream);

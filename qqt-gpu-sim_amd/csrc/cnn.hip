@@ -13,7 +13,7 @@
 // wavefronts per CU (one wavefront per SIMD each, 256 registers), each
 // walking a contiguous range of items (row, player) one item at a time, so
 // one workgroup's barriers and LayerNorm reductions overlap the other's
-// convolutions.  cnn_head_kernel: 16 items per workgroup, from the trunk's
+// convolutions.  cnn_head_kernel: 32 items per workgroup, from the trunk's
 // flattened features in the workspace.
 //
 // Trunk.  Feature maps live in LDS as zero-bordered 15 x 15 grids of
@@ -42,7 +42,7 @@
 // flattened index c * 169 + p, zero from 1352).
 // Head: Linear(1352,128) on the same float16 MFMA with the three hi/lo
 // products (K = 43 steps of 32), then Linear(128,128) and the heads' hidden
-// layer as v_mfma_f32_16x16x4_f32 GEMMs with M = the 16 items,
+// layer as v_mfma_f32_16x16x4_f32 GEMMs with M = the 32 items,
 // LayerNorm(128) by 16 threads per item, the output layer and the masked
 // sampling per item.
 
@@ -70,11 +70,18 @@ constexpr int PW = 16;                      // padded row: x = -1 .. 14 (lane x 
 constexpr int PP = 15 * PW + 2;             // padded positions (row tile 12's lane 15 reads 2 past)
 constexpr int CS = 72;                      // halves per position (64 channels + 8: bank spread)
 constexpr int C0 = 14;
-constexpr int HB = 16;                      // items per head workgroup (the 16 MFMA rows)
+constexpr int HB = 32, HM = HB / 16;        // items per head workgroup, its 16-row M tiles
 constexpr int FLAT = 8 * NP;                // 1352
 constexpr int KF = 1376;                    // flattened features padded to 43 K steps of 32
 constexpr int S0H = KF / 32;                // 43
-constexpr int WS_ROW = 2 * KF;              // workspace halves per item (hi row, lo row)
+constexpr int WS_ROW = 2 * KF;              // workspace halves per item (hi and lo planes)
+// Workspace layout, per block of HB items: [plane hi, lo][K step 43][item][32
+// halves], so that a head workgroup reads one contiguous span, 2 KB per K
+// step.  Item i's value k of plane pl is at
+//   (i / HB) * HB * WS_ROW + ((pl * S0H + k / 32) * HB + i % HB) * 32 + k % 32.
+__device__ __forceinline__ int ws_off(int pl, int k) {
+  return (pl * S0H + (k >> 5)) * HB * 32 + (k & 31);   // + (i % HB) * 32 in the item's base
+}
 constexpr int HID = 128, HS = 130, HYS = 194;
 constexpr int S0 = 5, S1 = 5, S2 = 9, S3 = 2;       // 32-deep K steps of the four convolutions
 constexpr int L1 = HID / 4;                         // K steps of the float32 head GEMMs
@@ -89,8 +96,16 @@ struct __align__(16) Lds {                 // every member a multiple of 16 byte
 static_assert(sizeof(uint16_t) * 2 * PP * CS % 16 == 0, "16-byte fragment reads stay aligned");
 static_assert(2 * sizeof(Lds) <= 160 * 1024, "two trunk workgroups fit in one CU's LDS");
 
+// the head's small weights, staged in LDS: biases, LayerNorm affines and
+// the output layer, at these offsets
+constexpr int V_S0B = 0, V_S1W = 128, V_S1B = 256, V_S3B = 384, V_S4W = 512, V_S4B = 640,
+              V_HB = 768, V_FW = 960, V_FB = 1472, V_N = 1480;
+
 struct __align__(16) HeadLds {
-  float h[HB * HS], h2[HB * HS], hy[HB * HYS], lg[HB * 8];
+  float hy[HB * HYS];                       // heads' hidden layer; before it the first layer's
+  float h2[HB * HS];                        // output h (stride HS, read by the second layer)
+  float lg[HB * 8];
+  float v[V_N];
 };
 
 __device__ __forceinline__ floatx4 mfma(float a, float b, floatx4 c) {
@@ -284,8 +299,8 @@ __device__ __forceinline__ void ln_write(const floatx4 (&acc)[NTL], int mt0, int
         const int f0 = n0 * NP + y * HW + x;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          fl[f0 + q * NP] = hi[q];
-          fl[KF + f0 + q * NP] = lo[q];
+          fl[ws_off(0, f0 + q * NP)] = hi[q];
+          fl[ws_off(1, f0 + q * NP)] = lo[q];
         }
       } else {
         const int i0 = ((y + 1) * PW + x + 1) * CS + n0;
@@ -297,21 +312,37 @@ __device__ __forceinline__ void ln_write(const floatx4 (&acc)[NTL], int mt0, int
     }
 }
 
-// Head GEMM for tiles nt0 + i (i < NTW): D[m][n] = sum_k A[m * as + k] W[k][n],
-// A in LDS, W packed [tile][step][lane] in global memory.
+// A head layer's weight operands for tiles nt0 + i (i < NTW), W packed
+// [tile][step][lane] in global memory: loaded ahead of the GEMM.
 template <int STEPS, int NTW>
-__device__ __forceinline__ void head_gemm(const float* A, int as, const float* __restrict__ w,
-                                          int nt0, floatx4 (&c)[NTW]) {
+__device__ __forceinline__ void head_weights(const float* __restrict__ w, int nt0,
+                                             float (&bw)[NTW][STEPS]) {
+  const float* b = w + (size_t)nt0 * STEPS * 64 + (threadIdx.x & 63);
+#pragma unroll
+  for (int i = 0; i < NTW; ++i)
+#pragma unroll
+    for (int j = 0; j < STEPS; ++j) bw[i][j] = b[(i * STEPS + j) * 64];
+}
+
+// Head GEMM over the HM row tiles: D[m][n] = sum_k A[m * as + k] W[k][n],
+// A in LDS, the weight operands in registers (each feeds every row tile).
+template <int STEPS, int NTW>
+__device__ __forceinline__ void head_gemm(const float* A, int as, const float (&bw)[NTW][STEPS],
+                                          floatx4 (&c)[HM][NTW]) {
   const int lane = threadIdx.x & 63, i16 = lane & 15, kq = lane >> 4;
-  const float* a = A + i16 * as + kq;
-  const float* b = w + (size_t)nt0 * STEPS * 64 + lane;
 #pragma unroll
-  for (int i = 0; i < NTW; ++i) c[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 2
+  for (int m = 0; m < HM; ++m)
+#pragma unroll
+    for (int i = 0; i < NTW; ++i) c[m][i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
   for (int j = 0; j < STEPS; ++j) {
-    const float av = a[4 * j];
+    float av[HM];
 #pragma unroll
-    for (int i = 0; i < NTW; ++i) c[i] = mfma(av, b[(i * STEPS + j) * 64], c[i]);
+    for (int m = 0; m < HM; ++m) av[m] = A[(16 * m + i16) * as + kq + 4 * j];
+#pragma unroll
+    for (int i = 0; i < NTW; ++i)
+#pragma unroll
+      for (int m = 0; m < HM; ++m) c[m][i] = mfma(av[m], bw[i][j], c[m][i]);
   }
 }
 
@@ -331,28 +362,31 @@ __device__ __forceinline__ void head_store(floatx4 c, float* dst, int ds, int nt
 // LayerNorm(128) + ReLU of rows m < nb of h (stride HS), 16 threads per row.
 __device__ __forceinline__ void head_ln(float* h, int nb, const float* __restrict__ g,
                                         const float* __restrict__ bt) {
-  const int m = threadIdx.x >> 4, c = threadIdx.x & 15;
-  float v[8];
-  float s = 0.0f;
+  const int c = threadIdx.x & 15;
 #pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    v[r] = h[m * HS + c + 16 * r];
-    s += v[r];
-  }
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
-  const float mean = s * (1.0f / HID);
-  float q = 0.0f;
-#pragma unroll
-  for (int r = 0; r < 8; ++r) q += (v[r] - mean) * (v[r] - mean);
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) q += __shfl_xor(q, o, 64);
-  const float rstd = 1.0f / sqrtf(q * (1.0f / HID) + 1e-5f);
-  if (m < nb) {
+  for (int m = threadIdx.x >> 4; m < HB; m += T / 16) {
+    float v[8];
+    float s = 0.0f;
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
-      const int k = c + 16 * r;
-      h[m * HS + k] = fmaxf((v[r] - mean) * rstd * g[k] + bt[k], 0.0f);
+      v[r] = h[m * HS + c + 16 * r];
+      s += v[r];
+    }
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+    const float mean = s * (1.0f / HID);
+    float q = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) q += (v[r] - mean) * (v[r] - mean);
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) q += __shfl_xor(q, o, 64);
+    const float rstd = 1.0f / sqrtf(q * (1.0f / HID) + 1e-5f);
+    if (m < nb) {
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const int k = c + 16 * r;
+        h[m * HS + k] = fmaxf((v[r] - mean) * rstd * g[k] + bt[k], 0.0f);
+      }
     }
   }
 }
@@ -467,16 +501,16 @@ __global__ __launch_bounds__(T, 2) void cnn_trunk_kernel(const qqt_cnn_args a, i
       floatx4 acc[4];
       float4 gg[4], bb[4];
       conv<2, S3, 4, true>(s.act[0], s.act[1], bglob3, bias3, w, 4, acc);
-      uint16_t* const fl = a.workspace + (size_t)item * WS_ROW;
+      uint16_t* const fl = a.workspace + (size_t)(item / HB) * HB * WS_ROW + (item % HB) * 32;
       ln_tables<4>(w, 4, 0, a.ln3w, a.ln3b, gg, bb);
       ln_stats<4>(acc, w, 4, 2, s.red, rslot, 1.0f / (8 * NP), mean, rstd);
       ln_write<4>(acc, w, 4, 0, 2, mean, rstd, gg, bb, s.act[0], s.act[1], fl);
-      if (t < KF - FLAT) fl[FLAT + t] = fl[KF + FLAT + t] = 0;
+      if (t < KF - FLAT) fl[ws_off(0, FLAT + t)] = fl[ws_off(1, FLAT + t)] = 0;
     }
   }
 }
 
-// Head over items ib .. ib + 15 (rows m of the GEMMs; rows past the batch
+// Head over items ib .. ib + 31 (rows m of the GEMMs; rows past the batch
 // repeat its last item and are not written out).
 __global__ __launch_bounds__(T) void cnn_head_kernel(const qqt_cnn_args a, int items) {
   __shared__ HeadLds s;
@@ -484,57 +518,109 @@ __global__ __launch_bounds__(T) void cnn_head_kernel(const qqt_cnn_args a, int i
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int lane = t & 63, i16 = lane & 15, kq = lane >> 4;
   const int ib = blockIdx.x * HB, nb = min(HB, items - ib);
-
-  // Linear(1352,128): wavefront w computes output tiles 2w, 2w + 1
+  float* const h = s.hy;
+  float w3[2][L1];                                  // Linear(128,128) operands, in flight early
+  head_weights<L1, 2>(a.s3p, 2 * w, w3);
   {
-    const uint16_t* const ar = a.workspace + (size_t)min(ib + i16, items - 1) * WS_ROW + 8 * kq;
+    const float* const src[9] = {a.s0b, a.s1w, a.s1b, a.s3b, a.s4w, a.s4b, a.hb, a.fw, a.fb};
+    const int off[10] = {V_S0B, V_S1W, V_S1B, V_S3B, V_S4W, V_S4B, V_HB, V_FW, V_FB, V_N};
+#pragma unroll
+    for (int k = 0; k < 9; ++k)
+      for (int i = t; i < off[k + 1] - off[k]; i += T) s.v[off[k] + i] = src[k][i];
+  }
+
+  // Linear(1352,128): wavefront w computes output tiles 2w, 2w + 1 of every
+  // row tile (each B fragment feeds HM row tiles)
+  {
+    const uint16_t* ar[HM];
+#pragma unroll
+    for (int m = 0; m < HM; ++m)
+      ar[m] = a.workspace + (size_t)ib * WS_ROW + min(16 * m + i16, nb - 1) * 32 + 8 * kq;
     const size_t tile = (size_t)S0H * BFRAG;
     const uint16_t* const bh = a.s0h + 2 * w * tile + lane * 8;
     const uint16_t* const bl = a.s0l + 2 * w * tile + lane * 8;
-    floatx4 c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0;
-#pragma unroll 4
-    for (int st = 0; st < S0H; ++st) {
-      const half8 ah = ld8(ar + 32 * st), al = ld8(ar + KF + 32 * st);
-      const half8 h0 = ld8(bh + st * BFRAG), l0 = ld8(bl + st * BFRAG);
-      const half8 h1 = ld8(bh + tile + st * BFRAG), l1 = ld8(bl + tile + st * BFRAG);
-      c0 = mfma16(ah, h0, c0);
-      c1 = mfma16(ah, h1, c1);
-      c0 = mfma16(ah, l0, c0);
-      c1 = mfma16(ah, l1, c1);
-      c0 = mfma16(al, h0, c0);
-      c1 = mfma16(al, h1, c1);
-    }
-    head_store(c0, s.h, HS, 2 * w, a.s0b, false);
-    head_store(c1, s.h, HS, 2 * w + 1, a.s0b, false);
-  }
-  __syncthreads();
-  head_ln(s.h, nb, a.s1w, a.s1b);
-  __syncthreads();
-  {
-    floatx4 c[2];
-    head_gemm<L1, 2>(s.h, HS, a.s3p, 2 * w, c);
-    head_store(c[0], s.h2, HS, 2 * w, a.s3b, false);
-    head_store(c[1], s.h2, HS, 2 * w + 1, a.s3b, false);
-  }
-  __syncthreads();
-  head_ln(s.h2, nb, a.s4w, a.s4b);
-  __syncthreads();
-  {
-    floatx4 c[3];
-    head_gemm<L1, 3>(s.h2, HS, a.hp, 3 * w, c);
+    struct Frag { half8 ah[HM], al[HM], h0, l0, h1, l1; };
+    auto load = [&](int st) {
+      Frag f;
 #pragma unroll
-    for (int i = 0; i < 3; ++i) head_store(c[i], s.hy, HYS, 3 * w + i, a.hb, true);
+      for (int m = 0; m < HM; ++m) {
+        f.ah[m] = ld8(ar[m] + st * HB * 32);
+        f.al[m] = ld8(ar[m] + (S0H + st) * HB * 32);
+      }
+      f.h0 = ld8(bh + st * BFRAG);
+      f.l0 = ld8(bl + st * BFRAG);
+      f.h1 = ld8(bh + tile + st * BFRAG);
+      f.l1 = ld8(bl + tile + st * BFRAG);
+      return f;
+    };
+    floatx4 c[HM][2];
+#pragma unroll
+    for (int m = 0; m < HM; ++m) c[m][0] = c[m][1] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    // rolled K loop, fragments loaded two steps ahead
+    Frag f0 = load(0), f1 = load(1);
+#pragma unroll 1
+    for (int st = 0; st < S0H; ++st) {
+      const Frag f2 = load(min(st + 2, S0H - 1));
+#pragma unroll
+      for (int m = 0; m < HM; ++m) {
+        c[m][0] = mfma16(f0.ah[m], f0.h0, c[m][0]);
+        c[m][1] = mfma16(f0.ah[m], f0.h1, c[m][1]);
+      }
+#pragma unroll
+      for (int m = 0; m < HM; ++m) {
+        c[m][0] = mfma16(f0.ah[m], f0.l0, c[m][0]);
+        c[m][1] = mfma16(f0.ah[m], f0.l1, c[m][1]);
+      }
+#pragma unroll
+      for (int m = 0; m < HM; ++m) {
+        c[m][0] = mfma16(f0.al[m], f0.h0, c[m][0]);
+        c[m][1] = mfma16(f0.al[m], f0.h1, c[m][1]);
+      }
+      f0 = f1;
+      f1 = f2;
+    }
+#pragma unroll
+    for (int m = 0; m < HM; ++m) {
+      head_store(c[m][0], h + 16 * m * HS, HS, 2 * w, s.v + V_S0B, false);
+      head_store(c[m][1], h + 16 * m * HS, HS, 2 * w + 1, s.v + V_S0B, false);
+    }
+  }
+  __syncthreads();
+  head_ln(h, nb, s.v + V_S1W, s.v + V_S1B);
+  __syncthreads();
+  {
+    floatx4 c[HM][2];
+    head_gemm<L1, 2>(h, HS, w3, c);
+#pragma unroll
+    for (int m = 0; m < HM; ++m) {
+      head_store(c[m][0], s.h2 + 16 * m * HS, HS, 2 * w, s.v + V_S3B, false);
+      head_store(c[m][1], s.h2 + 16 * m * HS, HS, 2 * w + 1, s.v + V_S3B, false);
+    }
+  }
+  float wh[3][L1];                                  // heads' operands, loaded under the LayerNorm
+  head_weights<L1, 3>(a.hp, 3 * w, wh);
+  __syncthreads();
+  head_ln(s.h2, nb, s.v + V_S4W, s.v + V_S4B);
+  __syncthreads();
+  {
+    floatx4 c[HM][3];
+    head_gemm<L1, 3>(s.h2, HS, wh, c);
+#pragma unroll
+    for (int m = 0; m < HM; ++m)
+#pragma unroll
+      for (int i = 0; i < 3; ++i)
+        head_store(c[m][i], s.hy + 16 * m * HYS, HYS, 3 * w + i, s.v + V_HB, true);
   }
   __syncthreads();
   if (t < HB * 8) {                                   // output layer: item m, output o
     const int m = t >> 3, o = t & 7;
     const int base = o < 5 ? 0 : o < 7 ? 64 : 128;
     const float* x = s.hy + m * HYS + base;
-    const float* wf = a.fw + o * 64;
+    const float* wf = s.v + V_FW + o * 64;
     float acc = 0.0f;
 #pragma unroll 8
     for (int k = 0; k < 64; ++k) acc += x[k] * wf[k];
-    s.lg[m * 8 + o] = acc + a.fb[o];
+    s.lg[m * 8 + o] = acc + s.v[V_FB + o];
   }
   __syncthreads();
   if (t < nb) {
@@ -645,10 +731,10 @@ int qqt_cnn_act(const qqt_cnn_args* a, void* stream) {
   }
   const int items = a->batch * a->npid;
   if (!a->workspace || ((uintptr_t)a->workspace & 15) ||
-      a->workspace_bytes < (int64_t)items * QQT_CNN_WS_BYTES_PER_ITEM) {
+      a->workspace_bytes < (int64_t)((items + HB - 1) / HB) * HB * QQT_CNN_WS_BYTES_PER_ITEM) {
     snprintf(g_err, sizeof(g_err),
-             "qqt_cnn_act: workspace must be 16-byte aligned and hold %d bytes per item",
-             QQT_CNN_WS_BYTES_PER_ITEM);
+             "qqt_cnn_act: workspace must be 16-byte aligned and hold %d bytes per item "
+             "(items rounded up to %d)", QQT_CNN_WS_BYTES_PER_ITEM, HB);
     return QQT_E_ARG;
   }
   const int grid = min(2 * cu_count(), items);

@@ -579,7 +579,8 @@ class HipCnnActorCritic(HipActorCritic):
         if ws is None:
             ws = self._ws = {}
         if items not in ws:
-            ws[items] = torch.empty(items * CNN_WS_BYTES_PER_ITEM, dtype=torch.uint8,
+            blocks = (items + 31) // 32             # the kernels' 32-item blocks
+            ws[items] = torch.empty(blocks * 32 * CNN_WS_BYTES_PER_ITEM, dtype=torch.uint8,
                                     device=self.device)
         return ws[items]
 

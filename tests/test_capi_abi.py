@@ -222,7 +222,7 @@ def _cnn_args(**kw):
     a.batch, a.npid, a.obs_stride, a.w_players = 4, 2, 14 * 169, 2
     for i, name in enumerate(_CNN_PTRS):
         setattr(a, name, 0x10000 * (i + 1))
-    a.workspace_bytes = 4 * 2 * 5504
+    a.workspace_bytes = 32 * 5504                 # 8 items, rounded up to one 32-item block
     for k, v in kw.items():
         setattr(a, k, v)
     return a
@@ -247,7 +247,7 @@ def _cnn_args(**kw):
     (dict(s0h=0x10002), "16-byte aligned"),
     (dict(workspace=None), "workspace"),
     (dict(workspace=0x10008), "workspace"),
-    (dict(workspace_bytes=4 * 2 * 5504 - 1), "workspace"),
+    (dict(workspace_bytes=32 * 5504 - 1), "workspace"),
 ])
 def test_cnn_rejects_bad_arguments(lib, kw, msg):
     assert lib.qqt_cnn_act(_cnn_args(**kw), None) == -1
