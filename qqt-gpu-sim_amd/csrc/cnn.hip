@@ -132,6 +132,17 @@ __device__ __forceinline__ half8 ld8(const uint16_t* p) {
   c.u = *reinterpret_cast<const uint4*>(p);
   return c.h;
 }
+// Uniform base + unsigned 32-bit byte offset: the form the compiler turns
+// into a scalar-base global access (no 64-bit address arithmetic per lane).
+template <class T>
+__device__ __forceinline__ const T* at(const T* base, uint32_t byte_off) {
+  return reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + byte_off);
+}
+template <class T>
+__device__ __forceinline__ T* at(T* base, uint32_t byte_off) {
+  return reinterpret_cast<T*>(reinterpret_cast<char*>(base) + byte_off);
+}
+
 __device__ __forceinline__ floatx4 mfma16(half8 a, half8 b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
@@ -151,12 +162,20 @@ __device__ __forceinline__ int opaque_tid() {
   return t;
 }
 
-// float32 -> float16 hi + lo (x = hi + lo to ~2^-22 relative), saturating
-// at float16's range so that both halves stay finite.
-__device__ __forceinline__ void split16(float x, uint16_t& hi, uint16_t& lo) {
-  const __half h = __float2half_rn(fminf(fmaxf(x, -65504.0f), 65504.0f));
-  hi = __half_as_ushort(h);
-  lo = __half_as_ushort(__float2half_rn(fminf(fmaxf(x - __half2float(h), -65504.0f), 65504.0f)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// relu of four float32 values, saturated at float16's 65504 (one med3 each),
+// split into float16 hi + lo (y = hi + lo to ~2^-22 relative), each plane
+// packed two halves per word (v_cvt_pk_f16_f32, round to nearest)
+__device__ __forceinline__ void relu_split4(const float (&z)[4], uint2& hi, uint2& lo) {
+  float y[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) y[q] = __builtin_amdgcn_fmed3f(z[q], 0.0f, 65504.0f);
+  const half2v h01 = {(_Float16)y[0], (_Float16)y[1]}, h23 = {(_Float16)y[2], (_Float16)y[3]};
+  const half2v l01 = {(_Float16)(y[0] - (float)h01.x), (_Float16)(y[1] - (float)h01.y)};
+  const half2v l23 = {(_Float16)(y[2] - (float)h23.x), (_Float16)(y[3] - (float)h23.y)};
+  hi = uint2{__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23)};
+  lo = uint2{__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)};
 }
 
 __device__ __forceinline__ constexpr int tap_off(int tap) { return (tap / 3) * PW + tap % 3; }
@@ -249,7 +268,7 @@ __device__ __forceinline__ void ln_stats(const floatx4 (&acc)[NTL], int mt0, int
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const float d = acc[t][q] - mean;
-        v += d * d;
+        v = fmaf(d, d, v);
       }
     }
   rstd = 1.0f / sqrtf(block_sum(on ? v : 0.0f, red, slot) * inv_count + 1e-5f);
@@ -263,20 +282,20 @@ __device__ __forceinline__ void ln_tables(int mt0, int ms, int ntile,
                                           const float* __restrict__ g,
                                           const float* __restrict__ bt, float4 (&gg)[NTL],
                                           float4 (&bb)[NTL]) {
-  const int tl = opaque_lane() * 4;
+  const uint32_t tl = opaque_lane() * 16u;
 #pragma unroll
   for (int t = 0; t < NTL; ++t) {
-    const int gi = (ntile * MT + min(mt0 + t * ms, MT - 1)) * 256 + tl;
-    gg[t] = *reinterpret_cast<const float4*>(g + gi);
-    bb[t] = *reinterpret_cast<const float4*>(bt + gi);
+    const uint32_t gi = (uint32_t)(ntile * MT + min(mt0 + t * ms, MT - 1)) * 1024u + tl;
+    gg[t] = *at(reinterpret_cast<const float4*>(g), gi);
+    bb[t] = *at(reinterpret_cast<const float4*>(bt), gi);
   }
 }
 
 // relu(LN affine) of this wavefront's outputs (lanes x < 13, channel groups
-// kq < cq): a lane's four values are four consecutive channels of one
-// position, one 8-byte store per plane into the activation planes, or
-// (fl != nullptr) into the workspace row fl (hi at n * 169 + p, lo KF
-// halves on).
+// kq < cq; saturated at 65504): a lane's four values are four consecutive
+// channels of one position, one 8-byte store per plane into the activation
+// planes, or (fl != nullptr) into the item's workspace block (value
+// n * 169 + p of each plane, ws_off).
 template <int NTL>
 __device__ __forceinline__ void ln_write(const floatx4 (&acc)[NTL], int mt0, int ms, int ntile,
                                          int cq, float mean, float rstd,
@@ -291,23 +310,24 @@ __device__ __forceinline__ void ln_write(const floatx4 (&acc)[NTL], int mt0, int
       const int y = mt0 + t * ms;
       const float gv[4] = {gg[t].x, gg[t].y, gg[t].z, gg[t].w};
       const float bv[4] = {bb[t].x, bb[t].y, bb[t].z, bb[t].w};
-      uint16_t hi[4], lo[4];
+      float z[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        split16(fmaxf((acc[t][q] - mean) * rstd * gv[q] + bv[q], 0.0f), hi[q], lo[q]);
+      for (int q = 0; q < 4; ++q) z[q] = fmaf(acc[t][q] - mean, rstd * gv[q], bv[q]);
+      uint2 hi, lo;
+      relu_split4(z, hi, lo);
       if (fl) {
         const int f0 = n0 * NP + y * HW + x;
+        const uint32_t hw[4] = {hi.x, hi.x >> 16, hi.y, hi.y >> 16};
+        const uint32_t lw[4] = {lo.x, lo.x >> 16, lo.y, lo.y >> 16};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          fl[ws_off(0, f0 + q * NP)] = hi[q];
-          fl[ws_off(1, f0 + q * NP)] = lo[q];
+          *at(fl, (uint32_t)ws_off(0, f0 + q * NP) * 2u) = (uint16_t)hw[q];
+          *at(fl, (uint32_t)ws_off(1, f0 + q * NP) * 2u) = (uint16_t)lw[q];
         }
       } else {
         const int i0 = ((y + 1) * PW + x + 1) * CS + n0;
-        *reinterpret_cast<uint2*>(act_hi + i0) =
-            uint2{hi[0] | (uint32_t)hi[1] << 16, hi[2] | (uint32_t)hi[3] << 16};
-        *reinterpret_cast<uint2*>(act_lo + i0) =
-            uint2{lo[0] | (uint32_t)lo[1] << 16, lo[2] | (uint32_t)lo[3] << 16};
+        *reinterpret_cast<uint2*>(act_hi + i0) = hi;
+        *reinterpret_cast<uint2*>(act_lo + i0) = lo;
       }
     }
 }
@@ -415,17 +435,26 @@ __global__ __launch_bounds__(T, 2) void cnn_trunk_kernel(const qqt_cnn_args a, i
   const int mt1 = w >> 1;
 
   for (int i = t; i < PP * CS; i += T) s.act[0][i] = s.act[1][i] = 0;
-  const uint16_t* const c1h = a.c1w + ((size_t)n1 * S1 * 64 + lane) * 8;
-  const uint16_t* const c1l = a.c1w_lo + ((size_t)n1 * S1 * 64 + lane) * 8;
-  auto breg1 = [&](int j) { return BFrag{ld8(c1h + j * BFRAG), ld8(c1l + j * BFRAG)}; };
-  const uint16_t* const c2h = a.c2w + ((size_t)n2 * S2 * 64 + lane) * 8;
-  const uint16_t* const c2l = a.c2w_lo + ((size_t)n2 * S2 * 64 + lane) * 8;
-  auto breg2 = [&](int j) { return BFrag{ld8(c2h + j * BFRAG), ld8(c2l + j * BFRAG)}; };
+  const uint32_t lb = (uint32_t)lane * 16u;        // this lane's bytes in a step's fragments
+  const uint16_t* const c1h = a.c1w + (size_t)n1 * S1 * BFRAG;
+  const uint16_t* const c1l = a.c1w_lo + (size_t)n1 * S1 * BFRAG;
+  auto breg1 = [&](int j) {
+    const uint32_t o = lb + (uint32_t)j * (BFRAG * 2);
+    return BFrag{ld8(at(c1h, o)), ld8(at(c1l, o))};
+  };
+  const uint16_t* const c2h = a.c2w + (size_t)n2 * S2 * BFRAG;
+  const uint16_t* const c2l = a.c2w_lo + (size_t)n2 * S2 * BFRAG;
+  auto breg2 = [&](int j) {
+    const uint32_t o = lb + (uint32_t)j * (BFRAG * 2);
+    return BFrag{ld8(at(c2h, o)), ld8(at(c2l, o))};
+  };
   auto bglob0 = [&](int j) {
-    return BFrag{ld8(a.c0w + (j * 64 + lane) * 8), ld8(a.c0w_lo + (j * 64 + lane) * 8)};
+    const uint32_t o = lb + (uint32_t)j * (BFRAG * 2);
+    return BFrag{ld8(at(a.c0w, o)), ld8(at(a.c0w_lo, o))};
   };
   auto bglob3 = [&](int j) {
-    return BFrag{ld8(a.c3w + (j * 64 + lane) * 8), ld8(a.c3w_lo + (j * 64 + lane) * 8)};
+    const uint32_t o = lb + (uint32_t)j * (BFRAG * 2);
+    return BFrag{ld8(at(a.c3w, o)), ld8(at(a.c3w_lo, o))};
   };
 
   // Observation staging: thread t moves values i = t + 256 k (k < OBS_K) of
@@ -448,7 +477,7 @@ __global__ __launch_bounds__(T, 2) void cnn_trunk_kernel(const qqt_cnn_args a, i
 #pragma unroll
     for (int k = 0; k < OBS_K; ++k) {
       const int i = min(tt + T * k, C0 * NP - 1), c = i / NP;
-      ov[k] = ob[s.perm[kind][c] * NP + (i - c * NP)];
+      ov[k] = *at(ob, (uint32_t)(s.perm[kind][c] * NP + (i - c * NP)) * 2u);
     }
   };
   auto stage = [&]() {
