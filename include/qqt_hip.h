@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 23
+#define QQT_ABI_VERSION 24
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -434,22 +434,23 @@ int qqt_gather_rows(const qqt_gather_args* args, void* stream);
  * arch "cnn" (:167-196, 230-245) as qqt_mlp_act does for the MLP: the same
  * masks, uniforms and output layout.  Every LayerNorm normalises one sample
  * over all of its values (eps 1e-5) with an elementwise affine of that shape.
- * Weights come in the kernel's operand order.  Conv weights are float16
- * hi / lo planes (w = hi + lo), index [tile][step][lane][8]: lane l holds
- * output 16 tile + l % 16 and 8 consecutive input channels at one tap, the
- * block of lane group g = l / 16: for 16 input channels (conv0 padded from
- * 14 with zero weights, and conv 16->32) combination c = 4 step + g, tap
- * c / 2 (taps 3 dy + dx; combinations 18, 19 are zero), channels 8 (c % 2)..;
- * for 32 input channels tap = step, channels 8 g..; for the 1x1 conv
- * channels 8 (4 step + g)...  Linear(1352,128) comes as float16 hi / lo
+ * Weights come in the kernel's operand order.  The 3x3 conv weights are
+ * float16 hi / lo planes (w = hi + lo), index [tile][step][lane][8]: lane l
+ * holds output 16 tile + l % 16 and 8 consecutive input channels at one
+ * tap, the block of lane group g = l / 16: for 16 input channels (conv0
+ * padded from 14 with zero weights, and conv 16->32) combination
+ * c = 4 step + g, tap c / 2 (taps 3 dy + dx; combinations 18, 19 are zero),
+ * channels 8 (c % 2)..; for 32 input channels tap = step, channels 8 g...
+ * The 1x1 conv is float16 hi / lo per block of 16 input channels (see
+ * c3w).  Linear(1352,128) comes as float16 hi / lo
  * planes [tile][43 steps][lane][8]: lane l holds output 16 tile + l % 16 and
  * inputs 32 step + 8 (l / 16) .. + 7 of the flattened [8][13][13] (inputs
  * 1352..1375 zero).  The other Linear weights are float32
  * [tile][step][lane], lane l holding output 16 tile + l % 16, input
- * 4 step + l / 16.  LayerNorm tables are packed [tile][13 rows][lane][4]
- * (value q of lane l in row y: channel 16 tile + 4 (l / 16) + q at position
- * (y, x = l % 16); zero for x >= 13 or past the channel count), 16-byte
- * aligned.  Two launches on `stream`: the trunk writes each item's
+ * 4 step + l / 16.  The 3x3 convs' LayerNorm tables are packed [tile][13
+ * rows][lane][4] (value q of lane l in row y: channel 16 tile + 4 (l / 16) +
+ * q at position (y, x = l % 16); zero for x >= 13 or past the channel
+ * count), 16-byte aligned; the 1x1 conv's are plain [8][13][13].  Two launches on `stream`: the trunk writes each item's
  * flattened features as float16 hi / lo rows into the workspace, the head
  * reads them; calls that overlap on one workspace race. */
 #define QQT_CNN_WS_BYTES_PER_ITEM 5504   /* workspace bytes per (row, player) item */
@@ -477,8 +478,10 @@ typedef struct qqt_cnn_args {
   const float *c1b, *ln1w, *ln1b;         /* [32]; LN [2][13][64][4] */
   const uint16_t *c2w, *c2w_lo;           /* conv 32->64 [4][9][64][8] */
   const float *c2b, *ln2w, *ln2b;         /* [64]; LN [4][13][64][4] */
-  const uint16_t *c3w, *c3w_lo;           /* 1x1 64->8 [1][2][64][8] (outputs 8..15 zero) */
-  const float *c3b, *ln3w, *ln3b;         /* [16] (8..15 zero); LN [1][13][64][4] */
+  const uint16_t *c3w, *c3w_lo;           /* 1x1 64->8 [4 input blocks][64][4]: value j of lane
+                                             l is W[l % 16][16 b + 4 (l / 16) + j] (rows 8..15
+                                             zero) */
+  const float *c3b, *ln3w, *ln3b;         /* [16] (8..15 zero); LN plain [8][13][13] */
   const uint16_t *s0h, *s0l;  /* Linear(1352,128) float16 hi / lo [8][43][64][8] (input
                                  index c * 169 + p of the flattened [8][13][13]) */
   const float* s0b;           /* [128] */

@@ -68,7 +68,7 @@ constexpr int T = 256, NW = 4;
 constexpr int HW = 13, NP = 169, MT = 13;    // position tiles = the 13 output rows
 constexpr int PW = 16;                      // padded row: x = -1 .. 14 (lane x of a row tile)
 constexpr int PP = 15 * PW + 2;             // padded positions (row tile 12's lane 15 reads 2 past)
-constexpr int CS = 72;                      // halves per position (64 channels + 8: bank spread)
+constexpr int CS = 40;                      // halves per position (32 channels + 8: bank spread)
 constexpr int C0 = 14;
 constexpr int HB = 32, HM = HB / 16;        // items per head workgroup, its 16-row M tiles
 constexpr int FLAT = 8 * NP;                // 1352
@@ -89,12 +89,17 @@ constexpr int BFRAG = 64 * 8;                       // halves of one step's B fr
 static_assert(WS_ROW * 2 == QQT_CNN_WS_BYTES_PER_ITEM, "workspace row size");
 
 struct __align__(16) Lds {                 // every member a multiple of 16 bytes long
-  uint16_t act[2][PP * CS];                 // hi, lo planes [position][channel]
+  union {
+    uint16_t act[2][PP * CS];               // hi, lo planes [position][channel]
+    float part[NW][MT][8][16];              // the 1x1 conv's partial sums [wave][row][out][x]
+  };
   float red[2][NW];
   int perm[2][16];                          // view permutations of the two item kinds
 };
 static_assert(sizeof(uint16_t) * 2 * PP * CS % 16 == 0, "16-byte fragment reads stay aligned");
-static_assert(2 * sizeof(Lds) <= 160 * 1024, "two trunk workgroups fit in one CU's LDS");
+static_assert(sizeof(float) * NW * MT * 8 * 16 <= sizeof(uint16_t) * 2 * PP * CS,
+              "the partial sums fit in the activation planes");
+static_assert(3 * sizeof(Lds) <= 160 * 1024, "three trunk workgroups fit in one CU's LDS");
 
 // the head's small weights, staged in LDS: biases, LayerNorm affines and
 // the output layer, at these offsets
@@ -145,6 +150,10 @@ __device__ __forceinline__ T* at(T* base, uint32_t byte_off) {
 
 __device__ __forceinline__ floatx4 mfma16(half8 a, half8 b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ floatx4 mfma16k16(half4 a, half4 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 struct BFrag { half8 hi, lo; };
 
@@ -197,7 +206,7 @@ __device__ __forceinline__ constexpr int tap_off(int tap) { return (tap / 3) * P
 template <int KIND, int STEPS, int NTL, bool ALO, class BF>
 __device__ __forceinline__ void conv(const uint16_t* act_hi, const uint16_t* act_lo, BF bfrag,
                                      floatx4 bias, int mt0, int ms, floatx4 (&acc)[NTL]) {
-  constexpr int CG = NTL > 8 ? (NTL + 1) / 2 : NTL;
+  constexpr int CG = NTL > 8 ? (NTL + 2) / 3 : NTL;
   const int lane = opaque_lane(), i16 = lane & 15, kq = lane >> 4;
   int base[NTL];
 #pragma unroll
@@ -218,7 +227,8 @@ __device__ __forceinline__ void conv(const uint16_t* act_hi, const uint16_t* act
       off = tap_off(st) * CS;
     else
       off = 32 * st;
-    // tiles in groups of at most 8, so that one group's A fragments are live
+    // tiles in groups (at most 8; 5 of the 13), so that one group's A
+    // fragments are live
 #pragma unroll
     for (int t0 = 0; t0 < NTL; t0 += CG) {
       half8 ah[CG], al[CG];
@@ -332,6 +342,43 @@ __device__ __forceinline__ void ln_write(const floatx4 (&acc)[NTL], int mt0, int
     }
 }
 
+// relu(LN affine) of conv 32->64's row tiles (this wavefront's 16 output
+// channels, all 13 rows) taken straight into the 1x1 conv 64->8: a lane's
+// four values (channels 4 kq .. + 3 of the block at position x) are the B
+// operand of v_mfma_f32_16x16x16_f16, the block's 8 x 16 slice of the 1x1
+// weights (w3h + w3l, rows 8..15 zero) the A operand, three products per
+// tile (hi*hi + lo*hi + hi*lo); the partial sums of outputs o < 8 go to
+// part[w][row][o][x] for the workgroup to add up.
+template <int NTL>
+__device__ __forceinline__ void ln_conv3(const floatx4 (&acc)[NTL], int ntile, float mean,
+                                         float rstd, const float* __restrict__ g,
+                                         const float* __restrict__ bt, half4 w3h, half4 w3l,
+                                         float* part) {
+  const int lane = opaque_lane(), x = lane & 15, kq = lane >> 4;
+  const uint32_t tl = (uint32_t)lane * 16u;
+#pragma unroll
+  for (int t = 0; t < NTL; ++t) {
+    const uint32_t gi = (uint32_t)(ntile * MT + t) * 1024u + tl;
+    const float4 gg = *at(reinterpret_cast<const float4*>(g), gi);
+    const float4 bb = *at(reinterpret_cast<const float4*>(bt), gi);
+    const float z[4] = {fmaf(acc[t][0] - mean, rstd * gg.x, bb.x),
+                        fmaf(acc[t][1] - mean, rstd * gg.y, bb.y),
+                        fmaf(acc[t][2] - mean, rstd * gg.z, bb.z),
+                        fmaf(acc[t][3] - mean, rstd * gg.w, bb.w)};
+    uint2 hi, lo;
+    relu_split4(z, hi, lo);
+    const half4 yh = __builtin_bit_cast(half4, hi), yl = __builtin_bit_cast(half4, lo);
+    floatx4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+    d = mfma16k16(w3h, yh, d);
+    d = mfma16k16(w3l, yh, d);
+    d = mfma16k16(w3h, yl, d);
+    if (kq < 2) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) part[(t * 8 + 4 * kq + q) * 16 + x] = d[q];
+    }
+  }
+}
+
 // A head layer's weight operands for tiles nt0 + i (i < NTW), W packed
 // [tile][step][lane] in global memory: loaded ahead of the GEMM.
 template <int STEPS, int NTW>
@@ -411,15 +458,16 @@ __device__ __forceinline__ void head_ln(float* h, int nb, const float* __restric
   }
 }
 
-__global__ __launch_bounds__(T, 2) void cnn_trunk_kernel(const qqt_cnn_args a, int items,
+__global__ __launch_bounds__(T, 3) void cnn_trunk_kernel(const qqt_cnn_args a, int items,
                                                           int per) {
   __shared__ Lds s;
   const int t = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int lane = t & 63, i16 = lane & 15;
 
-  // B operands of every conv from global memory step by step (L2 hits:
-  // 10, 20, 72 and 4 KB shared by every workgroup)
+  // B operands of the 3x3 convs from global memory step by step (L2 hits:
+  // 10, 20 and 72 KB shared by every workgroup); this wavefront's slice of
+  // the 1x1 conv (its 16 input channels) in registers
   const int n1 = w & 1, n2 = w;
   // biases of the four output channels 16 tile + 4 (lane / 16) .. + 3
   const int kq4 = 4 * (lane >> 4);
@@ -428,10 +476,11 @@ __global__ __launch_bounds__(T, 2) void cnn_trunk_kernel(const qqt_cnn_args a, i
     return floatx4{p[0], p[1], p[2], p[3]};
   };
   const floatx4 bias0 = bias4(a.c0b, 0), bias1 = bias4(a.c1b, n1), bias2 = bias4(a.c2b, n2);
-  const floatx4 bias3 = bias4(a.c3b, 0);
+  const half4 w3h = *at(reinterpret_cast<const half4*>(a.c3w), (uint32_t)(w * 64 + lane) * 8u);
+  const half4 w3l = *at(reinterpret_cast<const half4*>(a.c3w_lo), (uint32_t)(w * 64 + lane) * 8u);
 
-  // row tiles per wavefront: conv0 / conv3 {w + 4i}, i < 4; conv1
-  // {w/2 + 2i}, i < 7; conv2 all 13
+  // row tiles per wavefront: conv0 {w + 4i}, i < 4; conv1 {w/2 + 2i},
+  // i < 7; conv2 (and its 1x1 slice) all 13
   const int mt1 = w >> 1;
 
   for (int i = t; i < PP * CS; i += T) s.act[0][i] = s.act[1][i] = 0;
@@ -451,10 +500,6 @@ __global__ __launch_bounds__(T, 2) void cnn_trunk_kernel(const qqt_cnn_args a, i
   auto bglob0 = [&](int j) {
     const uint32_t o = lb + (uint32_t)j * (BFRAG * 2);
     return BFrag{ld8(at(a.c0w, o)), ld8(at(a.c0w_lo, o))};
-  };
-  auto bglob3 = [&](int j) {
-    const uint32_t o = lb + (uint32_t)j * (BFRAG * 2);
-    return BFrag{ld8(at(a.c3w, o)), ld8(at(a.c3w_lo, o))};
   };
 
   // Observation staging: thread t moves values i = t + 256 k (k < OBS_K) of
@@ -519,21 +564,54 @@ __global__ __launch_bounds__(T, 2) void cnn_trunk_kernel(const qqt_cnn_args a, i
     __syncthreads();
     {
       floatx4 acc[MT];
-      float4 gg[MT], bb[MT];
       conv<1, S2, MT, true>(s.act[0], s.act[1], breg2, bias2, 0, 1, acc);
-      ln_tables<MT>(0, 1, n2, a.ln2w, a.ln2b, gg, bb);
       ln_stats<MT>(acc, 0, 1, 4, s.red, rslot, 1.0f / (64 * NP), mean, rstd);
-      ln_write<MT>(acc, 0, 1, n2, 4, mean, rstd, gg, bb, s.act[0], s.act[1], nullptr);
+      // every wavefront is past its conv reads: the planes take the partials
+      ln_conv3<MT>(acc, n2, mean, rstd, a.ln2w, a.ln2b, w3h, w3l, &s.part[w][0][0][0]);
     }
     __syncthreads();
+    // 1x1 conv outputs (o < 8, 169 positions) = bias + the four partial
+    // sums; thread t takes slots t + 256 i = row * 128 + o * 16 + x (x < 13)
     {
-      floatx4 acc[4];
-      float4 gg[4], bb[4];
-      conv<2, S3, 4, true>(s.act[0], s.act[1], bglob3, bias3, w, 4, acc);
+      constexpr int NS = (MT * 128 + T - 1) / T;
+      const int tt = opaque_tid();
+      float v[NS];
+      float sum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        const int sl = min(tt + T * i, MT * 128 - 1), o = (sl >> 4) & 7, x = sl & 15;
+        const bool ok = tt + T * i < MT * 128 && x < HW;
+        const float* const pp = &s.part[0][0][0][0] + sl;
+        const float u = pp[0] + pp[MT * 128] + pp[2 * MT * 128] + pp[3 * MT * 128] + a.c3b[o];
+        v[i] = ok ? u : 0.0f;
+        sum += v[i];
+      }
+      mean = block_sum(sum, s.red, rslot) * (1.0f / FLAT);
+      // every thread is past its partial-sum reads: zero the bytes they
+      // occupied, the next item's padding and unused channel slots
+      for (int i = tt; i < (int)(sizeof(s.part) / 16); i += T)
+        reinterpret_cast<uint4*>(&s.part[0][0][0][0])[i] = uint4{0u, 0u, 0u, 0u};
+      float var = 0.0f;
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        const int sl = tt + T * i;
+        const float d = v[i] - mean;
+        if (sl < MT * 128 && (sl & 15) < HW) var = fmaf(d, d, var);
+      }
+      rstd = 1.0f / sqrtf(block_sum(var, s.red, rslot) * (1.0f / FLAT) + 1e-5f);
       uint16_t* const fl = a.workspace + (size_t)(item / HB) * HB * WS_ROW + (item % HB) * 32;
-      ln_tables<4>(w, 4, 0, a.ln3w, a.ln3b, gg, bb);
-      ln_stats<4>(acc, w, 4, 2, s.red, rslot, 1.0f / (8 * NP), mean, rstd);
-      ln_write<4>(acc, w, 4, 0, 2, mean, rstd, gg, bb, s.act[0], s.act[1], fl);
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        const int sl = tt + T * i, y = sl >> 7, o = (sl >> 4) & 7, x = sl & 15;
+        if (sl < MT * 128 && x < HW) {
+          const int k = o * NP + y * HW + x;              // flattened [8][13][13] index
+          const float z[4] = {fmaf(v[i] - mean, rstd * a.ln3w[k], a.ln3b[k]), 0.0f, 0.0f, 0.0f};
+          uint2 hi, lo;
+          relu_split4(z, hi, lo);
+          *at(fl, (uint32_t)ws_off(0, k) * 2u) = (uint16_t)hi.x;
+          *at(fl, (uint32_t)ws_off(1, k) * 2u) = (uint16_t)lo.x;
+        }
+      }
       if (t < KF - FLAT) fl[ws_off(0, FLAT + t)] = fl[ws_off(1, FLAT + t)] = 0;
     }
   }
@@ -766,7 +844,7 @@ int qqt_cnn_act(const qqt_cnn_args* a, void* stream) {
              "(items rounded up to %d)", QQT_CNN_WS_BYTES_PER_ITEM, HB);
     return QQT_E_ARG;
   }
-  const int grid = min(2 * cu_count(), items);
+  const int grid = min(3 * cu_count(), items);     // three resident workgroups per CU
   const int per = (items + grid - 1) / grid;
   hipStream_t st = (hipStream_t)stream;
   QQT_LAUNCH(QQT_KERNEL_CNN, cnn_trunk_kernel, dim3(grid), dim3(T), st, *a, items, per);

@@ -488,6 +488,17 @@ def _pack_ln(g: torch.Tensor, n_tiles: int) -> torch.Tensor:
     return x.permute(0, 3, 1, 4, 2).reshape(-1).contiguous()
 
 
+def _conv3_frag(w: torch.Tensor) -> torch.Tensor:
+    """1x1 conv weight [8][64][1][1] -> [block][lane][4]: value j of lane l in
+    input block b is W[o = l % 16][c = 16 b + 4 (l // 16) + j] (zero for
+    o >= 8), the A operand of v_mfma_f32_16x16x16_f16 for each block of 16
+    input channels."""
+    wk = torch.zeros((16, 64), dtype=torch.float32)
+    wk[:8] = w.float().reshape(8, 64)
+    x = wk.view(16, 4, 4, 4)                                  # [o][block][kq][j]
+    return x.permute(1, 2, 0, 3).reshape(-1).contiguous()
+
+
 CNN_FLAT_PAD = 1376            # flattened trunk features padded to 43 K steps of 32
 CNN_WS_BYTES_PER_ITEM = 5504   # QQT_CNN_WS_BYTES_PER_ITEM
 
@@ -525,7 +536,7 @@ def pack_cnn(params: dict, n_players: int = 2, obs_shape=(14, 13, 13)) -> dict:
         c2b=f("conv.5.bias"),
         ln2w=_pack_ln(f("conv.6.weight"), 4), ln2b=_pack_ln(f("conv.6.bias"), 4),
         c3b=c3b,
-        ln3w=_pack_ln(f("conv.9.weight"), 1), ln3b=_pack_ln(f("conv.9.bias"), 1),
+        ln3w=f("conv.9.weight").reshape(-1), ln3b=f("conv.9.bias").reshape(-1),
         s0b=f("shared.0.bias"),
         s1w=f("shared.1.weight"), s1b=f("shared.1.bias"),
         s3p=_pack_linear(f("shared.3.weight")), s3b=f("shared.3.bias"),
@@ -534,10 +545,12 @@ def pack_cnn(params: dict, n_players: int = 2, obs_shape=(14, 13, 13)) -> dict:
         hb=torch.cat([f(f"{n}.0.bias") for n in heads]),
         fw=fw, fb=torch.cat([f(f"{n}.2.bias") for n in heads]))
     for key, src, nt in (("c0w", "conv0.weight", 1), ("c1w", "conv.2.weight", 2),
-                         ("c2w", "conv.5.weight", 4), ("c3w", "conv.8.weight", 1)):
+                         ("c2w", "conv.5.weight", 4)):
         out[key], out[key + "_lo"] = _split16(_conv_operand(f(src), nt))
+    out["c3w"], out["c3w_lo"] = _split16(_conv3_frag(f("conv.8.weight")))
     out["s0h"], out["s0l"] = _frag16_planes(f("shared.0.weight"), CNN_FLAT_PAD)
-    expect = dict(c0w=5 * 64 * 8, c1w=2 * 5 * 64 * 8, c2w=4 * 9 * 64 * 8, c3w=2 * 64 * 8,
+    expect = dict(c0w=5 * 64 * 8, c1w=2 * 5 * 64 * 8, c2w=4 * 9 * 64 * 8, c3w=4 * 64 * 4,
+                  ln3w=8 * 169,
                   s0h=8 * 43 * 64 * 8, s3p=8 * 32 * 64, hp=12 * 32 * 64, ln2w=4 * 13 * 64 * 4)
     for k, numel in expect.items():
         if out[k].numel() != numel:

@@ -286,8 +286,7 @@ def test_pack_cnn_operands_reproduce_the_reference_layers():
             params["conv0.bias"].double()[:, None, None]
         torch.testing.assert_close(got, want, rtol=1e-12, atol=1e-12)
     for key, src, bk, cin, nt, steps, kind in (("c1w", "conv.2.weight", "conv.2.bias", 16, 2, 5, 0),
-                                               ("c2w", "conv.5.weight", "conv.5.bias", 32, 4, 9, 1),
-                                               ("c3w", "conv.8.weight", "conv.8.bias", 64, 1, 2, 2)):
+                                               ("c2w", "conv.5.weight", "conv.5.bias", 32, 4, 9, 1)):
         x = torch.rand((cin, 13, 13), generator=g, dtype=torch.float64)
         wd = dense(key, src, nt, steps, kind)
         want = F.conv2d(x[None], wd, params[bk].double(), padding=wd.shape[-1] // 2)[0]
@@ -311,8 +310,15 @@ def test_pack_cnn_operands_reproduce_the_reference_layers():
     assert float(ln[2, 12, 3, 12, 0]) == float(gam[32 + 12, 12, 12])
     assert float(ln[0, 10, 3, 13, 1]) == 0.0                     # x = 13 is past the row
     assert torch.equal(ln.permute(0, 2, 4, 1, 3).reshape(64, 13, 16)[:, :, :13], gam)
-    ln3 = pk["ln3w"].view(1, 13, 4, 16, 4)
-    assert float(ln3[0, 0, 2:].abs().max()) == 0.0               # channels 8..15 are zero
+    assert torch.equal(pk["ln3w"], params["conv.9.weight"].reshape(-1))   # plain [8][13][13]
+    # the 1x1 conv as per-block A operands [block][kq * 16 + o][j] = W[o][16 block + 4 kq + j]
+    w3 = params["conv.8.weight"].reshape(8, 64).double()
+    f3 = (pk["c3w"].double() + pk["c3w_lo"].double()).view(4, 4, 16, 4)
+    back = f3.permute(2, 0, 1, 3).reshape(16, 64)
+    assert float(back[8:].abs().max()) == 0.0
+    assert bool(((back[:8] - w3).abs() <= 2.0 ** -22 * w3.abs() + 2.0 ** -24).all())
+    assert float(pk["c3w"][(2 * 64 + 16 * 3 + 5) * 4 + 2]) == \
+        float(params["conv.8.weight"][5, 16 * 2 + 4 * 3 + 2].half())
     assert torch.equal(pk["fw"][5:7], params["bomb_head.2.weight"])
     assert sum(v.numel() for v in params.values()) == 281744
 
