@@ -502,35 +502,35 @@ __global__ __launch_bounds__(T, 3) void cnn_trunk_kernel(const qqt_cnn_args a, i
     return BFrag{ld8(at(a.c0w, o)), ld8(at(a.c0w_lo, o))};
   };
 
-  // Observation staging: thread t moves values i = t + 256 k (k < OBS_K) of
-  // the item's 14 x 169 input planes (plane c = i / 169 is observation
-  // channel view_perm[pid][c]); the next item's values are loaded into
-  // registers while this item computes.  Threads past the 2366 values load
-  // a valid value and write nothing.
-  constexpr int OBS_K = (C0 * NP + T - 1) / T;
+  // Observation staging: thread t < 169 moves position p = t of the item's
+  // 14 input planes (plane c is observation channel view_perm[pid][c]): the
+  // next item's 14 values are loaded into registers while this item
+  // computes, and leave as three 8-byte and one 4-byte LDS store (channels
+  // contiguous at the position).  Threads past 169 load position 168 and
+  // store nothing.
   if (t < 2 * C0) {
     const int kind = t / C0;
     const int pid = a.npid == 2 ? kind : a.pid0;
     s.perm[kind][t % C0] = a.view_perm[pid * C0 + t % C0];
   }
   __syncthreads();
-  uint16_t ov[OBS_K];
+  uint32_t ov[C0];
   auto fetch = [&](int item) {
     const int row = item / a.npid, kind = a.npid == 2 ? (item & 1) : 0;
     const uint16_t* const ob = a.obs + (size_t)row * a.obs_stride;
-    const int tt = opaque_tid();
+    const int pt = min(opaque_tid(), NP - 1);
 #pragma unroll
-    for (int k = 0; k < OBS_K; ++k) {
-      const int i = min(tt + T * k, C0 * NP - 1), c = i / NP;
-      ov[k] = *at(ob, (uint32_t)(s.perm[kind][c] * NP + (i - c * NP)) * 2u);
-    }
+    for (int c = 0; c < C0; ++c) ov[c] = *at(ob, (uint32_t)(s.perm[kind][c] * NP + pt) * 2u);
   };
   auto stage = [&]() {
-    const int tt = opaque_tid();
-#pragma unroll
-    for (int k = 0; k < OBS_K; ++k) {
-      const int i = tt + T * k, c = i / NP, p = i - c * NP, y = p / HW;
-      if (i < C0 * NP) s.act[0][((y + 1) * PW + (p - y * HW) + 1) * CS + c] = ov[k];
+    const int pt = opaque_tid();
+    if (pt < NP) {
+      const int y = pt / HW;
+      uint16_t* const d = &s.act[0][((y + 1) * PW + (pt - y * HW) + 1) * CS];
+      *reinterpret_cast<uint2*>(d) = uint2{ov[0] | ov[1] << 16, ov[2] | ov[3] << 16};
+      *reinterpret_cast<uint2*>(d + 4) = uint2{ov[4] | ov[5] << 16, ov[6] | ov[7] << 16};
+      *reinterpret_cast<uint2*>(d + 8) = uint2{ov[8] | ov[9] << 16, ov[10] | ov[11] << 16};
+      *reinterpret_cast<uint32_t*>(d + 12) = ov[12] | ov[13] << 16;
     }
   };
 
