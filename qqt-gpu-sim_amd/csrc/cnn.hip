@@ -256,9 +256,10 @@ __device__ __forceinline__ void conv(const uint16_t* act_hi, const uint16_t* act
 }
 
 // LayerNorm statistics over the valid outputs of a layer (lane x < 13,
-// channel group kq < cq, row tile < 13).
+// channel group kq < cq, row tile < 13); the accumulators are left centred
+// (acc - mean).
 template <int NTL>
-__device__ __forceinline__ void ln_stats(const floatx4 (&acc)[NTL], int mt0, int ms, int cq,
+__device__ __forceinline__ void ln_stats(floatx4 (&acc)[NTL], int mt0, int ms, int cq,
                                          float (*red)[NW], int& slot, float inv_count,
                                          float& mean, float& rstd) {
   const int lane = opaque_lane();
@@ -277,8 +278,8 @@ __device__ __forceinline__ void ln_stats(const floatx4 (&acc)[NTL], int mt0, int
     if (mt0 + t * ms < MT) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const float d = acc[t][q] - mean;
-        v = fmaf(d, d, v);
+        acc[t][q] -= mean;                         // left centred for the write
+        v = fmaf(acc[t][q], acc[t][q], v);
       }
     }
   rstd = 1.0f / sqrtf(block_sum(on ? v : 0.0f, red, slot) * inv_count + 1e-5f);
@@ -301,14 +302,14 @@ __device__ __forceinline__ void ln_tables(int mt0, int ms, int ntile,
   }
 }
 
-// relu(LN affine) of this wavefront's outputs (lanes x < 13, channel groups
-// kq < cq; saturated at 65504): a lane's four values are four consecutive
+// relu(LN affine) of this wavefront's centred outputs (lanes x < 13,
+// channel groups kq < cq; saturated at 65504): a lane's four values are four consecutive
 // channels of one position, one 8-byte store per plane into the activation
 // planes, or (fl != nullptr) into the item's workspace block (value
 // n * 169 + p of each plane, ws_off).
 template <int NTL>
 __device__ __forceinline__ void ln_write(const floatx4 (&acc)[NTL], int mt0, int ms, int ntile,
-                                         int cq, float mean, float rstd,
+                                         int cq, float rstd,
                                          const float4 (&gg)[NTL], const float4 (&bb)[NTL],
                                          uint16_t* act_hi, uint16_t* act_lo, uint16_t* fl) {
   const int lane = opaque_lane(), x = lane & 15, kq = lane >> 4;
@@ -322,7 +323,7 @@ __device__ __forceinline__ void ln_write(const floatx4 (&acc)[NTL], int mt0, int
       const float bv[4] = {bb[t].x, bb[t].y, bb[t].z, bb[t].w};
       float z[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) z[q] = fmaf(acc[t][q] - mean, rstd * gv[q], bv[q]);
+      for (int q = 0; q < 4; ++q) z[q] = fmaf(acc[t][q], rstd * gv[q], bv[q]);
       uint2 hi, lo;
       relu_split4(z, hi, lo);
       if (fl) {
@@ -350,8 +351,7 @@ __device__ __forceinline__ void ln_write(const floatx4 (&acc)[NTL], int mt0, int
 // tile (hi*hi + lo*hi + hi*lo); the partial sums of outputs o < 8 go to
 // part[w][row][o][x] for the workgroup to add up.
 template <int NTL>
-__device__ __forceinline__ void ln_conv3(const floatx4 (&acc)[NTL], int ntile, float mean,
-                                         float rstd, const float* __restrict__ g,
+__device__ __forceinline__ void ln_conv3(const floatx4 (&acc)[NTL], int ntile, float rstd, const float* __restrict__ g,
                                          const float* __restrict__ bt, half4 w3h, half4 w3l,
                                          float* part) {
   const int lane = opaque_lane(), x = lane & 15, kq = lane >> 4;
@@ -361,10 +361,8 @@ __device__ __forceinline__ void ln_conv3(const floatx4 (&acc)[NTL], int ntile, f
     const uint32_t gi = (uint32_t)(ntile * MT + t) * 1024u + tl;
     const float4 gg = *at(reinterpret_cast<const float4*>(g), gi);
     const float4 bb = *at(reinterpret_cast<const float4*>(bt), gi);
-    const float z[4] = {fmaf(acc[t][0] - mean, rstd * gg.x, bb.x),
-                        fmaf(acc[t][1] - mean, rstd * gg.y, bb.y),
-                        fmaf(acc[t][2] - mean, rstd * gg.z, bb.z),
-                        fmaf(acc[t][3] - mean, rstd * gg.w, bb.w)};
+    const float z[4] = {fmaf(acc[t][0], rstd * gg.x, bb.x), fmaf(acc[t][1], rstd * gg.y, bb.y),
+                        fmaf(acc[t][2], rstd * gg.z, bb.z), fmaf(acc[t][3], rstd * gg.w, bb.w)};
     uint2 hi, lo;
     relu_split4(z, hi, lo);
     const half4 yh = __builtin_bit_cast(half4, hi), yl = __builtin_bit_cast(half4, lo);
@@ -550,7 +548,7 @@ __global__ __launch_bounds__(T, 3) void cnn_trunk_kernel(const qqt_cnn_args a, i
       conv<0, S0, 4, false>(s.act[0], s.act[1], bglob0, bias0, w, 4, acc);
       ln_tables<4>(w, 4, 0, a.ln0w, a.ln0b, gg, bb);
       ln_stats<4>(acc, w, 4, 4, s.red, rslot, 1.0f / (16 * NP), mean, rstd);
-      ln_write<4>(acc, w, 4, 0, 4, mean, rstd, gg, bb, s.act[0], s.act[1], nullptr);
+      ln_write<4>(acc, w, 4, 0, 4, rstd, gg, bb, s.act[0], s.act[1], nullptr);
     }
     __syncthreads();
     {
@@ -559,7 +557,7 @@ __global__ __launch_bounds__(T, 3) void cnn_trunk_kernel(const qqt_cnn_args a, i
       conv<0, S1, 7, true>(s.act[0], s.act[1], breg1, bias1, mt1, 2, acc);
       ln_tables<7>(mt1, 2, n1, a.ln1w, a.ln1b, gg, bb);
       ln_stats<7>(acc, mt1, 2, 4, s.red, rslot, 1.0f / (32 * NP), mean, rstd);
-      ln_write<7>(acc, mt1, 2, n1, 4, mean, rstd, gg, bb, s.act[0], s.act[1], nullptr);
+      ln_write<7>(acc, mt1, 2, n1, 4, rstd, gg, bb, s.act[0], s.act[1], nullptr);
     }
     __syncthreads();
     {
@@ -567,7 +565,7 @@ __global__ __launch_bounds__(T, 3) void cnn_trunk_kernel(const qqt_cnn_args a, i
       conv<1, S2, MT, true>(s.act[0], s.act[1], breg2, bias2, 0, 1, acc);
       ln_stats<MT>(acc, 0, 1, 4, s.red, rslot, 1.0f / (64 * NP), mean, rstd);
       // every wavefront is past its conv reads: the planes take the partials
-      ln_conv3<MT>(acc, n2, mean, rstd, a.ln2w, a.ln2b, w3h, w3l, &s.part[w][0][0][0]);
+      ln_conv3<MT>(acc, n2, rstd, a.ln2w, a.ln2b, w3h, w3l, &s.part[w][0][0][0]);
     }
     __syncthreads();
     // 1x1 conv outputs (o < 8, 169 positions) = bias + the four partial
@@ -582,7 +580,8 @@ __global__ __launch_bounds__(T, 3) void cnn_trunk_kernel(const qqt_cnn_args a, i
         const int sl = min(tt + T * i, MT * 128 - 1), o = (sl >> 4) & 7, x = sl & 15;
         const bool ok = tt + T * i < MT * 128 && x < HW;
         const float* const pp = &s.part[0][0][0][0] + sl;
-        const float u = pp[0] + pp[MT * 128] + pp[2 * MT * 128] + pp[3 * MT * 128] + a.c3b[o];
+        const float u = pp[0] + pp[MT * 128] + pp[2 * MT * 128] + pp[3 * MT * 128] +
+                        *at(a.c3b, (uint32_t)o * 4u);
         v[i] = ok ? u : 0.0f;
         sum += v[i];
       }
@@ -605,11 +604,12 @@ __global__ __launch_bounds__(T, 3) void cnn_trunk_kernel(const qqt_cnn_args a, i
         const int sl = tt + T * i, y = sl >> 7, o = (sl >> 4) & 7, x = sl & 15;
         if (sl < MT * 128 && x < HW) {
           const int k = o * NP + y * HW + x;              // flattened [8][13][13] index
-          const float z[4] = {fmaf(v[i] - mean, rstd * a.ln3w[k], a.ln3b[k]), 0.0f, 0.0f, 0.0f};
-          uint2 hi, lo;
-          relu_split4(z, hi, lo);
-          *at(fl, (uint32_t)ws_off(0, k) * 2u) = (uint16_t)hi.x;
-          *at(fl, (uint32_t)ws_off(1, k) * 2u) = (uint16_t)lo.x;
+          const float y = __builtin_amdgcn_fmed3f(
+              fmaf(v[i] - mean, rstd * *at(a.ln3w, (uint32_t)k * 4u), *at(a.ln3b, (uint32_t)k * 4u)),
+              0.0f, 65504.0f);
+          const _Float16 hi = (_Float16)y, lo = (_Float16)(y - (float)hi);
+          *at(fl, (uint32_t)ws_off(0, k) * 2u) = __builtin_bit_cast(uint16_t, hi);
+          *at(fl, (uint32_t)ws_off(1, k) * 2u) = __builtin_bit_cast(uint16_t, lo);
         }
       }
       if (t < KF - FLAT) fl[ws_off(0, FLAT + t)] = fl[ws_off(1, FLAT + t)] = 0;
