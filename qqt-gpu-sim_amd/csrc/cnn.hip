@@ -9,43 +9,38 @@
 // heads 128 -> 64 -> ReLU -> 5 | 2 | 1.  Every LayerNorm normalises one
 // sample over all of its values (eps 1e-5) with an elementwise affine.
 //
-// Two kernels.  cnn_trunk_kernel: persistent, two workgroups of 4
-// wavefronts per CU (one wavefront per SIMD each, 256 registers), each
-// walking a contiguous range of items (row, player) one item at a time, so
-// one workgroup's barriers and LayerNorm reductions overlap the other's
-// convolutions.  cnn_head_kernel: 32 items per workgroup, from the trunk's
-// flattened features in the workspace.
+// Two kernels.  cnn_trunk_kernel: persistent, three workgroups of 4
+// wavefronts per CU (one wavefront per SIMD each, at most 168 registers),
+// each walking a contiguous range of items (row, player) one item at a
+// time, so the workgroups' LayerNorm phases and convolutions overlap.
+// cnn_head_kernel: 32 items per workgroup, from the trunk's flattened
+// features in the workspace.
 //
-// Trunk.  Feature maps live in LDS as zero-bordered 15 x 15 grids of
-// positions with the channels of a position contiguous (72 halves per
-// position), as float16 hi and lo planes (x = hi + lo).  Convolutions are
-// implicit GEMMs on v_mfma_f32_16x16x32_f16 with float32 accumulation: M =
-// positions (11 tiles of 16), N = output channels, K in steps of 32 = four
-// 8-channel blocks, so lane l's A operand (8 halves) is one 16-byte LDS read
-// of 8 channels at one position and tap:
+// Trunk.  Feature maps live in LDS as float16 hi and lo planes (x = hi +
+// lo) on a zero-bordered grid 16 positions wide (x = -1 .. 14) with the 32
+// channels of a position contiguous (40 halves per position).  The 3x3
+// convs are implicit GEMMs on v_mfma_f32_16x16x32_f16 with float32
+// accumulation: M = one output row (lane x = position; x >= 13 computed
+// from the padding and ignored), N = output channels, K in steps of 32 =
+// four 8-channel blocks, so lane l's A operand (8 halves) is one 16-byte LDS
+// read of 8 channels at one position and tap, 16 lanes at consecutive
+// positions:
 //   16 input channels (conv0, conv 16->32): step s, lane group g = l / 16
 //     takes combination c = 4 s + g: tap min(c / 2, 8), channels 8 (c % 2)..;
 //     combinations 18, 19 carry zero weights;
-//   32 input channels (conv 32->64): step s = tap, channels 8 g..;
-//   64 input channels (1x1): step s, channels 8 (4 s + g)...
-// Each product is hi*hi + hi*lo + lo*hi of the activation and weight
-// planes (the observation is exact in float16, so conv0 skips its lo
-// plane), which keeps the layer outputs within ~1e-6 relative of float32.
-// The B operands of the 16->32 and 32->64 convs stay in registers for the
-// whole kernel (wavefront w owns output tile w % NT of each); those of conv0
-// and the 1x1 conv (one output tile, used by every wavefront) sit in LDS; all
-// are packed on the host as [tile][step][lane][8] halves.  The accumulators
-// are the layer's output: the per-sample LayerNorm reduces them across the
-// workgroup (mean, then squared deviations) and the rectified, normalised
-// values are written over the input planes as hi/lo halves (after the last
-// conv, into this item's workspace row: 1376 hi halves, then 1376 lo, the
-// flattened index c * 169 + p, zero from 1352).
-// Head: Linear(1352,128) on the same float16 MFMA with the three hi/lo
-// products (K = 43 steps of 32), then Linear(128,128) and the heads' hidden
-// layer as v_mfma_f32_16x16x4_f32 GEMMs with M = the 32 items,
-// LayerNorm(128) by 16 threads per item, the output layer and the masked
-// sampling per item.
-
+//   32 input channels (conv 32->64): step s = tap, channels 8 g...
+// Each product is hi*hi + hi*lo + lo*hi of the weight and activation planes
+// (the observation is exact in float16, so conv0 skips its lo plane), which
+// keeps the layer outputs within ~1e-6 relative of float32.  Products are
+// taken as weights x activations, so a lane's accumulators are four
+// consecutive channels of one position.  B operands come from L2 two K
+// steps ahead (packed on the host as [tile][step][lane][8] halves).  The
+// per-sample LayerNorm reduces the accumulators across the workgroup (mean,
+// then squared deviations) and the rectified, normalised values are written
+// over the input planes as hi/lo halves; after conv 32->64 they feed the
+// 1x1 conv 64 -> 8 directly (v_mfma_f32_16x16x16_f16 per wavefront's
+// 16-channel slice, partial sums added in LDS), whose LayerNorm output goes
+// into this item's workspace rows (flattened index c * 169 + p).
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <math.h>
