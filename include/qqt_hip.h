@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QQT_ABI_VERSION 24
+#define QQT_ABI_VERSION 25
 
 #define QQT_OK 0
 #define QQT_E_ARG (-1)      /* bad argument (shape, null pointer, range) */
@@ -262,6 +262,16 @@ typedef struct qqt_bot_args {
                                  16], 16-byte aligned, zero past the tick's entries */
   int64_t* actions;           /* [N][P][2], slot pid written; or NULL */
   int8_t* actions_i8;         /* same as int8; or NULL */
+  int8_t* mode;               /* [N] behaviour mode per env, 0 approach / 1 flee
+                                 (sim/bots.py:433-443, 496-503), or NULL = always
+                                 approach (make_bot(..., mode=False)) */
+  int32_t* mode_timer;        /* [N] countdown of the mode ticker (sim/bots.py:241-264) */
+  uint32_t mode_tick;         /* this call's ticker count (1, 2, ...): every timer
+                                 counts down by one and, on multiples of 16, envs at
+                                 or below 0 draw a new mode (probability 1/2 each)
+                                 and timer (60 .. 239) from Philox stream 9 (counter
+                                 env, mode_tick); 0 = modes as given, no ticker step */
+  int32_t reserved;
 } qqt_bot_args;
 
 /* ABI version (QQT_ABI_VERSION). */

@@ -1,9 +1,11 @@
 """The astar bot (restates sim/bots.py:179-238 and :267-508).  TEST
 INFRASTRUCTURE ONLY (see the package docstring).
 
-`astar_act` is `astar_attack(sim, obs, mmask, bmask, pid)` with behaviour
-modes off (no `_bmode` on the sim) and `eat_crates=False`, the configuration
-the learner-vs-bot workload uses.  Differences, shared with the HIP kernel:
+`astar_act` is `astar_attack(sim, obs, mmask, bmask, pid)` with
+`eat_crates=False`, behaviour modes off (no `_bmode` on the sim, the
+configuration the learner-vs-bot workload uses) or given per env (`mode`,
+the flee branch of sim/bots.py:433-443 and :496-503); `mode_tick` is the
+mode ticker (:241-264).  Differences, shared with the HIP kernel:
 
 * the 0.05-scaled noise comes in as injected uniforms `u` (N, 5) instead of
   `torch.rand(n, 5)` (sim/bots.py:355): noise = 0.05 * u;
@@ -52,13 +54,35 @@ def cost_field(sources, danger, blocked, lam: float = 2.0, max_passes=None):
     return dist
 
 
-def astar_act(cfg, st, obs, mmask, bmask, pid: int, u, reach=None):
+def mode_tick(mode, timer, count: int, seed: int):
+    """One step of the astar bot's approach / flee mode ticker (sim/bots.py:
+    241-264, `_mode_ticker`) for its call number `count` (1, 2, ...): every
+    env's timer counts down by one, and on calls with count % 16 == 0 the
+    envs whose timer is at or below 0 draw a new mode (0 approach, 1 flee,
+    probability 1/2 each) and a new timer uniform on 60 .. 239.  The draws are
+    Philox stream 9 (key seed, counter (env, count)): the reference's laws,
+    not its torch draws.  Returns the new (mode, timer)."""
+    from .philox import STREAM_BOT_MODE, uniforms
+
+    timer = timer - 1
+    if count % 16 == 0:
+        sw = timer <= 0
+        u = torch.from_numpy(uniforms(seed, range(mode.shape[0]), count, STREAM_BOT_MODE, 2))
+        new_mode = (u[:, 0] >= 0.5).to(mode.dtype)
+        new_timer = (60 + (u[:, 1] * 180.0).long().clamp(max=179)).to(timer.dtype)
+        mode = torch.where(sw, new_mode, mode)
+        timer = torch.where(sw, new_timer, timer)
+    return mode, timer
+
+
+def astar_act(cfg, st, obs, mmask, bmask, pid: int, u, reach=None, mode=None):
     """(N, 2) int64 [move, place] of the astar bot for player `pid`.
 
     st: dict of reference-layout state tensors (wall, brick, fuse, owner, pos,
     alive, blast_cap); obs: (N, C, H, W) observation (danger is channel
     2P+1, read back from float16); mmask/bmask: (N, 5)/(N, 2) bool legality of
-    `pid`; u: (N, 5) float32 uniforms."""
+    `pid`; u: (N, 5) float32 uniforms; mode: (N,) behaviour mode per env (0
+    approach, 1 flee; None = always approach, `make_bot(..., mode=False)`)."""
     n = obs.shape[0]
     p, h, w = cfg.n_players, cfg.height, cfg.width
     wall, brick = st["wall"].bool(), st["brick"].bool()
@@ -114,6 +138,14 @@ def astar_act(cfg, st, obs, mmask, bmask, pid: int, u, reach=None):
     esc = torch.where(use_esc.unsqueeze(1) & (k5 == 4), inf, esc)
     esc = torch.where(legal, esc, inf)
     score = torch.where(use_esc.unsqueeze(1), esc, app)
+    if mode is not None:
+        # flee (sim/bots.py:433-443): away from the opponent (V_opp clamped
+        # at 1e3), avoiding danger; escape first when escaping
+        flee = -vopp_c.clamp(max=1e3) + 2.0 * dng_c + 2.0 * thr_c + noise
+        flee = torch.where(dng_c >= 0.5, inf, flee)
+        flee = torch.where(legal, flee, inf)
+        flee = torch.where(use_esc.unsqueeze(1), esc, flee)
+        score = torch.where((mode == 1).unsqueeze(1), flee, score)
     move = score.argmin(dim=1).long()
 
     any_legal = legal.any(dim=1)
@@ -147,6 +179,11 @@ def astar_act(cfg, st, obs, mmask, bmask, pid: int, u, reach=None):
     can_escape = (legal & (dng_c < 0.35) & ~thr_c.bool()).any(dim=1)
     place = (bmask[:, 1].bool() & (aligned | near | chain) & (own_dng < 0.2)
              & can_escape).long()
+    if mode is not None:
+        # flee places only on an opponent in reach, never for a chain (:496-503)
+        flee_place = (bmask[:, 1].bool() & (aligned | near) & (own_dng < 0.2)
+                      & can_escape).long()
+        place = torch.where(mode == 1, flee_place, place)
 
     dead = ~alive[:, pid]
     move = torch.where(dead, torch.full_like(move, 4), move)

@@ -27,6 +27,7 @@ STREAM_RANDOM_ACT = 5  # per tick: uniform-legal random actions
 STREAM_INJECT_ACT = 6  # per tick: unmasked injected actions
 STREAM_BOT = 7        # per tick: rule-bot noise
 STREAM_RECYCLE = 8    # per flush: one key per (player, cell) for recycle crates
+STREAM_BOT_MODE = 9   # per switch of the astar bot's mode: (u_mode, u_timer) per env
 
 
 def philox4x32(c0, c1, c2, c3, k0, k1, rounds: int = 10):

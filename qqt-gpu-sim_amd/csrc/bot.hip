@@ -297,22 +297,41 @@ __global__ __launch_bounds__(64 * WPB) void bot_kernel(const qqt_sim_config cf, 
   const float noise_k = 0.05f * s.u[kk];
   const float dng_k = s.dng[ck];
   float ap_k = ((s.vo[ck] + 2.0f * dng_k) + 2.0f * thf_k) + noise_k;
-  if (dng_k >= 0.5f || !legal_k) ap_k = INF;
+  // flee (mode 1): away from the opponent, V_opp clamped at 1e3
+  float fl_k = ((-fminf(s.vo[ck], 1e3f) + 2.0f * dng_k) + 2.0f * thf_k) + noise_k;
+  if (dng_k >= 0.5f || !legal_k) ap_k = fl_k = INF;
   const float esc_k = ((s.vs[ck] * 100.0f) + 2.0f * thf_k) + noise_k;
   const int flags_k = (legal_k ? 1 : 0) | (thr_k ? 2 : 0);
-  float app[5], esc[5], dngc[5];
+  float app[5], esc[5], dngc[5], flee[5];
   bool legal[5], thr[5];
 #pragma unroll
   for (int k = 0; k < 5; ++k) {
     app[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ap_k), k));
     esc[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(esc_k), k));
     dngc[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dng_k), k));
+    flee[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fl_k), k));
     const int f = __builtin_amdgcn_readlane(flags_k, k);
     legal[k] = (f & 1) != 0;
     thr[k] = (f & 2) != 0;
   }
 
   if (lane == 0) {
+    // behaviour mode of this env, after this call's ticker step
+    int md = 0;
+    if (a.mode) {
+      md = a.mode[g];
+      if (a.mode_tick != 0u) {
+        int tmr = a.mode_timer[g] - 1;
+        if ((a.mode_tick & 15u) == 0u && tmr <= 0) {
+          float u4[4];
+          philox_block(a.seed, (uint32_t)g, a.mode_tick, STREAM_BOT_MODE, 0u, u4);
+          md = u4[0] >= 0.5f ? 1 : 0;
+          tmr = 60 + min((int)(u4[1] * 180.0f), 179);
+          a.mode[g] = (int8_t)md;
+        }
+        a.mode_timer[g] = tmr;
+      }
+    }
     const uint8_t* bm = s.bm;
     const float own_dng = s.dng[r * W + c];
     bool app_ok = false;
@@ -324,7 +343,7 @@ __global__ __launch_bounds__(64 * WPB) void bot_kernel(const qqt_sim_config cf, 
     for (int k = 0; k < 5; ++k) {
       float e = esc[k];
       if ((use_esc && k == 4) || !legal[k]) e = INF;
-      score[k] = use_esc ? e : app[k];
+      score[k] = use_esc ? e : md == 1 ? flee[k] : app[k];
     }
     // argmin with the first index winning ties (all-inf -> 0)
     int move = 0;
@@ -368,7 +387,9 @@ __global__ __launch_bounds__(64 * WPB) void bot_kernel(const qqt_sim_config cf, 
     bool can_escape = false;
 #pragma unroll
     for (int k = 0; k < 5; ++k) can_escape |= legal[k] && dngc[k] < 0.35f && !thr[k];
-    int place = (bm[1] != 0 && (aligned || near || chain) && own_dng < 0.2f && can_escape) ? 1 : 0;
+    // a fleeing bot places only on an opponent in reach, never for a chain
+    int place = (bm[1] != 0 && (aligned || near || (chain && md != 1)) && own_dng < 0.2f &&
+                 can_escape) ? 1 : 0;
     if (!alive) {
       move = 4;
       place = 0;
@@ -452,6 +473,10 @@ int qqt_bot_act(const qqt_sim_config* cfg, const qqt_bot_args* a, void* stream) 
   if (a->pid < 0 || a->pid >= cfg->n_players || cfg->growth_blast_max < 0 ||
       cfg->growth_blast_max > 64) {
     snprintf(g_err, sizeof(g_err), "qqt_bot_act: bad player id or dilation count");
+    return QQT_E_ARG;
+  }
+  if (a->mode && a->mode_tick != 0u && !a->mode_timer) {
+    snprintf(g_err, sizeof(g_err), "qqt_bot_act: the mode ticker needs mode_timer");
     return QQT_E_ARG;
   }
   hipStream_t st = (hipStream_t)stream;

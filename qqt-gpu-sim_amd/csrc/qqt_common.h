@@ -29,7 +29,7 @@ __host__ __device__ inline int tick_envs_per_wave(int n_envs) {
 enum : uint32_t {
   STREAM_CRATE = 1, STREAM_RESET_CELL = 2, STREAM_RESET_MISC = 3,
   STREAM_POLICY = 4, STREAM_RANDOM_ACT = 5, STREAM_INJECT_ACT = 6, STREAM_BOT = 7,
-  STREAM_RECYCLE = 8
+  STREAM_RECYCLE = 8, STREAM_BOT_MODE = 9
 };
 
 // Philox4x32 with 10 rounds (Salmon et al., SC'11).  c holds the counter on

@@ -14,7 +14,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 
 from ._build import LIB
 
-ABI_VERSION = 24
+ABI_VERSION = 25
 
 MODE_STEP, MODE_OBSERVE, MODE_RESET, MODE_PROBE, MODE_FLUSH = 0, 1, 2, 3, 4
 MAP_PILLARS, MAP_OPEN, MAP_REFERENCE = 0, 1, 2
@@ -82,7 +82,8 @@ class BotArgsC(ctypes.Structure):
     _fields_ = [("n_envs", _i32), ("pid", _i32), ("seed", _u64), ("tick", _u32),
                 ("reach_mode", _i32), ("reach_slot", _i32)] + [
         (n, _vp) for n in ("cells", "players", "obs", "move_mask", "bomb_mask", "uniforms",
-                           "reach", "reach_caps", "actions", "actions_i8")]
+                           "reach", "reach_caps", "actions", "actions_i8", "mode",
+                           "mode_timer")] + [("mode_tick", _u32), ("reserved", _i32)]
 
 
 class L1GradArgsC(ctypes.Structure):

@@ -1,12 +1,16 @@
 """`HipAstarBot`: the reference's astar rule bot on the MI355X kernel.
 
-Drop-in for `make_bot(sim, "astar", mode=False)` (sim/bots.py:538-560: the
-`astar_attack` policy of :267-508 in a `BotWrapper`, :511-535, without the
-approach/flee mode ticker) for the learner-vs-bot rollout: `act(obs, mmask,
-bmask, pid)` returns (N, 2) int64 actions like the reference bot, computed by
-one `qqt_bot_act` call that reads the sim's device state directly.  The mode
-ticker of `mode=True` and the crate-eating layer (`eat_crates=True`, the
-"hunter" bot) are not on this path.
+Drop-in for `make_bot(sim, "astar", mode=...)` (sim/bots.py:538-560: the
+`astar_attack` policy of :267-508 in a `BotWrapper`, :511-535) for the
+learner-vs-bot rollout: `act(obs, mmask, bmask, pid)` returns (N, 2) int64
+actions like the reference bot, computed by one `qqt_bot_act` call that reads
+the sim's device state directly.  `mode=True` attaches the approach / flee
+mode ticker (`_mode_ticker`, :241-264): per env a mode and a countdown
+drawn at construction (torch generator seeded by the bot's seed), advanced
+by every call on the device (new draws from Philox stream 9); `mode=False`
+(the default here, as in the learner-vs-bot benchmark) always approaches.
+The crate-eating layer (`eat_crates=True`, the "hunter" bot) is not on this
+path.
 
 The noise uniforms come from Philox (stream 7, keyed by env and this bot's
 call counter) unless `uniforms=(N, 5)` is passed.  The chain check reaches
@@ -30,7 +34,7 @@ class HipAstarBot:
     is_bot = True
 
     def __init__(self, sim: HipBatchedSim, pid: int = 1, seed: int | None = None,
-                 own_cap_reach: bool = False):
+                 own_cap_reach: bool = False, mode: bool = False):
         if not 0 <= pid < sim.cfg.n_players:
             raise ValueError("pid out of range")
         self.sim, self.pid = sim, int(pid)
@@ -56,7 +60,26 @@ class HipAstarBot:
         b.move_mask, b.bomb_mask = sim._mm.data_ptr(), sim._bm.data_ptr()
         b.reach_mode = 0 if own_cap_reach else 1
         b.reach = self._reach.data_ptr()
+        self.mode_count = 0
+        if mode:
+            # the ticker's initial draws (sim/bots.py:248-250): mode 0 / 1,
+            # countdown 60 .. 239
+            g = torch.Generator().manual_seed(self.seed)
+            n = sim.num_envs
+            self.modes = torch.randint(0, 2, (n,), generator=g, dtype=torch.int8).to(sim.device)
+            self.mode_timers = torch.randint(60, 240, (n,), generator=g,
+                                             dtype=torch.int32).to(sim.device)
+            b.mode, b.mode_timer = self.modes.data_ptr(), self.mode_timers.data_ptr()
+        else:
+            self.modes = self.mode_timers = None
         self._args = b
+
+    def _step_modes(self, b) -> None:
+        """This call's ticker count (the reference steps its ticker on every
+        act call, sim/bots.py:529-531)."""
+        if self.modes is not None:
+            self.mode_count += 1
+            b.mode_tick = self.mode_count & 0xFFFFFFFF or 1
 
     def _set_reach(self, b) -> None:
         """The chain check's reach source for this call: the caps the last STEP
@@ -93,6 +116,7 @@ class HipAstarBot:
         b = self._args
         b.tick = self.tick & 0xFFFFFFFF
         self._set_reach(b)
+        self._step_modes(b)
         b.uniforms = None
         b.actions = actions.data_ptr() if actions.dtype == torch.int64 else None
         b.actions_i8 = actions.data_ptr() if actions.dtype == torch.int8 else None
@@ -121,6 +145,7 @@ class HipAstarBot:
         b.obs, b.move_mask, b.bomb_mask = obs_t.data_ptr(), mm.data_ptr(), bm.data_ptr()
         b.tick = self.tick & 0xFFFFFFFF
         self._set_reach(b)
+        self._step_modes(b)
         b.uniforms = _capi.ptr(u)
         b.actions, b.actions_i8 = self._out.data_ptr(), None
         try:

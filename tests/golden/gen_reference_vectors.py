@@ -34,6 +34,11 @@ permutation):
   for player 0: per tick the bot's inputs (state, observation, masks, the
   noise uniforms its torch.rand(n, 5) draws, seeded per tick), its output,
   and on every 4th tick its two cost fields (V_safe, V_opp).
+* astar_flee.npz - the same with behaviour modes: a seeded approach / flee
+  mode per env, from tick 32 on flipped every 4 ticks (so that bots that
+  approached flee from close by), set as the sim's `_bmode` before each astar_attack call
+  (the flee branch of sim/bots.py:433-443, 496-503) and recorded per tick
+  with the bot's inputs and outputs.
 
 Run a subset by name: `python tests/golden/gen_reference_vectors.py astar`.
 """
@@ -401,6 +406,48 @@ def astar(name, spec, n=64, ticks=64, seed=11):
           f"alive1={int(out['alive'][-1][:, 1].sum())}")
 
 
+def astar_flee(spec, n=64, ticks=96, seed=29):
+    import sim.bots as ref_bots
+
+    s = ref_sim(n, spec, seed)
+    g = torch.Generator().manual_seed(seed)
+    mode = torch.randint(0, 2, (n,), generator=g)
+    keys = ("wall", "brick", "fuse", "owner", "pos", "alive", "blast_cap")
+    rec = {k: [] for k in keys + ("obs", "mm1", "bm1", "u", "bot", "mode")}
+    for tick in range(ticks):
+        if tick >= 32 and tick % 4 == 0:
+            mode = 1 - mode
+        snap = snapshot(s)
+        obs = s.observe()
+        mm, bm = s.legal_mask()
+        seed_t = seed * 100003 + tick
+        torch.manual_seed(seed_t)
+        u = torch.rand(n, 5)
+        torch.manual_seed(seed_t)
+        s._bmode = mode
+        bot = ref_bots.astar_attack(s, obs, mm[:, 1], bm[:, 1], 1)
+        for k in keys:
+            rec[k].append(snap[k])
+        rec["obs"].append(obs.numpy().copy())
+        rec["mm1"].append(mm[:, 1].numpy().copy())
+        rec["bm1"].append(bm[:, 1].numpy().copy())
+        rec["u"].append(u.numpy().copy())
+        rec["bot"].append(bot.numpy().copy())
+        rec["mode"].append(mode.numpy().astype(np.int8))
+        a = actions_for("legal", mm.numpy(), bm.numpy(), n, seed, tick)
+        a[:, 1] = bot.numpy()
+        cu = philox.uniforms(seed, np.arange(n), tick, philox.STREAM_CRATE, 2 * s.cfg.n_players)
+        cu = cu.reshape(n, s.cfg.n_players, 2).transpose(1, 2, 0).copy()
+        s._rand_buf = torch.from_numpy(np.concatenate(
+            [cu[:, 0, :].T.reshape(-1), cu[:, 1, :].T.reshape(-1)]))
+        s.step(torch.from_numpy(a), auto_reset=False)
+    out = {k: np.stack(v) for k, v in rec.items()}
+    np.savez_compressed(os.path.join(HERE, "astar_flee.npz"), **out)
+    bots, md = out["bot"], out["mode"]
+    print(f"astar_flee: ticks={ticks} moves={np.bincount(bots[..., 0].ravel(), minlength=5)} "
+          f"places approach={int(bots[..., 1][md == 0].sum())} flee={int(bots[..., 1][md == 1].sum())}")
+
+
 def astar_chain(seed=19):
     """Hand-built states where the bot's chain check matters: the bot stands
     in the open with a short-fuse bomb k cells away in a straight line; env 0's
@@ -448,6 +495,8 @@ if __name__ == "__main__" and len(sys.argv) > 1:
             astar("open", MapSpec(kind="open", bombs_cap=(2, 3), blast_cap=(2, 4)), ticks=96,
                   seed=17)
             astar_chain()
+        elif what == "astar_flee":
+            astar_flee(MapSpec(kind="open", bombs_cap=(2, 3), blast_cap=(2, 4)))
         elif what == "cnn":
             mlp(arch="cnn")
         elif what == "lstm":
@@ -470,4 +519,5 @@ elif __name__ == "__main__":
           seed=13)
     astar("open", MapSpec(kind="open", bombs_cap=(2, 3), blast_cap=(2, 4)), ticks=96, seed=17)
     astar_chain()
+    astar_flee(MapSpec(kind="open", bombs_cap=(2, 3), blast_cap=(2, 4)))
     lstm()

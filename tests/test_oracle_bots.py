@@ -136,3 +136,48 @@ def test_planted_own_cap_reach_fails():
     assert z["bot"][0][:, 1].sum() > 0
     own = astar_act(*base, reach=2)
     assert not np.array_equal(own.numpy(), z["bot"][0])
+
+
+def test_flee_mode_actions_match_reference():
+    """Behaviour modes (sim/bots.py:433-443, 496-503): with the fixture's
+    per-env approach / flee modes the oracle reproduces the reference's
+    decisions; ignoring the modes does not (the fixture discriminates), and
+    it holds placements of both modes."""
+    z = np.load(f"{GOLDEN}/astar_flee.npz")
+    cfg = corridor_training_config()
+    assert 0 < int(z["mode"].sum()) < z["mode"].size
+    differs = 0
+    for t in range(z["bot"].shape[0]):
+        args = (cfg, _state(z, t), torch.from_numpy(z["obs"][t]), torch.from_numpy(z["mm1"][t]),
+                torch.from_numpy(z["bm1"][t]), 1, torch.from_numpy(z["u"][t]))
+        got = astar_act(*args, mode=torch.from_numpy(z["mode"][t]).long())
+        np.testing.assert_array_equal(got.numpy(), z["bot"][t], err_msg=f"tick {t}")
+        differs += int((astar_act(*args).numpy() != z["bot"][t]).any(axis=1).sum())
+    assert differs > 100
+    places = z["bot"][..., 1]
+    assert places[z["mode"] == 0].sum() > 0 and places[z["mode"] == 1].sum() > 0
+
+
+def test_mode_ticker_laws():
+    """The mode ticker (sim/bots.py:241-264): timers count down by one per
+    call; only on calls that are multiples of 16, and only for envs at or
+    below 0, does a switch happen, to a timer on 60 .. 239 and a mode that is
+    1 about half the time."""
+    from oracle.bots import mode_tick
+
+    n = 4096
+    g = torch.Generator().manual_seed(5)
+    mode = torch.randint(0, 2, (n,), generator=g, dtype=torch.int8)
+    timer = torch.randint(-20, 40, (n,), generator=g, dtype=torch.int32)
+    new_modes = []
+    for count in range(1, 65):
+        m2, t2 = mode_tick(mode, timer, count, seed=9)
+        due = (timer - 1 <= 0) & (count % 16 == 0)
+        assert torch.equal(t2[~due], timer[~due] - 1)
+        assert torch.equal(m2[~due], mode[~due])
+        if due.any():
+            assert int(t2[due].min()) >= 60 and int(t2[due].max()) <= 239
+            new_modes.append(m2[due])
+        mode, timer = m2, t2
+    drawn = torch.cat(new_modes).float()
+    assert drawn.numel() > 1000 and abs(float(drawn.mean()) - 0.5) < 0.05
