@@ -48,6 +48,7 @@
 #include <stdio.h>
 
 #include "qqt_common.h"
+#include "pipeline.h"
 #include "qqt_hip.h"
 
 namespace qqt {
@@ -81,6 +82,14 @@ constexpr int HID = 128, HS = 130, HYS = 194;
 constexpr int S0 = 5, S1 = 5, S2 = 9, S3 = 2;       // 32-deep K steps of the four convolutions
 constexpr int L1 = HID / 4;                         // K steps of the float32 head GEMMs
 constexpr int BFRAG = 64 * 8;                       // halves of one step's B fragments
+#ifndef QQT_CNN_HEAD_D
+#define QQT_CNN_HEAD_D 3
+#endif
+#ifndef QQT_CNN_CONV_D
+#define QQT_CNN_CONV_D 1
+#endif
+constexpr int CONV_D = QQT_CNN_CONV_D;              // steps the convs' B fragments load ahead
+constexpr int HEAD_D = QQT_CNN_HEAD_D;              // steps the head's layer-1 operands load ahead
 static_assert(WS_ROW * 2 == QQT_CNN_WS_BYTES_PER_ITEM, "workspace row size");
 
 struct __align__(16) Lds {                 // every member a multiple of 16 bytes long
@@ -143,6 +152,8 @@ __device__ __forceinline__ T* at(T* base, uint32_t byte_off) {
   return reinterpret_cast<T*>(reinterpret_cast<char*>(base) + byte_off);
 }
 
+__device__ __forceinline__ half8 bld8(Rsrc r, uint32_t byte_off) { return bld16<half8>(r, byte_off); }
+
 __device__ __forceinline__ floatx4 mfma16(half8 a, half8 b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
@@ -194,8 +205,8 @@ __device__ __forceinline__ constexpr int tap_off(int tap) { return (tap / 3) * P
 // value q of lane l is output channel 16 ntile + 4 (l / 16) + q at
 // position x = l % 16 of the row; acc[t] = bias +
 // sum over steps of A B, three float16 products per step (two without the
-// activations' lo plane).  bfrag(s) returns step s's B fragments; the step
-// loop stays rolled, with B fragments loaded two steps ahead, and each
+// activations' lo plane).  bfrag(s) returns step s's B fragments, loaded
+// CONV_D steps ahead (pipeline), and each
 // product kind runs over all tiles before the next, so no two consecutive
 // MFMAs share an accumulator.
 template <int KIND, int STEPS, int NTL, bool ALO, class BF>
@@ -211,10 +222,7 @@ __device__ __forceinline__ void conv(const uint16_t* act_hi, const uint16_t* act
                         : (pb + PW + 1) * CS + 8 * kq;
     acc[t] = bias;
   }
-  BFrag b = bfrag(0), b1 = bfrag(min(1, STEPS - 1));
-#pragma unroll 1
-  for (int st = 0; st < STEPS; ++st) {
-    const BFrag bn = bfrag(min(st + 2, STEPS - 1));
+  pipeline<STEPS, CONV_D>(bfrag, [&](int st, const BFrag& b) {
     int off;
     if constexpr (KIND == 0)
       off = tap_off(min(2 * st + (kq >> 1), 8)) * CS;
@@ -245,9 +253,7 @@ __device__ __forceinline__ void conv(const uint16_t* act_hi, const uint16_t* act
           if (t0 + u < NTL) acc[t0 + u] = mfma16(b.hi, al[u], acc[t0 + u]);
       }
     }
-    b = b1;
-    b1 = bn;
-  }
+  });
 }
 
 // LayerNorm statistics over the valid outputs of a layer (lane x < 13,
@@ -478,21 +484,23 @@ __global__ __launch_bounds__(T, 3) void cnn_trunk_kernel(const qqt_cnn_args a, i
 
   for (int i = t; i < PP * CS; i += T) s.act[0][i] = s.act[1][i] = 0;
   const uint32_t lb = (uint32_t)lane * 16u;        // this lane's bytes in a step's fragments
-  const uint16_t* const c1h = a.c1w + (size_t)n1 * S1 * BFRAG;
-  const uint16_t* const c1l = a.c1w_lo + (size_t)n1 * S1 * BFRAG;
+  // buffer resources over this wavefront's B slices (STEPS fragments each)
+  const Rsrc c1h = rsrc(a.c1w + (size_t)n1 * S1 * BFRAG, S1 * BFRAG * 2);
+  const Rsrc c1l = rsrc(a.c1w_lo + (size_t)n1 * S1 * BFRAG, S1 * BFRAG * 2);
   auto breg1 = [&](int j) {
     const uint32_t o = lb + (uint32_t)j * (BFRAG * 2);
-    return BFrag{ld8(at(c1h, o)), ld8(at(c1l, o))};
+    return BFrag{bld8(c1h, o), bld8(c1l, o)};
   };
-  const uint16_t* const c2h = a.c2w + (size_t)n2 * S2 * BFRAG;
-  const uint16_t* const c2l = a.c2w_lo + (size_t)n2 * S2 * BFRAG;
+  const Rsrc c2h = rsrc(a.c2w + (size_t)n2 * S2 * BFRAG, S2 * BFRAG * 2);
+  const Rsrc c2l = rsrc(a.c2w_lo + (size_t)n2 * S2 * BFRAG, S2 * BFRAG * 2);
   auto breg2 = [&](int j) {
     const uint32_t o = lb + (uint32_t)j * (BFRAG * 2);
-    return BFrag{ld8(at(c2h, o)), ld8(at(c2l, o))};
+    return BFrag{bld8(c2h, o), bld8(c2l, o)};
   };
+  const Rsrc c0h = rsrc(a.c0w, S0 * BFRAG * 2), c0l = rsrc(a.c0w_lo, S0 * BFRAG * 2);
   auto bglob0 = [&](int j) {
     const uint32_t o = lb + (uint32_t)j * (BFRAG * 2);
-    return BFrag{ld8(at(a.c0w, o)), ld8(at(a.c0w_lo, o))};
+    return BFrag{bld8(c0h, o), bld8(c0l, o)};
   };
 
   // Observation staging: thread t < 169 moves position p = t of the item's
@@ -634,35 +642,35 @@ __global__ __launch_bounds__(T) void cnn_head_kernel(const qqt_cnn_args a, int i
   // Linear(1352,128): wavefront w computes output tiles 2w, 2w + 1 of every
   // row tile (each B fragment feeds HM row tiles)
   {
-    const uint16_t* ar[HM];
+    // the workgroup's HB workspace rows, and this wavefront's two output
+    // tiles of the float16 hi/lo weight planes
+    const Rsrc ws = rsrc(a.workspace + (size_t)ib * WS_ROW, HB * WS_ROW * 2);
+    uint32_t ar[HM];
 #pragma unroll
-    for (int m = 0; m < HM; ++m)
-      ar[m] = a.workspace + (size_t)ib * WS_ROW + min(16 * m + i16, nb - 1) * 32 + 8 * kq;
-    const size_t tile = (size_t)S0H * BFRAG;
-    const uint16_t* const bh = a.s0h + 2 * w * tile + lane * 8;
-    const uint16_t* const bl = a.s0l + 2 * w * tile + lane * 8;
+    for (int m = 0; m < HM; ++m) ar[m] = (uint32_t)(min(16 * m + i16, nb - 1) * 32 + 8 * kq) * 2u;
+    constexpr uint32_t tile = S0H * BFRAG * 2;       // bytes of one output tile's plane
+    const Rsrc bh = rsrc(a.s0h + (size_t)2 * w * S0H * BFRAG, 2 * tile);
+    const Rsrc bl = rsrc(a.s0l + (size_t)2 * w * S0H * BFRAG, 2 * tile);
+    const uint32_t lb = (uint32_t)lane * 16u;
     struct Frag { half8 ah[HM], al[HM], h0, l0, h1, l1; };
     auto load = [&](int st) {
       Frag f;
 #pragma unroll
       for (int m = 0; m < HM; ++m) {
-        f.ah[m] = ld8(ar[m] + st * HB * 32);
-        f.al[m] = ld8(ar[m] + (S0H + st) * HB * 32);
+        f.ah[m] = bld8(ws, ar[m] + (uint32_t)st * (HB * 32 * 2));
+        f.al[m] = bld8(ws, ar[m] + (uint32_t)(S0H + st) * (HB * 32 * 2));
       }
-      f.h0 = ld8(bh + st * BFRAG);
-      f.l0 = ld8(bl + st * BFRAG);
-      f.h1 = ld8(bh + tile + st * BFRAG);
-      f.l1 = ld8(bl + tile + st * BFRAG);
+      const uint32_t o = lb + (uint32_t)st * (BFRAG * 2);
+      f.h0 = bld8(bh, o);
+      f.l0 = bld8(bl, o);
+      f.h1 = bld8(bh, o + tile);
+      f.l1 = bld8(bl, o + tile);
       return f;
     };
     floatx4 c[HM][2];
 #pragma unroll
     for (int m = 0; m < HM; ++m) c[m][0] = c[m][1] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    // rolled K loop, fragments loaded two steps ahead
-    Frag f0 = load(0), f1 = load(1);
-#pragma unroll 1
-    for (int st = 0; st < S0H; ++st) {
-      const Frag f2 = load(min(st + 2, S0H - 1));
+    pipeline<S0H, HEAD_D>(load, [&](int, const Frag& f0) {
 #pragma unroll
       for (int m = 0; m < HM; ++m) {
         c[m][0] = mfma16(f0.ah[m], f0.h0, c[m][0]);
@@ -678,9 +686,7 @@ __global__ __launch_bounds__(T) void cnn_head_kernel(const qqt_cnn_args a, int i
         c[m][0] = mfma16(f0.al[m], f0.h0, c[m][0]);
         c[m][1] = mfma16(f0.al[m], f0.h1, c[m][1]);
       }
-      f0 = f1;
-      f1 = f2;
-    }
+    });
 #pragma unroll
     for (int m = 0; m < HM; ++m) {
       head_store(c[m][0], h + 16 * m * HS, HS, 2 * w, s.v + V_S0B, false);

@@ -44,6 +44,7 @@
 #include <stdio.h>
 
 #include "qqt_common.h"
+#include "pipeline.h"
 #include "qqt_hip.h"
 
 namespace qqt {
@@ -82,6 +83,10 @@ static_assert(RG * 36 % 16 == 0, "whole conv2 tiles per group");
 // bank groups
 constexpr int PP = 584, PX = 200, PXH = 392, PHN = 136, PHD = 200, PR = 72, PG = 40;
 constexpr int LD_LG = 16;                 // float32 outputs
+#ifndef QQT_LSTM_GEMM_D
+#define QQT_LSTM_GEMM_D 1
+#endif
+constexpr int GEMM_D = QQT_LSTM_GEMM_D;   // K steps the head GEMMs' weight fragments load ahead
 
 // packed parameter block (floats; built by qqtsim/policy.py pack_lstm): the
 // convolutions k-major [in][out]; each head layer W [K][N] as float16 hi
@@ -234,34 +239,40 @@ struct __align__(16) ActLds {
 // read per plane (row r, k = 32 s + 8 q .. + 7) and one 16-byte fragment
 // read per plane and tile feed hi*hi + hi*lo + lo*hi (LO = false: the A
 // values are float16 exactly, hi*hi + hi*lo).
-template <int NT, bool LO, class Tile>
+template <int NT, bool LO, int K, int N, class Tile>
 __device__ __forceinline__ void gemmh(floatx4 (&acc)[NT], const uint16_t* Ah, const uint16_t* Al,
-                                      int lda, const float* F, int K, int N, Tile tile, int lane) {
+                                      int lda, const float* F, Tile tile, int lane) {
+  static_assert(K % 32 == 0, "whole K steps");
+  constexpr int ks = K / 32;
   const int r = lane & 15, q = lane >> 4;
-  const int ks = K / 32;
-  const half8* Fh = reinterpret_cast<const half8*>(F);
-  const half8* Fl = reinterpret_cast<const half8*>(F + (size_t)K * N / 2);
+  // the fragments' hi plane, then the lo plane, K * N halves each; loaded
+  // GEMM_D steps ahead
+  const Rsrc fr = rsrc(F, (uint32_t)K * N * 4);
   const uint16_t* ah = Ah + r * lda + 8 * q;
   const uint16_t* al = Al + r * lda + 8 * q;
-#pragma unroll 2
-  for (int st = 0; st < ks; ++st) {
-    const half8 xh = *reinterpret_cast<const half8*>(ah + 32 * st);
-    half8 xl;
-    if constexpr (LO) xl = *reinterpret_cast<const half8*>(al + 32 * st);
-    half8 bh[NT], bl[NT];
+  struct Frag { half8 h[NT], l[NT]; };
+  pipeline<ks, GEMM_D>(
+      [&](int st) {
+        Frag f;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const size_t f = ((size_t)tile(t) * ks + st) * 64 + lane;
-      bh[t] = Fh[f];
-      bl[t] = Fl[f];
-    }
+        for (int t = 0; t < NT; ++t) {
+          const uint32_t o = (uint32_t)(((tile(t) * ks + st) * 64 + lane) * 16);
+          f.h[t] = bld16<half8>(fr, o);
+          f.l[t] = bld16<half8>(fr, o + (uint32_t)K * N * 2);
+        }
+        return f;
+      },
+      [&](int st, const Frag& f) {
+        const half8 xh = *reinterpret_cast<const half8*>(ah + 32 * st);
+        half8 xl;
+        if constexpr (LO) xl = *reinterpret_cast<const half8*>(al + 32 * st);
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      acc[t] = mfma16(xh, bh[t], acc[t]);
-      acc[t] = mfma16(xh, bl[t], acc[t]);
-      if constexpr (LO) acc[t] = mfma16(xl, bh[t], acc[t]);
-    }
-  }
+        for (int t = 0; t < NT; ++t) {
+          acc[t] = mfma16(xh, f.h[t], acc[t]);
+          acc[t] = mfma16(xh, f.l[t], acc[t]);
+          if constexpr (LO) acc[t] = mfma16(xl, f.h[t], acc[t]);
+        }
+      });
 }
 
 // NT consecutive column tiles from t0
@@ -513,20 +524,20 @@ __global__ __launch_bounds__(NTHR) void lstm_act_kernel(const qqt_lstm_args a) {
     // Linear(576, 128) + ReLU: 8 column tiles, one per wavefront
     {
       floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
-      gemmh<1, true>(acc, s.pooled[0] + 16 * ht * PP, s.pooled[1] + 16 * ht * PP, PP, P + OFF_FCW,
-                     FEAT, HID, Tiles{w}, lane);
+      gemmh<1, true, FEAT, HID>(acc, s.pooled[0] + 16 * ht * PP, s.pooled[1] + 16 * ht * PP, PP, P + OFF_FCW,
+                     Tiles{w}, lane);
       store16h<1>(acc, s.h.xin[0], s.h.xin[1], PX, 16 * w, P + OFF_FCB, lane, HID);
     }
     __syncthreads();
     // rel 60 -> 64 (wavefronts 0-3), glob 5 -> 16 (wavefront 4)
     if (w < 4) {
       floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
-      gemmh<1, false>(acc, s.h.rel, s.h.rel, PR, P + OFF_R1W, 64, 64, Tiles{w}, lane);
+      gemmh<1, false, 64, 64>(acc, s.h.rel, s.h.rel, PR, P + OFF_R1W, Tiles{w}, lane);
       store16h<1>(acc, s.h.r1[0], s.h.r1[1], PR, 16 * w, P + OFF_R1B, lane, 64);
     } else {
       if (w == 4) {
         floatx4 ag[1] = {floatx4{0, 0, 0, 0}};
-        gemmh<1, false>(ag, s.h.glb, s.h.glb, PG, P + OFF_G1W, GK, 16, Tiles{0}, lane);
+        gemmh<1, false, GK, 16>(ag, s.h.glb, s.h.glb, PG, P + OFF_G1W, Tiles{0}, lane);
         store16h<1>(ag, s.h.g1[0], s.h.g1[1], PG, 0, P + OFF_G1B, lane, 16);
       }
     }
@@ -534,18 +545,18 @@ __global__ __launch_bounds__(NTHR) void lstm_act_kernel(const qqt_lstm_args a) {
     // rel 64 -> 32 (wavefronts 0, 1), glob 16 -> 8 (wavefront 2)
     if (w < 2) {
       floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
-      gemmh<1, true>(acc, s.h.r1[0], s.h.r1[1], PR, P + OFF_R2W, 64, 32, Tiles{w}, lane);
+      gemmh<1, true, 64, 32>(acc, s.h.r1[0], s.h.r1[1], PR, P + OFF_R2W, Tiles{w}, lane);
       store16h<1>(acc, s.h.xin[0] + HID, s.h.xin[1] + HID, PX, 16 * w, P + OFF_R2B, lane, 32);
     } else if (w == 2) {
       floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
-      gemmh<1, true>(acc, s.h.g1[0], s.h.g1[1], PG, P + OFF_G2W, GK, 16, Tiles{0}, lane);
+      gemmh<1, true, GK, 16>(acc, s.h.g1[0], s.h.g1[1], PG, P + OFF_G2W, Tiles{0}, lane);
       store16h<1>(acc, s.h.xin[0] + HID + 32, s.h.xin[1] + HID + 32, PX, 0, P + OFF_G2B, lane, 8);
     }
     __syncthreads();
     // fusion Linear(168, 256) + ReLU: 16 tiles, two per wavefront
     {
       floatx4 acc[2] = {floatx4{0, 0, 0, 0}, floatx4{0, 0, 0, 0}};
-      gemmh<2, true>(acc, s.h.xin[0], s.h.xin[1], PX, P + OFF_FUW, XINP, 256, Tiles{2 * w}, lane);
+      gemmh<2, true, XINP, 256>(acc, s.h.xin[0], s.h.xin[1], PX, P + OFF_FUW, Tiles{2 * w}, lane);
       store16h<2>(acc, s.h.xh[0], s.h.xh[1], PXH, 32 * w, P + OFF_FUB, lane, 256);
     }
     __syncthreads();
@@ -557,7 +568,7 @@ __global__ __launch_bounds__(NTHR) void lstm_act_kernel(const qqt_lstm_args a) {
       floatx4 acc[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) acc[t] = floatx4{0, 0, 0, 0};
-      gemmh<4, true>(acc, s.h.xh[0], s.h.xh[1], PXH, P + OFF_LW, 384, G4,
+      gemmh<4, true, 384, G4>(acc, s.h.xh[0], s.h.xh[1], PXH, P + OFF_LW,
                      [&](int t) { return 8 * t + w; }, lane);
       {
         const int u = 16 * w + r16;
@@ -586,11 +597,11 @@ __global__ __launch_bounds__(NTHR) void lstm_act_kernel(const qqt_lstm_args a) {
     // 0-3 and one per wavefront 4-7
     if (w < 4) {
       floatx4 acc[2] = {floatx4{0, 0, 0, 0}, floatx4{0, 0, 0, 0}};
-      gemmh<2, true>(acc, s.h.hn[0], s.h.hn[1], PHN, P + OFF_HW, HID, 3 * HEAD, Tiles{2 * w}, lane);
+      gemmh<2, true, HID, 3 * HEAD>(acc, s.h.hn[0], s.h.hn[1], PHN, P + OFF_HW, Tiles{2 * w}, lane);
       store16h<2>(acc, s.h.hd[0], s.h.hd[1], PHD, 32 * w, P + OFF_HB, lane, 3 * HEAD);
     } else {
       floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
-      gemmh<1, true>(acc, s.h.hn[0], s.h.hn[1], PHN, P + OFF_HW, HID, 3 * HEAD, Tiles{8 + (w - 4)},
+      gemmh<1, true, HID, 3 * HEAD>(acc, s.h.hn[0], s.h.hn[1], PHN, P + OFF_HW, Tiles{8 + (w - 4)},
                      lane);
       store16h<1>(acc, s.h.hd[0], s.h.hd[1], PHD, 128 + 16 * (w - 4), P + OFF_HB, lane, 3 * HEAD);
     }
@@ -598,7 +609,7 @@ __global__ __launch_bounds__(NTHR) void lstm_act_kernel(const qqt_lstm_args a) {
     // output layer 192 -> 8 (block diagonal, 16 padded columns): wavefront 0
     if (w == 0) {
       floatx4 acc[1] = {floatx4{0, 0, 0, 0}};
-      gemmh<1, true>(acc, s.h.hd[0], s.h.hd[1], PHD, P + OFF_OW, 3 * HEAD, 16, Tiles{0}, lane);
+      gemmh<1, true, 3 * HEAD, 16>(acc, s.h.hd[0], s.h.hd[1], PHD, P + OFF_OW, Tiles{0}, lane);
       store16<1>(acc, s.h.lg, LD_LG, 0, P + OFF_OB, false, lane, 16);
     }
     __syncthreads();
