@@ -83,7 +83,7 @@ constexpr int S0 = 5, S1 = 5, S2 = 9, S3 = 2;       // 32-deep K steps of the fo
 constexpr int L1 = HID / 4;                         // K steps of the float32 head GEMMs
 constexpr int BFRAG = 64 * 8;                       // halves of one step's B fragments
 #ifndef QQT_CNN_HEAD_D
-#define QQT_CNN_HEAD_D 3
+#define QQT_CNN_HEAD_D 1
 #endif
 #ifndef QQT_CNN_CONV_D
 #define QQT_CNN_CONV_D 1
@@ -110,12 +110,16 @@ static_assert(3 * sizeof(Lds) <= 160 * 1024, "three trunk workgroups fit in one 
 constexpr int V_S0B = 0, V_S1W = 128, V_S1B = 256, V_S3B = 384, V_S4W = 512, V_S4B = 640,
               V_HB = 768, V_FW = 960, V_FB = 1472, V_N = 1480;
 
+constexpr int PART_N = NW * HM * 8 * 64 * 4;        // layer 1's partial sums: [wave][M tile][N tile][lane][4]
 struct __align__(16) HeadLds {
   float hy[HB * HYS];                       // heads' hidden layer; before it the first layer's
   float h2[HB * HS];                        // output h (stride HS, read by the second layer)
+  float pad[PART_N - HB * HYS - HB * HS];   // hy .. pad: the partial sums before that
   float lg[HB * 8];
   float v[V_N];
 };
+static_assert(PART_N > HB * HYS + HB * HS, "the partial sums span hy, h2 and pad");
+static_assert(2 * sizeof(HeadLds) <= 160 * 1024, "two head workgroups fit in one CU's LDS");
 
 __device__ __forceinline__ floatx4 mfma(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -629,8 +633,6 @@ __global__ __launch_bounds__(T) void cnn_head_kernel(const qqt_cnn_args a, int i
   const int lane = t & 63, i16 = lane & 15, kq = lane >> 4;
   const int ib = blockIdx.x * HB, nb = min(HB, items - ib);
   float* const h = s.hy;
-  float w3[2][L1];                                  // Linear(128,128) operands, in flight early
-  head_weights<L1, 2>(a.s3p, 2 * w, w3);
   {
     const float* const src[9] = {a.s0b, a.s1w, a.s1b, a.s3b, a.s4w, a.s4b, a.hb, a.fw, a.fb};
     const int off[10] = {V_S0B, V_S1W, V_S1B, V_S3B, V_S4W, V_S4B, V_HB, V_FW, V_FB, V_N};
@@ -639,21 +641,23 @@ __global__ __launch_bounds__(T) void cnn_head_kernel(const qqt_cnn_args a, int i
       for (int i = t; i < off[k + 1] - off[k]; i += T) s.v[off[k] + i] = src[k][i];
   }
 
-  // Linear(1352,128): wavefront w computes output tiles 2w, 2w + 1 of every
-  // row tile (each B fragment feeds HM row tiles)
+  // Linear(1352,128): wavefront w takes K steps KQ w .. KQ w + KQ - 1 (the
+  // last wavefront the 10 that remain) for all HM x 8 output tiles, so the
+  // workgroup reads its items' features once; the four partial sums meet in
+  // LDS and wavefront w finishes output tiles 2w, 2w + 1 of every row tile
   {
-    // the workgroup's HB workspace rows, and this wavefront's two output
-    // tiles of the float16 hi/lo weight planes
+    constexpr int KQ = (S0H + NW - 1) / NW;
+    const int k0 = KQ * w, kn = min(KQ, S0H - k0);
     const Rsrc ws = rsrc(a.workspace + (size_t)ib * WS_ROW, HB * WS_ROW * 2);
     uint32_t ar[HM];
 #pragma unroll
     for (int m = 0; m < HM; ++m) ar[m] = (uint32_t)(min(16 * m + i16, nb - 1) * 32 + 8 * kq) * 2u;
     constexpr uint32_t tile = S0H * BFRAG * 2;       // bytes of one output tile's plane
-    const Rsrc bh = rsrc(a.s0h + (size_t)2 * w * S0H * BFRAG, 2 * tile);
-    const Rsrc bl = rsrc(a.s0l + (size_t)2 * w * S0H * BFRAG, 2 * tile);
+    const Rsrc bh = rsrc(a.s0h, 8 * tile), bl = rsrc(a.s0l, 8 * tile);
     const uint32_t lb = (uint32_t)lane * 16u;
-    struct Frag { half8 ah[HM], al[HM], h0, l0, h1, l1; };
-    auto load = [&](int st) {
+    struct Frag { half8 ah[HM], al[HM], h[8], l[8]; };
+    auto load = [&](int i) {
+      const int st = min(k0 + i, S0H - 1);
       Frag f;
 #pragma unroll
       for (int m = 0; m < HM; ++m) {
@@ -661,32 +665,56 @@ __global__ __launch_bounds__(T) void cnn_head_kernel(const qqt_cnn_args a, int i
         f.al[m] = bld8(ws, ar[m] + (uint32_t)(S0H + st) * (HB * 32 * 2));
       }
       const uint32_t o = lb + (uint32_t)st * (BFRAG * 2);
-      f.h0 = bld8(bh, o);
-      f.l0 = bld8(bl, o);
-      f.h1 = bld8(bh, o + tile);
-      f.l1 = bld8(bl, o + tile);
+#pragma unroll
+      for (int n = 0; n < 8; ++n) {
+        f.h[n] = bld8(bh, o + n * tile);
+        f.l[n] = bld8(bl, o + n * tile);
+      }
       return f;
     };
-    floatx4 c[HM][2];
+    floatx4 c[HM][8];
 #pragma unroll
-    for (int m = 0; m < HM; ++m) c[m][0] = c[m][1] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    pipeline<S0H, HEAD_D>(load, [&](int, const Frag& f0) {
+    for (int m = 0; m < HM; ++m)
 #pragma unroll
-      for (int m = 0; m < HM; ++m) {
-        c[m][0] = mfma16(f0.ah[m], f0.h0, c[m][0]);
-        c[m][1] = mfma16(f0.ah[m], f0.h1, c[m][1]);
-      }
+      for (int n = 0; n < 8; ++n) c[m][n] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    pipeline<KQ, HEAD_D>(load, [&](int i, const Frag& f) {
+      if (i < kn) {
 #pragma unroll
-      for (int m = 0; m < HM; ++m) {
-        c[m][0] = mfma16(f0.ah[m], f0.l0, c[m][0]);
-        c[m][1] = mfma16(f0.ah[m], f0.l1, c[m][1]);
-      }
+        for (int m = 0; m < HM; ++m)
 #pragma unroll
-      for (int m = 0; m < HM; ++m) {
-        c[m][0] = mfma16(f0.al[m], f0.h0, c[m][0]);
-        c[m][1] = mfma16(f0.al[m], f0.h1, c[m][1]);
+          for (int n = 0; n < 8; ++n) c[m][n] = mfma16(f.ah[m], f.h[n], c[m][n]);
+#pragma unroll
+        for (int m = 0; m < HM; ++m)
+#pragma unroll
+          for (int n = 0; n < 8; ++n) c[m][n] = mfma16(f.ah[m], f.l[n], c[m][n]);
+#pragma unroll
+        for (int m = 0; m < HM; ++m)
+#pragma unroll
+          for (int n = 0; n < 8; ++n) c[m][n] = mfma16(f.al[m], f.h[n], c[m][n]);
       }
     });
+    floatx4* const part = reinterpret_cast<floatx4*>(s.hy);
+#pragma unroll
+    for (int m = 0; m < HM; ++m)
+#pragma unroll
+      for (int n = 0; n < 8; ++n) part[((w * HM + m) * 8 + n) * 64 + lane] = c[m][n];
+  }
+  float w3[2][L1];                                  // Linear(128,128) operands, loaded under the sums
+  head_weights<L1, 2>(a.s3p, 2 * w, w3);
+  __syncthreads();
+  {
+    const floatx4* const part = reinterpret_cast<const floatx4*>(s.hy);
+    floatx4 c[HM][2];
+#pragma unroll
+    for (int m = 0; m < HM; ++m)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int n = 2 * w + j;
+        c[m][j] = part[(m * 8 + n) * 64 + lane];
+#pragma unroll
+        for (int v = 1; v < NW; ++v) c[m][j] += part[((v * HM + m) * 8 + n) * 64 + lane];
+      }
+    __syncthreads();                                  // every sum read before h overwrites them
 #pragma unroll
     for (int m = 0; m < HM; ++m) {
       head_store(c[m][0], h + 16 * m * HS, HS, 2 * w, s.v + V_S0B, false);
