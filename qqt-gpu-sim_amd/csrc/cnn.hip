@@ -545,7 +545,6 @@ __global__ __launch_bounds__(T, 3) void cnn_trunk_kernel(const qqt_cnn_args a, i
   for (int item = start; item < end; ++item) {
     __syncthreads();                                  // channels 0..13 free
     stage();                                          // exact in float16: hi plane only
-    fetch(min(item + 1, end - 1));
     __syncthreads();
 
     float mean, rstd;
@@ -592,6 +591,19 @@ __global__ __launch_bounds__(T, 3) void cnn_trunk_kernel(const qqt_cnn_args a, i
         v[i] = ok ? u : 0.0f;
         sum += v[i];
       }
+      // this thread's LayerNorm affines, then the next item's observation:
+      // no load is issued after the fetch before the next item stages it
+      // (loads complete in issue order, so a wait for a later load would
+      // wait for the fetch as well)
+      float lw[NS], lb[NS];
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        const int sl = min(tt + T * i, MT * 128 - 1), y = sl >> 7, o = (sl >> 4) & 7;
+        const int k = o * NP + y * HW + min(sl & 15, HW - 1);
+        lw[i] = *at(a.ln3w, (uint32_t)k * 4u);
+        lb[i] = *at(a.ln3b, (uint32_t)k * 4u);
+      }
+      fetch(min(item + 1, end - 1));
       mean = block_sum(sum, s.red, rslot) * (1.0f / FLAT);
       // every thread is past its partial-sum reads: zero the bytes they
       // occupied, the next item's padding and unused channel slots
@@ -611,9 +623,7 @@ __global__ __launch_bounds__(T, 3) void cnn_trunk_kernel(const qqt_cnn_args a, i
         const int sl = tt + T * i, y = sl >> 7, o = (sl >> 4) & 7, x = sl & 15;
         if (sl < MT * 128 && x < HW) {
           const int k = o * NP + y * HW + x;              // flattened [8][13][13] index
-          const float y = __builtin_amdgcn_fmed3f(
-              fmaf(v[i] - mean, rstd * *at(a.ln3w, (uint32_t)k * 4u), *at(a.ln3b, (uint32_t)k * 4u)),
-              0.0f, 65504.0f);
+          const float y = __builtin_amdgcn_fmed3f(fmaf(v[i] - mean, rstd * lw[i], lb[i]), 0.0f, 65504.0f);
           const _Float16 hi = (_Float16)y, lo = (_Float16)(y - (float)hi);
           *at(fl, (uint32_t)ws_off(0, k) * 2u) = __builtin_bit_cast(uint16_t, hi);
           *at(fl, (uint32_t)ws_off(1, k) * 2u) = __builtin_bit_cast(uint16_t, lo);
